@@ -1,0 +1,151 @@
+"""CPU oracle bindings — TEST INFRASTRUCTURE ONLY.
+
+Restates the reference's CPU path (see ``oracle.h`` for the file:line each
+function follows). Only ``tests/``, ``__graft_entry__.smoke()`` and the
+``cpu_baseline`` leg of ``bench.py`` may import this module, and only as the
+checker. The product library ``summa_amd`` never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import subprocess
+from pathlib import Path
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "liboracle.so"
+
+_lib = None
+
+f64p = np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS")
+f32p = np.ctypeslib.ndpointer(dtype=np.float32, flags="C_CONTIGUOUS")
+i32p = np.ctypeslib.ndpointer(dtype=np.int32, flags="C_CONTIGUOUS")
+u8p = np.ctypeslib.ndpointer(dtype=np.uint8, flags="C_CONTIGUOUS")
+u16p = np.ctypeslib.ndpointer(dtype=np.uint16, flags="C_CONTIGUOUS")
+
+
+def build() -> Path:
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        _lib = C.CDLL(str(LIB_PATH))
+        _declare(_lib)
+    return _lib
+
+
+def _declare(L: C.CDLL) -> None:
+    vp, i64, d = C.c_void_p, C.c_int64, C.c_double
+    L.or_ce_rows.argtypes = [vp, C.c_int, i32p, i64, i64, i64, vp, vp, vp, d, vp]
+    L.or_ce_rows.restype = None
+    L.or_grpo_loss.argtypes = [f64p, f64p, f64p, vp, vp, i64, i64, i64, d, d, d, f64p, f64p, f64p]
+    L.or_grpo_loss.restype = C.c_int
+    L.or_q4_quantize.argtypes = [f32p, i64, u8p, u16p]
+    L.or_q4_decode.argtypes = [u8p, u16p, i64, f32p]
+    L.or_q4_matvec.argtypes = [u8p, u16p, i64, i64, f32p, f32p]
+    for name in ("or_q4_quantize", "or_q4_decode", "or_q4_matvec"):
+        getattr(L, name).restype = None
+    _declare_model(L)
+
+
+def _declare_model(L: C.CDLL) -> None:
+    """Model-level entry points (added as the oracle grows)."""
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+# ---------------------------------------------------------------- helpers ---
+
+def bf16_bits(x: np.ndarray) -> np.ndarray:
+    """float32 -> bf16 bit patterns, round to nearest even (NaN kept quiet)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(b: np.ndarray) -> np.ndarray:
+    return (np.ascontiguousarray(b, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def round_bf16(x: np.ndarray) -> np.ndarray:
+    return bf16_to_f32(bf16_bits(x))
+
+
+# --------------------------------------------------------------------- CE ---
+
+def ce_rows(logits: np.ndarray, targets: np.ndarray, logical_vocab: int | None = None,
+            grad: bool = False, grad_scale: float = 1.0, row_scale=None):
+    """Row-wise log-softmax / CE in f64. ``logits`` float32 or uint16 (bf16 bits)."""
+    rows, stored = logits.shape
+    lv = stored if logical_vocab is None else logical_vocab
+    dtype = 1 if logits.dtype == np.uint16 else 0
+    lg = np.ascontiguousarray(logits)
+    tg = np.ascontiguousarray(targets, dtype=np.int32)
+    lp = np.empty(rows, np.float64)
+    lse = np.empty(rows, np.float64)
+    g = np.empty((rows, stored), np.float32) if grad else None
+    rs = None if row_scale is None else np.ascontiguousarray(row_scale, dtype=np.float64)
+    lib().or_ce_rows(lg.ctypes.data, dtype, tg, rows, stored, lv, lp.ctypes.data,
+                     lse.ctypes.data, _ptr(g), grad_scale, _ptr(rs))
+    return lp, lse, g
+
+
+# ------------------------------------------------------------------- GRPO ---
+
+class GrpoError(ValueError):
+    pass
+
+
+def grpo_loss(rewards, lp_cur, lp_beh, lp_ref=None, mask=None, clip=0.2, adv_eps=1e-6, beta=0.04):
+    """Batched GRPO loss. Arrays: rewards [B, G]; log-probs / mask [B, G, T].
+
+    Returns (stats [B, 5], advantages [B, G], dlp [B, G, T], error_flags)."""
+    r = np.ascontiguousarray(rewards, dtype=np.float64)
+    B, G = r.shape
+    cur = np.ascontiguousarray(lp_cur, dtype=np.float64)
+    T = cur.shape[-1]
+    beh = np.ascontiguousarray(lp_beh, dtype=np.float64)
+    ref = None if lp_ref is None else np.ascontiguousarray(lp_ref, dtype=np.float64)
+    mk = None if mask is None else np.ascontiguousarray(mask, dtype=np.float64)
+    stats = np.empty((B, 5), np.float64)
+    adv = np.empty((B, G), np.float64)
+    dlp = np.empty((B, G, T), np.float64)
+    err = lib().or_grpo_loss(r, cur, beh, _ptr(ref), _ptr(mk), B, G, T, clip, adv_eps, beta,
+                             stats, adv, dlp)
+    return stats, adv, dlp, err
+
+
+# ----------------------------------------------------------------- Q4G128 ---
+
+def q4_quantize(w: np.ndarray):
+    """Returns (codes uint8 [ceil(n/128)*64], scales uint16 [ceil(n/128)])."""
+    w = np.ascontiguousarray(w, dtype=np.float32).ravel()
+    n = w.size
+    groups = (n + 127) // 128
+    codes = np.empty(groups * 64, np.uint8)
+    scales = np.empty(groups, np.uint16)
+    lib().or_q4_quantize(w, n, codes, scales)
+    return codes, scales
+
+
+def q4_decode(codes, scales, n: int) -> np.ndarray:
+    out = np.empty(n, np.float32)
+    lib().or_q4_decode(np.ascontiguousarray(codes), np.ascontiguousarray(scales), n, out)
+    return out
+
+
+def q4_matvec(codes, scales, rows: int, cols: int, x) -> np.ndarray:
+    y = np.empty(rows, np.float32)
+    lib().or_q4_matvec(np.ascontiguousarray(codes), np.ascontiguousarray(scales), rows, cols,
+                       np.ascontiguousarray(x, dtype=np.float32), y)
+    return y

@@ -1,0 +1,63 @@
+"""ctypes binding of the C ABI in ``include/summa_amd.h``.
+
+The library is the in-tree ``summa_amd/libsumma_amd.so`` built by
+``summa_amd.build``. There is no fallback: if it is missing or fails to load,
+every op raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libsumma_amd.so"
+
+SM_OK = 0
+SM_F32, SM_BF16, SM_F16 = 0, 1, 2
+
+_lib = None
+
+vp, i32, i64, u64, f32, f64 = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_float, C.c_double
+
+# name -> (restype, argtypes). Kept in the order of include/summa_amd.h.
+SIGNATURES: dict[str, tuple] = {
+    "sm_version": (i32, []),
+    "sm_last_error": (C.c_char_p, []),
+    "sm_ce_rows": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, f32, vp, vp, vp]),
+    "sm_grpo_loss": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, f64, f64, f64, vp, vp, vp, vp, vp]),
+    "sm_grpo_flags_message": (C.c_char_p, [C.c_int32]),
+    "sm_fill_normal": (i32, [vp, i32, i64, f32, f32, u64, vp]),
+    "sm_fill_ce_stress": (i32, [vp, i32, vp, i64, i64, f32, f32, u64, vp]),
+}
+
+
+class SummaError(RuntimeError):
+    """Raised when a C-ABI call returns a non-zero status."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(message)
+        self.status = status
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is not built; run `python -m summa_amd.build` (no CPU fallback exists)")
+        L = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def check(status: int) -> None:
+    if status != SM_OK:
+        msg = lib().sm_last_error().decode(errors="replace")
+        raise SummaError(status, msg)
+
+
+def call(name: str, *args) -> None:
+    check(getattr(lib(), name)(*args))

@@ -1,0 +1,139 @@
+// Shared host/device helpers for the summa_amd HIP library (gfx950 only).
+//
+// Status convention of every exported entry point: 0 on success, a negative
+// sm_status on failure, with a message retrievable via sm_last_error() from the
+// calling thread. No entry point aborts or throws across the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "../../include/summa_amd.h"
+
+namespace sm {
+
+// ---------------------------------------------------------------- errors ---
+void set_error(const char* fmt, ...) __attribute__((format(printf, 1, 2)));
+void clear_error();
+
+#define SM_REQUIRE(cond, ...)                \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::sm::set_error(__VA_ARGS__);          \
+      return SM_ERR_INVALID;                 \
+    }                                        \
+  } while (0)
+
+#define SM_HIP(call)                                                         \
+  do {                                                                       \
+    hipError_t _e = (call);                                                  \
+    if (_e != hipSuccess) {                                                  \
+      ::sm::set_error("%s failed: %s (%s:%d)", #call, hipGetErrorString(_e), \
+                      __FILE__, __LINE__);                                   \
+      return SM_ERR_HIP;                                                     \
+    }                                                                        \
+  } while (0)
+
+// Checks the launch that was just enqueued.
+#define SM_LAUNCH_CHECK() SM_HIP(hipGetLastError())
+
+#define SM_TRY(expr)              \
+  do {                            \
+    int _s = (expr);              \
+    if (_s != SM_OK) return _s;   \
+  } while (0)
+
+// Native 16-byte vector (usable with the nontemporal load/store builtins).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// ------------------------------------------------------------------ bf16 ---
+// bf16 values travel as raw uint16_t bit patterns; conversions are the IEEE
+// truncation of fp32 with round-to-nearest-even.
+__host__ __device__ inline float bf16_to_f32(uint16_t b) {
+  uint32_t u = static_cast<uint32_t>(b) << 16;
+  float f;
+  __builtin_memcpy(&f, &u, 4);
+  return f;
+}
+
+__host__ __device__ inline uint16_t f32_to_bf16(float f) {
+  uint32_t u;
+  __builtin_memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) {
+    return static_cast<uint16_t>((u >> 16) | 0x40u);  // quiet NaN
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+// Low / high bf16 halves of a packed 32-bit word, as fp32.
+__device__ inline float bf16lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ inline float bf16hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// -------------------------------------------------------- wave reductions ---
+constexpr int kWave = 64;
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ inline double wave_sum_f64(double v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+// Merge two online-softmax partials (max m, sum of exp(x - m) s). Empty
+// partials carry (-inf, 0) and merge as exact zeros.
+__device__ inline void lse_merge(float& m, float& s, float m2, float s2) {
+  float mm = fmaxf(m, m2);
+  float a = (s > 0.f) ? s * __expf(m - mm) : 0.f;
+  float b = (s2 > 0.f) ? s2 * __expf(m2 - mm) : 0.f;
+  m = mm;
+  s = a + b;
+}
+
+__device__ inline void wave_lse(float& m, float& s) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float m2 = __shfl_xor(m, o, kWave);
+    float s2 = __shfl_xor(s, o, kWave);
+    lse_merge(m, s, m2, s2);
+  }
+}
+
+// ------------------------------------------------------------ counter RNG ---
+// SplitMix64 finaliser over a (seed, stream, counter) key. Stateless, so any
+// thread can draw the value for any (row, step, column) without coordination.
+__host__ __device__ inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+__host__ __device__ inline uint64_t rng_key(uint64_t seed, uint64_t stream, uint64_t counter) {
+  return mix64(mix64(seed + 0x9e3779b97f4a7c15ull * (stream + 1)) ^ (counter * 0xd1b54a32d192ed03ull));
+}
+
+// Uniform in (0, 1): 24 random bits, offset by half a step so 0 and 1 never occur.
+__host__ __device__ inline float u01(uint64_t bits) {
+  return (static_cast<float>(bits >> 40) + 0.5f) * (1.0f / 16777216.0f);
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace sm

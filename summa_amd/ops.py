@@ -1,0 +1,147 @@
+"""Host-side mirror of the reference's kernel entry points, over the C ABI.
+
+Tensors are torch device tensors (torch is only the allocator and stream
+provider here); every computation runs in ``libsumma_amd.so``. Names and
+argument meaning follow the reference interfaces cited in each docstring.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+from ._lib import SM_BF16, SM_F16, SM_F32, call
+
+_DTYPES = {torch.float32: SM_F32, torch.bfloat16: SM_BF16, torch.float16: SM_F16}
+
+
+def _stream() -> int:
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dt(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError as e:
+        raise TypeError(f"unsupported dtype {t.dtype}") from e
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _dev(t: torch.Tensor, name: str) -> None:
+    if not t.is_cuda:
+        raise ValueError(f"{name} must be a device tensor")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+# ------------------------------------------------------------------- CE ---
+
+def ce_rows(logits: torch.Tensor, targets: torch.Tensor, logical_vocab: int | None = None, *,
+            grad_in_place: bool = False, grad_scale: float = 1.0,
+            row_scale: torch.Tensor | None = None, want_lse: bool = False,
+            want_loss: bool = True):
+    """Row-wise fused log-softmax / CE / token log-prob.
+
+    Mirrors ``ce_row_statistics`` + ``ce_row_gradient``
+    (summa-llm/src/model/linear_cross_entropy/gpu.rs:29-158) and the
+    ``log_softmax(..).gather(targets)`` of tensor_sleep.rs:2609-2614.
+    Returns ``(token_logprob [rows] f32, loss [1] f32 or None, lse or None)``;
+    with ``grad_in_place`` the logits buffer is overwritten by
+    ``(softmax - onehot) * grad_scale * row_scale``.
+    """
+    _dev(logits, "logits")
+    _dev(targets, "targets")
+    if targets.dtype != torch.int32:
+        raise TypeError("targets must be int32")
+    rows, stored = logits.shape
+    lv = stored if logical_vocab is None else int(logical_vocab)
+    lp = torch.empty(rows, dtype=torch.float32, device=logits.device)
+    loss = torch.empty(1, dtype=torch.float32, device=logits.device) if want_loss else None
+    lse = torch.empty(rows, dtype=torch.float32, device=logits.device) if want_lse else None
+    if row_scale is not None:
+        _dev(row_scale, "row_scale")
+    call("sm_ce_rows", logits.data_ptr(), _dt(logits), targets.data_ptr(), rows, stored, lv,
+         lp.data_ptr(), _p(lse), logits.data_ptr() if grad_in_place else None, float(grad_scale),
+         _p(row_scale), _p(loss), _stream())
+    return lp, loss, lse
+
+
+# ----------------------------------------------------------------- GRPO ---
+
+class GrpoValidationError(ValueError):
+    """Raised with the reference's message when a device validation flag is set."""
+
+
+def grpo_loss_batched(rewards: torch.Tensor, current: torch.Tensor, behavior: torch.Tensor,
+                      reference: torch.Tensor | None, active_mask: torch.Tensor | None,
+                      clip_epsilon: float = 0.2, advantage_epsilon: float = 1e-6,
+                      kl_coefficient: float = 0.04, *, validate: bool = True):
+    """GRPO loss for ``B`` prompt groups at once.
+
+    ``rewards`` [B, G]; ``current``/``behavior``/``reference``/``active_mask``
+    [B, G, T] float32. Returns a dict of device tensors: ``stats`` [B, 5]
+    (loss, mean_reward, reward_stddev, mean_kl, clipped_fraction),
+    ``advantages`` [B, G], ``dlp`` [B, G, T], ``flags`` [B].
+    Follows grpo_loss_tensor (summa-train/src/posttrain.rs:874-1028). With
+    ``validate`` it performs the reference's single validation readback
+    (posttrain.rs:1007-1025) and raises GrpoValidationError.
+    """
+    for name, t in (("rewards", rewards), ("current", current), ("behavior", behavior)):
+        _dev(t, name)
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name} must be float32")
+    B, G, T = current.shape
+    if tuple(rewards.shape) != (B, G):
+        raise ValueError(f"GRPO rewards must have shape [{B}, {G}]")
+    for name, t in (("behavior", behavior), ("active_mask", active_mask), ("reference", reference)):
+        if t is not None:
+            _dev(t, name)
+            if tuple(t.shape) != (B, G, T):
+                raise ValueError(f"GRPO {name} tensor must have shape [{G}, {T}]")
+    dev = current.device
+    stats = torch.empty(B, 5, dtype=torch.float32, device=dev)
+    adv = torch.empty(B, G, dtype=torch.float32, device=dev)
+    dlp = torch.empty(B, G, T, dtype=torch.float32, device=dev)
+    flags = torch.empty(B, dtype=torch.int32, device=dev)
+    call("sm_grpo_loss", rewards.data_ptr(), current.data_ptr(), behavior.data_ptr(),
+         _p(reference), _p(active_mask), B, G, T, float(clip_epsilon), float(advantage_epsilon),
+         float(kl_coefficient), stats.data_ptr(), adv.data_ptr(), dlp.data_ptr(),
+         flags.data_ptr(), _stream())
+    if validate:
+        bad = flags.cpu()
+        for f in bad.tolist():
+            if f:
+                raise GrpoValidationError(_lib.lib().sm_grpo_flags_message(f).decode())
+    return {"stats": stats, "advantages": adv, "dlp": dlp, "flags": flags}
+
+
+def grpo_loss_tensor(rewards, current, behavior, reference, active_mask, clip_epsilon,
+                     advantage_epsilon, kl_coefficient):
+    """Single-group form of grpo_loss_tensor (posttrain.rs:874): [G] rewards,
+    [G, T] log-probs and mask; returns the scalar loss as a [1] device tensor."""
+    out = grpo_loss_batched(
+        rewards.unsqueeze(0), current.unsqueeze(0), behavior.unsqueeze(0),
+        None if reference is None else reference.unsqueeze(0),
+        None if active_mask is None else active_mask.unsqueeze(0),
+        clip_epsilon, advantage_epsilon, kl_coefficient)
+    return out["stats"][0, 0:1]
+
+
+# ------------------------------------------------------------ synthetic ---
+
+def fill_normal(t: torch.Tensor, mean: float, std: float, seed: int) -> torch.Tensor:
+    _dev(t, "out")
+    call("sm_fill_normal", t.data_ptr(), _dt(t), t.numel(), float(mean), float(std), int(seed),
+         _stream())
+    return t
+
+
+def fill_ce_stress(logits: torch.Tensor, targets: torch.Tensor, std: float = 3.0,
+                   spike: float = 8.0, seed: int = 0):
+    _dev(logits, "logits")
+    rows, vocab = logits.shape
+    call("sm_fill_ce_stress", logits.data_ptr(), _dt(logits), targets.data_ptr(), rows, vocab,
+         float(std), float(spike), int(seed), _stream())
+    return logits, targets

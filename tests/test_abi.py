@@ -1,0 +1,54 @@
+"""The C-ABI library loads and exports every entry point declared in include/*.h."""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from summa_amd import _lib
+
+ROOT = Path(__file__).resolve().parent.parent
+DECL = re.compile(r"^\s*(?:const\s+)?\w+\s*\*?\s*(sm_\w+)\s*\(", re.M)
+
+
+def declared():
+    names = []
+    for h in sorted((ROOT / "include").glob("*.h")):
+        names += DECL.findall(h.read_text())
+    return names
+
+
+def test_header_declares_entry_points():
+    names = declared()
+    assert "sm_ce_rows" in names and "sm_grpo_loss" in names
+    assert len(names) == len(set(names))
+
+
+def test_library_exports_every_declared_symbol():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail("libsumma_amd.so not built (python -m summa_amd.build)")
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [n for n in declared() if not hasattr(raw, n)]
+    assert not missing, missing
+
+
+def test_binding_table_matches_header():
+    assert set(_lib.SIGNATURES) == set(declared())
+
+
+def test_host_only_calls():
+    L = _lib.lib()
+    assert L.sm_version() >= 1
+    assert L.sm_grpo_flags_message(0) is None
+    assert L.sm_grpo_flags_message(1 << 3).decode() == \
+        "GRPO active_mask must contain only binary zero/one values"
+
+
+def test_argument_errors_are_reported_not_raised():
+    L = _lib.lib()
+    # invalid clip epsilon is rejected before any device work
+    st = L.sm_grpo_loss(1, 1, 1, None, None, 1, 2, 1, 1.5, 1e-6, 0.0, None, None, None, None, None)
+    assert st == -1
+    assert L.sm_last_error().decode() == "GRPO clip_epsilon must be finite and in (0, 1)"
+    st = L.sm_ce_rows(1, 1, 1, 4, 8, 9, None, None, None, 1.0, None, None, None)
+    assert st == -1 and b"logical vocabulary 9" in L.sm_last_error()

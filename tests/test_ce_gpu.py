@@ -1,0 +1,85 @@
+"""Fused CE / token log-prob on the GPU vs the f64 CPU oracle (sm_ce_rows)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from summa_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(dev, x_np, t_np, dtype, lv=None, grad=False, scale=1.0, row_scale=None):
+    if x_np.dtype == np.uint16:
+        x = torch.from_numpy(x_np.view(np.int16)).to(dev).view(torch.bfloat16)
+    else:
+        x = torch.from_numpy(x_np).to(dev)
+    t = torch.from_numpy(t_np).to(dev)
+    rs = None if row_scale is None else torch.from_numpy(row_scale.astype(np.float32)).to(dev)
+    lp, loss, lse = ops.ce_rows(x, t, lv, grad_in_place=grad, grad_scale=scale, row_scale=rs,
+                                want_lse=True)
+    torch.cuda.synchronize()
+    g = x.float().cpu().numpy() if grad else None
+    return lp.cpu().numpy(), loss.cpu().numpy()[0], lse.cpu().numpy(), g
+
+
+@pytest.mark.parametrize("rows,vocab,lv", [(7, 64, 50), (5, 4096, 4096), (3, 32768, 32768),
+                                           (4, 1001, 999), (2, 131072, 131072), (1, 3, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ce_lp_matches_oracle(dev, rows, vocab, lv, dtype):
+    print(f"case rows={rows} vocab={vocab} lv={lv} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(rows * 7 + vocab)
+    x = rng.normal(0, 3, (rows, vocab)).astype(np.float32)
+    t = rng.integers(0, lv, rows).astype(np.int32)
+    xin = oracle.bf16_bits(x) if dtype == torch.bfloat16 else x
+    lp, loss, lse, _ = _run(dev, xin, t, dtype, lv)
+    lp_ref, lse_ref, _ = oracle.ce_rows(xin, t, lv)
+    # fp32 arithmetic on the device vs f64 oracle: 1e-5 abs (BASELINE fp32 bound)
+    np.testing.assert_allclose(lp, lp_ref, atol=1e-5, rtol=0)
+    np.testing.assert_allclose(lse, lse_ref, atol=1e-5, rtol=0)
+    assert abs(loss - (-lp_ref.mean())) < 1e-5
+
+
+@pytest.mark.parametrize("rows,vocab,lv", [(7, 64, 50), (3, 4096, 4096), (2, 131072, 131072),
+                                           (2, 200000, 199990), (3, 1001, 1000)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_ce_grad_in_place(dev, rows, vocab, lv, dtype):
+    print(f"case rows={rows} vocab={vocab} lv={lv} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(rows + vocab)
+    x = rng.normal(0, 3, (rows, vocab)).astype(np.float32)
+    t = rng.integers(0, lv, rows).astype(np.int32)
+    rs = rng.normal(0, 1, rows)
+    xin = oracle.bf16_bits(x) if dtype == torch.bfloat16 else x
+    lp, loss, lse, g = _run(dev, xin, t, dtype, lv, grad=True, scale=0.5, row_scale=rs)
+    lp_ref, _, g_ref = oracle.ce_rows(xin, t, lv, grad=True, grad_scale=0.5, row_scale=rs)
+    np.testing.assert_allclose(lp, lp_ref, atol=1e-5, rtol=0)
+    assert np.all(g[:, lv:] == 0)  # padded columns: exact zeros
+    if dtype == torch.bfloat16:
+        # gradient emitted in bf16: one rounding of |g| <= |scale|
+        np.testing.assert_allclose(g, g_ref, rtol=2 ** -8, atol=1e-6)
+    else:
+        np.testing.assert_allclose(g, g_ref, rtol=1e-4, atol=1e-7)
+
+
+def test_ce_stress_generator_and_spike(dev):
+    # config[3] shape scaled down: N(0,3) + one +8 spike per row at the target
+    rows, vocab = 64, 131072
+    x = torch.empty(rows, vocab, dtype=torch.bfloat16, device=dev)
+    t = torch.empty(rows, dtype=torch.int32, device=dev)
+    ops.fill_ce_stress(x, t, 3.0, 8.0, seed=5)
+    lp, loss, _ = ops.ce_rows(x, t)
+    xs = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    tn = t.cpu().numpy()
+    lp_ref, _, _ = oracle.ce_rows(xs, tn)
+    np.testing.assert_allclose(lp.cpu().numpy(), lp_ref, atol=1e-5)
+    xf = oracle.bf16_to_f32(xs)
+    assert abs(float(xf.std()) - 3.0) < 0.02 and abs(float(xf.mean())) < 0.02
+    assert np.all(xf[np.arange(rows), tn] > 2.0)  # spikes are present
+
+
+def test_ce_bad_targets_give_nan_not_fault(dev):
+    x = torch.zeros(3, 64, device=dev)
+    t = torch.tensor([0, 64, -1], dtype=torch.int32, device=dev)
+    lp, _, _ = ops.ce_rows(x, t, want_loss=False)
+    v = lp.cpu().numpy()
+    assert abs(v[0] + np.log(64)) < 1e-6 and np.isnan(v[1]) and np.isnan(v[2])
