@@ -74,7 +74,8 @@ def test_ce_stress_generator_and_spike(dev):
     np.testing.assert_allclose(lp.cpu().numpy(), lp_ref, atol=1e-5)
     xf = oracle.bf16_to_f32(xs)
     assert abs(float(xf.std()) - 3.0) < 0.02 and abs(float(xf.mean())) < 0.02
-    assert np.all(xf[np.arange(rows), tn] > 2.0)  # spikes are present
+    # spikes present: N(0,3) + 8 at the targets has mean 8 (64 samples: sd 0.375)
+    assert abs(float(xf[np.arange(rows), tn].mean()) - 8.0) < 1.5
 
 
 def test_ce_bad_targets_give_nan_not_fault(dev):
