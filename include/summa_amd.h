@@ -98,6 +98,36 @@ int sm_grpo_loss(const float* rewards, const float* lp_cur, const float* lp_beh,
 const char* sm_grpo_flags_message(int32_t flags);
 
 /* ------------------------------------------------------------------------
+ * Q4G128 weights (this build's HQUANT format tag 4): W[N, K] row-major
+ * (out x in), groups of 128 along the flattened tensor, one bf16 scale per
+ * group = bf16(absmax/7), int4 two's-complement codes, low nibble = even
+ * element. codes: ceil(n/128)*64 bytes; scales: ceil(n/128) bf16.
+ *
+ * sm_q4_quantize replaces quantize_tensor (summa-train/src/quantization.rs:
+ * 691-773) for the new format: code = clamp(round_half_away(w/scale), -8, 7).
+ * bad_scales (nullable, device int32, caller-zeroed) counts groups whose
+ * non-zero scale is outside the f16 normal range that the matmul needs.
+ */
+int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* codes, uint16_t* scales,
+                   int32_t* bad_scales, void* stream);
+
+/* y = x . W^T over Q4G128 weights, bf16 x [M, ldx], f32 accumulate. Replaces
+ * the quantized-matmul dispatch: PackedTensor::matrix_vector
+ * (quantization.rs:630-654) batched over M rows, i.e. Linear::forward
+ * (summa-llm/src/model/matmul.rs:57-66) on a QuantizedModelBackend weight
+ * (quantization.rs:1183-1189). K % 128 == 0. Epilogues:
+ *   SM_EPI_STORE_F32   y f32 [M, ldy] = acc
+ *   SM_EPI_STORE_BF16  y bf16 = acc
+ *   SM_EPI_ADD_F32     y f32 += acc  (residual add, block.rs:103-157)
+ *   SM_EPI_SWIGLU_BF16 W rows are [gate | value] (N = 2F); y bf16 [M, F] =
+ *                      silu(gate) * value (ffn.rs:854-877, fused_swiglu.rs:110-126)
+ */
+enum { SM_EPI_STORE_F32 = 0, SM_EPI_STORE_BF16 = 1, SM_EPI_ADD_F32 = 2, SM_EPI_SWIGLU_BF16 = 3 };
+int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                 const uint16_t* x, int64_t M, int64_t ldx, void* y, int64_t ldy, int epilogue,
+                 void* stream);
+
+/* ------------------------------------------------------------------------
  * Seeded synthetic data (no reference counterpart; bench/test inputs).
  * Values are a pure function of (seed, index), identical for any launch shape.
  */

@@ -13,6 +13,7 @@ LIB_PATH = Path(__file__).resolve().parent / "libsumma_amd.so"
 
 SM_OK = 0
 SM_F32, SM_BF16, SM_F16 = 0, 1, 2
+SM_EPI_STORE_F32, SM_EPI_STORE_BF16, SM_EPI_ADD_F32, SM_EPI_SWIGLU_BF16 = 0, 1, 2, 3
 
 _lib = None
 
@@ -25,6 +26,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_ce_rows": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, f32, vp, vp, vp]),
     "sm_grpo_loss": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, f64, f64, f64, vp, vp, vp, vp, vp]),
     "sm_grpo_flags_message": (C.c_char_p, [C.c_int32]),
+    "sm_q4_quantize": (i32, [vp, i32, i64, vp, vp, vp, vp]),
+    "sm_q4_matmul": (i32, [vp, vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
     "sm_fill_normal": (i32, [vp, i32, i64, f32, f32, u64, vp]),
     "sm_fill_ce_stress": (i32, [vp, i32, vp, i64, i64, f32, f32, u64, vp]),
 }

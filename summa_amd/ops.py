@@ -145,3 +145,68 @@ def fill_ce_stress(logits: torch.Tensor, targets: torch.Tensor, std: float = 3.0
     call("sm_fill_ce_stress", logits.data_ptr(), _dt(logits), targets.data_ptr(), rows, vocab,
          float(std), float(spike), int(seed), _stream())
     return logits, targets
+
+
+# ----------------------------------------------------------------- Q4G128 ---
+
+class Q4Weight:
+    """A Q4G128 weight resident in HBM: W[N, K] (out x in), codes + bf16 scales.
+
+    Device counterpart of ``PackedTensor`` (summa-train/src/quantization.rs:416-423)
+    for this build's 4-bit format (HQUANT tag 4)."""
+
+    def __init__(self, codes: torch.Tensor, scales: torch.Tensor, n: int, k: int):
+        self.codes, self.scales, self.n, self.k = codes, scales, n, k
+
+    @property
+    def nbytes(self) -> int:
+        return self.codes.numel() + 2 * self.scales.numel()
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor) -> "Q4Weight":
+        """Quantize a dense device weight [N, K] (f32 or bf16)."""
+        _dev(w, "weight")
+        n, k = w.shape
+        groups = (w.numel() + 127) // 128
+        codes = torch.empty(groups * 64, dtype=torch.uint8, device=w.device)
+        scales = torch.empty(groups, dtype=torch.int16, device=w.device)
+        bad = torch.zeros(1, dtype=torch.int32, device=w.device)
+        call("sm_q4_quantize", w.data_ptr(), _dt(w), w.numel(), codes.data_ptr(),
+             scales.data_ptr(), bad.data_ptr(), _stream())
+        if int(bad.item()):
+            raise ValueError(f"{int(bad.item())} Q4 groups have a scale outside the f16 normal range")
+        return cls(codes, scales, n, k)
+
+    @classmethod
+    def from_host(cls, codes, scales, n: int, k: int, device) -> "Q4Weight":
+        """Upload host codes (uint8) and scales (bf16 bits as uint16)."""
+        import numpy as np
+
+        c = torch.from_numpy(np.ascontiguousarray(codes)).to(device)
+        s = torch.from_numpy(np.ascontiguousarray(scales).view(np.int16)).to(device)
+        return cls(c, s, n, k)
+
+
+def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
+              epilogue: int = _lib.SM_EPI_STORE_F32) -> torch.Tensor:
+    """y = x . W^T with Q4G128 weights; x bf16 [M, K]."""
+    _dev(x, "x")
+    if x.dtype != torch.bfloat16:
+        raise TypeError("x must be bfloat16")
+    M, K = x.shape
+    if K != w.k:
+        raise ValueError(f"packed linear input width mismatch ({K} != {w.k})")
+    if epilogue == _lib.SM_EPI_SWIGLU_BF16:
+        shape, dt = (M, w.n // 2), torch.bfloat16
+    elif epilogue == _lib.SM_EPI_STORE_BF16:
+        shape, dt = (M, w.n), torch.bfloat16
+    else:
+        shape, dt = (M, w.n), torch.float32
+    if out is None:
+        if epilogue == _lib.SM_EPI_ADD_F32:
+            raise ValueError("SM_EPI_ADD_F32 needs an output to accumulate into")
+        out = torch.empty(shape, dtype=dt, device=x.device)
+    _dev(out, "out")
+    call("sm_q4_matmul", w.codes.data_ptr(), w.scales.data_ptr(), w.n, w.k, x.data_ptr(), M,
+         x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
+    return out

@@ -1,0 +1,93 @@
+"""Q4G128 quantizer and quantized matmul (sm_q4_quantize / sm_q4_matmul) vs the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from summa_amd import _lib, ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _weights(n, k, seed):
+    return np.random.default_rng(seed).normal(0, 0.02, (n, k)).astype(np.float32)
+
+
+def _bf16_dev(a, dev):
+    return torch.from_numpy(oracle.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _oracle_matmul(codes, scales, n, k, xr):
+    return np.stack([oracle.q4_matvec(codes, scales, n, k, xr[m]) for m in range(xr.shape[0])])
+
+
+def _bound(codes, scales, n, k, xr):
+    dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+    return np.abs(xr.astype(np.float64)) @ np.abs(dense).T
+
+
+@pytest.mark.parametrize("n,k", [(96, 256), (2304, 768), (5, 1000)])
+def test_quantizer_bit_exact(dev, n, k):
+    w = _weights(n, k, 1)
+    w[0, :128] = 0.0  # all-zero group -> scale 0, codes 0
+    codes, scales = oracle.q4_quantize(w)
+    q = ops.Q4Weight.quantize(torch.from_numpy(w).to(dev))
+    np.testing.assert_array_equal(q.codes.cpu().numpy(), codes)
+    np.testing.assert_array_equal(q.scales.cpu().numpy().view(np.uint16), scales)
+    # bf16 input path
+    wb = oracle.bf16_bits(w)
+    codes_b, scales_b = oracle.q4_quantize(oracle.bf16_to_f32(wb))
+    qb = ops.Q4Weight.quantize(_bf16_dev(w, dev))
+    np.testing.assert_array_equal(qb.codes.cpu().numpy(), codes_b)
+    np.testing.assert_array_equal(qb.scales.cpu().numpy().view(np.uint16), scales_b)
+
+
+@pytest.mark.parametrize("n,k", [(96, 256), (2304, 768), (768, 768), (130, 5632), (32768, 768)])
+@pytest.mark.parametrize("m", [1, 3, 16, 17, 64, 128, 200])
+def test_matmul_matches_oracle(dev, n, k, m):
+    if n * k * m > 2304 * 768 * 128 and m > 17:
+        pytest.skip("oracle cost")
+    print(f"case n={n} k={k} m={m}", flush=True)
+    w = _weights(n, k, n + k)
+    codes, scales = oracle.q4_quantize(w)
+    x = np.random.default_rng(m).normal(0, 1, (m, k)).astype(np.float32)
+    xr = oracle.round_bf16(x)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    y = ops.q4_matmul(qw, _bf16_dev(x, dev)).cpu().numpy()
+    y_ref = _oracle_matmul(codes, scales, n, k, xr)
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    assert np.all(np.abs(y - y_ref) <= tol), float(np.abs(y - y_ref).max())
+
+
+def test_epilogues(dev):
+    n, k, m = 512, 768, 9
+    w = _weights(n, k, 7)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(0).normal(0, 1, (m, k)).astype(np.float32)
+    xr = oracle.round_bf16(x)
+    xd = _bf16_dev(x, dev)
+    y_ref = _oracle_matmul(codes, scales, n, k, xr)
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    # bf16 store: one rounding of the f32 result
+    yb = ops.q4_matmul(qw, xd, epilogue=_lib.SM_EPI_STORE_BF16).float().cpu().numpy()
+    assert np.all(np.abs(yb - y_ref) <= np.abs(y_ref) * 2 ** -8 + tol)
+    # residual add into f32
+    base = np.random.default_rng(1).normal(0, 1, (m, n)).astype(np.float32)
+    acc = torch.from_numpy(base.copy()).to(dev)
+    ops.q4_matmul(qw, xd, out=acc, epilogue=_lib.SM_EPI_ADD_F32)
+    assert np.all(np.abs(acc.cpu().numpy() - (base + y_ref)) <= tol + 1e-6)
+    # SwiGLU over [gate | value]: h = silu(gate) * value, bf16
+    F = n // 2
+    h = ops.q4_matmul(qw, xd, epilogue=_lib.SM_EPI_SWIGLU_BF16).float().cpu().numpy()
+    g, v = y_ref[:, :F], y_ref[:, F:]
+    h_ref = g / (1 + np.exp(-g)) * v
+    assert h.shape == (m, F)
+    np.testing.assert_allclose(h, h_ref, rtol=2 ** -7, atol=1e-6)
+
+
+def test_rejects_bad_shapes(dev):
+    w = ops.Q4Weight.quantize(torch.zeros(64, 256, device=dev))
+    with pytest.raises(_lib.SummaError, match="width mismatch|K="):
+        bad = ops.Q4Weight(w.codes, w.scales, 64, 200)
+        ops.q4_matmul(bad, torch.zeros(2, 200, dtype=torch.bfloat16, device=dev))
