@@ -2,6 +2,10 @@
 """Benchmark of the GRPO RL-step hot path on one MI355X.
 
 Prints ONE JSON line (the driver's contract). Workloads:
+  rl_step    config[1] (default): 12-layer d768 Q4G128 decoder, 16 prompts x 8
+             rollouts, 128-token prompts, 256 sampled tokens at T=1.0, then the
+             log-prob recompute of policy + frozen reference and the GRPO loss.
+             value = rollout tok/s; ms_per_step = whole RL step.
   ce_stress  config[3]: fused log-softmax/CE/token-logprob over bf16
              [65536 x 131072] logits (HBM-bound).
 Timing: W warmup steps, then K timed steps bracketed by synchronisation; kernel
@@ -94,15 +98,158 @@ def bench_ce_stress(args) -> dict:
     return res
 
 
-WORKLOADS = {"ce_stress": bench_ce_stress}
+CFG1 = dict(layers=12, d_model=768, heads=12, kv_heads=12, head_dim=64, ffn=3072, vocab=32768)
+
+
+def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 20) -> dict:
+    """M=1 Q4G128 GEMV over every linear of the model (whole-model weight sweep),
+    HIP events on the launch stream; bytes = N*K*(0.5 + 2/128) + (K + N*4)."""
+    import torch
+
+    from summa_amd import _lib, ops
+
+    d, F, V = model_cfg["d_model"], model_cfg["ffn"], model_cfg["vocab"]
+    qn = (model_cfg["heads"] + 2 * model_cfg["kv_heads"]) * model_cfg["head_dim"]
+    shapes = [(qn, d), (d, model_cfg["heads"] * model_cfg["head_dim"]), (2 * F, d), (d, F)]
+    mats = []
+    for layer in range(model_cfg["layers"]):
+        for n, k in shapes:
+            w = torch.empty(n, k, device=dev)
+            ops.fill_normal(w, 0.0, 0.02, seed=layer * 10 + n)
+            mats.append(ops.Q4Weight.quantize(w))
+    w = torch.empty(V, d, device=dev)
+    ops.fill_normal(w, 0.0, 0.02, seed=99)
+    mats.append(ops.Q4Weight.quantize(w))
+    del w
+    kmax = max(m.k for m in mats)
+    x = torch.randn(1, kmax, device=dev).to(torch.bfloat16)
+    ys = [torch.empty(1, m.n, device=dev) for m in mats]
+    xs = [x[:, :m.k].contiguous() for m in mats]
+    st = torch.cuda.current_stream()
+    for _ in range(3):
+        for m, xi, y in zip(mats, xs, ys):
+            ops.q4_matmul(m, xi, out=y)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(st)
+    for _ in range(reps):
+        for m, xi, y in zip(mats, xs, ys):
+            ops.q4_matmul(m, xi, out=y)
+    b.record(st)
+    torch.cuda.synchronize()
+    sweep_ms = a.elapsed_time(b) / reps
+    nbytes = sum(m.nbytes + m.k * 2 + m.n * 4 for m in mats)
+    # largest single matrix (LM head) on its own
+    big = mats[-1]
+    a.record(st)
+    for _ in range(reps):
+        ops.q4_matmul(big, xs[-1], out=ys[-1])
+    b.record(st)
+    torch.cuda.synchronize()
+    big_ms = a.elapsed_time(b) / reps
+    big_bytes = big.nbytes + big.k * 2 + big.n * 4
+    return {"sweep_ms": sweep_ms, "sweep_bytes": nbytes, "sweep_GBs": nbytes / sweep_ms / 1e6,
+            "launches": len(mats), "lm_head_ms": big_ms, "lm_head_bytes": big_bytes,
+            "lm_head_GBs": big_bytes / big_ms / 1e6}
+
+
+def cpu_baseline_rl(seconds_cap: float = 60.0) -> dict:
+    """Oracle (C restatement, OpenMP over the host cores) rollout on a bounded
+    sample of config[1]: 2 rollouts x (128-token prompt + 8 sampled tokens)."""
+    import numpy as np
+
+    import oracle
+
+    cfg = {"layers": CFG1["layers"], "d": CFG1["d_model"], "H": CFG1["heads"],
+           "KVH": CFG1["kv_heads"], "hd": CFG1["head_dim"], "F": CFG1["ffn"], "V": CFG1["vocab"]}
+    w = oracle.random_weights(cfg, seed=0, std=0.02)
+    host = oracle.HostModel(cfg, w, quantized=True)
+    S, P, N = 2, 128, 8
+    prompts = np.random.default_rng(0).integers(0, cfg["V"], (S, P)).astype(np.int32)
+    t0 = time.perf_counter()
+    host.generate(prompts, N, 1.0, 0)
+    dt = time.perf_counter() - t0
+    return {"value": round(S * N / dt, 3), "unit": "rollout tok/s", "cores": os.cpu_count(),
+            "kind": "port",
+            "sample": f"config[1] Q4 model, {S} rollouts x ({P}-token prompt + {N} sampled), "
+                      f"{dt:.1f} s"}
+
+
+def bench_rl_step(args) -> dict:
+    import torch
+
+    from summa_amd.model import Model, ModelConfig, batch_result, rl_prepare
+
+    groups, G, P, N = 16, 8, 128, 256
+    S = groups * G
+    dev = torch.device("cuda:0")
+    mc = ModelConfig(**CFG1, max_seq=P + N, quantized=True)
+    policy = Model(mc)
+    policy.init_random(seed=0, std=0.02)
+    reference = Model(mc)
+    reference.init_random(seed=0, std=0.02)  # frozen copy of the initial policy
+    gen = torch.Generator().manual_seed(0)
+    prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
+    rewards = torch.bernoulli(torch.full((groups, G), 0.3), generator=gen).to(dev)
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+
+    def step(seed):
+        tok, lp_beh = policy.generate(prompts, N, temperature=1.0, seed=seed)
+        e_mid.record(st)
+        out = rl_prepare(policy, reference, prompts, tok, lp_beh, rewards, clip_epsilon=0.2,
+                         advantage_epsilon=1e-6, kl_coefficient=0.04)
+        return out
+
+    e0, e_mid, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    log("bench: warmup")
+    for i in range(args.warmup):
+        step(1000 + i)
+    torch.cuda.synchronize()
+    roll_ms, step_ms = [], []
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        e0.record(st)
+        out = step(i)
+        e1.record(st)
+        torch.cuda.synchronize()
+        roll_ms.append(e0.elapsed_time(e_mid))
+        step_ms.append(e0.elapsed_time(e1))
+        log(f"bench: step {i} rollout {roll_ms[-1]:.1f} ms, RL step {step_ms[-1]:.1f} ms")
+    wall = time.perf_counter() - t0
+    res = batch_result(out)
+    roll = sum(roll_ms) / len(roll_ms)
+    full = sum(step_ms) / len(step_ms)
+    log("bench: q4 gemv sweep")
+    sweep = q4_gemv_sweep(CFG1, dev)
+    achieved = sweep["sweep_GBs"]
+    return {
+        "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
+        "value": S * N / (roll * 1e-3), "unit": "rollout tok/s",
+        "ms_per_step": full, "dtype": "q4g128 weights x bf16 activations, f32 accumulate",
+        "config": {"workload": "rl_step config[1]", "layers": 12, "d_model": 768, "heads": 12,
+                   "ffn": 3072, "vocab": 32768, "prompts": groups, "group": G,
+                   "prompt_len": P, "new_tokens": N, "temperature": 1.0,
+                   "weights": "Q4G128 (bf16 scales)", "rewards": "Bernoulli(0.3)"},
+        "rl_step_ms": round(full, 3), "rollout_ms": round(roll, 3),
+        "prepare_ms": round(full - roll, 3), "wall_s": round(wall, 3),
+        "grpo": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()},
+        "roofline": {"bound": "hbm", "kernel": "q4 GEMV M=1, whole-model weight sweep",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
+        "q4_gemv": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sweep.items()},
+    }
+
+
+WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress}
 
 
 def main() -> int:
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=3)
-    p.add_argument("--workload", default="ce_stress", choices=sorted(WORKLOADS))
+    p.add_argument("--steps", type=int, default=3)
+    p.add_argument("--warmup", type=int, default=1)
+    p.add_argument("--workload", default="rl_step", choices=sorted(WORKLOADS))
     p.add_argument("--rows", type=int, default=65536)
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args()
@@ -121,7 +268,8 @@ def main() -> int:
     out.update(res)
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
-        out["cpu_baseline"] = cpu_baseline_ce(256, 131072)
+        out["cpu_baseline"] = (cpu_baseline_rl() if args.workload == "rl_step"
+                               else cpu_baseline_ce(256, 131072))
     print(json.dumps(out), flush=True)
     return 0
 

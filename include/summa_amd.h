@@ -111,7 +111,8 @@ const char* sm_grpo_flags_message(int32_t flags);
 int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* codes, uint16_t* scales,
                    int32_t* bad_scales, void* stream);
 
-/* y = x . W^T over Q4G128 weights, bf16 x [M, ldx], f32 accumulate. Replaces
+/* y = x . W^T over Q4G128 weights, x [M, ldx] bf16 or f16 (x_dtype), f32
+ * accumulate. Replaces
  * the quantized-matmul dispatch: PackedTensor::matrix_vector
  * (quantization.rs:630-654) batched over M rows, i.e. Linear::forward
  * (summa-llm/src/model/matmul.rs:57-66) on a QuantizedModelBackend weight
@@ -121,11 +122,142 @@ int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* codes, uint16_t
  *   SM_EPI_ADD_F32     y f32 += acc  (residual add, block.rs:103-157)
  *   SM_EPI_SWIGLU_BF16 W rows are [gate | value] (N = 2F); y bf16 [M, F] =
  *                      silu(gate) * value (ffn.rs:854-877, fused_swiglu.rs:110-126)
+ *   SM_EPI_SWIGLU_F16  same with f16 output
  */
-enum { SM_EPI_STORE_F32 = 0, SM_EPI_STORE_BF16 = 1, SM_EPI_ADD_F32 = 2, SM_EPI_SWIGLU_BF16 = 3 };
+enum {
+  SM_EPI_STORE_F32 = 0,
+  SM_EPI_STORE_BF16 = 1,
+  SM_EPI_ADD_F32 = 2,
+  SM_EPI_SWIGLU_BF16 = 3,
+  SM_EPI_SWIGLU_F16 = 4
+};
 int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
-                 const uint16_t* x, int64_t M, int64_t ldx, void* y, int64_t ldy, int epilogue,
-                 void* stream);
+                 const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
+                 int epilogue, void* stream);
+
+/* Dense fp32 y = x . W^T (fp32 models; matmul::linear, summa-llm/src/model/
+ * matmul.rs:57-66). epilogue: SM_EPI_STORE_F32 or SM_EPI_ADD_F32. */
+int sm_gemm_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t M, int64_t ldx,
+                float* y, int64_t ldy, int epilogue, void* stream);
+/* out[r, c] = silu(gv[r, c]) * gv[r, F + c] (ffn.rs:854-886 gated activation). */
+int sm_swiglu_f32(const float* gate_value, int64_t rows, int64_t F, float* out, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decoder elementwise ops.
+ * sm_embed: x[r] = table[ids[r]] * scale, f32 out (Transformer::embed,
+ *   summa-llm/src/model/transformer.rs:511-518); out-of-range ids give NaN rows.
+ * sm_rmsnorm: y = x / sqrt(mean(x^2) + eps) * gamma, fp32 statistics
+ *   (Norm::forward, summa-llm/src/model/norm.rs:36-50), y in out_dtype
+ *   (SM_F32, SM_BF16 or SM_F16).
+ * sm_rope_append: qkv [S*L, (H+2KVH)*hd] f32 -> q_out [S*L, H, hd] with RoPE,
+ *   K (RoPE) and V written to caches [S, KVH, cap, hd] at position pos0[s]+i
+ *   (project_qkv + AttnCache slice_assign, attention.rs:142-177, 331-356).
+ *   rope_table [max_pos, hd/2, 2] f32 (cos, sin), adjacent-pair convention.
+ */
+int sm_embed(const void* table, int dtype, const int32_t* ids, int64_t rows, int64_t d,
+             int64_t vocab, float scale, float* x, void* stream);
+int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int64_t d, float eps, void* y,
+               int out_dtype, void* stream);
+int sm_rope_append(const float* qkv, const float* rope_table, const int32_t* pos0, int64_t S,
+                   int64_t L, int64_t H, int64_t KVH, int64_t head_dim, int64_t cap, void* q_out,
+                   int q_dtype, void* kcache, void* vcache, int cache_dtype, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Attention over the KV cache [S, KVH, cap, hd] (AttnCache, attention.rs:20-40).
+ * sm_attn_decode: one query per sequence, q/out [S, H, hd], keys 0..lens[s]-1
+ *   (forward_cached -> sdpa -> attention(q, repeat_kv(k), repeat_kv(v)),
+ *   attention.rs:216-265, 318-371; repeat_kv fused_attention.rs:114-125).
+ * sm_attn_prefill: causal, q/out [S, L, H, hd], row i at position pos0[s]+i
+ *   attends keys 0..=pos0[s]+i (fused_attention / CubeK flash forward,
+ *   attention.rs:250, cube_attention.rs:127-220).
+ * dtype (q and cache) SM_BF16 (MFMA kernels, out_dtype SM_BF16 or SM_F16) or
+ * SM_F32 (VALU, out_dtype SM_F32); head_dim 64 or 128.
+ */
+int sm_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* lens,
+                   void* out, int dtype, int out_dtype, int64_t S, int64_t H, int64_t KVH,
+                   int64_t cap, int64_t head_dim, void* stream);
+int sm_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* pos0,
+                    void* out, int dtype, int out_dtype, int64_t S, int64_t L, int64_t H,
+                    int64_t KVH, int64_t cap, int64_t head_dim, void* stream);
+
+/* Next-token selection for `rows` logits rows (select_next_token /
+ * sample_from_logits, summa-llm/src/generate.rs:127-202). temperature <= 0:
+ * greedy, first max wins ties; otherwise Gumbel-max sampling from
+ * softmax(logits / T) with the counter RNG keyed (seed, row, step) — one
+ * substream per rollout, as ModelExecutionRngRange (posttrain.rs:1043).
+ * tokens[r*tok_stride] <- token; logprobs[r*lp_stride] (nullable) <-
+ * log_softmax(logits)[token]; next_ids[r] (nullable) <- token. */
+int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab, float temperature,
+              uint64_t seed, int64_t step, int32_t* tokens, int64_t tok_stride, float* logprobs,
+              int64_t lp_stride, int32_t* next_ids, void* stream);
+
+/* ------------------------------------------------------------------------
+ * Decoder model (the MAL Transformer subset the configs use,
+ * summa-llm/src/model/transformer.rs, block.rs, attention.rs, ffn.rs) and the
+ * RL-step runtime behind GrpoDeviceBatchRuntime (posttrain.rs:1288-1305).
+ */
+typedef struct sm_model_config {
+  int32_t layers, d_model, heads, kv_heads, head_dim, ffn, vocab;
+  int32_t max_seq;   /* RoPE table rows = largest cache capacity */
+  float norm_eps;    /* RMSNorm epsilon (MAL default 1e-5) */
+  float rope_theta;  /* MAL default 1e4 */
+  int32_t quantized; /* 1: Q4G128 linears, f16 matmul inputs, bf16 q/KV/embedding;
+                        0: all fp32 */
+} sm_model_config;
+
+typedef struct sm_model sm_model;
+
+/* Tensor kinds for sm_model_set_tensor. Linear weights are [out, in]
+ * (transpose of Burn's Linear [d_in, d_out]); QKV rows are [q | k | v]
+ * (attention.rs:92), IN rows are [gate | value] (ffn.rs:64-88). */
+enum {
+  SM_W_EMBED = 0,      /* [vocab, d] */
+  SM_W_ATTN_NORM = 1,  /* [d] per layer */
+  SM_W_QKV = 2,        /* [H*hd + 2*KVH*hd, d] per layer */
+  SM_W_O = 3,          /* [d, H*hd] per layer */
+  SM_W_FFN_NORM = 4,   /* [d] per layer */
+  SM_W_IN = 5,         /* [2F, d] per layer */
+  SM_W_DOWN = 6,       /* [d, F] per layer */
+  SM_W_FINAL_NORM = 7, /* [d] */
+  SM_W_LM_HEAD = 8     /* [vocab, d] */
+};
+
+int sm_model_create(const sm_model_config* cfg, sm_model** out);
+int sm_model_destroy(sm_model* model);
+int64_t sm_model_weight_bytes(const sm_model* model);
+/* Load one tensor from a dense f32 device buffer; quantized models quantize
+ * linears on the device (QuantizedModelBackend::load_quantized_matrix /
+ * load_floating_tensor, quantization.rs:1183-1189). Synchronises `stream`
+ * for quantized linears (range check of the scales). */
+int sm_model_set_tensor(sm_model* model, int kind, int layer, const float* src, void* stream);
+/* Synthetic weights: every linear and the embedding ~ N(0, std) from the
+ * counter RNG, norms = 1 (the BASELINE configs' random init). */
+int sm_model_init_random(sm_model* model, uint64_t seed, float std, void* stream);
+
+/* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout
+ * the semantics of TextGenerator::generate, generate.rs:68-124, with no EOS):
+ * prompts [S, P] int32 -> tokens [S, N] int32 and behavior_lp [S, N] f32
+ * (nullable), one prefill then N-1 cached decode steps. */
+int sm_rl_generate(sm_model* model, const int32_t* prompts, int64_t S, int64_t P, int64_t N,
+                   float temperature, uint64_t seed, int32_t* tokens, float* behavior_lp,
+                   void* stream);
+/* Log-prob recompute (padded_group_log_probabilities /
+ * equal_length_continuation_log_probabilities, tensor_sleep.rs:2531-2689):
+ * lp_out[s, n] = log_softmax(model(prompt ‖ tokens[:, :N-1]))[P-1+n][tokens[s, n]].
+ * Sequences are processed in chunks of <= max_tokens_per_forward tokens
+ * (0 = 65536, the reference's bound, tensor_sleep.rs:52). */
+int sm_rl_logprobs(sm_model* model, const int32_t* prompts, const int32_t* tokens, int64_t S,
+                   int64_t P, int64_t N, int64_t max_tokens_per_forward, float* lp_out,
+                   void* stream);
+/* prepare_device_batch numerics (posttrain.rs:4420, 1234-1244): recompute the
+ * current (policy) and frozen (reference, nullable when kl_coefficient == 0)
+ * log-probs, then sm_grpo_loss over groups x group_size rollouts. */
+int sm_rl_prepare(sm_model* policy, sm_model* reference, const int32_t* prompts,
+                  const int32_t* tokens, const float* behavior_lp, const float* rewards,
+                  const float* mask, int64_t groups, int64_t group_size, int64_t P, int64_t N,
+                  double clip_epsilon, double advantage_epsilon, double kl_coefficient,
+                  int64_t max_tokens_per_forward, float* lp_cur, float* lp_ref,
+                  float* group_stats, float* dlp, int32_t* flags, void* stream);
 
 /* ------------------------------------------------------------------------
  * Seeded synthetic data (no reference counterpart; bench/test inputs).

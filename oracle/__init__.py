@@ -51,11 +51,30 @@ def _declare(L: C.CDLL) -> None:
     L.or_q4_matvec.argtypes = [u8p, u16p, i64, i64, f32p, f32p]
     for name in ("or_q4_quantize", "or_q4_decode", "or_q4_matvec"):
         getattr(L, name).restype = None
+    L.or_round_f16.argtypes = [C.c_float]
+    L.or_round_f16.restype = C.c_float
     _declare_model(L)
 
 
+class OrModel(C.Structure):
+    """Mirror of ``or_model`` in model.c (host weight pointers)."""
+    _fields_ = [(n, C.c_int32) for n in ("layers", "d", "H", "KVH", "hd", "F", "V", "quantized")] + \
+        [("eps", C.c_float), ("theta", C.c_float)] + \
+        [(n, C.c_void_p) for n in ("embed", "attn_norm", "ffn_norm", "final_norm",
+                                   "qkv", "o", "in_", "down", "lm_head",
+                                   "qkv_c", "o_c", "in_c", "down_c", "lm_c",
+                                   "qkv_s", "o_s", "in_s", "down_s", "lm_s")]
+
+
 def _declare_model(L: C.CDLL) -> None:
-    """Model-level entry points (added as the oracle grows)."""
+    vp, i32, i64 = C.c_void_p, C.c_int, C.c_int64
+    L.or_model_forward.argtypes = [C.POINTER(OrModel), vp, i32, i32, i32, vp, vp, i32, vp]
+    L.or_model_logits.argtypes = [C.POINTER(OrModel), vp, i64, vp]
+    L.or_sample.argtypes = [vp, i64, i64, C.c_float, C.c_uint64, i64, vp, i64, vp, i64]
+    L.or_generate.argtypes = [C.POINTER(OrModel), vp, i32, i32, i32, C.c_float, C.c_uint64, vp, vp]
+    L.or_logprobs.argtypes = [C.POINTER(OrModel), vp, vp, i32, i32, i32, vp]
+    for n in ("or_model_forward", "or_model_logits", "or_sample", "or_generate", "or_logprobs"):
+        getattr(L, n).restype = None
 
 
 def _ptr(a):
@@ -149,3 +168,104 @@ def q4_matvec(codes, scales, rows: int, cols: int, x) -> np.ndarray:
     lib().or_q4_matvec(np.ascontiguousarray(codes), np.ascontiguousarray(scales), rows, cols,
                        np.ascontiguousarray(x, dtype=np.float32), y)
     return y
+
+
+# ------------------------------------------------------------------ model ---
+
+class HostModel:
+    """Host copy of a decoder's weights for the oracle.
+
+    ``weights`` maps names to float32 arrays: embed [V, d], attn_norm / ffn_norm
+    [layers, d], final_norm [d], and linears qkv / o / in / down [layers, N, K],
+    lm_head [V, d] in [out, in] layout. When ``quantized`` the linears are
+    packed with the Q4G128 oracle codec and the embedding is rounded to bf16.
+    """
+
+    def __init__(self, cfg: dict, weights: dict, quantized: bool):
+        self.cfg, self.quantized = cfg, quantized
+        self._keep = []
+        w = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}
+        if quantized:
+            w["embed"] = round_bf16(w["embed"])
+        self.w = w
+        m = OrModel()
+        for k in ("layers", "d", "H", "KVH", "hd", "F", "V"):
+            setattr(m, k, int(cfg[k]))
+        m.quantized = int(quantized)
+        m.eps, m.theta = float(cfg.get("eps", 1e-5)), float(cfg.get("theta", 1e4))
+        for k in ("embed", "attn_norm", "ffn_norm", "final_norm"):
+            setattr(m, k, self._ptr(w[k]))
+        names = {"qkv": "qkv", "o": "o", "in": "in_", "down": "down", "lm_head": "lm_head"}
+        short = {"qkv": "qkv", "o": "o", "in": "in", "down": "down", "lm_head": "lm"}
+        self.packed = {}
+        for k, field in names.items():
+            if quantized:
+                arr = w[k] if k != "lm_head" else w[k][None]
+                cs, ss = zip(*[q4_quantize(a) for a in arr])
+                codes, scales = np.concatenate(cs), np.concatenate(ss)
+                self.packed[k] = (codes, scales)
+                setattr(m, short[k] + "_c", self._ptr(codes))
+                setattr(m, short[k] + "_s", self._ptr(scales))
+            else:
+                setattr(m, field, self._ptr(w[k]))
+        self.m = m
+
+    def _ptr(self, a):
+        a = np.ascontiguousarray(a)
+        self._keep.append(a)
+        return a.ctypes.data
+
+    def generate(self, prompts, N, temperature=0.0, seed=0):
+        prompts = np.ascontiguousarray(prompts, dtype=np.int32)
+        S, P = prompts.shape
+        tok = np.empty((S, N), np.int32)
+        lp = np.empty((S, N), np.float64)
+        lib().or_generate(C.byref(self.m), prompts.ctypes.data, S, P, N, temperature, seed,
+                          tok.ctypes.data, lp.ctypes.data)
+        return tok, lp
+
+    def logprobs(self, prompts, tokens):
+        prompts = np.ascontiguousarray(prompts, dtype=np.int32)
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        S, P = prompts.shape
+        N = tokens.shape[1]
+        lp = np.empty((S, N), np.float64)
+        lib().or_logprobs(C.byref(self.m), prompts.ctypes.data, tokens.ctypes.data, S, P, N,
+                          lp.ctypes.data)
+        return lp
+
+    def forward_logits(self, ids):
+        """Full causal forward over ids [S, L]; returns logits [S, L, V] (float32)."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        S, L = ids.shape
+        c = self.cfg
+        kc = np.zeros(c["layers"] * S * c["KVH"] * L * c["hd"], np.float32)
+        vc = np.zeros_like(kc)
+        x = np.empty((S * L, c["d"]), np.float32)
+        lib().or_model_forward(C.byref(self.m), ids.ctypes.data, S, L, 0, kc.ctypes.data,
+                               vc.ctypes.data, L, x.ctypes.data)
+        logits = np.empty((S * L, c["V"]), np.float32)
+        lib().or_model_logits(C.byref(self.m), x.ctypes.data, S * L, logits.ctypes.data)
+        return logits.reshape(S, L, c["V"])
+
+
+def sample(logits, temperature, seed, step):
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, V = logits.shape
+    tok = np.empty(rows, np.int32)
+    lp = np.empty(rows, np.float64)
+    lib().or_sample(logits.ctypes.data, rows, V, temperature, seed, step, tok.ctypes.data, 1,
+                    lp.ctypes.data, 1)
+    return tok, lp
+
+
+def random_weights(cfg: dict, seed: int = 0, std: float = 0.02) -> dict:
+    """N(0, std) linears and embedding, unit norms (the configs' synthetic init)."""
+    rng = np.random.default_rng(seed)
+    Lr, d, H, KVH, hd, F, V = (cfg[k] for k in ("layers", "d", "H", "KVH", "hd", "F", "V"))
+    qn = H * hd + 2 * KVH * hd
+    n = lambda *s: rng.normal(0, std, s).astype(np.float32)  # noqa: E731
+    return {"embed": n(V, d), "attn_norm": np.ones((Lr, d), np.float32),
+            "ffn_norm": np.ones((Lr, d), np.float32), "final_norm": np.ones(d, np.float32),
+            "qkv": n(Lr, qn, d), "o": n(Lr, d, H * hd), "in": n(Lr, 2 * F, d),
+            "down": n(Lr, d, F), "lm_head": n(V, d)}

@@ -1,0 +1,289 @@
+/*
+ * CPU oracle, model level — TEST INFRASTRUCTURE ONLY (see oracle.h).
+ *
+ * Restates the reference decoder forward, generation loop and GRPO log-prob
+ * recompute for the configs' architecture:
+ *   embed                 summa-llm/src/model/transformer.rs:511-518
+ *   pre-norm block        summa-llm/src/model/block.rs:80-157
+ *   RMSNorm (fp32 stats)  summa-llm/src/model/norm.rs:36-50
+ *   qkv / RoPE / cache    summa-llm/src/model/attention.rs:92, 142-177, 318-371
+ *   attention             attention.rs:216-265 (softmax(qK^T/sqrt(hd))V, GQA repeat_kv)
+ *   SwiGLU FFN            summa-llm/src/model/ffn.rs:854-886
+ *   final norm + head     transformer.rs:802-909
+ *   generation            summa-llm/src/generate.rs:53-250
+ *   log-prob recompute    summa-train/src/tensor_sleep.rs:2531-2689
+ * with the build's precision policy for quantized models: values rounded to
+ * f16 where the device feeds a matmul (norm outputs, attention output, SwiGLU
+ * output), to bf16 where it stores bf16 (q, k, v, embedding), fp32 everywhere
+ * else, sequential fp32 accumulation in every dot product (the
+ * order PackedTensor::matrix_vector uses, quantization.rs:642-651).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "oracle.h"
+
+typedef struct or_model {
+  int32_t layers, d, H, KVH, hd, F, V, quantized;
+  float eps, theta;
+  const float* embed;      /* [V, d] */
+  const float* attn_norm;  /* [layers, d] */
+  const float* ffn_norm;   /* [layers, d] */
+  const float* final_norm; /* [d] */
+  const float *qkv, *o, *in, *down, *lm_head;           /* dense [N, K] per layer */
+  const uint8_t *qkv_c, *o_c, *in_c, *down_c, *lm_c;    /* Q4 codes per layer */
+  const uint16_t *qkv_s, *o_s, *in_s, *down_s, *lm_s;   /* Q4 scales per layer */
+} or_model;
+
+/* bf16 rounding: q, k, v (KV cache) and the embedding of quantized models. */
+static float rb(const or_model* m, float v) {
+  return m->quantized ? or_bf16_to_f32(or_f32_to_bf16(v)) : v;
+}
+
+/* f16 rounding: matmul-input activations (norm outputs, attention output,
+ * SwiGLU output) of quantized models. */
+static float rh(const or_model* m, float v) { return m->quantized ? or_round_f16(v) : v; }
+
+static float q4_at(const uint8_t* codes, const uint16_t* scales, int64_t i) {
+  const uint8_t byte = codes[i / 2];
+  int q = (i & 1) ? (byte >> 4) : (byte & 0xf);
+  if (q >= 8) q -= 16;
+  return or_bf16_to_f32(scales[i / 128]) * (float)q;
+}
+
+/* y[r, n] (+)= sum_k x[r, k] * W[n, k] with sequential f32 accumulation. */
+static void linear(const or_model* m, int kind, int layer, const float* x, int64_t M, float* y,
+                   int add) {
+  int64_t N, K;
+  const float* w = NULL;
+  const uint8_t* c = NULL;
+  const uint16_t* s = NULL;
+  const int64_t qdim = (int64_t)m->H * m->hd, kvdim = (int64_t)m->KVH * m->hd;
+  switch (kind) {
+    case 0: N = qdim + 2 * kvdim; K = m->d; break;
+    case 1: N = m->d; K = qdim; break;
+    case 2: N = 2 * (int64_t)m->F; K = m->d; break;
+    case 3: N = m->d; K = m->F; break;
+    default: N = m->V; K = m->d; break;
+  }
+  const int64_t off = (kind == 4) ? 0 : (int64_t)layer * N * K;
+  if (m->quantized) {
+    const uint8_t* cs[] = {m->qkv_c, m->o_c, m->in_c, m->down_c, m->lm_c};
+    const uint16_t* ss[] = {m->qkv_s, m->o_s, m->in_s, m->down_s, m->lm_s};
+    c = cs[kind] + off / 2;
+    s = ss[kind] + off / 128;
+  } else {
+    const float* ws[] = {m->qkv, m->o, m->in, m->down, m->lm_head};
+    w = ws[kind] + off;
+  }
+#pragma omp parallel for schedule(static) collapse(2)
+  for (int64_t r = 0; r < M; ++r)
+    for (int64_t n = 0; n < N; ++n) {
+      float acc = 0.f;
+      const float* xr = x + r * K;
+      if (w) {
+        const float* wr = w + n * K;
+        for (int64_t k = 0; k < K; ++k) acc += wr[k] * xr[k];
+      } else {
+        for (int64_t k = 0; k < K; ++k) acc += q4_at(c, s, n * K + k) * xr[k];
+      }
+      if (add) y[r * N + n] += acc; else y[r * N + n] = acc;
+    }
+}
+
+static void rmsnorm(const or_model* m, const float* x, const float* g, int64_t M, float* y) {
+  const int d = m->d;
+  for (int64_t r = 0; r < M; ++r) {
+    float ss = 0.f;
+    for (int c = 0; c < d; ++c) ss += x[r * d + c] * x[r * d + c];
+    const float rms = sqrtf(ss / (float)d + m->eps);
+    for (int c = 0; c < d; ++c) y[r * d + c] = rh(m, x[r * d + c] / rms * g[c]);
+  }
+}
+
+/* RoPE cos/sin of (pos, pair): theta^(-2p/hd) and the angle in double, then f32. */
+static void rope_cs(const or_model* m, int pos, int p, float* cs, float* sn) {
+  const double freq = pow((double)m->theta, -2.0 * p / (double)m->hd);
+  const double ang = (double)pos * freq;
+  *cs = (float)cos(ang);
+  *sn = (float)sin(ang);
+}
+
+/* Forward S sequences x L new tokens at positions pos0..pos0+L-1 through all
+ * layers, appending K/V to caches [layers][S][KVH][cap][hd]; x [S*L, d] out. */
+void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int pos0, float* kc,
+                      float* vc, int cap, float* x) {
+  const int d = m->d, H = m->H, KVH = m->KVH, hd = m->hd, F = m->F;
+  const int64_t rows = (int64_t)S * L;
+  const int64_t qdim = (int64_t)H * hd, kvdim = (int64_t)KVH * hd, qn = qdim + 2 * kvdim;
+  float* h = malloc(sizeof(float) * rows * (d > qdim ? d : qdim));
+  float* qkv = malloc(sizeof(float) * rows * qn);
+  float* q = malloc(sizeof(float) * rows * qdim);
+  float* att = malloc(sizeof(float) * rows * qdim);
+  float* gv = malloc(sizeof(float) * rows * 2 * F);
+  float* u = malloc(sizeof(float) * rows * F);
+  const float scale = 1.0f / sqrtf((float)hd);
+  for (int64_t r = 0; r < rows; ++r)
+    for (int c = 0; c < d; ++c) x[r * d + c] = m->embed[(int64_t)ids[r] * d + c];
+  for (int l = 0; l < m->layers; ++l) {
+    float* kl = kc + (size_t)l * S * KVH * cap * hd;
+    float* vl = vc + (size_t)l * S * KVH * cap * hd;
+    rmsnorm(m, x, m->attn_norm + (size_t)l * d, rows, h);
+    linear(m, 0, l, h, rows, qkv, 0);
+    for (int64_t r = 0; r < rows; ++r) {
+      const int s = (int)(r / L), pos = pos0 + (int)(r % L);
+      const float* src = qkv + r * qn;
+      for (int slot = 0; slot < H + 2 * KVH; ++slot)
+        for (int p = 0; p < hd / 2; ++p) {
+          const float a = src[slot * hd + 2 * p], b = src[slot * hd + 2 * p + 1];
+          float ra = a, rbv = b;
+          if (slot < H + KVH) {
+            float cs, sn;
+            rope_cs(m, pos, p, &cs, &sn);
+            ra = a * cs - b * sn;
+            rbv = b * cs + a * sn;
+          }
+          if (slot < H) {
+            q[r * qdim + slot * hd + 2 * p] = rb(m, ra);
+            q[r * qdim + slot * hd + 2 * p + 1] = rb(m, rbv);
+          } else {
+            const int kv = slot < H + KVH ? slot - H : slot - H - KVH;
+            float* dst = (slot < H + KVH ? kl : vl) + (((size_t)s * KVH + kv) * cap + pos) * hd;
+            dst[2 * p] = rb(m, ra);
+            dst[2 * p + 1] = rb(m, rbv);
+          }
+        }
+    }
+    /* causal attention, each query over keys 0..pos (two-pass softmax in f32) */
+#pragma omp parallel for schedule(static) collapse(2)
+    for (int64_t r = 0; r < rows; ++r)
+      for (int hh = 0; hh < H; ++hh) {
+        const int s = (int)(r / L), pos = pos0 + (int)(r % L);
+        const int kv = hh / (H / KVH);
+        const float* qp = q + r * qdim + hh * hd;
+        const float* kb = kl + ((size_t)s * KVH + kv) * cap * hd;
+        const float* vb = vl + ((size_t)s * KVH + kv) * cap * hd;
+        float* sc = malloc(sizeof(float) * (pos + 1));
+        float mx = -INFINITY;
+        for (int t = 0; t <= pos; ++t) {
+          float acc = 0.f;
+          for (int e = 0; e < hd; ++e) acc += qp[e] * kb[(size_t)t * hd + e];
+          sc[t] = acc * scale;
+          if (sc[t] > mx) mx = sc[t];
+        }
+        float sum = 0.f;
+        for (int t = 0; t <= pos; ++t) {
+          sc[t] = expf(sc[t] - mx);
+          sum += sc[t];
+        }
+        for (int e = 0; e < hd; ++e) {
+          float acc = 0.f;
+          for (int t = 0; t <= pos; ++t) acc += sc[t] * vb[(size_t)t * hd + e];
+          att[r * qdim + hh * hd + e] = rh(m, acc / sum);
+        }
+        free(sc);
+      }
+    linear(m, 1, l, att, rows, x, 1);
+    rmsnorm(m, x, m->ffn_norm + (size_t)l * d, rows, h);
+    linear(m, 2, l, h, rows, gv, 0);
+    for (int64_t r = 0; r < rows; ++r)
+      for (int c = 0; c < F; ++c) {
+        const float g = gv[r * 2 * F + c], v = gv[r * 2 * F + F + c];
+        u[r * F + c] = rh(m, g / (1.0f + expf(-g)) * v);
+      }
+    linear(m, 3, l, u, rows, x, 1);
+  }
+  free(h); free(qkv); free(q); free(att); free(gv); free(u);
+}
+
+void or_model_logits(const or_model* m, const float* x, int64_t M, float* logits) {
+  float* h = malloc(sizeof(float) * M * m->d);
+  rmsnorm(m, x, m->final_norm, M, h);
+  linear(m, 4, 0, h, M, logits, 0);
+  free(h);
+}
+
+/* Counter RNG identical to the device sampler's (SplitMix64 finaliser). */
+static uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+static uint64_t rng_key(uint64_t seed, uint64_t stream, uint64_t counter) {
+  return mix64(mix64(seed + 0x9e3779b97f4a7c15ull * (stream + 1)) ^ (counter * 0xd1b54a32d192ed03ull));
+}
+static float u01(uint64_t bits) { return ((float)(bits >> 40) + 0.5f) * (1.0f / 16777216.0f); }
+
+/* select_next_token (generate.rs:127-202): greedy first-max argmax, or a
+ * Gumbel-max draw from softmax(l/T); lp = log_softmax(l)[token] in f64. */
+void or_sample(const float* logits, int64_t rows, int64_t V, float temperature, uint64_t seed,
+               int64_t step, int32_t* tok, int64_t tok_stride, double* lp, int64_t lp_stride) {
+  for (int64_t r = 0; r < rows; ++r) {
+    const float* l = logits + r * V;
+    float best = -INFINITY;
+    int bi = 0;
+    double mx = -INFINITY;
+    for (int64_t v = 0; v < V; ++v) {
+      float key = l[v];
+      if (temperature > 0.f) {
+        const float u = u01(rng_key(seed, (uint64_t)r, (uint64_t)step * (uint64_t)V + (uint64_t)v));
+        key = l[v] * (1.0f / temperature) - logf(-logf(u));
+      }
+      if (key > best) { best = key; bi = (int)v; }
+      if (l[v] > mx) mx = l[v];
+    }
+    double s = 0.0;
+    for (int64_t v = 0; v < V; ++v) s += exp((double)l[v] - mx);
+    tok[r * tok_stride] = bi;
+    if (lp) lp[r * lp_stride] = (double)l[bi] - (mx + log(s));
+  }
+}
+
+/* generate (generate.rs:68-124, no EOS) for S rollouts at once. */
+void or_generate(const or_model* m, const int32_t* prompts, int S, int P, int N, float temperature,
+                 uint64_t seed, int32_t* tokens, double* lp) {
+  const int cap = P + N - 1, d = m->d;
+  const size_t cache = (size_t)m->layers * S * m->KVH * cap * m->hd;
+  float* kc = calloc(cache, sizeof(float));
+  float* vc = calloc(cache, sizeof(float));
+  float* x = malloc(sizeof(float) * (size_t)S * P * d);
+  float* last = malloc(sizeof(float) * (size_t)S * d);
+  float* logits = malloc(sizeof(float) * (size_t)S * m->V);
+  int32_t* ids = malloc(sizeof(int32_t) * S);
+  or_model_forward(m, prompts, S, P, 0, kc, vc, cap, x);
+  for (int s = 0; s < S; ++s) memcpy(last + (size_t)s * d, x + ((size_t)s * P + P - 1) * d, sizeof(float) * d);
+  or_model_logits(m, last, S, logits);
+  or_sample(logits, S, m->V, temperature, seed, 0, tokens, N, lp, N);
+  for (int t = 1; t < N; ++t) {
+    for (int s = 0; s < S; ++s) ids[s] = tokens[(size_t)s * N + t - 1];
+    or_model_forward(m, ids, S, 1, P + t - 1, kc, vc, cap, last);
+    or_model_logits(m, last, S, logits);
+    or_sample(logits, S, m->V, temperature, seed, t, tokens + t, N, lp ? lp + t : NULL, N);
+  }
+  free(kc); free(vc); free(x); free(last); free(logits); free(ids);
+}
+
+/* Log-probs of tokens[:, n] given prompt ‖ tokens[:, :n] (tensor_sleep.rs:2531-2615). */
+void or_logprobs(const or_model* m, const int32_t* prompts, const int32_t* tokens, int S, int P,
+                 int N, double* lp) {
+  const int L = P + N - 1, d = m->d;
+  const size_t cache = (size_t)m->layers * S * m->KVH * L * m->hd;
+  float* kc = calloc(cache, sizeof(float));
+  float* vc = calloc(cache, sizeof(float));
+  int32_t* ids = calloc((size_t)S * L, sizeof(int32_t));
+  float* x = malloc(sizeof(float) * (size_t)S * L * d);
+  float* rows = malloc(sizeof(float) * (size_t)S * N * d);
+  float* logits = malloc(sizeof(float) * (size_t)S * N * m->V);
+  for (int s = 0; s < S; ++s)
+    for (int t = 0; t < L; ++t)
+      ids[(size_t)s * L + t] = t < P ? prompts[(size_t)s * P + t] : tokens[(size_t)s * N + t - P];
+  or_model_forward(m, ids, S, L, 0, kc, vc, L, x);
+  for (int s = 0; s < S; ++s)
+    for (int n = 0; n < N; ++n)
+      memcpy(rows + ((size_t)s * N + n) * d, x + ((size_t)s * L + P - 1 + n) * d, sizeof(float) * d);
+  or_model_logits(m, rows, (int64_t)S * N, logits);
+  or_ce_rows(logits, 0, tokens, (int64_t)S * N, m->V, m->V, lp, NULL, NULL, 1.0, NULL);
+  free(kc); free(vc); free(ids); free(x); free(rows); free(logits);
+}

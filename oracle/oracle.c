@@ -22,6 +22,21 @@ uint16_t or_f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+float or_round_f16(float f) {
+  if (!isfinite(f)) return f;
+  const float a = fabsf(f);
+  if (a >= 65520.0f) return copysignf(INFINITY, f); /* halfway above 65504 rounds to inf */
+  float q;
+  if (a < 6.103515625e-05f) {
+    q = 5.9604644775390625e-08f; /* subnormal quantum 2^-24 */
+  } else {
+    int e;
+    frexpf(a, &e);          /* a in [2^(e-1), 2^e) */
+    q = ldexpf(1.0f, e - 11); /* 10 fraction bits */
+  }
+  return copysignf(nearbyintf(a / q) * q, f); /* ties to even (default rounding mode) */
+}
+
 static double load_logit(const void* p, int dtype, int64_t i) {
   if (dtype == 1) return (double)or_bf16_to_f32(((const uint16_t*)p)[i]);
   return (double)((const float*)p)[i];

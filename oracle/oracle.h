@@ -23,6 +23,9 @@ extern "C" {
 /* bf16 <-> f32 (round to nearest even), the rounding the device path uses. */
 float or_bf16_to_f32(uint16_t b);
 uint16_t or_f32_to_bf16(float f);
+/* f32 -> nearest IEEE binary16 value (ties to even, subnormals, overflow to
+ * inf), returned as f32. */
+float or_round_f16(float f);
 
 /* Row-wise log-softmax / CE in f64, two passes.
  * linear_cross_entropy/reference.rs:21-92 (mask_padded_logits + chunked_loss)

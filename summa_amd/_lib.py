@@ -13,7 +13,8 @@ LIB_PATH = Path(__file__).resolve().parent / "libsumma_amd.so"
 
 SM_OK = 0
 SM_F32, SM_BF16, SM_F16 = 0, 1, 2
-SM_EPI_STORE_F32, SM_EPI_STORE_BF16, SM_EPI_ADD_F32, SM_EPI_SWIGLU_BF16 = 0, 1, 2, 3
+SM_EPI_STORE_F32, SM_EPI_STORE_BF16, SM_EPI_ADD_F32, SM_EPI_SWIGLU_BF16, SM_EPI_SWIGLU_F16 = \
+    0, 1, 2, 3, 4
 
 _lib = None
 
@@ -27,7 +28,24 @@ SIGNATURES: dict[str, tuple] = {
     "sm_grpo_loss": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, f64, f64, f64, vp, vp, vp, vp, vp]),
     "sm_grpo_flags_message": (C.c_char_p, [C.c_int32]),
     "sm_q4_quantize": (i32, [vp, i32, i64, vp, vp, vp, vp]),
-    "sm_q4_matmul": (i32, [vp, vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
+    "sm_q4_matmul": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
+    "sm_gemm_f32": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
+    "sm_swiglu_f32": (i32, [vp, i64, i64, vp, vp]),
+    "sm_embed": (i32, [vp, i32, vp, i64, i64, i64, f32, vp, vp]),
+    "sm_rmsnorm": (i32, [vp, vp, i64, i64, f32, vp, i32, vp]),
+    "sm_rope_append": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i64, vp, i32, vp, vp, i32, vp]),
+    "sm_attn_decode": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, vp]),
+    "sm_attn_prefill": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
+    "sm_sample": (i32, [vp, i64, i64, i64, f32, u64, i64, vp, i64, vp, i64, vp, vp]),
+    "sm_model_create": (i32, [vp, vp]),
+    "sm_model_destroy": (i32, [vp]),
+    "sm_model_weight_bytes": (i64, [vp]),
+    "sm_model_set_tensor": (i32, [vp, i32, i32, vp, vp]),
+    "sm_model_init_random": (i32, [vp, u64, f32, vp]),
+    "sm_rl_generate": (i32, [vp, vp, i64, i64, i64, f32, u64, vp, vp, vp]),
+    "sm_rl_logprobs": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
+    "sm_rl_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64, i64,
+                            vp, vp, vp, vp, vp, vp]),
     "sm_fill_normal": (i32, [vp, i32, i64, f32, f32, u64, vp]),
     "sm_fill_ce_stress": (i32, [vp, i32, vp, i64, i64, f32, f32, u64, vp]),
 }

@@ -1,0 +1,305 @@
+// Attention over a contiguous KV cache (kernel 2 and the prefill/recompute
+// attention).
+//
+// Semantics: MultiHeadAttention::forward_cached / sdpa
+// (summa-llm/src/model/attention.rs:216-265, 318-371): softmax(q.K^T / sqrt(hd)) . V
+// over key positions 0..=pos of the query, GQA query head h reading KV head
+// h / (H / KVH) (repeat_kv, fused_attention.rs:114-125 — here never
+// materialised: each KV head is read once for its whole query-head group).
+// Cache layout [S, KVH, cap, hd] as AttnCache (attention.rs:20-40, 115-134).
+//
+// bf16 decode kernel (one query per sequence): one workgroup per
+// (KV head, sequence); its four waves split the key range in tiles of 64.
+// Scores Q.K^T come from v_mfma_f32_16x16x32_bf16 with the group's query heads
+// as the 16-row A operand (padded) and K rows read straight from HBM as the B
+// operand (natural [pos][hd] layout is already k-contiguous per lane). The
+// online softmax runs on the MFMA output registers, probabilities go through a
+// per-wave LDS slice, and P.V is a VALU FMA pass with lanes spread over hd so
+// each V row is one coalesced wave-wide load. Waves merge (max, sum, O) in LDS
+// at the end in a fixed order.
+//
+// Prefill / recompute (many queries, causal) uses the flash-attention kernel
+// in prefill_attention.hip; fp32 models (config[0]) use the simple VALU
+// kernel below for both.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace sm {
+namespace {
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+constexpr int kMaxQpk = 16;  // query heads per KV head handled by one WG
+
+template <int HD, int QM, typename TO>
+__global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ lens,
+    TO* __restrict__ out, int H, int KVH, int cap, float scale) {
+  constexpr int LPK = HD / 2;      // lanes per key row in the P.V pass (2 dims each)
+  constexpr int PPI = 64 / LPK;    // keys per P.V iteration per wave
+  constexpr int STEPS = HD / 32;   // MFMA k-steps over head_dim
+  const int kvh = blockIdx.x, s = blockIdx.y;
+  const int qpk = H / KVH;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  const int len = min(lens[s], cap);
+  const size_t kv_base = ((size_t)s * KVH + kvh) * cap * HD;
+
+  __shared__ float pbuf[4][QM][64];
+  __shared__ float mrg_m[4][QM], mrg_l[4][QM];
+  __shared__ float mrg_o[4][QM][HD];
+
+  // A operand: query head (kvh*qpk + j) if j < qpk.
+  bf8 qa[STEPS];
+#pragma unroll
+  for (int st = 0; st < STEPS; ++st) {
+    if (j < qpk) {
+      const uint16_t* qp = q + ((size_t)s * H + kvh * qpk + j) * HD + st * 32 + g * 8;
+      qa[st] = *reinterpret_cast<const bf8*>(qp);
+    } else {
+      qa[st] = bf8{};
+    }
+  }
+
+  float m_i[QM], l_i[QM], o0[QM], o1[QM];
+#pragma unroll
+  for (int i = 0; i < QM; ++i) { m_i[i] = -INFINITY; l_i[i] = 0.f; o0[i] = 0.f; o1[i] = 0.f; }
+
+  const int sub = lane / LPK;          // which key of the PPI group this lane handles
+  const int dl = (lane % LPK) * 2;     // first of the two dims this lane owns
+
+  for (int t0 = wave * 64; t0 < len; t0 += 256) {
+    // ---- scores for 64 keys: 4 MFMA blocks of 16 keys
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = t0 + kb * 16 + j;
+      f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        bf8 kf = bf8{};
+        if (key < len)
+          kf = *reinterpret_cast<const bf8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], kf, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 4 * g + r;
+        if (row < qpk) pbuf[wave][row][kb * 16 + j] = (key < len) ? acc[r] * scale : -INFINITY;
+      }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- online softmax per query head (lane = key within the tile)
+#pragma unroll
+    for (int i = 0; i < QM; ++i) {
+      if (i >= qpk) break;
+      const float v = pbuf[wave][i][lane];
+      const float mnew = fmaxf(m_i[i], wave_max(v));
+      const float alpha = (m_i[i] == -INFINITY) ? 0.f : __expf(m_i[i] - mnew);
+      const float p = (v == -INFINITY) ? 0.f : __expf(v - mnew);
+      l_i[i] = l_i[i] * alpha + wave_sum(p);
+      m_i[i] = mnew;
+      o0[i] *= alpha;
+      o1[i] *= alpha;
+      pbuf[wave][i][lane] = p;
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- P.V: lanes over head_dim, PPI keys per iteration
+    const int tend = min(64, len - t0);
+    for (int tt = sub; tt < tend; tt += PPI) {
+      const uint32_t vv = *reinterpret_cast<const uint32_t*>(vc + kv_base + (size_t)(t0 + tt) * HD + dl);
+      const float v0 = bf16lo(vv), v1 = bf16hi(vv);
+#pragma unroll
+      for (int i = 0; i < QM; ++i) {
+        if (i >= qpk) break;
+        const float p = pbuf[wave][i][tt];
+        o0[i] = fmaf(p, v0, o0[i]);
+        o1[i] = fmaf(p, v1, o1[i]);
+      }
+    }
+    __builtin_amdgcn_wave_barrier();
+  }
+  // combine the PPI key-subsets inside the wave
+  if constexpr (PPI > 1) {
+#pragma unroll
+    for (int i = 0; i < QM; ++i) {
+#pragma unroll
+      for (int o = LPK; o < 64; o <<= 1) {
+        o0[i] += __shfl_xor(o0[i], o, kWave);
+        o1[i] += __shfl_xor(o1[i], o, kWave);
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < QM; ++i) {
+    if (i >= qpk) break;
+    if (lane == 0) { mrg_m[wave][i] = m_i[i]; mrg_l[wave][i] = l_i[i]; }
+    if (lane < LPK) { mrg_o[wave][i][dl] = o0[i]; mrg_o[wave][i][dl + 1] = o1[i]; }
+  }
+  __syncthreads();
+  // merge the four waves: thread t handles (head, dim) pairs
+  for (int e = threadIdx.x; e < qpk * HD; e += 256) {
+    const int i = e / HD, d = e % HD;
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) m = fmaxf(m, mrg_m[w][i]);
+    float l = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (mrg_m[w][i] == -INFINITY) continue;
+      const float c = __expf(mrg_m[w][i] - m);
+      l += mrg_l[w][i] * c;
+      o += mrg_o[w][i][d] * c;
+    }
+    const float v = o / l;
+    if constexpr (sizeof(TO) == 2 && __is_same(TO, _Float16))
+      out[((size_t)s * H + kvh * qpk + i) * HD + d] = (_Float16)v;
+    else
+      out[((size_t)s * H + kvh * qpk + i) * HD + d] = f32_to_bf16(v);
+  }
+}
+
+// Generic VALU attention (fp32 models): one thread per (query row, head);
+// query row r of sequence s sits at position pos0[s] + r + pos_off and attends
+// keys 0..=pos. q [S, L, H, hd] f32; cache [S, KVH, cap, hd] f32; out like q.
+template <int HD>
+__global__ __launch_bounds__(256) void attn_valu_f32_kernel(
+    const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
+    const int32_t* __restrict__ pos0, int pos_off, float* __restrict__ out, int S, int L, int H,
+    int KVH, int cap, float scale) {
+  constexpr int hd = HD;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)S * L * H) return;
+  const int h = idx % H;
+  const int r = (idx / H) % L;
+  const int s = idx / ((int64_t)H * L);
+  const int kvh = h / (H / KVH);
+  const int pos = pos0[s] + r + pos_off;
+  const float* qp = q + idx * hd;
+  const float* kb = kc + ((size_t)s * KVH + kvh) * cap * hd;
+  const float* vb = vc + ((size_t)s * KVH + kvh) * cap * hd;
+  float* op = out + idx * hd;
+  float m = -INFINITY, l = 0.f;
+  float acc[HD];
+#pragma unroll
+  for (int d = 0; d < hd; ++d) acc[d] = 0.f;
+  for (int t = 0; t <= pos; ++t) {
+    float sc = 0.f;
+#pragma unroll
+    for (int d = 0; d < hd; ++d) sc = fmaf(qp[d], kb[(size_t)t * hd + d], sc);
+    sc *= scale;
+    const float mnew = fmaxf(m, sc);
+    const float alpha = (m == -INFINITY) ? 0.f : expf(m - mnew);
+    const float p = expf(sc - mnew);
+    l = l * alpha + p;
+#pragma unroll
+    for (int d = 0; d < hd; ++d) acc[d] = acc[d] * alpha + p * vb[(size_t)t * hd + d];
+    m = mnew;
+  }
+#pragma unroll
+  for (int d = 0; d < hd; ++d) op[d] = acc[d] / l;
+}
+
+int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_t* pos0,
+                  int pos_off, float* out, int S, int L, int H, int KVH, int cap, int hd,
+                  hipStream_t st) {
+  const int64_t n = (int64_t)S * L * H;
+  if (n == 0) return SM_OK;
+  const unsigned blocks = (unsigned)ceil_div(n, 256);
+  const float scale = 1.0f / sqrtf((float)hd);
+  if (hd == 64)
+    attn_valu_f32_kernel<64><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, S, L, H, KVH, cap, scale);
+  else if (hd == 128)
+    attn_valu_f32_kernel<128><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, S, L, H, KVH, cap, scale);
+  else {
+    set_error("f32 attention: head_dim must be 64 or 128 (got %d)", hd);
+    return SM_ERR_UNSUPPORTED;
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+}  // namespace
+
+int attn_prefill_bf16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                      const int32_t* pos0, void* out, bool out_f16, int S, int L, int H, int KVH,
+                      int cap, int hd, hipStream_t st);
+
+}  // namespace sm
+
+extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vcache,
+                              const int32_t* lens, void* out, int dtype, int out_dtype, int64_t S,
+                              int64_t H, int64_t KVH, int64_t cap, int64_t head_dim,
+                              void* stream) {
+  using namespace sm;
+  SM_REQUIRE(q && kcache && vcache && lens && out, "sm_attn_decode: null buffer");
+  SM_REQUIRE(S >= 0 && S <= 65535 && H > 0 && KVH > 0 && H % KVH == 0,
+             "sm_attn_decode: need 0 <= S <= 65535 and H a multiple of KVH");
+  SM_REQUIRE(cap > 0 && cap <= (1 << 24), "sm_attn_decode: bad cache capacity");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128, "sm_attn_decode: head_dim must be 64 or 128");
+  if (S == 0) return SM_OK;
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  hipStream_t st = as_stream(stream);
+  if (dtype == SM_F32) {
+    SM_REQUIRE(out_dtype == SM_F32, "sm_attn_decode: f32 attention writes f32");
+    return attn_valu_f32((const float*)q, (const float*)kcache, (const float*)vcache, lens, -1,
+                         (float*)out, (int)S, 1, (int)H, (int)KVH, (int)cap, (int)head_dim, st);
+  }
+  SM_REQUIRE(dtype == SM_BF16, "sm_attn_decode: dtype must be SM_BF16 or SM_F32");
+  SM_REQUIRE(out_dtype == SM_BF16 || out_dtype == SM_F16,
+             "sm_attn_decode: bf16 attention writes bf16 or f16");
+  const int qpk = (int)(H / KVH);
+  SM_REQUIRE(qpk <= kMaxQpk, "sm_attn_decode: at most %d query heads per KV head", kMaxQpk);
+  const dim3 grid((unsigned)KVH, (unsigned)S);
+  const uint16_t *qq = (const uint16_t*)q, *kk = (const uint16_t*)kcache,
+                 *vv = (const uint16_t*)vcache;
+#define SM_DEC(HD, QM)                                                                            \
+  do {                                                                                            \
+    if (out_dtype == SM_F16)                                                                      \
+      attn_decode_bf16_kernel<HD, QM, _Float16><<<grid, 256, 0, st>>>(                            \
+          qq, kk, vv, lens, (_Float16*)out, (int)H, (int)KVH, (int)cap, scale);                   \
+    else                                                                                          \
+      attn_decode_bf16_kernel<HD, QM, uint16_t><<<grid, 256, 0, st>>>(                            \
+          qq, kk, vv, lens, (uint16_t*)out, (int)H, (int)KVH, (int)cap, scale);                   \
+  } while (0)
+  if (head_dim == 64) {
+    if (qpk == 1) SM_DEC(64, 1); else if (qpk <= 4) SM_DEC(64, 4); else SM_DEC(64, 16);
+  } else {
+    if (qpk == 1) SM_DEC(128, 1); else if (qpk <= 4) SM_DEC(128, 4); else SM_DEC(128, 16);
+  }
+#undef SM_DEC
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_attn_prefill(const void* q, const void* kcache, const void* vcache,
+                               const int32_t* pos0, void* out, int dtype, int out_dtype,
+                               int64_t S, int64_t L, int64_t H, int64_t KVH, int64_t cap,
+                               int64_t head_dim, void* stream) {
+  using namespace sm;
+  SM_REQUIRE(q && kcache && vcache && pos0 && out, "sm_attn_prefill: null buffer");
+  SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && H % KVH == 0,
+             "sm_attn_prefill: bad shape");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128, "sm_attn_prefill: head_dim must be 64 or 128");
+  SM_REQUIRE(cap > 0 && cap <= (1 << 24), "sm_attn_prefill: bad cache capacity");
+  if (S == 0 || L == 0) return SM_OK;
+  hipStream_t st = as_stream(stream);
+  if (dtype == SM_F32) {
+    SM_REQUIRE(out_dtype == SM_F32, "sm_attn_prefill: f32 attention writes f32");
+    return attn_valu_f32((const float*)q, (const float*)kcache, (const float*)vcache, pos0, 0,
+                         (float*)out, (int)S, (int)L, (int)H, (int)KVH, (int)cap, (int)head_dim,
+                         st);
+  }
+  SM_REQUIRE(dtype == SM_BF16, "sm_attn_prefill: dtype must be SM_BF16 or SM_F32");
+  SM_REQUIRE(out_dtype == SM_BF16 || out_dtype == SM_F16,
+             "sm_attn_prefill: bf16 attention writes bf16 or f16");
+  return attn_prefill_bf16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
+                           pos0, out, out_dtype == SM_F16, (int)S, (int)L, (int)H, (int)KVH,
+                           (int)cap, (int)head_dim, st);
+}

@@ -1,0 +1,231 @@
+// Decoder elementwise ops and token selection.
+//
+//   embed        Transformer::embed (summa-llm/src/model/transformer.rs:511-518)
+//   rmsnorm      Norm::forward -> Burn RmsNorm, fp32 statistics
+//                (summa-llm/src/model/norm.rs:36-50): y = x / sqrt(mean(x^2) + eps) * gamma
+//   rope_append  project_qkv's [q | k | v] split + RoPE (adjacent-pair convention,
+//                attention.rs:142-177; docs/uni-stack-inference.md:24) + the
+//                AttnCache slice_assign (attention.rs:331-356)
+//   sample       select_next_token (summa-llm/src/generate.rs:127-202): greedy
+//                first-max argmax, or a temperature sample, plus the token's
+//                log-prob under log_softmax(logits) (the quantity the GRPO
+//                recompute produces, summa-train/src/tensor_sleep.rs:2609-2614)
+//
+// The residual stream is fp32; activations that feed a matmul are emitted in
+// the model's activation dtype (bf16 for quantized models, fp32 otherwise).
+#include <cmath>
+
+#include "common.hpp"
+
+namespace sm {
+namespace {
+
+template <typename T> __device__ inline float to_f(T v);
+template <> __device__ inline float to_f<float>(float v) { return v; }
+template <> __device__ inline float to_f<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+template <typename T> __device__ inline T from_f(float v);
+template <> __device__ inline float from_f<float>(float v) { return v; }
+template <> __device__ inline uint16_t from_f<uint16_t>(float v) { return f32_to_bf16(v); }
+template <> __device__ inline _Float16 from_f<_Float16>(float v) { return (_Float16)v; }
+
+// x[r, :] = table[ids[r], :] * scale  (f32 out)
+template <typename T>
+__global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restrict__ ids,
+                             int64_t rows, int d, int vocab, float scale, float* __restrict__ x) {
+  const int64_t r = blockIdx.x;
+  const int32_t id = ids[r];
+  const bool ok = id >= 0 && id < vocab;
+  for (int c = threadIdx.x; c < d; c += blockDim.x)
+    x[r * d + c] = ok ? to_f(table[(size_t)id * d + c]) * scale : NAN;
+}
+
+// One 256-thread workgroup per row.
+template <typename TO>
+__global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ gamma, int d,
+                                                      float eps, TO* __restrict__ y) {
+  __shared__ float part[4];
+  const int64_t r = blockIdx.x;
+  const float* xr = x + r * d;
+  float ss = 0.f;
+  for (int c = threadIdx.x; c < d; c += 256) ss = fmaf(xr[c], xr[c], ss);
+  ss = wave_sum(ss);
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = ss;
+  __syncthreads();
+  const float tot = part[0] + part[1] + part[2] + part[3];
+  const float rms = sqrtf(tot / (float)d + eps);
+  for (int c = threadIdx.x; c < d; c += 256) y[r * d + c] = from_f<TO>(xr[c] / rms * gamma[c]);
+}
+
+// qkv: [rows, (H + 2*KVH) * hd] f32, row = s*L + i at position pos0[s] + i.
+// One thread per (row, head slot, pair).
+template <typename TA, typename TC>
+__global__ void rope_append_kernel(const float* __restrict__ qkv, const float2* __restrict__ rope,
+                                   const int32_t* __restrict__ pos0, int L, int H, int KVH,
+                                   int hd, int cap, int64_t rows, TA* __restrict__ q_out,
+                                   TC* __restrict__ kc, TC* __restrict__ vc) {
+  const int half = hd / 2;
+  const int slots = H + 2 * KVH;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * slots * half) return;
+  const int p = idx % half;
+  const int slot = (idx / half) % slots;
+  const int64_t row = idx / ((int64_t)half * slots);
+  const int s = (int)(row / L), i = (int)(row % L);
+  const int pos = pos0[s] + i;
+  if (pos < 0 || pos >= cap) return;
+  const float* src = qkv + row * (int64_t)slots * hd + (int64_t)slot * hd + 2 * p;
+  const float a = src[0], b = src[1];
+  if (slot >= H + KVH) {  // value: no rotation
+    const int kvh = slot - H - KVH;
+    TC* dst = vc + (((size_t)s * KVH + kvh) * cap + pos) * hd + 2 * p;
+    dst[0] = from_f<TC>(a);
+    dst[1] = from_f<TC>(b);
+    return;
+  }
+  const float2 cs = rope[(size_t)pos * half + p];  // (cos, sin)
+  const float ra = a * cs.x - b * cs.y;
+  const float rb = b * cs.x + a * cs.y;
+  if (slot < H) {
+    TA* dst = q_out + (row * H + slot) * hd + 2 * p;
+    dst[0] = from_f<TA>(ra);
+    dst[1] = from_f<TA>(rb);
+  } else {
+    const int kvh = slot - H;
+    TC* dst = kc + (((size_t)s * KVH + kvh) * cap + pos) * hd + 2 * p;
+    dst[0] = from_f<TC>(ra);
+    dst[1] = from_f<TC>(rb);
+  }
+}
+
+// Gumbel-max sampling / greedy argmax over one logits row per workgroup, plus
+// the chosen token's log-prob. Ties resolve to the lowest index (Burn argmax /
+// the host sampler's reverse index order, generate.rs:144-152).
+__global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ logits,
+                                                     int64_t ld, int vocab, float inv_temp,
+                                                     uint64_t seed, int64_t step,
+                                                     int32_t* __restrict__ tok, int64_t tok_stride,
+                                                     float* __restrict__ lp, int64_t lp_stride,
+                                                     int32_t* __restrict__ next_ids) {
+  __shared__ float s_best[4];
+  __shared__ int s_idx[4];
+  __shared__ float s_m[4], s_s[4];
+  const int64_t r = blockIdx.x;
+  const float* row = logits + r * ld;
+  float m = -INFINITY, s = 0.f, best = -INFINITY;
+  int bidx = 0x7fffffff;
+  for (int v = threadIdx.x; v < vocab; v += 256) {
+    const float x = row[v];
+    if (x > m) { s = s * __expf(m - x) + 1.f; m = x; } else { s += __expf(x - m); }
+    float key = x;
+    if (inv_temp > 0.f) {
+      const float u = u01(rng_key(seed, (uint64_t)r, (uint64_t)step * (uint64_t)vocab + v));
+      key = x * inv_temp - logf(-logf(u));
+    }
+    if (key > best) { best = key; bidx = v; }  // v increases per thread: first max kept
+  }
+  // wave reduce (max with lowest index on ties)
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float ob = __shfl_xor(best, o, kWave);
+    const int oi = __shfl_xor(bidx, o, kWave);
+    if (ob > best || (ob == best && oi < bidx)) { best = ob; bidx = oi; }
+    const float om = __shfl_xor(m, o, kWave), os = __shfl_xor(s, o, kWave);
+    lse_merge(m, s, om, os);
+  }
+  const int w = threadIdx.x / kWave;
+  if (threadIdx.x % kWave == 0) { s_best[w] = best; s_idx[w] = bidx; s_m[w] = m; s_s[w] = s; }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int k = 1; k < 4; ++k) {
+      if (s_best[k] > best || (s_best[k] == best && s_idx[k] < bidx)) { best = s_best[k]; bidx = s_idx[k]; }
+      lse_merge(m, s, s_m[k], s_s[k]);
+    }
+    if (bidx >= vocab) bidx = 0;  // all-NaN row: deterministic fallback
+    tok[r * tok_stride] = bidx;
+    if (next_ids) next_ids[r] = bidx;
+    if (lp) lp[r * lp_stride] = row[bidx] - (m + __logf(s));
+  }
+}
+
+}  // namespace
+}  // namespace sm
+
+using namespace sm;
+
+extern "C" int sm_embed(const void* table, int dtype, const int32_t* ids, int64_t rows, int64_t d,
+                        int64_t vocab, float scale, float* x, void* stream) {
+  SM_REQUIRE(table && ids && x, "sm_embed: null buffer");
+  SM_REQUIRE(rows >= 0 && d > 0 && vocab > 0, "sm_embed: bad shape");
+  if (rows == 0) return SM_OK;
+  if (dtype == SM_BF16)
+    embed_kernel<uint16_t><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+        (const uint16_t*)table, ids, rows, (int)d, (int)vocab, scale, x);
+  else if (dtype == SM_F32)
+    embed_kernel<float><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+        (const float*)table, ids, rows, (int)d, (int)vocab, scale, x);
+  else SM_REQUIRE(false, "sm_embed: dtype must be SM_BF16 or SM_F32");
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int64_t d, float eps,
+                          void* y, int out_dtype, void* stream) {
+  SM_REQUIRE(x && gamma && y, "sm_rmsnorm: null buffer");
+  SM_REQUIRE(rows >= 0 && d > 0, "sm_rmsnorm: bad shape");
+  if (rows == 0) return SM_OK;
+  if (out_dtype == SM_BF16)
+    rmsnorm_kernel<uint16_t><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
+                                                                           (uint16_t*)y);
+  else if (out_dtype == SM_F16)
+    rmsnorm_kernel<_Float16><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
+                                                                           (_Float16*)y);
+  else if (out_dtype == SM_F32)
+    rmsnorm_kernel<float><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
+                                                                        (float*)y);
+  else SM_REQUIRE(false, "sm_rmsnorm: out_dtype must be SM_F32, SM_BF16 or SM_F16");
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_rope_append(const float* qkv, const float* rope_table, const int32_t* pos0,
+                              int64_t S, int64_t L, int64_t H, int64_t KVH, int64_t head_dim,
+                              int64_t cap, void* q_out, int q_dtype, void* kcache, void* vcache,
+                              int cache_dtype, void* stream) {
+  SM_REQUIRE(qkv && rope_table && pos0 && q_out && kcache && vcache, "sm_rope_append: null buffer");
+  SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && head_dim > 0 && head_dim % 2 == 0 && cap > 0,
+             "sm_rope_append: bad shape");
+  const int64_t rows = S * L;
+  const int64_t n = rows * (H + 2 * KVH) * (head_dim / 2);
+  if (n == 0) return SM_OK;
+  const unsigned blocks = (unsigned)ceil_div(n, 256);
+  hipStream_t st = as_stream(stream);
+  const float2* rt = reinterpret_cast<const float2*>(rope_table);
+#define SM_ROPE(TA, TC)                                                                         \
+  rope_append_kernel<TA, TC><<<blocks, 256, 0, st>>>(qkv, rt, pos0, (int)L, (int)H, (int)KVH,  \
+                                                     (int)head_dim, (int)cap, rows, (TA*)q_out, \
+                                                     (TC*)kcache, (TC*)vcache)
+  if (q_dtype == SM_BF16 && cache_dtype == SM_BF16) SM_ROPE(uint16_t, uint16_t);
+  else if (q_dtype == SM_F32 && cache_dtype == SM_F32) SM_ROPE(float, float);
+  else if (q_dtype == SM_F32 && cache_dtype == SM_BF16) SM_ROPE(float, uint16_t);
+  else SM_REQUIRE(false, "sm_rope_append: unsupported dtype combination");
+#undef SM_ROPE
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab,
+                         float temperature, uint64_t seed, int64_t step, int32_t* tokens,
+                         int64_t tok_stride, float* logprobs, int64_t lp_stride,
+                         int32_t* next_ids, void* stream) {
+  SM_REQUIRE(logits && tokens, "sm_sample: null buffer");
+  SM_REQUIRE(rows >= 0 && vocab > 0 && vocab <= ld, "sm_sample: bad shape");
+  SM_REQUIRE(!std::isnan(temperature), "temperature must not be NaN");
+  if (rows == 0) return SM_OK;
+  const float inv_temp = temperature > 0.f ? 1.f / temperature : 0.f;
+  sample_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+      logits, ld, (int)vocab, inv_temp, seed, step, tokens, tok_stride, logprobs, lp_stride,
+      next_ids);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}

@@ -1,0 +1,546 @@
+// Decoder model + RL-step runtime (host C++ over the HIP kernels).
+//
+// This is the device side of GrpoDeviceBatchRuntime
+// (summa-train/src/posttrain.rs:1288-1305): batched rollout generation
+// (generate_device_batch; the reference runs TextGenerator::generate batch 1
+// per rollout, summa-llm/src/generate.rs:53-124), log-prob recompute for the
+// current and frozen policies (padded_group_log_probabilities,
+// summa-train/src/tensor_sleep.rs:2531-2689) and the GRPO loss
+// (prepare_device_batch). The model is the MAL Transformer restricted to what
+// the configs use: pre-norm blocks x += Attn(RMSNorm(x)); x += FFN(RMSNorm(x))
+// (block.rs:80-157), RoPE GQA attention (attention.rs:66-371), SwiGLU FFN
+// (ffn.rs:854-886), final RMSNorm + LM head (transformer.rs:802-909).
+//
+// Precision policy. fp32 models: everything fp32 (the reference CPU path).
+// Quantized models: Q4G128 linears (incl. LM head), bf16 embedding table,
+// fp32 residual stream (the reference's decode stream, transformer.rs:588-592),
+// f16 activations into every matmul (the Q4 MFMA operand type; its 11-bit
+// significand keeps the log-prob noise of the activation roundings below the
+// 2e-3 parity bar, which bf16 activations exceed), bf16 q and KV cache, fp32
+// logits.
+#include <cmath>
+#include <cstring>
+#include <vector>
+
+#include "common.hpp"
+
+extern "C" {
+int sm_q4_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
+                 int64_t, void*, int64_t, int, void*);
+int sm_q4_quantize(const void*, int, int64_t, uint8_t*, uint16_t*, int32_t*, void*);
+int sm_gemm_f32(const float*, int64_t, int64_t, const float*, int64_t, int64_t, float*, int64_t,
+                int, void*);
+int sm_swiglu_f32(const float*, int64_t, int64_t, float*, void*);
+int sm_embed(const void*, int, const int32_t*, int64_t, int64_t, int64_t, float, float*, void*);
+int sm_rmsnorm(const float*, const float*, int64_t, int64_t, float, void*, int, void*);
+int sm_rope_append(const float*, const float*, const int32_t*, int64_t, int64_t, int64_t, int64_t,
+                   int64_t, int64_t, void*, int, void*, void*, int, void*);
+int sm_attn_decode(const void*, const void*, const void*, const int32_t*, void*, int, int,
+                   int64_t, int64_t, int64_t, int64_t, int64_t, void*);
+int sm_attn_prefill(const void*, const void*, const void*, const int32_t*, void*, int, int,
+                    int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void*);
+int sm_sample(const float*, int64_t, int64_t, int64_t, float, uint64_t, int64_t, int32_t*, int64_t,
+              float*, int64_t, int32_t*, void*);
+int sm_ce_rows(const void*, int, const int32_t*, int64_t, int64_t, int64_t, float*, float*, void*,
+               float, const float*, float*, void*);
+int sm_grpo_loss(const float*, const float*, const float*, const float*, const float*, int64_t,
+                 int64_t, int64_t, double, double, double, float*, float*, float*, int32_t*, void*);
+int sm_fill_normal(void*, int, int64_t, float, float, uint64_t, void*);
+}
+
+namespace sm {
+namespace {
+
+struct DevBuf {
+  void* p = nullptr;
+  size_t n = 0;
+};
+
+int ensure(DevBuf& b, size_t bytes) {
+  if (b.n >= bytes) return SM_OK;
+  if (b.p) SM_HIP(hipFree(b.p));
+  b.p = nullptr;
+  b.n = 0;
+  SM_HIP(hipMalloc(&b.p, bytes ? bytes : 16));
+  b.n = bytes;
+  return SM_OK;
+}
+
+struct Linear {
+  int64_t N = 0, K = 0;
+  uint8_t* codes = nullptr;
+  uint16_t* scales = nullptr;
+  float* w = nullptr;
+};
+
+struct Layer {
+  float* attn_norm = nullptr;
+  float* ffn_norm = nullptr;
+  Linear qkv, o, in, down;
+};
+
+__global__ void fill_f32_kernel(float* p, int64_t n, float v) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = v;
+}
+
+__global__ void set_positions_kernel(int32_t* pos, int32_t* lens, int S, int value) {
+  const int s = blockIdx.x * blockDim.x + threadIdx.x;
+  if (s < S) {
+    pos[s] = value;
+    lens[s] = value + 1;
+  }
+}
+
+// rows [S, d] <- x[s*L + off, :]
+__global__ void gather_rows_kernel(const float* __restrict__ x, int S, int L, int off, int d,
+                                   float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * d) return;
+  const int64_t s = i / d;
+  const int c = i % d;
+  out[i] = x[(s * L + off) * d + c];
+}
+
+// out [S, N, d] <- x[s*L + P-1 + n, :] for n < N
+__global__ void gather_span_kernel(const float* __restrict__ x, int S, int L, int first, int N,
+                                   int d, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * N * d) return;
+  const int c = i % d;
+  const int64_t sn = i / d;
+  const int64_t s = sn / N;
+  const int n = sn % N;
+  out[i] = x[(s * L + first + n) * d + c];
+}
+
+// ids [S, P+N-1] <- prompt ‖ tokens[:, :N-1]
+__global__ void build_ids_kernel(const int32_t* __restrict__ prompts,
+                                 const int32_t* __restrict__ tokens, int S, int P, int N,
+                                 int32_t* __restrict__ ids) {
+  const int L = P + N - 1;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * L) return;
+  const int64_t s = i / L;
+  const int t = i % L;
+  ids[i] = (t < P) ? prompts[s * P + t] : tokens[s * N + (t - P)];
+}
+
+__global__ void zero_i32_kernel(int32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0;
+}
+
+unsigned blocks_for(int64_t n) { return (unsigned)ceil_div(n > 0 ? n : 1, 256); }
+
+}  // namespace
+}  // namespace sm
+
+struct sm_model {
+  sm_model_config cfg;
+  int act = SM_F32;       // matmul-input activation dtype (f16 when quantized)
+  int kvt = SM_F32;       // q / KV cache / embedding dtype (bf16 when quantized)
+  size_t act_size = 4;    // bytes of either 16-bit type, or 4
+  int64_t qdim = 0, kvdim = 0, qkv_n = 0;
+  void* embed = nullptr;
+  float* final_norm = nullptr;
+  sm::Linear lm_head;
+  std::vector<sm::Layer> layers;
+  float* rope = nullptr;
+  std::vector<void*> owned;
+  size_t weight_bytes = 0;
+  // workspace
+  sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
+      lp_tmp, flags;
+  int64_t gen_cap = 0, gen_S = 0;
+};
+
+namespace sm {
+namespace {
+
+int dalloc(sm_model* m, void** p, size_t bytes, bool weight) {
+  SM_HIP(hipMalloc(p, bytes ? bytes : 16));
+  m->owned.push_back(*p);
+  if (weight) m->weight_bytes += bytes;
+  return SM_OK;
+}
+
+int alloc_linear(sm_model* m, Linear& L, int64_t N, int64_t K) {
+  L.N = N;
+  L.K = K;
+  if (m->cfg.quantized) {
+    const int64_t groups = ceil_div(N * K, 128);
+    SM_TRY(dalloc(m, (void**)&L.codes, (size_t)groups * 64, true));
+    SM_TRY(dalloc(m, (void**)&L.scales, (size_t)groups * 2, true));
+  } else {
+    SM_TRY(dalloc(m, (void**)&L.w, (size_t)(N * K) * 4, true));
+  }
+  return SM_OK;
+}
+
+// y (+)= x . W^T. x: activation dtype [M, K]; y f32 [M, N] (ADD or STORE).
+int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float* y, bool add,
+                  hipStream_t st) {
+  const int epi = add ? SM_EPI_ADD_F32 : SM_EPI_STORE_F32;
+  if (m->cfg.quantized)
+    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, L.K, y, L.N, epi, st);
+  return sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, y, L.N, epi, st);
+}
+
+// u = silu(x W_gate^T) * (x W_value^T) in the activation dtype.
+int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* u,
+                  hipStream_t st) {
+  if (m->cfg.quantized)
+    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, L.K, u, L.N / 2,
+                        SM_EPI_SWIGLU_F16, st);
+  SM_TRY(ensure(m->gv, (size_t)M * L.N * 4));
+  SM_TRY(sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, (float*)m->gv.p, L.N,
+                     SM_EPI_STORE_F32, st));
+  return sm_swiglu_f32((const float*)m->gv.p, M, L.N / 2, (float*)u, st);
+}
+
+size_t cache_layer_elems(const sm_model* m, int64_t S, int64_t cap) {
+  return (size_t)S * m->cfg.kv_heads * cap * m->cfg.head_dim;
+}
+
+// All decoder layers over S sequences x L tokens (ids [S*L]) at positions
+// pos0[s] + i. K/V go to caches (per-layer stride `layer_elems`, 0 = one
+// buffer reused by every layer). decode: L == 1 and attention uses `lens`.
+int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int32_t* pos0,
+               const int32_t* lens, void* kc, void* vc, size_t layer_elems, int64_t cap,
+               bool decode, hipStream_t st) {
+  const auto& c = m->cfg;
+  const int64_t rows = S * L;
+  const int64_t d = c.d_model;
+  SM_TRY(ensure(m->x, (size_t)rows * d * 4));
+  SM_TRY(ensure(m->h, (size_t)rows * std::max<int64_t>(d, m->qdim) * m->act_size));
+  SM_TRY(ensure(m->qkv, (size_t)rows * m->qkv_n * 4));
+  SM_TRY(ensure(m->qb, (size_t)rows * m->qdim * m->act_size));
+  SM_TRY(ensure(m->attn, (size_t)rows * m->qdim * m->act_size));
+  SM_TRY(ensure(m->u, (size_t)rows * c.ffn * m->act_size));
+  float* x = (float*)m->x.p;
+  SM_TRY(sm_embed(m->embed, m->kvt, ids, rows, d, c.vocab, 1.0f, x, st));
+  for (int l = 0; l < c.layers; ++l) {
+    const Layer& Ly = m->layers[l];
+    char* kl = (char*)kc + (size_t)l * layer_elems * m->act_size;
+    char* vl = (char*)vc + (size_t)l * layer_elems * m->act_size;
+    SM_TRY(sm_rmsnorm(x, Ly.attn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
+    SM_TRY(linear_f32out(m, Ly.qkv, m->h.p, rows, (float*)m->qkv.p, false, st));
+    SM_TRY(sm_rope_append((const float*)m->qkv.p, m->rope, pos0, S, L, c.heads, c.kv_heads,
+                          c.head_dim, cap, m->qb.p, m->kvt, kl, vl, m->kvt, st));
+    if (decode)
+      SM_TRY(sm_attn_decode(m->qb.p, kl, vl, lens, m->attn.p, m->kvt, m->act, S, c.heads,
+                            c.kv_heads, cap, c.head_dim, st));
+    else
+      SM_TRY(sm_attn_prefill(m->qb.p, kl, vl, pos0, m->attn.p, m->kvt, m->act, S, L, c.heads,
+                             c.kv_heads, cap, c.head_dim, st));
+    SM_TRY(linear_f32out(m, Ly.o, m->attn.p, rows, x, true, st));
+    SM_TRY(sm_rmsnorm(x, Ly.ffn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
+    SM_TRY(linear_swiglu(m, Ly.in, m->h.p, rows, m->u.p, st));
+    SM_TRY(linear_f32out(m, Ly.down, m->u.p, rows, x, true, st));
+  }
+  return SM_OK;
+}
+
+// logits [M, V] f32 = LM_head(RMSNorm_final(xrows))
+int head(sm_model* m, const float* xrows, int64_t M, float* logits, hipStream_t st) {
+  SM_TRY(ensure(m->h, (size_t)M * std::max<int64_t>(m->cfg.d_model, m->qdim) * m->act_size));
+  SM_TRY(sm_rmsnorm(xrows, m->final_norm, M, m->cfg.d_model, m->cfg.norm_eps, m->h.p, m->act, st));
+  return linear_f32out(m, m->lm_head, m->h.p, M, logits, false, st);
+}
+
+}  // namespace
+}  // namespace sm
+
+using namespace sm;
+
+extern "C" int sm_model_create(const sm_model_config* cfg, sm_model** out) {
+  SM_REQUIRE(cfg && out, "sm_model_create: null argument");
+  const sm_model_config& c = *cfg;
+  SM_REQUIRE(c.layers > 0 && c.d_model > 0 && c.heads > 0 && c.kv_heads > 0 &&
+                 c.heads % c.kv_heads == 0 && c.head_dim > 0 && c.head_dim % 2 == 0 &&
+                 c.ffn > 0 && c.vocab > 0 && c.max_seq > 0,
+             "sm_model_create: invalid model config");
+  SM_REQUIRE(c.head_dim == 64 || c.head_dim == 128, "sm_model_create: head_dim must be 64 or 128");
+  if (c.quantized)
+    SM_REQUIRE(c.d_model % 128 == 0 && c.ffn % 128 == 0 && (c.heads * c.head_dim) % 128 == 0,
+               "sm_model_create: quantized models need d_model, ffn and heads*head_dim % 128 == 0");
+  sm_model* m = new sm_model();
+  m->cfg = c;
+  m->act = c.quantized ? SM_F16 : SM_F32;
+  m->kvt = c.quantized ? SM_BF16 : SM_F32;
+  m->act_size = c.quantized ? 2 : 4;
+  m->qdim = (int64_t)c.heads * c.head_dim;
+  m->kvdim = (int64_t)c.kv_heads * c.head_dim;
+  m->qkv_n = m->qdim + 2 * m->kvdim;
+  auto fail = [&](int s) { sm_model_destroy(m); return s; };
+  int s;
+  if ((s = dalloc(m, &m->embed, (size_t)c.vocab * c.d_model * m->act_size, true))) return fail(s);
+  if ((s = dalloc(m, (void**)&m->final_norm, (size_t)c.d_model * 4, true))) return fail(s);
+  if ((s = alloc_linear(m, m->lm_head, c.vocab, c.d_model))) return fail(s);
+  m->layers.resize(c.layers);
+  for (auto& Ly : m->layers) {
+    if ((s = dalloc(m, (void**)&Ly.attn_norm, (size_t)c.d_model * 4, true))) return fail(s);
+    if ((s = dalloc(m, (void**)&Ly.ffn_norm, (size_t)c.d_model * 4, true))) return fail(s);
+    if ((s = alloc_linear(m, Ly.qkv, m->qkv_n, c.d_model))) return fail(s);
+    if ((s = alloc_linear(m, Ly.o, c.d_model, m->qdim))) return fail(s);
+    if ((s = alloc_linear(m, Ly.in, 2 * (int64_t)c.ffn, c.d_model))) return fail(s);
+    if ((s = alloc_linear(m, Ly.down, c.d_model, c.ffn))) return fail(s);
+  }
+  // RoPE table: adjacent pairs, theta^(-2p/hd), angle = pos * freq, computed in
+  // double and rounded to f32 (cos, sin) per (pos, pair).
+  const int half = c.head_dim / 2;
+  std::vector<float> tab((size_t)c.max_seq * half * 2);
+  for (int pos = 0; pos < c.max_seq; ++pos)
+    for (int p = 0; p < half; ++p) {
+      const double freq = std::pow((double)c.rope_theta, -2.0 * p / (double)c.head_dim);
+      const double ang = (double)pos * freq;
+      tab[((size_t)pos * half + p) * 2] = (float)std::cos(ang);
+      tab[((size_t)pos * half + p) * 2 + 1] = (float)std::sin(ang);
+    }
+  if ((s = dalloc(m, (void**)&m->rope, tab.size() * 4, false))) return fail(s);
+  if (hipMemcpy(m->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    set_error("sm_model_create: rope upload failed");
+    return fail(SM_ERR_HIP);
+  }
+  *out = m;
+  return SM_OK;
+}
+
+extern "C" int sm_model_destroy(sm_model* m) {
+  if (!m) return SM_OK;
+  hipDeviceSynchronize();
+  for (void* p : m->owned) hipFree(p);
+  DevBuf* bufs[] = {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits,
+                    &m->rows, &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc,
+                    &m->rkc, &m->rvc, &m->lp_tmp, &m->flags};
+  for (DevBuf* b : bufs)
+    if (b->p) hipFree(b->p);
+  delete m;
+  return SM_OK;
+}
+
+extern "C" int64_t sm_model_weight_bytes(const sm_model* m) { return m ? (int64_t)m->weight_bytes : 0; }
+
+static int tensor_target(sm_model* m, int kind, int layer, Linear** lin, void** dense,
+                         int64_t* n) {
+  const auto& c = m->cfg;
+  *lin = nullptr;
+  *dense = nullptr;
+  const bool per_layer = kind == SM_W_ATTN_NORM || kind == SM_W_FFN_NORM || kind == SM_W_QKV ||
+                         kind == SM_W_O || kind == SM_W_IN || kind == SM_W_DOWN;
+  if (per_layer) SM_REQUIRE(layer >= 0 && layer < c.layers, "layer %d out of range", layer);
+  switch (kind) {
+    case SM_W_EMBED: *dense = m->embed; *n = (int64_t)c.vocab * c.d_model; break;
+    case SM_W_FINAL_NORM: *dense = m->final_norm; *n = c.d_model; break;
+    case SM_W_LM_HEAD: *lin = &m->lm_head; break;
+    case SM_W_ATTN_NORM: *dense = m->layers[layer].attn_norm; *n = c.d_model; break;
+    case SM_W_FFN_NORM: *dense = m->layers[layer].ffn_norm; *n = c.d_model; break;
+    case SM_W_QKV: *lin = &m->layers[layer].qkv; break;
+    case SM_W_O: *lin = &m->layers[layer].o; break;
+    case SM_W_IN: *lin = &m->layers[layer].in; break;
+    case SM_W_DOWN: *lin = &m->layers[layer].down; break;
+    default: set_error("unknown tensor kind %d", kind); return SM_ERR_INVALID;
+  }
+  if (*lin) *n = (*lin)->N * (*lin)->K;
+  return SM_OK;
+}
+
+namespace sm {
+namespace {
+__global__ void f32_to_bf16_kernel(const float* __restrict__ a, int64_t n, uint16_t* __restrict__ b) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) b[i] = f32_to_bf16(a[i]);
+}
+}  // namespace
+}  // namespace sm
+
+extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float* src,
+                                   void* stream) {
+  SM_REQUIRE(m && src, "sm_model_set_tensor: null argument");
+  Linear* lin;
+  void* dense;
+  int64_t n;
+  SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n));
+  hipStream_t st = as_stream(stream);
+  if (lin) {
+    if (m->cfg.quantized) {
+      DevBuf bad;
+      SM_TRY(ensure(bad, 4));
+      zero_i32_kernel<<<1, 1, 0, st>>>((int32_t*)bad.p, 1);
+      SM_TRY(sm_q4_quantize(src, SM_F32, n, lin->codes, lin->scales, (int32_t*)bad.p, stream));
+      int32_t nbad = 0;
+      SM_HIP(hipMemcpyAsync(&nbad, bad.p, 4, hipMemcpyDeviceToHost, st));
+      SM_HIP(hipStreamSynchronize(st));
+      SM_HIP(hipFree(bad.p));
+      SM_REQUIRE(nbad == 0, "%d Q4 groups have a scale outside the f16 normal range", nbad);
+      return SM_OK;
+    }
+    SM_HIP(hipMemcpyAsync(lin->w, src, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
+    return SM_OK;
+  }
+  if (kind == SM_W_EMBED && m->kvt == SM_BF16) {
+    f32_to_bf16_kernel<<<blocks_for(n), 256, 0, st>>>(src, n, (uint16_t*)dense);
+    SM_LAUNCH_CHECK();
+    return SM_OK;
+  }
+  SM_HIP(hipMemcpyAsync(dense, src, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
+  return SM_OK;
+}
+
+extern "C" int sm_model_init_random(sm_model* m, uint64_t seed, float std, void* stream) {
+  SM_REQUIRE(m, "sm_model_init_random: null model");
+  hipStream_t st = as_stream(stream);
+  const auto& c = m->cfg;
+  int64_t maxn = (int64_t)c.vocab * c.d_model;
+  for (const auto& Ly : m->layers)
+    for (const Linear* L : {&Ly.qkv, &Ly.o, &Ly.in, &Ly.down}) maxn = std::max(maxn, L->N * L->K);
+  DevBuf tmp;
+  SM_TRY(ensure(tmp, (size_t)maxn * 4));
+  auto fill_ones = [&](float* p) {
+    fill_f32_kernel<<<blocks_for(c.d_model), 256, 0, st>>>(p, c.d_model, 1.0f);
+  };
+  uint64_t tid = 0;
+  auto randn = [&](int kind, int layer) -> int {
+    Linear* lin;
+    void* dense;
+    int64_t n;
+    SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n));
+    SM_TRY(sm_fill_normal(tmp.p, SM_F32, n, 0.f, std, mix64(seed ^ (0x51ed27ull * ++tid)), stream));
+    return sm_model_set_tensor(m, kind, layer, (const float*)tmp.p, stream);
+  };
+  auto body = [&]() -> int {
+    SM_TRY(randn(SM_W_EMBED, -1));
+    fill_ones(m->final_norm);
+    SM_TRY(randn(SM_W_LM_HEAD, -1));
+    for (int l = 0; l < c.layers; ++l) {
+      fill_ones(m->layers[l].attn_norm);
+      fill_ones(m->layers[l].ffn_norm);
+      for (int k : {SM_W_QKV, SM_W_O, SM_W_IN, SM_W_DOWN}) SM_TRY(randn(k, l));
+    }
+    return SM_OK;
+  };
+  const int s = body();
+  hipStreamSynchronize(st);
+  hipFree(tmp.p);
+  return s;
+}
+
+// ---------------------------------------------------------------- generate ---
+
+extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, int64_t P,
+                              int64_t N, float temperature, uint64_t seed, int32_t* tokens,
+                              float* behavior_lp, void* stream) {
+  SM_REQUIRE(m && prompts && tokens, "sm_rl_generate: null argument");
+  SM_REQUIRE(S > 0 && P > 0, "cannot generate from an empty prompt");
+  SM_REQUIRE(N > 0, "sm_rl_generate: max_new_tokens must be positive");
+  SM_REQUIRE(!std::isnan(temperature), "temperature must not be NaN");
+  const int64_t cap = P + N - 1;
+  SM_REQUIRE(cap <= m->cfg.max_seq, "attention cache capacity %lld exceeds max_seq_len %d",
+             (long long)cap, m->cfg.max_seq);
+  hipStream_t st = as_stream(stream);
+  const auto& c = m->cfg;
+  const size_t layer_elems = cache_layer_elems(m, S, cap);
+  SM_TRY(ensure(m->kc, layer_elems * c.layers * m->act_size));
+  SM_TRY(ensure(m->vc, layer_elems * c.layers * m->act_size));
+  SM_TRY(ensure(m->pos, (size_t)S * 4));
+  SM_TRY(ensure(m->lens, (size_t)S * 4));
+  SM_TRY(ensure(m->next_ids, (size_t)S * 4));
+  SM_TRY(ensure(m->rows, (size_t)S * c.d_model * 4));
+  SM_TRY(ensure(m->logits, (size_t)S * c.vocab * 4));
+  int32_t* pos = (int32_t*)m->pos.p;
+  int32_t* lens = (int32_t*)m->lens.p;
+  // prefill over the prompts at positions 0..P-1
+  set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, 0);
+  SM_TRY(run_layers(m, prompts, S, P, pos, nullptr, m->kc.p, m->vc.p, layer_elems, cap, false, st));
+  gather_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>((const float*)m->x.p, (int)S,
+                                                                (int)P, (int)P - 1, c.d_model,
+                                                                (float*)m->rows.p);
+  SM_TRY(head(m, (const float*)m->rows.p, S, (float*)m->logits.p, st));
+  SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, 0, tokens, N,
+                   behavior_lp, N, (int32_t*)m->next_ids.p, st));
+  // cached single-token steps
+  for (int64_t t = 1; t < N; ++t) {
+    set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, (int)(P + t - 1));
+    SM_TRY(run_layers(m, (const int32_t*)m->next_ids.p, S, 1, pos, lens, m->kc.p, m->vc.p,
+                      layer_elems, cap, true, st));
+    SM_TRY(head(m, (const float*)m->x.p, S, (float*)m->logits.p, st));
+    SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, t,
+                     tokens + t, N, behavior_lp ? behavior_lp + t : nullptr, N,
+                     (int32_t*)m->next_ids.p, st));
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+// ---------------------------------------------------------------- logprobs ---
+
+extern "C" int sm_rl_logprobs(sm_model* m, const int32_t* prompts, const int32_t* tokens,
+                              int64_t S, int64_t P, int64_t N, int64_t max_tokens_per_forward,
+                              float* lp_out, void* stream) {
+  SM_REQUIRE(m && prompts && tokens && lp_out, "sm_rl_logprobs: null argument");
+  SM_REQUIRE(S > 0 && P > 0 && N > 0, "sm_rl_logprobs: bad shape");
+  const int64_t L = P + N - 1;
+  SM_REQUIRE(L <= m->cfg.max_seq, "sequence length %lld exceeds max_seq_len %d", (long long)L,
+             m->cfg.max_seq);
+  hipStream_t st = as_stream(stream);
+  const auto& c = m->cfg;
+  const int64_t budget = max_tokens_per_forward > 0 ? max_tokens_per_forward : 65536;
+  const int64_t chunk = std::max<int64_t>(1, budget / L);
+  for (int64_t s0 = 0; s0 < S; s0 += chunk) {
+    const int64_t cs = std::min(chunk, S - s0);
+    const size_t layer_elems = cache_layer_elems(m, cs, L);
+    SM_TRY(ensure(m->rkc, layer_elems * m->act_size));
+    SM_TRY(ensure(m->rvc, layer_elems * m->act_size));
+    SM_TRY(ensure(m->ids, (size_t)cs * L * 4));
+    SM_TRY(ensure(m->pos, (size_t)cs * 4));
+    SM_TRY(ensure(m->lens, (size_t)cs * 4));
+    int32_t* ids = (int32_t*)m->ids.p;
+    build_ids_kernel<<<blocks_for(cs * L), 256, 0, st>>>(prompts + s0 * P, tokens + s0 * N, (int)cs,
+                                                         (int)P, (int)N, ids);
+    set_positions_kernel<<<blocks_for(cs), 256, 0, st>>>((int32_t*)m->pos.p, (int32_t*)m->lens.p,
+                                                         (int)cs, 0);
+    // one K/V buffer reused by every layer (layer stride 0)
+    SM_TRY(run_layers(m, ids, cs, L, (const int32_t*)m->pos.p, nullptr, m->rkc.p, m->rvc.p, 0, L,
+                      false, st));
+    // hidden states that predict tokens[:, n] sit at positions P-1+n
+    const int64_t rows = cs * N;
+    SM_TRY(ensure(m->rows, (size_t)rows * c.d_model * 4));
+    gather_span_kernel<<<blocks_for(rows * c.d_model), 256, 0, st>>>(
+        (const float*)m->x.p, (int)cs, (int)L, (int)P - 1, (int)N, c.d_model, (float*)m->rows.p);
+    // LM head + CE in row chunks bounding the [rows, V] logits to ~2 GiB
+    const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 29) / c.vocab);
+    SM_TRY(ensure(m->logits, (size_t)std::min(rows, rchunk) * c.vocab * 4));
+    for (int64_t r0 = 0; r0 < rows; r0 += rchunk) {
+      const int64_t rn = std::min(rchunk, rows - r0);
+      SM_TRY(head(m, (const float*)m->rows.p + r0 * c.d_model, rn, (float*)m->logits.p, st));
+      SM_TRY(sm_ce_rows(m->logits.p, SM_F32, tokens + s0 * N + r0, rn, c.vocab, c.vocab,
+                        lp_out + s0 * N + r0, nullptr, nullptr, 1.0f, nullptr, nullptr, st));
+    }
+  }
+  return SM_OK;
+}
+
+// ----------------------------------------------------------------- prepare ---
+
+extern "C" int sm_rl_prepare(sm_model* policy, sm_model* reference, const int32_t* prompts,
+                             const int32_t* tokens, const float* behavior_lp,
+                             const float* rewards, const float* mask, int64_t groups,
+                             int64_t group_size, int64_t P, int64_t N, double clip_epsilon,
+                             double advantage_epsilon, double kl_coefficient,
+                             int64_t max_tokens_per_forward, float* lp_cur, float* lp_ref,
+                             float* group_stats, float* dlp, int32_t* flags, void* stream) {
+  SM_REQUIRE(policy && prompts && tokens && behavior_lp && rewards && lp_cur,
+             "sm_rl_prepare: null argument");
+  SM_REQUIRE(kl_coefficient == 0.0 || (reference && lp_ref),
+             "GRPO rollout needs reference log-probs for positive KL coefficient");
+  const int64_t S = groups * group_size;
+  SM_TRY(sm_rl_logprobs(policy, prompts, tokens, S, P, N, max_tokens_per_forward, lp_cur, stream));
+  const bool use_ref = reference && lp_ref;
+  if (use_ref)
+    SM_TRY(sm_rl_logprobs(reference, prompts, tokens, S, P, N, max_tokens_per_forward, lp_ref,
+                          stream));
+  return sm_grpo_loss(rewards, lp_cur, behavior_lp, use_ref ? lp_ref : nullptr, mask, groups,
+                      group_size, N, clip_epsilon, advantage_epsilon, kl_coefficient, group_stats,
+                      nullptr, dlp, flags, stream);
+}

@@ -1,0 +1,198 @@
+// Causal flash attention for prefill and log-prob recompute (bf16 MFMA).
+//
+// Semantics: Transformer full-sequence attention (sdpa with causal mask,
+// summa-llm/src/model/attention.rs:216-298; CubeK flash forward
+// cube_attention.rs:127-220): query row r of sequence s sits at absolute
+// position pos0[s] + r and attends keys 0..=pos0[s]+r of the cache, scale
+// 1/sqrt(hd), GQA head h -> KV head h / (H/KVH).
+//
+// Tiling: one workgroup per (64 query rows, head, sequence), 4 waves x 16 rows.
+// Per 64-key tile the workgroup stages K [64][hd] and V transposed [hd][64] in
+// LDS (padded rows), then each wave computes S = Q.K^T with
+// v_mfma_f32_16x16x32_bf16 (Q fragments stay in registers for the whole
+// sweep), applies the causal mask and the online softmax on the MFMA output
+// registers (row stats reduced across the 16 lanes that share a row), writes P
+// as f16 to its LDS slice and accumulates O += P.V with a second (f16) MFMA
+// whose B operand reads the transposed V tile, converted bf16 -> f16 while
+// staging. P in f16 (11-bit significand) keeps the probability rounding 8x
+// below bf16's, which is what holds recomputed log-probs to the bf16 bar. O stays in registers; the final 1/l
+// scaling and bf16 store happen once.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace sm {
+namespace {
+
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+template <int HD, bool OF16>
+__global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
+    const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos0,
+    void* __restrict__ out, int L, int H, int KVH, int cap, float scale) {
+  constexpr int STEPS = HD / 32;
+  constexpr int KP = HD + 8;   // padded K row (elements)
+  constexpr int VP = 64 + 8;   // padded transposed-V row
+  constexpr int PP = 64 + 8;   // padded P row
+  __shared__ __attribute__((aligned(16))) uint16_t ks[64 * KP];
+  __shared__ __attribute__((aligned(16))) _Float16 vts[HD * VP];
+  __shared__ __attribute__((aligned(16))) _Float16 ps[4][16 * PP];
+
+  const int qt = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
+  const int kvh = h / (H / KVH);
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  const int p0 = pos0[s];
+  const int r0 = qt * 64 + wave * 16;  // first query row of this wave
+  const size_t kv_base = ((size_t)s * KVH + kvh) * cap * HD;
+
+  // Q fragments (A operand): lane (row j, group g)
+  bf8 qa[STEPS];
+  {
+    const int r = r0 + j;
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) {
+      if (r < L)
+        qa[st] = *reinterpret_cast<const bf8*>(q + (((size_t)s * L + r) * H + h) * HD + st * 32 + g * 8);
+      else
+        qa[st] = bf8{};
+    }
+  }
+  f4 o[HD / 16];
+#pragma unroll
+  for (int d = 0; d < HD / 16; ++d) o[d] = f4{0.f, 0.f, 0.f, 0.f};
+  float m[4], l[4];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) { m[r] = -INFINITY; l[r] = 0.f; }
+
+  const int last_row = min(qt * 64 + 63, L - 1);
+  const int kend = p0 + last_row + 1;  // keys [0, kend) needed by this workgroup
+  for (int kt = 0; kt < kend; kt += 64) {
+    __syncthreads();  // previous tile fully consumed
+    // ---- stage K tile (row-major, padded) and V tile transposed
+    constexpr int CH = HD / 8;  // 16-byte chunks per row
+    for (int c = threadIdx.x; c < 64 * CH; c += 256) {
+      const int kr = c / CH, cc = c % CH;
+      const int key = kt + kr;
+      u32x4 kv = u32x4{0u, 0u, 0u, 0u}, vv = u32x4{0u, 0u, 0u, 0u};
+      if (key < kend && key < cap) {
+        kv = *reinterpret_cast<const u32x4*>(kc + kv_base + (size_t)key * HD + cc * 8);
+        vv = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)key * HD + cc * 8);
+      }
+      *reinterpret_cast<u32x4*>(&ks[kr * KP + cc * 8]) = kv;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        vts[(cc * 8 + 2 * e) * VP + kr] = (_Float16)bf16lo(vv[e]);
+        vts[(cc * 8 + 2 * e + 1) * VP + kr] = (_Float16)bf16hi(vv[e]);
+      }
+    }
+    __syncthreads();
+    if (r0 >= L) continue;  // wave has no rows (uniform per wave)
+    // ---- S = Q K^T for 4 key blocks
+    f4 sc[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) {
+        const bf8 kf = *reinterpret_cast<const bf8*>(&ks[(kb * 16 + j) * KP + st * 32 + g * 8]);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], kf, acc, 0, 0, 0);
+      }
+      sc[kb] = acc;
+    }
+    // ---- mask + online softmax; lane holds rows 4g+r, key kb*16+j
+    float alpha[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = r0 + 4 * g + r;
+      const int qpos = p0 + row;
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const int key = kt + kb * 16 + j;
+        const float v = (row < L && key <= qpos) ? sc[kb][r] * scale : -INFINITY;
+        sc[kb][r] = v;
+        mx = fmaxf(mx, v);
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+      const float mnew = fmaxf(m[r], mx);
+      alpha[r] = (m[r] == -INFINITY) ? 0.f : __expf(m[r] - mnew);
+      float sum = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const float p = (sc[kb][r] == -INFINITY) ? 0.f : __expf(sc[kb][r] - mnew);
+        sc[kb][r] = p;
+        sum += p;
+      }
+#pragma unroll
+      for (int off = 1; off < 16; off <<= 1) sum += __shfl_xor(sum, off, kWave);
+      l[r] = l[r] * alpha[r] + sum;
+      m[r] = mnew;
+    }
+#pragma unroll
+    for (int d = 0; d < HD / 16; ++d)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) o[d][r] *= alpha[r];
+    // ---- P (f16) to this wave's LDS slice: P[row 4g+r][key kb*16+j]
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ps[wave][(4 * g + r) * PP + kb * 16 + j] = (_Float16)sc[kb][r];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- O += P V: A = P rows (lane row j), B = V^T rows (lane dim j)
+#pragma unroll
+    for (int st = 0; st < 2; ++st) {
+      const h8 pa = *reinterpret_cast<const h8*>(&ps[wave][j * PP + st * 32 + g * 8]);
+#pragma unroll
+      for (int d = 0; d < HD / 16; ++d) {
+        const h8 vb = *reinterpret_cast<const h8*>(&vts[(d * 16 + j) * VP + st * 32 + g * 8]);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
+      }
+    }
+  }
+  if (r0 >= L) return;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = r0 + 4 * g + r;
+    if (row >= L) continue;
+    const float inv = 1.f / l[r];
+    const size_t ob = (((size_t)s * L + row) * H + h) * HD;
+#pragma unroll
+    for (int d = 0; d < HD / 16; ++d) {
+      if constexpr (OF16) static_cast<_Float16*>(out)[ob + d * 16 + j] = (_Float16)(o[d][r] * inv);
+      else static_cast<uint16_t*>(out)[ob + d * 16 + j] = f32_to_bf16(o[d][r] * inv);
+    }
+  }
+}
+
+}  // namespace
+
+int attn_prefill_bf16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                      const int32_t* pos0, void* out, bool out_f16, int S, int L, int H, int KVH,
+                      int cap, int hd, hipStream_t st) {
+  if (S > 65535 || H > 65535) {
+    set_error("sm_attn_prefill: S and H must be <= 65535");
+    return SM_ERR_UNSUPPORTED;
+  }
+  const dim3 grid((unsigned)ceil_div(L, 64), (unsigned)H, (unsigned)S);
+  const float scale = 1.0f / sqrtf((float)hd);
+#define SM_PF(HD, OF)                                                                         \
+  attn_prefill_bf16_kernel<HD, OF><<<grid, 256, 0, st>>>(q, kc, vc, pos0, out, L, H, KVH, cap, \
+                                                         scale)
+  if (hd == 64) {
+    if (out_f16) SM_PF(64, true); else SM_PF(64, false);
+  } else {
+    if (out_f16) SM_PF(128, true); else SM_PF(128, false);
+  }
+#undef SM_PF
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+}  // namespace sm

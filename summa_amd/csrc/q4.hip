@@ -23,8 +23,9 @@
 // mantissa, one packed subtract / fma) and one packed multiply by the group
 // scale. q * scale is exact in f16 (<= 11 significant bits) as long as the
 // scale is an f16 normal, which sm_q4_quantize checks. The A operand
-// (activations) is read by the lanes whose row is < M only, converted from
-// bf16 to f16 and permuted to the same k order as the dequantised words. For
+// (activations, f16 or bf16 in HBM) is read by the lanes whose row is < M
+// only, converted to f16 if needed and permuted to the same k order as the
+// dequantised words. For
 // tiny N the four waves of a workgroup split the K groups and merge their
 // accumulators through LDS in a fixed order (deterministic).
 #include <cmath>
@@ -42,8 +43,11 @@ enum Epi : int {
   EPI_STORE_F32 = 0,   // y (f32) = acc
   EPI_STORE_BF16 = 1,  // y (bf16) = acc
   EPI_ADD_F32 = 2,     // y (f32) += acc          (residual stream)
-  EPI_SWIGLU_BF16 = 3  // y (bf16)[m, j] = silu(acc[m, j]) * acc[m, F + j]
+  EPI_SWIGLU_BF16 = 3, // y (bf16)[m, j] = silu(acc[m, j]) * acc[m, F + j]
+  EPI_SWIGLU_F16 = 4   // same, f16 output
 };
+
+constexpr bool is_swiglu(int e) { return e == EPI_SWIGLU_BF16 || e == EPI_SWIGLU_F16; }
 
 __device__ inline h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 
@@ -69,12 +73,17 @@ __device__ inline h8 act_frag(u32x4 v) {
             (_Float16)bf16hi(v.y), (_Float16)bf16hi(v.w)};
 }
 
+// 8 f16 activations (k..k+7) -> k order [0,4,1,5,2,6,3,7].
+__device__ inline h8 act_frag_f16(h8 v) {
+  return h8{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+}
+
 __device__ inline float silu(float g) { return g / (1.f + __expf(-g)); }
 
 struct Q4Args {
   const uint8_t* codes;    // [N, K/2]
   const uint16_t* scales;  // [N, K/128] bf16
-  const uint16_t* x;       // [M, ldx] bf16
+  const void* x;           // [M, ldx] bf16 or f16
   void* y;                 // [M, ldy]
   int M, N, K;             // N = weight rows (for SWIGLU: 2F)
   int ldx, ldy;
@@ -84,7 +93,7 @@ struct Q4Args {
 // MT: 16-row M blocks per wave; NB: 16-column N blocks per wave;
 // KSPLIT: 1 = the 4 waves tile N (WG tile 16MT x 64NB), 4 = the 4 waves split
 // the K groups of one 16MT x 16NB tile.
-template <int MT, int NB, int KSPLIT, int EPI>
+template <int MT, int NB, int KSPLIT, int EPI, bool XF16>
 __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
@@ -93,12 +102,12 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
   const int c0 = blockIdx.x * tile_cols + ((KSPLIT == 1) ? wave * wave_cols : 0);
   const int ngroups = a.K / 128;
-  const int half_cols = (EPI == EPI_SWIGLU_BF16) ? wave_cols / 2 : wave_cols;
+  const int half_cols = is_swiglu(EPI) ? wave_cols / 2 : wave_cols;
   // Weight row read by this lane for block b.
   int brow[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    if (EPI == EPI_SWIGLU_BF16) {
+    if (is_swiglu(EPI)) {
       // first NB/2 blocks: gate columns, last NB/2: value columns (same j)
       const int col = c0 / 2 + (b % (NB / 2)) * 16 + j;  // logical h column
       brow[b] = (col < a.ncols) ? ((b < NB / 2) ? col : a.ncols + col) : -1;
@@ -140,8 +149,11 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
         const int row = m0 + mt * 16 + j;
         h8 af = h8{0, 0, 0, 0, 0, 0, 0, 0};
         if (row < a.M) {
-          const uint16_t* xp = a.x + (size_t)row * a.ldx + kg * 128 + g * 32 + s * 8;
-          af = act_frag(*reinterpret_cast<const u32x4*>(xp));
+          const size_t xo = (size_t)row * a.ldx + kg * 128 + g * 32 + s * 8;
+          if constexpr (XF16)
+            af = act_frag_f16(*reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo));
+          else
+            af = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
         }
 #pragma unroll
         for (int b = 0; b < NB; ++b)
@@ -175,13 +187,16 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
     for (int r = 0; r < 4; ++r) {
       const int row = m0 + mt * 16 + 4 * g + r;
       if (row >= a.M) continue;
-      if constexpr (EPI == EPI_SWIGLU_BF16) {
+      if constexpr (is_swiglu(EPI)) {
 #pragma unroll
         for (int b = 0; b < NB / 2; ++b) {
           const int col = c0 / 2 + b * 16 + j;
           if (col < a.ncols) {
             const float h = silu(acc[mt][b][r]) * acc[mt][b + NB / 2][r];
-            static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(h);
+            if constexpr (EPI == EPI_SWIGLU_F16)
+              static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = (_Float16)h;
+            else
+              static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(h);
           }
         }
       } else {
@@ -200,44 +215,46 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   }
 }
 
-template <int MT, int NB, int KSPLIT>
-int launch_q4(const Q4Args& a, int epi, hipStream_t st) {
+template <int MT, int NB, int KSPLIT, bool XF16>
+int launch_q4_x(const Q4Args& a, int epi, hipStream_t st) {
+  static_assert(NB % 2 == 0, "SwiGLU pairs gate/value blocks");
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
-  const int logical_cols = (epi == EPI_SWIGLU_BF16) ? 2 * a.ncols : a.N;
+  const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
   dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)ceil_div(a.M, 16 * MT));
   switch (epi) {
-    case EPI_STORE_F32: q4_gemm_kernel<MT, NB, KSPLIT, EPI_STORE_F32><<<grid, 256, 0, st>>>(a); break;
-    case EPI_STORE_BF16: q4_gemm_kernel<MT, NB, KSPLIT, EPI_STORE_BF16><<<grid, 256, 0, st>>>(a); break;
-    case EPI_ADD_F32: q4_gemm_kernel<MT, NB, KSPLIT, EPI_ADD_F32><<<grid, 256, 0, st>>>(a); break;
-    case EPI_SWIGLU_BF16:
-      if constexpr (NB % 2 == 0) {
-        q4_gemm_kernel<MT, NB, KSPLIT, EPI_SWIGLU_BF16><<<grid, 256, 0, st>>>(a);
-        break;
-      } else {
-        set_error("internal: SwiGLU epilogue needs an even NB");
-        return SM_ERR_INVALID;
-      }
+#define SM_Q4_EPI(E) \
+    case E: q4_gemm_kernel<MT, NB, KSPLIT, E, XF16><<<grid, 256, 0, st>>>(a); break;
+    SM_Q4_EPI(EPI_STORE_F32)
+    SM_Q4_EPI(EPI_STORE_BF16)
+    SM_Q4_EPI(EPI_ADD_F32)
+    SM_Q4_EPI(EPI_SWIGLU_BF16)
+    SM_Q4_EPI(EPI_SWIGLU_F16)
+#undef SM_Q4_EPI
     default: set_error("sm_q4_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
   }
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
 
+template <int MT, int NB, int KSPLIT>
+int launch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
+  return xf16 ? launch_q4_x<MT, NB, KSPLIT, true>(a, epi, st)
+              : launch_q4_x<MT, NB, KSPLIT, false>(a, epi, st);
+}
+
 // Picks the tile shape: M-blocks per wave from M, and K-split across the four
 // waves when there are too few column tiles to fill the 256 CUs.
-int dispatch_q4(const Q4Args& a, int epi, hipStream_t st) {
-  const int logical_cols = (epi == EPI_SWIGLU_BF16) ? 2 * a.ncols : a.N;
-  const bool swiglu = epi == EPI_SWIGLU_BF16;
+int dispatch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
+  const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
   const int mtiles16 = (int)ceil_div(a.M, 16);
   // Waves along N with 2 blocks each gives 128-column tiles.
   const bool few = ceil_div(logical_cols, 128) * ceil_div(a.M, 128) < 512;
 #define SM_Q4_CASE(MT)                                                      \
   do {                                                                      \
-    if (few && a.K >= 4 * 128) return launch_q4<MT, 2, 4>(a, epi, st);      \
-    return launch_q4<MT, 2, 1>(a, epi, st);                                 \
+    if (few && a.K >= 4 * 128) return launch_q4<MT, 2, 4>(a, epi, xf16, st); \
+    return launch_q4<MT, 2, 1>(a, epi, xf16, st);                           \
   } while (0)
-  (void)swiglu;
   if (mtiles16 <= 1) SM_Q4_CASE(1);
   if (mtiles16 <= 2) SM_Q4_CASE(2);
   if (mtiles16 <= 4) SM_Q4_CASE(4);
@@ -311,8 +328,8 @@ extern "C" int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* code
 }
 
 extern "C" int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
-                            const uint16_t* x, int64_t M, int64_t ldx, void* y, int64_t ldy,
-                            int epilogue, void* stream) {
+                            const void* x, int x_dtype, int64_t M, int64_t ldx, void* y,
+                            int64_t ldy, int epilogue, void* stream) {
   using namespace sm;
   SM_REQUIRE(codes && scales && x && y, "sm_q4_matmul: null buffer");
   SM_REQUIRE(K > 0 && K % 128 == 0, "sm_q4_matmul: K=%lld must be a positive multiple of 128",
@@ -323,12 +340,13 @@ extern "C" int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_
   SM_REQUIRE(reinterpret_cast<uintptr_t>(codes) % 16 == 0 &&
                  reinterpret_cast<uintptr_t>(x) % 16 == 0,
              "sm_q4_matmul: codes and x must be 16-byte aligned");
-  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_BF16,
+  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16,
              "sm_q4_matmul: unknown epilogue %d", epilogue);
-  const int64_t ncols = (epilogue == EPI_SWIGLU_BF16) ? N / 2 : N;
-  SM_REQUIRE(epilogue != EPI_SWIGLU_BF16 || N % 2 == 0, "sm_q4_matmul: SwiGLU needs even N");
+  SM_REQUIRE(x_dtype == SM_BF16 || x_dtype == SM_F16, "sm_q4_matmul: x must be bf16 or f16");
+  const int64_t ncols = is_swiglu(epilogue) ? N / 2 : N;
+  SM_REQUIRE(!is_swiglu(epilogue) || N % 2 == 0, "sm_q4_matmul: SwiGLU needs even N");
   SM_REQUIRE(ldy >= ncols, "sm_q4_matmul: ldy < output columns");
   if (M == 0) return SM_OK;
   Q4Args a{codes, scales, x, y, (int)M, (int)N, (int)K, (int)ldx, (int)ldy, (int)ncols};
-  return dispatch_q4(a, epilogue, as_stream(stream));
+  return dispatch_q4(a, epilogue, x_dtype == SM_F16, as_stream(stream));
 }

@@ -189,15 +189,17 @@ class Q4Weight:
 
 def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
               epilogue: int = _lib.SM_EPI_STORE_F32) -> torch.Tensor:
-    """y = x . W^T with Q4G128 weights; x bf16 [M, K]."""
+    """y = x . W^T with Q4G128 weights; x bf16 or f16 [M, K]."""
     _dev(x, "x")
-    if x.dtype != torch.bfloat16:
-        raise TypeError("x must be bfloat16")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("x must be bfloat16 or float16")
     M, K = x.shape
     if K != w.k:
         raise ValueError(f"packed linear input width mismatch ({K} != {w.k})")
     if epilogue == _lib.SM_EPI_SWIGLU_BF16:
         shape, dt = (M, w.n // 2), torch.bfloat16
+    elif epilogue == _lib.SM_EPI_SWIGLU_F16:
+        shape, dt = (M, w.n // 2), torch.float16
     elif epilogue == _lib.SM_EPI_STORE_BF16:
         shape, dt = (M, w.n), torch.bfloat16
     else:
@@ -207,6 +209,6 @@ def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
             raise ValueError("SM_EPI_ADD_F32 needs an output to accumulate into")
         out = torch.empty(shape, dtype=dt, device=x.device)
     _dev(out, "out")
-    call("sm_q4_matmul", w.codes.data_ptr(), w.scales.data_ptr(), w.n, w.k, x.data_ptr(), M,
-         x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
+    call("sm_q4_matmul", w.codes.data_ptr(), w.scales.data_ptr(), w.n, w.k, x.data_ptr(), _dt(x),
+         M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
     return out

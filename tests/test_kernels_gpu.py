@@ -1,0 +1,169 @@
+"""Per-kernel GPU checks: attention (decode / prefill), RoPE + KV append, RMSNorm,
+embedding and token selection, each against a CPU restatement."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from summa_amd import _lib
+from summa_amd._lib import SM_BF16, SM_F32, call
+
+pytestmark = pytest.mark.gpu
+
+
+def _s():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _bf16(a, dev):
+    return torch.from_numpy(oracle.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _attn_ref(q, k, v, lens):
+    """q [S, H, hd], k/v [S, KVH, T, hd] -> [S, H, hd] in f64 (repeat_kv GQA)."""
+    S, H, hd = q.shape
+    KVH = k.shape[1]
+    out = np.zeros((S, H, hd))
+    for s in range(S):
+        for h in range(H):
+            kv = h // (H // KVH)
+            n = lens[s]
+            sc = k[s, kv, :n].astype(np.float64) @ q[s, h].astype(np.float64) / np.sqrt(hd)
+            p = np.exp(sc - sc.max())
+            out[s, h] = (p / p.sum()) @ v[s, kv, :n].astype(np.float64)
+    return out
+
+
+@pytest.mark.parametrize("S,H,KVH,hd,cap", [(3, 12, 12, 64, 300), (4, 16, 4, 128, 1100),
+                                            (2, 4, 4, 64, 70), (5, 8, 1, 128, 257)])
+def test_attn_decode_bf16(dev, S, H, KVH, hd, cap):
+    print(f"case S={S} H={H} KVH={KVH} hd={hd} cap={cap}", flush=True)
+    rng = np.random.default_rng(S * H + cap)
+    q = oracle.round_bf16(rng.normal(0, 1, (S, H, hd)).astype(np.float32))
+    k = oracle.round_bf16(rng.normal(0, 1, (S, KVH, cap, hd)).astype(np.float32))
+    v = oracle.round_bf16(rng.normal(0, 1, (S, KVH, cap, hd)).astype(np.float32))
+    lens = rng.integers(1, cap + 1, S).astype(np.int32)
+    lens[0] = cap
+    out = torch.empty(S, H, hd, dtype=torch.bfloat16, device=dev)
+    L = torch.from_numpy(lens).to(dev)
+    qd, kd, vd = _bf16(q, dev), _bf16(k, dev), _bf16(v, dev)
+    call("sm_attn_decode", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), L.data_ptr(),
+         out.data_ptr(), SM_BF16, SM_BF16, S, H, KVH, cap, hd, _s())
+    ref = _attn_ref(q, k, v, lens)
+    # bf16 output: one rounding (2^-8 relative) on top of fp32 accumulation
+    np.testing.assert_allclose(out.float().cpu().numpy(), ref, rtol=2 ** -7, atol=2e-3)
+
+
+@pytest.mark.parametrize("S,L,p0,H,KVH,hd", [(2, 100, 0, 4, 4, 64), (2, 64, 0, 16, 4, 128),
+                                             (3, 37, 5, 12, 12, 64), (1, 130, 3, 8, 2, 128)])
+@pytest.mark.parametrize("dtype", [SM_BF16, SM_F32])
+def test_attn_prefill(dev, S, L, p0, H, KVH, hd, dtype):
+    print(f"case S={S} L={L} p0={p0} H={H} KVH={KVH} hd={hd} dtype={dtype}", flush=True)
+    rng = np.random.default_rng(L + hd)
+    cap = p0 + L
+    q = rng.normal(0, 1, (S, L, H, hd)).astype(np.float32)
+    k = rng.normal(0, 1, (S, KVH, cap, hd)).astype(np.float32)
+    v = rng.normal(0, 1, (S, KVH, cap, hd)).astype(np.float32)
+    if dtype == SM_BF16:
+        q, k, v = oracle.round_bf16(q), oracle.round_bf16(k), oracle.round_bf16(v)
+        qd, kd, vd = _bf16(q, dev), _bf16(k, dev), _bf16(v, dev)
+        out = torch.empty(S, L, H, hd, dtype=torch.bfloat16, device=dev)
+    else:
+        qd, kd, vd = (torch.from_numpy(a).to(dev) for a in (q, k, v))
+        out = torch.empty(S, L, H, hd, dtype=torch.float32, device=dev)
+    pos0 = torch.full((S,), p0, dtype=torch.int32, device=dev)
+    call("sm_attn_prefill", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), pos0.data_ptr(),
+         out.data_ptr(), dtype, dtype, S, L, H, KVH, cap, hd, _s())
+    got = out.float().cpu().numpy()
+    for r in range(L):
+        ref = _attn_ref(q[:, r], k, v, np.full(S, p0 + r + 1))
+        if dtype == SM_BF16:
+            # P and V enter the P.V MFMA as f16; output rounded to bf16
+            np.testing.assert_allclose(got[:, r], ref, rtol=2 ** -7, atol=3e-3)
+        else:
+            np.testing.assert_allclose(got[:, r], ref, rtol=1e-5, atol=1e-5)
+
+
+def _rope_table(max_pos, hd, theta=1e4):
+    half = hd // 2
+    p = np.arange(half)
+    freq = theta ** (-2.0 * p / hd)
+    ang = np.arange(max_pos)[:, None] * freq[None, :]
+    return np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)
+
+
+def test_rope_append_adjacent_pairs(dev):
+    S, L, H, KVH, hd, cap = 2, 5, 4, 2, 64, 16
+    rng = np.random.default_rng(0)
+    qkv = rng.normal(0, 1, (S * L, (H + 2 * KVH) * hd)).astype(np.float32)
+    tab = _rope_table(cap, hd)
+    pos0 = np.array([0, 7], np.int32)
+    q = torch.empty(S * L, H, hd, device=dev)
+    kc = torch.zeros(S, KVH, cap, hd, device=dev)
+    vc = torch.zeros(S, KVH, cap, hd, device=dev)
+    qkv_d, tab_d, pos_d = (torch.from_numpy(a).to(dev) for a in (qkv, tab, pos0))
+    call("sm_rope_append", qkv_d.data_ptr(), tab_d.data_ptr(), pos_d.data_ptr(), S, L, H, KVH,
+         hd, cap, q.data_ptr(), SM_F32, kc.data_ptr(), vc.data_ptr(), SM_F32, _s())
+    x = qkv.reshape(S, L, H + 2 * KVH, hd)
+    for s in range(S):
+        for i in range(L):
+            pos = pos0[s] + i
+            c, sn = tab[pos, :, 0], tab[pos, :, 1]
+            a, b = x[s, i, :, 0::2], x[s, i, :, 1::2]
+            rot = np.empty_like(x[s, i])
+            rot[:, 0::2] = a * c - b * sn
+            rot[:, 1::2] = b * c + a * sn
+            np.testing.assert_allclose(q.cpu().numpy()[s * L + i], rot[:H], rtol=1e-6, atol=1e-6)
+            np.testing.assert_allclose(kc.cpu().numpy()[s, :, pos], rot[H:H + KVH], rtol=1e-6, atol=1e-6)
+            np.testing.assert_array_equal(vc.cpu().numpy()[s, :, pos], x[s, i, H + KVH:])
+    # untouched cache slots stay zero
+    assert np.all(kc.cpu().numpy()[0, :, L:] == 0)
+
+
+def test_rmsnorm_and_embed(dev):
+    rows, d, V = 5, 768, 100
+    rng = np.random.default_rng(1)
+    table = rng.normal(0, 0.02, (V, d)).astype(np.float32)
+    ids = np.array([3, 0, 99, 42, 3], np.int32)
+    x = torch.empty(rows, d, device=dev)
+    table_d, ids_d = torch.from_numpy(table).to(dev), torch.from_numpy(ids).to(dev)
+    call("sm_embed", table_d.data_ptr(), SM_F32, ids_d.data_ptr(), rows, d, V, 1.0,
+         x.data_ptr(), _s())
+    np.testing.assert_array_equal(x.cpu().numpy(), table[ids])
+    g = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    y = torch.empty(rows, d, dtype=torch.bfloat16, device=dev)
+    g_d = torch.from_numpy(g).to(dev)
+    call("sm_rmsnorm", x.data_ptr(), g_d.data_ptr(), rows, d, 1e-5, y.data_ptr(), SM_BF16, _s())
+    xr = table[ids].astype(np.float64)
+    ref = xr / np.sqrt((xr ** 2).mean(1, keepdims=True) + 1e-5) * g
+    np.testing.assert_allclose(y.float().cpu().numpy(), ref, rtol=2 ** -8, atol=1e-6)
+
+
+@pytest.mark.parametrize("temperature", [0.0, 1.0, 0.7])
+def test_sample_matches_oracle(dev, temperature):
+    rows, V = 16, 32768
+    rng = np.random.default_rng(2)
+    logits = rng.normal(0, 1, (rows, V)).astype(np.float32)
+    logits[3, 100] = logits[3, 200] = 50.0  # exact tie: lowest index wins under greedy
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    lp = torch.empty(rows, device=dev)
+    ld = torch.from_numpy(logits).to(dev)
+    call("sm_sample", ld.data_ptr(), rows, V, V, float(temperature), 1234, 5, tok.data_ptr(), 1,
+         lp.data_ptr(), 1, None, _s())
+    rt, rlp = oracle.sample(logits, temperature, 1234, 5)
+    np.testing.assert_array_equal(tok.cpu().numpy(), rt)
+    np.testing.assert_allclose(lp.cpu().numpy(), rlp, atol=1e-5)
+    if temperature == 0.0:
+        assert tok.cpu().numpy()[3] == 100
+
+
+def test_sample_temperature_distribution(dev):
+    # Gumbel-max draws follow softmax(l / T): chi-square-style check on a 4-way row
+    V, rows, T = 4, 20000, 0.5
+    base = np.array([0.0, 0.5, 1.0, -1.0], np.float32)
+    logits = torch.from_numpy(np.tile(base, (rows, 1))).to(dev)
+    tok = torch.empty(rows, dtype=torch.int32, device=dev)
+    call("sm_sample", logits.data_ptr(), rows, V, V, T, 7, 0, tok.data_ptr(), 1, None, 1, None, _s())
+    counts = np.bincount(tok.cpu().numpy(), minlength=V) / rows
+    p = np.exp(base / T) / np.exp(base / T).sum()
+    assert np.all(np.abs(counts - p) < 0.015), (counts, p)

@@ -227,3 +227,13 @@ def test_q4_matvec_equals_decode_times_x():
     np.testing.assert_allclose(y, dense @ x, atol=1e-5)
     # transposed operand would differ
     assert not np.allclose(y, (dense.T[:rows, :rows] @ x[:rows]), atol=1e-3)
+
+
+def test_f16_rounding_matches_numpy_float16():
+    # IEEE binary16 round-to-nearest-even incl. subnormals and overflow
+    rng = np.random.default_rng(0)
+    v = np.concatenate([rng.normal(0, 1, 2000), rng.normal(0, 1e-5, 500), rng.normal(0, 3e4, 500),
+                        [65504.0, 65519.0, 65520.0, -70000.0, 0.0, -0.0, 2.0 ** -25, 3 * 2.0 ** -26]])
+    v = v.astype(np.float32)
+    got = np.array([oracle.lib().or_round_f16(float(x)) for x in v], np.float32)
+    np.testing.assert_array_equal(got, v.astype(np.float16).astype(np.float32))

@@ -91,3 +91,23 @@ def test_rejects_bad_shapes(dev):
     with pytest.raises(_lib.SummaError, match="width mismatch|K="):
         bad = ops.Q4Weight(w.codes, w.scales, 64, 200)
         ops.q4_matmul(bad, torch.zeros(2, 200, dtype=torch.bfloat16, device=dev))
+
+
+@pytest.mark.parametrize("m", [1, 7, 128])
+def test_matmul_f16_activations_and_swiglu_f16(dev, m):
+    n, k = 768, 3072
+    w = _weights(n, k, 3)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(m).normal(0, 1, (m, k)).astype(np.float32)
+    xh = x.astype(np.float16)
+    xr = xh.astype(np.float32)  # f16 values are what the kernel consumes
+    y = ops.q4_matmul(qw, torch.from_numpy(xh).to(dev)).cpu().numpy()
+    y_ref = _oracle_matmul(codes, scales, n, k, xr)
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    assert np.all(np.abs(y - y_ref) <= tol)
+    F = n // 2
+    h = ops.q4_matmul(qw, torch.from_numpy(xh).to(dev),
+                      epilogue=_lib.SM_EPI_SWIGLU_F16).float().cpu().numpy()
+    g, v = y_ref[:, :F], y_ref[:, F:]
+    np.testing.assert_allclose(h, g / (1 + np.exp(-g)) * v, rtol=2 ** -10, atol=1e-6)
