@@ -58,7 +58,8 @@ def _declare(L: C.CDLL) -> None:
 
 class OrModel(C.Structure):
     """Mirror of ``or_model`` in model.c (host weight pointers)."""
-    _fields_ = [(n, C.c_int32) for n in ("layers", "d", "H", "KVH", "hd", "F", "V", "quantized")] + \
+    _fields_ = [(n, C.c_int32) for n in ("layers", "d", "H", "KVH", "hd", "F", "V", "quantized",
+                                         "acc64")] + \
         [("eps", C.c_float), ("theta", C.c_float)] + \
         [(n, C.c_void_p) for n in ("embed", "attn_norm", "ffn_norm", "final_norm",
                                    "qkv", "o", "in_", "down", "lm_head",
@@ -179,9 +180,10 @@ class HostModel:
     [layers, d], final_norm [d], and linears qkv / o / in / down [layers, N, K],
     lm_head [V, d] in [out, in] layout. When ``quantized`` the linears are
     packed with the Q4G128 oracle codec and the embedding is rounded to bf16.
+    ``acc64`` (default: on for quantized models) accumulates matmuls in f64.
     """
 
-    def __init__(self, cfg: dict, weights: dict, quantized: bool):
+    def __init__(self, cfg: dict, weights: dict, quantized: bool, acc64: bool | None = None):
         self.cfg, self.quantized = cfg, quantized
         self._keep = []
         w = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}
@@ -192,6 +194,7 @@ class HostModel:
         for k in ("layers", "d", "H", "KVH", "hd", "F", "V"):
             setattr(m, k, int(cfg[k]))
         m.quantized = int(quantized)
+        m.acc64 = int(quantized if acc64 is None else acc64)
         m.eps, m.theta = float(cfg.get("eps", 1e-5)), float(cfg.get("theta", 1e4))
         for k in ("embed", "attn_norm", "ffn_norm", "final_norm"):
             setattr(m, k, self._ptr(w[k]))

@@ -15,8 +15,11 @@
  * with the build's precision policy for quantized models: values rounded to
  * f16 where the device feeds a matmul (norm outputs, attention output, SwiGLU
  * output), to bf16 where it stores bf16 (q, k, v, embedding), fp32 everywhere
- * else, sequential fp32 accumulation in every dot product (the
- * order PackedTensor::matrix_vector uses, quantization.rs:642-651).
+ * else. Matmul dot products accumulate sequentially in fp32 (the order
+ * PackedTensor::matrix_vector uses, quantization.rs:642-651) or, with acc64,
+ * in f64: with 16-bit activations any fp32 summation order moves per-token
+ * log-probs by up to ~1e-3 at d=2048, so the quantized parity checks compare
+ * the device against the exactly-accumulated value of the same products.
  */
 #include <math.h>
 #include <stdint.h>
@@ -27,6 +30,8 @@
 
 typedef struct or_model {
   int32_t layers, d, H, KVH, hd, F, V, quantized;
+  int32_t acc64; /* 1: accumulate matmul dot products in f64 (exact sum of the
+                    same products); 0: sequential f32 as matrix_vector does */
   float eps, theta;
   const float* embed;      /* [V, d] */
   const float* attn_norm;  /* [layers, d] */
@@ -82,13 +87,17 @@ static void linear(const or_model* m, int kind, int layer, const float* x, int64
   for (int64_t r = 0; r < M; ++r)
     for (int64_t n = 0; n < N; ++n) {
       float acc = 0.f;
+      double acc64 = 0.0;
       const float* xr = x + r * K;
       if (w) {
         const float* wr = w + n * K;
-        for (int64_t k = 0; k < K; ++k) acc += wr[k] * xr[k];
+        if (m->acc64) for (int64_t k = 0; k < K; ++k) acc64 += (double)wr[k] * xr[k];
+        else for (int64_t k = 0; k < K; ++k) acc += wr[k] * xr[k];
       } else {
-        for (int64_t k = 0; k < K; ++k) acc += q4_at(c, s, n * K + k) * xr[k];
+        if (m->acc64) for (int64_t k = 0; k < K; ++k) acc64 += (double)q4_at(c, s, n * K + k) * xr[k];
+        else for (int64_t k = 0; k < K; ++k) acc += q4_at(c, s, n * K + k) * xr[k];
       }
+      if (m->acc64) acc = (float)acc64;
       if (add) y[r * N + n] += acc; else y[r * N + n] = acc;
     }
 }

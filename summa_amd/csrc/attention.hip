@@ -14,8 +14,9 @@
 // as the 16-row A operand (padded) and K rows read straight from HBM as the B
 // operand (natural [pos][hd] layout is already k-contiguous per lane). The
 // online softmax runs on the MFMA output registers, probabilities go through a
-// per-wave LDS slice, and P.V is a VALU FMA pass with lanes spread over hd so
-// each V row is one coalesced wave-wide load. Waves merge (max, sum, O) in LDS
+// per-wave LDS slice, and P.V is a VALU FMA pass with hd/8 lanes per V row
+// (16-byte loads, several rows per wave instruction, unrolled for loads in
+// flight). Waves merge (max, sum, O) in LDS
 // at the end in a fixed order.
 //
 // Prefill / recompute (many queries, causal) uses the flash-attention kernel
@@ -38,7 +39,7 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ lens,
     TO* __restrict__ out, int H, int KVH, int cap, float scale) {
-  constexpr int LPK = HD / 2;      // lanes per key row in the P.V pass (2 dims each)
+  constexpr int LPK = HD / 8;      // lanes per V row in the P.V pass (8 dims = 16 B each)
   constexpr int PPI = 64 / LPK;    // keys per P.V iteration per wave
   constexpr int STEPS = HD / 32;   // MFMA k-steps over head_dim
   const int kvh = blockIdx.x, s = blockIdx.y;
@@ -64,12 +65,17 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
     }
   }
 
-  float m_i[QM], l_i[QM], o0[QM], o1[QM];
+  float m_i[QM], l_i[QM], o[QM][8];
 #pragma unroll
-  for (int i = 0; i < QM; ++i) { m_i[i] = -INFINITY; l_i[i] = 0.f; o0[i] = 0.f; o1[i] = 0.f; }
+  for (int i = 0; i < QM; ++i) {
+    m_i[i] = -INFINITY;
+    l_i[i] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[i][e] = 0.f;
+  }
 
   const int sub = lane / LPK;          // which key of the PPI group this lane handles
-  const int dl = (lane % LPK) * 2;     // first of the two dims this lane owns
+  const int dl = (lane % LPK) * 8;     // first of the eight dims this lane owns
 
   for (int t0 = wave * 64; t0 < len; t0 += 256) {
     // ---- scores for 64 keys: 4 MFMA blocks of 16 keys
@@ -103,24 +109,26 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
       const float p = (v == -INFINITY) ? 0.f : __expf(v - mnew);
       l_i[i] = l_i[i] * alpha + wave_sum(p);
       m_i[i] = mnew;
-      o0[i] *= alpha;
-      o1[i] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[i][e] *= alpha;
       pbuf[wave][i][lane] = p;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- P.V: lanes over head_dim, PPI keys per iteration
+    // ---- P.V: LPK lanes per V row (16-byte loads), PPI rows per iteration
     const int tend = min(64, len - t0);
+#pragma unroll 4
     for (int tt = sub; tt < tend; tt += PPI) {
-      const uint32_t vv = *reinterpret_cast<const uint32_t*>(vc + kv_base + (size_t)(t0 + tt) * HD + dl);
-      const float v0 = bf16lo(vv), v1 = bf16hi(vv);
+      const u32x4 vv = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)(t0 + tt) * HD + dl);
+      const float v[8] = {bf16lo(vv.x), bf16hi(vv.x), bf16lo(vv.y), bf16hi(vv.y),
+                          bf16lo(vv.z), bf16hi(vv.z), bf16lo(vv.w), bf16hi(vv.w)};
 #pragma unroll
       for (int i = 0; i < QM; ++i) {
         if (i >= qpk) break;
         const float p = pbuf[wave][i][tt];
-        o0[i] = fmaf(p, v0, o0[i]);
-        o1[i] = fmaf(p, v1, o1[i]);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[i][e] = fmaf(p, v[e], o[i][e]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -128,19 +136,20 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
   // combine the PPI key-subsets inside the wave
   if constexpr (PPI > 1) {
 #pragma unroll
-    for (int i = 0; i < QM; ++i) {
+    for (int i = 0; i < QM; ++i)
 #pragma unroll
-      for (int o = LPK; o < 64; o <<= 1) {
-        o0[i] += __shfl_xor(o0[i], o, kWave);
-        o1[i] += __shfl_xor(o1[i], o, kWave);
-      }
-    }
+      for (int off = LPK; off < 64; off <<= 1)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[i][e] += __shfl_xor(o[i][e], off, kWave);
   }
 #pragma unroll
   for (int i = 0; i < QM; ++i) {
     if (i >= qpk) break;
     if (lane == 0) { mrg_m[wave][i] = m_i[i]; mrg_l[wave][i] = l_i[i]; }
-    if (lane < LPK) { mrg_o[wave][i][dl] = o0[i]; mrg_o[wave][i][dl + 1] = o1[i]; }
+    if (lane < LPK) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) mrg_o[wave][i][dl + e] = o[i][e];
+    }
   }
   __syncthreads();
   // merge the four waves: thread t handles (head, dim) pairs

@@ -101,25 +101,31 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float2* 
 // Gumbel-max sampling / greedy argmax over one logits row per workgroup, plus
 // the chosen token's log-prob. Ties resolve to the lowest index (Burn argmax /
 // the host sampler's reverse index order, generate.rs:144-152).
-__global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ logits,
+constexpr int kSampleThreads = 1024;
+
+__global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __restrict__ logits,
                                                      int64_t ld, int vocab, float inv_temp,
                                                      uint64_t seed, int64_t step,
                                                      int32_t* __restrict__ tok, int64_t tok_stride,
                                                      float* __restrict__ lp, int64_t lp_stride,
                                                      int32_t* __restrict__ next_ids) {
-  __shared__ float s_best[4];
-  __shared__ int s_idx[4];
-  __shared__ float s_m[4], s_s[4];
+  constexpr int NW = kSampleThreads / kWave;
+  __shared__ float s_best[NW];
+  __shared__ int s_idx[NW];
+  __shared__ float s_m[NW], s_s[NW];
   const int64_t r = blockIdx.x;
   const float* row = logits + r * ld;
   float m = -INFINITY, s = 0.f, best = -INFINITY;
   int bidx = 0x7fffffff;
-  for (int v = threadIdx.x; v < vocab; v += 256) {
+  // rng_key(seed, r, c) = mix64(row_key ^ c * K2): the per-row half is hoisted.
+  const uint64_t row_key = mix64(seed + 0x9e3779b97f4a7c15ull * ((uint64_t)r + 1));
+  const uint64_t cbase = (uint64_t)step * (uint64_t)vocab;
+  for (int v = threadIdx.x; v < vocab; v += kSampleThreads) {
     const float x = row[v];
     if (x > m) { s = s * __expf(m - x) + 1.f; m = x; } else { s += __expf(x - m); }
     float key = x;
     if (inv_temp > 0.f) {
-      const float u = u01(rng_key(seed, (uint64_t)r, (uint64_t)step * (uint64_t)vocab + v));
+      const float u = u01(mix64(row_key ^ ((cbase + (uint64_t)v) * 0xd1b54a32d192ed03ull)));
       key = x * inv_temp - logf(-logf(u));
     }
     if (key > best) { best = key; bidx = v; }  // v increases per thread: first max kept
@@ -137,7 +143,7 @@ __global__ __launch_bounds__(256) void sample_kernel(const float* __restrict__ l
   if (threadIdx.x % kWave == 0) { s_best[w] = best; s_idx[w] = bidx; s_m[w] = m; s_s[w] = s; }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int k = 1; k < 4; ++k) {
+    for (int k = 1; k < NW; ++k) {
       if (s_best[k] > best || (s_best[k] == best && s_idx[k] < bidx)) { best = s_best[k]; bidx = s_idx[k]; }
       lse_merge(m, s, s_m[k], s_s[k]);
     }
@@ -223,7 +229,7 @@ extern "C" int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t 
   SM_REQUIRE(!std::isnan(temperature), "temperature must not be NaN");
   if (rows == 0) return SM_OK;
   const float inv_temp = temperature > 0.f ? 1.f / temperature : 0.f;
-  sample_kernel<<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+  sample_kernel<<<(unsigned)rows, kSampleThreads, 0, as_stream(stream)>>>(
       logits, ld, (int)vocab, inv_temp, seed, step, tokens, tok_stride, logprobs, lp_stride,
       next_ids);
   SM_LAUNCH_CHECK();

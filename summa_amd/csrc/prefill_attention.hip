@@ -12,10 +12,11 @@
 // v_mfma_f32_16x16x32_bf16 (Q fragments stay in registers for the whole
 // sweep), applies the causal mask and the online softmax on the MFMA output
 // registers (row stats reduced across the 16 lanes that share a row), writes P
-// as f16 to its LDS slice and accumulates O += P.V with a second (f16) MFMA
-// whose B operand reads the transposed V tile, converted bf16 -> f16 while
-// staging. P in f16 (11-bit significand) keeps the probability rounding 8x
-// below bf16's, which is what holds recomputed log-probs to the bf16 bar. O stays in registers; the final 1/l
+// to its LDS slice as a pair of f16 values (hi + lo, ~21 significant bits)
+// and accumulates O += P.V with two f16 MFMAs whose B operand reads the
+// transposed V tile (bf16 -> f16 while staging, exact). The split keeps P.V at
+// fp32-like precision, so the prefill path matches the decode path's fp32
+// probabilities; a single bf16 or f16 P costs measurable log-prob accuracy. O stays in registers; the final 1/l
 // scaling and bf16 store happen once.
 #include <cmath>
 
@@ -39,7 +40,7 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
   constexpr int PP = 64 + 8;   // padded P row
   __shared__ __attribute__((aligned(16))) uint16_t ks[64 * KP];
   __shared__ __attribute__((aligned(16))) _Float16 vts[HD * VP];
-  __shared__ __attribute__((aligned(16))) _Float16 ps[4][16 * PP];
+  __shared__ __attribute__((aligned(16))) _Float16 ps[4][2][16 * PP];  // P = hi + lo
 
   const int qt = blockIdx.x, h = blockIdx.y, s = blockIdx.z;
   const int kvh = h / (H / KVH);
@@ -137,22 +138,29 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
     for (int d = 0; d < HD / 16; ++d)
 #pragma unroll
       for (int r = 0; r < 4; ++r) o[d][r] *= alpha[r];
-    // ---- P (f16) to this wave's LDS slice: P[row 4g+r][key kb*16+j]
+    // ---- P as an f16 pair (hi + lo carries ~21 significant bits) to this
+    //      wave's LDS slice: P[row 4g+r][key kb*16+j]
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ps[wave][(4 * g + r) * PP + kb * 16 + j] = (_Float16)sc[kb][r];
+      for (int r = 0; r < 4; ++r) {
+        const _Float16 hi = (_Float16)sc[kb][r];
+        ps[wave][0][(4 * g + r) * PP + kb * 16 + j] = hi;
+        ps[wave][1][(4 * g + r) * PP + kb * 16 + j] = (_Float16)(sc[kb][r] - (float)hi);
+      }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     // ---- O += P V: A = P rows (lane row j), B = V^T rows (lane dim j)
 #pragma unroll
     for (int st = 0; st < 2; ++st) {
-      const h8 pa = *reinterpret_cast<const h8*>(&ps[wave][j * PP + st * 32 + g * 8]);
+      const h8 pa = *reinterpret_cast<const h8*>(&ps[wave][0][j * PP + st * 32 + g * 8]);
+      const h8 pl = *reinterpret_cast<const h8*>(&ps[wave][1][j * PP + st * 32 + g * 8]);
 #pragma unroll
       for (int d = 0; d < HD / 16; ++d) {
         const h8 vb = *reinterpret_cast<const h8*>(&vts[(d * 16 + j) * VP + st * 32 + g * 8]);
         o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, vb, o[d], 0, 0, 0);
+        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vb, o[d], 0, 0, 0);
       }
     }
   }

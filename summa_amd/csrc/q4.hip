@@ -123,41 +123,54 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
 #pragma unroll
     for (int b = 0; b < NB; ++b) acc[mt][b] = f4{0.f, 0.f, 0.f, 0.f};
 
+  // U k-groups of weights are loaded before any of them is consumed, so each
+  // lane keeps U*NB 16-byte loads in flight (the M=1 GEMV is pure latency x
+  // bandwidth: these loads are all the work there is).
+  constexpr int U = (MT <= 2) ? 4 : 2;
   const int kg0 = (KSPLIT == 1) ? 0 : wave;
-  for (int kg = kg0; kg < ngroups; kg += KSPLIT) {
-    u32x4 wv[NB];
-    h2 sc[NB];
+  for (int kb0 = kg0; kb0 < ngroups; kb0 += KSPLIT * U) {
+    u32x4 wv[U][NB];
+    h2 sc[U][NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      if (brow[b] >= 0) {
-        const uint8_t* p = a.codes + (size_t)brow[b] * (a.K / 2) + kg * 64 + g * 16;
-        wv[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-        const _Float16 s = (_Float16)bf16_to_f32(a.scales[(size_t)brow[b] * ngroups + kg]);
-        sc[b] = h2{s, s};
-      } else {
-        wv[b] = u32x4{0u, 0u, 0u, 0u};
-        sc[b] = h2{(_Float16)0.f, (_Float16)0.f};
+    for (int u = 0; u < U; ++u) {
+      const int kg = kb0 + u * KSPLIT;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        if (brow[b] >= 0 && kg < ngroups) {
+          const uint8_t* p = a.codes + (size_t)brow[b] * (a.K / 2) + kg * 64 + g * 16;
+          wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+          const _Float16 s = (_Float16)bf16_to_f32(a.scales[(size_t)brow[b] * ngroups + kg]);
+          sc[u][b] = h2{s, s};
+        } else {
+          wv[u][b] = u32x4{0u, 0u, 0u, 0u};
+          sc[u][b] = h2{(_Float16)0.f, (_Float16)0.f};
+        }
       }
     }
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      h8 bf[NB];
+    for (int u = 0; u < U; ++u) {
+      const int kg = kb0 + u * KSPLIT;
+      if (kg >= ngroups) break;
 #pragma unroll
-      for (int b = 0; b < NB; ++b) bf[b] = dequant_word(wv[b][s], sc[b]);
+      for (int s = 0; s < 4; ++s) {
+        h8 bf[NB];
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int row = m0 + mt * 16 + j;
-        h8 af = h8{0, 0, 0, 0, 0, 0, 0, 0};
-        if (row < a.M) {
-          const size_t xo = (size_t)row * a.ldx + kg * 128 + g * 32 + s * 8;
-          if constexpr (XF16)
-            af = act_frag_f16(*reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo));
-          else
-            af = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
+        for (int b = 0; b < NB; ++b) bf[b] = dequant_word(wv[u][b][s], sc[u][b]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          const int row = m0 + mt * 16 + j;
+          h8 af = h8{0, 0, 0, 0, 0, 0, 0, 0};
+          if (row < a.M) {
+            const size_t xo = (size_t)row * a.ldx + kg * 128 + g * 32 + s * 8;
+            if constexpr (XF16)
+              af = act_frag_f16(*reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo));
+            else
+              af = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
+          }
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+            acc[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[mt][b], 0, 0, 0);
         }
-#pragma unroll
-        for (int b = 0; b < NB; ++b)
-          acc[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[mt][b], 0, 0, 0);
       }
     }
   }
@@ -243,23 +256,21 @@ int launch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
               : launch_q4_x<MT, NB, KSPLIT, false>(a, epi, st);
 }
 
-// Picks the tile shape: M-blocks per wave from M, and K-split across the four
-// waves when there are too few column tiles to fill the 256 CUs.
+// Picks the tile shape. Up to 256 rows (decode batches, GEMV) every wave owns
+// 16 rows so the grid has M/16 row tiles; bigger M (prefill / recompute) uses
+// 128-row tiles. When the grid would have fewer than 512 workgroups the four
+// waves of a workgroup split K instead of N (more workgroups, same work).
 int dispatch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
-  const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
-  const int mtiles16 = (int)ceil_div(a.M, 16);
-  // Waves along N with 2 blocks each gives 128-column tiles.
-  const bool few = ceil_div(logical_cols, 128) * ceil_div(a.M, 128) < 512;
-#define SM_Q4_CASE(MT)                                                      \
-  do {                                                                      \
-    if (few && a.K >= 4 * 128) return launch_q4<MT, 2, 4>(a, epi, xf16, st); \
-    return launch_q4<MT, 2, 1>(a, epi, xf16, st);                           \
-  } while (0)
-  if (mtiles16 <= 1) SM_Q4_CASE(1);
-  if (mtiles16 <= 2) SM_Q4_CASE(2);
-  if (mtiles16 <= 4) SM_Q4_CASE(4);
-  SM_Q4_CASE(8);
-#undef SM_Q4_CASE
+  const int64_t logical_cols = is_swiglu(epi) ? 2 * (int64_t)a.ncols : a.N;
+  const bool ksplit_ok = a.K >= 4 * 128;
+  if (a.M <= 256) {
+    const int64_t wgs = ceil_div(logical_cols, 128) * ceil_div(a.M, 16);
+    if (wgs < 512 && ksplit_ok) return launch_q4<1, 2, 4>(a, epi, xf16, st);
+    return launch_q4<1, 2, 1>(a, epi, xf16, st);
+  }
+  const int64_t wgs = ceil_div(logical_cols, 128) * ceil_div(a.M, 128);
+  if (wgs < 512 && ksplit_ok) return launch_q4<8, 2, 4>(a, epi, xf16, st);
+  return launch_q4<8, 2, 1>(a, epi, xf16, st);
 }
 
 // ----------------------------------------------------------- quantizer ---
