@@ -111,8 +111,17 @@ const char* sm_grpo_flags_message(int32_t flags);
 int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* codes, uint16_t* scales,
                    int32_t* bad_scales, void* stream);
 
-/* y = x . W^T over Q4G128 weights, x [M, ldx] bf16 or f16 (x_dtype), f32
- * accumulate. Replaces
+/* Prepared (tiled) device copy of a Q4G128 weight, the counterpart of
+ * prepare_linear_for_inference (summa-llm/src/model/matmul.rs:20-35): 16 rows
+ * x one 128-element group form one contiguous 1 KB tile (row r at byte 64*r),
+ * tiles ordered [row_block][group]; scales 16 per tile in the same order.
+ * Sizes: tiled_codes ceil(N/16)*16 * K/2 bytes, tiled_scales ceil(N/16)*16 *
+ * K/128 bf16; rows beyond N are zero. K % 128 == 0. */
+int sm_q4_pack(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+               uint8_t* tiled_codes, uint16_t* tiled_scales, void* stream);
+
+/* y = x . W^T over Q4G128 weights in the prepared layout (sm_q4_pack), x [M,
+ * ldx] bf16 or f16 (x_dtype), f32 accumulate. Replaces
  * the quantized-matmul dispatch: PackedTensor::matrix_vector
  * (quantization.rs:630-654) batched over M rows, i.e. Linear::forward
  * (summa-llm/src/model/matmul.rs:57-66) on a QuantizedModelBackend weight

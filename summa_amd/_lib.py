@@ -28,6 +28,7 @@ SIGNATURES: dict[str, tuple] = {
     "sm_grpo_loss": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, f64, f64, f64, vp, vp, vp, vp, vp]),
     "sm_grpo_flags_message": (C.c_char_p, [C.c_int32]),
     "sm_q4_quantize": (i32, [vp, i32, i64, vp, vp, vp, vp]),
+    "sm_q4_pack": (i32, [vp, vp, i64, i64, vp, vp, vp]),
     "sm_q4_matmul": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
     "sm_gemm_f32": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
     "sm_swiglu_f32": (i32, [vp, i64, i64, vp, vp]),

@@ -134,6 +134,61 @@ __host__ __device__ inline float u01(uint64_t bits) {
   return (static_cast<float>(bits >> 40) + 0.5f) * (1.0f / 16777216.0f);
 }
 
-inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+__host__ __device__ inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// ------------------------------------------------- prepared Q4G128 layout ---
+// Device weights use a tiled copy of the row-major Q4G128 codec: 16 weight
+// rows x one 128-element group form a 1 KB tile (row r of the tile at byte
+// 64*r), tiles ordered [row_block][group]. One wave instruction in which lane
+// (r = lane%16, c = lane/16) loads 16 bytes at 64*r + 16*c reads the whole tile
+// contiguously. Scales follow the same order: 16 bf16 per tile.
+__host__ __device__ inline size_t q4t_code_offset(int64_t row, int64_t group, int64_t ngroups) {
+  return ((size_t)(row >> 4) * ngroups + group) * 1024 + (size_t)(row & 15) * 64;
+}
+__host__ __device__ inline size_t q4t_scale_index(int64_t row, int64_t group, int64_t ngroups) {
+  return ((size_t)(row >> 4) * ngroups + group) * 16 + (size_t)(row & 15);
+}
+__host__ __device__ inline int64_t q4t_rows(int64_t n) { return ceil_div(n, 16) * 16; }
+
+// Inside the prepared layout each 32-bit word (8 consecutive k of one row)
+// stores offset-binary nibbles u = q + 8, the even k in nibbles 0-3 and the
+// odd k in nibbles 4-7, so that the magic-exponent unpack below yields the
+// eight values in natural k order with no extra shuffles.
+__host__ __device__ inline uint32_t q4_prepare_word(uint32_t w) {
+  uint32_t out = 0;
+  for (int k = 0; k < 8; ++k) {
+    const uint32_t u = ((w >> (4 * k)) & 0xfu) ^ 0x8u;
+    const int dst = (k & 1) ? 4 + (k >> 1) : (k >> 1);
+    out |= u << (4 * dst);
+  }
+  return out;
+}
+
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+
+__device__ inline h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
+
+// One prepared word -> its 8 codes q in natural k order as f16. Each 16-bit
+// half becomes 1024 + u (or 1024 + 16u) by OR-ing the nibble into the
+// mantissa of 0x6400; one packed add / fma removes the bias. 9 VALU ops.
+__device__ inline h8 q4_unpack(uint32_t w) {
+  const uint32_t w2 = w >> 8;
+  const h2 k1032 = {(_Float16)-1032.f, (_Float16)-1032.f};
+  const h2 k72 = {(_Float16)-72.f, (_Float16)-72.f};
+  const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
+  const h2 a = as_h2((w & 0x000F000Fu) | 0x64006400u) + k1032;       // k0, k1
+  const h2 b = as_h2((w & 0x00F000F0u) | 0x64006400u) * k16 + k72;   // k2, k3
+  const h2 c = as_h2((w2 & 0x000F000Fu) | 0x64006400u) + k1032;      // k4, k5
+  const h2 d = as_h2((w2 & 0x00F000F0u) | 0x64006400u) * k16 + k72;  // k6, k7
+  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+}
+
+// Same, times the group scale: q * scale is exact in f16 while the scale is an
+// f16 normal (<= 11 significant bits), which the quantizer checks.
+__device__ inline h8 q4_unpack_scaled(uint32_t w, _Float16 s) {
+  h8 v = q4_unpack(w);
+  return v * s;
+}
 
 }  // namespace sm

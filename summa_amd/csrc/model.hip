@@ -28,6 +28,7 @@ extern "C" {
 int sm_q4_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
                  int64_t, void*, int64_t, int, void*);
 int sm_q4_quantize(const void*, int, int64_t, uint8_t*, uint16_t*, int32_t*, void*);
+int sm_q4_pack(const uint8_t*, const uint16_t*, int64_t, int64_t, uint8_t*, uint16_t*, void*);
 int sm_gemm_f32(const float*, int64_t, int64_t, const float*, int64_t, int64_t, float*, int64_t,
                 int, void*);
 int sm_swiglu_f32(const float*, int64_t, int64_t, float*, void*);
@@ -169,9 +170,10 @@ int alloc_linear(sm_model* m, Linear& L, int64_t N, int64_t K) {
   L.N = N;
   L.K = K;
   if (m->cfg.quantized) {
-    const int64_t groups = ceil_div(N * K, 128);
-    SM_TRY(dalloc(m, (void**)&L.codes, (size_t)groups * 64, true));
-    SM_TRY(dalloc(m, (void**)&L.scales, (size_t)groups * 2, true));
+    // prepared tiled layout (sm_q4_pack): rows padded to a multiple of 16
+    const int64_t rows = q4t_rows(N);
+    SM_TRY(dalloc(m, (void**)&L.codes, (size_t)rows * K / 2, true));
+    SM_TRY(dalloc(m, (void**)&L.scales, (size_t)rows * (K / 128) * 2, true));
   } else {
     SM_TRY(dalloc(m, (void**)&L.w, (size_t)(N * K) * 4, true));
   }
@@ -365,14 +367,22 @@ extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float
   hipStream_t st = as_stream(stream);
   if (lin) {
     if (m->cfg.quantized) {
-      DevBuf bad;
-      SM_TRY(ensure(bad, 4));
-      zero_i32_kernel<<<1, 1, 0, st>>>((int32_t*)bad.p, 1);
-      SM_TRY(sm_q4_quantize(src, SM_F32, n, lin->codes, lin->scales, (int32_t*)bad.p, stream));
+      // quantize to the row-major codec in a temporary, then prepare (tile)
+      const int64_t groups = ceil_div(n, 128);
+      DevBuf tmp;
+      SM_TRY(ensure(tmp, (size_t)groups * 64 + (size_t)groups * 2 + 16));
+      uint8_t* codes = (uint8_t*)tmp.p;
+      uint16_t* scales = (uint16_t*)(codes + groups * 64);
+      int32_t* bad = (int32_t*)(codes + groups * 64 + groups * 2 + (groups * 2) % 4);
+      SM_HIP(hipMemsetAsync(bad, 0, 4, st));
+      int s = sm_q4_quantize(src, SM_F32, n, codes, scales, bad, stream);
+      if (s == SM_OK) s = sm_q4_pack(codes, scales, lin->N, lin->K, lin->codes, lin->scales, stream);
       int32_t nbad = 0;
-      SM_HIP(hipMemcpyAsync(&nbad, bad.p, 4, hipMemcpyDeviceToHost, st));
-      SM_HIP(hipStreamSynchronize(st));
-      SM_HIP(hipFree(bad.p));
+      if (s == SM_OK && hipMemcpyAsync(&nbad, bad, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
+        s = SM_ERR_HIP;
+      hipStreamSynchronize(st);
+      hipFree(tmp.p);
+      if (s != SM_OK) return s;
       SM_REQUIRE(nbad == 0, "%d Q4 groups have a scale outside the f16 normal range", nbad);
       return SM_OK;
     }

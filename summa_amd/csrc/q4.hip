@@ -15,17 +15,20 @@
 // matmul the reference's PackedTensor::matrix_vector states for one row of x
 // (quantization.rs:630-654) and Linear::forward computes for a batch.
 //
-// MI355X design: v_mfma_f32_16x16x32_f16. The B operand (weights) goes from
-// HBM straight into registers: lane (j = l%16, g = l/16) loads one 16-byte
-// chunk = 32 consecutive k of weight row n0+j per 128-k group, and each of its
-// four 32-bit words becomes the lane's 8 f16 B values of one MFMA step via the
-// 0x6400 magic-exponent trick (x ^ 0x8 -> offset binary, OR into the f16
-// mantissa, one packed subtract / fma) and one packed multiply by the group
-// scale. q * scale is exact in f16 (<= 11 significant bits) as long as the
-// scale is an f16 normal, which sm_q4_quantize checks. The A operand
-// (activations, f16 or bf16 in HBM) is read by the lanes whose row is < M
-// only, converted to f16 if needed and permuted to the same k order as the
-// dequantised words. For
+// MI355X design: v_mfma_f32_16x16x32_f16. The kernels read the prepared tiled
+// copy of the codec (sm_q4_pack; common.hpp q4t_*), in which one 16-row x
+// 128-group MFMA block is a contiguous 1 KB: lane (j = l%16, g = l/16) loads
+// the 16-byte chunk = 32 consecutive k of weight row n0+j, so each wave load
+// instruction streams 1 KB contiguously (the row-major codec would make it 16
+// 64-byte pieces 1 KB apart). The prepared words hold offset-binary nibbles in
+// an order that unpacks to natural k order, so each of the chunk's four 32-bit
+// words becomes the lane's 8 f16 B values of one MFMA step in 9 VALU ops (0x6400
+// magic exponent, common.hpp q4_unpack), and f16 activations feed the A operand
+// with no conversion at all. The small-M kernel accumulates each group's four
+// k-steps unscaled and applies the group scale with one FMA per output; the
+// large-M kernel folds the scale into B (exact in f16 for an f16-normal scale,
+// which sm_q4_quantize checks). The A operand is read by the lanes whose row
+// is < M only. For
 // tiny N the four waves of a workgroup split the K groups and merge their
 // accumulators through LDS in a fixed order (deterministic).
 #include <cmath>
@@ -35,8 +38,6 @@
 namespace sm {
 namespace {
 
-typedef _Float16 h2 __attribute__((ext_vector_type(2)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
 enum Epi : int {
@@ -49,33 +50,11 @@ enum Epi : int {
 
 constexpr bool is_swiglu(int e) { return e == EPI_SWIGLU_BF16 || e == EPI_SWIGLU_F16; }
 
-__device__ inline h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
-
-// 8 signed nibbles of `w` times scale `s` -> f16 in k order [0,4,1,5,2,6,3,7].
-__device__ inline h8 dequant_word(uint32_t w, h2 s) {
-  w ^= 0x88888888u;  // two's complement -> offset binary (u = q + 8)
-  const uint32_t w2 = w >> 8;
-  const h2 k1032 = {(_Float16)-1032.f, (_Float16)-1032.f};
-  const h2 k72 = {(_Float16)-72.f, (_Float16)-72.f};
-  const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-  h2 a = as_h2((w & 0x000F000Fu) | 0x64006400u) + k1032;        // q0, q4
-  h2 b = as_h2((w & 0x00F000F0u) | 0x64006400u) * k16 + k72;    // q1, q5
-  h2 c = as_h2((w2 & 0x000F000Fu) | 0x64006400u) + k1032;       // q2, q6
-  h2 d = as_h2((w2 & 0x00F000F0u) | 0x64006400u) * k16 + k72;   // q3, q7
-  a *= s; b *= s; c *= s; d *= s;
-  return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-}
-
-// 8 bf16 activations (one 16-byte load, k..k+7) -> f16 in k order [0,4,1,5,2,6,3,7].
+// 8 bf16 activations (one 16-byte load, k..k+7) -> f16, natural order.
 __device__ inline h8 act_frag(u32x4 v) {
-  return h8{(_Float16)bf16lo(v.x), (_Float16)bf16lo(v.z), (_Float16)bf16hi(v.x),
-            (_Float16)bf16hi(v.z), (_Float16)bf16lo(v.y), (_Float16)bf16lo(v.w),
-            (_Float16)bf16hi(v.y), (_Float16)bf16hi(v.w)};
-}
-
-// 8 f16 activations (k..k+7) -> k order [0,4,1,5,2,6,3,7].
-__device__ inline h8 act_frag_f16(h8 v) {
-  return h8{v[0], v[4], v[1], v[5], v[2], v[6], v[3], v[7]};
+  return h8{(_Float16)bf16lo(v.x), (_Float16)bf16hi(v.x), (_Float16)bf16lo(v.y),
+            (_Float16)bf16hi(v.y), (_Float16)bf16lo(v.z), (_Float16)bf16hi(v.z),
+            (_Float16)bf16lo(v.w), (_Float16)bf16hi(v.w)};
 }
 
 __device__ inline float silu(float g) { return g / (1.f + __expf(-g)); }
@@ -90,24 +69,29 @@ struct Q4Args {
   int ncols;               // logical output columns (N, or F for SWIGLU)
 };
 
-// MT: 16-row M blocks per wave; NB: 16-column N blocks per wave;
-// KSPLIT: 1 = the 4 waves tile N (WG tile 16MT x 64NB), 4 = the 4 waves split
-// the K groups of one 16MT x 16NB tile.
-template <int MT, int NB, int KSPLIT, int EPI, bool XF16>
+// One workgroup = 16 rows (M tile) x its column tile. NB: 16-column blocks per
+// wave; KSPLIT: 1 = the 4 waves tile N (workgroup tile 16 x 64NB), 4 = the 4
+// waves split the K groups of one 16 x 16NB tile and merge in LDS.
+// Per wave, kU K groups of weights are requested before any is consumed (the
+// M=1 GEMV is nothing but these loads: the more in flight, the closer to HBM
+// rate), and the activation fragments of the next group are fetched while the
+// current one is multiplied.
+constexpr int kU = 8;
+
+template <int NB, int KSPLIT, int EPI, bool XF16>
 __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
-  const int m0 = blockIdx.y * (16 * MT);
+  const int m0 = blockIdx.y * 16;
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
   const int c0 = blockIdx.x * tile_cols + ((KSPLIT == 1) ? wave * wave_cols : 0);
   const int ngroups = a.K / 128;
-  const int half_cols = is_swiglu(EPI) ? wave_cols / 2 : wave_cols;
   // Weight row read by this lane for block b.
   int brow[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
-    if (is_swiglu(EPI)) {
+    if constexpr (is_swiglu(EPI)) {
       // first NB/2 blocks: gate columns, last NB/2: value columns (same j)
       const int col = c0 / 2 + (b % (NB / 2)) * 16 + j;  // logical h column
       brow[b] = (col < a.ncols) ? ((b < NB / 2) ? col : a.ncols + col) : -1;
@@ -116,161 +100,185 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
       brow[b] = (col < a.N) ? col : -1;
     }
   }
-  (void)half_cols;
-  f4 acc[MT][NB];
+  // All loads below are branch-free (clamped addresses, zeroed afterwards):
+  // loads inside divergent branches make the compiler wait on each one, which
+  // serialises the round trips this kernel exists to overlap.
+  const int arow = min(m0 + j, a.M - 1);  // activation row this lane feeds to the A operand
+  const bool arow_ok = m0 + j < a.M;
+  auto load_act = [&](int kg, h8 (&af)[4]) {
+    const int kc = min(kg, ngroups - 1);
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
+    for (int s = 0; s < 4; ++s) {
+      const size_t xo = (size_t)arow * a.ldx + kc * 128 + g * 32 + s * 8;
+      if constexpr (XF16)
+        af[s] = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo);
+      else
+        af[s] = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
+    }
+  };
+  int brow_c[NB];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) acc[mt][b] = f4{0.f, 0.f, 0.f, 0.f};
+  for (int b = 0; b < NB; ++b) brow_c[b] = brow[b] >= 0 ? brow[b] : 0;
 
-  // U k-groups of weights are loaded before any of them is consumed, so each
-  // lane keeps U*NB 16-byte loads in flight (the M=1 GEMV is pure latency x
-  // bandwidth: these loads are all the work there is).
-  constexpr int U = (MT <= 2) ? 4 : 2;
-  const int kg0 = (KSPLIT == 1) ? 0 : wave;
-  for (int kb0 = kg0; kb0 < ngroups; kb0 += KSPLIT * U) {
-    u32x4 wv[U][NB];
-    h2 sc[U][NB];
+  f4 acc[NB];
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int kg = kb0 + u * KSPLIT;
+  for (int b = 0; b < NB; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int kg0 = (KSPLIT == 1) ? 0 : wave;
+  h8 an[4];
+  load_act(kg0, an);
+  for (int kb0 = kg0; kb0 < ngroups; kb0 += KSPLIT * kU) {
+    u32x4 wv[kU][NB];
+    uint16_t sraw[kU][NB];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kc = min(kb0 + u * KSPLIT, ngroups - 1);
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        if (brow[b] >= 0 && kg < ngroups) {
-          const uint8_t* p = a.codes + (size_t)brow[b] * (a.K / 2) + kg * 64 + g * 16;
-          wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-          const _Float16 s = (_Float16)bf16_to_f32(a.scales[(size_t)brow[b] * ngroups + kg]);
-          sc[u][b] = h2{s, s};
-        } else {
-          wv[u][b] = u32x4{0u, 0u, 0u, 0u};
-          sc[u][b] = h2{(_Float16)0.f, (_Float16)0.f};
-        }
+        wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+            a.codes + q4t_code_offset(brow_c[b], kc, ngroups) + g * 16));
+        sraw[u][b] = a.scales[q4t_scale_index(brow_c[b], kc, ngroups)];
       }
     }
+    // keep the whole batch of loads ahead of the math (the scheduler would
+    // otherwise sink each load next to its first use)
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
+    for (int u = 0; u < kU; ++u) {
       const int kg = kb0 + u * KSPLIT;
       if (kg >= ngroups) break;
+      h8 af[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        h8 bf[NB];
+      for (int s = 0; s < 4; ++s) af[s] = arow_ok ? an[s] : h8{0, 0, 0, 0, 0, 0, 0, 0};
+      load_act(kg + KSPLIT, an);  // next group's activations, in flight during this one
+      // Per block: the group's 4 k-steps accumulate unscaled codes, then one
+      // FMA per output applies the group scale (cheaper than scaling B).
 #pragma unroll
-        for (int b = 0; b < NB; ++b) bf[b] = dequant_word(wv[u][b][s], sc[u][b]);
+      for (int b = 0; b < NB; ++b) {
+        f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0], q4_unpack(wv[u][b][0]),
+                                                      f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
 #pragma unroll
-        for (int mt = 0; mt < MT; ++mt) {
-          const int row = m0 + mt * 16 + j;
-          h8 af = h8{0, 0, 0, 0, 0, 0, 0, 0};
-          if (row < a.M) {
-            const size_t xo = (size_t)row * a.ldx + kg * 128 + g * 32 + s * 8;
-            if constexpr (XF16)
-              af = act_frag_f16(*reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo));
-            else
-              af = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
-          }
+        for (int s = 1; s < 4; ++s)
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], q4_unpack(wv[u][b][s]), t, 0, 0, 0);
+        const float sc = brow[b] >= 0 ? bf16_to_f32(sraw[u][b]) : 0.f;
 #pragma unroll
-          for (int b = 0; b < NB; ++b)
-            acc[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[mt][b], 0, 0, 0);
-        }
+        for (int r = 0; r < 4; ++r) acc[b][r] = fmaf(t[r], sc, acc[b][r]);
       }
     }
   }
 
   if constexpr (KSPLIT > 1) {
-    __shared__ f4 red[KSPLIT - 1][MT * NB][kWave];
+    __shared__ f4 red[KSPLIT - 1][NB][kWave];
     if (wave > 0) {
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) red[wave - 1][mt * NB + b][lane] = acc[mt][b];
+      for (int b = 0; b < NB; ++b) red[wave - 1][b][lane] = acc[b];
     }
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
     for (int w = 0; w < KSPLIT - 1; ++w)
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[mt][b] += red[w][mt * NB + b][lane];
+      for (int b = 0; b < NB; ++b) acc[b] += red[w][b][lane];
   }
 
   // Epilogue: lane holds rows 4*g + r (r = 0..3) of column j of every block.
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt) {
+  for (int r = 0; r < 4; ++r) {
+    const int row = m0 + 4 * g + r;
+    if (row >= a.M) continue;
+    if constexpr (is_swiglu(EPI)) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = m0 + mt * 16 + 4 * g + r;
-      if (row >= a.M) continue;
-      if constexpr (is_swiglu(EPI)) {
-#pragma unroll
-        for (int b = 0; b < NB / 2; ++b) {
-          const int col = c0 / 2 + b * 16 + j;
-          if (col < a.ncols) {
-            const float h = silu(acc[mt][b][r]) * acc[mt][b + NB / 2][r];
-            if constexpr (EPI == EPI_SWIGLU_F16)
-              static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = (_Float16)h;
-            else
-              static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(h);
-          }
+      for (int b = 0; b < NB / 2; ++b) {
+        const int col = c0 / 2 + b * 16 + j;
+        if (col < a.ncols) {
+          const float h = silu(acc[b][r]) * acc[b + NB / 2][r];
+          if constexpr (EPI == EPI_SWIGLU_F16)
+            static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = (_Float16)h;
+          else
+            static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(h);
         }
-      } else {
+      }
+    } else {
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const int col = c0 + b * 16 + j;
-          if (col >= a.N) continue;
-          const size_t o = (size_t)row * a.ldy + col;
-          const float v = acc[mt][b][r];
-          if constexpr (EPI == EPI_STORE_F32) static_cast<float*>(a.y)[o] = v;
-          else if constexpr (EPI == EPI_STORE_BF16) static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(v);
-          else static_cast<float*>(a.y)[o] += v;
-        }
+      for (int b = 0; b < NB; ++b) {
+        const int col = c0 + b * 16 + j;
+        if (col >= a.N) continue;
+        const size_t o = (size_t)row * a.ldy + col;
+        const float v = acc[b][r];
+        if constexpr (EPI == EPI_STORE_F32) static_cast<float*>(a.y)[o] = v;
+        else if constexpr (EPI == EPI_STORE_BF16) static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(v);
+        else static_cast<float*>(a.y)[o] += v;
       }
     }
   }
 }
 
-template <int MT, int NB, int KSPLIT, bool XF16>
+template <int NB, int KSPLIT, bool XF16>
 int launch_q4_x(const Q4Args& a, int epi, hipStream_t st) {
-  static_assert(NB % 2 == 0, "SwiGLU pairs gate/value blocks");
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
   const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
-  dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)ceil_div(a.M, 16 * MT));
+  dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)ceil_div(a.M, 16));
   switch (epi) {
 #define SM_Q4_EPI(E) \
-    case E: q4_gemm_kernel<MT, NB, KSPLIT, E, XF16><<<grid, 256, 0, st>>>(a); break;
+    case E: q4_gemm_kernel<NB, KSPLIT, E, XF16><<<grid, 256, 0, st>>>(a); break;
     SM_Q4_EPI(EPI_STORE_F32)
     SM_Q4_EPI(EPI_STORE_BF16)
     SM_Q4_EPI(EPI_ADD_F32)
-    SM_Q4_EPI(EPI_SWIGLU_BF16)
-    SM_Q4_EPI(EPI_SWIGLU_F16)
 #undef SM_Q4_EPI
+    case EPI_SWIGLU_BF16:
+    case EPI_SWIGLU_F16:
+      if constexpr (NB % 2 == 0) {
+        if (epi == EPI_SWIGLU_F16)
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16, XF16><<<grid, 256, 0, st>>>(a);
+        else
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_BF16, XF16><<<grid, 256, 0, st>>>(a);
+        break;
+      } else {
+        set_error("internal: SwiGLU needs an even number of column blocks");
+        return SM_ERR_INVALID;
+      }
     default: set_error("sm_q4_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
   }
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
 
-template <int MT, int NB, int KSPLIT>
+template <int NB, int KSPLIT>
 int launch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
-  return xf16 ? launch_q4_x<MT, NB, KSPLIT, true>(a, epi, st)
-              : launch_q4_x<MT, NB, KSPLIT, false>(a, epi, st);
+  return xf16 ? launch_q4_x<NB, KSPLIT, true>(a, epi, st)
+              : launch_q4_x<NB, KSPLIT, false>(a, epi, st);
 }
 
-// Picks the tile shape. Up to 256 rows (decode batches, GEMV) every wave owns
-// 16 rows so the grid has M/16 row tiles; bigger M (prefill / recompute) uses
-// 128-row tiles. When the grid would have fewer than 512 workgroups the four
-// waves of a workgroup split K instead of N (more workgroups, same work).
+}  // namespace
+
+int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
+                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st);
+
+namespace {
+
+// Picks the kernel. Up to 256 rows (decode batches, GEMV): the register-direct
+// kernel above with 16-row wave tiles (M/16 row tiles); when that grid would
+// have fewer than 512 workgroups the four waves of a workgroup split K instead
+// of N. Bigger M (prefill / recompute): the LDS-tiled 256x128 kernel in
+// q4_gemm_lds.hip.
 int dispatch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
   const int64_t logical_cols = is_swiglu(epi) ? 2 * (int64_t)a.ncols : a.N;
   const bool ksplit_ok = a.K >= 4 * 128;
   if (a.M <= 256) {
-    const int64_t wgs = ceil_div(logical_cols, 128) * ceil_div(a.M, 16);
-    if (wgs < 512 && ksplit_ok) return launch_q4<1, 2, 4>(a, epi, xf16, st);
-    return launch_q4<1, 2, 1>(a, epi, xf16, st);
+    // GEMV-like M: 16-column wave tiles double the workgroup count (SwiGLU
+    // needs gate/value block pairs, so it keeps 32).
+    const bool narrow = a.M <= 16 && !is_swiglu(epi);
+    const int64_t wgs = ceil_div(logical_cols, narrow ? 64 : 128) * ceil_div(a.M, 16);
+    if (narrow) {
+      if (wgs < 512 && ksplit_ok) return launch_q4<1, 4>(a, epi, xf16, st);
+      return launch_q4<1, 1>(a, epi, xf16, st);
+    }
+    if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xf16, st);
+    return launch_q4<2, 1>(a, epi, xf16, st);
   }
-  const int64_t wgs = ceil_div(logical_cols, 128) * ceil_div(a.M, 128);
-  if (wgs < 512 && ksplit_ok) return launch_q4<8, 2, 4>(a, epi, xf16, st);
-  return launch_q4<8, 2, 1>(a, epi, xf16, st);
+  return q4_gemm_lds(a.codes, a.scales, a.N, a.K, a.x, xf16, a.M, a.ldx, a.y, a.ldy, epi,
+                     a.ncols, st);
 }
 
 // ----------------------------------------------------------- quantizer ---
@@ -317,8 +325,46 @@ __global__ __launch_bounds__(256) void q4_quantize_kernel(const T* __restrict__ 
   }
 }
 
+// Row-major codec -> prepared tiled layout; one thread per 16-byte chunk.
+// Rows n..q4t_rows(N) beyond N are zero (padding of the last row block).
+__global__ void q4_pack_kernel(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ scales,
+                               int64_t N, int64_t K, uint8_t* __restrict__ tcodes,
+                               uint16_t* __restrict__ tscales) {
+  const int64_t ngroups = K / 128;
+  const int64_t rows = q4t_rows(N);
+  const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // 16-byte chunk
+  if (chunk >= rows * ngroups * 4) return;
+  const int c = chunk % 4;
+  const int64_t kg = (chunk / 4) % ngroups;
+  const int64_t row = chunk / (4 * ngroups);
+  u32x4 v = u32x4{0u, 0u, 0u, 0u};
+  if (row < N) {
+    v = *reinterpret_cast<const u32x4*>(codes + row * (K / 2) + kg * 64 + c * 16);
+    v = u32x4{q4_prepare_word(v.x), q4_prepare_word(v.y), q4_prepare_word(v.z),
+              q4_prepare_word(v.w)};
+  }
+  *reinterpret_cast<u32x4*>(tcodes + q4t_code_offset(row, kg, ngroups) + c * 16) = v;
+  if (c == 0) tscales[q4t_scale_index(row, kg, ngroups)] = (row < N) ? scales[row * ngroups + kg] : 0;
+}
+
 }  // namespace
 }  // namespace sm
+
+extern "C" int sm_q4_pack(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                          uint8_t* tiled_codes, uint16_t* tiled_scales, void* stream) {
+  using namespace sm;
+  SM_REQUIRE(codes && scales && tiled_codes && tiled_scales, "sm_q4_pack: null buffer");
+  SM_REQUIRE(N > 0 && K > 0 && K % 128 == 0, "sm_q4_pack: K=%lld must be a positive multiple of 128",
+             (long long)K);
+  SM_REQUIRE(reinterpret_cast<uintptr_t>(codes) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(tiled_codes) % 16 == 0,
+             "sm_q4_pack: code buffers must be 16-byte aligned");
+  const int64_t chunks = q4t_rows(N) * (K / 128) * 4;
+  q4_pack_kernel<<<(unsigned)ceil_div(chunks, 256), 256, 0, as_stream(stream)>>>(
+      codes, scales, N, K, tiled_codes, tiled_scales);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
 
 extern "C" int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* codes,
                               uint16_t* scales, int32_t* bad_scales, void* stream) {

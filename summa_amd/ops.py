@@ -150,17 +150,31 @@ def fill_ce_stress(logits: torch.Tensor, targets: torch.Tensor, std: float = 3.0
 # ----------------------------------------------------------------- Q4G128 ---
 
 class Q4Weight:
-    """A Q4G128 weight resident in HBM: W[N, K] (out x in), codes + bf16 scales.
+    """A Q4G128 weight resident in HBM: W[N, K] (out x in).
 
     Device counterpart of ``PackedTensor`` (summa-train/src/quantization.rs:416-423)
-    for this build's 4-bit format (HQUANT tag 4)."""
+    for this build's 4-bit format (HQUANT tag 4). ``codes``/``scales`` hold the
+    row-major codec (the interchange format); ``tcodes``/``tscales`` the
+    prepared tiled copy the matmul kernels read (sm_q4_pack)."""
 
     def __init__(self, codes: torch.Tensor, scales: torch.Tensor, n: int, k: int):
         self.codes, self.scales, self.n, self.k = codes, scales, n, k
+        self.tcodes = self.tscales = None
+        if k % 128 == 0:  # groups never straddle rows: the matmul layout exists
+            rows = (n + 15) // 16 * 16
+            self.tcodes = torch.empty(rows * k // 2, dtype=torch.uint8, device=codes.device)
+            self.tscales = torch.empty(rows * k // 128, dtype=torch.int16, device=codes.device)
+            call("sm_q4_pack", codes.data_ptr(), scales.data_ptr(), n, k, self.tcodes.data_ptr(),
+                 self.tscales.data_ptr(), _stream())
 
     @property
     def nbytes(self) -> int:
-        return self.codes.numel() + 2 * self.scales.numel()
+        """Algorithmic bytes of the weight: N*K/2 codes + N*K/128 bf16 scales."""
+        return self.n * self.k // 2 + 2 * (self.n * self.k // 128)
+
+    def drop_rowmajor(self) -> None:
+        """Free the row-major copy (the kernels only read the tiled one)."""
+        self.codes = self.scales = None
 
     @classmethod
     def quantize(cls, w: torch.Tensor) -> "Q4Weight":
@@ -196,6 +210,8 @@ def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
     M, K = x.shape
     if K != w.k:
         raise ValueError(f"packed linear input width mismatch ({K} != {w.k})")
+    if w.tcodes is None:
+        raise ValueError(f"Q4 matmul needs K % 128 == 0 (K={w.k})")
     if epilogue == _lib.SM_EPI_SWIGLU_BF16:
         shape, dt = (M, w.n // 2), torch.bfloat16
     elif epilogue == _lib.SM_EPI_SWIGLU_F16:
@@ -209,6 +225,6 @@ def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
             raise ValueError("SM_EPI_ADD_F32 needs an output to accumulate into")
         out = torch.empty(shape, dtype=dt, device=x.device)
     _dev(out, "out")
-    call("sm_q4_matmul", w.codes.data_ptr(), w.scales.data_ptr(), w.n, w.k, x.data_ptr(), _dt(x),
+    call("sm_q4_matmul", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k, x.data_ptr(), _dt(x),
          M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
     return out

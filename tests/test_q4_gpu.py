@@ -88,9 +88,14 @@ def test_epilogues(dev):
 
 def test_rejects_bad_shapes(dev):
     w = ops.Q4Weight.quantize(torch.zeros(64, 256, device=dev))
-    with pytest.raises(_lib.SummaError, match="width mismatch|K="):
+    with pytest.raises(ValueError, match="K % 128"):
         bad = ops.Q4Weight(w.codes, w.scales, 64, 200)
         ops.q4_matmul(bad, torch.zeros(2, 200, dtype=torch.bfloat16, device=dev))
+    # the C ABI rejects it too (no kernel launch)
+    from summa_amd._lib import lib
+    st = lib().sm_q4_matmul(w.tcodes.data_ptr(), w.tscales.data_ptr(), 64, 200,
+                            w.tcodes.data_ptr(), 1, 2, 200, w.tcodes.data_ptr(), 64, 0, None)
+    assert st == -1 and b"multiple of 128" in lib().sm_last_error()
 
 
 @pytest.mark.parametrize("m", [1, 7, 128])
@@ -111,3 +116,34 @@ def test_matmul_f16_activations_and_swiglu_f16(dev, m):
                       epilogue=_lib.SM_EPI_SWIGLU_F16).float().cpu().numpy()
     g, v = y_ref[:, :F], y_ref[:, F:]
     np.testing.assert_allclose(h, g / (1 + np.exp(-g)) * v, rtol=2 ** -10, atol=1e-6)
+
+
+@pytest.mark.parametrize("m,n,k", [(257, 768, 768), (600, 130, 1024), (1000, 2304, 768),
+                                   (2100, 64, 256)])
+@pytest.mark.parametrize("xdt", ["bf16", "f16"])
+def test_large_m_lds_kernel(dev, m, n, k, xdt):
+    """M > 256 runs the LDS-tiled kernel (XCD-ordered 256x128 tiles, padded M tiles)."""
+    print(f"case m={m} n={n} k={k} x={xdt}", flush=True)
+    w = _weights(n, k, m + n)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(k).normal(0, 1, (m, k)).astype(np.float32)
+    if xdt == "f16":
+        xr = x.astype(np.float16).astype(np.float32)
+        xd = torch.from_numpy(x.astype(np.float16)).to(dev)
+    else:
+        xr = oracle.round_bf16(x)
+        xd = _bf16_dev(x, dev)
+    y_ref = _oracle_matmul(codes, scales, n, k, xr)
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    y = ops.q4_matmul(qw, xd).cpu().numpy()
+    assert np.all(np.abs(y - y_ref) <= tol), float(np.abs(y - y_ref).max())
+    base = np.random.default_rng(2).normal(0, 1, (m, n)).astype(np.float32)
+    acc = torch.from_numpy(base.copy()).to(dev)
+    ops.q4_matmul(qw, xd, out=acc, epilogue=_lib.SM_EPI_ADD_F32)
+    assert np.all(np.abs(acc.cpu().numpy() - (base + y_ref)) <= tol + 1e-6)
+    if n % 2 == 0:
+        F = n // 2
+        h = ops.q4_matmul(qw, xd, epilogue=_lib.SM_EPI_SWIGLU_F16).float().cpu().numpy()
+        g, v = y_ref[:, :F], y_ref[:, F:]
+        np.testing.assert_allclose(h, g / (1 + np.exp(-g)) * v, rtol=2 ** -10, atol=1e-5)
