@@ -261,7 +261,7 @@ def bench_rl_step(args) -> dict:
     return {
         "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
         "value": S * N / (roll * 1e-3), "unit": "rollout tok/s",
-        "ms_per_step": full, "dtype": "q4g128 weights x bf16 activations, f32 accumulate",
+        "ms_per_step": full, "dtype": "q4g128 weights, f16 matmul inputs, bf16 KV, f32 accumulate",
         "config": {"workload": "rl_step config[1]", "layers": 12, "d_model": 768, "heads": 12,
                    "ffn": 3072, "vocab": 32768, "prompts": groups, "group": G,
                    "prompt_len": P, "new_tokens": N, "temperature": 1.0,

@@ -15,8 +15,9 @@
 // operand (natural [pos][hd] layout is already k-contiguous per lane). The
 // online softmax runs on the MFMA output registers, probabilities go through a
 // per-wave LDS slice, and P.V is a VALU FMA pass with hd/8 lanes per V row
-// (16-byte loads, several rows per wave instruction, unrolled for loads in
-// flight). Waves merge (max, sum, O) in LDS
+// (16-byte loads, several rows per wave instruction). All K and V loads of a
+// 64-key tile are issued together before any math, so a tile costs one HBM
+// round trip. Waves merge (max, sum, O) in LDS
 // at the end in a fixed order.
 //
 // Prefill / recompute (many queries, causal) uses the flash-attention kernel
@@ -77,19 +78,35 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
   const int sub = lane / LPK;          // which key of the PPI group this lane handles
   const int dl = (lane % LPK) * 8;     // first of the eight dims this lane owns
 
+  constexpr int VR = 64 / PPI;  // V rows of a 64-key tile held by each lane
   for (int t0 = wave * 64; t0 < len; t0 += 256) {
+    // ---- issue every load of the tile up front (K fragments for the score
+    //      MFMAs and this lane's V rows for P.V), branch-free: rows past the
+    //      end are clamped to a valid row and masked out below. One round trip
+    //      per tile instead of one per dependent phase.
+    bf8 kf[4][STEPS];
+    u32x4 vr[VR];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const int key = min(t0 + kb * 16 + j, len - 1);
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st)
+        kf[kb][st] = *reinterpret_cast<const bf8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
+    }
+#pragma unroll
+    for (int i = 0; i < VR; ++i) {
+      const int key = min(t0 + sub + i * PPI, len - 1);
+      vr[i] = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)key * HD + dl);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     // ---- scores for 64 keys: 4 MFMA blocks of 16 keys
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int key = t0 + kb * 16 + j;
       f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int st = 0; st < STEPS; ++st) {
-        bf8 kf = bf8{};
-        if (key < len)
-          kf = *reinterpret_cast<const bf8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], kf, acc, 0, 0, 0);
-      }
+      for (int st = 0; st < STEPS; ++st)
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], kf[kb][st], acc, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
@@ -116,11 +133,11 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- P.V: LPK lanes per V row (16-byte loads), PPI rows per iteration
-    const int tend = min(64, len - t0);
-#pragma unroll 4
-    for (int tt = sub; tt < tend; tt += PPI) {
-      const u32x4 vv = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)(t0 + tt) * HD + dl);
+    // ---- P.V from the V rows already in registers (p = 0 past the end)
+#pragma unroll
+    for (int vi = 0; vi < VR; ++vi) {
+      const int tt = sub + vi * PPI;
+      const u32x4 vv = vr[vi];
       const float v[8] = {bf16lo(vv.x), bf16hi(vv.x), bf16lo(vv.y), bf16hi(vv.y),
                           bf16lo(vv.z), bf16hi(vv.z), bf16lo(vv.w), bf16hi(vv.w)};
 #pragma unroll
