@@ -104,6 +104,19 @@ CFG1 = dict(layers=12, d_model=768, heads=12, kv_heads=12, head_dim=64, ffn=3072
 CFG2 = dict(layers=24, d_model=2048, heads=16, kv_heads=4, head_dim=128, ffn=5632, vocab=65536)
 
 
+# config[4]: attention geometry is not specified by the config; H16 = KVH16,
+# head_dim 128 (d_model / heads). The dense FFN width is unused (all layers MoE).
+CFG4 = dict(layers=16, d_model=2048, heads=16, kv_heads=16, head_dim=128, ffn=1408, vocab=65536,
+            experts=32, expert_ffn=1408)
+
+# (model, prompts, group, prompt_len, new_tokens, reward sampler)
+RL_CONFIGS = {
+    1: (CFG1, 16, 8, 128, 256, "bernoulli0.3"),
+    2: (CFG2, 32, 8, 512, 512, "uniform"),
+    4: (CFG4, 16, 8, 256, 256, "bernoulli0.3"),
+}
+
+
 def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 10) -> dict:
     """M=1 Q4G128 GEMV over every linear of a model (whole-model weight sweep).
 
@@ -186,26 +199,32 @@ def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 10) -> dict:
             "lm_head_GBs": head_bytes / head_us / 1e3}
 
 
-def cpu_baseline_rl(seconds_cap: float = 60.0) -> dict:
+def cpu_baseline_rl(config: int) -> dict:
     """Oracle (C restatement, OpenMP over the host cores) rollout on a bounded
-    sample of config[1]: 2 rollouts x (128-token prompt + 8 sampled tokens)."""
+    sample of the workload: 2 rollouts x (full-length prompt + 8 sampled tokens)
+    for config[1], 1 x (prompt + 2) for the larger configs."""
     import numpy as np
 
     import oracle
 
-    cfg = {"layers": CFG1["layers"], "d": CFG1["d_model"], "H": CFG1["heads"],
-           "KVH": CFG1["kv_heads"], "hd": CFG1["head_dim"], "F": CFG1["ffn"], "V": CFG1["vocab"]}
+    mcfg, _, _, P, _, _ = RL_CONFIGS[config]
+    cfg = {"layers": mcfg["layers"], "d": mcfg["d_model"], "H": mcfg["heads"],
+           "KVH": mcfg["kv_heads"], "hd": mcfg["head_dim"], "F": mcfg["ffn"], "V": mcfg["vocab"]}
+    if mcfg.get("experts"):
+        cfg.update(E=mcfg["experts"], Fe=mcfg["expert_ffn"])
     w = oracle.random_weights(cfg, seed=0, std=0.02)
     host = oracle.HostModel(cfg, w, quantized=True)
-    S, P, N = 2, 128, 8
+    del w
+    S, N = (2, 8) if config == 1 else (1, 2)
     prompts = np.random.default_rng(0).integers(0, cfg["V"], (S, P)).astype(np.int32)
     t0 = time.perf_counter()
     host.generate(prompts, N, 1.0, 0)
     dt = time.perf_counter() - t0
-    return {"value": round(S * N / dt, 3), "unit": "rollout tok/s", "cores": os.cpu_count(),
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
+    return {"value": round(S * N / dt, 4), "unit": "rollout tok/s", "cores": threads,
             "kind": "port",
-            "sample": f"config[1] Q4 model, {S} rollouts x ({P}-token prompt + {N} sampled), "
-                      f"{dt:.1f} s"}
+            "sample": f"config[{config}] Q4 model, {S} rollouts x ({P}-token prompt + {N} "
+                      f"sampled), {dt:.1f} s (prefill included, as in the rollout)"}
 
 
 def bench_rl_step(args) -> dict:
@@ -213,17 +232,20 @@ def bench_rl_step(args) -> dict:
 
     from summa_amd.model import Model, ModelConfig, batch_result, rl_prepare
 
-    groups, G, P, N = 16, 8, 128, 256
+    mcfg, groups, G, P, N, reward_kind = RL_CONFIGS[args.config]
     S = groups * G
     dev = torch.device("cuda:0")
-    mc = ModelConfig(**CFG1, max_seq=P + N, quantized=True)
+    mc = ModelConfig(**mcfg, max_seq=P + N, quantized=True)
     policy = Model(mc)
     policy.init_random(seed=0, std=0.02)
     reference = Model(mc)
     reference.init_random(seed=0, std=0.02)  # frozen copy of the initial policy
     gen = torch.Generator().manual_seed(0)
     prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
-    rewards = torch.bernoulli(torch.full((groups, G), 0.3), generator=gen).to(dev)
+    if reward_kind == "uniform":
+        rewards = torch.rand((groups, G), generator=gen).to(dev)
+    else:
+        rewards = torch.bernoulli(torch.full((groups, G), 0.3), generator=gen).to(dev)
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
 
@@ -262,10 +284,10 @@ def bench_rl_step(args) -> dict:
         "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
         "value": S * N / (roll * 1e-3), "unit": "rollout tok/s",
         "ms_per_step": full, "dtype": "q4g128 weights, f16 matmul inputs, bf16 KV, f32 accumulate",
-        "config": {"workload": "rl_step config[1]", "layers": 12, "d_model": 768, "heads": 12,
-                   "ffn": 3072, "vocab": 32768, "prompts": groups, "group": G,
-                   "prompt_len": P, "new_tokens": N, "temperature": 1.0,
-                   "weights": "Q4G128 (bf16 scales)", "rewards": "Bernoulli(0.3)"},
+        "config": {"workload": f"rl_step config[{args.config}]", **mcfg, "prompts": groups,
+                   "group": G, "prompt_len": P, "new_tokens": N, "temperature": 1.0,
+                   "weights": "Q4G128 (bf16 scales)",
+                   "rewards": "U[0,1]" if reward_kind == "uniform" else "Bernoulli(0.3)"},
         "rl_step_ms": round(full, 3), "rollout_ms": round(roll, 3),
         "prepare_ms": round(full - roll, 3), "wall_s": round(wall, 3),
         "grpo": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()},
@@ -288,6 +310,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--workload", default="rl_step", choices=sorted(WORKLOADS))
     p.add_argument("--rows", type=int, default=65536)
+    p.add_argument("--config", type=int, default=1, choices=sorted(RL_CONFIGS),
+                   help="rl_step: BASELINE config index (1 = the headline line)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args()
     if args.gpus != 1:
@@ -305,7 +329,7 @@ def main() -> int:
     out.update(res)
     if not args.no_cpu_baseline:
         log("bench: cpu baseline")
-        out["cpu_baseline"] = (cpu_baseline_rl() if args.workload == "rl_step"
+        out["cpu_baseline"] = (cpu_baseline_rl(args.config) if args.workload == "rl_step"
                                else cpu_baseline_ce(256, 131072))
     print(json.dumps(out), flush=True)
     return 0

@@ -201,6 +201,43 @@ int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab, floa
               int64_t lp_stride, int32_t* next_ids, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Top-2 mixture of experts (SparseMoe::forward, summa-llm/src/model/ffn.rs:
+ * 478-711), all on the device with no host round trip.
+ * sm_moe_router_top2: logits = f32 h . W_r^T (W_r [E, d] f32), top-2 with a
+ *   strict '>' scan (top2_indices_kernel, moe_topk.rs:74-104), weights =
+ *   softmax over the pair. top_idx/top_w [tokens, 2]; logits_out nullable.
+ *   h f32 or f16 [tokens, d], d <= 8192, 2 <= E <= 64.
+ * sm_moe_route_plan: stable sort of routes r = t*k + j by expert
+ *   (host_route_plan ffn.rs:888-929 / route_plan moe_route.rs:22-142) into the
+ *   int32 `plan` buffer of sm_moe_plan_words() words: counts[E],
+ *   offsets[E+1], order[R], inverse[R], src_rows[R], then 16- and 256-row
+ *   tile lists used by sm_q4_grouped_matmul. error (device int32, caller-zeroed)
+ *   gets bit 0 set for an expert index outside [0, E); such a route is left
+ *   out of the plan (inverse = -1) and contributes nothing in sm_moe_combine.
+ *   One workgroup; E <= 64.
+ * sm_q4_grouped_matmul: per expert e, rows offsets[e]..offsets[e+1]-1 of y =
+ *   A . W_e^T with W_e the e-th of `experts` stacked prepared Q4 weights
+ *   [N, K]; A row p = x[src_rows[p]] when gather != 0 (the token gather,
+ *   route_gather moe_dispatch.rs:57, folded into the matmul) else x[p]
+ *   (grouped_linear / grouped_swiglu_mlp, grouped_linear.rs:65-104).
+ *   Epilogues: SM_EPI_STORE_F32/BF16 or SM_EPI_SWIGLU_BF16/F16.
+ * sm_moe_combine: x[t] += sum_j top_w[t,j] * routed[inverse[t*k+j]] (f32)
+ *   (route_combine_forward, moe_dispatch.rs:290-312).
+ */
+int64_t sm_moe_plan_words(int64_t tokens, int64_t top_k, int64_t experts);
+int sm_moe_router_top2(const void* h, int h_dtype, const float* w_router, int64_t tokens,
+                       int64_t d, int64_t experts, float* logits_out, int32_t* top_idx,
+                       float* top_w, void* stream);
+int sm_moe_route_plan(const int32_t* top_idx, int64_t tokens, int64_t top_k, int64_t experts,
+                      int32_t* plan, int32_t* error, void* stream);
+int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts, int64_t N,
+                         int64_t K, const void* x, int x_dtype, int64_t ldx, int gather,
+                         const int32_t* plan, int64_t tokens, int64_t top_k, void* y, int64_t ldy,
+                         int epilogue, void* stream);
+int sm_moe_combine(const float* routed, const float* top_w, const int32_t* plan, int64_t tokens,
+                   int64_t top_k, int64_t experts, int64_t d, float* x, void* stream);
+
+/* ------------------------------------------------------------------------
  * Decoder model (the MAL Transformer subset the configs use,
  * summa-llm/src/model/transformer.rs, block.rs, attention.rs, ffn.rs) and the
  * RL-step runtime behind GrpoDeviceBatchRuntime (posttrain.rs:1288-1305).
@@ -212,6 +249,8 @@ typedef struct sm_model_config {
   float rope_theta;  /* MAL default 1e4 */
   int32_t quantized; /* 1: Q4G128 linears, f16 matmul inputs, bf16 q/KV/embedding;
                         0: all fp32 */
+  int32_t experts;    /* 0: dense SwiGLU FFN; > 0: top-2 MoE FFN in every layer */
+  int32_t expert_ffn; /* expert intermediate width (MoE only) */
 } sm_model_config;
 
 typedef struct sm_model sm_model;
@@ -228,7 +267,10 @@ enum {
   SM_W_IN = 5,         /* [2F, d] per layer */
   SM_W_DOWN = 6,       /* [d, F] per layer */
   SM_W_FINAL_NORM = 7, /* [d] */
-  SM_W_LM_HEAD = 8     /* [vocab, d] */
+  SM_W_LM_HEAD = 8,    /* [vocab, d] */
+  SM_W_ROUTER = 9,     /* [E, d] per layer, kept f32 (router math is fp32, ffn.rs:489) */
+  SM_W_EXPERT_IN = 10, /* [E, 2Fe, d] per layer ([gate | value] rows per expert) */
+  SM_W_EXPERT_DOWN = 11 /* [E, d, Fe] per layer */
 };
 
 int sm_model_create(const sm_model_config* cfg, sm_model** out);
@@ -240,7 +282,8 @@ int64_t sm_model_weight_bytes(const sm_model* model);
  * for quantized linears (range check of the scales). */
 int sm_model_set_tensor(sm_model* model, int kind, int layer, const float* src, void* stream);
 /* Synthetic weights: every linear and the embedding ~ N(0, std) from the
- * counter RNG, norms = 1 (the BASELINE configs' random init). */
+ * counter RNG, norms = 1, router ~ N(0, 1/sqrt(d)) so router logits are
+ * ~N(0, 1) (the BASELINE configs' random init). */
 int sm_model_init_random(sm_model* model, uint64_t seed, float std, void* stream);
 
 /* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout

@@ -64,7 +64,10 @@ class OrModel(C.Structure):
         [(n, C.c_void_p) for n in ("embed", "attn_norm", "ffn_norm", "final_norm",
                                    "qkv", "o", "in_", "down", "lm_head",
                                    "qkv_c", "o_c", "in_c", "down_c", "lm_c",
-                                   "qkv_s", "o_s", "in_s", "down_s", "lm_s")]
+                                   "qkv_s", "o_s", "in_s", "down_s", "lm_s")] + \
+        [("experts", C.c_int32), ("expert_ffn", C.c_int32)] + \
+        [(n, C.c_void_p) for n in ("router", "exp_in", "exp_down", "exp_in_c", "exp_down_c",
+                                   "exp_in_s", "exp_down_s", "router_gap")]
 
 
 def _declare_model(L: C.CDLL) -> None:
@@ -178,7 +181,9 @@ class HostModel:
 
     ``weights`` maps names to float32 arrays: embed [V, d], attn_norm / ffn_norm
     [layers, d], final_norm [d], and linears qkv / o / in / down [layers, N, K],
-    lm_head [V, d] in [out, in] layout. When ``quantized`` the linears are
+    lm_head [V, d] in [out, in] layout; MoE models (cfg "E", "Fe") carry router
+    [layers, E, d], exp_in [layers, E, 2Fe, d], exp_down [layers, E, d, Fe]
+    instead of in / down, each expert quantized as its own tensor. When ``quantized`` the linears are
     packed with the Q4G128 oracle codec and the embedding is rounded to bf16.
     ``acc64`` (default: on for quantized models) accumulates matmuls in f64.
     """
@@ -198,10 +203,28 @@ class HostModel:
         m.eps, m.theta = float(cfg.get("eps", 1e-5)), float(cfg.get("theta", 1e4))
         for k in ("embed", "attn_norm", "ffn_norm", "final_norm"):
             setattr(m, k, self._ptr(w[k]))
+        self.packed = {}
+        m.experts = int(cfg.get("E", 0))
+        m.expert_ffn = int(cfg.get("Fe", 0))
+        if m.experts:
+            if quantized and (2 * m.expert_ffn * m.d) % 128:
+                raise ValueError("quantized experts need 2 * Fe * d % 128 == 0")
+            m.router = self._ptr(w["router"])
+            for k in ("exp_in", "exp_down"):
+                if quantized:
+                    arr = w[k].reshape(-1, *w[k].shape[2:])  # [layers*E, N, K]
+                    cs, ss = zip(*[q4_quantize(a) for a in arr])
+                    codes, scales = np.concatenate(cs), np.concatenate(ss)
+                    self.packed[k] = (codes, scales)
+                    setattr(m, k + "_c", self._ptr(codes))
+                    setattr(m, k + "_s", self._ptr(scales))
+                else:
+                    setattr(m, k, self._ptr(w[k]))
         names = {"qkv": "qkv", "o": "o", "in": "in_", "down": "down", "lm_head": "lm_head"}
         short = {"qkv": "qkv", "o": "o", "in": "in", "down": "down", "lm_head": "lm"}
-        self.packed = {}
         for k, field in names.items():
+            if k not in w:  # MoE models have no dense FFN
+                continue
             if quantized:
                 arr = w[k] if k != "lm_head" else w[k][None]
                 cs, ss = zip(*[q4_quantize(a) for a in arr])
@@ -252,6 +275,22 @@ class HostModel:
         return logits.reshape(S, L, c["V"])
 
 
+    def router_gaps(self, ids):
+        """MoE router margins of a full forward over ids [S, L]: [layers, S, L]
+        array of (2nd-largest - 3rd-largest) router logit per token; a small
+        margin means the top-2 expert set is a near-tie."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        S, L = ids.shape
+        c = self.cfg
+        gaps = np.full((c["layers"], S * L), np.inf, np.float32)
+        self.m.router_gap = gaps.ctypes.data
+        try:
+            self.forward_logits(ids)
+        finally:
+            self.m.router_gap = None
+        return gaps.reshape(c["layers"], S, L)
+
+
 def sample(logits, temperature, seed, step):
     logits = np.ascontiguousarray(logits, dtype=np.float32)
     rows, V = logits.shape
@@ -263,12 +302,23 @@ def sample(logits, temperature, seed, step):
 
 
 def random_weights(cfg: dict, seed: int = 0, std: float = 0.02) -> dict:
-    """N(0, std) linears and embedding, unit norms (the configs' synthetic init)."""
+    """N(0, std) linears and embedding, unit norms (the configs' synthetic init).
+    MoE configs (cfg["E"] > 0) get a router ~ N(0, 1/sqrt(d)) (router logits
+    ~ N(0, 1)) and stacked experts instead of the dense FFN."""
     rng = np.random.default_rng(seed)
     Lr, d, H, KVH, hd, F, V = (cfg[k] for k in ("layers", "d", "H", "KVH", "hd", "F", "V"))
     qn = H * hd + 2 * KVH * hd
     n = lambda *s: rng.normal(0, std, s).astype(np.float32)  # noqa: E731
-    return {"embed": n(V, d), "attn_norm": np.ones((Lr, d), np.float32),
-            "ffn_norm": np.ones((Lr, d), np.float32), "final_norm": np.ones(d, np.float32),
-            "qkv": n(Lr, qn, d), "o": n(Lr, d, H * hd), "in": n(Lr, 2 * F, d),
-            "down": n(Lr, d, F), "lm_head": n(V, d)}
+    w = {"embed": n(V, d), "attn_norm": np.ones((Lr, d), np.float32),
+         "ffn_norm": np.ones((Lr, d), np.float32), "final_norm": np.ones(d, np.float32),
+         "qkv": n(Lr, qn, d), "o": n(Lr, d, H * hd), "lm_head": n(V, d)}
+    E = cfg.get("E", 0)
+    if E:
+        Fe = cfg["Fe"]
+        w["router"] = rng.normal(0, 1 / np.sqrt(d), (Lr, E, d)).astype(np.float32)
+        w["exp_in"] = n(Lr, E, 2 * Fe, d)
+        w["exp_down"] = n(Lr, E, d, Fe)
+    else:
+        w["in"] = n(Lr, 2 * F, d)
+        w["down"] = n(Lr, d, F)
+    return w

@@ -40,6 +40,16 @@ typedef struct or_model {
   const float *qkv, *o, *in, *down, *lm_head;           /* dense [N, K] per layer */
   const uint8_t *qkv_c, *o_c, *in_c, *down_c, *lm_c;    /* Q4 codes per layer */
   const uint16_t *qkv_s, *o_s, *in_s, *down_s, *lm_s;   /* Q4 scales per layer */
+  /* top-2 MoE FFN (experts > 0): router [layers][E][d] f32, expert weights
+   * [layers][E][2Fe, d] and [layers][E][d, Fe], dense or Q4 like the rest */
+  int32_t experts, expert_ffn;
+  const float* router;
+  const float *exp_in, *exp_down;
+  const uint8_t *exp_in_c, *exp_down_c;
+  const uint16_t *exp_in_s, *exp_down_s;
+  /* optional diagnostics: when set, moe_ffn stores for layer l and row t the
+   * router margin (2nd-largest minus 3rd-largest logit) at [l * M + t] */
+  float* router_gap;
 } or_model;
 
 /* bf16 rounding: q, k, v (KV cache) and the embedding of quantized models. */
@@ -58,31 +68,10 @@ static float q4_at(const uint8_t* codes, const uint16_t* scales, int64_t i) {
   return or_bf16_to_f32(scales[i / 128]) * (float)q;
 }
 
-/* y[r, n] (+)= sum_k x[r, k] * W[n, k] with sequential f32 accumulation. */
-static void linear(const or_model* m, int kind, int layer, const float* x, int64_t M, float* y,
-                   int add) {
-  int64_t N, K;
-  const float* w = NULL;
-  const uint8_t* c = NULL;
-  const uint16_t* s = NULL;
-  const int64_t qdim = (int64_t)m->H * m->hd, kvdim = (int64_t)m->KVH * m->hd;
-  switch (kind) {
-    case 0: N = qdim + 2 * kvdim; K = m->d; break;
-    case 1: N = m->d; K = qdim; break;
-    case 2: N = 2 * (int64_t)m->F; K = m->d; break;
-    case 3: N = m->d; K = m->F; break;
-    default: N = m->V; K = m->d; break;
-  }
-  const int64_t off = (kind == 4) ? 0 : (int64_t)layer * N * K;
-  if (m->quantized) {
-    const uint8_t* cs[] = {m->qkv_c, m->o_c, m->in_c, m->down_c, m->lm_c};
-    const uint16_t* ss[] = {m->qkv_s, m->o_s, m->in_s, m->down_s, m->lm_s};
-    c = cs[kind] + off / 2;
-    s = ss[kind] + off / 128;
-  } else {
-    const float* ws[] = {m->qkv, m->o, m->in, m->down, m->lm_head};
-    w = ws[kind] + off;
-  }
+/* y[r, n] (+)= sum_k x[r, k] * W[n, k]; W dense f32 (w) or Q4 codes/scales
+ * (c, s); sequential f32 accumulation, or f64 with acc64. */
+static void linear_w(const or_model* m, int64_t N, int64_t K, const float* w, const uint8_t* c,
+                     const uint16_t* s, const float* x, int64_t M, float* y, int add) {
 #pragma omp parallel for schedule(static) collapse(2)
   for (int64_t r = 0; r < M; ++r)
     for (int64_t n = 0; n < N; ++n) {
@@ -100,6 +89,87 @@ static void linear(const or_model* m, int kind, int layer, const float* x, int64
       if (m->acc64) acc = (float)acc64;
       if (add) y[r * N + n] += acc; else y[r * N + n] = acc;
     }
+}
+
+/* kind: 0 qkv, 1 o, 2 in, 3 down, 4 lm_head */
+static void linear(const or_model* m, int kind, int layer, const float* x, int64_t M, float* y,
+                   int add) {
+  int64_t N, K;
+  const int64_t qdim = (int64_t)m->H * m->hd, kvdim = (int64_t)m->KVH * m->hd;
+  switch (kind) {
+    case 0: N = qdim + 2 * kvdim; K = m->d; break;
+    case 1: N = m->d; K = qdim; break;
+    case 2: N = 2 * (int64_t)m->F; K = m->d; break;
+    case 3: N = m->d; K = m->F; break;
+    default: N = m->V; K = m->d; break;
+  }
+  const int64_t off = (kind == 4) ? 0 : (int64_t)layer * N * K;
+  if (m->quantized) {
+    const uint8_t* cs[] = {m->qkv_c, m->o_c, m->in_c, m->down_c, m->lm_c};
+    const uint16_t* ss[] = {m->qkv_s, m->o_s, m->in_s, m->down_s, m->lm_s};
+    linear_w(m, N, K, NULL, cs[kind] + off / 2, ss[kind] + off / 128, x, M, y, add);
+  } else {
+    const float* ws[] = {m->qkv, m->o, m->in, m->down, m->lm_head};
+    linear_w(m, N, K, ws[kind] + off, NULL, NULL, x, M, y, add);
+  }
+}
+
+static float rh(const or_model* m, float v);
+
+/* x += SparseMoe(h) (ffn.rs:478-711) for M tokens: fp32 router, strict top-2,
+ * softmax over the pair, per-route SwiGLU expert MLP, weighted sum. */
+static void moe_ffn(const or_model* m, int layer, const float* h, int64_t M, float* x) {
+  const int E = m->experts, Fe = m->expert_ffn, d = m->d;
+  const float* wr = m->router + (size_t)layer * E * d;
+  const int64_t nin = 2 * (int64_t)Fe * d, ndown = (int64_t)d * Fe;
+  float* gv = malloc(sizeof(float) * 2 * Fe);
+  float* u = malloc(sizeof(float) * Fe);
+  float* yv = malloc(sizeof(float) * 2 * d);
+  float* lg = malloc(sizeof(float) * E);
+  for (int64_t t = 0; t < M; ++t) {
+    const float* ht = h + t * d;
+    for (int e = 0; e < E; ++e) {
+      float acc = 0.f;
+      double acc64 = 0.0;
+      if (m->acc64) { for (int c = 0; c < d; ++c) acc64 += (double)ht[c] * wr[(size_t)e * d + c]; acc = (float)acc64; }
+      else for (int c = 0; c < d; ++c) acc += ht[c] * wr[(size_t)e * d + c];
+      lg[e] = acc;
+    }
+    float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY;
+    int i0 = 0, i1 = 0;
+    for (int e = 0; e < E; ++e) {
+      if (lg[e] > v0) { v2 = v1; v1 = v0; i1 = i0; v0 = lg[e]; i0 = e; }
+      else if (lg[e] > v1) { v2 = v1; v1 = lg[e]; i1 = e; }
+      else if (lg[e] > v2) v2 = lg[e];
+    }
+    if (m->router_gap) m->router_gap[(int64_t)layer * M + t] = v1 - v2;
+    const float e1 = expf(v1 - v0);
+    const float w0 = 1.f / (1.f + e1), w1 = e1 / (1.f + e1);
+    const int sel[2] = {i0, i1};
+    for (int j = 0; j < 2; ++j) {
+      const int e = sel[j];
+      const int64_t base_in = ((int64_t)layer * E + e) * nin, base_down = ((int64_t)layer * E + e) * ndown;
+      if (m->quantized)
+        linear_w(m, 2 * Fe, d, NULL, m->exp_in_c + base_in / 2, m->exp_in_s + base_in / 128, ht, 1, gv, 0);
+      else
+        linear_w(m, 2 * Fe, d, m->exp_in + base_in, NULL, NULL, ht, 1, gv, 0);
+      for (int c = 0; c < Fe; ++c) {
+        const float g = gv[c], v = gv[Fe + c];
+        u[c] = rh(m, g / (1.0f + expf(-g)) * v);
+      }
+      if (m->quantized)
+        linear_w(m, d, Fe, NULL, m->exp_down_c + base_down / 2, m->exp_down_s + base_down / 128, u, 1, yv + j * d, 0);
+      else
+        linear_w(m, d, Fe, m->exp_down + base_down, NULL, NULL, u, 1, yv + j * d, 0);
+    }
+    for (int c = 0; c < d; ++c) {
+      float sum = 0.f;
+      sum += yv[c] * w0;
+      sum += yv[d + c] * w1;
+      x[t * d + c] += sum;
+    }
+  }
+  free(gv); free(u); free(yv); free(lg);
 }
 
 static void rmsnorm(const or_model* m, const float* x, const float* g, int64_t M, float* y) {
@@ -196,6 +266,10 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
       }
     linear(m, 1, l, att, rows, x, 1);
     rmsnorm(m, x, m->ffn_norm + (size_t)l * d, rows, h);
+    if (m->experts > 0) {
+      moe_ffn(m, l, h, rows, x);
+      continue;
+    }
     linear(m, 2, l, h, rows, gv, 0);
     for (int64_t r = 0; r < rows; ++r)
       for (int c = 0; c < F; ++c) {

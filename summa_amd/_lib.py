@@ -38,6 +38,12 @@ SIGNATURES: dict[str, tuple] = {
     "sm_attn_decode": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, vp]),
     "sm_attn_prefill": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_sample": (i32, [vp, i64, i64, i64, f32, u64, i64, vp, i64, vp, i64, vp, vp]),
+    "sm_moe_plan_words": (i64, [i64, i64, i64]),
+    "sm_moe_router_top2": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, vp]),
+    "sm_moe_route_plan": (i32, [vp, i64, i64, i64, vp, vp, vp]),
+    "sm_q4_grouped_matmul": (i32, [vp, vp, i64, i64, i64, vp, i32, i64, i32, vp, i64, i64, vp, i64,
+                                   i32, vp]),
+    "sm_moe_combine": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "sm_model_create": (i32, [vp, vp]),
     "sm_model_destroy": (i32, [vp]),
     "sm_model_weight_bytes": (i64, [vp]),

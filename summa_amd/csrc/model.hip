@@ -47,6 +47,15 @@ int sm_ce_rows(const void*, int, const int32_t*, int64_t, int64_t, int64_t, floa
 int sm_grpo_loss(const float*, const float*, const float*, const float*, const float*, int64_t,
                  int64_t, int64_t, double, double, double, float*, float*, float*, int32_t*, void*);
 int sm_fill_normal(void*, int, int64_t, float, float, uint64_t, void*);
+int64_t sm_moe_plan_words(int64_t, int64_t, int64_t);
+int sm_moe_router_top2(const void*, int, const float*, int64_t, int64_t, int64_t, float*, int32_t*,
+                       float*, void*);
+int sm_moe_route_plan(const int32_t*, int64_t, int64_t, int64_t, int32_t*, int32_t*, void*);
+int sm_q4_grouped_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, const void*,
+                         int, int64_t, int, const int32_t*, int64_t, int64_t, void*, int64_t, int,
+                         void*);
+int sm_moe_combine(const float*, const float*, const int32_t*, int64_t, int64_t, int64_t, int64_t,
+                   float*, void*);
 }
 
 namespace sm {
@@ -78,6 +87,10 @@ struct Layer {
   float* attn_norm = nullptr;
   float* ffn_norm = nullptr;
   Linear qkv, o, in, down;
+  // MoE layers: router [E, d] f32 and E stacked experts (prepared Q4), each
+  // expert's weights at codes + e * (rows(N) * K/2), scales + e * (rows(N) * K/128)
+  float* router = nullptr;
+  Linear exp_in, exp_down;  // N/K are one expert's shape
 };
 
 __global__ void fill_f32_kernel(float* p, int64_t n, float v) {
@@ -152,7 +165,7 @@ struct sm_model {
   size_t weight_bytes = 0;
   // workspace
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
-      lp_tmp, flags;
+      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err;
   int64_t gen_cap = 0, gen_S = 0;
 };
 
@@ -166,14 +179,14 @@ int dalloc(sm_model* m, void** p, size_t bytes, bool weight) {
   return SM_OK;
 }
 
-int alloc_linear(sm_model* m, Linear& L, int64_t N, int64_t K) {
+int alloc_linear(sm_model* m, Linear& L, int64_t N, int64_t K, int64_t count = 1) {
   L.N = N;
   L.K = K;
   if (m->cfg.quantized) {
     // prepared tiled layout (sm_q4_pack): rows padded to a multiple of 16
     const int64_t rows = q4t_rows(N);
-    SM_TRY(dalloc(m, (void**)&L.codes, (size_t)rows * K / 2, true));
-    SM_TRY(dalloc(m, (void**)&L.scales, (size_t)rows * (K / 128) * 2, true));
+    SM_TRY(dalloc(m, (void**)&L.codes, (size_t)count * rows * K / 2, true));
+    SM_TRY(dalloc(m, (void**)&L.scales, (size_t)count * rows * (K / 128) * 2, true));
   } else {
     SM_TRY(dalloc(m, (void**)&L.w, (size_t)(N * K) * 4, true));
   }
@@ -199,6 +212,31 @@ int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* 
   SM_TRY(sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, (float*)m->gv.p, L.N,
                      SM_EPI_STORE_F32, st));
   return sm_swiglu_f32((const float*)m->gv.p, M, L.N / 2, (float*)u, st);
+}
+
+// x += MoE(h) for `rows` tokens: router + top-2, route plan, two grouped Q4
+// matmuls (gathered SwiGLU in, down), combine. All device side.
+int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st) {
+  const auto& c = m->cfg;
+  const int64_t E = c.experts, Fe = c.expert_ffn, d = c.d_model, k = 2;
+  const int64_t routes = rows * k;
+  SM_TRY(ensure(m->moe_idx, (size_t)routes * 4));
+  SM_TRY(ensure(m->moe_w, (size_t)routes * 4));
+  SM_TRY(ensure(m->moe_plan, (size_t)sm_moe_plan_words(rows, k, E) * 4));
+  SM_TRY(ensure(m->moe_u, (size_t)routes * Fe * 2));
+  SM_TRY(ensure(m->moe_y, (size_t)routes * d * 4));
+  SM_TRY(ensure(m->moe_err, 4));
+  int32_t* plan = (int32_t*)m->moe_plan.p;
+  SM_TRY(sm_moe_router_top2(m->h.p, m->act, Ly.router, rows, d, E, nullptr,
+                            (int32_t*)m->moe_idx.p, (float*)m->moe_w.p, st));
+  SM_TRY(sm_moe_route_plan((const int32_t*)m->moe_idx.p, rows, k, E, plan,
+                           (int32_t*)m->moe_err.p, st));
+  SM_TRY(sm_q4_grouped_matmul(Ly.exp_in.codes, Ly.exp_in.scales, E, 2 * Fe, d, m->h.p, m->act, d,
+                              1, plan, rows, k, m->moe_u.p, Fe, SM_EPI_SWIGLU_F16, st));
+  SM_TRY(sm_q4_grouped_matmul(Ly.exp_down.codes, Ly.exp_down.scales, E, d, Fe, m->moe_u.p,
+                              SM_F16, Fe, 0, plan, rows, k, m->moe_y.p, d, SM_EPI_STORE_F32, st));
+  return sm_moe_combine((const float*)m->moe_y.p, (const float*)m->moe_w.p, plan, rows, k, E, d,
+                        (float*)m->x.p, st);
 }
 
 size_t cache_layer_elems(const sm_model* m, int64_t S, int64_t cap) {
@@ -238,8 +276,12 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
                              c.kv_heads, cap, c.head_dim, st));
     SM_TRY(linear_f32out(m, Ly.o, m->attn.p, rows, x, true, st));
     SM_TRY(sm_rmsnorm(x, Ly.ffn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
-    SM_TRY(linear_swiglu(m, Ly.in, m->h.p, rows, m->u.p, st));
-    SM_TRY(linear_f32out(m, Ly.down, m->u.p, rows, x, true, st));
+    if (c.experts > 0) {
+      SM_TRY(moe_ffn(m, Ly, rows, st));
+    } else {
+      SM_TRY(linear_swiglu(m, Ly.in, m->h.p, rows, m->u.p, st));
+      SM_TRY(linear_f32out(m, Ly.down, m->u.p, rows, x, true, st));
+    }
   }
   return SM_OK;
 }
@@ -267,6 +309,12 @@ extern "C" int sm_model_create(const sm_model_config* cfg, sm_model** out) {
   if (c.quantized)
     SM_REQUIRE(c.d_model % 128 == 0 && c.ffn % 128 == 0 && (c.heads * c.head_dim) % 128 == 0,
                "sm_model_create: quantized models need d_model, ffn and heads*head_dim % 128 == 0");
+  SM_REQUIRE(c.experts >= 0 && c.experts <= 64, "sm_model_create: experts must be in 0..=64");
+  if (c.experts > 0) {
+    SM_REQUIRE(c.quantized, "sm_model_create: MoE layers are built for quantized models");
+    SM_REQUIRE(c.experts >= 2 && c.expert_ffn > 0 && c.expert_ffn % 128 == 0,
+               "sm_model_create: MoE needs >= 2 experts and expert_ffn % 128 == 0");
+  }
   sm_model* m = new sm_model();
   m->cfg = c;
   m->act = c.quantized ? SM_F16 : SM_F32;
@@ -286,8 +334,15 @@ extern "C" int sm_model_create(const sm_model_config* cfg, sm_model** out) {
     if ((s = dalloc(m, (void**)&Ly.ffn_norm, (size_t)c.d_model * 4, true))) return fail(s);
     if ((s = alloc_linear(m, Ly.qkv, m->qkv_n, c.d_model))) return fail(s);
     if ((s = alloc_linear(m, Ly.o, c.d_model, m->qdim))) return fail(s);
-    if ((s = alloc_linear(m, Ly.in, 2 * (int64_t)c.ffn, c.d_model))) return fail(s);
-    if ((s = alloc_linear(m, Ly.down, c.d_model, c.ffn))) return fail(s);
+    if (c.experts > 0) {
+      if ((s = dalloc(m, (void**)&Ly.router, (size_t)c.experts * c.d_model * 4, true))) return fail(s);
+      if ((s = alloc_linear(m, Ly.exp_in, 2 * (int64_t)c.expert_ffn, c.d_model, c.experts)))
+        return fail(s);
+      if ((s = alloc_linear(m, Ly.exp_down, c.d_model, c.expert_ffn, c.experts))) return fail(s);
+    } else {
+      if ((s = alloc_linear(m, Ly.in, 2 * (int64_t)c.ffn, c.d_model))) return fail(s);
+      if ((s = alloc_linear(m, Ly.down, c.d_model, c.ffn))) return fail(s);
+    }
   }
   // RoPE table: adjacent pairs, theta^(-2p/hd), angle = pos * freq, computed in
   // double and rounded to f32 (cos, sin) per (pos, pair).
@@ -315,7 +370,8 @@ extern "C" int sm_model_destroy(sm_model* m) {
   for (void* p : m->owned) hipFree(p);
   DevBuf* bufs[] = {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits,
                     &m->rows, &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc,
-                    &m->rkc, &m->rvc, &m->lp_tmp, &m->flags};
+                    &m->rkc, &m->rvc, &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w,
+                    &m->moe_plan, &m->moe_u, &m->moe_y, &m->moe_err};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
   delete m;
@@ -325,12 +381,17 @@ extern "C" int sm_model_destroy(sm_model* m) {
 extern "C" int64_t sm_model_weight_bytes(const sm_model* m) { return m ? (int64_t)m->weight_bytes : 0; }
 
 static int tensor_target(sm_model* m, int kind, int layer, Linear** lin, void** dense,
-                         int64_t* n) {
+                         int64_t* n, int64_t* count) {
   const auto& c = m->cfg;
   *lin = nullptr;
   *dense = nullptr;
+  *count = 1;
+  const bool moe_kind = kind == SM_W_ROUTER || kind == SM_W_EXPERT_IN || kind == SM_W_EXPERT_DOWN;
   const bool per_layer = kind == SM_W_ATTN_NORM || kind == SM_W_FFN_NORM || kind == SM_W_QKV ||
-                         kind == SM_W_O || kind == SM_W_IN || kind == SM_W_DOWN;
+                         kind == SM_W_O || kind == SM_W_IN || kind == SM_W_DOWN || moe_kind;
+  if (moe_kind) SM_REQUIRE(c.experts > 0, "tensor kind %d needs an MoE model", kind);
+  if (kind == SM_W_IN || kind == SM_W_DOWN)
+    SM_REQUIRE(c.experts == 0, "MoE models have no dense FFN (tensor kind %d)", kind);
   if (per_layer) SM_REQUIRE(layer >= 0 && layer < c.layers, "layer %d out of range", layer);
   switch (kind) {
     case SM_W_EMBED: *dense = m->embed; *n = (int64_t)c.vocab * c.d_model; break;
@@ -342,6 +403,9 @@ static int tensor_target(sm_model* m, int kind, int layer, Linear** lin, void** 
     case SM_W_O: *lin = &m->layers[layer].o; break;
     case SM_W_IN: *lin = &m->layers[layer].in; break;
     case SM_W_DOWN: *lin = &m->layers[layer].down; break;
+    case SM_W_ROUTER: *dense = m->layers[layer].router; *n = (int64_t)c.experts * c.d_model; break;
+    case SM_W_EXPERT_IN: *lin = &m->layers[layer].exp_in; *count = c.experts; break;
+    case SM_W_EXPERT_DOWN: *lin = &m->layers[layer].exp_down; *count = c.experts; break;
     default: set_error("unknown tensor kind %d", kind); return SM_ERR_INVALID;
   }
   if (*lin) *n = (*lin)->N * (*lin)->K;
@@ -362,12 +426,13 @@ extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float
   SM_REQUIRE(m && src, "sm_model_set_tensor: null argument");
   Linear* lin;
   void* dense;
-  int64_t n;
-  SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n));
+  int64_t n, count;
+  SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n, &count));
   hipStream_t st = as_stream(stream);
   if (lin) {
     if (m->cfg.quantized) {
-      // quantize to the row-major codec in a temporary, then prepare (tile)
+      // quantize to the row-major codec in a temporary, then prepare (tile);
+      // stacked experts: one [N, K] weight after the other
       const int64_t groups = ceil_div(n, 128);
       DevBuf tmp;
       SM_TRY(ensure(tmp, (size_t)groups * 64 + (size_t)groups * 2 + 16));
@@ -375,8 +440,15 @@ extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float
       uint16_t* scales = (uint16_t*)(codes + groups * 64);
       int32_t* bad = (int32_t*)(codes + groups * 64 + groups * 2 + (groups * 2) % 4);
       SM_HIP(hipMemsetAsync(bad, 0, 4, st));
-      int s = sm_q4_quantize(src, SM_F32, n, codes, scales, bad, stream);
-      if (s == SM_OK) s = sm_q4_pack(codes, scales, lin->N, lin->K, lin->codes, lin->scales, stream);
+      const size_t cstride = (size_t)q4t_rows(lin->N) * (lin->K / 2);
+      const size_t sstride = (size_t)q4t_rows(lin->N) * (lin->K / 128);
+      int s = SM_OK;
+      for (int64_t e = 0; e < count && s == SM_OK; ++e) {
+        s = sm_q4_quantize(src + e * n, SM_F32, n, codes, scales, bad, stream);
+        if (s == SM_OK)
+          s = sm_q4_pack(codes, scales, lin->N, lin->K, lin->codes + e * cstride,
+                         lin->scales + e * sstride, stream);
+      }
       int32_t nbad = 0;
       if (s == SM_OK && hipMemcpyAsync(&nbad, bad, 4, hipMemcpyDeviceToHost, st) != hipSuccess)
         s = SM_ERR_HIP;
@@ -386,6 +458,7 @@ extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float
       SM_REQUIRE(nbad == 0, "%d Q4 groups have a scale outside the f16 normal range", nbad);
       return SM_OK;
     }
+    SM_REQUIRE(count == 1, "stacked expert weights need a quantized model");
     SM_HIP(hipMemcpyAsync(lin->w, src, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
     return SM_OK;
   }
@@ -403,30 +476,42 @@ extern "C" int sm_model_init_random(sm_model* m, uint64_t seed, float std, void*
   hipStream_t st = as_stream(stream);
   const auto& c = m->cfg;
   int64_t maxn = (int64_t)c.vocab * c.d_model;
-  for (const auto& Ly : m->layers)
+  for (const auto& Ly : m->layers) {
     for (const Linear* L : {&Ly.qkv, &Ly.o, &Ly.in, &Ly.down}) maxn = std::max(maxn, L->N * L->K);
+    for (const Linear* L : {&Ly.exp_in, &Ly.exp_down})
+      maxn = std::max(maxn, L->N * L->K * (int64_t)c.experts);
+  }
   DevBuf tmp;
   SM_TRY(ensure(tmp, (size_t)maxn * 4));
   auto fill_ones = [&](float* p) {
     fill_f32_kernel<<<blocks_for(c.d_model), 256, 0, st>>>(p, c.d_model, 1.0f);
   };
   uint64_t tid = 0;
-  auto randn = [&](int kind, int layer) -> int {
+  auto randn = [&](int kind, int layer, float sd) -> int {
     Linear* lin;
     void* dense;
-    int64_t n;
-    SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n));
-    SM_TRY(sm_fill_normal(tmp.p, SM_F32, n, 0.f, std, mix64(seed ^ (0x51ed27ull * ++tid)), stream));
+    int64_t n, count;
+    SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n, &count));
+    SM_TRY(sm_fill_normal(tmp.p, SM_F32, n * count, 0.f, sd, mix64(seed ^ (0x51ed27ull * ++tid)),
+                          stream));
     return sm_model_set_tensor(m, kind, layer, (const float*)tmp.p, stream);
   };
   auto body = [&]() -> int {
-    SM_TRY(randn(SM_W_EMBED, -1));
+    SM_TRY(randn(SM_W_EMBED, -1, std));
     fill_ones(m->final_norm);
-    SM_TRY(randn(SM_W_LM_HEAD, -1));
+    SM_TRY(randn(SM_W_LM_HEAD, -1, std));
     for (int l = 0; l < c.layers; ++l) {
       fill_ones(m->layers[l].attn_norm);
       fill_ones(m->layers[l].ffn_norm);
-      for (int k : {SM_W_QKV, SM_W_O, SM_W_IN, SM_W_DOWN}) SM_TRY(randn(k, l));
+      for (int k : {SM_W_QKV, SM_W_O}) SM_TRY(randn(k, l, std));
+      if (c.experts > 0) {
+        SM_TRY(randn(SM_W_ROUTER, l, 1.0f / std::sqrt((float)c.d_model)));
+        SM_TRY(randn(SM_W_EXPERT_IN, l, std));
+        SM_TRY(randn(SM_W_EXPERT_DOWN, l, std));
+      } else {
+        SM_TRY(randn(SM_W_IN, l, std));
+        SM_TRY(randn(SM_W_DOWN, l, std));
+      }
     }
     return SM_OK;
   };

@@ -1,0 +1,251 @@
+// Top-2 mixture-of-experts FFN on one GPU (config[4]).
+//
+// Semantics of SparseMoe::forward (summa-llm/src/model/ffn.rs:478-711):
+//   router logits = fp32 x . W_r (:489-490)
+//   top-2 indices, strict '>' scan so the first index wins ties
+//     (top2_indices_kernel, moe_topk.rs:74-104)
+//   route weights = softmax over the two selected logits (:514)
+//   routes r = t*k + j sorted stably by expert, inverse permutation
+//     (host_route_plan ffn.rs:888-929, stable_route_pack moe_route.rs:88-142)
+//   per-expert SwiGLU MLP on each expert's contiguous rows (forward_grouped_swiglu)
+//   out[t] = sum_j w[t,j] * routed[inverse[t*k+j]] (route_combine_forward,
+//     moe_dispatch.rs:290-312), added to the residual stream.
+//
+// MI355X design: no host round trip anywhere. The route plan (one workgroup,
+// deterministic stable counting sort) also emits two device tile lists
+// (16-row and 256-row tiles per expert), which the grouped Q4 matmuls consume
+// directly: the small-M kernel for decode (q4.hip) and the LDS kernel for
+// prefill / recompute (q4_gemm_lds.hip). The token gather is folded into the
+// first grouped matmul's A-operand addressing (row index = src_rows[p]), so
+// routed inputs are never materialised.
+#include <cmath>
+
+#include "common.hpp"
+#include "moe_plan.hpp"
+
+namespace sm {
+
+int64_t moe_max_tiles(int64_t routes, int64_t experts, int64_t rows) {
+  return ceil_div(routes, rows) + experts;
+}
+
+PlanView plan_view(int32_t* plan, int64_t routes, int64_t experts) {
+  PlanView v;
+  int32_t* p = plan;
+  v.counts = p; p += experts;
+  v.offsets = p; p += experts + 1;
+  v.order = p; p += routes;
+  v.inverse = p; p += routes;
+  v.src_rows = p; p += routes;
+  v.ntiles16 = p; p += 1;
+  v.tiles16 = p; p += 2 * moe_max_tiles(routes, experts, 16);
+  v.ntiles256 = p; p += 1;
+  v.tiles256 = p;
+  return v;
+}
+
+namespace {
+
+constexpr int kRouterThreads = 256;
+
+// One workgroup per token: h row -> LDS (f32), each wave computes its share of
+// the E router dot products (lanes over d, wave reduction), then one lane does
+// the strict top-2 scan and the softmax over the pair.
+template <typename TH>
+__global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
+    const TH* __restrict__ h, const float* __restrict__ wr, int d, int E,
+    float* __restrict__ logits_out, int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
+  extern __shared__ float smem[];
+  float* hs = smem;       // [d]
+  float* lg = smem + d;  // [E]
+  const int64_t t = blockIdx.x;
+  for (int c = threadIdx.x; c < d; c += kRouterThreads) {
+    if constexpr (sizeof(TH) == 2) hs[c] = (float)h[t * d + c];
+    else hs[c] = h[t * d + c];
+  }
+  __syncthreads();
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  for (int e = wave; e < E; e += kRouterThreads / kWave) {
+    float acc = 0.f;
+    for (int c = lane; c < d; c += kWave) acc = fmaf(hs[c], wr[(size_t)e * d + c], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) lg[e] = acc;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float v0 = -INFINITY, v1 = -INFINITY;
+    int i0 = 0, i1 = 0;
+    for (int e = 0; e < E; ++e) {
+      const float v = lg[e];
+      if (v > v0) { v1 = v0; i1 = i0; v0 = v; i0 = e; }
+      else if (v > v1) { v1 = v; i1 = e; }
+    }
+    // softmax over [v0, v1] (v0 >= v1)
+    const float e1 = expf(v1 - v0);
+    top_idx[t * 2] = i0;
+    top_idx[t * 2 + 1] = i1;
+    top_w[t * 2] = 1.f / (1.f + e1);
+    top_w[t * 2 + 1] = e1 / (1.f + e1);
+    if (logits_out)
+      for (int e = 0; e < E; ++e) logits_out[t * E + e] = lg[e];
+  }
+}
+
+// Stable counting sort of the routes by expert in one workgroup. Thread i owns
+// the contiguous route chunk [i*C, (i+1)*C); per-(thread, expert) counts live in
+// LDS, an exclusive scan over threads per expert gives each thread's write
+// base, and each thread then places its routes in order: the result equals the
+// reference's host plan (experts ascending, route ids ascending within one).
+constexpr int kPlanThreads = 128;
+constexpr int kMaxExperts = 64;
+
+__global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const int32_t* __restrict__ idx,
+                                                                  int routes, int k, int E,
+                                                                  PlanView pv, int max16,
+                                                                  int max256,
+                                                                  int32_t* __restrict__ error) {
+  __shared__ int32_t cnt[kPlanThreads][kMaxExperts + 1];
+  __shared__ int32_t offs[kMaxExperts + 1];
+  const int t = threadIdx.x;
+  const int C = (routes + kPlanThreads - 1) / kPlanThreads;
+  const int r0 = min(t * C, routes), r1 = min(r0 + C, routes);
+  for (int e = 0; e < E; ++e) cnt[t][e] = 0;
+  int bad = 0;
+  for (int r = r0; r < r1; ++r) {
+    const int e = idx[r];
+    if (e < 0 || e >= E) { bad = 1; continue; }
+    cnt[t][e] += 1;
+  }
+  if (bad) atomicOr(error, 1);
+  __syncthreads();
+  // per expert: exclusive scan over threads (thread e does expert e)
+  if (t < E) {
+    int run = 0;
+    for (int i = 0; i < kPlanThreads; ++i) {
+      const int c = cnt[i][t];
+      cnt[i][t] = run;
+      run += c;
+    }
+    pv.counts[t] = run;
+    offs[t] = run;  // total per expert, turned into offsets below
+  }
+  __syncthreads();
+  if (t == 0) {
+    int acc = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = offs[e];
+      offs[e] = acc;
+      pv.offsets[e] = acc;
+      acc += c;
+    }
+    offs[E] = acc;
+    pv.offsets[E] = acc;
+    // tile lists: (expert, first row) for 16- and 256-row tiles
+    int n16 = 0, n256 = 0;
+    for (int e = 0; e < E; ++e) {
+      const int c = offs[e + 1] - offs[e];
+      for (int r = 0; r < c && n16 < max16; r += 16, ++n16) {
+        pv.tiles16[2 * n16] = e;
+        pv.tiles16[2 * n16 + 1] = r;
+      }
+      for (int r = 0; r < c && n256 < max256; r += 256, ++n256) {
+        pv.tiles256[2 * n256] = e;
+        pv.tiles256[2 * n256 + 1] = r;
+      }
+    }
+    pv.ntiles16[0] = n16;
+    pv.ntiles256[0] = n256;
+  }
+  __syncthreads();
+  for (int r = r0; r < r1; ++r) {
+    const int e = idx[r];
+    if (e < 0 || e >= E) {
+      pv.inverse[r] = -1;  // flagged route: combine skips it
+      continue;
+    }
+    const int pos = offs[e] + cnt[t][e];
+    cnt[t][e] += 1;
+    pv.order[pos] = r;
+    pv.inverse[r] = pos;
+    pv.src_rows[pos] = r / k;
+  }
+}
+
+// x[t, c] += sum_j w[t, j] * routed[inverse[t*k + j], c]   (f32); routes the
+// plan flagged (inverse < 0) contribute nothing
+__global__ void combine_kernel(const float* __restrict__ routed, const float* __restrict__ w,
+                               const int32_t* __restrict__ inverse, int64_t tokens, int k, int d,
+                               float* __restrict__ x) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= tokens * d) return;
+  const int64_t t = i / d;
+  const int c = i % d;
+  const int64_t routes = tokens * k;
+  float sum = 0.f;
+  for (int j = 0; j < k; ++j) {
+    const int64_t route = t * k + j;
+    const int p = inverse[route];
+    if (p >= 0 && p < routes) sum += routed[(int64_t)p * d + c] * w[route];
+  }
+  x[i] += sum;
+}
+
+}  // namespace
+}  // namespace sm
+
+using namespace sm;
+
+extern "C" int64_t sm_moe_plan_words(int64_t tokens, int64_t top_k, int64_t experts) {
+  const int64_t routes = tokens * top_k;
+  return experts + (experts + 1) + 3 * routes + 1 + 2 * moe_max_tiles(routes, experts, 16) + 1 +
+         2 * moe_max_tiles(routes, experts, 256);
+}
+
+extern "C" int sm_moe_router_top2(const void* h, int h_dtype, const float* w_router,
+                                  int64_t tokens, int64_t d, int64_t experts, float* logits_out,
+                                  int32_t* top_idx, float* top_w, void* stream) {
+  SM_REQUIRE(h && w_router && top_idx && top_w, "sm_moe_router_top2: null buffer");
+  SM_REQUIRE(experts >= 2, "top-2 routing needs at least two experts");
+  SM_REQUIRE(tokens >= 0 && tokens <= 0x7fffffff && d > 0 && d <= 8192 && experts <= kMaxExperts,
+             "sm_moe_router_top2: bad shape (d <= 8192, experts <= %d)", kMaxExperts);
+  if (tokens == 0) return SM_OK;
+  const size_t shmem = (size_t)(d + experts) * sizeof(float);
+  if (h_dtype == SM_F16)
+    router_top2_kernel<_Float16><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
+        (const _Float16*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
+  else if (h_dtype == SM_F32)
+    router_top2_kernel<float><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
+        (const float*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
+  else SM_REQUIRE(false, "sm_moe_router_top2: h must be f16 or f32");
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_moe_route_plan(const int32_t* top_idx, int64_t tokens, int64_t top_k,
+                                 int64_t experts, int32_t* plan, int32_t* error, void* stream) {
+  SM_REQUIRE((top_idx || tokens == 0) && plan && error, "sm_moe_route_plan: null buffer");
+  SM_REQUIRE(experts >= 1 && experts <= kMaxExperts, "sm_moe_route_plan: experts must be <= %d",
+             kMaxExperts);
+  SM_REQUIRE(top_k >= 1 && tokens >= 0 && tokens * top_k <= 0x7fffffff,
+             "sm_moe_route_plan: bad shape");
+  const int64_t routes = tokens * top_k;
+  PlanView pv = plan_view(plan, routes, experts);
+  route_plan_kernel<<<1, kPlanThreads, 0, as_stream(stream)>>>(
+      top_idx, (int)routes, (int)top_k, (int)experts, pv,
+      (int)moe_max_tiles(routes, experts, 16), (int)moe_max_tiles(routes, experts, 256), error);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_moe_combine(const float* routed, const float* top_w, const int32_t* plan,
+                              int64_t tokens, int64_t top_k, int64_t experts, int64_t d, float* x,
+                              void* stream) {
+  SM_REQUIRE(routed && top_w && plan && x, "sm_moe_combine: null buffer");
+  SM_REQUIRE(tokens >= 0 && top_k >= 1 && d > 0, "sm_moe_combine: bad shape");
+  if (tokens == 0) return SM_OK;
+  PlanView pv = plan_view(const_cast<int32_t*>(plan), tokens * top_k, experts);
+  combine_kernel<<<(unsigned)ceil_div(tokens * d, 256), 256, 0, as_stream(stream)>>>(
+      routed, top_w, pv.inverse, tokens, (int)top_k, (int)d, x);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}

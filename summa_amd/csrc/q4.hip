@@ -34,6 +34,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "moe_plan.hpp"
 
 namespace sm {
 namespace {
@@ -67,6 +68,15 @@ struct Q4Args {
   int M, N, K;             // N = weight rows (for SWIGLU: 2F)
   int ldx, ldy;
   int ncols;               // logical output columns (N, or F for SWIGLU)
+  // Grouped (MoE) mode when tiles != nullptr: workgroup row tile y is tile
+  // (expert e, first row r) of the route plan; its rows are sorted positions
+  // goff[e] + r .. goff[e+1]-1, the A row of position p is rowidx[p] (or p),
+  // and expert e's weights start at codes + e*cstride, scales + e*sstride.
+  const int32_t* tiles = nullptr;
+  const int32_t* ntiles = nullptr;
+  const int32_t* goff = nullptr;
+  const int32_t* rowidx = nullptr;
+  size_t cstride = 0, sstride = 0;
 };
 
 // One workgroup = 16 rows (M tile) x its column tile. NB: 16-column blocks per
@@ -82,7 +92,18 @@ template <int NB, int KSPLIT, int EPI, bool XF16>
 __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
-  const int m0 = blockIdx.y * 16;
+  int m0 = blockIdx.y * 16;
+  int mlim = a.M;  // rows [m0, mlim) are valid for this workgroup
+  const uint8_t* codes = a.codes;
+  const uint16_t* scales = a.scales;
+  if (a.tiles) {
+    if ((int)blockIdx.y >= a.ntiles[0]) return;  // uniform per workgroup
+    const int e = a.tiles[2 * blockIdx.y];
+    m0 = a.goff[e] + a.tiles[2 * blockIdx.y + 1];
+    mlim = a.goff[e + 1];
+    codes += (size_t)e * a.cstride;
+    scales += (size_t)e * a.sstride;
+  }
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
   const int c0 = blockIdx.x * tile_cols + ((KSPLIT == 1) ? wave * wave_cols : 0);
@@ -103,8 +124,9 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   // All loads below are branch-free (clamped addresses, zeroed afterwards):
   // loads inside divergent branches make the compiler wait on each one, which
   // serialises the round trips this kernel exists to overlap.
-  const int arow = min(m0 + j, a.M - 1);  // activation row this lane feeds to the A operand
-  const bool arow_ok = m0 + j < a.M;
+  const int prow = min(m0 + j, mlim - 1);  // activation row this lane feeds to the A operand
+  const int arow = a.rowidx ? a.rowidx[prow] : prow;
+  const bool arow_ok = m0 + j < mlim;
   auto load_act = [&](int kg, h8 (&af)[4]) {
     const int kc = min(kg, ngroups - 1);
 #pragma unroll
@@ -136,8 +158,8 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         wv[u][b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
-            a.codes + q4t_code_offset(brow_c[b], kc, ngroups) + g * 16));
-        sraw[u][b] = a.scales[q4t_scale_index(brow_c[b], kc, ngroups)];
+            codes + q4t_code_offset(brow_c[b], kc, ngroups) + g * 16));
+        sraw[u][b] = scales[q4t_scale_index(brow_c[b], kc, ngroups)];
       }
     }
     // keep the whole batch of loads ahead of the math (the scheduler would
@@ -185,7 +207,7 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = m0 + 4 * g + r;
-    if (row >= a.M) continue;
+    if (row >= mlim) continue;
     if constexpr (is_swiglu(EPI)) {
 #pragma unroll
       for (int b = 0; b < NB / 2; ++b) {
@@ -214,11 +236,11 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
 }
 
 template <int NB, int KSPLIT, bool XF16>
-int launch_q4_x(const Q4Args& a, int epi, hipStream_t st) {
+int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
   const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
-  dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)ceil_div(a.M, 16));
+  dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)row_tiles);
   switch (epi) {
 #define SM_Q4_EPI(E) \
     case E: q4_gemm_kernel<NB, KSPLIT, E, XF16><<<grid, 256, 0, st>>>(a); break;
@@ -245,15 +267,17 @@ int launch_q4_x(const Q4Args& a, int epi, hipStream_t st) {
 }
 
 template <int NB, int KSPLIT>
-int launch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
-  return xf16 ? launch_q4_x<NB, KSPLIT, true>(a, epi, st)
-              : launch_q4_x<NB, KSPLIT, false>(a, epi, st);
+int launch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st, int64_t row_tiles) {
+  return xf16 ? launch_q4_x<NB, KSPLIT, true>(a, epi, st, row_tiles)
+              : launch_q4_x<NB, KSPLIT, false>(a, epi, st, row_tiles);
 }
 
 }  // namespace
 
 int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
-                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st);
+                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
+                const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
+                const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride);
 
 namespace {
 
@@ -266,19 +290,20 @@ int dispatch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
   const int64_t logical_cols = is_swiglu(epi) ? 2 * (int64_t)a.ncols : a.N;
   const bool ksplit_ok = a.K >= 4 * 128;
   if (a.M <= 256) {
+    const int64_t rt = ceil_div(a.M, 16);
     // GEMV-like M: 16-column wave tiles double the workgroup count (SwiGLU
     // needs gate/value block pairs, so it keeps 32).
     const bool narrow = a.M <= 16 && !is_swiglu(epi);
-    const int64_t wgs = ceil_div(logical_cols, narrow ? 64 : 128) * ceil_div(a.M, 16);
+    const int64_t wgs = ceil_div(logical_cols, narrow ? 64 : 128) * rt;
     if (narrow) {
-      if (wgs < 512 && ksplit_ok) return launch_q4<1, 4>(a, epi, xf16, st);
-      return launch_q4<1, 1>(a, epi, xf16, st);
+      if (wgs < 512 && ksplit_ok) return launch_q4<1, 4>(a, epi, xf16, st, rt);
+      return launch_q4<1, 1>(a, epi, xf16, st, rt);
     }
-    if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xf16, st);
-    return launch_q4<2, 1>(a, epi, xf16, st);
+    if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xf16, st, rt);
+    return launch_q4<2, 1>(a, epi, xf16, st, rt);
   }
   return q4_gemm_lds(a.codes, a.scales, a.N, a.K, a.x, xf16, a.M, a.ldx, a.y, a.ldy, epi,
-                     a.ncols, st);
+                     a.ncols, st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0);
 }
 
 // ----------------------------------------------------------- quantizer ---
@@ -406,4 +431,44 @@ extern "C" int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_
   if (M == 0) return SM_OK;
   Q4Args a{codes, scales, x, y, (int)M, (int)N, (int)K, (int)ldx, (int)ldy, (int)ncols};
   return dispatch_q4(a, epilogue, x_dtype == SM_F16, as_stream(stream));
+}
+
+extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts,
+                                    int64_t N, int64_t K, const void* x, int x_dtype, int64_t ldx,
+                                    int gather, const int32_t* plan, int64_t tokens, int64_t top_k,
+                                    void* y, int64_t ldy, int epilogue, void* stream) {
+  using namespace sm;
+  SM_REQUIRE(codes && scales && x && plan && y, "sm_q4_grouped_matmul: null buffer");
+  SM_REQUIRE(experts >= 1 && K > 0 && K % 128 == 0 && N > 0,
+             "sm_q4_grouped_matmul: K must be a positive multiple of 128");
+  SM_REQUIRE(x_dtype == SM_BF16 || x_dtype == SM_F16, "sm_q4_grouped_matmul: x must be bf16/f16");
+  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16 && epilogue != EPI_ADD_F32,
+             "sm_q4_grouped_matmul: epilogue must store (f32/bf16) or SwiGLU");
+  SM_REQUIRE(ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
+             "sm_q4_grouped_matmul: x must be 16-byte aligned rows");
+  const int64_t routes = tokens * top_k;
+  if (routes == 0) return SM_OK;
+  const int64_t ncols = is_swiglu(epilogue) ? N / 2 : N;
+  PlanView pv = plan_view(const_cast<int32_t*>(plan), routes, experts);
+  const size_t cstride = (size_t)q4t_rows(N) * (K / 2), sstride = (size_t)q4t_rows(N) * (K / 128);
+  const int32_t* rowidx = gather ? pv.src_rows : nullptr;
+  hipStream_t st = as_stream(stream);
+  if (routes <= 4096) {
+    Q4Args a{codes, scales, x, y, (int)routes, (int)N, (int)K, (int)ldx, (int)ldy, (int)ncols};
+    a.tiles = pv.tiles16;
+    a.ntiles = pv.ntiles16;
+    a.goff = pv.offsets;
+    a.rowidx = rowidx;
+    a.cstride = cstride;
+    a.sstride = sstride;
+    const int64_t rt = moe_max_tiles(routes, experts, 16);
+    if (is_swiglu(epilogue) || K < 4 * 128)
+      return x_dtype == SM_F16 ? launch_q4_x<2, 1, true>(a, epilogue, st, rt)
+                               : launch_q4_x<2, 1, false>(a, epilogue, st, rt);
+    return x_dtype == SM_F16 ? launch_q4_x<2, 4, true>(a, epilogue, st, rt)
+                             : launch_q4_x<2, 4, false>(a, epilogue, st, rt);
+  }
+  return q4_gemm_lds(codes, scales, (int)N, (int)K, x, x_dtype == SM_F16, (int)routes, (int)ldx,
+                     y, (int)ldy, epilogue, (int)ncols, st, pv.tiles256, pv.ntiles256,
+                     moe_max_tiles(routes, experts, 256), pv.offsets, rowidx, cstride, sstride);
 }

@@ -41,6 +41,12 @@ struct Args {
   void* y;
   int M, N, K, ldx, ldy, ncols;
   int mtiles8, ntiles;  // M tiles rounded up to a multiple of 8; N tiles
+  // grouped (MoE) mode when tiles != nullptr (see Q4Args in q4.hip)
+  const int32_t* tiles;
+  const int32_t* ntiles_dev;
+  const int32_t* goff;
+  const int32_t* rowidx;
+  size_t cstride, sstride;
 };
 
 // EPI: 0 store f32, 1 store bf16, 2 add f32, 3 swiglu bf16, 4 swiglu f16.
@@ -49,13 +55,28 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
   constexpr bool SWIGLU = (EPI == 3 || EPI == 4);
   __shared__ __attribute__((aligned(16))) _Float16 As[kTM * kAP];
 
-  // XCD-aware tile order (see header).
-  const int w = blockIdx.x;
-  const int xcd = w % 8, q = w / 8;
-  const int tn = q % a.ntiles;
-  const int tm = (q / a.ntiles) * 8 + xcd;
-  const int m_base = tm * kTM;
-  if (m_base >= a.M) return;  // padding tile (uniform per workgroup)
+  int tn, m_base, mlim = a.M;
+  const uint8_t* codes = a.codes;
+  const uint16_t* scales = a.scales;
+  if (a.tiles) {
+    // grouped: workgroup = (route-plan tile, N tile)
+    tn = blockIdx.x % a.ntiles;
+    const int ti = blockIdx.x / a.ntiles;
+    if (ti >= a.ntiles_dev[0]) return;  // uniform per workgroup
+    const int e = a.tiles[2 * ti];
+    m_base = a.goff[e] + a.tiles[2 * ti + 1];
+    mlim = a.goff[e + 1];
+    codes += (size_t)e * a.cstride;
+    scales += (size_t)e * a.sstride;
+  } else {
+    // XCD-aware tile order (see header).
+    const int w = blockIdx.x;
+    const int xcd = w % 8, q = w / 8;
+    tn = q % a.ntiles;
+    const int tm = (q / a.ntiles) * 8 + xcd;
+    m_base = tm * kTM;
+    if (m_base >= a.M) return;  // padding tile (uniform per workgroup)
+  }
 
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
@@ -92,8 +113,8 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
     for (int b = 0; b < kNB; ++b) {
       const int rr = brow[b] >= 0 ? brow[b] : 0;
       wv[b] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4*>(a.codes + q4t_code_offset(rr, kg, ngroups) + g * 16));
-      sraw[b] = a.scales[q4t_scale_index(rr, kg, ngroups)];
+          reinterpret_cast<const u32x4*>(codes + q4t_code_offset(rr, kg, ngroups) + g * 16));
+      sraw[b] = scales[q4t_scale_index(rr, kg, ngroups)];
     }
     __builtin_amdgcn_sched_barrier(0);
     __syncthreads();  // previous group's A fully consumed
@@ -101,7 +122,8 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
 #pragma unroll 2
     for (int c = threadIdx.x; c < kTM * 16; c += 256) {
       const int r = c / 16, ch = c % 16;
-      const int row = min(m_base + r, a.M - 1);
+      const int prow = min(m_base + r, mlim - 1);
+      const int row = a.rowidx ? a.rowidx[prow] : prow;
       const size_t xo = (size_t)row * a.ldx + kg * 128 + ch * 8;
       h8 v;
       if constexpr (XF16) {
@@ -112,7 +134,7 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
                (_Float16)bf16hi(u.y), (_Float16)bf16lo(u.z), (_Float16)bf16hi(u.z),
                (_Float16)bf16lo(u.w), (_Float16)bf16hi(u.w)};
       }
-      if (m_base + r >= a.M) v = h8{0, 0, 0, 0, 0, 0, 0, 0};
+      if (m_base + r >= mlim) v = h8{0, 0, 0, 0, 0, 0, 0, 0};
       *reinterpret_cast<h8*>(&As[r * kAP + ch * 8]) = v;
     }
     __syncthreads();
@@ -141,7 +163,7 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = m_base + wm * 128 + mt * 16 + 4 * g + r;
-      if (row >= a.M) continue;
+      if (row >= mlim) continue;
       if constexpr (SWIGLU) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
@@ -172,12 +194,15 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
 
 // Called by sm_q4_matmul for M > 256 (argument checks done there).
 int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
-                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st) {
-  Args a{codes, scales, x, y, M, N, K, ldx, ldy, ncols, 0, 0};
+                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
+                const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
+                const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride) {
+  Args a{codes, scales, x, y, M, N, K, ldx, ldy, ncols, 0, 0,
+         tiles, ntiles, goff, rowidx, cstride, sstride};
   const int logical_cols = (epi == 3 || epi == 4) ? 2 * ncols : N;
   a.ntiles = (int)ceil_div(logical_cols, kTN);
   a.mtiles8 = (int)ceil_div(ceil_div(M, kTM), 8) * 8;
-  const int64_t blocks = (int64_t)a.mtiles8 * a.ntiles;
+  const int64_t blocks = (int64_t)(tiles ? max_tiles : a.mtiles8) * a.ntiles;
   if (blocks > 0x7fffffff) {
     set_error("sm_q4_matmul: problem too large");
     return SM_ERR_UNSUPPORTED;

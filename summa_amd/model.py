@@ -17,13 +17,15 @@ from ._lib import call
 
 # tensor kinds (include/summa_amd.h SM_W_*)
 KIND = {"embed": 0, "attn_norm": 1, "qkv": 2, "o": 3, "ffn_norm": 4, "in": 5, "down": 6,
-        "final_norm": 7, "lm_head": 8}
+        "final_norm": 7, "lm_head": 8, "router": 9, "exp_in": 10, "exp_down": 11}
+PER_LAYER = ("attn_norm", "ffn_norm", "qkv", "o", "in", "down", "router", "exp_in", "exp_down")
 
 
 class ModelConfigC(C.Structure):
     _fields_ = [(n, C.c_int32) for n in ("layers", "d_model", "heads", "kv_heads", "head_dim",
                                          "ffn", "vocab", "max_seq")] + \
-        [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("quantized", C.c_int32)]
+        [("norm_eps", C.c_float), ("rope_theta", C.c_float), ("quantized", C.c_int32),
+         ("experts", C.c_int32), ("expert_ffn", C.c_int32)]
 
 
 @dataclass
@@ -40,16 +42,21 @@ class ModelConfig:
     quantized: bool
     norm_eps: float = 1e-5
     rope_theta: float = 1e4
+    experts: int = 0
+    expert_ffn: int = 0
 
     def c(self) -> ModelConfigC:
         return ModelConfigC(self.layers, self.d_model, self.heads, self.kv_heads, self.head_dim,
                             self.ffn, self.vocab, self.max_seq, self.norm_eps, self.rope_theta,
-                            int(self.quantized))
+                            int(self.quantized), self.experts, self.expert_ffn)
 
     def oracle_cfg(self) -> dict:
-        return {"layers": self.layers, "d": self.d_model, "H": self.heads, "KVH": self.kv_heads,
-                "hd": self.head_dim, "F": self.ffn, "V": self.vocab, "eps": self.norm_eps,
-                "theta": self.rope_theta}
+        cfg = {"layers": self.layers, "d": self.d_model, "H": self.heads, "KVH": self.kv_heads,
+               "hd": self.head_dim, "F": self.ffn, "V": self.vocab, "eps": self.norm_eps,
+               "theta": self.rope_theta}
+        if self.experts:
+            cfg.update(E=self.experts, Fe=self.expert_ffn)
+        return cfg
 
 
 def _stream() -> int:
@@ -93,7 +100,7 @@ class Model:
         """weights as produced by ``oracle.random_weights`` style dicts (numpy)."""
         for name, arr in weights.items():
             t = torch.from_numpy(arr).to(device)
-            if name in ("attn_norm", "ffn_norm", "qkv", "o", "in", "down"):
+            if name in PER_LAYER:
                 for layer in range(self.cfg.layers):
                     self.set_tensor(name, t[layer], layer)
             else:

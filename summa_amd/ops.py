@@ -228,3 +228,122 @@ def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
     call("sm_q4_matmul", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k, x.data_ptr(), _dt(x),
          M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
     return out
+
+
+# ------------------------------------------------------------------ MoE ---
+
+class ExpertBank:
+    """Stacked Q4G128 expert weights W_e[N, K], e < E, resident in HBM.
+
+    Counterpart of ``ExpertBank`` (summa-llm/src/model/ffn.rs:146-217, stacked
+    ``[E, d, 2F]`` / ``[E, F, d]``) in this build's [out, in] Q4 layout: each
+    expert is quantized as its own tensor and stored in the prepared tiled
+    layout, expert e at a fixed stride."""
+
+    def __init__(self, experts: list[Q4Weight]):
+        if not experts:
+            raise ValueError("an expert bank needs at least one expert")
+        n, k = experts[0].n, experts[0].k
+        if any(e.n != n or e.k != k for e in experts):
+            raise ValueError("experts must share one shape")
+        if experts[0].tcodes is None:
+            raise ValueError(f"grouped Q4 matmul needs K % 128 == 0 (K={k})")
+        self.n, self.k, self.experts = n, k, len(experts)
+        self.tcodes = torch.stack([e.tcodes for e in experts]).contiguous()
+        self.tscales = torch.stack([e.tscales for e in experts]).contiguous()
+
+    @classmethod
+    def quantize(cls, w: torch.Tensor) -> "ExpertBank":
+        """Quantize dense device experts [E, N, K]."""
+        return cls([Q4Weight.quantize(w[e].contiguous()) for e in range(w.shape[0])])
+
+
+class RoutePlan:
+    """Device route plan of ``route_plan`` (summa-llm/src/model/moe_route.rs:22,
+    kernels :61-142): routes r = t*top_k + j sorted stably by expert. Views:
+    counts [E], offsets [E+1], order [R] (route id at each sorted position),
+    inverse [R] (sorted position of each route), src_rows [R] (token of each
+    sorted position)."""
+
+    def __init__(self, words: torch.Tensor, tokens: int, top_k: int, experts: int,
+                 error: torch.Tensor):
+        self.words, self.tokens, self.top_k, self.experts, self.error = (
+            words, tokens, top_k, experts, error)
+        R, E = tokens * top_k, experts
+        o = [0]
+        for n in (E, E + 1, R, R, R):
+            o.append(o[-1] + n)
+        self.counts, self.offsets, self.order, self.inverse, self.src_rows = (
+            words[o[i]:o[i + 1]] for i in range(5))
+
+
+def moe_top2_indices(h: torch.Tensor, router: torch.Tensor, *, want_logits: bool = False):
+    """Router logits (fp32 h . W_r^T, ffn.rs:489-490), strict top-2 with the
+    first index winning ties (moe_topk.rs:74-104) and the softmax over the
+    selected pair (ffn.rs:514). h [T, d] f32/f16, router [E, d] f32.
+    Returns (top_idx [T, 2] int32, top_w [T, 2] f32, logits [T, E] or None)."""
+    _dev(h, "h")
+    _dev(router, "router")
+    T, d = h.shape
+    E = router.shape[0]
+    if router.dtype != torch.float32 or router.shape[1] != d:
+        raise ValueError("router must be f32 [experts, d]")
+    idx = torch.empty((T, 2), dtype=torch.int32, device=h.device)
+    wts = torch.empty((T, 2), dtype=torch.float32, device=h.device)
+    logits = torch.empty((T, E), dtype=torch.float32, device=h.device) if want_logits else None
+    call("sm_moe_router_top2", h.data_ptr(), _dt(h), router.data_ptr(), T, d, E, _p(logits),
+         idx.data_ptr(), wts.data_ptr(), _stream())
+    return idx, wts, logits
+
+
+def moe_route_plan(top_idx: torch.Tensor, experts: int) -> RoutePlan:
+    """Stable expert-major route plan of top_idx [T, k] (moe_route.rs:22)."""
+    _dev(top_idx, "top_idx")
+    if top_idx.dtype != torch.int32:
+        raise TypeError("top_idx must be int32")
+    T, k = top_idx.shape
+    words = torch.empty(int(_lib.lib().sm_moe_plan_words(T, k, experts)), dtype=torch.int32,
+                        device=top_idx.device)
+    error = torch.zeros(1, dtype=torch.int32, device=top_idx.device)
+    call("sm_moe_route_plan", top_idx.data_ptr(), T, k, experts, words.data_ptr(),
+         error.data_ptr(), _stream())
+    return RoutePlan(words, T, k, experts, error)
+
+
+def grouped_q4_matmul(bank: ExpertBank, x: torch.Tensor, plan: RoutePlan, *, gather: bool,
+                      epilogue: int = _lib.SM_EPI_STORE_F32) -> torch.Tensor:
+    """Per-expert y[p] = x[row(p)] . W_e^T over the plan's sorted positions p
+    (grouped_linear.rs:65 / forward_grouped_swiglu ffn.rs:321). With ``gather``
+    row(p) = src_rows[p] (the token; route_gather folded in), else row(p) = p."""
+    _dev(x, "x")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise TypeError("x must be bfloat16 or float16")
+    if x.shape[1] != bank.k:
+        raise ValueError(f"grouped linear input width mismatch ({x.shape[1]} != {bank.k})")
+    R = plan.tokens * plan.top_k
+    if epilogue == _lib.SM_EPI_SWIGLU_F16:
+        shape, dt = (R, bank.n // 2), torch.float16
+    elif epilogue == _lib.SM_EPI_SWIGLU_BF16:
+        shape, dt = (R, bank.n // 2), torch.bfloat16
+    elif epilogue == _lib.SM_EPI_STORE_BF16:
+        shape, dt = (R, bank.n), torch.bfloat16
+    else:
+        shape, dt = (R, bank.n), torch.float32
+    out = torch.empty(shape, dtype=dt, device=x.device)
+    call("sm_q4_grouped_matmul", bank.tcodes.data_ptr(), bank.tscales.data_ptr(), bank.experts,
+         bank.n, bank.k, x.data_ptr(), _dt(x), x.stride(0), int(gather), plan.words.data_ptr(),
+         plan.tokens, plan.top_k, out.data_ptr(), out.stride(0), int(epilogue), _stream())
+    return out
+
+
+def moe_route_combine(routed: torch.Tensor, top_w: torch.Tensor, plan: RoutePlan,
+                      x: torch.Tensor) -> torch.Tensor:
+    """x[t] += sum_j top_w[t, j] * routed[inverse[t*k + j]] in f32
+    (route_combine_forward, moe_dispatch.rs:290-312), in place on x."""
+    for t, n in ((routed, "routed"), (top_w, "top_w"), (x, "x")):
+        _dev(t, n)
+        if t.dtype != torch.float32:
+            raise TypeError(f"{n} must be float32")
+    call("sm_moe_combine", routed.data_ptr(), top_w.data_ptr(), plan.words.data_ptr(),
+         plan.tokens, plan.top_k, plan.experts, x.shape[1], x.data_ptr(), _stream())
+    return x

@@ -51,10 +51,35 @@ def _np_forward(cfg, w, ids):
         att = np.einsum("shlt,sthd->slhd", p, v).reshape(S, L, H * hd)
         x = x + att @ w["o"][l].T
         h = norm(x, w["ffn_norm"][l])
+        if cfg.get("E"):
+            x = x + _np_moe(cfg, w, l, h)
+            continue
         gv = h @ w["in"][l].T
         g, val = gv[..., :F], gv[..., F:]
         x = x + (g / (1 + np.exp(-g)) * val) @ w["down"][l].T
     return norm(x, w["final_norm"]) @ w["lm_head"].T
+
+
+def _np_moe(cfg, w, l, h):
+    """Top-2 MoE of SparseMoe::forward (ffn.rs:478-711) in f64: general CPU
+    top-k (stable argsort: on equal logits the lower expert index ranks first,
+    as the strict '>' scan of moe_topk.rs:74-104), softmax over the pair."""
+    Fe = cfg["Fe"]
+    lead = h.shape[:-1]
+    h2 = h.reshape(-1, h.shape[-1])
+    logits = h2 @ w["router"][l].T.astype(np.float64)
+    top = np.argsort(-logits, axis=1, kind="stable")[:, :2]
+    sel = np.take_along_axis(logits, top, 1)
+    wts = np.exp(sel - sel[:, :1])
+    wts /= wts.sum(1, keepdims=True)
+    out = np.zeros_like(h2)
+    for t in range(h2.shape[0]):
+        for j in range(2):
+            e = top[t, j]
+            gv = w["exp_in"][l, e].astype(np.float64) @ h2[t]
+            u = gv[:Fe] / (1 + np.exp(-gv[:Fe])) * gv[Fe:]
+            out[t] += wts[t, j] * (w["exp_down"][l, e].astype(np.float64) @ u)
+    return out.reshape(*lead, -1)
 
 
 def test_forward_matches_independent_numpy():
@@ -65,6 +90,48 @@ def test_forward_matches_independent_numpy():
     got = m.forward_logits(ids)
     ref = _np_forward(TINY, w, ids)
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-5)
+
+
+TINY_MOE = dict(TINY, E=6, Fe=48)
+
+
+def test_moe_forward_matches_independent_numpy():
+    w = oracle.random_weights(TINY_MOE, seed=11, std=0.2)
+    m = oracle.HostModel(TINY_MOE, w, quantized=False)
+    ids = np.random.default_rng(12).integers(0, TINY["V"], (2, 9)).astype(np.int32)
+    gaps = m.router_gaps(ids)
+    assert gaps.min() > 1e-3  # no top-2 near-tie, so f32 vs f64 picks the same experts
+    np.testing.assert_allclose(m.forward_logits(ids), _np_forward(TINY_MOE, w, ids),
+                               rtol=1e-4, atol=1e-5)
+
+
+def test_moe_router_ties_pick_lowest_index():
+    # Router rows built so logits tie exactly: e0 = 3z, e1 = e4 = z, others -z
+    # with z = h.r. For z > 0 experts 1 and 4 tie for second place and the
+    # strict '>' scan keeps expert 1; for z < 0 experts 2, 3, 5 tie and 2, 3 win.
+    # Expert 4 and 5 are therefore never used: their weights must not matter.
+    cfg = dict(TINY_MOE, layers=1)
+    w = oracle.random_weights(cfg, seed=13, std=0.2)
+    r = np.random.default_rng(17).normal(0, 0.2, cfg["d"]).astype(np.float32)
+    w["router"][0] = np.stack([3 * r, r, -r, -r, r, -r])
+    ids = np.random.default_rng(14).integers(0, cfg["V"], (2, 7)).astype(np.int32)
+    base = oracle.HostModel(cfg, w, quantized=False).forward_logits(ids)
+    np.testing.assert_allclose(base, _np_forward(cfg, w, ids), rtol=1e-4, atol=1e-5)
+    w2 = {k: v.copy() for k, v in w.items()}
+    w2["exp_in"][0, 4] = w2["exp_in"][0, 0]
+    w2["exp_down"][0, 5] *= -3.0
+    np.testing.assert_array_equal(base, oracle.HostModel(cfg, w2, quantized=False).forward_logits(ids))
+    w3 = {k: v.copy() for k, v in w.items()}
+    w3["exp_down"][0, 1] *= -3.0  # expert 1 is used by the tokens with z > 0
+    assert np.abs(oracle.HostModel(cfg, w3, quantized=False).forward_logits(ids) - base).max() > 1e-3
+
+
+def test_moe_cached_decode_equals_stateless_forward():
+    w = oracle.random_weights(TINY_MOE, seed=15, std=0.2)
+    m = oracle.HostModel(TINY_MOE, w, quantized=False)
+    prompts = np.random.default_rng(16).integers(0, TINY["V"], (2, 5)).astype(np.int32)
+    tok, lp_gen = m.generate(prompts, 6, temperature=0.0)
+    np.testing.assert_allclose(lp_gen, m.logprobs(prompts, tok), atol=1e-5)
 
 
 def test_cached_decode_equals_stateless_forward():
@@ -136,3 +203,21 @@ def test_quantized_oracle_close_to_dequantized_f32():
     a, b = q.forward_logits(ids), f.forward_logits(ids)
     assert np.abs(a - b).max() < 2e-2 * max(1.0, np.abs(b).max())
     assert np.abs(a - b).max() > 0  # bf16 rounding points are really applied
+
+
+def test_moe_quantized_oracle_close_to_dequantized_f32():
+    # per-expert Q4G128 packing: decoding each expert's codes gives the f32
+    # model the quantized MoE path approximates (f16 activation rounding only)
+    cfg = dict(TINY_MOE, d=128, Fe=128, hd=32, H=4, KVH=4)
+    w = oracle.random_weights(cfg, seed=18, std=0.05)
+    q = oracle.HostModel(cfg, w, quantized=True)
+    wd = dict(w)
+    for k in ("qkv", "o", "lm_head", "exp_in", "exp_down"):
+        codes, scales = q.packed[k]
+        wd[k] = oracle.q4_decode(codes, scales, w[k].size).reshape(w[k].shape)
+    wd["embed"] = oracle.round_bf16(w["embed"])
+    f = oracle.HostModel(cfg, wd, quantized=False)
+    ids = np.random.default_rng(19).integers(0, cfg["V"], (2, 9)).astype(np.int32)
+    assert min(q.router_gaps(ids).min(), f.router_gaps(ids).min()) > 1e-2
+    a, b = q.forward_logits(ids), f.forward_logits(ids)
+    assert 0 < np.abs(a - b).max() < 2e-2 * max(1.0, np.abs(b).max())
