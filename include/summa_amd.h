@@ -29,7 +29,12 @@ typedef enum sm_status {
   SM_ERR_NUMERIC = -4      /* device-side validation failed (non-finite, ratio > 80, ...) */
 } sm_status;
 
-typedef enum sm_dtype { SM_F32 = 0, SM_BF16 = 1, SM_F16 = 2 } sm_dtype;
+/* SM_F16X2: an f16 pair carrying an fp32-grade activation. A row of K values
+ * holds K f16 "hi" values followed by K f16 "lo" values, x = hi + lo with
+ * hi = f16(x), lo = f16(x - hi) (about 22 significant bits); the row stride
+ * (ldx / ldy) counts f16 elements and is >= 2K. Matmul inputs of quantized
+ * models use it so the f16 MFMA path keeps fp32-level activation precision. */
+typedef enum sm_dtype { SM_F32 = 0, SM_BF16 = 1, SM_F16 = 2, SM_F16X2 = 3 } sm_dtype;
 
 /* Library identity / diagnostics. */
 int sm_version(void);
@@ -121,7 +126,8 @@ int sm_q4_pack(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t 
                uint8_t* tiled_codes, uint16_t* tiled_scales, void* stream);
 
 /* y = x . W^T over Q4G128 weights in the prepared layout (sm_q4_pack), x [M,
- * ldx] bf16 or f16 (x_dtype), f32 accumulate. Replaces
+ * ldx] bf16, f16 or f16 pairs (x_dtype SM_F16X2: two f16 MFMAs per step, hi
+ * and lo), f32 accumulate. Replaces
  * the quantized-matmul dispatch: PackedTensor::matrix_vector
  * (quantization.rs:630-654) batched over M rows, i.e. Linear::forward
  * (summa-llm/src/model/matmul.rs:57-66) on a QuantizedModelBackend weight
@@ -132,13 +138,16 @@ int sm_q4_pack(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t 
  *   SM_EPI_SWIGLU_BF16 W rows are [gate | value] (N = 2F); y bf16 [M, F] =
  *                      silu(gate) * value (ffn.rs:854-877, fused_swiglu.rs:110-126)
  *   SM_EPI_SWIGLU_F16  same with f16 output
+ *   SM_EPI_SWIGLU_F16X2 same as an SM_F16X2 row: hi at [m, j], lo at [m, F + j]
+ *                      (ldy >= 2F)
  */
 enum {
   SM_EPI_STORE_F32 = 0,
   SM_EPI_STORE_BF16 = 1,
   SM_EPI_ADD_F32 = 2,
   SM_EPI_SWIGLU_BF16 = 3,
-  SM_EPI_SWIGLU_F16 = 4
+  SM_EPI_SWIGLU_F16 = 4,
+  SM_EPI_SWIGLU_F16X2 = 5
 };
 int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
                  const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
@@ -159,7 +168,8 @@ int sm_swiglu_f32(const float* gate_value, int64_t rows, int64_t F, float* out, 
  *   (Norm::forward, summa-llm/src/model/norm.rs:36-50), y in out_dtype
  *   (SM_F32, SM_BF16 or SM_F16).
  * sm_rope_append: qkv [S*L, (H+2KVH)*hd] f32 -> q_out [S*L, H, hd] with RoPE,
- *   K (RoPE) and V written to caches [S, KVH, cap, hd] at position pos0[s]+i
+ *   K (RoPE) and V written to caches [S, KVH, cap, hd] at position pos0[s]+i;
+ *   q_dtype / cache_dtype: (f32, f32), (f32 or bf16, bf16) or (f16, f16)
  *   (project_qkv + AttnCache slice_assign, attention.rs:142-177, 331-356).
  *   rope_table [max_pos, hd/2, 2] f32 (cos, sin), adjacent-pair convention.
  */
@@ -179,8 +189,9 @@ int sm_rope_append(const float* qkv, const float* rope_table, const int32_t* pos
  * sm_attn_prefill: causal, q/out [S, L, H, hd], row i at position pos0[s]+i
  *   attends keys 0..=pos0[s]+i (fused_attention / CubeK flash forward,
  *   attention.rs:250, cube_attention.rs:127-220).
- * dtype (q and cache) SM_BF16 (MFMA kernels, out_dtype SM_BF16 or SM_F16) or
- * SM_F32 (VALU, out_dtype SM_F32); head_dim 64 or 128.
+ * dtype (q and cache) SM_BF16 or SM_F16 (MFMA kernels; out_dtype SM_BF16,
+ * SM_F16 or SM_F16X2 rows of 2*H*hd f16) or SM_F32 (VALU, out_dtype SM_F32);
+ * head_dim 64 or 128.
  */
 int sm_attn_decode(const void* q, const void* kcache, const void* vcache, const int32_t* lens,
                    void* out, int dtype, int out_dtype, int64_t S, int64_t H, int64_t KVH,
@@ -206,7 +217,7 @@ int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab, floa
  * sm_moe_router_top2: logits = f32 h . W_r^T (W_r [E, d] f32), top-2 with a
  *   strict '>' scan (top2_indices_kernel, moe_topk.rs:74-104), weights =
  *   softmax over the pair. top_idx/top_w [tokens, 2]; logits_out nullable.
- *   h f32 or f16 [tokens, d], d <= 8192, 2 <= E <= 64.
+ *   h f32, f16 or f16 pairs [tokens, d], d <= 8192, 2 <= E <= 64.
  * sm_moe_route_plan: stable sort of routes r = t*k + j by expert
  *   (host_route_plan ffn.rs:888-929 / route_plan moe_route.rs:22-142) into the
  *   int32 `plan` buffer of sm_moe_plan_words() words: counts[E],
@@ -220,7 +231,8 @@ int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab, floa
  *   [N, K]; A row p = x[src_rows[p]] when gather != 0 (the token gather,
  *   route_gather moe_dispatch.rs:57, folded into the matmul) else x[p]
  *   (grouped_linear / grouped_swiglu_mlp, grouped_linear.rs:65-104).
- *   Epilogues: SM_EPI_STORE_F32/BF16 or SM_EPI_SWIGLU_BF16/F16.
+ *   Epilogues: SM_EPI_STORE_F32/BF16 or SM_EPI_SWIGLU_BF16/F16/F16X2; x
+ *   bf16, f16 or f16 pairs.
  * sm_moe_combine: x[t] += sum_j top_w[t,j] * routed[inverse[t*k+j]] (f32)
  *   (route_combine_forward, moe_dispatch.rs:290-312).
  */

@@ -12,14 +12,14 @@
  *   final norm + head     transformer.rs:802-909
  *   generation            summa-llm/src/generate.rs:53-250
  *   log-prob recompute    summa-train/src/tensor_sleep.rs:2531-2689
- * with the build's precision policy for quantized models: values rounded to
- * f16 where the device feeds a matmul (norm outputs, attention output, SwiGLU
- * output), to bf16 where it stores bf16 (q, k, v, embedding), fp32 everywhere
- * else. Matmul dot products accumulate sequentially in fp32 (the order
- * PackedTensor::matrix_vector uses, quantization.rs:642-651) or, with acc64,
- * in f64: with 16-bit activations any fp32 summation order moves per-token
- * log-probs by up to ~1e-3 at d=2048, so the quantized parity checks compare
- * the device against the exactly-accumulated value of the same products.
+ * in fp32, as the reference's CPU path computes, with one storage rounding
+ * for quantized models: q, k and v are rounded to f16 (the device's 16-bit KV
+ * cache and query); the embedding table is bf16 (rounded by the caller). The
+ * device keeps matmul inputs at fp32-grade precision (f16 hi + lo pairs), so
+ * no activation rounding is modelled here. Matmul dot products accumulate
+ * sequentially in fp32 (the order PackedTensor::matrix_vector uses,
+ * quantization.rs:642-651) or, with acc64, in f64, the exactly-accumulated
+ * value the quantized parity checks compare against.
  */
 #include <math.h>
 #include <stdint.h>
@@ -52,14 +52,8 @@ typedef struct or_model {
   float* router_gap;
 } or_model;
 
-/* bf16 rounding: q, k, v (KV cache) and the embedding of quantized models. */
-static float rb(const or_model* m, float v) {
-  return m->quantized ? or_bf16_to_f32(or_f32_to_bf16(v)) : v;
-}
-
-/* f16 rounding: matmul-input activations (norm outputs, attention output,
- * SwiGLU output) of quantized models. */
-static float rh(const or_model* m, float v) { return m->quantized ? or_round_f16(v) : v; }
+/* f16 rounding of q, k and v (the 16-bit KV cache) of quantized models. */
+static float rkv(const or_model* m, float v) { return m->quantized ? or_round_f16(v) : v; }
 
 static float q4_at(const uint8_t* codes, const uint16_t* scales, int64_t i) {
   const uint8_t byte = codes[i / 2];
@@ -114,8 +108,6 @@ static void linear(const or_model* m, int kind, int layer, const float* x, int64
   }
 }
 
-static float rh(const or_model* m, float v);
-
 /* x += SparseMoe(h) (ffn.rs:478-711) for M tokens: fp32 router, strict top-2,
  * softmax over the pair, per-route SwiGLU expert MLP, weighted sum. */
 static void moe_ffn(const or_model* m, int layer, const float* h, int64_t M, float* x) {
@@ -155,7 +147,7 @@ static void moe_ffn(const or_model* m, int layer, const float* h, int64_t M, flo
         linear_w(m, 2 * Fe, d, m->exp_in + base_in, NULL, NULL, ht, 1, gv, 0);
       for (int c = 0; c < Fe; ++c) {
         const float g = gv[c], v = gv[Fe + c];
-        u[c] = rh(m, g / (1.0f + expf(-g)) * v);
+        u[c] = g / (1.0f + expf(-g)) * v;
       }
       if (m->quantized)
         linear_w(m, d, Fe, NULL, m->exp_down_c + base_down / 2, m->exp_down_s + base_down / 128, u, 1, yv + j * d, 0);
@@ -178,7 +170,7 @@ static void rmsnorm(const or_model* m, const float* x, const float* g, int64_t M
     float ss = 0.f;
     for (int c = 0; c < d; ++c) ss += x[r * d + c] * x[r * d + c];
     const float rms = sqrtf(ss / (float)d + m->eps);
-    for (int c = 0; c < d; ++c) y[r * d + c] = rh(m, x[r * d + c] / rms * g[c]);
+    for (int c = 0; c < d; ++c) y[r * d + c] = x[r * d + c] / rms * g[c];
   }
 }
 
@@ -225,13 +217,13 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
             rbv = b * cs + a * sn;
           }
           if (slot < H) {
-            q[r * qdim + slot * hd + 2 * p] = rb(m, ra);
-            q[r * qdim + slot * hd + 2 * p + 1] = rb(m, rbv);
+            q[r * qdim + slot * hd + 2 * p] = rkv(m, ra);
+            q[r * qdim + slot * hd + 2 * p + 1] = rkv(m, rbv);
           } else {
             const int kv = slot < H + KVH ? slot - H : slot - H - KVH;
             float* dst = (slot < H + KVH ? kl : vl) + (((size_t)s * KVH + kv) * cap + pos) * hd;
-            dst[2 * p] = rb(m, ra);
-            dst[2 * p + 1] = rb(m, rbv);
+            dst[2 * p] = rkv(m, ra);
+            dst[2 * p + 1] = rkv(m, rbv);
           }
         }
     }
@@ -260,7 +252,7 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
         for (int e = 0; e < hd; ++e) {
           float acc = 0.f;
           for (int t = 0; t <= pos; ++t) acc += sc[t] * vb[(size_t)t * hd + e];
-          att[r * qdim + hh * hd + e] = rh(m, acc / sum);
+          att[r * qdim + hh * hd + e] = acc / sum;
         }
         free(sc);
       }
@@ -274,7 +266,7 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
     for (int64_t r = 0; r < rows; ++r)
       for (int c = 0; c < F; ++c) {
         const float g = gv[r * 2 * F + c], v = gv[r * 2 * F + F + c];
-        u[r * F + c] = rh(m, g / (1.0f + expf(-g)) * v);
+        u[r * F + c] = g / (1.0f + expf(-g)) * v;
       }
     linear(m, 3, l, u, rows, x, 1);
   }

@@ -12,9 +12,9 @@ from pathlib import Path
 LIB_PATH = Path(__file__).resolve().parent / "libsumma_amd.so"
 
 SM_OK = 0
-SM_F32, SM_BF16, SM_F16 = 0, 1, 2
-SM_EPI_STORE_F32, SM_EPI_STORE_BF16, SM_EPI_ADD_F32, SM_EPI_SWIGLU_BF16, SM_EPI_SWIGLU_F16 = \
-    0, 1, 2, 3, 4
+SM_F32, SM_BF16, SM_F16, SM_F16X2 = 0, 1, 2, 3
+(SM_EPI_STORE_F32, SM_EPI_STORE_BF16, SM_EPI_ADD_F32, SM_EPI_SWIGLU_BF16, SM_EPI_SWIGLU_F16,
+ SM_EPI_SWIGLU_F16X2) = 0, 1, 2, 3, 4, 5
 
 _lib = None
 

@@ -8,9 +8,10 @@
 // materialised: each KV head is read once for its whole query-head group).
 // Cache layout [S, KVH, cap, hd] as AttnCache (attention.rs:20-40, 115-134).
 //
-// bf16 decode kernel (one query per sequence): one workgroup per
-// (KV head, sequence); its four waves split the key range in tiles of 64.
-// Scores Q.K^T come from v_mfma_f32_16x16x32_bf16 with the group's query heads
+// 16-bit decode kernel (one query per sequence; q and cache bf16 or f16): one
+// workgroup per (KV head, sequence); its four waves split the key range in
+// tiles of 64. Scores Q.K^T come from v_mfma_f32_16x16x32_{bf16,f16} with the
+// group's query heads
 // as the 16-row A operand (padded) and K rows read straight from HBM as the B
 // operand (natural [pos][hd] layout is already k-contiguous per lane). The
 // online softmax runs on the MFMA output registers, probabilities go through a
@@ -25,21 +26,20 @@
 // kernel below for both.
 #include <cmath>
 
+#include "attn_common.hpp"
 #include "common.hpp"
 
 namespace sm {
 namespace {
 
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
 constexpr int kMaxQpk = 16;  // query heads per KV head handled by one WG
 
-template <int HD, int QM, typename TO>
-__global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
+template <int HD, int QM, bool KF16, int OM>
+__global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ lens,
-    TO* __restrict__ out, int H, int KVH, int cap, float scale) {
+    void* __restrict__ out, int H, int KVH, int cap, float scale) {
+  typedef typename Op8<KF16>::T op8;
   constexpr int LPK = HD / 8;      // lanes per V row in the P.V pass (8 dims = 16 B each)
   constexpr int PPI = 64 / LPK;    // keys per P.V iteration per wave
   constexpr int STEPS = HD / 32;   // MFMA k-steps over head_dim
@@ -55,14 +55,14 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
   __shared__ float mrg_o[4][QM][HD];
 
   // A operand: query head (kvh*qpk + j) if j < qpk.
-  bf8 qa[STEPS];
+  op8 qa[STEPS];
 #pragma unroll
   for (int st = 0; st < STEPS; ++st) {
     if (j < qpk) {
       const uint16_t* qp = q + ((size_t)s * H + kvh * qpk + j) * HD + st * 32 + g * 8;
-      qa[st] = *reinterpret_cast<const bf8*>(qp);
+      qa[st] = *reinterpret_cast<const op8*>(qp);
     } else {
-      qa[st] = bf8{};
+      qa[st] = op8{};
     }
   }
 
@@ -84,14 +84,14 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
     //      MFMAs and this lane's V rows for P.V), branch-free: rows past the
     //      end are clamped to a valid row and masked out below. One round trip
     //      per tile instead of one per dependent phase.
-    bf8 kf[4][STEPS];
+    op8 kf[4][STEPS];
     u32x4 vr[VR];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const int key = min(t0 + kb * 16 + j, len - 1);
 #pragma unroll
       for (int st = 0; st < STEPS; ++st)
-        kf[kb][st] = *reinterpret_cast<const bf8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
+        kf[kb][st] = *reinterpret_cast<const op8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
     }
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
@@ -106,7 +106,7 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
       f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < STEPS; ++st)
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], kf[kb][st], acc, 0, 0, 0);
+        acc = Op8<KF16>::mfma(qa[st], kf[kb][st], acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
@@ -137,9 +137,8 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
 #pragma unroll
     for (int vi = 0; vi < VR; ++vi) {
       const int tt = sub + vi * PPI;
-      const u32x4 vv = vr[vi];
-      const float v[8] = {bf16lo(vv.x), bf16hi(vv.x), bf16lo(vv.y), bf16hi(vv.y),
-                          bf16lo(vv.z), bf16hi(vv.z), bf16lo(vv.w), bf16hi(vv.w)};
+      float v[8];
+      unpack8<KF16>(vr[vi], v);
 #pragma unroll
       for (int i = 0; i < QM; ++i) {
         if (i >= qpk) break;
@@ -183,11 +182,7 @@ __global__ __launch_bounds__(256) void attn_decode_bf16_kernel(
       l += mrg_l[w][i] * c;
       o += mrg_o[w][i][d] * c;
     }
-    const float v = o / l;
-    if constexpr (sizeof(TO) == 2 && __is_same(TO, _Float16))
-      out[((size_t)s * H + kvh * qpk + i) * HD + d] = (_Float16)v;
-    else
-      out[((size_t)s * H + kvh * qpk + i) * HD + d] = f32_to_bf16(v);
+    store_out<OM>(out, (size_t)s, H * HD, (kvh * qpk + i) * HD + d, o / l);
   }
 }
 
@@ -253,9 +248,13 @@ int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_
 
 }  // namespace
 
-int attn_prefill_bf16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                      const int32_t* pos0, void* out, bool out_f16, int S, int L, int H, int KVH,
-                      int cap, int hd, hipStream_t st);
+int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                    const int32_t* pos0, void* out, bool kf16, int om, int S, int L, int H,
+                    int KVH, int cap, int hd, hipStream_t st);
+
+inline int out_mode(int out_dtype) {
+  return out_dtype == SM_BF16 ? 0 : out_dtype == SM_F16 ? 1 : out_dtype == SM_F16X2 ? 2 : -1;
+}
 
 }  // namespace sm
 
@@ -277,22 +276,31 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
     return attn_valu_f32((const float*)q, (const float*)kcache, (const float*)vcache, lens, -1,
                          (float*)out, (int)S, 1, (int)H, (int)KVH, (int)cap, (int)head_dim, st);
   }
-  SM_REQUIRE(dtype == SM_BF16, "sm_attn_decode: dtype must be SM_BF16 or SM_F32");
-  SM_REQUIRE(out_dtype == SM_BF16 || out_dtype == SM_F16,
-             "sm_attn_decode: bf16 attention writes bf16 or f16");
+  SM_REQUIRE(dtype == SM_BF16 || dtype == SM_F16,
+             "sm_attn_decode: dtype must be SM_BF16, SM_F16 or SM_F32");
+  const int om = out_mode(out_dtype);
+  SM_REQUIRE(om >= 0, "sm_attn_decode: 16-bit attention writes bf16, f16 or f16 pairs");
   const int qpk = (int)(H / KVH);
   SM_REQUIRE(qpk <= kMaxQpk, "sm_attn_decode: at most %d query heads per KV head", kMaxQpk);
   const dim3 grid((unsigned)KVH, (unsigned)S);
   const uint16_t *qq = (const uint16_t*)q, *kk = (const uint16_t*)kcache,
                  *vv = (const uint16_t*)vcache;
-#define SM_DEC(HD, QM)                                                                            \
-  do {                                                                                            \
-    if (out_dtype == SM_F16)                                                                      \
-      attn_decode_bf16_kernel<HD, QM, _Float16><<<grid, 256, 0, st>>>(                            \
-          qq, kk, vv, lens, (_Float16*)out, (int)H, (int)KVH, (int)cap, scale);                   \
-    else                                                                                          \
-      attn_decode_bf16_kernel<HD, QM, uint16_t><<<grid, 256, 0, st>>>(                            \
-          qq, kk, vv, lens, (uint16_t*)out, (int)H, (int)KVH, (int)cap, scale);                   \
+#define SM_DEC_K(HD, QM, KF)                                                                   \
+  do {                                                                                         \
+    if (om == 2)                                                                               \
+      attn_decode_kernel<HD, QM, KF, 2><<<grid, 256, 0, st>>>(qq, kk, vv, lens, out, (int)H,   \
+                                                             (int)KVH, (int)cap, scale);       \
+    else if (om == 1)                                                                          \
+      attn_decode_kernel<HD, QM, KF, 1><<<grid, 256, 0, st>>>(qq, kk, vv, lens, out, (int)H,   \
+                                                             (int)KVH, (int)cap, scale);       \
+    else                                                                                       \
+      attn_decode_kernel<HD, QM, KF, 0><<<grid, 256, 0, st>>>(qq, kk, vv, lens, out, (int)H,   \
+                                                             (int)KVH, (int)cap, scale);       \
+  } while (0)
+#define SM_DEC(HD, QM)                                   \
+  do {                                                   \
+    if (dtype == SM_F16) SM_DEC_K(HD, QM, true);         \
+    else SM_DEC_K(HD, QM, false);                        \
   } while (0)
   if (head_dim == 64) {
     if (qpk == 1) SM_DEC(64, 1); else if (qpk <= 4) SM_DEC(64, 4); else SM_DEC(64, 16);
@@ -300,6 +308,7 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
     if (qpk == 1) SM_DEC(128, 1); else if (qpk <= 4) SM_DEC(128, 4); else SM_DEC(128, 16);
   }
 #undef SM_DEC
+#undef SM_DEC_K
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
@@ -322,10 +331,11 @@ extern "C" int sm_attn_prefill(const void* q, const void* kcache, const void* vc
                          (float*)out, (int)S, (int)L, (int)H, (int)KVH, (int)cap, (int)head_dim,
                          st);
   }
-  SM_REQUIRE(dtype == SM_BF16, "sm_attn_prefill: dtype must be SM_BF16 or SM_F32");
-  SM_REQUIRE(out_dtype == SM_BF16 || out_dtype == SM_F16,
-             "sm_attn_prefill: bf16 attention writes bf16 or f16");
-  return attn_prefill_bf16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
-                           pos0, out, out_dtype == SM_F16, (int)S, (int)L, (int)H, (int)KVH,
-                           (int)cap, (int)head_dim, st);
+  SM_REQUIRE(dtype == SM_BF16 || dtype == SM_F16,
+             "sm_attn_prefill: dtype must be SM_BF16, SM_F16 or SM_F32");
+  const int om = out_mode(out_dtype);
+  SM_REQUIRE(om >= 0, "sm_attn_prefill: 16-bit attention writes bf16, f16 or f16 pairs");
+  return attn_prefill_16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
+                         pos0, out, dtype == SM_F16, om, (int)S, (int)L, (int)H, (int)KVH,
+                         (int)cap, (int)head_dim, st);
 }

@@ -169,6 +169,13 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 __device__ inline h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 
+// fp32 -> f16 pair (the SM_F16X2 activation format): hi = f16(x),
+// lo = f16(x - hi), so hi + lo carries x to about 22 significant bits.
+__device__ inline void split_f16(float x, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
+
 // One prepared word -> its 8 codes q in natural k order as f16. Each 16-bit
 // half becomes 1024 + u (or 1024 + 16u) by OR-ing the nibble into the
 // mantissa of 0x6400; one packed add / fma removes the bias. 9 VALU ops.

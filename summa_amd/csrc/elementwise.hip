@@ -12,7 +12,7 @@
 //                recompute produces, summa-train/src/tensor_sleep.rs:2609-2614)
 //
 // The residual stream is fp32; activations that feed a matmul are emitted in
-// the model's activation dtype (bf16 for quantized models, fp32 otherwise).
+// the model's activation dtype (f16 pairs for quantized models, fp32 otherwise).
 #include <cmath>
 
 #include "common.hpp"
@@ -23,6 +23,7 @@ namespace {
 template <typename T> __device__ inline float to_f(T v);
 template <> __device__ inline float to_f<float>(float v) { return v; }
 template <> __device__ inline float to_f<uint16_t>(uint16_t v) { return bf16_to_f32(v); }
+template <> __device__ inline float to_f<_Float16>(_Float16 v) { return (float)v; }
 template <typename T> __device__ inline T from_f(float v);
 template <> __device__ inline float from_f<float>(float v) { return v; }
 template <> __device__ inline uint16_t from_f<uint16_t>(float v) { return f32_to_bf16(v); }
@@ -39,8 +40,8 @@ __global__ void embed_kernel(const T* __restrict__ table, const int32_t* __restr
     x[r * d + c] = ok ? to_f(table[(size_t)id * d + c]) * scale : NAN;
 }
 
-// One 256-thread workgroup per row.
-template <typename TO>
+// One 256-thread workgroup per row. PAIR: y rows are SM_F16X2 (hi | lo).
+template <typename TO, bool PAIR = false>
 __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ gamma, int d,
                                                       float eps, TO* __restrict__ y) {
@@ -54,7 +55,12 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   __syncthreads();
   const float tot = part[0] + part[1] + part[2] + part[3];
   const float rms = sqrtf(tot / (float)d + eps);
-  for (int c = threadIdx.x; c < d; c += 256) y[r * d + c] = from_f<TO>(xr[c] / rms * gamma[c]);
+  if constexpr (PAIR) {
+    _Float16* yr = reinterpret_cast<_Float16*>(y) + r * 2 * d;
+    for (int c = threadIdx.x; c < d; c += 256) split_f16(xr[c] / rms * gamma[c], yr[c], yr[d + c]);
+  } else {
+    for (int c = threadIdx.x; c < d; c += 256) y[r * d + c] = from_f<TO>(xr[c] / rms * gamma[c]);
+  }
 }
 
 // qkv: [rows, (H + 2*KVH) * hd] f32, row = s*L + i at position pos0[s] + i.
@@ -186,10 +192,13 @@ extern "C" int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int6
   else if (out_dtype == SM_F16)
     rmsnorm_kernel<_Float16><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
                                                                            (_Float16*)y);
+  else if (out_dtype == SM_F16X2)
+    rmsnorm_kernel<_Float16, true><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
+        x, gamma, (int)d, eps, (_Float16*)y);
   else if (out_dtype == SM_F32)
     rmsnorm_kernel<float><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
                                                                         (float*)y);
-  else SM_REQUIRE(false, "sm_rmsnorm: out_dtype must be SM_F32, SM_BF16 or SM_F16");
+  else SM_REQUIRE(false, "sm_rmsnorm: out_dtype must be SM_F32, SM_BF16, SM_F16 or SM_F16X2");
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
@@ -214,6 +223,7 @@ extern "C" int sm_rope_append(const float* qkv, const float* rope_table, const i
   if (q_dtype == SM_BF16 && cache_dtype == SM_BF16) SM_ROPE(uint16_t, uint16_t);
   else if (q_dtype == SM_F32 && cache_dtype == SM_F32) SM_ROPE(float, float);
   else if (q_dtype == SM_F32 && cache_dtype == SM_BF16) SM_ROPE(float, uint16_t);
+  else if (q_dtype == SM_F16 && cache_dtype == SM_F16) SM_ROPE(_Float16, _Float16);
   else SM_REQUIRE(false, "sm_rope_append: unsupported dtype combination");
 #undef SM_ROPE
   SM_LAUNCH_CHECK();

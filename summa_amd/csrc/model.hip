@@ -152,9 +152,14 @@ unsigned blocks_for(int64_t n) { return (unsigned)ceil_div(n > 0 ? n : 1, 256); 
 
 struct sm_model {
   sm_model_config cfg;
-  int act = SM_F32;       // matmul-input activation dtype (f16 when quantized)
-  int kvt = SM_F32;       // q / KV cache / embedding dtype (bf16 when quantized)
-  size_t act_size = 4;    // bytes of either 16-bit type, or 4
+  int act = SM_F32;       // matmul-input activation dtype (f16 pairs when quantized)
+  int kvt = SM_F32;       // q / KV cache dtype (f16 when quantized)
+  int embt = SM_F32;      // embedding table dtype (bf16 when quantized)
+  size_t act_size = 4;    // bytes per activation value (f32, or an f16 pair)
+  size_t kv_size = 4;     // bytes per q / cache value
+  size_t emb_size = 4;
+  // f16 elements (or f32 values) per activation row of `width` values
+  int64_t act_ld(int64_t width) const { return act == SM_F16X2 ? 2 * width : width; }
   int64_t qdim = 0, kvdim = 0, qkv_n = 0;
   void* embed = nullptr;
   float* final_norm = nullptr;
@@ -198,7 +203,8 @@ int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float*
                   hipStream_t st) {
   const int epi = add ? SM_EPI_ADD_F32 : SM_EPI_STORE_F32;
   if (m->cfg.quantized)
-    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, L.K, y, L.N, epi, st);
+    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, m->act_ld(L.K), y, L.N, epi,
+                        st);
   return sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, y, L.N, epi, st);
 }
 
@@ -206,8 +212,8 @@ int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float*
 int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* u,
                   hipStream_t st) {
   if (m->cfg.quantized)
-    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, L.K, u, L.N / 2,
-                        SM_EPI_SWIGLU_F16, st);
+    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, m->act_ld(L.K), u,
+                        m->act_ld(L.N / 2), SM_EPI_SWIGLU_F16X2, st);
   SM_TRY(ensure(m->gv, (size_t)M * L.N * 4));
   SM_TRY(sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, (float*)m->gv.p, L.N,
                      SM_EPI_STORE_F32, st));
@@ -223,7 +229,7 @@ int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st) {
   SM_TRY(ensure(m->moe_idx, (size_t)routes * 4));
   SM_TRY(ensure(m->moe_w, (size_t)routes * 4));
   SM_TRY(ensure(m->moe_plan, (size_t)sm_moe_plan_words(rows, k, E) * 4));
-  SM_TRY(ensure(m->moe_u, (size_t)routes * Fe * 2));
+  SM_TRY(ensure(m->moe_u, (size_t)routes * Fe * m->act_size));
   SM_TRY(ensure(m->moe_y, (size_t)routes * d * 4));
   SM_TRY(ensure(m->moe_err, 4));
   int32_t* plan = (int32_t*)m->moe_plan.p;
@@ -231,10 +237,12 @@ int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st) {
                             (int32_t*)m->moe_idx.p, (float*)m->moe_w.p, st));
   SM_TRY(sm_moe_route_plan((const int32_t*)m->moe_idx.p, rows, k, E, plan,
                            (int32_t*)m->moe_err.p, st));
-  SM_TRY(sm_q4_grouped_matmul(Ly.exp_in.codes, Ly.exp_in.scales, E, 2 * Fe, d, m->h.p, m->act, d,
-                              1, plan, rows, k, m->moe_u.p, Fe, SM_EPI_SWIGLU_F16, st));
+  SM_TRY(sm_q4_grouped_matmul(Ly.exp_in.codes, Ly.exp_in.scales, E, 2 * Fe, d, m->h.p, m->act,
+                              m->act_ld(d), 1, plan, rows, k, m->moe_u.p, m->act_ld(Fe),
+                              SM_EPI_SWIGLU_F16X2, st));
   SM_TRY(sm_q4_grouped_matmul(Ly.exp_down.codes, Ly.exp_down.scales, E, d, Fe, m->moe_u.p,
-                              SM_F16, Fe, 0, plan, rows, k, m->moe_y.p, d, SM_EPI_STORE_F32, st));
+                              m->act, m->act_ld(Fe), 0, plan, rows, k, m->moe_y.p, d,
+                              SM_EPI_STORE_F32, st));
   return sm_moe_combine((const float*)m->moe_y.p, (const float*)m->moe_w.p, plan, rows, k, E, d,
                         (float*)m->x.p, st);
 }
@@ -255,15 +263,15 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
   SM_TRY(ensure(m->x, (size_t)rows * d * 4));
   SM_TRY(ensure(m->h, (size_t)rows * std::max<int64_t>(d, m->qdim) * m->act_size));
   SM_TRY(ensure(m->qkv, (size_t)rows * m->qkv_n * 4));
-  SM_TRY(ensure(m->qb, (size_t)rows * m->qdim * m->act_size));
+  SM_TRY(ensure(m->qb, (size_t)rows * m->qdim * m->kv_size));
   SM_TRY(ensure(m->attn, (size_t)rows * m->qdim * m->act_size));
   SM_TRY(ensure(m->u, (size_t)rows * c.ffn * m->act_size));
   float* x = (float*)m->x.p;
-  SM_TRY(sm_embed(m->embed, m->kvt, ids, rows, d, c.vocab, 1.0f, x, st));
+  SM_TRY(sm_embed(m->embed, m->embt, ids, rows, d, c.vocab, 1.0f, x, st));
   for (int l = 0; l < c.layers; ++l) {
     const Layer& Ly = m->layers[l];
-    char* kl = (char*)kc + (size_t)l * layer_elems * m->act_size;
-    char* vl = (char*)vc + (size_t)l * layer_elems * m->act_size;
+    char* kl = (char*)kc + (size_t)l * layer_elems * m->kv_size;
+    char* vl = (char*)vc + (size_t)l * layer_elems * m->kv_size;
     SM_TRY(sm_rmsnorm(x, Ly.attn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
     SM_TRY(linear_f32out(m, Ly.qkv, m->h.p, rows, (float*)m->qkv.p, false, st));
     SM_TRY(sm_rope_append((const float*)m->qkv.p, m->rope, pos0, S, L, c.heads, c.kv_heads,
@@ -317,15 +325,18 @@ extern "C" int sm_model_create(const sm_model_config* cfg, sm_model** out) {
   }
   sm_model* m = new sm_model();
   m->cfg = c;
-  m->act = c.quantized ? SM_F16 : SM_F32;
-  m->kvt = c.quantized ? SM_BF16 : SM_F32;
-  m->act_size = c.quantized ? 2 : 4;
+  m->act = c.quantized ? SM_F16X2 : SM_F32;
+  m->kvt = c.quantized ? SM_F16 : SM_F32;
+  m->embt = c.quantized ? SM_BF16 : SM_F32;
+  m->act_size = 4;
+  m->kv_size = c.quantized ? 2 : 4;
+  m->emb_size = c.quantized ? 2 : 4;
   m->qdim = (int64_t)c.heads * c.head_dim;
   m->kvdim = (int64_t)c.kv_heads * c.head_dim;
   m->qkv_n = m->qdim + 2 * m->kvdim;
   auto fail = [&](int s) { sm_model_destroy(m); return s; };
   int s;
-  if ((s = dalloc(m, &m->embed, (size_t)c.vocab * c.d_model * m->act_size, true))) return fail(s);
+  if ((s = dalloc(m, &m->embed, (size_t)c.vocab * c.d_model * m->emb_size, true))) return fail(s);
   if ((s = dalloc(m, (void**)&m->final_norm, (size_t)c.d_model * 4, true))) return fail(s);
   if ((s = alloc_linear(m, m->lm_head, c.vocab, c.d_model))) return fail(s);
   m->layers.resize(c.layers);
@@ -462,7 +473,7 @@ extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float
     SM_HIP(hipMemcpyAsync(lin->w, src, (size_t)n * 4, hipMemcpyDeviceToDevice, st));
     return SM_OK;
   }
-  if (kind == SM_W_EMBED && m->kvt == SM_BF16) {
+  if (kind == SM_W_EMBED && m->embt == SM_BF16) {
     f32_to_bf16_kernel<<<blocks_for(n), 256, 0, st>>>(src, n, (uint16_t*)dense);
     SM_LAUNCH_CHECK();
     return SM_OK;
@@ -536,8 +547,8 @@ extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, in
   hipStream_t st = as_stream(stream);
   const auto& c = m->cfg;
   const size_t layer_elems = cache_layer_elems(m, S, cap);
-  SM_TRY(ensure(m->kc, layer_elems * c.layers * m->act_size));
-  SM_TRY(ensure(m->vc, layer_elems * c.layers * m->act_size));
+  SM_TRY(ensure(m->kc, layer_elems * c.layers * m->kv_size));
+  SM_TRY(ensure(m->vc, layer_elems * c.layers * m->kv_size));
   SM_TRY(ensure(m->pos, (size_t)S * 4));
   SM_TRY(ensure(m->lens, (size_t)S * 4));
   SM_TRY(ensure(m->next_ids, (size_t)S * 4));
@@ -585,8 +596,8 @@ extern "C" int sm_rl_logprobs(sm_model* m, const int32_t* prompts, const int32_t
   for (int64_t s0 = 0; s0 < S; s0 += chunk) {
     const int64_t cs = std::min(chunk, S - s0);
     const size_t layer_elems = cache_layer_elems(m, cs, L);
-    SM_TRY(ensure(m->rkc, layer_elems * m->act_size));
-    SM_TRY(ensure(m->rvc, layer_elems * m->act_size));
+    SM_TRY(ensure(m->rkc, layer_elems * m->kv_size));
+    SM_TRY(ensure(m->rvc, layer_elems * m->kv_size));
     SM_TRY(ensure(m->ids, (size_t)cs * L * 4));
     SM_TRY(ensure(m->pos, (size_t)cs * 4));
     SM_TRY(ensure(m->lens, (size_t)cs * 4));

@@ -51,7 +51,8 @@ constexpr int kRouterThreads = 256;
 // One workgroup per token: h row -> LDS (f32), each wave computes its share of
 // the E router dot products (lanes over d, wave reduction), then one lane does
 // the strict top-2 scan and the softmax over the pair.
-template <typename TH>
+// TH: f32, f16, or f16 pair (PAIR: row t is hi[d] | lo[d]).
+template <typename TH, bool PAIR = false>
 __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
     const TH* __restrict__ h, const float* __restrict__ wr, int d, int E,
     float* __restrict__ logits_out, int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
@@ -60,8 +61,8 @@ __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
   float* lg = smem + d;  // [E]
   const int64_t t = blockIdx.x;
   for (int c = threadIdx.x; c < d; c += kRouterThreads) {
-    if constexpr (sizeof(TH) == 2) hs[c] = (float)h[t * d + c];
-    else hs[c] = h[t * d + c];
+    if constexpr (PAIR) hs[c] = (float)h[t * 2 * d + c] + (float)h[t * 2 * d + d + c];
+    else hs[c] = (float)h[t * d + c];
   }
   __syncthreads();
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -210,13 +211,16 @@ extern "C" int sm_moe_router_top2(const void* h, int h_dtype, const float* w_rou
              "sm_moe_router_top2: bad shape (d <= 8192, experts <= %d)", kMaxExperts);
   if (tokens == 0) return SM_OK;
   const size_t shmem = (size_t)(d + experts) * sizeof(float);
-  if (h_dtype == SM_F16)
+  if (h_dtype == SM_F16X2)
+    router_top2_kernel<_Float16, true><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
+        (const _Float16*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
+  else if (h_dtype == SM_F16)
     router_top2_kernel<_Float16><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
         (const _Float16*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
   else if (h_dtype == SM_F32)
     router_top2_kernel<float><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
         (const float*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
-  else SM_REQUIRE(false, "sm_moe_router_top2: h must be f16 or f32");
+  else SM_REQUIRE(false, "sm_moe_router_top2: h must be f32, f16 or f16 pairs");
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

@@ -1,4 +1,5 @@
-// Causal flash attention for prefill and log-prob recompute (bf16 MFMA).
+// Causal flash attention for prefill and log-prob recompute (16-bit MFMA;
+// q and cache bf16 or f16).
 //
 // Semantics: Transformer full-sequence attention (sdpa with causal mask,
 // summa-llm/src/model/attention.rs:216-298; CubeK flash forward
@@ -9,31 +10,30 @@
 // Tiling: one workgroup per (64 query rows, head, sequence), 4 waves x 16 rows.
 // Per 64-key tile the workgroup stages K [64][hd] and V transposed [hd][64] in
 // LDS (padded rows), then each wave computes S = Q.K^T with
-// v_mfma_f32_16x16x32_bf16 (Q fragments stay in registers for the whole
+// v_mfma_f32_16x16x32_{bf16,f16} (Q fragments stay in registers for the whole
 // sweep), applies the causal mask and the online softmax on the MFMA output
 // registers (row stats reduced across the 16 lanes that share a row), writes P
 // to its LDS slice as a pair of f16 values (hi + lo, ~21 significant bits)
 // and accumulates O += P.V with two f16 MFMAs whose B operand reads the
-// transposed V tile (bf16 -> f16 while staging, exact). The split keeps P.V at
+// transposed V tile (f16 as stored, or bf16 -> f16 while staging, exact for
+// |v| < 65504 and above the f16 subnormal range). The split keeps P.V at
 // fp32-like precision, so the prefill path matches the decode path's fp32
-// probabilities; a single bf16 or f16 P costs measurable log-prob accuracy. O stays in registers; the final 1/l
-// scaling and bf16 store happen once.
+// probabilities; a single bf16 or f16 P costs measurable log-prob accuracy.
+// O stays in registers; the final 1/l scaling and store happen once.
 #include <cmath>
 
+#include "attn_common.hpp"
 #include "common.hpp"
 
 namespace sm {
 namespace {
 
-typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
-typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-typedef float f4 __attribute__((ext_vector_type(4)));
-
-template <int HD, bool OF16>
-__global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
+template <int HD, bool KF16, int OM>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos0,
     void* __restrict__ out, int L, int H, int KVH, int cap, float scale) {
+  typedef typename Op8<KF16>::T op8;
   constexpr int STEPS = HD / 32;
   constexpr int KP = HD + 8;   // padded K row (elements)
   constexpr int VP = 64 + 8;   // padded transposed-V row
@@ -51,15 +51,15 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
   const size_t kv_base = ((size_t)s * KVH + kvh) * cap * HD;
 
   // Q fragments (A operand): lane (row j, group g)
-  bf8 qa[STEPS];
+  op8 qa[STEPS];
   {
     const int r = r0 + j;
 #pragma unroll
     for (int st = 0; st < STEPS; ++st) {
       if (r < L)
-        qa[st] = *reinterpret_cast<const bf8*>(q + (((size_t)s * L + r) * H + h) * HD + st * 32 + g * 8);
+        qa[st] = *reinterpret_cast<const op8*>(q + (((size_t)s * L + r) * H + h) * HD + st * 32 + g * 8);
       else
-        qa[st] = bf8{};
+        qa[st] = op8{};
     }
   }
   f4 o[HD / 16];
@@ -84,11 +84,10 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
         vv = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)key * HD + cc * 8);
       }
       *reinterpret_cast<u32x4*>(&ks[kr * KP + cc * 8]) = kv;
+      float vf[8];
+      unpack8<KF16>(vv, vf);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        vts[(cc * 8 + 2 * e) * VP + kr] = (_Float16)bf16lo(vv[e]);
-        vts[(cc * 8 + 2 * e + 1) * VP + kr] = (_Float16)bf16hi(vv[e]);
-      }
+      for (int e = 0; e < 8; ++e) vts[(cc * 8 + e) * VP + kr] = (_Float16)vf[e];
     }
     __syncthreads();
     if (r0 >= L) continue;  // wave has no rows (uniform per wave)
@@ -99,8 +98,8 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
       f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < STEPS; ++st) {
-        const bf8 kf = *reinterpret_cast<const bf8*>(&ks[(kb * 16 + j) * KP + st * 32 + g * 8]);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[st], kf, acc, 0, 0, 0);
+        const op8 kf = *reinterpret_cast<const op8*>(&ks[(kb * 16 + j) * KP + st * 32 + g * 8]);
+        acc = Op8<KF16>::mfma(qa[st], kf, acc);
       }
       sc[kb] = acc;
     }
@@ -170,35 +169,42 @@ __global__ __launch_bounds__(256) void attn_prefill_bf16_kernel(
     const int row = r0 + 4 * g + r;
     if (row >= L) continue;
     const float inv = 1.f / l[r];
-    const size_t ob = (((size_t)s * L + row) * H + h) * HD;
 #pragma unroll
-    for (int d = 0; d < HD / 16; ++d) {
-      if constexpr (OF16) static_cast<_Float16*>(out)[ob + d * 16 + j] = (_Float16)(o[d][r] * inv);
-      else static_cast<uint16_t*>(out)[ob + d * 16 + j] = f32_to_bf16(o[d][r] * inv);
-    }
+    for (int d = 0; d < HD / 16; ++d)
+      store_out<OM>(out, (size_t)s * L + row, H * HD, h * HD + d * 16 + j, o[d][r] * inv);
   }
 }
 
 }  // namespace
 
-int attn_prefill_bf16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                      const int32_t* pos0, void* out, bool out_f16, int S, int L, int H, int KVH,
-                      int cap, int hd, hipStream_t st) {
+int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
+                    const int32_t* pos0, void* out, bool kf16, int om, int S, int L, int H,
+                    int KVH, int cap, int hd, hipStream_t st) {
   if (S > 65535 || H > 65535) {
     set_error("sm_attn_prefill: S and H must be <= 65535");
     return SM_ERR_UNSUPPORTED;
   }
   const dim3 grid((unsigned)ceil_div(L, 64), (unsigned)H, (unsigned)S);
   const float scale = 1.0f / sqrtf((float)hd);
-#define SM_PF(HD, OF)                                                                         \
-  attn_prefill_bf16_kernel<HD, OF><<<grid, 256, 0, st>>>(q, kc, vc, pos0, out, L, H, KVH, cap, \
-                                                         scale)
-  if (hd == 64) {
-    if (out_f16) SM_PF(64, true); else SM_PF(64, false);
-  } else {
-    if (out_f16) SM_PF(128, true); else SM_PF(128, false);
-  }
+#define SM_PF3(HD, KF, OM)                                                                \
+  attn_prefill_kernel<HD, KF, OM><<<grid, 256, 0, st>>>(q, kc, vc, pos0, out, L, H, KVH, cap, \
+                                                        scale)
+#define SM_PF2(HD, KF)                          \
+  do {                                          \
+    if (om == 2) SM_PF3(HD, KF, 2);             \
+    else if (om == 1) SM_PF3(HD, KF, 1);        \
+    else SM_PF3(HD, KF, 0);                     \
+  } while (0)
+#define SM_PF(HD)                               \
+  do {                                          \
+    if (kf16) SM_PF2(HD, true);                 \
+    else SM_PF2(HD, false);                     \
+  } while (0)
+  if (hd == 64) SM_PF(64);
+  else SM_PF(128);
 #undef SM_PF
+#undef SM_PF2
+#undef SM_PF3
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

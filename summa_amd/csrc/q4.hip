@@ -46,10 +46,18 @@ enum Epi : int {
   EPI_STORE_BF16 = 1,  // y (bf16) = acc
   EPI_ADD_F32 = 2,     // y (f32) += acc          (residual stream)
   EPI_SWIGLU_BF16 = 3, // y (bf16)[m, j] = silu(acc[m, j]) * acc[m, F + j]
-  EPI_SWIGLU_F16 = 4   // same, f16 output
+  EPI_SWIGLU_F16 = 4,  // same, f16 output
+  EPI_SWIGLU_F16X2 = 5 // same, f16 pair (hi at [m, j], lo at [m, F + j])
 };
 
-constexpr bool is_swiglu(int e) { return e == EPI_SWIGLU_BF16 || e == EPI_SWIGLU_F16; }
+constexpr bool is_swiglu(int e) { return e >= EPI_SWIGLU_BF16 && e <= EPI_SWIGLU_F16X2; }
+
+// Activation input modes (template parameter XT of the kernels).
+enum XMode : int { X_BF16 = 0, X_F16 = 1, X_F16X2 = 2 };
+
+inline int xmode_of(int dtype) {
+  return dtype == SM_BF16 ? X_BF16 : dtype == SM_F16 ? X_F16 : dtype == SM_F16X2 ? X_F16X2 : -1;
+}
 
 // 8 bf16 activations (one 16-byte load, k..k+7) -> f16, natural order.
 __device__ inline h8 act_frag(u32x4 v) {
@@ -63,7 +71,7 @@ __device__ inline float silu(float g) { return g / (1.f + __expf(-g)); }
 struct Q4Args {
   const uint8_t* codes;    // [N, K/2]
   const uint16_t* scales;  // [N, K/128] bf16
-  const void* x;           // [M, ldx] bf16 or f16
+  const void* x;           // [M, ldx] bf16, f16 or f16 pairs (lo at +K)
   void* y;                 // [M, ldy]
   int M, N, K;             // N = weight rows (for SWIGLU: 2F)
   int ldx, ldy;
@@ -88,8 +96,9 @@ struct Q4Args {
 // current one is multiplied.
 constexpr int kU = 8;
 
-template <int NB, int KSPLIT, int EPI, bool XF16>
+template <int NB, int KSPLIT, int EPI, int XT>
 __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
+  constexpr int NA = (XT == X_F16X2) ? 2 : 1;  // A fragments per k-step (hi, lo)
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
   int m0 = blockIdx.y * 16;
@@ -127,15 +136,18 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   const int prow = min(m0 + j, mlim - 1);  // activation row this lane feeds to the A operand
   const int arow = a.rowidx ? a.rowidx[prow] : prow;
   const bool arow_ok = m0 + j < mlim;
-  auto load_act = [&](int kg, h8 (&af)[4]) {
+  auto load_act = [&](int kg, h8 (&af)[NA][4]) {
     const int kc = min(kg, ngroups - 1);
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const size_t xo = (size_t)arow * a.ldx + kc * 128 + g * 32 + s * 8;
-      if constexpr (XF16)
-        af[s] = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo);
-      else
-        af[s] = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
+      if constexpr (XT == X_BF16) {
+        af[0][s] = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
+      } else {
+        af[0][s] = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo);
+        if constexpr (NA == 2)
+          af[1][s] = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo + a.K);
+      }
     }
   };
   int brow_c[NB];
@@ -147,7 +159,7 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   for (int b = 0; b < NB; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
 
   const int kg0 = (KSPLIT == 1) ? 0 : wave;
-  h8 an[4];
+  h8 an[NA][4];
   load_act(kg0, an);
   for (int kb0 = kg0; kb0 < ngroups; kb0 += KSPLIT * kU) {
     u32x4 wv[kU][NB];
@@ -169,19 +181,24 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
     for (int u = 0; u < kU; ++u) {
       const int kg = kb0 + u * KSPLIT;
       if (kg >= ngroups) break;
-      h8 af[4];
+      h8 af[NA][4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) af[s] = arow_ok ? an[s] : h8{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int h = 0; h < NA; ++h)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) af[h][s] = arow_ok ? an[h][s] : h8{0, 0, 0, 0, 0, 0, 0, 0};
       load_act(kg + KSPLIT, an);  // next group's activations, in flight during this one
       // Per block: the group's 4 k-steps accumulate unscaled codes, then one
-      // FMA per output applies the group scale (cheaper than scaling B).
+      // FMA per output applies the group scale (cheaper than scaling B). f16
+      // pairs take a second MFMA on the same unpacked codes for the lo half.
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
-        f4 t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0], q4_unpack(wv[u][b][0]),
-                                                      f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+        f4 t = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s = 1; s < 4; ++s)
-          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[s], q4_unpack(wv[u][b][s]), t, 0, 0, 0);
+        for (int s = 0; s < 4; ++s) {
+          const h8 bq = q4_unpack(wv[u][b][s]);
+          t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0][s], bq, t, 0, 0, 0);
+          if constexpr (NA == 2) t = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[1][s], bq, t, 0, 0, 0);
+        }
         const float sc = brow[b] >= 0 ? bf16_to_f32(sraw[u][b]) : 0.f;
 #pragma unroll
         for (int r = 0; r < 4; ++r) acc[b][r] = fmaf(t[r], sc, acc[b][r]);
@@ -214,7 +231,12 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
         const int col = c0 / 2 + b * 16 + j;
         if (col < a.ncols) {
           const float h = silu(acc[b][r]) * acc[b + NB / 2][r];
-          if constexpr (EPI == EPI_SWIGLU_F16)
+          if constexpr (EPI == EPI_SWIGLU_F16X2) {
+            _Float16 hi, lo;
+            split_f16(h, hi, lo);
+            static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = hi;
+            static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + a.ncols + col] = lo;
+          } else if constexpr (EPI == EPI_SWIGLU_F16)
             static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = (_Float16)h;
           else
             static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(h);
@@ -235,7 +257,7 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   }
 }
 
-template <int NB, int KSPLIT, bool XF16>
+template <int NB, int KSPLIT, int XT>
 int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
@@ -243,18 +265,21 @@ int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)row_tiles);
   switch (epi) {
 #define SM_Q4_EPI(E) \
-    case E: q4_gemm_kernel<NB, KSPLIT, E, XF16><<<grid, 256, 0, st>>>(a); break;
+    case E: q4_gemm_kernel<NB, KSPLIT, E, XT><<<grid, 256, 0, st>>>(a); break;
     SM_Q4_EPI(EPI_STORE_F32)
     SM_Q4_EPI(EPI_STORE_BF16)
     SM_Q4_EPI(EPI_ADD_F32)
 #undef SM_Q4_EPI
     case EPI_SWIGLU_BF16:
     case EPI_SWIGLU_F16:
+    case EPI_SWIGLU_F16X2:
       if constexpr (NB % 2 == 0) {
-        if (epi == EPI_SWIGLU_F16)
-          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16, XF16><<<grid, 256, 0, st>>>(a);
+        if (epi == EPI_SWIGLU_F16X2)
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16X2, XT><<<grid, 256, 0, st>>>(a);
+        else if (epi == EPI_SWIGLU_F16)
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16, XT><<<grid, 256, 0, st>>>(a);
         else
-          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_BF16, XF16><<<grid, 256, 0, st>>>(a);
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_BF16, XT><<<grid, 256, 0, st>>>(a);
         break;
       } else {
         set_error("internal: SwiGLU needs an even number of column blocks");
@@ -267,15 +292,18 @@ int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
 }
 
 template <int NB, int KSPLIT>
-int launch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st, int64_t row_tiles) {
-  return xf16 ? launch_q4_x<NB, KSPLIT, true>(a, epi, st, row_tiles)
-              : launch_q4_x<NB, KSPLIT, false>(a, epi, st, row_tiles);
+int launch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, int64_t row_tiles) {
+  switch (xt) {
+    case X_BF16: return launch_q4_x<NB, KSPLIT, X_BF16>(a, epi, st, row_tiles);
+    case X_F16: return launch_q4_x<NB, KSPLIT, X_F16>(a, epi, st, row_tiles);
+    default: return launch_q4_x<NB, KSPLIT, X_F16X2>(a, epi, st, row_tiles);
+  }
 }
 
 }  // namespace
 
 int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
-                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
+                int xt, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
                 const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
                 const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride);
 
@@ -286,7 +314,7 @@ namespace {
 // have fewer than 512 workgroups the four waves of a workgroup split K instead
 // of N. Bigger M (prefill / recompute): the LDS-tiled 256x128 kernel in
 // q4_gemm_lds.hip.
-int dispatch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
+int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st) {
   const int64_t logical_cols = is_swiglu(epi) ? 2 * (int64_t)a.ncols : a.N;
   const bool ksplit_ok = a.K >= 4 * 128;
   if (a.M <= 256) {
@@ -296,13 +324,13 @@ int dispatch_q4(const Q4Args& a, int epi, bool xf16, hipStream_t st) {
     const bool narrow = a.M <= 16 && !is_swiglu(epi);
     const int64_t wgs = ceil_div(logical_cols, narrow ? 64 : 128) * rt;
     if (narrow) {
-      if (wgs < 512 && ksplit_ok) return launch_q4<1, 4>(a, epi, xf16, st, rt);
-      return launch_q4<1, 1>(a, epi, xf16, st, rt);
+      if (wgs < 512 && ksplit_ok) return launch_q4<1, 4>(a, epi, xt, st, rt);
+      return launch_q4<1, 1>(a, epi, xt, st, rt);
     }
-    if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xf16, st, rt);
-    return launch_q4<2, 1>(a, epi, xf16, st, rt);
+    if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xt, st, rt);
+    return launch_q4<2, 1>(a, epi, xt, st, rt);
   }
-  return q4_gemm_lds(a.codes, a.scales, a.N, a.K, a.x, xf16, a.M, a.ldx, a.y, a.ldy, epi,
+  return q4_gemm_lds(a.codes, a.scales, a.N, a.K, a.x, xt, a.M, a.ldx, a.y, a.ldy, epi,
                      a.ncols, st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0);
 }
 
@@ -418,19 +446,23 @@ extern "C" int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_
              (long long)K);
   SM_REQUIRE(N > 0 && N <= 0x7fffffff && K <= 0x7fffffff, "sm_q4_matmul: bad N");
   SM_REQUIRE(M >= 0 && M <= 0x7fffffff, "sm_q4_matmul: bad M");
-  SM_REQUIRE(ldx >= K && ldx % 8 == 0, "sm_q4_matmul: ldx must be >= K and a multiple of 8");
+  const int xt = xmode_of(x_dtype);
+  SM_REQUIRE(xt >= 0, "sm_q4_matmul: x must be bf16, f16 or f16 pairs");
+  const int64_t xw = (xt == X_F16X2) ? 2 * K : K;  // f16 elements per x row
+  SM_REQUIRE(ldx >= xw && ldx % 8 == 0 && ldx <= 0x7fffffff,
+             "sm_q4_matmul: ldx must be >= %lld and a multiple of 8", (long long)xw);
   SM_REQUIRE(reinterpret_cast<uintptr_t>(codes) % 16 == 0 &&
                  reinterpret_cast<uintptr_t>(x) % 16 == 0,
              "sm_q4_matmul: codes and x must be 16-byte aligned");
-  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16,
+  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16X2,
              "sm_q4_matmul: unknown epilogue %d", epilogue);
-  SM_REQUIRE(x_dtype == SM_BF16 || x_dtype == SM_F16, "sm_q4_matmul: x must be bf16 or f16");
   const int64_t ncols = is_swiglu(epilogue) ? N / 2 : N;
   SM_REQUIRE(!is_swiglu(epilogue) || N % 2 == 0, "sm_q4_matmul: SwiGLU needs even N");
-  SM_REQUIRE(ldy >= ncols, "sm_q4_matmul: ldy < output columns");
+  const int64_t yw = (epilogue == EPI_SWIGLU_F16X2) ? 2 * ncols : ncols;
+  SM_REQUIRE(ldy >= yw && ldy <= 0x7fffffff, "sm_q4_matmul: ldy < output row width");
   if (M == 0) return SM_OK;
   Q4Args a{codes, scales, x, y, (int)M, (int)N, (int)K, (int)ldx, (int)ldy, (int)ncols};
-  return dispatch_q4(a, epilogue, x_dtype == SM_F16, as_stream(stream));
+  return dispatch_q4(a, epilogue, xt, as_stream(stream));
 }
 
 extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts,
@@ -441,14 +473,20 @@ extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales
   SM_REQUIRE(codes && scales && x && plan && y, "sm_q4_grouped_matmul: null buffer");
   SM_REQUIRE(experts >= 1 && K > 0 && K % 128 == 0 && N > 0,
              "sm_q4_grouped_matmul: K must be a positive multiple of 128");
-  SM_REQUIRE(x_dtype == SM_BF16 || x_dtype == SM_F16, "sm_q4_grouped_matmul: x must be bf16/f16");
-  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16 && epilogue != EPI_ADD_F32,
+  const int xt = xmode_of(x_dtype);
+  SM_REQUIRE(xt >= 0, "sm_q4_grouped_matmul: x must be bf16, f16 or f16 pairs");
+  SM_REQUIRE(epilogue >= EPI_STORE_F32 && epilogue <= EPI_SWIGLU_F16X2 && epilogue != EPI_ADD_F32,
              "sm_q4_grouped_matmul: epilogue must store (f32/bf16) or SwiGLU");
-  SM_REQUIRE(ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
-             "sm_q4_grouped_matmul: x must be 16-byte aligned rows");
+  const int64_t xw = (xt == X_F16X2) ? 2 * K : K;
+  SM_REQUIRE(ldx >= xw && ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0,
+             "sm_q4_grouped_matmul: x must be 16-byte aligned rows of >= %lld elements",
+             (long long)xw);
+  SM_REQUIRE(!is_swiglu(epilogue) || N % 2 == 0, "sm_q4_grouped_matmul: SwiGLU needs even N");
   const int64_t routes = tokens * top_k;
-  if (routes == 0) return SM_OK;
   const int64_t ncols = is_swiglu(epilogue) ? N / 2 : N;
+  SM_REQUIRE(ldy >= ((epilogue == EPI_SWIGLU_F16X2) ? 2 * ncols : ncols),
+             "sm_q4_grouped_matmul: ldy < output row width");
+  if (routes == 0) return SM_OK;
   PlanView pv = plan_view(const_cast<int32_t*>(plan), routes, experts);
   const size_t cstride = (size_t)q4t_rows(N) * (K / 2), sstride = (size_t)q4t_rows(N) * (K / 128);
   const int32_t* rowidx = gather ? pv.src_rows : nullptr;
@@ -462,13 +500,10 @@ extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales
     a.cstride = cstride;
     a.sstride = sstride;
     const int64_t rt = moe_max_tiles(routes, experts, 16);
-    if (is_swiglu(epilogue) || K < 4 * 128)
-      return x_dtype == SM_F16 ? launch_q4_x<2, 1, true>(a, epilogue, st, rt)
-                               : launch_q4_x<2, 1, false>(a, epilogue, st, rt);
-    return x_dtype == SM_F16 ? launch_q4_x<2, 4, true>(a, epilogue, st, rt)
-                             : launch_q4_x<2, 4, false>(a, epilogue, st, rt);
+    if (is_swiglu(epilogue) || K < 4 * 128) return launch_q4<2, 1>(a, epilogue, xt, st, rt);
+    return launch_q4<2, 4>(a, epilogue, xt, st, rt);
   }
-  return q4_gemm_lds(codes, scales, (int)N, (int)K, x, x_dtype == SM_F16, (int)routes, (int)ldx,
+  return q4_gemm_lds(codes, scales, (int)N, (int)K, x, xt, (int)routes, (int)ldx,
                      y, (int)ldy, epilogue, (int)ncols, st, pv.tiles256, pv.ntiles256,
                      moe_max_tiles(routes, experts, 256), pv.offsets, rowidx, cstride, sstride);
 }

@@ -49,11 +49,14 @@ struct Args {
   size_t cstride, sstride;
 };
 
-// EPI: 0 store f32, 1 store bf16, 2 add f32, 3 swiglu bf16, 4 swiglu f16.
-template <int EPI, bool XF16>
+// EPI: 0 store f32, 1 store bf16, 2 add f32, 3 swiglu bf16, 4 swiglu f16,
+// 5 swiglu f16 pair. XT: 0 bf16 x, 1 f16 x, 2 f16-pair x (hi and lo tiles are
+// both staged; each k-step issues the MFMA twice on the same B fragment).
+template <int EPI, int XT>
 __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
-  constexpr bool SWIGLU = (EPI == 3 || EPI == 4);
-  __shared__ __attribute__((aligned(16))) _Float16 As[kTM * kAP];
+  constexpr bool SWIGLU = (EPI == 3 || EPI == 4 || EPI == 5);
+  constexpr int NA = (XT == 2) ? 2 : 1;
+  __shared__ __attribute__((aligned(16))) _Float16 As[NA][kTM * kAP];
 
   int tn, m_base, mlim = a.M;
   const uint8_t* codes = a.codes;
@@ -125,8 +128,9 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
       const int prow = min(m_base + r, mlim - 1);
       const int row = a.rowidx ? a.rowidx[prow] : prow;
       const size_t xo = (size_t)row * a.ldx + kg * 128 + ch * 8;
+      const bool live = m_base + r < mlim;
       h8 v;
-      if constexpr (XF16) {
+      if constexpr (XT != 0) {
         v = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo);
       } else {
         const u32x4 u = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo);
@@ -134,8 +138,13 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
                (_Float16)bf16hi(u.y), (_Float16)bf16lo(u.z), (_Float16)bf16hi(u.z),
                (_Float16)bf16lo(u.w), (_Float16)bf16hi(u.w)};
       }
-      if (m_base + r >= mlim) v = h8{0, 0, 0, 0, 0, 0, 0, 0};
-      *reinterpret_cast<h8*>(&As[r * kAP + ch * 8]) = v;
+      if (!live) v = h8{0, 0, 0, 0, 0, 0, 0, 0};
+      *reinterpret_cast<h8*>(&As[0][r * kAP + ch * 8]) = v;
+      if constexpr (NA == 2) {
+        h8 lo = *reinterpret_cast<const h8*>(static_cast<const _Float16*>(a.x) + xo + a.K);
+        if (!live) lo = h8{0, 0, 0, 0, 0, 0, 0, 0};
+        *reinterpret_cast<h8*>(&As[1][r * kAP + ch * 8]) = lo;
+      }
     }
     __syncthreads();
     _Float16 sc[kNB];
@@ -149,10 +158,16 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
 #pragma unroll
       for (int mt = 0; mt < kMT; ++mt) {
         const int r = wm * 128 + mt * 16 + j;
-        const h8 af = *reinterpret_cast<const h8*>(&As[r * kAP + g * 32 + s * 8]);
+        const h8 af = *reinterpret_cast<const h8*>(&As[0][r * kAP + g * 32 + s * 8]);
 #pragma unroll
         for (int b = 0; b < kNB; ++b)
           acc[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[b], acc[mt][b], 0, 0, 0);
+        if constexpr (NA == 2) {
+          const h8 al = *reinterpret_cast<const h8*>(&As[1][r * kAP + g * 32 + s * 8]);
+#pragma unroll
+          for (int b = 0; b < kNB; ++b)
+            acc[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bf[b], acc[mt][b], 0, 0, 0);
+        }
       }
     }
   }
@@ -171,8 +186,16 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
           if (hcol >= a.ncols) continue;
           const float h = silu(acc[mt][b][r]) * acc[mt][b + 2][r];
           const size_t o = (size_t)row * a.ldy + hcol;
-          if constexpr (EPI == 4) static_cast<_Float16*>(a.y)[o] = (_Float16)h;
-          else static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(h);
+          if constexpr (EPI == 5) {
+            _Float16 hi, lo;
+            split_f16(h, hi, lo);
+            static_cast<_Float16*>(a.y)[o] = hi;
+            static_cast<_Float16*>(a.y)[o + a.ncols] = lo;
+          } else if constexpr (EPI == 4) {
+            static_cast<_Float16*>(a.y)[o] = (_Float16)h;
+          } else {
+            static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(h);
+          }
         }
       } else {
 #pragma unroll
@@ -194,12 +217,12 @@ __global__ __launch_bounds__(256, 1) void q4_gemm_lds_kernel(Args a) {
 
 // Called by sm_q4_matmul for M > 256 (argument checks done there).
 int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
-                bool xf16, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
+                int xt, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
                 const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
                 const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride) {
   Args a{codes, scales, x, y, M, N, K, ldx, ldy, ncols, 0, 0,
          tiles, ntiles, goff, rowidx, cstride, sstride};
-  const int logical_cols = (epi == 3 || epi == 4) ? 2 * ncols : N;
+  const int logical_cols = (epi >= 3) ? 2 * ncols : N;
   a.ntiles = (int)ceil_div(logical_cols, kTN);
   a.mtiles8 = (int)ceil_div(ceil_div(M, kTM), 8) * 8;
   const int64_t blocks = (int64_t)(tiles ? max_tiles : a.mtiles8) * a.ntiles;
@@ -210,8 +233,9 @@ int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, cons
   const dim3 grid((unsigned)blocks);
 #define SM_LDS(E)                                                                    \
   do {                                                                               \
-    if (xf16) q4_gemm_lds_kernel<E, true><<<grid, 256, 0, st>>>(a);                  \
-    else q4_gemm_lds_kernel<E, false><<<grid, 256, 0, st>>>(a);                      \
+    if (xt == 2) q4_gemm_lds_kernel<E, 2><<<grid, 256, 0, st>>>(a);                  \
+    else if (xt == 1) q4_gemm_lds_kernel<E, 1><<<grid, 256, 0, st>>>(a);             \
+    else q4_gemm_lds_kernel<E, 0><<<grid, 256, 0, st>>>(a);                          \
   } while (0)
   switch (epi) {
     case 0: SM_LDS(0); break;
@@ -219,6 +243,7 @@ int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, cons
     case 2: SM_LDS(2); break;
     case 3: SM_LDS(3); break;
     case 4: SM_LDS(4); break;
+    case 5: SM_LDS(5); break;
     default: set_error("sm_q4_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
   }
 #undef SM_LDS

@@ -201,31 +201,59 @@ class Q4Weight:
         return cls(c, s, n, k)
 
 
-def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
-              epilogue: int = _lib.SM_EPI_STORE_F32) -> torch.Tensor:
-    """y = x . W^T with Q4G128 weights; x bf16 or f16 [M, K]."""
-    _dev(x, "x")
+def f16_pair(x: torch.Tensor) -> torch.Tensor:
+    """fp32 [M, K] -> SM_F16X2 rows [M, 2K] f16: hi = f16(x), lo = f16(x - hi)."""
+    hi = x.to(torch.float16)
+    lo = (x - hi.float()).to(torch.float16)
+    return torch.cat([hi, lo], dim=1).contiguous()
+
+
+def unpair(y: torch.Tensor) -> torch.Tensor:
+    """SM_F16X2 rows [M, 2K] -> fp32 [M, K] (hi + lo)."""
+    k = y.shape[1] // 2
+    return y[:, :k].float() + y[:, k:].float()
+
+
+def _x_dtype(x: torch.Tensor, pair: bool) -> int:
     if x.dtype not in (torch.bfloat16, torch.float16):
         raise TypeError("x must be bfloat16 or float16")
+    if pair and x.dtype != torch.float16:
+        raise TypeError("f16 pairs are float16 rows of [hi | lo]")
+    return _lib.SM_F16X2 if pair else _dt(x)
+
+
+def _out_spec(epilogue: int, rows: int, n: int):
+    if epilogue == _lib.SM_EPI_SWIGLU_BF16:
+        return (rows, n // 2), torch.bfloat16
+    if epilogue == _lib.SM_EPI_SWIGLU_F16:
+        return (rows, n // 2), torch.float16
+    if epilogue == _lib.SM_EPI_SWIGLU_F16X2:
+        return (rows, 2 * (n // 2)), torch.float16
+    if epilogue == _lib.SM_EPI_STORE_BF16:
+        return (rows, n), torch.bfloat16
+    return (rows, n), torch.float32
+
+
+def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
+              epilogue: int = _lib.SM_EPI_STORE_F32, *, pair: bool = False) -> torch.Tensor:
+    """y = x . W^T with Q4G128 weights; x bf16 or f16 [M, K], or with ``pair``
+    f16 [M, 2K] SM_F16X2 rows (see f16_pair)."""
+    _dev(x, "x")
+    xdt = _x_dtype(x, pair)
     M, K = x.shape
+    if pair:
+        K //= 2
     if K != w.k:
         raise ValueError(f"packed linear input width mismatch ({K} != {w.k})")
     if w.tcodes is None:
         raise ValueError(f"Q4 matmul needs K % 128 == 0 (K={w.k})")
-    if epilogue == _lib.SM_EPI_SWIGLU_BF16:
-        shape, dt = (M, w.n // 2), torch.bfloat16
-    elif epilogue == _lib.SM_EPI_SWIGLU_F16:
-        shape, dt = (M, w.n // 2), torch.float16
-    elif epilogue == _lib.SM_EPI_STORE_BF16:
-        shape, dt = (M, w.n), torch.bfloat16
-    else:
-        shape, dt = (M, w.n), torch.float32
+    shape, dt = _out_spec(epilogue, M, w.n)
     if out is None:
         if epilogue == _lib.SM_EPI_ADD_F32:
             raise ValueError("SM_EPI_ADD_F32 needs an output to accumulate into")
         out = torch.empty(shape, dtype=dt, device=x.device)
     _dev(out, "out")
-    call("sm_q4_matmul", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k, x.data_ptr(), _dt(x),
+    call("sm_q4_matmul", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k, x.data_ptr(), xdt,
          M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
     return out
 
@@ -277,21 +305,26 @@ class RoutePlan:
             words[o[i]:o[i + 1]] for i in range(5))
 
 
-def moe_top2_indices(h: torch.Tensor, router: torch.Tensor, *, want_logits: bool = False):
+def moe_top2_indices(h: torch.Tensor, router: torch.Tensor, *, want_logits: bool = False,
+                     pair: bool = False):
     """Router logits (fp32 h . W_r^T, ffn.rs:489-490), strict top-2 with the
     first index winning ties (moe_topk.rs:74-104) and the softmax over the
-    selected pair (ffn.rs:514). h [T, d] f32/f16, router [E, d] f32.
+    selected pair (ffn.rs:514). h [T, d] f32/f16 (or f16 pairs [T, 2d] with
+    ``pair``), router [E, d] f32.
     Returns (top_idx [T, 2] int32, top_w [T, 2] f32, logits [T, E] or None)."""
     _dev(h, "h")
     _dev(router, "router")
     T, d = h.shape
+    if pair:
+        d //= 2
     E = router.shape[0]
     if router.dtype != torch.float32 or router.shape[1] != d:
         raise ValueError("router must be f32 [experts, d]")
     idx = torch.empty((T, 2), dtype=torch.int32, device=h.device)
     wts = torch.empty((T, 2), dtype=torch.float32, device=h.device)
     logits = torch.empty((T, E), dtype=torch.float32, device=h.device) if want_logits else None
-    call("sm_moe_router_top2", h.data_ptr(), _dt(h), router.data_ptr(), T, d, E, _p(logits),
+    call("sm_moe_router_top2", h.data_ptr(), _lib.SM_F16X2 if pair else _dt(h),
+         router.data_ptr(), T, d, E, _p(logits),
          idx.data_ptr(), wts.data_ptr(), _stream())
     return idx, wts, logits
 
@@ -311,27 +344,20 @@ def moe_route_plan(top_idx: torch.Tensor, experts: int) -> RoutePlan:
 
 
 def grouped_q4_matmul(bank: ExpertBank, x: torch.Tensor, plan: RoutePlan, *, gather: bool,
-                      epilogue: int = _lib.SM_EPI_STORE_F32) -> torch.Tensor:
+                      epilogue: int = _lib.SM_EPI_STORE_F32, pair: bool = False) -> torch.Tensor:
     """Per-expert y[p] = x[row(p)] . W_e^T over the plan's sorted positions p
     (grouped_linear.rs:65 / forward_grouped_swiglu ffn.rs:321). With ``gather``
     row(p) = src_rows[p] (the token; route_gather folded in), else row(p) = p."""
     _dev(x, "x")
-    if x.dtype not in (torch.bfloat16, torch.float16):
-        raise TypeError("x must be bfloat16 or float16")
-    if x.shape[1] != bank.k:
-        raise ValueError(f"grouped linear input width mismatch ({x.shape[1]} != {bank.k})")
+    xdt = _x_dtype(x, pair)
+    width = x.shape[1] // 2 if pair else x.shape[1]
+    if width != bank.k:
+        raise ValueError(f"grouped linear input width mismatch ({width} != {bank.k})")
     R = plan.tokens * plan.top_k
-    if epilogue == _lib.SM_EPI_SWIGLU_F16:
-        shape, dt = (R, bank.n // 2), torch.float16
-    elif epilogue == _lib.SM_EPI_SWIGLU_BF16:
-        shape, dt = (R, bank.n // 2), torch.bfloat16
-    elif epilogue == _lib.SM_EPI_STORE_BF16:
-        shape, dt = (R, bank.n), torch.bfloat16
-    else:
-        shape, dt = (R, bank.n), torch.float32
+    shape, dt = _out_spec(epilogue, R, bank.n)
     out = torch.empty(shape, dtype=dt, device=x.device)
     call("sm_q4_grouped_matmul", bank.tcodes.data_ptr(), bank.tscales.data_ptr(), bank.experts,
-         bank.n, bank.k, x.data_ptr(), _dt(x), x.stride(0), int(gather), plan.words.data_ptr(),
+         bank.n, bank.k, x.data_ptr(), xdt, x.stride(0), int(gather), plan.words.data_ptr(),
          plan.tokens, plan.top_k, out.data_ptr(), out.stride(0), int(epilogue), _stream())
     return out
 

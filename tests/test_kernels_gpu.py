@@ -6,7 +6,7 @@ import torch
 
 import oracle
 from summa_amd import _lib
-from summa_amd._lib import SM_BF16, SM_F32, call
+from summa_amd._lib import SM_BF16, SM_F16, SM_F16X2, SM_F32, call
 
 pytestmark = pytest.mark.gpu
 
@@ -17,6 +17,16 @@ def _s():
 
 def _bf16(a, dev):
     return torch.from_numpy(oracle.bf16_bits(a).view(np.int16)).to(dev).view(torch.bfloat16)
+
+
+def _f16(a, dev):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float16)).to(dev)
+
+
+def _unpair(t, width):
+    """SM_F16X2 rows (hi[width] | lo[width]) -> f64 values hi + lo."""
+    a = t.cpu().numpy().astype(np.float64).reshape(-1, 2 * width)
+    return a[:, :width] + a[:, width:]
 
 
 def _attn_ref(q, k, v, lens):
@@ -52,6 +62,47 @@ def test_attn_decode_bf16(dev, S, H, KVH, hd, cap):
     ref = _attn_ref(q, k, v, lens)
     # bf16 output: one rounding (2^-8 relative) on top of fp32 accumulation
     np.testing.assert_allclose(out.float().cpu().numpy(), ref, rtol=2 ** -7, atol=2e-3)
+
+
+@pytest.mark.parametrize("S,H,KVH,hd,cap", [(3, 12, 12, 64, 300), (4, 16, 4, 128, 1100),
+                                            (5, 8, 1, 128, 257)])
+def test_attn_decode_f16_cache_pair_out(dev, S, H, KVH, hd, cap):
+    """f16 q / cache (the quantized models' KV dtype), f16-pair output: only the
+    fp32 accumulation separates the result from the exact attention."""
+    print(f"case f16 S={S} H={H} KVH={KVH} hd={hd} cap={cap}", flush=True)
+    rng = np.random.default_rng(S * H + cap + 1)
+    q, k, v = (rng.normal(0, 1, sh).astype(np.float16)
+               for sh in ((S, H, hd), (S, KVH, cap, hd), (S, KVH, cap, hd)))
+    lens = rng.integers(1, cap + 1, S).astype(np.int32)
+    lens[0] = cap
+    out = torch.empty(S, 2 * H * hd, dtype=torch.float16, device=dev)
+    L = torch.from_numpy(lens).to(dev)
+    qd, kd, vd = _f16(q, dev), _f16(k, dev), _f16(v, dev)
+    call("sm_attn_decode", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), L.data_ptr(),
+         out.data_ptr(), SM_F16, SM_F16X2, S, H, KVH, cap, hd, _s())
+    ref = _attn_ref(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), lens)
+    np.testing.assert_allclose(_unpair(out, H * hd).reshape(S, H, hd), ref, rtol=2e-5, atol=2e-6)
+
+
+@pytest.mark.parametrize("S,L,p0,H,KVH,hd", [(2, 100, 0, 4, 4, 64), (2, 64, 0, 16, 4, 128),
+                                             (1, 130, 3, 8, 2, 128)])
+def test_attn_prefill_f16_cache_pair_out(dev, S, L, p0, H, KVH, hd):
+    print(f"case f16 prefill S={S} L={L} p0={p0} H={H} KVH={KVH} hd={hd}", flush=True)
+    rng = np.random.default_rng(L + hd + 1)
+    cap = p0 + L
+    q, k, v = (rng.normal(0, 1, sh).astype(np.float16)
+               for sh in ((S, L, H, hd), (S, KVH, cap, hd), (S, KVH, cap, hd)))
+    out = torch.empty(S * L, 2 * H * hd, dtype=torch.float16, device=dev)
+    pos0 = torch.full((S,), p0, dtype=torch.int32, device=dev)
+    qd, kd, vd = _f16(q, dev), _f16(k, dev), _f16(v, dev)
+    call("sm_attn_prefill", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), pos0.data_ptr(),
+         out.data_ptr(), SM_F16, SM_F16X2, S, L, H, KVH, cap, hd, _s())
+    got = _unpair(out, H * hd).reshape(S, L, H, hd)
+    qf, kf, vf = (a.astype(np.float32) for a in (q, k, v))
+    for r in range(L):
+        ref = _attn_ref(qf[:, r], kf, vf, np.full(S, p0 + r + 1))
+        # P as an f16 hi + lo pair (~21 bits) and exact f16 V in the P.V MFMA
+        np.testing.assert_allclose(got[:, r], ref, rtol=2e-5, atol=2e-6)
 
 
 @pytest.mark.parametrize("S,L,p0,H,KVH,hd", [(2, 100, 0, 4, 4, 64), (2, 64, 0, 16, 4, 128),
@@ -118,6 +169,15 @@ def test_rope_append_adjacent_pairs(dev):
             np.testing.assert_array_equal(vc.cpu().numpy()[s, :, pos], x[s, i, H + KVH:])
     # untouched cache slots stay zero
     assert np.all(kc.cpu().numpy()[0, :, L:] == 0)
+    # f16 q / cache (quantized models): the same values rounded once to f16
+    q16 = torch.empty(S * L, H, hd, dtype=torch.float16, device=dev)
+    kc16 = torch.zeros(S, KVH, cap, hd, dtype=torch.float16, device=dev)
+    vc16 = torch.zeros(S, KVH, cap, hd, dtype=torch.float16, device=dev)
+    call("sm_rope_append", qkv_d.data_ptr(), tab_d.data_ptr(), pos_d.data_ptr(), S, L, H, KVH,
+         hd, cap, q16.data_ptr(), SM_F16, kc16.data_ptr(), vc16.data_ptr(), SM_F16, _s())
+    np.testing.assert_array_equal(q16.cpu().numpy(), q.cpu().numpy().astype(np.float16))
+    np.testing.assert_array_equal(kc16.cpu().numpy(), kc.cpu().numpy().astype(np.float16))
+    np.testing.assert_array_equal(vc16.cpu().numpy(), vc.cpu().numpy().astype(np.float16))
 
 
 def test_rmsnorm_and_embed(dev):
@@ -137,6 +197,14 @@ def test_rmsnorm_and_embed(dev):
     xr = table[ids].astype(np.float64)
     ref = xr / np.sqrt((xr ** 2).mean(1, keepdims=True) + 1e-5) * g
     np.testing.assert_allclose(y.float().cpu().numpy(), ref, rtol=2 ** -8, atol=1e-6)
+    # f16-pair output: hi = f16(y), lo = f16(y - hi); fp32-level precision
+    yp = torch.empty(rows, 2 * d, dtype=torch.float16, device=dev)
+    call("sm_rmsnorm", x.data_ptr(), g_d.data_ptr(), rows, d, 1e-5, yp.data_ptr(), SM_F16X2, _s())
+    hi = yp.cpu().numpy()[:, :d].astype(np.float64)
+    assert np.all(np.abs(hi - ref) <= np.abs(ref) * 2.0 ** -11 + 2.0 ** -24)  # hi = f16(y)
+    np.testing.assert_allclose(_unpair(yp, d), ref, rtol=1e-6, atol=1e-7)
+    assert np.all(np.abs(yp.cpu().numpy()[:, d:].astype(np.float64))
+                  <= np.abs(hi) * 2.0 ** -11 + 2.0 ** -24)
 
 
 @pytest.mark.parametrize("temperature", [0.0, 1.0, 0.7])

@@ -186,8 +186,8 @@ def test_gumbel_sampler_distribution_and_determinism():
 
 def test_quantized_oracle_close_to_dequantized_f32():
     # The Q4 path computes with dequantised weights (scale * code exact in f32)
-    # and bf16-rounded activations: logits stay close to the f32 model whose
-    # weights are the decoded Q4 values.
+    # and f16-rounded q/k/v: logits stay close to the f32 model whose weights
+    # are the decoded Q4 values.
     cfg = dict(TINY, d=128, F=128, hd=32, H=4, KVH=4)
     w = oracle.random_weights(cfg, seed=8, std=0.05)
     q = oracle.HostModel(cfg, w, quantized=True)
@@ -202,12 +202,12 @@ def test_quantized_oracle_close_to_dequantized_f32():
     ids = np.random.default_rng(9).integers(0, cfg["V"], (2, 9)).astype(np.int32)
     a, b = q.forward_logits(ids), f.forward_logits(ids)
     assert np.abs(a - b).max() < 2e-2 * max(1.0, np.abs(b).max())
-    assert np.abs(a - b).max() > 0  # bf16 rounding points are really applied
+    assert np.abs(a - b).max() > 0  # the f16 q/k/v rounding is really applied
 
 
 def test_moe_quantized_oracle_close_to_dequantized_f32():
     # per-expert Q4G128 packing: decoding each expert's codes gives the f32
-    # model the quantized MoE path approximates (f16 activation rounding only)
+    # model the quantized MoE path approximates (f16 q/k/v rounding only)
     cfg = dict(TINY_MOE, d=128, Fe=128, hd=32, H=4, KVH=4)
     w = oracle.random_weights(cfg, seed=18, std=0.05)
     q = oracle.HostModel(cfg, w, quantized=True)

@@ -132,7 +132,7 @@ def _bank(E, n, k, seed, dev):
 
 @pytest.mark.parametrize("T,E,used,n,k", [(128, 8, 8, 512, 512), (5, 16, 3, 256, 384),
                                           (2500, 8, 8, 256, 256), (3000, 4, 2, 384, 128)])
-@pytest.mark.parametrize("mode", ["swiglu_gather", "store"])
+@pytest.mark.parametrize("mode", ["swiglu_gather", "store", "pair_swiglu_gather", "pair_store"])
 def test_grouped_matmul_matches_per_expert(dev, T, E, used, n, k, mode):
     """Routes <= 4096 run the small-M kernel (16-row tiles), more the LDS kernel."""
     print(f"case grouped T={T} E={E} n={n} k={k} {mode}", flush=True)
@@ -148,6 +148,17 @@ def test_grouped_matmul_matches_per_expert(dev, T, E, used, n, k, mode):
         rows = x[order // 2].astype(np.float64)
         y = ops.grouped_q4_matmul(bank, torch.from_numpy(x).to(dev), plan, gather=True,
                                   epilogue=_lib.SM_EPI_SWIGLU_F16).float().cpu().numpy()
+    elif mode.startswith("pair"):
+        gather = mode == "pair_swiglu_gather"
+        x = torch.from_numpy(rng.normal(0, 1, (T if gather else R, k)).astype(np.float32)).to(dev)
+        xp = ops.f16_pair(x)
+        exact = ops.unpair(xp).cpu().numpy().astype(np.float64)
+        rows = exact[order // 2] if gather else exact
+        if gather:
+            y = ops.unpair(ops.grouped_q4_matmul(bank, xp, plan, gather=True, pair=True,
+                                                 epilogue=_lib.SM_EPI_SWIGLU_F16X2)).cpu().numpy()
+        else:
+            y = ops.grouped_q4_matmul(bank, xp, plan, gather=False, pair=True).cpu().numpy()
     else:
         x = rng.normal(0, 1, (R, k)).astype(np.float16)
         rows = x.astype(np.float64)
@@ -163,6 +174,10 @@ def test_grouped_matmul_matches_per_expert(dev, T, E, used, n, k, mode):
         F = n // 2
         g, v = ref[:, :F], ref[:, F:]
         np.testing.assert_allclose(y, g / (1 + np.exp(-g)) * v, rtol=2 ** -10, atol=1e-5)
+    elif mode == "pair_swiglu_gather":
+        F = n // 2
+        g, v = ref[:, :F], ref[:, F:]
+        np.testing.assert_allclose(y, g / (1 + np.exp(-g)) * v, rtol=1e-5, atol=2e-6)
     else:
         assert np.all(np.abs(y - ref) <= 2e-6 * bound + 1e-7), float(np.abs(y - ref).max())
 

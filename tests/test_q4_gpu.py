@@ -147,3 +147,52 @@ def test_large_m_lds_kernel(dev, m, n, k, xdt):
         h = ops.q4_matmul(qw, xd, epilogue=_lib.SM_EPI_SWIGLU_F16).float().cpu().numpy()
         g, v = y_ref[:, :F], y_ref[:, F:]
         np.testing.assert_allclose(h, g / (1 + np.exp(-g)) * v, rtol=2 ** -10, atol=1e-5)
+
+
+def _pair_host(x):
+    """fp32 -> SM_F16X2 rows (hi | lo) and the exact value they carry."""
+    hi = x.astype(np.float16)
+    lo = (x - hi.astype(np.float32)).astype(np.float16)
+    return np.concatenate([hi, lo], 1), hi.astype(np.float32) + lo.astype(np.float32)
+
+
+@pytest.mark.parametrize("m,n,k", [(1, 768, 3072), (7, 2304, 768), (128, 11264, 2048),
+                                   (600, 768, 768), (1000, 256, 1024)])
+def test_matmul_f16_pair_activations(dev, m, n, k):
+    """SM_F16X2 input (two MFMAs per step on the same codes) and the SwiGLU
+    f16-pair epilogue: fp32-grade activations through the f16 MFMA path.
+    m > 256 runs the LDS kernel (hi and lo tiles staged)."""
+    print(f"case pair m={m} n={n} k={k}", flush=True)
+    w = _weights(n, k, m + 7)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(m + 1).normal(0, 1, (m, k)).astype(np.float32)
+    xp, xr = _pair_host(x)
+    assert np.abs(xr - x).max() <= 2.0 ** -21 * np.abs(x).max()
+    xd = torch.from_numpy(xp).to(dev)
+    y = ops.q4_matmul(qw, xd, pair=True).cpu().numpy()
+    dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+    y_ref = xr.astype(np.float64) @ dense.T
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    assert np.all(np.abs(y - y_ref) <= tol), float(np.abs(y - y_ref).max())
+    # device split of an f32 activation gives the same result
+    y2 = ops.q4_matmul(qw, ops.f16_pair(torch.from_numpy(x).to(dev)), pair=True).cpu().numpy()
+    np.testing.assert_array_equal(y2, y)
+    F = n // 2
+    h = ops.unpair(ops.q4_matmul(qw, xd, epilogue=_lib.SM_EPI_SWIGLU_F16X2, pair=True))
+    g, v = y_ref[:, :F], y_ref[:, F:]
+    ref_h = g / (1 + np.exp(-g)) * v
+    hb = (np.abs(g) + 1) * (tol[:, F:] + tol[:, :F]) * (np.abs(v) + 1)  # propagated matmul error
+    assert np.all(np.abs(h.cpu().numpy() - ref_h) <= hb + 1e-6 * np.abs(ref_h) + 1e-7)
+
+
+def test_pair_rejects_short_rows(dev):
+    w = _weights(64, 256, 1)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, 64, 256, dev)
+    x = torch.zeros((2, 256), dtype=torch.float16, device=dev)  # pair rows need 2K
+    y = torch.empty((2, 64), device=dev)
+    with pytest.raises(_lib.SummaError, match="ldx must be >= 512"):
+        _lib.call("sm_q4_matmul", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), 64, 256,
+                  x.data_ptr(), _lib.SM_F16X2, 2, 256, y.data_ptr(), 64, 0,
+                  torch.cuda.current_stream().cuda_stream)
