@@ -152,6 +152,17 @@ enum {
 int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
                  const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
                  int epilogue, void* stream);
+/* Same contract with a caller-owned device workspace (16-byte aligned): when
+ * workspace_bytes >= sm_q4_matmul_workspace_bytes(M, N, K, epilogue) a batch
+ * call whose grid would underfill the GPU splits K over several workgroups
+ * and a second kernel sums the fp32 partials in split order (deterministic)
+ * and applies the epilogue. A smaller workspace only limits the split. The
+ * workspace contents are scratch; calls sharing one workspace must not
+ * overlap. */
+int64_t sm_q4_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue);
+int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                    const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
+                    int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
 
 /* Dense fp32 y = x . W^T (fp32 models; matmul::linear, summa-llm/src/model/
  * matmul.rs:57-66). epilogue: SM_EPI_STORE_F32 or SM_EPI_ADD_F32. */
@@ -221,7 +232,7 @@ int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab, floa
  * sm_moe_route_plan: stable sort of routes r = t*k + j by expert
  *   (host_route_plan ffn.rs:888-929 / route_plan moe_route.rs:22-142) into the
  *   int32 `plan` buffer of sm_moe_plan_words() words: counts[E],
- *   offsets[E+1], order[R], inverse[R], src_rows[R], then 16- and 256-row
+ *   offsets[E+1], order[R], inverse[R], src_rows[R], then 16- and 128-row
  *   tile lists used by sm_q4_grouped_matmul. error (device int32, caller-zeroed)
  *   gets bit 0 set for an expert index outside [0, E); such a route is left
  *   out of the plan (inverse = -1) and contributes nothing in sm_moe_combine.

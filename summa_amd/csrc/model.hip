@@ -27,6 +27,9 @@
 extern "C" {
 int sm_q4_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
                  int64_t, void*, int64_t, int, void*);
+int64_t sm_q4_matmul_workspace_bytes(int64_t, int64_t, int64_t, int);
+int sm_q4_matmul_ws(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
+                    int64_t, void*, int64_t, int, void*, int64_t, void*);
 int sm_q4_quantize(const void*, int, int64_t, uint8_t*, uint16_t*, int32_t*, void*);
 int sm_q4_pack(const uint8_t*, const uint16_t*, int64_t, int64_t, uint8_t*, uint16_t*, void*);
 int sm_gemm_f32(const float*, int64_t, int64_t, const float*, int64_t, int64_t, float*, int64_t,
@@ -170,7 +173,7 @@ struct sm_model {
   size_t weight_bytes = 0;
   // workspace
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
-      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err;
+      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws;
   int64_t gen_cap = 0, gen_S = 0;
 };
 
@@ -198,13 +201,23 @@ int alloc_linear(sm_model* m, Linear& L, int64_t N, int64_t K, int64_t count = 1
   return SM_OK;
 }
 
+// Split-K workspace for batch-size Q4 matmuls (capped: the split is only used
+// when a grid underfills the GPU, i.e. at decode batch sizes).
+constexpr int64_t kMatmulWs = 64ll << 20;
+
+int q4_linear(sm_model* m, const Linear& L, const void* x, int64_t M, void* y, int64_t ldy,
+              int epi, hipStream_t st) {
+  const int64_t want = std::min(kMatmulWs, sm_q4_matmul_workspace_bytes(M, L.N, L.K, epi));
+  if (want > 0) SM_TRY(ensure(m->mmws, (size_t)want));
+  return sm_q4_matmul_ws(L.codes, L.scales, L.N, L.K, x, m->act, M, m->act_ld(L.K), y, ldy, epi,
+                         want > 0 ? m->mmws.p : nullptr, want, st);
+}
+
 // y (+)= x . W^T. x: activation dtype [M, K]; y f32 [M, N] (ADD or STORE).
 int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float* y, bool add,
                   hipStream_t st) {
   const int epi = add ? SM_EPI_ADD_F32 : SM_EPI_STORE_F32;
-  if (m->cfg.quantized)
-    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, m->act_ld(L.K), y, L.N, epi,
-                        st);
+  if (m->cfg.quantized) return q4_linear(m, L, x, M, y, L.N, epi, st);
   return sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, y, L.N, epi, st);
 }
 
@@ -212,8 +225,7 @@ int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float*
 int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* u,
                   hipStream_t st) {
   if (m->cfg.quantized)
-    return sm_q4_matmul(L.codes, L.scales, L.N, L.K, x, m->act, M, m->act_ld(L.K), u,
-                        m->act_ld(L.N / 2), SM_EPI_SWIGLU_F16X2, st);
+    return q4_linear(m, L, x, M, u, m->act_ld(L.N / 2), SM_EPI_SWIGLU_F16X2, st);
   SM_TRY(ensure(m->gv, (size_t)M * L.N * 4));
   SM_TRY(sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, (float*)m->gv.p, L.N,
                      SM_EPI_STORE_F32, st));
@@ -382,7 +394,7 @@ extern "C" int sm_model_destroy(sm_model* m) {
   DevBuf* bufs[] = {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits,
                     &m->rows, &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc,
                     &m->rkc, &m->rvc, &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w,
-                    &m->moe_plan, &m->moe_u, &m->moe_y, &m->moe_err};
+                    &m->moe_plan, &m->moe_u, &m->moe_y, &m->moe_err, &m->mmws};
   for (DevBuf* b : bufs)
     if (b->p) hipFree(b->p);
   delete m;

@@ -13,9 +13,9 @@
 //
 // MI355X design: no host round trip anywhere. The route plan (one workgroup,
 // deterministic stable counting sort) also emits two device tile lists
-// (16-row and 256-row tiles per expert), which the grouped Q4 matmuls consume
+// (16-row and 128-row tiles per expert), which the grouped Q4 matmuls consume
 // directly: the small-M kernel for decode (q4.hip) and the LDS kernel for
-// prefill / recompute (q4_gemm_lds.hip). The token gather is folded into the
+// prefill / recompute (q4_gemm_bl.hip). The token gather is folded into the
 // first grouped matmul's A-operand addressing (row index = src_rows[p]), so
 // routed inputs are never materialised.
 #include <cmath>
@@ -39,8 +39,8 @@ PlanView plan_view(int32_t* plan, int64_t routes, int64_t experts) {
   v.src_rows = p; p += routes;
   v.ntiles16 = p; p += 1;
   v.tiles16 = p; p += 2 * moe_max_tiles(routes, experts, 16);
-  v.ntiles256 = p; p += 1;
-  v.tiles256 = p;
+  v.ntiles128 = p; p += 1;
+  v.tiles128 = p;
   return v;
 }
 
@@ -103,7 +103,7 @@ constexpr int kMaxExperts = 64;
 __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const int32_t* __restrict__ idx,
                                                                   int routes, int k, int E,
                                                                   PlanView pv, int max16,
-                                                                  int max256,
+                                                                  int max128,
                                                                   int32_t* __restrict__ error) {
   __shared__ int32_t cnt[kPlanThreads][kMaxExperts + 1];
   __shared__ int32_t offs[kMaxExperts + 1];
@@ -141,21 +141,21 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const int32_t*
     }
     offs[E] = acc;
     pv.offsets[E] = acc;
-    // tile lists: (expert, first row) for 16- and 256-row tiles
-    int n16 = 0, n256 = 0;
+    // tile lists: (expert, first row) for 16- and 128-row tiles
+    int n16 = 0, n128 = 0;
     for (int e = 0; e < E; ++e) {
       const int c = offs[e + 1] - offs[e];
       for (int r = 0; r < c && n16 < max16; r += 16, ++n16) {
         pv.tiles16[2 * n16] = e;
         pv.tiles16[2 * n16 + 1] = r;
       }
-      for (int r = 0; r < c && n256 < max256; r += 256, ++n256) {
-        pv.tiles256[2 * n256] = e;
-        pv.tiles256[2 * n256 + 1] = r;
+      for (int r = 0; r < c && n128 < max128; r += 128, ++n128) {
+        pv.tiles128[2 * n128] = e;
+        pv.tiles128[2 * n128 + 1] = r;
       }
     }
     pv.ntiles16[0] = n16;
-    pv.ntiles256[0] = n256;
+    pv.ntiles128[0] = n128;
   }
   __syncthreads();
   for (int r = r0; r < r1; ++r) {
@@ -199,7 +199,7 @@ using namespace sm;
 extern "C" int64_t sm_moe_plan_words(int64_t tokens, int64_t top_k, int64_t experts) {
   const int64_t routes = tokens * top_k;
   return experts + (experts + 1) + 3 * routes + 1 + 2 * moe_max_tiles(routes, experts, 16) + 1 +
-         2 * moe_max_tiles(routes, experts, 256);
+         2 * moe_max_tiles(routes, experts, 128);
 }
 
 extern "C" int sm_moe_router_top2(const void* h, int h_dtype, const float* w_router,
@@ -236,7 +236,7 @@ extern "C" int sm_moe_route_plan(const int32_t* top_idx, int64_t tokens, int64_t
   PlanView pv = plan_view(plan, routes, experts);
   route_plan_kernel<<<1, kPlanThreads, 0, as_stream(stream)>>>(
       top_idx, (int)routes, (int)top_k, (int)experts, pv,
-      (int)moe_max_tiles(routes, experts, 16), (int)moe_max_tiles(routes, experts, 256), error);
+      (int)moe_max_tiles(routes, experts, 16), (int)moe_max_tiles(routes, experts, 128), error);
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

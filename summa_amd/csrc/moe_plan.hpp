@@ -14,8 +14,8 @@ struct PlanView {
   int32_t *src_rows;   // [R] sorted position -> token (route id / k)
   int32_t *ntiles16;   // [1] number of 16-row (expert, first row) tiles
   int32_t *tiles16;    // [max16][2]
-  int32_t *ntiles256;  // [1] number of 256-row tiles
-  int32_t *tiles256;   // [max256][2]
+  int32_t *ntiles128;  // [1] number of 128-row tiles
+  int32_t *tiles128;   // [max128][2]
 };
 
 int64_t moe_max_tiles(int64_t routes, int64_t experts, int64_t rows);

@@ -31,6 +31,7 @@
 // is < M only. For
 // tiny N the four waves of a workgroup split the K groups and merge their
 // accumulators through LDS in a fixed order (deterministic).
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -302,22 +303,28 @@ int launch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, int64_t row_tile
 
 }  // namespace
 
-int q4_gemm_lds(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
-                int xt, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
-                const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
-                const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride);
+int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
+               int xt, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
+               const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
+               const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride,
+               void* ws, int64_t ws_bytes);
+int64_t bl_counter_bytes();
 
 namespace {
 
-// Picks the kernel. Up to 256 rows (decode batches, GEMV): the register-direct
-// kernel above with 16-row wave tiles (M/16 row tiles); when that grid would
-// have fewer than 512 workgroups the four waves of a workgroup split K instead
-// of N. Bigger M (prefill / recompute): the LDS-tiled 256x128 kernel in
-// q4_gemm_lds.hip.
-int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st) {
+// Picks the kernel. More than 32 rows (decode batches, prefill, recompute):
+// q4_gemm_bl.hip, which dequantises each weight once per workgroup into LDS
+// (and, given a workspace, splits K when its grid is small), unless its grid
+// would have fewer than 64 workgroups (a narrow N at decode batch size), where
+// the in-workgroup K-split of the kernel above was measured faster. Otherwise (GEMV-like, HBM-bound): the
+// register-direct kernel above with 16-row wave tiles (M/16 row tiles); when
+// that grid would have fewer than 512 workgroups the four waves of a
+// workgroup split K instead of N.
+int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int64_t ws_bytes) {
   const int64_t logical_cols = is_swiglu(epi) ? 2 * (int64_t)a.ncols : a.N;
   const bool ksplit_ok = a.K >= 4 * 128;
-  if (a.M <= 256) {
+  const int64_t bl_wgs = ceil_div(a.M, 64) * ceil_div(logical_cols, 64);
+  if (a.M <= 32 || (a.M <= 256 && bl_wgs < 64)) {
     const int64_t rt = ceil_div(a.M, 16);
     // GEMV-like M: 16-column wave tiles double the workgroup count (SwiGLU
     // needs gate/value block pairs, so it keeps 32).
@@ -330,8 +337,8 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st) {
     if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xt, st, rt);
     return launch_q4<2, 1>(a, epi, xt, st, rt);
   }
-  return q4_gemm_lds(a.codes, a.scales, a.N, a.K, a.x, xt, a.M, a.ldx, a.y, a.ldy, epi,
-                     a.ncols, st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0);
+  return q4_gemm_bl(a.codes, a.scales, a.N, a.K, a.x, xt, a.M, a.ldx, a.y, a.ldy, epi, a.ncols,
+                    st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, ws, ws_bytes);
 }
 
 // ----------------------------------------------------------- quantizer ---
@@ -437,11 +444,29 @@ extern "C" int sm_q4_quantize(const void* w, int dtype, int64_t n, uint8_t* code
   return SM_OK;
 }
 
+extern "C" int64_t sm_q4_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilogue) {
+  (void)K;
+  if (M <= 32 || M > 0x7fffffff || N <= 0) return 0;
+  const int64_t cols = (epilogue >= sm::EPI_SWIGLU_BF16) ? 2 * (N / 2) : N;
+  return sm::bl_counter_bytes() + 8 * M * cols * (int64_t)sizeof(float);
+}
+
 extern "C" int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
                             const void* x, int x_dtype, int64_t M, int64_t ldx, void* y,
                             int64_t ldy, int epilogue, void* stream) {
+  return sm_q4_matmul_ws(codes, scales, N, K, x, x_dtype, M, ldx, y, ldy, epilogue, nullptr, 0,
+                         stream);
+}
+
+extern "C" int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                               const void* x, int x_dtype, int64_t M, int64_t ldx, void* y,
+                               int64_t ldy, int epilogue, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
   using namespace sm;
   SM_REQUIRE(codes && scales && x && y, "sm_q4_matmul: null buffer");
+  SM_REQUIRE(workspace_bytes >= 0 && (workspace || workspace_bytes == 0) &&
+                 reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+             "sm_q4_matmul: bad workspace");
   SM_REQUIRE(K > 0 && K % 128 == 0, "sm_q4_matmul: K=%lld must be a positive multiple of 128",
              (long long)K);
   SM_REQUIRE(N > 0 && N <= 0x7fffffff && K <= 0x7fffffff, "sm_q4_matmul: bad N");
@@ -462,7 +487,7 @@ extern "C" int sm_q4_matmul(const uint8_t* codes, const uint16_t* scales, int64_
   SM_REQUIRE(ldy >= yw && ldy <= 0x7fffffff, "sm_q4_matmul: ldy < output row width");
   if (M == 0) return SM_OK;
   Q4Args a{codes, scales, x, y, (int)M, (int)N, (int)K, (int)ldx, (int)ldy, (int)ncols};
-  return dispatch_q4(a, epilogue, xt, as_stream(stream));
+  return dispatch_q4(a, epilogue, xt, as_stream(stream), workspace, workspace_bytes);
 }
 
 extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts,
@@ -503,7 +528,8 @@ extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales
     if (is_swiglu(epilogue) || K < 4 * 128) return launch_q4<2, 1>(a, epilogue, xt, st, rt);
     return launch_q4<2, 4>(a, epilogue, xt, st, rt);
   }
-  return q4_gemm_lds(codes, scales, (int)N, (int)K, x, xt, (int)routes, (int)ldx,
-                     y, (int)ldy, epilogue, (int)ncols, st, pv.tiles256, pv.ntiles256,
-                     moe_max_tiles(routes, experts, 256), pv.offsets, rowidx, cstride, sstride);
+  return q4_gemm_bl(codes, scales, (int)N, (int)K, x, xt, (int)routes, (int)ldx, y, (int)ldy,
+                    epilogue, (int)ncols, st, pv.tiles128, pv.ntiles128,
+                    moe_max_tiles(routes, experts, 128), pv.offsets, rowidx, cstride, sstride,
+                    nullptr, 0);
 }

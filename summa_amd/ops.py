@@ -201,6 +201,12 @@ class Q4Weight:
         return cls(c, s, n, k)
 
 
+def q4_workspace(m: int, n: int, k: int, epilogue: int, device) -> torch.Tensor:
+    """Device workspace sized by sm_q4_matmul_workspace_bytes."""
+    nbytes = int(_lib.lib().sm_q4_matmul_workspace_bytes(m, n, k, int(epilogue)))
+    return torch.zeros(max(nbytes, 16), dtype=torch.uint8, device=device)
+
+
 def f16_pair(x: torch.Tensor) -> torch.Tensor:
     """fp32 [M, K] -> SM_F16X2 rows [M, 2K] f16: hi = f16(x), lo = f16(x - hi)."""
     hi = x.to(torch.float16)
@@ -235,9 +241,11 @@ def _out_spec(epilogue: int, rows: int, n: int):
 
 
 def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
-              epilogue: int = _lib.SM_EPI_STORE_F32, *, pair: bool = False) -> torch.Tensor:
+              epilogue: int = _lib.SM_EPI_STORE_F32, *, pair: bool = False,
+              workspace: torch.Tensor | None = None) -> torch.Tensor:
     """y = x . W^T with Q4G128 weights; x bf16 or f16 [M, K], or with ``pair``
-    f16 [M, 2K] SM_F16X2 rows (see f16_pair)."""
+    f16 [M, 2K] SM_F16X2 rows (see f16_pair). ``workspace`` (a device byte
+    tensor) lets batch calls split K (sm_q4_matmul_ws)."""
     _dev(x, "x")
     xdt = _x_dtype(x, pair)
     M, K = x.shape
@@ -253,8 +261,14 @@ def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
             raise ValueError("SM_EPI_ADD_F32 needs an output to accumulate into")
         out = torch.empty(shape, dtype=dt, device=x.device)
     _dev(out, "out")
-    call("sm_q4_matmul", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k, x.data_ptr(), xdt,
-         M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
+    if workspace is None:
+        call("sm_q4_matmul", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k, x.data_ptr(),
+             xdt, M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue), _stream())
+    else:
+        _dev(workspace, "workspace")
+        call("sm_q4_matmul_ws", w.tcodes.data_ptr(), w.tscales.data_ptr(), w.n, w.k,
+             x.data_ptr(), xdt, M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue),
+             workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream())
     return out
 
 

@@ -97,13 +97,19 @@ def test_logprob_chunking_is_exact(dev):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("geom", ["cfg1", "cfg2"])
+@pytest.mark.parametrize("geom", ["cfg1", "cfg2", "batch"])
 def test_quantized_rollout_and_logprobs(dev, geom):
+    """cfg1 / cfg2 geometry at small batch; "batch" decodes 128 sequences at
+    once, so every decode matmul runs the batch kernel (with split-K)."""
     print(f"case quantized {geom}", flush=True)
     if geom == "cfg1":
         mc = ModelConfig(layers=2, d_model=768, heads=12, kv_heads=12, head_dim=64, ffn=3072,
                          vocab=32768, max_seq=64, quantized=True)
         S, P, N = 8, 16, 8
+    elif geom == "batch":
+        mc = ModelConfig(layers=2, d_model=768, heads=12, kv_heads=4, head_dim=64, ffn=3072,
+                         vocab=4096, max_seq=64, quantized=True)
+        S, P, N = 128, 8, 4
     else:
         mc = ModelConfig(layers=2, d_model=2048, heads=16, kv_heads=4, head_dim=128, ffn=5632,
                          vocab=4096, max_seq=64, quantized=True)

@@ -97,7 +97,7 @@ def test_route_plan_is_stable_and_invertible(dev, T, k, E, used):
         np.testing.assert_array_equal(inv[order], np.arange(R))
         np.testing.assert_array_equal(plan.src_rows.cpu().numpy(), order // k)
     assert int(plan.error.item()) == 0
-    # device tile lists (16- and 256-row tiles per non-empty expert)
+    # device tile lists (16- and 128-row tiles per non-empty expert)
     w = plan.words.cpu().numpy()
     o = 2 * E + 1 + 3 * R
     m16 = (R + 15) // 16 + E
@@ -105,9 +105,9 @@ def test_route_plan_is_stable_and_invertible(dev, T, k, E, used):
     t16 = [tuple(x) for x in w[o + 1:o + 1 + 2 * n16].reshape(-1, 2)]
     assert t16 == _expected_tiles(counts, 16)
     o2 = o + 1 + 2 * m16
-    n256 = int(w[o2])
-    t256 = [tuple(x) for x in w[o2 + 1:o2 + 1 + 2 * n256].reshape(-1, 2)]
-    assert t256 == _expected_tiles(counts, 256)
+    n128 = int(w[o2])
+    t128 = [tuple(x) for x in w[o2 + 1:o2 + 1 + 2 * n128].reshape(-1, 2)]
+    assert t128 == _expected_tiles(counts, 128)
 
 
 def test_route_plan_flags_bad_expert_index(dev):
@@ -134,7 +134,8 @@ def _bank(E, n, k, seed, dev):
                                           (2500, 8, 8, 256, 256), (3000, 4, 2, 384, 128)])
 @pytest.mark.parametrize("mode", ["swiglu_gather", "store", "pair_swiglu_gather", "pair_store"])
 def test_grouped_matmul_matches_per_expert(dev, T, E, used, n, k, mode):
-    """Routes <= 4096 run the small-M kernel (16-row tiles), more the LDS kernel."""
+    """Routes <= 4096 run the small-M kernel (16-row tiles), more the batch
+    kernel over the plan's 128-row tiles."""
     print(f"case grouped T={T} E={E} n={n} k={k} {mode}", flush=True)
     rng = np.random.default_rng(T * E + n)
     bank, dense = _bank(E, n, k, T + k, dev)

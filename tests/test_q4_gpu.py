@@ -118,11 +118,12 @@ def test_matmul_f16_activations_and_swiglu_f16(dev, m):
     np.testing.assert_allclose(h, g / (1 + np.exp(-g)) * v, rtol=2 ** -10, atol=1e-6)
 
 
-@pytest.mark.parametrize("m,n,k", [(257, 768, 768), (600, 130, 1024), (1000, 2304, 768),
-                                   (2100, 64, 256)])
+@pytest.mark.parametrize("m,n,k", [(33, 768, 768), (257, 768, 768), (600, 130, 1024),
+                                   (1000, 2304, 768), (2100, 64, 256), (1100, 11264, 256)])
 @pytest.mark.parametrize("xdt", ["bf16", "f16"])
 def test_large_m_lds_kernel(dev, m, n, k, xdt):
-    """M > 256 runs the LDS-tiled kernel (XCD-ordered 256x128 tiles, padded M tiles)."""
+    """M > 32 runs the batch kernel (weights dequantised once per workgroup into
+    LDS; XCD-ordered row tiles with padding once there are >= 8 row tiles)."""
     print(f"case m={m} n={n} k={k} x={xdt}", flush=True)
     w = _weights(n, k, m + n)
     codes, scales = oracle.q4_quantize(w)
@@ -161,7 +162,7 @@ def _pair_host(x):
 def test_matmul_f16_pair_activations(dev, m, n, k):
     """SM_F16X2 input (two MFMAs per step on the same codes) and the SwiGLU
     f16-pair epilogue: fp32-grade activations through the f16 MFMA path.
-    m > 256 runs the LDS kernel (hi and lo tiles staged)."""
+    m > 32 runs the batch kernel (two MFMAs per weight fragment)."""
     print(f"case pair m={m} n={n} k={k}", flush=True)
     w = _weights(n, k, m + 7)
     codes, scales = oracle.q4_quantize(w)
@@ -196,3 +197,51 @@ def test_pair_rejects_short_rows(dev):
         _lib.call("sm_q4_matmul", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), 64, 256,
                   x.data_ptr(), _lib.SM_F16X2, 2, 256, y.data_ptr(), 64, 0,
                   torch.cuda.current_stream().cuda_stream)
+
+
+@pytest.mark.parametrize("m,n,k,epi", [(256, 2048, 2048, "add"), (256, 2048, 5632, "add"),
+                                       (200, 1024, 2048, "swiglu"), (256, 1024, 4096, "store")])
+def test_split_k_workspace(dev, m, n, k, epi):
+    """sm_q4_matmul_ws: with a workspace, batch calls that would underfill the
+    GPU split K and reduce fp32 partials in a fixed order (run-to-run exact)."""
+    print(f"case split-k m={m} n={n} k={k} {epi}", flush=True)
+    w = _weights(n, k, m + n + 3)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(m + 5).normal(0, 1, (m, k)).astype(np.float32)
+    xp, xr = _pair_host(x)
+    xd = torch.from_numpy(xp).to(dev)
+    dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+    y_ref = xr.astype(np.float64) @ dense.T
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    e = {"add": _lib.SM_EPI_ADD_F32, "store": _lib.SM_EPI_STORE_F32,
+         "swiglu": _lib.SM_EPI_SWIGLU_F16X2}[epi]
+    ws = ops.q4_workspace(m, n, k, e, dev)
+    ws.zero_()
+    if epi == "swiglu":
+        outs = [ops.unpair(ops.q4_matmul(qw, xd, epilogue=e, pair=True, workspace=ws))
+                for _ in range(2)]
+        torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
+        F = n // 2
+        g, v = y_ref[:, :F], y_ref[:, F:]
+        np.testing.assert_allclose(outs[0].cpu().numpy(), g / (1 + np.exp(-g)) * v,
+                                   rtol=1e-5, atol=2e-6)
+        return
+    base = np.random.default_rng(9).normal(0, 1, (m, n)).astype(np.float32)
+    outs = []
+    for _ in range(2):
+        acc = torch.from_numpy(base.copy()).to(dev)
+        ops.q4_matmul(qw, xd, out=acc, epilogue=e, pair=True, workspace=ws)
+        outs.append(acc.cpu().numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    # a call of another shape on the same workspace leaves nothing behind that
+    # changes the next result
+    other = torch.zeros((m, 128), device=dev)
+    w2 = ops.Q4Weight.from_host(*oracle.q4_quantize(_weights(128, k, 1)), 128, k, dev)
+    ops.q4_matmul(w2, xd, out=other, pair=True, workspace=ws)
+    acc = torch.from_numpy(base.copy()).to(dev)
+    ops.q4_matmul(qw, xd, out=acc, epilogue=e, pair=True, workspace=ws)
+    np.testing.assert_array_equal(acc.cpu().numpy(), outs[0])
+    assert int(ws.int().abs().sum().item()) != 0  # the split really ran
+    expect = (base + y_ref) if epi == "add" else y_ref
+    assert np.all(np.abs(outs[0] - expect) <= tol + 1e-6), float(np.abs(outs[0] - expect).max())
