@@ -91,13 +91,12 @@ struct Q4Args {
 // One workgroup = 16 rows (M tile) x its column tile. NB: 16-column blocks per
 // wave; KSPLIT: 1 = the 4 waves tile N (workgroup tile 16 x 64NB), 4 = the 4
 // waves split the K groups of one 16 x 16NB tile and merge in LDS.
-// Per wave, kU K groups of weights are requested before any is consumed (the
-// M=1 GEMV is nothing but these loads: the more in flight, the closer to HBM
-// rate), and the activation fragments of the next group are fetched while the
-// current one is multiplied.
-constexpr int kU = 8;
+// Per wave, kU K groups of weights are requested before any is consumed, and
+// the activation fragments of the next group are fetched while the current
+// one is multiplied. (For the narrow M=1 GEMV 4 groups measured best: with
+// one 16-column block per wave there are enough waves in flight already.)
 
-template <int NB, int KSPLIT, int EPI, int XT>
+template <int NB, int KSPLIT, int EPI, int XT, int kU>
 __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   constexpr int NA = (XT == X_F16X2) ? 2 : 1;  // A fragments per k-step (hi, lo)
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -258,7 +257,7 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   }
 }
 
-template <int NB, int KSPLIT, int XT>
+template <int NB, int KSPLIT, int XT, int KU = 8>
 int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   const int wave_cols = 16 * NB;
   const int tile_cols = (KSPLIT == 1) ? 4 * wave_cols : wave_cols;
@@ -266,7 +265,7 @@ int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   dim3 grid((unsigned)ceil_div(logical_cols, tile_cols), (unsigned)row_tiles);
   switch (epi) {
 #define SM_Q4_EPI(E) \
-    case E: q4_gemm_kernel<NB, KSPLIT, E, XT><<<grid, 256, 0, st>>>(a); break;
+    case E: q4_gemm_kernel<NB, KSPLIT, E, XT, KU><<<grid, 256, 0, st>>>(a); break;
     SM_Q4_EPI(EPI_STORE_F32)
     SM_Q4_EPI(EPI_STORE_BF16)
     SM_Q4_EPI(EPI_ADD_F32)
@@ -276,11 +275,11 @@ int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
     case EPI_SWIGLU_F16X2:
       if constexpr (NB % 2 == 0) {
         if (epi == EPI_SWIGLU_F16X2)
-          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16X2, XT><<<grid, 256, 0, st>>>(a);
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16X2, XT, KU><<<grid, 256, 0, st>>>(a);
         else if (epi == EPI_SWIGLU_F16)
-          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16, XT><<<grid, 256, 0, st>>>(a);
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_F16, XT, KU><<<grid, 256, 0, st>>>(a);
         else
-          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_BF16, XT><<<grid, 256, 0, st>>>(a);
+          q4_gemm_kernel<NB, KSPLIT, EPI_SWIGLU_BF16, XT, KU><<<grid, 256, 0, st>>>(a);
         break;
       } else {
         set_error("internal: SwiGLU needs an even number of column blocks");
@@ -292,12 +291,12 @@ int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   return SM_OK;
 }
 
-template <int NB, int KSPLIT>
+template <int NB, int KSPLIT, int KU = 8>
 int launch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, int64_t row_tiles) {
   switch (xt) {
-    case X_BF16: return launch_q4_x<NB, KSPLIT, X_BF16>(a, epi, st, row_tiles);
-    case X_F16: return launch_q4_x<NB, KSPLIT, X_F16>(a, epi, st, row_tiles);
-    default: return launch_q4_x<NB, KSPLIT, X_F16X2>(a, epi, st, row_tiles);
+    case X_BF16: return launch_q4_x<NB, KSPLIT, X_BF16, KU>(a, epi, st, row_tiles);
+    case X_F16: return launch_q4_x<NB, KSPLIT, X_F16, KU>(a, epi, st, row_tiles);
+    default: return launch_q4_x<NB, KSPLIT, X_F16X2, KU>(a, epi, st, row_tiles);
   }
 }
 
@@ -332,7 +331,7 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
     const int64_t wgs = ceil_div(logical_cols, narrow ? 64 : 128) * rt;
     if (narrow) {
       if (wgs < 512 && ksplit_ok) return launch_q4<1, 4>(a, epi, xt, st, rt);
-      return launch_q4<1, 1>(a, epi, xt, st, rt);
+      return launch_q4<1, 1, 4>(a, epi, xt, st, rt);  // measured best batch depth for GEMV
     }
     if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xt, st, rt);
     return launch_q4<2, 1>(a, epi, xt, st, rt);
