@@ -18,6 +18,7 @@
 // prefill / recompute (q4_gemm_bl.hip). The token gather is folded into the
 // first grouped matmul's A-operand addressing (row index = src_rows[p]), so
 // routed inputs are never materialised.
+#include <algorithm>
 #include <cmath>
 
 #include "common.hpp"
@@ -47,49 +48,129 @@ PlanView plan_view(int32_t* plan, int64_t routes, int64_t experts) {
 namespace {
 
 constexpr int kRouterThreads = 256;
+constexpr int kRouterLds = 64 * 1024;  // dynamic LDS budget (h rows + logits)
 
-// One workgroup per token: h row -> LDS (f32), each wave computes its share of
-// the E router dot products (lanes over d, wave reduction), then one lane does
-// the strict top-2 scan and the softmax over the pair.
-// TH: f32, f16, or f16 pair (PAIR: row t is hi[d] | lo[d]).
-template <typename TH, bool PAIR = false>
+// One workgroup per TT tokens: their h rows go to LDS (f32), then each wave
+// takes experts e = wave, wave + 4, ...: its lanes stream W_r[e] once
+// (coalesced, c = lane + 64 u, eight loads in flight) and accumulate the dot
+// products of all TT tokens, reduced across the wave in a fixed order; the
+// router weights are read once per TT tokens instead of once per token. One
+// thread per token then does the strict top-2 scan and the softmax over the
+// pair. Rows past the last token repeat the last token (their results are
+// not stored), so the inner loops carry no per-token branches.
+// TH: f32, f16, or f16 pair (PAIR: row t is hi[d] | lo[d]); VEC: d % 64 == 0.
+template <typename TH, bool PAIR, int TT, bool VEC>
 __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
-    const TH* __restrict__ h, const float* __restrict__ wr, int d, int E,
+    const TH* __restrict__ h, const float* __restrict__ wr, int64_t tokens, int d, int E,
     float* __restrict__ logits_out, int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
   extern __shared__ float smem[];
-  float* hs = smem;       // [d]
-  float* lg = smem + d;  // [E]
-  const int64_t t = blockIdx.x;
-  for (int c = threadIdx.x; c < d; c += kRouterThreads) {
-    if constexpr (PAIR) hs[c] = (float)h[t * 2 * d + c] + (float)h[t * 2 * d + d + c];
-    else hs[c] = (float)h[t * d + c];
+  float* hs = smem;            // [TT][d]
+  float* lg = smem + TT * d;   // [TT][E]
+  const int64_t t0 = (int64_t)blockIdx.x * TT;
+#pragma unroll
+  for (int t = 0; t < TT; ++t) {
+    const int64_t r = min<int64_t>(t0 + t, tokens - 1);
+    const TH* row = h + r * (PAIR ? 2 * d : d);
+    if constexpr (VEC && sizeof(TH) == 2) {
+      for (int c8 = threadIdx.x; c8 < d / 8; c8 += kRouterThreads) {
+        const h8 lo8 = *reinterpret_cast<const h8*>(row + 8 * c8);
+        h8 hi8 = h8{0, 0, 0, 0, 0, 0, 0, 0};
+        if constexpr (PAIR) hi8 = *reinterpret_cast<const h8*>(row + d + 8 * c8);
+#pragma unroll
+        for (int u = 0; u < 8; ++u) hs[t * d + 8 * c8 + u] = (float)lo8[u] + (float)hi8[u];
+      }
+    } else {
+      for (int c = threadIdx.x; c < d; c += kRouterThreads) {
+        float v = (float)row[c];
+        if constexpr (PAIR) v += (float)row[d + c];
+        hs[t * d + c] = v;
+      }
+    }
   }
   __syncthreads();
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   for (int e = wave; e < E; e += kRouterThreads / kWave) {
-    float acc = 0.f;
-    for (int c = lane; c < d; c += kWave) acc = fmaf(hs[c], wr[(size_t)e * d + c], acc);
-    acc = wave_sum(acc);
-    if (lane == 0) lg[e] = acc;
+    float acc[TT];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[t] = 0.f;
+    const float* we = wr + (size_t)e * d;
+    if constexpr (VEC) {
+      const int chunks = d / kWave;
+      int ch = 0;
+      for (; ch + 8 <= chunks; ch += 8) {
+        float w[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) w[u] = we[(ch + u) * kWave + lane];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int t = 0; t < TT; ++t)
+            acc[t] = fmaf(hs[t * d + (ch + u) * kWave + lane], w[u], acc[t]);
+      }
+      for (; ch < chunks; ++ch) {
+        const float w = we[ch * kWave + lane];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = fmaf(hs[t * d + ch * kWave + lane], w, acc[t]);
+      }
+    } else {
+      for (int c = lane; c < d; c += kWave) {
+        const float w = we[c];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = fmaf(hs[t * d + c], w, acc[t]);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      const float v = wave_sum(acc[t]);
+      if (lane == 0) lg[t * E + e] = v;
+    }
   }
   __syncthreads();
-  if (threadIdx.x == 0) {
+  if (threadIdx.x < TT && t0 + threadIdx.x < tokens) {
+    const int t = threadIdx.x;
+    const int64_t r = t0 + t;
+    const float* l = lg + t * E;
     float v0 = -INFINITY, v1 = -INFINITY;
     int i0 = 0, i1 = 0;
     for (int e = 0; e < E; ++e) {
-      const float v = lg[e];
+      const float v = l[e];
       if (v > v0) { v1 = v0; i1 = i0; v0 = v; i0 = e; }
       else if (v > v1) { v1 = v; i1 = e; }
     }
     // softmax over [v0, v1] (v0 >= v1)
     const float e1 = expf(v1 - v0);
-    top_idx[t * 2] = i0;
-    top_idx[t * 2 + 1] = i1;
-    top_w[t * 2] = 1.f / (1.f + e1);
-    top_w[t * 2 + 1] = e1 / (1.f + e1);
+    top_idx[r * 2] = i0;
+    top_idx[r * 2 + 1] = i1;
+    top_w[r * 2] = 1.f / (1.f + e1);
+    top_w[r * 2 + 1] = e1 / (1.f + e1);
     if (logits_out)
-      for (int e = 0; e < E; ++e) logits_out[t * E + e] = lg[e];
+      for (int e = 0; e < E; ++e) logits_out[r * E + e] = l[e];
   }
+}
+
+template <typename TH, bool PAIR, int TT>
+void launch_router(const void* h, const float* wr, int64_t tokens, int d, int E, float* lo,
+                   int32_t* idx, float* w, hipStream_t st) {
+  const size_t shmem = (size_t)TT * (d + E) * sizeof(float);
+  const unsigned grid = (unsigned)ceil_div(tokens, TT);
+  const bool vec = d % kWave == 0 && reinterpret_cast<uintptr_t>(h) % 16 == 0;
+  if (vec)
+    router_top2_kernel<TH, PAIR, TT, true><<<grid, kRouterThreads, shmem, st>>>(
+        static_cast<const TH*>(h), wr, tokens, d, E, lo, idx, w);
+  else
+    router_top2_kernel<TH, PAIR, TT, false><<<grid, kRouterThreads, shmem, st>>>(
+        static_cast<const TH*>(h), wr, tokens, d, E, lo, idx, w);
+}
+
+template <typename TH, bool PAIR>
+void launch_router_tt(const void* h, const float* wr, int64_t tokens, int d, int E, float* lo,
+                      int32_t* idx, float* w, hipStream_t st) {
+  // tokens per workgroup: the largest of 8 / 4 / 2 / 1 whose rows fit the LDS budget
+  const int64_t row = (int64_t)(d + E) * sizeof(float);
+  if (8 * row <= kRouterLds) launch_router<TH, PAIR, 8>(h, wr, tokens, d, E, lo, idx, w, st);
+  else if (4 * row <= kRouterLds) launch_router<TH, PAIR, 4>(h, wr, tokens, d, E, lo, idx, w, st);
+  else if (2 * row <= kRouterLds) launch_router<TH, PAIR, 2>(h, wr, tokens, d, E, lo, idx, w, st);
+  else launch_router<TH, PAIR, 1>(h, wr, tokens, d, E, lo, idx, w, st);
 }
 
 // Stable counting sort of the routes by expert in one workgroup. Thread i owns
@@ -209,17 +290,18 @@ extern "C" int sm_moe_router_top2(const void* h, int h_dtype, const float* w_rou
   SM_REQUIRE(experts >= 2, "top-2 routing needs at least two experts");
   SM_REQUIRE(tokens >= 0 && tokens <= 0x7fffffff && d > 0 && d <= 8192 && experts <= kMaxExperts,
              "sm_moe_router_top2: bad shape (d <= 8192, experts <= %d)", kMaxExperts);
+  static_assert(kRouterLds >= (8192 + kMaxExperts) * 4, "one token must fit the router LDS");
   if (tokens == 0) return SM_OK;
-  const size_t shmem = (size_t)(d + experts) * sizeof(float);
+  hipStream_t st = as_stream(stream);
   if (h_dtype == SM_F16X2)
-    router_top2_kernel<_Float16, true><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
-        (const _Float16*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
+    launch_router_tt<_Float16, true>(h, w_router, tokens, (int)d, (int)experts, logits_out,
+                                     top_idx, top_w, st);
   else if (h_dtype == SM_F16)
-    router_top2_kernel<_Float16><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
-        (const _Float16*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
+    launch_router_tt<_Float16, false>(h, w_router, tokens, (int)d, (int)experts, logits_out,
+                                      top_idx, top_w, st);
   else if (h_dtype == SM_F32)
-    router_top2_kernel<float><<<(unsigned)tokens, kRouterThreads, shmem, as_stream(stream)>>>(
-        (const float*)h, w_router, (int)d, (int)experts, logits_out, top_idx, top_w);
+    launch_router_tt<float, false>(h, w_router, tokens, (int)d, (int)experts, logits_out,
+                                   top_idx, top_w, st);
   else SM_REQUIRE(false, "sm_moe_router_top2: h must be f32, f16 or f16 pairs");
   SM_LAUNCH_CHECK();
   return SM_OK;
