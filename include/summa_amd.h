@@ -164,6 +164,20 @@ int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int64_t N, int
                     const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
                     int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
 
+/* qkv projection fused with RoPE and the KV-cache append: y = x . W^T over
+ * the Q4 qkv weight (rows [q heads | k heads | v heads], N = (H + 2 KVH) hd)
+ * for S sequences x L rows (row s*L + i at position pos0[s] + i), then q and
+ * k rotated (adjacent-pair RoPE from rope_table [max_pos, hd/2, 2]) and q
+ * written to q_out [S*L, H, hd], k and v to the caches [S, KVH, cap, hd] at
+ * their positions (positions outside [0, cap) are skipped). Replaces
+ * project_qkv + the AttnCache slice_assign (attention.rs:142-177, 331-356) as
+ * sm_q4_matmul + sm_rope_append would, without the fp32 qkv round trip.
+ * cache_dtype SM_F16; head_dim a power of two >= 16. */
+int sm_q4_qkv_rope(const uint8_t* codes, const uint16_t* scales, int64_t H, int64_t KVH,
+                   int64_t head_dim, int64_t K, const void* x, int x_dtype, int64_t S, int64_t L,
+                   int64_t ldx, const float* rope_table, const int32_t* pos0, int64_t cap,
+                   void* q_out, void* kcache, void* vcache, int cache_dtype, void* stream);
+
 /* Dense fp32 y = x . W^T (fp32 models; matmul::linear, summa-llm/src/model/
  * matmul.rs:57-66). epilogue: SM_EPI_STORE_F32 or SM_EPI_ADD_F32. */
 int sm_gemm_f32(const float* w, int64_t N, int64_t K, const float* x, int64_t M, int64_t ldx,

@@ -31,6 +31,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_q4_pack": (i32, [vp, vp, i64, i64, vp, vp, vp]),
     "sm_q4_matmul": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
     "sm_q4_matmul_workspace_bytes": (i64, [i64, i64, i64, i32]),
+    "sm_q4_qkv_rope": (i32, [vp, vp, i64, i64, i64, i64, vp, i32, i64, i64, i64, vp, vp, i64, vp,
+                             vp, vp, i32, vp]),
     "sm_q4_matmul_ws": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp, i64, vp]),
     "sm_gemm_f32": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
     "sm_swiglu_f32": (i32, [vp, i64, i64, vp, vp]),

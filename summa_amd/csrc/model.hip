@@ -27,6 +27,9 @@
 extern "C" {
 int sm_q4_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
                  int64_t, void*, int64_t, int, void*);
+int sm_q4_qkv_rope(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, int64_t,
+                   const void*, int, int64_t, int64_t, int64_t, const float*, const int32_t*,
+                   int64_t, void*, void*, void*, int, void*);
 int64_t sm_q4_matmul_workspace_bytes(int64_t, int64_t, int64_t, int);
 int sm_q4_matmul_ws(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
                     int64_t, void*, int64_t, int, void*, int64_t, void*);
@@ -274,7 +277,7 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
   const int64_t d = c.d_model;
   SM_TRY(ensure(m->x, (size_t)rows * d * 4));
   SM_TRY(ensure(m->h, (size_t)rows * std::max<int64_t>(d, m->qdim) * m->act_size));
-  SM_TRY(ensure(m->qkv, (size_t)rows * m->qkv_n * 4));
+  if (!c.quantized) SM_TRY(ensure(m->qkv, (size_t)rows * m->qkv_n * 4));
   SM_TRY(ensure(m->qb, (size_t)rows * m->qdim * m->kv_size));
   SM_TRY(ensure(m->attn, (size_t)rows * m->qdim * m->act_size));
   SM_TRY(ensure(m->u, (size_t)rows * c.ffn * m->act_size));
@@ -285,9 +288,15 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
     char* kl = (char*)kc + (size_t)l * layer_elems * m->kv_size;
     char* vl = (char*)vc + (size_t)l * layer_elems * m->kv_size;
     SM_TRY(sm_rmsnorm(x, Ly.attn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
-    SM_TRY(linear_f32out(m, Ly.qkv, m->h.p, rows, (float*)m->qkv.p, false, st));
-    SM_TRY(sm_rope_append((const float*)m->qkv.p, m->rope, pos0, S, L, c.heads, c.kv_heads,
-                          c.head_dim, cap, m->qb.p, m->kvt, kl, vl, m->kvt, st));
+    if (c.quantized) {  // qkv projection with RoPE + cache append in its epilogue
+      SM_TRY(sm_q4_qkv_rope(Ly.qkv.codes, Ly.qkv.scales, c.heads, c.kv_heads, c.head_dim, d,
+                            m->h.p, m->act, S, L, m->act_ld(d), m->rope, pos0, cap, m->qb.p, kl,
+                            vl, m->kvt, st));
+    } else {
+      SM_TRY(linear_f32out(m, Ly.qkv, m->h.p, rows, (float*)m->qkv.p, false, st));
+      SM_TRY(sm_rope_append((const float*)m->qkv.p, m->rope, pos0, S, L, c.heads, c.kv_heads,
+                            c.head_dim, cap, m->qb.p, m->kvt, kl, vl, m->kvt, st));
+    }
     if (decode)
       SM_TRY(sm_attn_decode(m->qb.p, kl, vl, lens, m->attn.p, m->kvt, m->act, S, c.heads,
                             c.kv_heads, cap, c.head_dim, st));

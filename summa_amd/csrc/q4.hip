@@ -36,6 +36,7 @@
 
 #include "common.hpp"
 #include "moe_plan.hpp"
+#include "q4_internal.hpp"
 
 namespace sm {
 namespace {
@@ -302,12 +303,7 @@ int launch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, int64_t row_tile
 
 }  // namespace
 
-int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
-               int xt, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
-               const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
-               const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride,
-               void* ws, int64_t ws_bytes);
-int64_t bl_counter_bytes();
+
 
 namespace {
 
@@ -337,7 +333,7 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
     return launch_q4<2, 1>(a, epi, xt, st, rt);
   }
   return q4_gemm_bl(a.codes, a.scales, a.N, a.K, a.x, xt, a.M, a.ldx, a.y, a.ldy, epi, a.ncols,
-                    st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, ws, ws_bytes);
+                    st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, ws, ws_bytes, nullptr);
 }
 
 // ----------------------------------------------------------- quantizer ---
@@ -530,5 +526,34 @@ extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales
   return q4_gemm_bl(codes, scales, (int)N, (int)K, x, xt, (int)routes, (int)ldx, y, (int)ldy,
                     epilogue, (int)ncols, st, pv.tiles128, pv.ntiles128,
                     moe_max_tiles(routes, experts, 128), pv.offsets, rowidx, cstride, sstride,
-                    nullptr, 0);
+                    nullptr, 0, nullptr);
+}
+
+extern "C" int sm_q4_qkv_rope(const uint8_t* codes, const uint16_t* scales, int64_t H,
+                              int64_t KVH, int64_t head_dim, int64_t K, const void* x,
+                              int x_dtype, int64_t S, int64_t L, int64_t ldx,
+                              const float* rope_table, const int32_t* pos0, int64_t cap,
+                              void* q_out, void* kcache, void* vcache, int cache_dtype,
+                              void* stream) {
+  using namespace sm;
+  SM_REQUIRE(codes && scales && x && rope_table && pos0 && q_out && kcache && vcache,
+             "sm_q4_qkv_rope: null buffer");
+  SM_REQUIRE(cache_dtype == SM_F16, "sm_q4_qkv_rope: the fused path writes f16 q / cache");
+  SM_REQUIRE(H > 0 && KVH > 0 && head_dim >= 16 && (head_dim & (head_dim - 1)) == 0 && cap > 0 &&
+                 S >= 0 && L > 0 && S * L <= 0x7fffffff,
+             "sm_q4_qkv_rope: bad shape (head_dim a power of two >= 16)");
+  SM_REQUIRE(K > 0 && K % 128 == 0, "sm_q4_qkv_rope: K must be a positive multiple of 128");
+  const int xt = xmode_of(x_dtype);
+  SM_REQUIRE(xt >= 0, "sm_q4_qkv_rope: x must be bf16, f16 or f16 pairs");
+  const int64_t xw = (xt == X_F16X2) ? 2 * K : K;
+  SM_REQUIRE(ldx >= xw && ldx % 8 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(codes) % 16 == 0,
+             "sm_q4_qkv_rope: x rows must be 16-byte aligned, >= %lld elements", (long long)xw);
+  const int64_t N = (H + 2 * KVH) * head_dim;
+  if (S == 0) return SM_OK;
+  QkvRope qr{rope_table, pos0, (int)L, (int)cap, (int)H, (int)KVH, (int)head_dim,
+             q_out, kcache, vcache};
+  return q4_gemm_bl(codes, scales, (int)N, (int)K, x, xt, (int)(S * L), (int)ldx, nullptr, 0, 6,
+                    (int)N, as_stream(stream), nullptr, nullptr, 0, nullptr, nullptr, 0, 0,
+                    nullptr, 0, &qr);
 }

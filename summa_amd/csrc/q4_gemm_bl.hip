@@ -26,6 +26,7 @@
 #include <cmath>
 
 #include "common.hpp"
+#include "q4_internal.hpp"
 
 namespace sm {
 namespace {
@@ -57,13 +58,22 @@ struct BLArgs {
   // split order and applies the epilogue.
   float* part;
   int gper;
+  // EPI 6 (qkv projection + RoPE + KV-cache append): row = s*rope_L + i sits
+  // at position pos0[s] + i; columns are [q | k | v] heads of hd.
+  const float2* rope;  // [max_pos][hd/2] (cos, sin)
+  const int32_t* pos0;
+  int rope_L, cap, H, KVH, hd;
+  _Float16* q_out;  // [M][H][hd]
+  _Float16* kc;     // [S][KVH][cap][hd]
+  _Float16* vc;
 };
 
 // EPI: 0 store f32, 1 store bf16, 2 add f32, 3 swiglu bf16, 4 swiglu f16,
-// 5 swiglu f16 pair. XT: 0 bf16 x, 1 f16 x, 2 f16-pair x.
+// 5 swiglu f16 pair, 6 qkv + RoPE + cache append (f16). XT: 0 bf16 x, 1 f16 x,
+// 2 f16-pair x.
 template <int WR, int TN, int EPI, int XT>
 __global__ __launch_bounds__(256, 2) void q4_gemm_bl_kernel(BLArgs a) {
-  constexpr bool SWIGLU = (EPI >= 3);
+  constexpr bool SWIGLU = (EPI >= 3 && EPI <= 5);
   constexpr int NA = (XT == 2) ? 2 : 1;  // A fragments per k-step (hi, lo)
   constexpr int MT = WR / 16;            // 16-row blocks per wave
   constexpr int NBK = TN / 16;           // 16-column blocks per workgroup
@@ -172,6 +182,33 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_bl_kernel(BLArgs a) {
       }
   };
 
+  // EPI 6: the epilogue's positions do not depend on the product: load them
+  // before the main loop (one independent load per row) so their latency is
+  // hidden behind it. Even lanes own pairs (e, e+1).
+  int slot_b[NBK], e_b[NBK];
+  int srow[MT][4], prow[MT][4];
+  float2 cs[MT][4][NBK];
+  if constexpr (EPI == 6) {
+    const int hd_shift = __builtin_ctz(a.hd);
+#pragma unroll
+    for (int b = 0; b < NBK; ++b) {
+      const int col = tn * TN + b * 16 + j;
+      slot_b[b] = col < a.N ? (col >> hd_shift) : -1;
+      e_b[b] = col & (a.hd - 1);
+    }
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m_base + wave * WR + mt * 16 + 4 * g + r;
+        const int rc = min(row, mlim - 1);
+        const int sq = (a.rope_L == 1) ? rc : rc / a.rope_L;
+        const int pos = a.pos0[sq] + (rc - sq * a.rope_L);
+        srow[mt][r] = sq;
+        prow[mt][r] = (row < mlim && pos >= 0 && pos < a.cap) ? pos : -1;
+      }
+  }
+
   f4 acc[MT][NBK];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
@@ -224,6 +261,55 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_bl_kernel(BLArgs a) {
   }
 
   // ---- epilogue: lane holds rows 4g + r of column j in every block
+  if constexpr (EPI == 6) {
+    // RoPE pairs (2p, 2p+1) are adjacent columns, i.e. lanes j and j^1 of the
+    // same rows: swap partners before any lane-dependent branch
+    f4 partner[MT][NBK];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int b = 0; b < NBK; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) partner[mt][b][r] = __shfl_xor(acc[mt][b][r], 1, kWave);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float2* rrow = a.rope + (size_t)max(prow[mt][r], 0) * (a.hd / 2);
+#pragma unroll
+        for (int b = 0; b < NBK; ++b) cs[mt][r][b] = rrow[e_b[b] >> 1];
+      }
+    if ((j & 1) == 0) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int pos = prow[mt][r];
+          if (pos < 0) continue;
+          const int row = m_base + wave * WR + mt * 16 + 4 * g + r, sq = srow[mt][r];
+#pragma unroll
+          for (int b = 0; b < NBK; ++b) {
+            const int slot = slot_b[b], e = e_b[b];
+            if (slot < 0) continue;
+            const float va = acc[mt][b][r], vb = partner[mt][b][r];  // columns e, e+1
+            h2 out;
+            _Float16* dst;
+            if (slot >= a.H + a.KVH) {  // value: no rotation
+              out = h2{(_Float16)va, (_Float16)vb};
+              dst = a.vc + (((size_t)sq * a.KVH + (slot - a.H - a.KVH)) * a.cap + pos) * a.hd + e;
+            } else {
+              const float2 c = cs[mt][r][b];
+              out = h2{(_Float16)(va * c.x - vb * c.y), (_Float16)(vb * c.x + va * c.y)};
+              dst = (slot < a.H)
+                        ? a.q_out + ((size_t)row * a.H + slot) * a.hd + e
+                        : a.kc + (((size_t)sq * a.KVH + (slot - a.H)) * a.cap + pos) * a.hd + e;
+            }
+            *reinterpret_cast<h2*>(dst) = out;
+          }
+        }
+    }
+    return;
+  }
   if (a.part) {  // split-K (uniform branch): partial tile, logical columns
     const int lc_total = SWIGLU ? 2 * a.ncols : a.N;
     float* pp = a.part + (size_t)blockIdx.y * a.M * lc_total;
@@ -338,6 +424,7 @@ int launch_bl(const BLArgs& a, int epi, dim3 grid, hipStream_t st) {
     SM_BL(3)
     SM_BL(4)
     SM_BL(5)
+    SM_BL(6)
 #undef SM_BL
     default: set_error("sm_q4_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
   }
@@ -366,10 +453,23 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
                int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
                const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
                const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride,
-               void* ws, int64_t ws_bytes) {
+               void* ws, int64_t ws_bytes, const QkvRope* qr) {
   BLArgs a{codes, scales, x, y, M, N, K, ldx, ldy, ncols, 0, 0, 0,
            tiles, ntiles, goff, rowidx, cstride, sstride, nullptr, K / 128};
-  const bool swiglu = epi >= 3;
+  if (epi == 6) {
+    a.rope = reinterpret_cast<const float2*>(qr->rope);
+    a.pos0 = qr->pos0;
+    a.rope_L = qr->L;
+    a.cap = qr->cap;
+    a.H = qr->H;
+    a.KVH = qr->KVH;
+    a.hd = qr->hd;
+    a.q_out = static_cast<_Float16*>(qr->q_out);
+    a.kc = static_cast<_Float16*>(qr->kc);
+    a.vc = static_cast<_Float16*>(qr->vc);
+    ws = nullptr;  // the RoPE epilogue needs whole output tiles: no K split
+  }
+  const bool swiglu = epi >= 3 && epi <= 5;
   const int64_t logical_cols = swiglu ? 2 * (int64_t)ncols : N;
   // Tile shape (measured on MI355X over the configs' decode, prefill and
   // recompute shapes): 32 rows per wave (128-row tiles; grouped plan tiles are
@@ -415,7 +515,7 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
   else s = (tn == 128) ? launch_bl_x<32, 128>(a, epi, xt, grid, st)
                        : launch_bl_x<32, 64>(a, epi, xt, grid, st);
   if (s != SM_OK || ks == 1) return s;
-  const int64_t width = (epi >= 3) ? ncols : N;
+  const int64_t width = swiglu ? ncols : N;
   const unsigned rb = (unsigned)ceil_div((int64_t)M * width, 256);
   switch (epi) {
 #define SM_RED(E)                                                                       \

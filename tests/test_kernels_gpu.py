@@ -235,3 +235,41 @@ def test_sample_temperature_distribution(dev):
     counts = np.bincount(tok.cpu().numpy(), minlength=V) / rows
     p = np.exp(base / T) / np.exp(base / T).sum()
     assert np.all(np.abs(counts - p) < 0.015), (counts, p)
+
+
+@pytest.mark.parametrize("S,L,p0,H,KVH,hd,K", [(64, 1, 37, 12, 12, 64, 768), (2, 40, 3, 16, 4, 128, 512),
+                                               (3, 5, 0, 4, 2, 64, 256), (1, 1, 70, 4, 4, 64, 256)])
+def test_qkv_rope_fused_matches_separate(dev, S, L, p0, H, KVH, hd, K):
+    """sm_q4_qkv_rope == sm_q4_matmul (f16 pairs) followed by sm_rope_append:
+    the same f16 q / cache values up to one f16 rounding step (the two paths
+    may accumulate the projection in different kernels)."""
+    from summa_amd import ops
+    print(f"case qkv-rope S={S} L={L} p0={p0} H={H} KVH={KVH} hd={hd} K={K}", flush=True)
+    N = (H + 2 * KVH) * hd
+    rng = np.random.default_rng(S + L + K)
+    w = rng.normal(0, 0.02, (N, K)).astype(np.float32)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, N, K, dev)
+    x = torch.from_numpy(rng.normal(0, 1, (S * L, K)).astype(np.float32)).to(dev)
+    xp = ops.f16_pair(x)
+    cap = p0 + L + 2
+    tab = torch.from_numpy(_rope_table(cap, hd)).to(dev)
+    pos0 = torch.full((S,), p0, dtype=torch.int32, device=dev)
+    outs = []
+    for fused in (True, False):
+        q = torch.zeros(S * L, H, hd, dtype=torch.float16, device=dev)
+        kc = torch.zeros(S, KVH, cap, hd, dtype=torch.float16, device=dev)
+        vc = torch.zeros(S, KVH, cap, hd, dtype=torch.float16, device=dev)
+        if fused:
+            call("sm_q4_qkv_rope", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), H, KVH, hd, K,
+                 xp.data_ptr(), SM_F16X2, S, L, xp.stride(0), tab.data_ptr(), pos0.data_ptr(),
+                 cap, q.data_ptr(), kc.data_ptr(), vc.data_ptr(), SM_F16, _s())
+        else:
+            y = ops.q4_matmul(qw, xp, pair=True)
+            call("sm_rope_append", y.data_ptr(), tab.data_ptr(), pos0.data_ptr(), S, L, H, KVH,
+                 hd, cap, q.data_ptr(), SM_F16, kc.data_ptr(), vc.data_ptr(), SM_F16, _s())
+        outs.append([t.float().cpu().numpy() for t in (q, kc, vc)])
+    for a, b in zip(*outs):
+        np.testing.assert_allclose(a, b, rtol=2 ** -10, atol=1e-6)
+    # untouched cache positions stay zero
+    assert np.all(outs[0][1][:, :, :p0] == 0) and np.all(outs[0][1][:, :, p0 + L:] == 0)
