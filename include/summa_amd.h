@@ -224,6 +224,14 @@ int sm_attn_decode(const void* q, const void* kcache, const void* vcache, const 
 int sm_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* pos0,
                     void* out, int dtype, int out_dtype, int64_t S, int64_t L, int64_t H,
                     int64_t KVH, int64_t cap, int64_t head_dim, void* stream);
+/* Same, also writing the per-row log-sum-exp of the scaled, masked scores
+ * (natural log) to lse [S*H, L] f32 (nullable): the convention of the flash
+ * forward and attention_log_sum_exp (fused_attention.rs:166-172), which the
+ * attention backward consumes. */
+int sm_attn_prefill_lse(const void* q, const void* kcache, const void* vcache,
+                        const int32_t* pos0, void* out, float* lse, int dtype, int out_dtype,
+                        int64_t S, int64_t L, int64_t H, int64_t KVH, int64_t cap,
+                        int64_t head_dim, void* stream);
 
 /* Next-token selection for `rows` logits rows (select_next_token /
  * sample_from_logits, summa-llm/src/generate.rs:127-202). temperature <= 0:

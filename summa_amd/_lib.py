@@ -41,6 +41,7 @@ SIGNATURES: dict[str, tuple] = {
     "sm_rope_append": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i64, vp, i32, vp, vp, i32, vp]),
     "sm_attn_decode": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, vp]),
     "sm_attn_prefill": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
+    "sm_attn_prefill_lse": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_sample": (i32, [vp, i64, i64, i64, f32, u64, i64, vp, i64, vp, i64, vp, vp]),
     "sm_moe_plan_words": (i64, [i64, i64, i64]),
     "sm_moe_router_top2": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, vp]),

@@ -192,7 +192,8 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 template <int HD>
 __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
-    const int32_t* __restrict__ pos0, int pos_off, float* __restrict__ out, int S, int L, int H,
+    const int32_t* __restrict__ pos0, int pos_off, float* __restrict__ out,
+    float* __restrict__ lse, int S, int L, int H,
     int KVH, int cap, float scale) {
   constexpr int hd = HD;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -225,19 +226,20 @@ __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
   }
 #pragma unroll
   for (int d = 0; d < hd; ++d) op[d] = acc[d] / l;
+  if (lse) lse[((size_t)s * H + h) * L + r] = m + logf(l);
 }
 
 int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_t* pos0,
-                  int pos_off, float* out, int S, int L, int H, int KVH, int cap, int hd,
-                  hipStream_t st) {
+                  int pos_off, float* out, float* lse, int S, int L, int H, int KVH, int cap,
+                  int hd, hipStream_t st) {
   const int64_t n = (int64_t)S * L * H;
   if (n == 0) return SM_OK;
   const unsigned blocks = (unsigned)ceil_div(n, 256);
   const float scale = 1.0f / sqrtf((float)hd);
   if (hd == 64)
-    attn_valu_f32_kernel<64><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, S, L, H, KVH, cap, scale);
+    attn_valu_f32_kernel<64><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, H, KVH, cap, scale);
   else if (hd == 128)
-    attn_valu_f32_kernel<128><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, S, L, H, KVH, cap, scale);
+    attn_valu_f32_kernel<128><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, H, KVH, cap, scale);
   else {
     set_error("f32 attention: head_dim must be 64 or 128 (got %d)", hd);
     return SM_ERR_UNSUPPORTED;
@@ -249,8 +251,8 @@ int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_
 }  // namespace
 
 int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                    const int32_t* pos0, void* out, bool kf16, int om, int S, int L, int H,
-                    int KVH, int cap, int hd, hipStream_t st);
+                    const int32_t* pos0, void* out, float* lse, bool kf16, int om, int S, int L,
+                    int H, int KVH, int cap, int hd, hipStream_t st);
 
 inline int out_mode(int out_dtype) {
   return out_dtype == SM_BF16 ? 0 : out_dtype == SM_F16 ? 1 : out_dtype == SM_F16X2 ? 2 : -1;
@@ -274,7 +276,7 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
   if (dtype == SM_F32) {
     SM_REQUIRE(out_dtype == SM_F32, "sm_attn_decode: f32 attention writes f32");
     return attn_valu_f32((const float*)q, (const float*)kcache, (const float*)vcache, lens, -1,
-                         (float*)out, (int)S, 1, (int)H, (int)KVH, (int)cap, (int)head_dim, st);
+                         (float*)out, nullptr, (int)S, 1, (int)H, (int)KVH, (int)cap, (int)head_dim, st);
   }
   SM_REQUIRE(dtype == SM_BF16 || dtype == SM_F16,
              "sm_attn_decode: dtype must be SM_BF16, SM_F16 or SM_F32");
@@ -313,10 +315,23 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
   return SM_OK;
 }
 
+extern "C" int sm_attn_prefill_lse(const void* q, const void* kcache, const void* vcache,
+                                   const int32_t* pos0, void* out, float* lse, int dtype,
+                                   int out_dtype, int64_t S, int64_t L, int64_t H, int64_t KVH,
+                                   int64_t cap, int64_t head_dim, void* stream);
+
 extern "C" int sm_attn_prefill(const void* q, const void* kcache, const void* vcache,
                                const int32_t* pos0, void* out, int dtype, int out_dtype,
                                int64_t S, int64_t L, int64_t H, int64_t KVH, int64_t cap,
                                int64_t head_dim, void* stream) {
+  return sm_attn_prefill_lse(q, kcache, vcache, pos0, out, nullptr, dtype, out_dtype, S, L, H, KVH,
+                             cap, head_dim, stream);
+}
+
+extern "C" int sm_attn_prefill_lse(const void* q, const void* kcache, const void* vcache,
+                                   const int32_t* pos0, void* out, float* lse, int dtype,
+                                   int out_dtype, int64_t S, int64_t L, int64_t H, int64_t KVH,
+                                   int64_t cap, int64_t head_dim, void* stream) {
   using namespace sm;
   SM_REQUIRE(q && kcache && vcache && pos0 && out, "sm_attn_prefill: null buffer");
   SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && H % KVH == 0,
@@ -328,7 +343,7 @@ extern "C" int sm_attn_prefill(const void* q, const void* kcache, const void* vc
   if (dtype == SM_F32) {
     SM_REQUIRE(out_dtype == SM_F32, "sm_attn_prefill: f32 attention writes f32");
     return attn_valu_f32((const float*)q, (const float*)kcache, (const float*)vcache, pos0, 0,
-                         (float*)out, (int)S, (int)L, (int)H, (int)KVH, (int)cap, (int)head_dim,
+                         (float*)out, lse, (int)S, (int)L, (int)H, (int)KVH, (int)cap, (int)head_dim,
                          st);
   }
   SM_REQUIRE(dtype == SM_BF16 || dtype == SM_F16,
@@ -336,6 +351,6 @@ extern "C" int sm_attn_prefill(const void* q, const void* kcache, const void* vc
   const int om = out_mode(out_dtype);
   SM_REQUIRE(om >= 0, "sm_attn_prefill: 16-bit attention writes bf16, f16 or f16 pairs");
   return attn_prefill_16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
-                         pos0, out, dtype == SM_F16, om, (int)S, (int)L, (int)H, (int)KVH,
+                         pos0, out, lse, dtype == SM_F16, om, (int)S, (int)L, (int)H, (int)KVH,
                          (int)cap, (int)head_dim, st);
 }

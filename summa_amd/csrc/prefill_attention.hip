@@ -32,7 +32,8 @@ template <int HD, bool KF16, int OM>
 __global__ __launch_bounds__(256) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos0,
-    void* __restrict__ out, int L, int H, int KVH, int cap, float scale) {
+    void* __restrict__ out, float* __restrict__ lse, int L, int H, int KVH, int cap,
+    float scale) {
   typedef typename Op8<KF16>::T op8;
   constexpr int STEPS = HD / 32;
   constexpr int KP = HD + 8;   // padded K row (elements)
@@ -168,6 +169,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
   for (int r = 0; r < 4; ++r) {
     const int row = r0 + 4 * g + r;
     if (row >= L) continue;
+    // log-sum-exp of the scaled, masked scores, [S*H, L] (fused_attention.rs:166-172)
+    if (lse && j == 0) lse[((size_t)s * H + h) * L + row] = m[r] + logf(l[r]);
     const float inv = 1.f / l[r];
 #pragma unroll
     for (int d = 0; d < HD / 16; ++d)
@@ -178,8 +181,8 @@ __global__ __launch_bounds__(256) void attn_prefill_kernel(
 }  // namespace
 
 int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
-                    const int32_t* pos0, void* out, bool kf16, int om, int S, int L, int H,
-                    int KVH, int cap, int hd, hipStream_t st) {
+                    const int32_t* pos0, void* out, float* lse, bool kf16, int om, int S, int L,
+                    int H, int KVH, int cap, int hd, hipStream_t st) {
   if (S > 65535 || H > 65535) {
     set_error("sm_attn_prefill: S and H must be <= 65535");
     return SM_ERR_UNSUPPORTED;
@@ -187,7 +190,7 @@ int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
   const dim3 grid((unsigned)ceil_div(L, 64), (unsigned)H, (unsigned)S);
   const float scale = 1.0f / sqrtf((float)hd);
 #define SM_PF3(HD, KF, OM)                                                                \
-  attn_prefill_kernel<HD, KF, OM><<<grid, 256, 0, st>>>(q, kc, vc, pos0, out, L, H, KVH, cap, \
+  attn_prefill_kernel<HD, KF, OM><<<grid, 256, 0, st>>>(q, kc, vc, pos0, out, lse, L, H, KVH, cap, \
                                                         scale)
 #define SM_PF2(HD, KF)                          \
   do {                                          \

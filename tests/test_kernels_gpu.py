@@ -273,3 +273,36 @@ def test_qkv_rope_fused_matches_separate(dev, S, L, p0, H, KVH, hd, K):
         np.testing.assert_allclose(a, b, rtol=2 ** -10, atol=1e-6)
     # untouched cache positions stay zero
     assert np.all(outs[0][1][:, :, :p0] == 0) and np.all(outs[0][1][:, :, p0 + L:] == 0)
+
+
+@pytest.mark.parametrize("dtype", [SM_F16, SM_F32])
+def test_attn_prefill_lse(dev, dtype):
+    """sm_attn_prefill_lse: log-sum-exp of the scaled, masked scores, [S*H, L]
+    (fused_attention.rs:166-172), next to the same output as sm_attn_prefill."""
+    S, L, p0, H, KVH, hd = 2, 70, 5, 8, 2, 64
+    rng = np.random.default_rng(11)
+    cap = p0 + L
+    q, k, v = (rng.normal(0, 1, sh).astype(np.float32)
+               for sh in ((S, L, H, hd), (S, KVH, cap, hd), (S, KVH, cap, hd)))
+    if dtype == SM_F16:
+        q, k, v = (a.astype(np.float16).astype(np.float32) for a in (q, k, v))
+        qd, kd, vd = (_f16(a, dev) for a in (q, k, v))
+        out = torch.empty(S * L, 2 * H * hd, dtype=torch.float16, device=dev)
+        od = SM_F16X2
+    else:
+        qd, kd, vd = (torch.from_numpy(a).to(dev) for a in (q, k, v))
+        out = torch.empty(S, L, H, hd, device=dev)
+        od = SM_F32
+    pos0 = torch.full((S,), p0, dtype=torch.int32, device=dev)
+    lse = torch.empty(S * H, L, device=dev)
+    call("sm_attn_prefill_lse", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), pos0.data_ptr(),
+         out.data_ptr(), lse.data_ptr(), dtype, od, S, L, H, KVH, cap, hd, _s())
+    got = lse.cpu().numpy().reshape(S, H, L)
+    for s in range(S):
+        for h in range(H):
+            kv = h // (H // KVH)
+            sc = q[s, :, h].astype(np.float64) @ k[s, kv].T.astype(np.float64) / np.sqrt(hd)
+            sc[np.arange(cap)[None, :] > (p0 + np.arange(L))[:, None]] = -np.inf
+            m = sc.max(1)
+            ref = m + np.log(np.exp(sc - m[:, None]).sum(1))
+            np.testing.assert_allclose(got[s, h], ref, rtol=1e-5, atol=1e-5)
