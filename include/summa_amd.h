@@ -244,6 +244,45 @@ int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t vocab, floa
               uint64_t seed, int64_t step, int32_t* tokens, int64_t tok_stride, float* logprobs,
               int64_t lp_stride, int32_t* next_ids, void* stream);
 
+/* Sampling options of a rollout (SamplingConfig, summa-llm/src/generate.rs:12-23,
+ * and RolloutSampling, summa-train/src/posttrain.rs:353-387). */
+typedef struct sm_sampling {
+  float temperature;        /* <= 0: greedy; NaN is rejected */
+  int32_t top_k;            /* < 0: off (None); 0 is rejected; k >= 1 samples among the k
+                               largest logits (value, then lowest index) */
+  float repetition_penalty; /* 1: off; must be finite and >= 1 */
+  int32_t eos_token;        /* -1: none */
+  float top_p;              /* must be finite and in (0, 1] (RolloutSampling::validate) */
+  int32_t apply_top_p;      /* 0: top_p is validated only, as in the reference, which has no
+                               nucleus sampler; 1: keep the smallest value-ordered prefix of the
+                               candidates whose softmax(logits / T) mass reaches top_p */
+} sm_sampling;
+
+/* Next-token selection with the full option set (select_next_token,
+ * apply_repetition_penalty, sample_from_values; generate.rs:127-250).
+ * Per row: the penalty divides (positive) or multiplies (negative) the logit of
+ * every token set in seen[r] (a bitmap [rows, seen_ld] u32, bit v of word v/32;
+ * required when the penalty is on), then greedy argmax (lowest index on ties) or
+ * a Gumbel-max draw among the top-k / nucleus candidates with the counter RNG of
+ * sm_sample (with the options off, the draw equals sm_sample's). The chosen
+ * token is set in seen (when non-null). done [rows] (nullable, needs eos_token):
+ * a row with done != 0 emits eos_token with log-prob 0; a row that emits
+ * eos_token gets done = 1 and lengths[r] (nullable) = step + 1.
+ * logprobs <- log_softmax(logits)[token] of the raw logits. Validation errors
+ * carry the reference's messages ("top_k must be >= 1 (got 0)", "temperature
+ * must not be NaN", "repetition_penalty must be finite and >= 1 (got x)",
+ * "rollout top_p must be finite and in (0, 1]"). */
+int sm_sample_ex(const float* logits, int64_t rows, int64_t ld, int64_t vocab,
+                 const sm_sampling* sampling, uint64_t seed, int64_t step, uint32_t* seen,
+                 int64_t seen_ld, int32_t* done, int32_t* lengths, int32_t* tokens,
+                 int64_t tok_stride, float* logprobs, int64_t lp_stride, int32_t* next_ids,
+                 void* stream);
+/* seen[r] |= {ids[r, 0..n)} (ids [rows, ids_ld] int32; ids outside [0, vocab)
+ * mark nothing); clear != 0 zeroes the rows first. The prior_tokens set of
+ * apply_repetition_penalty (generate.rs:155-182). */
+int sm_seen_tokens(const int32_t* ids, int64_t rows, int64_t n, int64_t ids_ld, int64_t vocab,
+                   uint32_t* seen, int64_t seen_ld, int clear, void* stream);
+
 /* ------------------------------------------------------------------------
  * Top-2 mixture of experts (SparseMoe::forward, summa-llm/src/model/ffn.rs:
  * 478-711), all on the device with no host round trip.
@@ -338,6 +377,15 @@ int sm_model_init_random(sm_model* model, uint64_t seed, float std, void* stream
 int sm_rl_generate(sm_model* model, const int32_t* prompts, int64_t S, int64_t P, int64_t N,
                    float temperature, uint64_t seed, int32_t* tokens, float* behavior_lp,
                    void* stream);
+/* Same with the full sampling options (TextGenerator::generate, generate.rs:68-124,
+ * for S rollouts at once): the repetition penalty counts the prompt and every
+ * generated token of the rollout; a rollout that emits eos_token stops (its later
+ * tokens are eos_token with behavior log-prob 0, lengths[s] = tokens generated
+ * including the EOS; N when none), and the loop ends once every rollout has
+ * stopped (checked every 16 steps). lengths [S] int32 nullable. */
+int sm_rl_generate_ex(sm_model* model, const int32_t* prompts, int64_t S, int64_t P, int64_t N,
+                      const sm_sampling* sampling, uint64_t seed, int32_t* tokens,
+                      float* behavior_lp, int32_t* lengths, void* stream);
 /* Log-prob recompute (padded_group_log_probabilities /
  * equal_length_continuation_log_probabilities, tensor_sleep.rs:2531-2689):
  * lp_out[s, n] = log_softmax(model(prompt ‖ tokens[:, :N-1]))[P-1+n][tokens[s, n]].

@@ -77,7 +77,16 @@ def _declare_model(L: C.CDLL) -> None:
     L.or_sample.argtypes = [vp, i64, i64, C.c_float, C.c_uint64, i64, vp, i64, vp, i64]
     L.or_generate.argtypes = [C.POINTER(OrModel), vp, i32, i32, i32, C.c_float, C.c_uint64, vp, vp]
     L.or_logprobs.argtypes = [C.POINTER(OrModel), vp, vp, i32, i32, i32, vp]
-    for n in ("or_model_forward", "or_model_logits", "or_sample", "or_generate", "or_logprobs"):
+    f32 = C.c_float
+    L.or_apply_penalty.argtypes = [vp, i64, vp, i64, f32]
+    L.or_apply_penalty.restype = i32
+    L.or_sample_ex_row.argtypes = [vp, i64, f32, i32, f32, f32, i32, C.c_uint64, i64, i64, vp, i64,
+                                   vp, vp]
+    L.or_sample_ex_row.restype = i32
+    L.or_generate_ex.argtypes = [C.POINTER(OrModel), vp, i32, i32, i32, f32, i32, f32, f32, i32,
+                                 i32, C.c_uint64, vp, vp, vp]
+    for n in ("or_model_forward", "or_model_logits", "or_sample", "or_generate", "or_logprobs",
+              "or_generate_ex"):
         getattr(L, n).restype = None
 
 
@@ -250,6 +259,20 @@ class HostModel:
                           tok.ctypes.data, lp.ctypes.data)
         return tok, lp
 
+    def generate_ex(self, prompts, N, *, temperature=0.0, top_k=-1, repetition_penalty=1.0,
+                    top_p=1.0, apply_top_p=False, eos_token=-1, seed=0):
+        """``or_generate_ex``: rollouts with the full sampling options;
+        returns (tokens [S, N], log-probs [S, N] f64, lengths [S])."""
+        prompts = np.ascontiguousarray(prompts, dtype=np.int32)
+        S, P = prompts.shape
+        tok = np.empty((S, N), np.int32)
+        lp = np.empty((S, N), np.float64)
+        lens = np.empty(S, np.int32)
+        lib().or_generate_ex(C.byref(self.m), prompts.ctypes.data, S, P, N, temperature, top_k,
+                             repetition_penalty, top_p, int(apply_top_p), eos_token, seed,
+                             tok.ctypes.data, lp.ctypes.data, lens.ctypes.data)
+        return tok, lp, lens
+
     def logprobs(self, prompts, tokens):
         prompts = np.ascontiguousarray(prompts, dtype=np.int32)
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
@@ -298,6 +321,37 @@ def sample(logits, temperature, seed, step):
     lp = np.empty(rows, np.float64)
     lib().or_sample(logits.ctypes.data, rows, V, temperature, seed, step, tok.ctypes.data, 1,
                     lp.ctypes.data, 1)
+    return tok, lp
+
+
+def apply_penalty(values, prior, penalty):
+    """``or_apply_penalty`` on a copy of ``values`` (apply_repetition_penalty)."""
+    v = np.array(values, dtype=np.float32)
+    pr = np.ascontiguousarray(prior, dtype=np.int32)
+    if lib().or_apply_penalty(v.ctypes.data, v.size, pr.ctypes.data, pr.size, penalty) != 0:
+        raise ValueError("token id outside the model vocabulary")
+    return v
+
+
+def sample_ex(logits, *, temperature, seed, step, top_k=-1, repetition_penalty=1.0, top_p=1.0,
+              apply_top_p=False, prior=None, row0=0):
+    """``or_sample_ex_row`` per row. prior: list (per row) of prior token ids;
+    row r draws from the counter stream of row ``row0 + r``."""
+    logits = np.ascontiguousarray(logits, dtype=np.float32)
+    rows, V = logits.shape
+    tok = np.empty(rows, np.int32)
+    lp = np.empty(rows, np.float64)
+    for r in range(rows):
+        pr = np.ascontiguousarray(prior[r] if prior is not None else [], dtype=np.int32)
+        t = np.empty(1, np.int32)
+        l = np.empty(1, np.float64)
+        rc = lib().or_sample_ex_row(logits[r].ctypes.data, V, temperature, top_k,
+                                    repetition_penalty, top_p, int(apply_top_p), seed, row0 + r,
+                                    step,
+                                    pr.ctypes.data, pr.size, t.ctypes.data, l.ctypes.data)
+        if rc != 0:
+            raise ValueError("token id outside the model vocabulary")
+        tok[r], lp[r] = t[0], l[0]
     return tok, lp
 
 

@@ -340,6 +340,152 @@ void or_generate(const or_model* m, const int32_t* prompts, int S, int P, int N,
   free(kc); free(vc); free(x); free(last); free(logits); free(ids);
 }
 
+/* apply_repetition_penalty (generate.rs:155-182): every distinct token of
+ * prior[0..n) has its value divided by p (>= 0) or multiplied by p (< 0),
+ * once. Returns -1 (and changes nothing further) for a token outside [0, V). */
+int or_apply_penalty(float* values, int64_t V, const int32_t* prior, int64_t n, float penalty) {
+  if (penalty == 1.0f) return 0;
+  unsigned char* seen = calloc((size_t)V, 1);
+  int rc = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    const int32_t t = prior[i];
+    if (t < 0 || t >= V) { rc = -1; break; }
+    if (seen[t]) continue;
+    seen[t] = 1;
+    values[t] = values[t] < 0.0f ? values[t] * penalty : values[t] / penalty;
+  }
+  free(seen);
+  return rc;
+}
+
+/* f32::total_cmp as an unsigned key. */
+static uint32_t total_key(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+static const float* g_sort_vals;
+/* value descending (total order), then index ascending (generate.rs:218-225) */
+static int by_value_desc(const void* a, const void* b) {
+  const int32_t i = *(const int32_t*)a, j = *(const int32_t*)b;
+  const uint32_t ki = total_key(g_sort_vals[i]), kj = total_key(g_sort_vals[j]);
+  if (ki != kj) return ki > kj ? -1 : 1;
+  return i < j ? -1 : (i > j);
+}
+
+/* select_next_token with the full option set (generate.rs:127-250), one row:
+ * penalty over prior[0..n), greedy max (lowest index on ties) or a Gumbel-max
+ * draw (the device counter stream) among the top_k (top_k <= 0: all) largest,
+ * optionally narrowed to the smallest value-ordered prefix whose 2^-32
+ * fixed-point softmax(val / T) mass reaches ceil(top_p * total) (apply_top_p;
+ * the reference validates top_p but has no nucleus sampler: parity unpinned,
+ * checked against the definition in the tests). lp = log_softmax(raw)[token]. */
+int or_sample_ex_row(const float* logits, int64_t V, float temperature, int top_k, float penalty,
+                     float top_p, int apply_top_p, uint64_t seed, int64_t row, int64_t step,
+                     const int32_t* prior, int64_t n, int32_t* tok, double* lp) {
+  float* val = malloc(sizeof(float) * V);
+  memcpy(val, logits, sizeof(float) * V);
+  if (or_apply_penalty(val, V, prior, n, penalty) != 0) { free(val); return -1; }
+  int best_i = 0;
+  if (temperature <= 0.0f) {
+    uint32_t bk = 0;
+    int have = 0;
+    for (int64_t v = 0; v < V; ++v) {
+      const uint32_t k = total_key(val[v]);
+      if (!have || k > bk) { bk = k; best_i = (int)v; have = 1; }
+    }
+  } else {
+    int32_t* idx = malloc(sizeof(int32_t) * V);
+    for (int64_t v = 0; v < V; ++v) idx[v] = (int32_t)v;
+    g_sort_vals = val;
+    qsort(idx, (size_t)V, sizeof(int32_t), by_value_desc);
+    int64_t nc = (top_k > 0 && top_k < V) ? top_k : V;
+    const float inv_t = 1.0f / temperature;
+    if (apply_top_p && top_p < 1.0f) {
+      const float mx = val[idx[0]];
+      uint64_t* q = malloc(sizeof(uint64_t) * nc);
+      uint64_t total = 0;
+      for (int64_t i = 0; i < nc; ++i) {
+        const float w = expf((val[idx[i]] - mx) * inv_t);
+        q[i] = w > 0.0f ? (uint64_t)(w * 4294967296.0f) : 0;
+        total += q[i];
+      }
+      double x = ceil((double)top_p * (double)total);
+      uint64_t tgt = x < 1.0 ? 1 : (uint64_t)x;
+      if (tgt > total) tgt = total;
+      uint64_t cum = 0;
+      int64_t keep = 0;
+      while (keep < nc && cum < tgt) cum += q[keep++];
+      if (keep == 0) keep = 1;
+      nc = keep;
+      free(q);
+    }
+    unsigned char* cand = calloc((size_t)V, 1);
+    for (int64_t i = 0; i < nc; ++i) cand[idx[i]] = 1;
+    float best = -INFINITY;
+    best_i = -1;
+    for (int64_t v = 0; v < V; ++v) {
+      if (!cand[v]) continue;
+      const float u = u01(rng_key(seed, (uint64_t)row, (uint64_t)step * (uint64_t)V + (uint64_t)v));
+      const float key = val[v] * inv_t - logf(-logf(u));
+      if (key > best) { best = key; best_i = (int)v; }
+    }
+    if (best_i < 0) best_i = 0;
+    free(cand);
+    free(idx);
+  }
+  double mx = -INFINITY, s = 0.0;
+  for (int64_t v = 0; v < V; ++v) if (logits[v] > mx) mx = logits[v];
+  for (int64_t v = 0; v < V; ++v) s += exp((double)logits[v] - mx);
+  *tok = best_i;
+  if (lp) *lp = (double)logits[best_i] - (mx + log(s));
+  free(val);
+  return 0;
+}
+
+/* TextGenerator::generate (generate.rs:68-124) for S rollouts with the full
+ * options: the penalty sees prompt + generated tokens; a rollout stops at
+ * eos (>= 0): its later tokens are eos with lp 0, lengths = tokens generated
+ * including the EOS (N when none). */
+void or_generate_ex(const or_model* m, const int32_t* prompts, int S, int P, int N,
+                    float temperature, int top_k, float penalty, float top_p, int apply_top_p,
+                    int eos, uint64_t seed, int32_t* tokens, double* lp, int32_t* lengths) {
+  const int cap = P + N - 1, d = m->d;
+  const size_t cache = (size_t)m->layers * S * m->KVH * cap * m->hd;
+  float* kc = calloc(cache, sizeof(float));
+  float* vc = calloc(cache, sizeof(float));
+  float* x = malloc(sizeof(float) * (size_t)S * P * d);
+  float* last = malloc(sizeof(float) * (size_t)S * d);
+  float* logits = malloc(sizeof(float) * (size_t)S * m->V);
+  int32_t* ids = malloc(sizeof(int32_t) * S);
+  int32_t* hist = malloc(sizeof(int32_t) * (size_t)S * (P + N));
+  int* done = calloc((size_t)S, sizeof(int));
+  for (int s = 0; s < S; ++s) {
+    memcpy(hist + (size_t)s * (P + N), prompts + (size_t)s * P, sizeof(int32_t) * P);
+    lengths[s] = N;
+  }
+  or_model_forward(m, prompts, S, P, 0, kc, vc, cap, x);
+  for (int s = 0; s < S; ++s) memcpy(last + (size_t)s * d, x + ((size_t)s * P + P - 1) * d, sizeof(float) * d);
+  for (int t = 0; t < N; ++t) {
+    if (t > 0) {
+      for (int s = 0; s < S; ++s) ids[s] = tokens[(size_t)s * N + t - 1];
+      or_model_forward(m, ids, S, 1, P + t - 1, kc, vc, cap, last);
+    }
+    or_model_logits(m, last, S, logits);
+    for (int s = 0; s < S; ++s) {
+      int32_t* out = tokens + (size_t)s * N + t;
+      double* lo = lp ? lp + (size_t)s * N + t : NULL;
+      if (done[s]) { *out = eos; if (lo) *lo = 0.0; continue; }
+      or_sample_ex_row(logits + (size_t)s * m->V, m->V, temperature, top_k, penalty, top_p,
+                       apply_top_p, seed, s, t, hist + (size_t)s * (P + N), P + t, out, lo);
+      hist[(size_t)s * (P + N) + P + t] = *out;
+      if (eos >= 0 && *out == eos) { done[s] = 1; lengths[s] = t + 1; }
+    }
+  }
+  free(kc); free(vc); free(x); free(last); free(logits); free(ids); free(hist); free(done);
+}
+
 /* Log-probs of tokens[:, n] given prompt ‖ tokens[:, :n] (tensor_sleep.rs:2531-2615). */
 void or_logprobs(const or_model* m, const int32_t* prompts, const int32_t* tokens, int S, int P,
                  int N, double* lp) {

@@ -56,6 +56,16 @@ void or_q4_decode(const uint8_t* codes, const uint16_t* scales, int64_t n, float
 void or_q4_matvec(const uint8_t* codes, const uint16_t* scales, int64_t rows, int64_t cols,
                   const float* x, float* y);
 
+/* Sampling with the TextGenerator options (model.c; generate.rs:127-250).
+ * or_apply_penalty: apply_repetition_penalty (:155-182); -1 for a token outside
+ * [0, V). or_sample_ex_row: one row of select_next_token with top-k, penalty,
+ * greedy and the opt-in nucleus filter (parity unpinned for the nucleus part:
+ * the reference has no nucleus sampler). */
+int or_apply_penalty(float* values, int64_t V, const int32_t* prior, int64_t n, float penalty);
+int or_sample_ex_row(const float* logits, int64_t V, float temperature, int top_k, float penalty,
+                     float top_p, int apply_top_p, uint64_t seed, int64_t row, int64_t step,
+                     const int32_t* prior, int64_t n, int32_t* tok, double* lp);
+
 #ifdef __cplusplus
 }
 #endif

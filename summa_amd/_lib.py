@@ -43,6 +43,9 @@ SIGNATURES: dict[str, tuple] = {
     "sm_attn_prefill": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_attn_prefill_lse": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_sample": (i32, [vp, i64, i64, i64, f32, u64, i64, vp, i64, vp, i64, vp, vp]),
+    "sm_sample_ex": (i32, [vp, i64, i64, i64, vp, u64, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp,
+                           vp]),
+    "sm_seen_tokens": (i32, [vp, i64, i64, i64, i64, vp, i64, i32, vp]),
     "sm_moe_plan_words": (i64, [i64, i64, i64]),
     "sm_moe_router_top2": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, vp]),
     "sm_moe_route_plan": (i32, [vp, i64, i64, i64, vp, vp, vp]),
@@ -55,6 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     "sm_model_set_tensor": (i32, [vp, i32, i32, vp, vp]),
     "sm_model_init_random": (i32, [vp, u64, f32, vp]),
     "sm_rl_generate": (i32, [vp, vp, i64, i64, i64, f32, u64, vp, vp, vp]),
+    "sm_rl_generate_ex": (i32, [vp, vp, i64, i64, i64, vp, u64, vp, vp, vp, vp]),
     "sm_rl_logprobs": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "sm_rl_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64, i64,
                             vp, vp, vp, vp, vp, vp]),

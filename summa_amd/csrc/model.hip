@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "common.hpp"
+#include "sampling.hpp"
 
 extern "C" {
 int sm_q4_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int, int64_t,
@@ -176,7 +177,7 @@ struct sm_model {
   size_t weight_bytes = 0;
   // workspace
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
-      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws;
+      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws, seen, done;
   int64_t gen_cap = 0, gen_S = 0;
 };
 
@@ -595,6 +596,95 @@ extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, in
     SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, t,
                      tokens + t, N, behavior_lp ? behavior_lp + t : nullptr, N,
                      (int32_t*)m->next_ids.p, st));
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+namespace sm {
+namespace {
+
+// Rollouts that stopped: tokens[s, t0..N) = eos, behavior log-prob 0.
+__global__ void pad_tail_kernel(int32_t* tokens, float* lp, int S, int N, int t0, int eos) {
+  const int w = N - t0;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * w) return;
+  const int64_t at = (i / w) * N + t0 + i % w;
+  tokens[at] = eos;
+  if (lp) lp[at] = 0.f;
+}
+
+constexpr int64_t kEosPoll = 16;  // decode steps between all-stopped checks
+
+}  // namespace
+}  // namespace sm
+
+extern "C" int sm_rl_generate_ex(sm_model* m, const int32_t* prompts, int64_t S, int64_t P,
+                                 int64_t N, const sm_sampling* sp, uint64_t seed, int32_t* tokens,
+                                 float* behavior_lp, int32_t* lengths, void* stream) {
+  SM_REQUIRE(m && prompts && tokens, "sm_rl_generate_ex: null argument");
+  SM_REQUIRE(S > 0 && P > 0, "cannot generate from an empty prompt");
+  SM_REQUIRE(N > 0, "sm_rl_generate_ex: max_new_tokens must be positive");
+  const auto& c = m->cfg;
+  SM_TRY(validate_sampling(sp, c.vocab));
+  const int64_t cap = P + N - 1;
+  SM_REQUIRE(cap <= c.max_seq, "attention cache capacity %lld exceeds max_seq_len %d",
+             (long long)cap, c.max_seq);
+  hipStream_t st = as_stream(stream);
+  const size_t layer_elems = cache_layer_elems(m, S, cap);
+  SM_TRY(ensure(m->kc, layer_elems * c.layers * m->kv_size));
+  SM_TRY(ensure(m->vc, layer_elems * c.layers * m->kv_size));
+  SM_TRY(ensure(m->pos, (size_t)S * 4));
+  SM_TRY(ensure(m->lens, (size_t)S * 4));
+  SM_TRY(ensure(m->next_ids, (size_t)S * 4));
+  SM_TRY(ensure(m->rows, (size_t)S * c.d_model * 4));
+  SM_TRY(ensure(m->logits, (size_t)S * c.vocab * 4));
+  const bool pen = sp->repetition_penalty != 1.f;
+  const bool eos = sp->eos_token >= 0;
+  const int64_t seen_ld = ceil_div(c.vocab, 32);
+  uint32_t* seen = nullptr;
+  int32_t* done = nullptr;
+  if (pen) {
+    SM_TRY(ensure(m->seen, (size_t)S * seen_ld * 4));
+    seen = (uint32_t*)m->seen.p;
+    SM_TRY(seen_tokens(prompts, S, P, P, c.vocab, seen, seen_ld, true, st));
+  }
+  if (eos) {
+    SM_TRY(ensure(m->done, (size_t)(S + 1) * 4));  // S flags, then the stopped count
+    done = (int32_t*)m->done.p;
+    SM_TRY(fill_i32(done, S + 1, 0, st));
+  }
+  if (lengths) SM_TRY(fill_i32(lengths, S, (int32_t)N, st));
+  int32_t* next = (int32_t*)m->next_ids.p;
+  int32_t* pos = (int32_t*)m->pos.p;
+  int32_t* lens = (int32_t*)m->lens.p;
+  set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, 0);
+  SM_TRY(run_layers(m, prompts, S, P, pos, nullptr, m->kc.p, m->vc.p, layer_elems, cap, false, st));
+  gather_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>((const float*)m->x.p, (int)S,
+                                                                (int)P, (int)P - 1, c.d_model,
+                                                                (float*)m->rows.p);
+  SM_TRY(head(m, (const float*)m->rows.p, S, (float*)m->logits.p, st));
+  SM_TRY(sample_ex_launch((const float*)m->logits.p, S, c.vocab, c.vocab, sp, seed, 0, seen,
+                          seen_ld, done, eos ? lengths : nullptr, eos ? done + S : nullptr, tokens,
+                          N, behavior_lp, N, next, st));
+  for (int64_t t = 1; t < N; ++t) {
+    if (eos && t % kEosPoll == 0) {
+      int32_t stopped = 0;
+      SM_HIP(hipMemcpyAsync(&stopped, done + S, 4, hipMemcpyDeviceToHost, st));
+      SM_HIP(hipStreamSynchronize(st));
+      if (stopped >= S) {
+        const int64_t n = S * (N - t);
+        pad_tail_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(tokens, behavior_lp, (int)S,
+                                                                    (int)N, (int)t, sp->eos_token);
+        break;
+      }
+    }
+    set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, (int)(P + t - 1));
+    SM_TRY(run_layers(m, next, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true, st));
+    SM_TRY(head(m, (const float*)m->x.p, S, (float*)m->logits.p, st));
+    SM_TRY(sample_ex_launch((const float*)m->logits.p, S, c.vocab, c.vocab, sp, seed, t, seen,
+                            seen_ld, done, eos ? lengths : nullptr, eos ? done + S : nullptr,
+                            tokens + t, N, behavior_lp ? behavior_lp + t : nullptr, N, next, st));
   }
   SM_LAUNCH_CHECK();
   return SM_OK;

@@ -121,6 +121,22 @@ class Model:
              tok.data_ptr(), lp.data_ptr(), _stream())
         return tok, lp
 
+    def generate_ex(self, prompts: torch.Tensor, config, seed: int | None = None):
+        """Batched rollouts with a ``sampling.SamplingConfig`` (top-k, repetition
+        penalty, EOS, nucleus): (tokens [S, N], behavior_lp [S, N], lengths [S]).
+        ``seed`` defaults to ``config.seed`` (0 when neither is given)."""
+        import ctypes as C
+        S, P = prompts.shape
+        N = int(config.max_new_tokens)
+        tok = torch.empty(S, N, dtype=torch.int32, device=prompts.device)
+        lp = torch.empty(S, N, dtype=torch.float32, device=prompts.device)
+        lens = torch.empty(S, dtype=torch.int32, device=prompts.device)
+        sc = config.c()
+        seed = config.seed if seed is None else seed
+        call("sm_rl_generate_ex", self._h, prompts.data_ptr(), S, P, N, C.addressof(sc),
+             int(seed or 0), tok.data_ptr(), lp.data_ptr(), lens.data_ptr(), _stream())
+        return tok, lp, lens
+
     def logprobs(self, prompts: torch.Tensor, tokens: torch.Tensor, max_tokens_per_forward=0):
         S, P = prompts.shape
         N = tokens.shape[1]

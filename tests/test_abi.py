@@ -52,3 +52,36 @@ def test_argument_errors_are_reported_not_raised():
     assert L.sm_last_error().decode() == "GRPO clip_epsilon must be finite and in (0, 1)"
     st = L.sm_ce_rows(1, 1, 1, 4, 8, 9, None, None, None, 1.0, None, None, None)
     assert st == -1 and b"logical vocabulary 9" in L.sm_last_error()
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(top_k=0), "top_k must be >= 1 (got 0)"),
+    (dict(temperature=float("nan")), "temperature must not be NaN"),
+    (dict(repetition_penalty=0.5), "repetition_penalty must be finite and >= 1 (got 0.5)"),
+    (dict(repetition_penalty=float("inf")), "repetition_penalty must be finite and >= 1 (got inf)"),
+    (dict(top_p=0.0), "rollout top_p must be finite and in (0, 1]"),
+    (dict(top_p=1.5), "rollout top_p must be finite and in (0, 1]"),
+    (dict(eos_token=10), "eos_token 10 is outside the model vocabulary of 10 entries"),
+])
+def test_sampling_options_rejected_with_reference_messages(kw, msg):
+    """generate.rs:68-84 and RolloutSampling::validate (posttrain.rs:372-386):
+    rejected before any device work."""
+    import ctypes
+    from summa_amd.sampling import SamplingConfig
+    L = _lib.lib()
+    sc = SamplingConfig(**kw).c()
+    st = L.sm_sample_ex(1, 1, 10, 10, ctypes.addressof(sc), 0, 0, None, 0, None, None, 1, 1,
+                        None, 1, None, None)
+    assert st == -1
+    assert L.sm_last_error().decode() == msg
+
+
+def test_rollout_sampling_validate_messages():
+    from summa_amd.sampling import RolloutSampling
+    RolloutSampling().validate()
+    for kw, msg in [(dict(max_new_tokens=0), "max_new_tokens must be in 1..=1048576"),
+                    (dict(temperature=0.0), "rollout temperature must be finite and positive"),
+                    (dict(top_p=float("nan")), "rollout top_p must be finite and in (0, 1]")]:
+        with pytest.raises(ValueError, match=msg.replace("(", r"\(").replace(")", r"\)")
+                           .replace("[", r"\[").replace("]", r"\]").replace(".", r"\.")):
+            RolloutSampling(**kw).validate()
