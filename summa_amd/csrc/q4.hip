@@ -258,6 +258,108 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   }
 }
 
+// M = 1 (one sequence's decode step; the LM head at batch 1). One wave owns a
+// 16-row block of W; KS = 1: four blocks per workgroup, each wave over all of
+// K; KS = 4: one block per workgroup, wave w over the K groups w, w + 4, ...,
+// merged in LDS in wave order (for N too small to fill the GPU otherwise). The activation
+// row is staged in LDS once per workgroup, after the first weight group has
+// been requested, and feeds every A row of the MFMA (so every D row is the
+// result and no lane is masked). Weight groups are double-buffered in
+// registers, which leaves the weight stream alone on the vector-memory
+// counter: activation loads interleaved with it made every wait drain the
+// next group's weights too. The arithmetic per group is that of
+// q4_gemm_kernel (codes x activations over 4 k-steps, then one FMA with the
+// group scale), so the two kernels give the same bits.
+template <int NA, int EPI, int KS>
+__global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
+  extern __shared__ _Float16 xs[];  // NA * K activations (hi, then lo)
+  __shared__ float red[KS][4][16];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  constexpr int BPW = 4 / KS;  // row blocks per workgroup
+  const int blk = wave % BPW, part = wave / BPW;
+  const int nrb = (a.N + 15) / 16;
+  const int rb_raw = (int)blockIdx.x * BPW + blk;
+  const int rb = min(rb_raw, nrb - 1);  // tail waves re-read the last block, store nothing
+  const int ng = a.K / 128;
+  const uint8_t* cb = a.codes + q4t_code_offset((int64_t)rb * 16 + j, 0, ng) + g * 16;
+  const uint16_t* sb = a.scales + q4t_scale_index((int64_t)rb * 16 + j, 0, ng);
+  auto load = [&](int kc, u32x4& w, uint16_t& sc) {
+    kc = min(kc, ng - 1);
+    w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cb + (size_t)kc * 1024));
+    sc = sb[kc * 16];
+  };
+  u32x4 w0, w1;
+  uint16_t s0, s1;
+  load(part, w0, s0);
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  for (int i = threadIdx.x * 8; i < NA * a.K; i += 256 * 8)
+    *reinterpret_cast<h8*>(xs + i) = *reinterpret_cast<const h8*>(x + i);
+  __syncthreads();
+  float acc = 0.f;
+  auto group = [&](int kg, const u32x4& w, uint16_t sc) {
+    f4 t = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const h8 bq = q4_unpack(w[q]);
+      const h8 ah = *reinterpret_cast<const h8*>(xs + kg * 128 + g * 32 + q * 8);
+      t = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bq, t, 0, 0, 0);
+      if constexpr (NA == 2) {
+        const h8 al = *reinterpret_cast<const h8*>(xs + a.K + kg * 128 + g * 32 + q * 8);
+        t = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bq, t, 0, 0, 0);
+      }
+    }
+    acc = fmaf(t[0], bf16_to_f32(sc), acc);
+  };
+  for (int kb = part; kb < ng; kb += 2 * KS) {
+    load(kb + KS, w1, s1);
+    group(kb, w0, s0);
+    if (kb + KS >= ng) break;
+    load(kb + 2 * KS, w0, s0);
+    group(kb + KS, w1, s1);
+  }
+  if constexpr (KS > 1) {
+    if (g == 0) red[part][blk][j] = acc;
+    __syncthreads();
+    if (part != 0) return;
+    acc = red[0][blk][j];
+#pragma unroll
+    for (int p = 1; p < KS; ++p) acc += red[p][blk][j];
+  }
+  const int col = rb * 16 + j;
+  if (g != 0 || rb_raw >= nrb || col >= a.N) return;
+  if constexpr (EPI == EPI_STORE_F32) static_cast<float*>(a.y)[col] = acc;
+  else if constexpr (EPI == EPI_STORE_BF16) static_cast<uint16_t*>(a.y)[col] = f32_to_bf16(acc);
+  else static_cast<float*>(a.y)[col] += acc;
+}
+
+// The K-split variant runs where the tile kernel's narrow GEMV splits K (fewer
+// than 512 of its 64-column workgroups): the four-block variant would leave
+// most CUs idle there, and the same choice keeps the two kernels' bits equal.
+template <int NA, int EPI>
+int launch_gemv1(const Q4Args& a, hipStream_t st) {
+  const int64_t nrb = ceil_div(a.N, 16);
+  const size_t lds = (size_t)NA * a.K * 2;
+  if (ceil_div(a.N, 64) < 512 && a.K >= 4 * 128)
+    q4_gemv1_kernel<NA, EPI, 4><<<(unsigned)nrb, 256, lds, st>>>(a);
+  else
+    q4_gemv1_kernel<NA, EPI, 1><<<(unsigned)ceil_div(nrb, 4), 256, lds, st>>>(a);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+int launch_gemv1_x(const Q4Args& a, int epi, int xt, hipStream_t st) {
+#define SM_G1(NA)                                                        \
+  switch (epi) {                                                         \
+    case EPI_STORE_F32: return launch_gemv1<NA, EPI_STORE_F32>(a, st);   \
+    case EPI_STORE_BF16: return launch_gemv1<NA, EPI_STORE_BF16>(a, st); \
+    default: return launch_gemv1<NA, EPI_ADD_F32>(a, st);                \
+  }
+  if (xt == X_F16X2) SM_G1(2)
+  SM_G1(1)
+#undef SM_G1
+}
+
 template <int NB, int KSPLIT, int XT, int KU = 8>
 int launch_q4_x(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
   const int wave_cols = 16 * NB;
@@ -316,6 +418,10 @@ namespace {
 // that grid would have fewer than 512 workgroups the four waves of a
 // workgroup split K instead of N.
 int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int64_t ws_bytes) {
+  // one activation row in f16 (or pairs) with a plain epilogue: the M = 1 GEMV
+  if (a.M == 1 && !a.tiles && !a.rowidx && xt != X_BF16 && epi <= EPI_ADD_F32 &&
+      (int64_t)(xt == X_F16X2 ? 2 : 1) * a.K * 2 <= 65536)
+    return launch_gemv1_x(a, epi, xt, st);
   const int64_t logical_cols = is_swiglu(epi) ? 2 * (int64_t)a.ncols : a.N;
   const bool ksplit_ok = a.K >= 4 * 128;
   const int64_t bl_wgs = ceil_div(a.M, 64) * ceil_div(logical_cols, 64);

@@ -245,3 +245,35 @@ def test_split_k_workspace(dev, m, n, k, epi):
     assert int(ws.int().abs().sum().item()) != 0  # the split really ran
     expect = (base + y_ref) if epi == "add" else y_ref
     assert np.all(np.abs(outs[0] - expect) <= tol + 1e-6), float(np.abs(outs[0] - expect).max())
+
+
+@pytest.mark.parametrize("n,k,pair", [(16400, 2048, False), (16400, 1024, True), (1000, 640, False),
+                                      (1000, 640, True), (300, 256, False), (65536, 2048, False)])
+def test_gemv_m1_equals_tile_kernel(dev, n, k, pair):
+    """M = 1 runs the single-row GEMV (activation row in LDS, double-buffered
+    weight groups; K split across waves for small N). Its arithmetic and
+    summation order are the 16-row tile kernel's, so row 0 of an M = 2 call
+    matches bit for bit; the store-bf16 and add epilogues follow the same value."""
+    print(f"case gemv1 n={n} k={k} pair={pair}", flush=True)
+    w = torch.empty(n, k, device=dev)
+    ops.fill_normal(w, 0.0, 0.02, seed=n + k)
+    qw = ops.Q4Weight.quantize(w)
+    x = torch.randn(2, k, device=dev)
+    xd = ops.f16_pair(x) if pair else x.to(torch.float16)
+    y1 = ops.q4_matmul(qw, xd[:1], pair=pair)
+    y2 = ops.q4_matmul(qw, xd, pair=pair)
+    assert torch.equal(y1[0], y2[0])
+    yb = ops.q4_matmul(qw, xd[:1], pair=pair, epilogue=_lib.SM_EPI_STORE_BF16)
+    assert torch.equal(yb.float(), y1.to(torch.bfloat16).float())
+    base = torch.randn(1, n, device=dev)
+    acc = base.clone()
+    ops.q4_matmul(qw, xd[:1], out=acc, pair=pair, epilogue=_lib.SM_EPI_ADD_F32)
+    assert torch.equal(acc, base + y1)
+    if n * k <= 1000 * 640:  # against the decoded weights in f64
+        codes = qw.codes.cpu().numpy()
+        scales = qw.scales.cpu().numpy().view(np.uint16)
+        dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+        xr = (ops.unpair(xd[:1]) if pair else xd[:1].float()).cpu().numpy().astype(np.float64)
+        y_ref = xr @ dense.T
+        tol = 2e-6 * (np.abs(xr) @ np.abs(dense).T) + 1e-7
+        assert np.all(np.abs(y1.cpu().numpy() - y_ref) <= tol)
