@@ -444,6 +444,8 @@ int launch_bl_x(const BLArgs& a, int epi, int xt, dim3 grid, hipStream_t st) {
 // Split-K workspace: the fp32 partials [splits][M][cols].
 int64_t bl_counter_bytes() { return 0; }
 
+constexpr int64_t kWideMinTiles = 128;
+
 // Batch-M Q4 matmul (argument checks done by the callers in q4.hip).
 // Dense mode (tiles == nullptr): rows 0..M-1. Grouped mode: the route plan's
 // 128-row tile list (max_tiles entries at most). With a workspace (ws,
@@ -454,6 +456,11 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
                const int32_t* tiles, const int32_t* ntiles, int64_t max_tiles,
                const int32_t* goff, const int32_t* rowidx, size_t cstride, size_t sstride,
                void* ws, int64_t ws_bytes, const QkvRope* qr) {
+  // Large dense problems with f16 / f16-pair activations: the 256 x 256 tile
+  // kernel (same results), once it has at least half a wave of workgroups
+  // (one per CU); measured faster from there on.
+  if (!tiles && (xt == 1 || xt == 2) && q4_wide_tiles(M, N, ncols, epi) >= kWideMinTiles)
+    return q4_gemm_wide(codes, scales, N, K, x, xt, M, ldx, y, ldy, epi, ncols, st, qr);
   BLArgs a{codes, scales, x, y, M, N, K, ldx, ldy, ncols, 0, 0, 0,
            tiles, ntiles, goff, rowidx, cstride, sstride, nullptr, K / 128};
   if (epi == 6) {

@@ -26,4 +26,12 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
                void* ws, int64_t ws_bytes, const QkvRope* qr);
 int64_t bl_counter_bytes();
 
+// Dense large-M Q4 matmul with 256 x 256 tiles (q4_gemm_wide.hip): f16 (xt 1)
+// or f16-pair (xt 2) activations, epilogues 0..6; the same results as
+// q4_gemm_bl. q4_wide_tiles: its workgroup count for a shape.
+int q4_gemm_wide(const uint8_t* codes, const uint16_t* scales, int N, int K, const void* x,
+                 int xt, int M, int ldx, void* y, int ldy, int epi, int ncols, hipStream_t st,
+                 const QkvRope* qr);
+int64_t q4_wide_tiles(int M, int N, int ncols, int epi);
+
 }  // namespace sm

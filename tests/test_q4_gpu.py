@@ -277,3 +277,74 @@ def test_gemv_m1_equals_tile_kernel(dev, n, k, pair):
         y_ref = xr @ dense.T
         tol = 2e-6 * (np.abs(xr) @ np.abs(dense).T) + 1e-7
         assert np.all(np.abs(y1.cpu().numpy() - y_ref) <= tol)
+
+
+WIDE_EPI = [("store", _lib.SM_EPI_STORE_F32), ("bf16", _lib.SM_EPI_STORE_BF16),
+            ("add", _lib.SM_EPI_ADD_F32), ("swiglu_bf16", _lib.SM_EPI_SWIGLU_BF16),
+            ("swiglu_f16", _lib.SM_EPI_SWIGLU_F16), ("swiglu_pair", _lib.SM_EPI_SWIGLU_F16X2)]
+
+
+@pytest.mark.parametrize("m,n,k", [(2048, 4096, 512), (2000, 4000, 384)])
+@pytest.mark.parametrize("pair", [False, True])
+@pytest.mark.parametrize("epi", [e for e, _ in WIDE_EPI])
+def test_wide_kernel_equals_tile_kernel(dev, m, n, k, pair, epi):
+    """Large dense problems (>= 128 workgroups of 256 x 256) run the wide-tile
+    kernel; its accumulation order is the 128 x 128 kernel's, which row chunks
+    of <= 256 rows (16 workgroups) still run: results agree bit for bit, for
+    every epilogue, f16 and f16-pair inputs, and ragged M / N edges."""
+    print(f"case wide m={m} n={n} k={k} pair={pair} epi={epi}", flush=True)
+    e = dict(WIDE_EPI)[epi]
+    w = torch.empty(n, k, device=dev)
+    ops.fill_normal(w, 0.0, 0.05, seed=n + k)
+    qw = ops.Q4Weight.quantize(w)
+    x = torch.randn(m, k, device=dev)
+    xd = ops.f16_pair(x) if pair else x.to(torch.float16)
+    if e == _lib.SM_EPI_ADD_F32:
+        base = torch.randn(m, n, device=dev)
+        big = base.clone()
+        ops.q4_matmul(qw, xd, out=big, epilogue=e, pair=pair)
+        ref = base.clone()
+        for r0 in range(0, m, 256):
+            ops.q4_matmul(qw, xd[r0:r0 + 256], out=ref[r0:r0 + 256], epilogue=e, pair=pair)
+    else:
+        big = ops.q4_matmul(qw, xd, epilogue=e, pair=pair)
+        ref = torch.cat([ops.q4_matmul(qw, xd[r0:r0 + 256], epilogue=e, pair=pair)
+                         for r0 in range(0, m, 256)])
+    assert big.shape == ref.shape
+    assert torch.equal(big.view(torch.int16) if big.dtype != torch.float32 else big,
+                       ref.view(torch.int16) if ref.dtype != torch.float32 else ref)
+
+
+@pytest.mark.parametrize("S,L,H,KVH", [(8, 256, 32, 16), (10, 300, 32, 8)])
+def test_wide_kernel_qkv_rope_equals_tile_kernel(dev, S, L, H, KVH):
+    """sm_q4_qkv_rope over a prefill-sized batch (the wide kernel) writes the
+    same q / K / V cache bits as one sequence at a time (the 128 x 128 kernel)."""
+    from summa_amd._lib import SM_F16, SM_F16X2, call
+    print(f"case wide qkv-rope S={S} L={L} H={H} KVH={KVH}", flush=True)
+    hd, K, p0 = 64, 512, 3
+    N = (H + 2 * KVH) * hd
+    w = torch.empty(N, K, device=dev)
+    ops.fill_normal(w, 0.0, 0.05, seed=N)
+    qw = ops.Q4Weight.quantize(w)
+    xp = ops.f16_pair(torch.randn(S * L, K, device=dev))
+    cap = p0 + L + 1
+    half = hd // 2
+    inv = 1.0 / (10000.0 ** (np.arange(half) * 2.0 / hd))
+    ang = np.arange(cap)[:, None] * inv[None, :]
+    tab = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)).to(dev)
+    pos0 = torch.tensor([p0 + s for s in range(S)], dtype=torch.int32, device=dev) % 2
+    st = torch.cuda.current_stream().cuda_stream
+    outs = []
+    for chunked in (False, True):
+        q = torch.zeros(S * L, H, hd, dtype=torch.float16, device=dev)
+        kc = torch.zeros(S, KVH, cap, hd, dtype=torch.float16, device=dev)
+        vc = torch.zeros(S, KVH, cap, hd, dtype=torch.float16, device=dev)
+        spans = [(s, 1) for s in range(S)] if chunked else [(0, S)]
+        for s0, ns in spans:
+            call("sm_q4_qkv_rope", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), H, KVH, hd, K,
+                 xp[s0 * L:].data_ptr(), SM_F16X2, ns, L, xp.stride(0), tab.data_ptr(),
+                 pos0[s0:].data_ptr(), cap, q[s0 * L:].data_ptr(), kc[s0:].data_ptr(),
+                 vc[s0:].data_ptr(), SM_F16, st)
+        outs.append((q, kc, vc))
+    for a, b in zip(*outs):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
