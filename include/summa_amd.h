@@ -370,6 +370,55 @@ int sm_model_set_tensor(sm_model* model, int kind, int layer, const float* src, 
  * ~N(0, 1) (the BASELINE configs' random init). */
 int sm_model_init_random(sm_model* model, uint64_t seed, float std, void* stream);
 
+/* ------------------------------------------------------------------------
+ * HQUANT packed tensors (PackedTensor, summa-train/src/quantization.rs:414-689;
+ * container to_bytes / from_bytes :502-597). Formats 1-3 are the reference's
+ * (binary / ternary / ternary-entropy g128, FP16 group scales); 4 is this
+ * build's Q4G128 (two's-complement nibbles, low nibble first, bf16 scales),
+ * which has no counterpart in the reference codec. */
+enum {
+  SM_HQ_BINARY = 1,
+  SM_HQ_TERNARY = 2,
+  SM_HQ_TERNARY_ENTROPY = 3,
+  SM_HQ_Q4G128 = 4
+};
+typedef struct sm_hquant {
+  int32_t format;       /* SM_HQ_* */
+  int32_t group_size;   /* 128 */
+  int32_t rank;         /* 1..32 */
+  int64_t shape[32];
+  int64_t elements;
+  const uint16_t* scales; /* one per group: FP16 bits (formats 1-3), bf16 bits (4) */
+  int64_t nscales;
+  const uint8_t* codes;
+  int64_t ncodes;
+} sm_hquant;
+/* FNV-1a 64 of a byte range (the container checksum, quantization.rs:2274). */
+uint64_t sm_fnv1a64(const uint8_t* bytes, int64_t n);
+/* Parse and validate a container held in host memory (from_bytes +
+ * validate_packed, :530-597, :980-1071): `out` points into `bytes` (which must
+ * stay alive and be 2-byte aligned). Errors carry the reference's messages
+ * ("quantized tensor checksum mismatch", "invalid quantized tensor magic",
+ * "packed tensor contains reserved ternary code 3", ...). */
+int sm_hquant_parse(const uint8_t* bytes, int64_t n, sm_hquant* out);
+/* Serialized size of `t`, and the serialisation itself (to_bytes, :502-528):
+ * validates `t` (host pointers) first. */
+int64_t sm_hquant_bytes(const sm_hquant* t);
+int sm_hquant_write(const sm_hquant* t, uint8_t* out, int64_t cap, int64_t* written);
+/* Device decode (PackedTensor::decode, :445-497): t->scales / t->codes are
+ * device pointers; out [elements] f32, or with transpose = 1 a rank-2 [r, c]
+ * tensor written as [c, r]. */
+int sm_hquant_decode(const sm_hquant* t, float* out, int transpose, void* stream);
+/* QuantizedModelBackend::load_quantized_matrix (:1183-1189): install a packed
+ * tensor (device scales / codes) as model tensor `kind` / `layer`.
+ * layout 0: rows are [out, in] as sm_model_set_tensor; 1: [in, out] (Burn's
+ * Linear weight layout, the layout of reference archives). A Q4G128 tensor in
+ * layout 0 is installed bit for bit into a quantized model; everything else is
+ * decoded and stored like sm_model_set_tensor (a quantized model re-quantizes
+ * binary / ternary weights to Q4G128: not exact, FP16 scales are not bf16). */
+int sm_model_load_packed(sm_model* model, int kind, int layer, const sm_hquant* tensor,
+                         int layout, void* stream);
+
 /* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout
  * the semantics of TextGenerator::generate, generate.rs:68-124, with no EOS):
  * prompts [S, P] int32 -> tokens [S, N] int32 and behavior_lp [S, N] f32

@@ -355,6 +355,48 @@ def sample_ex(logits, *, temperature, seed, step, top_k=-1, repetition_penalty=1
     return tok, lp
 
 
+def fnv1a64(data: bytes) -> int:
+    L = lib()
+    L.or_fnv1a64.restype = C.c_uint64
+    L.or_fnv1a64.argtypes = [C.c_char_p, C.c_int64]
+    return int(L.or_fnv1a64(data, len(data)))
+
+
+def hq_quantize(values, fmt: int):
+    """``quantize_tensor`` for HQUANT formats 1-3: (scales u16 FP16 bits, codes u8)."""
+    v = np.ascontiguousarray(values, dtype=np.float32).ravel()
+    L = lib()
+    L.or_hq_bytes_per_group.restype = C.c_int64
+    L.or_hq_bytes_per_group.argtypes = [C.c_int]
+    L.or_hq_quantize.restype = C.c_int
+    L.or_hq_quantize.argtypes = [C.c_void_p, C.c_int64, C.c_int, C.c_void_p, C.c_void_p]
+    groups = (v.size + 127) // 128
+    scales = np.zeros(groups, np.uint16)
+    codes = np.zeros(groups * L.or_hq_bytes_per_group(fmt), np.uint8)
+    if L.or_hq_quantize(v.ctypes.data, v.size, fmt, scales.ctypes.data, codes.ctypes.data) != 0:
+        raise ValueError("quantization group scale is outside finite FP16 range")
+    return scales, codes
+
+
+def hq_decode(fmt: int, n: int, scales, codes):
+    """``PackedTensor::decode`` (formats 1-3; 4 = the Q4G128 codec): f32 [n]."""
+    L = lib()
+    L.or_hq_decode.restype = None
+    L.or_hq_decode.argtypes = [C.c_int, C.c_int64, C.c_void_p, C.c_void_p, C.c_void_p]
+    s = np.ascontiguousarray(scales, dtype=np.uint16)
+    c = np.ascontiguousarray(codes, dtype=np.uint8)
+    out = np.empty(n, np.float32)
+    L.or_hq_decode(fmt, n, s.ctypes.data, c.ctypes.data, out.ctypes.data)
+    return out
+
+
+def f32_to_f16_bits(x) -> np.ndarray:
+    L = lib()
+    L.or_f32_to_f16_bits.restype = C.c_uint16
+    L.or_f32_to_f16_bits.argtypes = [C.c_float]
+    return np.array([L.or_f32_to_f16_bits(float(v)) for v in np.ravel(x)], np.uint16)
+
+
 def random_weights(cfg: dict, seed: int = 0, std: float = 0.02) -> dict:
     """N(0, std) linears and embedding, unit norms (the configs' synthetic init).
     MoE configs (cfg["E"] > 0) get a router ~ N(0, 1/sqrt(d)) (router logits

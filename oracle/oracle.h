@@ -66,6 +66,15 @@ int or_sample_ex_row(const float* logits, int64_t V, float temperature, int top_
                      float top_p, int apply_top_p, uint64_t seed, int64_t row, int64_t step,
                      const int32_t* prior, int64_t n, int32_t* tok, double* lp);
 
+/* HQUANT codec (hquant.c; quantization.rs:445-773, :934-978, :2274-2281). */
+uint16_t or_f32_to_f16_bits(float f);
+float or_f16_bits_to_f32(uint16_t b);
+uint64_t or_fnv1a64(const uint8_t* p, int64_t n);
+int64_t or_hq_bytes_per_group(int format);
+int or_hq_quantize(const float* v, int64_t n, int format, uint16_t* scales, uint8_t* codes);
+void or_hq_decode(int format, int64_t n, const uint16_t* scales, const uint8_t* codes,
+                  float* out);
+
 #ifdef __cplusplus
 }
 #endif

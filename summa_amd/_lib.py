@@ -56,6 +56,12 @@ SIGNATURES: dict[str, tuple] = {
     "sm_model_destroy": (i32, [vp]),
     "sm_model_weight_bytes": (i64, [vp]),
     "sm_model_set_tensor": (i32, [vp, i32, i32, vp, vp]),
+    "sm_fnv1a64": (u64, [vp, i64]),
+    "sm_hquant_parse": (i32, [vp, i64, vp]),
+    "sm_hquant_bytes": (i64, [vp]),
+    "sm_hquant_write": (i32, [vp, vp, i64, vp]),
+    "sm_hquant_decode": (i32, [vp, vp, i32, vp]),
+    "sm_model_load_packed": (i32, [vp, i32, i32, vp, i32, vp]),
     "sm_model_init_random": (i32, [vp, u64, f32, vp]),
     "sm_rl_generate": (i32, [vp, vp, i64, i64, i64, f32, u64, vp, vp, vp]),
     "sm_rl_generate_ex": (i32, [vp, vp, i64, i64, i64, vp, u64, vp, vp, vp, vp]),

@@ -504,6 +504,52 @@ extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float
   return SM_OK;
 }
 
+namespace sm {
+int hquant_decode_device(const sm_hquant* t, float* out, int transpose, hipStream_t st);
+}
+
+extern "C" int sm_model_load_packed(sm_model* m, int kind, int layer, const sm_hquant* t,
+                                    int layout, void* stream) {
+  SM_REQUIRE(m && t && t->scales && t->codes, "sm_model_load_packed: null argument");
+  SM_REQUIRE(layout == 0 || layout == 1,
+             "sm_model_load_packed: layout must be 0 ([out, in]) or 1 ([in, out])");
+  Linear* lin;
+  void* dense;
+  int64_t n, count;
+  SM_TRY(tensor_target(m, kind, layer, &lin, &dense, &n, &count));
+  SM_REQUIRE(t->group_size == 128, "packed tensor is not g128");
+  SM_REQUIRE(t->elements == n * count,
+             "packed tensor has %lld elements; model tensor kind %d needs %lld",
+             (long long)t->elements, kind, (long long)(n * count));
+  SM_REQUIRE(t->nscales == ceil_div(t->elements, 128), "packed tensor scale count mismatch");
+  if (layout == 1)
+    SM_REQUIRE(lin && count == 1 && t->rank == 2 && t->shape[0] == lin->K && t->shape[1] == lin->N,
+               "an [in, out] packed tensor must be a rank-2 linear weight [%lld, %lld]",
+               lin ? (long long)lin->K : 0ll, lin ? (long long)lin->N : 0ll);
+  else if (lin)
+    SM_REQUIRE(t->rank >= 2 && t->shape[t->rank - 1] == lin->K,
+               "an [out, in] packed tensor must end in the input width %lld", (long long)lin->K);
+  hipStream_t st = as_stream(stream);
+  if (lin && m->cfg.quantized && t->format == SM_HQ_Q4G128 && layout == 0) {
+    // the row-major Q4G128 codec is this model's interchange format: tile it
+    // as is (K % 128 == 0, so no group straddles two rows)
+    SM_REQUIRE(t->ncodes == t->nscales * 64, "packed tensor code size mismatch");
+    const size_t cstride = (size_t)q4t_rows(lin->N) * (lin->K / 2);
+    const size_t sstride = (size_t)q4t_rows(lin->N) * (lin->K / 128);
+    for (int64_t e = 0; e < count; ++e)
+      SM_TRY(sm_q4_pack(t->codes + e * (n / 2), t->scales + e * (n / 128), lin->N, lin->K,
+                        lin->codes + e * cstride, lin->scales + e * sstride, stream));
+    return SM_OK;
+  }
+  DevBuf tmp;
+  SM_TRY(ensure(tmp, (size_t)(n * count) * 4));
+  int s = hquant_decode_device(t, (float*)tmp.p, layout == 1, st);
+  if (s == SM_OK) s = sm_model_set_tensor(m, kind, layer, (const float*)tmp.p, stream);
+  hipStreamSynchronize(st);
+  hipFree(tmp.p);
+  return s;
+}
+
 extern "C" int sm_model_init_random(sm_model* m, uint64_t seed, float std, void* stream) {
   SM_REQUIRE(m, "sm_model_init_random: null model");
   hipStream_t st = as_stream(stream);

@@ -96,6 +96,16 @@ class Model:
         src = src.contiguous().float()
         call("sm_model_set_tensor", self._h, KIND[name], layer, src.data_ptr(), _stream())
 
+    def load_packed(self, name: str, packed, layer: int = -1, layout: int = 0) -> None:
+        """Install an HQUANT ``PackedTensor`` (``sm_model_load_packed``):
+        layout 0 = rows [out, in], 1 = Burn's [in, out] Linear layout."""
+        from .hquant import DevicePacked
+        dev = torch.device("cuda", torch.cuda.current_device())
+        d = DevicePacked(packed, dev)
+        call("sm_model_load_packed", self._h, KIND[name], layer, C.addressof(d.c), int(layout),
+             _stream())
+        torch.cuda.current_stream().synchronize()
+
     def load_host_weights(self, weights: dict, device) -> None:
         """weights as produced by ``oracle.random_weights`` style dicts (numpy)."""
         for name, arr in weights.items():
