@@ -321,6 +321,32 @@ int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t e
 int sm_moe_combine(const float* routed, const float* top_w, const int32_t* plan, int64_t tokens,
                    int64_t top_k, int64_t experts, int64_t d, float* x, void* stream);
 
+/* MoE training kernels (route_gather_* / route_combine_*,
+ * summa-llm/src/model/moe_dispatch.rs:244-384; swiglu_forward / _backward,
+ * fused_swiglu.rs:106-150). Tensors f32 or bf16 (dtype SM_F32 / SM_BF16), f32
+ * arithmetic; routing weights top_w [tokens, k] f32; `plan` from
+ * sm_moe_route_plan.
+ * sm_moe_gather: routed[p] = x[order[p] / k] ([R, d], sorted route order).
+ * sm_moe_gather_backward: grad_x[t] = sum_j grad_routed[inverse[t*k + j]].
+ * sm_moe_combine_backward: grad_routed[inverse[r]] = grad_x[r / k] * top_w[r]
+ *   and grad_w[r] = <grad_x[r / k], routed[inverse[r]]> (either output
+ *   nullable; the weight gradient needs `routed`).
+ * sm_swiglu / sm_swiglu_backward over [gate | value] rows [rows, 2F]:
+ *   out = silu(g) * v; d gate = dy * v * s (1 + g (1 - s)) with s = sigmoid(g),
+ *   d value = dy * silu(g). */
+int sm_moe_gather(const void* x, int dtype, const int32_t* plan, int64_t tokens, int64_t top_k,
+                  int64_t experts, int64_t d, void* routed, void* stream);
+int sm_moe_gather_backward(const void* grad_routed, int dtype, const int32_t* plan,
+                           int64_t tokens, int64_t top_k, int64_t experts, int64_t d,
+                           void* grad_x, void* stream);
+int sm_moe_combine_backward(const void* grad_x, const void* routed, int dtype, const float* top_w,
+                            const int32_t* plan, int64_t tokens, int64_t top_k, int64_t experts,
+                            int64_t d, void* grad_routed, float* grad_w, void* stream);
+int sm_swiglu(const void* gate_value, int dtype, int64_t rows, int64_t F, void* out,
+              void* stream);
+int sm_swiglu_backward(const void* gate_value, const void* grad, int dtype, int64_t rows,
+                       int64_t F, void* grad_gate_value, void* stream);
+
 /* ------------------------------------------------------------------------
  * Decoder model (the MAL Transformer subset the configs use,
  * summa-llm/src/model/transformer.rs, block.rs, attention.rs, ffn.rs) and the

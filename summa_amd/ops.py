@@ -387,3 +387,70 @@ def moe_route_combine(routed: torch.Tensor, top_w: torch.Tensor, plan: RoutePlan
     call("sm_moe_combine", routed.data_ptr(), top_w.data_ptr(), plan.words.data_ptr(),
          plan.tokens, plan.top_k, plan.experts, x.shape[1], x.data_ptr(), _stream())
     return x
+
+
+# ------------------------------------------------------ MoE training kernels --
+
+def _f32_or_bf16(t: torch.Tensor, name: str) -> int:
+    _dev(t, name)
+    if t.dtype == torch.float32:
+        return _lib.SM_F32
+    if t.dtype == torch.bfloat16:
+        return _lib.SM_BF16
+    raise TypeError(f"{name} must be float32 or bfloat16")
+
+
+def moe_gather(x: torch.Tensor, plan: RoutePlan) -> torch.Tensor:
+    """routed[p] = x[order[p] // k] (route_gather_forward, moe_dispatch.rs:244-264)."""
+    dt = _f32_or_bf16(x, "x")
+    x = x.contiguous()
+    out = torch.empty(plan.tokens * plan.top_k, x.shape[1], dtype=x.dtype, device=x.device)
+    call("sm_moe_gather", x.data_ptr(), dt, plan.words.data_ptr(), plan.tokens, plan.top_k,
+         plan.experts, x.shape[1], out.data_ptr(), _stream())
+    return out
+
+
+def moe_gather_backward(grad_routed: torch.Tensor, plan: RoutePlan) -> torch.Tensor:
+    """grad_x[t] = sum_j grad_routed[inverse[t*k + j]] (route_gather_backward, :266-286)."""
+    dt = _f32_or_bf16(grad_routed, "grad_routed")
+    g = grad_routed.contiguous()
+    out = torch.empty(plan.tokens, g.shape[1], dtype=g.dtype, device=g.device)
+    call("sm_moe_gather_backward", g.data_ptr(), dt, plan.words.data_ptr(), plan.tokens,
+         plan.top_k, plan.experts, g.shape[1], out.data_ptr(), _stream())
+    return out
+
+
+def moe_combine_backward(grad_x: torch.Tensor, routed: torch.Tensor, top_w: torch.Tensor,
+                         plan: RoutePlan):
+    """(grad_routed, grad_w) of x += sum_j w[t,j] routed[inverse[t*k+j]]
+    (route_combine_routed_backward / route_combine_weight_backward, :314-384)."""
+    dt = _f32_or_bf16(grad_x, "grad_x")
+    if routed.dtype != grad_x.dtype or top_w.dtype != torch.float32:
+        raise TypeError("routed must match grad_x; top_w must be float32")
+    g, r, w = grad_x.contiguous(), routed.contiguous(), top_w.contiguous()
+    gr = torch.zeros_like(r)
+    gw = torch.empty(plan.tokens, plan.top_k, dtype=torch.float32, device=g.device)
+    call("sm_moe_combine_backward", g.data_ptr(), r.data_ptr(), dt, w.data_ptr(),
+         plan.words.data_ptr(), plan.tokens, plan.top_k, plan.experts, g.shape[1], gr.data_ptr(),
+         gw.data_ptr(), _stream())
+    return gr, gw
+
+
+def swiglu(gate_value: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * value over [gate | value] rows (swiglu_forward, fused_swiglu.rs:106-124)."""
+    dt = _f32_or_bf16(gate_value, "gate_value")
+    gv = gate_value.contiguous()
+    F = gv.shape[1] // 2
+    out = torch.empty(gv.shape[0], F, dtype=gv.dtype, device=gv.device)
+    call("sm_swiglu", gv.data_ptr(), dt, gv.shape[0], F, out.data_ptr(), _stream())
+    return out
+
+
+def swiglu_backward(gate_value: torch.Tensor, grad: torch.Tensor) -> torch.Tensor:
+    """d[gate | value] of swiglu (swiglu_backward, fused_swiglu.rs:126-150)."""
+    dt = _f32_or_bf16(gate_value, "gate_value")
+    gv, g = gate_value.contiguous(), grad.contiguous()
+    out = torch.empty_like(gv)
+    call("sm_swiglu_backward", gv.data_ptr(), g.data_ptr(), dt, gv.shape[0], gv.shape[1] // 2,
+         out.data_ptr(), _stream())
+    return out
