@@ -458,8 +458,11 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
                void* ws, int64_t ws_bytes, const QkvRope* qr) {
   // Large dense problems with f16 / f16-pair activations: the 256 x 256 tile
   // kernel (same results), once it has at least half a wave of workgroups
-  // (one per CU); measured faster from there on.
-  if (!tiles && (xt == 1 || xt == 2) && q4_wide_tiles(M, N, ncols, epi) >= kWideMinTiles)
+  // (one per CU) and its row tiles are at least 3/4 full; measured faster
+  // there (at M = 128 the half-empty tiles made the LM head 2x slower).
+  const int64_t wide_rows = ceil_div(M, 256) * 256;
+  if (!tiles && (xt == 1 || xt == 2) && M >= 256 && (wide_rows - M) * 4 <= wide_rows &&
+      q4_wide_tiles(M, N, ncols, epi) >= kWideMinTiles)
     return q4_gemm_wide(codes, scales, N, K, x, xt, M, ldx, y, ldy, epi, ncols, st, qr);
   BLArgs a{codes, scales, x, y, M, N, K, ldx, ldy, ncols, 0, 0, 0,
            tiles, ntiles, goff, rowidx, cstride, sstride, nullptr, K / 128};
