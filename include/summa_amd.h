@@ -348,6 +348,52 @@ int sm_swiglu_backward(const void* gate_value, const void* grad, int dtype, int6
                        int64_t F, void* grad_gate_value, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Policy-update kernels (backward of the recompute and the optimizer step:
+ * prepare_device_batch autodiff + optimizer_step, posttrain.rs:1288-1305,
+ * trainer.rs:1974-1975), f32 with f32 accumulation.
+ * sm_gemm_ex: C = alpha op(A) op(B) + beta C, op(A) [M, K] (A stored [M, K],
+ *   or [K, M] when trans_a), op(B) [K, N] (B stored [K, N], or [N, K] when
+ *   trans_b): the data / weight gradients of Linear::forward (matmul.rs:57-66).
+ * sm_rmsnorm_backward: dx (= or += with accumulate) and dgamma (nullable; =
+ *   or += ; summed over rows in order) of y = x / sqrt(mean x^2 + eps) * gamma
+ *   (norm.rs:36-50); rinv_scratch [rows].
+ * sm_rope_qk: rotate the q and k heads of qkv rows [S*L, (H+2KVH)*hd] in place
+ *   at positions pos0[s] + i (backward = 1: the transposed rotation, for
+ *   gradients) (attention.rs:142-177).
+ * sm_attn_backward_f32: causal GQA attention backward from the forward's
+ *   log-sum-exp (sm_attn_prefill_lse): q/o/dout [S*L, H, hd], k/v/dk/dv
+ *   [S, KVH, L, hd] (positions 0..L-1), lse [S*H, L]; delta_scratch [S*H*L]
+ *   (fused_attention.rs:219-405).
+ * sm_embed_backward: dtable[ids[r]] += dx[r] (atomic f32 adds).
+ * sm_adamw_step: m, v moments, bias correction at `step` (from 1), decoupled
+ *   weight decay: p = p (1 - lr wd) - lr mhat / (sqrt(vhat) + eps).
+ * sm_muon_momentum: velocity = g + mu velocity (g on the first step), update =
+ *   mu velocity + g (BatchedMuon, muon.rs:200-204); sm_axpby: y = a x + b y;
+ *   sm_frobenius_normalize: x /= max(||x||_F, eps), the norm to norm_out[0]
+ *   (zeropower_via_newton_schulz, muon.rs:257-285). */
+int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+               const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+               int64_t ldc, void* stream);
+int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy, int64_t rows,
+                        int64_t d, float eps, int accumulate, float* dx, float* dgamma,
+                        float* rinv_scratch, void* stream);
+int sm_rope_qk(float* qkv, const float* rope_table, const int32_t* pos0, int64_t S, int64_t L,
+               int64_t H, int64_t KVH, int64_t head_dim, int backward, void* stream);
+int sm_attn_backward_f32(const float* q, const float* k, const float* v, const float* o,
+                         const float* dout, const float* lse, int64_t S, int64_t L, int64_t H,
+                         int64_t KVH, int64_t head_dim, float* dq, float* dk, float* dv,
+                         float* delta_scratch, void* stream);
+int sm_embed_backward(const int32_t* ids, const float* dx, int64_t rows, int64_t d,
+                      int64_t vocab, float* dtable, void* stream);
+int sm_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr,
+                  float beta1, float beta2, float eps, float weight_decay, int64_t step,
+                  void* stream);
+int sm_muon_momentum(const float* grad, float* velocity, float* update, int64_t n,
+                     float momentum, int first_step, void* stream);
+int sm_axpby(const float* x, float* y, int64_t n, float a, float b, void* stream);
+int sm_frobenius_normalize(float* x, int64_t n, float eps, float* norm_out, void* stream);
+
+/* ------------------------------------------------------------------------
  * Decoder model (the MAL Transformer subset the configs use,
  * summa-llm/src/model/transformer.rs, block.rs, attention.rs, ffn.rs) and the
  * RL-step runtime behind GrpoDeviceBatchRuntime (posttrain.rs:1288-1305).

@@ -57,6 +57,16 @@ SIGNATURES: dict[str, tuple] = {
     "sm_moe_combine_backward": (i32, [vp, vp, i32, vp, vp, i64, i64, i64, i64, vp, vp, vp]),
     "sm_swiglu": (i32, [vp, i32, i64, i64, vp, vp]),
     "sm_swiglu_backward": (i32, [vp, vp, i32, i64, i64, vp, vp]),
+    "sm_gemm_ex": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp]),
+    "sm_rmsnorm_backward": (i32, [vp, vp, vp, i64, i64, f32, i32, vp, vp, vp, vp]),
+    "sm_rope_qk": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp]),
+    "sm_attn_backward_f32": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, vp,
+                                   vp]),
+    "sm_embed_backward": (i32, [vp, vp, i64, i64, i64, vp, vp]),
+    "sm_adamw_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, i64, vp]),
+    "sm_muon_momentum": (i32, [vp, vp, vp, i64, f32, i32, vp]),
+    "sm_axpby": (i32, [vp, vp, i64, f32, f32, vp]),
+    "sm_frobenius_normalize": (i32, [vp, i64, f32, vp, vp]),
     "sm_model_create": (i32, [vp, vp]),
     "sm_model_destroy": (i32, [vp]),
     "sm_model_weight_bytes": (i64, [vp]),

@@ -1,0 +1,453 @@
+// Backward-pass and optimizer kernels for the GRPO policy update of fp32
+// models (prepare_device_batch's autodiff and optimizer_step,
+// summa-train/src/posttrain.rs:1288-1305, trainer.rs:1974-1975):
+//   * a general f32 GEMM with transposes, C = alpha op(A) op(B) + beta C, for
+//     the data and weight gradients of every linear and Muon's Newton-Schulz
+//     iterations (matmul backward of Linear::forward, matmul.rs:57-66);
+//   * RMSNorm backward (Norm::forward, norm.rs:36-50), deterministic dgamma;
+//   * in-place RoPE on the q / k heads of a qkv block and its backward
+//     (adjacent-pair rotation, attention.rs:142-177);
+//   * causal GQA attention backward from the forward's log-sum-exp
+//     (fused_attention.rs:219-405: dq, dk, dv with delta = rowsum(dO * O));
+//   * embedding backward (scatter-add of row gradients);
+//   * AdamW and Muon's momentum step (burn_optim AdamW; BatchedMuon,
+//     summa-train/src/muon.rs:196-215).
+// All f32 with f32 accumulation: the precision of the reference CPU path.
+#include <cmath>
+
+#include "common.hpp"
+
+namespace sm {
+namespace {
+
+// ------------------------------------------------------------------ GEMM ---
+// 64 x 64 output tile per 256-thread workgroup, 4 x 4 outputs per thread, K in
+// steps of 16 through LDS; op(A) is [M, K] (A stored [M, K] or, transposed,
+// [K, M]), op(B) is [K, N] (B stored [K, N] or [N, K]).
+template <bool TA, bool TB>
+__global__ __launch_bounds__(256) void gemm_ex_kernel(const float* __restrict__ A, int64_t lda,
+                                                      const float* __restrict__ B, int64_t ldb,
+                                                      float* __restrict__ C, int64_t ldc, int M,
+                                                      int N, int K, float alpha, float beta) {
+  __shared__ float as[16][64 + 4];
+  __shared__ float bs[16][64 + 4];
+  const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+  const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
+  float acc[4][4] = {};
+  for (int k0 = 0; k0 < K; k0 += 16) {
+    for (int e = threadIdx.x; e < 64 * 16; e += 256) {
+      // consecutive threads walk the contiguous dimension of each operand
+      int r, kk;
+      if (TA) { kk = e / 64; r = e % 64; } else { r = e / 16; kk = e % 16; }
+      const int gm = m0 + r, gk = k0 + kk;
+      as[kk][r] = (gm < M && gk < K) ? (TA ? A[(size_t)gk * lda + gm] : A[(size_t)gm * lda + gk])
+                                     : 0.f;
+      int c, kb;
+      if (TB) { c = e / 16; kb = e % 16; } else { kb = e / 64; c = e % 64; }
+      const int gn = n0 + c, gkb = k0 + kb;
+      bs[kb][c] = (gn < N && gkb < K) ? (TB ? B[(size_t)gn * ldb + gkb] : B[(size_t)gkb * ldb + gn])
+                                      : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int kk = 0; kk < 16; ++kk) {
+      float a[4], b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        a[i] = as[kk][ty * 4 + i];
+        b[i] = bs[kk][tx * 4 + i];
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(a[i], b[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int gm = m0 + ty * 4 + i;
+    if (gm >= M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int gn = n0 + tx * 4 + j;
+      if (gn >= N) continue;
+      float* cp = C + (size_t)gm * ldc + gn;
+      *cp = alpha * acc[i][j] + (beta != 0.f ? beta * *cp : 0.f);
+    }
+  }
+}
+
+// --------------------------------------------------------------- RMSNorm ---
+// y = x r gamma with r = 1 / sqrt(mean(x^2) + eps):
+// dx = r gamma dy - x r^3 / d * sum_c(gamma dy x); dgamma_c = sum_rows dy x r.
+__global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ gamma,
+                                                          const float* __restrict__ dy, int d,
+                                                          float eps, int accumulate,
+                                                          float* __restrict__ dx,
+                                                          float* __restrict__ rinv) {
+  __shared__ float part[2][4];
+  const int64_t r = blockIdx.x;
+  const float* xr = x + r * d;
+  const float* gr = dy + r * d;
+  float ss = 0.f, dot = 0.f;
+  for (int c = threadIdx.x; c < d; c += 256) {
+    ss = fmaf(xr[c], xr[c], ss);
+    dot = fmaf(gamma[c] * gr[c], xr[c], dot);
+  }
+  ss = wave_sum(ss);
+  dot = wave_sum(dot);
+  if (threadIdx.x % kWave == 0) {
+    part[0][threadIdx.x / kWave] = ss;
+    part[1][threadIdx.x / kWave] = dot;
+  }
+  __syncthreads();
+  const float tot = part[0][0] + part[0][1] + part[0][2] + part[0][3];
+  const float sdot = part[1][0] + part[1][1] + part[1][2] + part[1][3];
+  const float rs = 1.f / sqrtf(tot / (float)d + eps);
+  const float k = rs * rs * rs / (float)d * sdot;
+  for (int c = threadIdx.x; c < d; c += 256) {
+    const float v = rs * gamma[c] * gr[c] - xr[c] * k;
+    dx[r * d + c] = accumulate ? dx[r * d + c] + v : v;
+  }
+  if (threadIdx.x == 0) rinv[r] = rs;
+}
+
+// dgamma_c = sum over rows in order (deterministic), one thread per column
+__global__ void rmsnorm_dgamma_kernel(const float* __restrict__ x, const float* __restrict__ dy,
+                                      const float* __restrict__ rinv, int64_t rows, int d,
+                                      int accumulate, float* __restrict__ dgamma) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  float s = 0.f;
+  for (int64_t r = 0; r < rows; ++r) s = fmaf(dy[r * d + c] * x[r * d + c], rinv[r], s);
+  dgamma[c] = accumulate ? dgamma[c] + s : s;
+}
+
+// ------------------------------------------------------------------ RoPE ---
+// qkv rows [rows, (H + 2 KVH) hd]: rotate the q and k heads in place (DIR = +1)
+// or apply the transposed rotation to their gradients (DIR = -1).
+template <int DIR>
+__global__ void rope_qk_kernel(float* __restrict__ qkv, const float2* __restrict__ rope,
+                               const int32_t* __restrict__ pos0, int L, int H, int KVH, int hd,
+                               int64_t rows) {
+  const int half = hd / 2, slots = H + KVH;  // q and k heads
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * slots * half) return;
+  const int p = idx % half;
+  const int slot = (idx / half) % slots;
+  const int64_t row = idx / ((int64_t)half * slots);
+  const int pos = pos0[row / L] + (int)(row % L);
+  float* e = qkv + row * (int64_t)(H + 2 * KVH) * hd + (int64_t)slot * hd + 2 * p;
+  const float2 cs = rope[(size_t)pos * half + p];
+  const float a = e[0], b = e[1];
+  if (DIR > 0) {
+    e[0] = a * cs.x - b * cs.y;
+    e[1] = b * cs.x + a * cs.y;
+  } else {
+    e[0] = a * cs.x + b * cs.y;
+    e[1] = b * cs.x - a * cs.y;
+  }
+}
+
+// ------------------------------------------------------------- attention ---
+// Forward inputs: q [S*L, H, hd], k / v [S, KVH, L, hd] (positions 0..L-1,
+// causal), o [S*L, H, hd], lse [S*H, L]; dO like o.
+// delta[s,h,r] = <dO, O>; dq = scale sum_t ds_t k_t with
+// ds_t = p_t (<dO, v_t> - delta), p_t = exp(scale <q, k_t> - lse).
+template <int HD>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ o, const float* __restrict__ dout, const float* __restrict__ lse,
+    int S, int L, int H, int KVH, float scale, float* __restrict__ dq, float* __restrict__ delta) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (s, r, h)
+  if (idx >= (int64_t)S * L * H) return;
+  const int h = idx % H, r = (idx / H) % L, s = (int)(idx / ((int64_t)H * L));
+  const int kvh = h / (H / KVH);
+  const float* qp = q + idx * HD;
+  const float* op = o + idx * HD;
+  const float* gp = dout + idx * HD;
+  const float* kb = k + ((size_t)s * KVH + kvh) * L * HD;
+  const float* vb = v + ((size_t)s * KVH + kvh) * L * HD;
+  float dlt = 0.f;
+  for (int d = 0; d < HD; ++d) dlt = fmaf(gp[d], op[d], dlt);
+  const float ls = lse[((size_t)s * H + h) * L + r];
+  float acc[HD];
+#pragma unroll
+  for (int d = 0; d < HD; ++d) acc[d] = 0.f;
+  for (int t = 0; t <= r; ++t) {
+    float sc = 0.f, dp = 0.f;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) {
+      sc = fmaf(qp[d], kb[(size_t)t * HD + d], sc);
+      dp = fmaf(gp[d], vb[(size_t)t * HD + d], dp);
+    }
+    const float p = expf(sc * scale - ls);
+    const float ds = p * (dp - dlt) * scale;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) acc[d] = fmaf(ds, kb[(size_t)t * HD + d], acc[d]);
+  }
+#pragma unroll
+  for (int d = 0; d < HD; ++d) dq[idx * HD + d] = acc[d];
+  delta[((size_t)s * H + h) * L + r] = dlt;
+}
+
+// dk_t = scale sum_{h in group, r >= t} ds q_r ; dv_t = sum p dO_r (GQA groups summed)
+template <int HD>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
+    int S, int L, int H, int KVH, float scale, float* __restrict__ dk, float* __restrict__ dv) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (s, kvh, t)
+  if (idx >= (int64_t)S * KVH * L) return;
+  const int t = idx % L, kvh = (idx / L) % KVH, s = (int)(idx / ((int64_t)L * KVH));
+  const int group = H / KVH;
+  const float* kt = k + idx * HD;
+  const float* vt = v + idx * HD;
+  float ak[HD], av[HD];
+#pragma unroll
+  for (int d = 0; d < HD; ++d) ak[d] = av[d] = 0.f;
+  for (int hh = 0; hh < group; ++hh) {
+    const int h = kvh * group + hh;
+    for (int r = t; r < L; ++r) {
+      const int64_t row = ((int64_t)s * L + r) * H + h;
+      const float* qp = q + row * HD;
+      const float* gp = dout + row * HD;
+      float sc = 0.f, dp = 0.f;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) {
+        sc = fmaf(qp[d], kt[d], sc);
+        dp = fmaf(gp[d], vt[d], dp);
+      }
+      const size_t li = ((size_t)s * H + h) * L + r;
+      const float p = expf(sc * scale - lse[li]);
+      const float ds = p * (dp - delta[li]) * scale;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) {
+        av[d] = fmaf(p, gp[d], av[d]);
+        ak[d] = fmaf(ds, qp[d], ak[d]);
+      }
+    }
+  }
+#pragma unroll
+  for (int d = 0; d < HD; ++d) {
+    dk[idx * HD + d] = ak[d];
+    dv[idx * HD + d] = av[d];
+  }
+}
+
+// ------------------------------------------------------------- embedding ---
+__global__ void embed_bwd_kernel(const int32_t* __restrict__ ids, const float* __restrict__ dx,
+                                 int64_t rows, int d, int vocab, float* __restrict__ dtable) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= rows * d) return;
+  const int id = ids[i / d];
+  if (id < 0 || id >= vocab) return;
+  atomicAdd(&dtable[(int64_t)id * d + i % d], dx[i]);
+}
+
+// ------------------------------------------------------------ optimizers ---
+// AdamW with decoupled weight decay: m, v moments, bias-corrected step.
+__global__ void adamw_kernel(float* __restrict__ p, const float* __restrict__ g,
+                             float* __restrict__ m, float* __restrict__ v, int64_t n, float lr,
+                             float b1, float b2, float eps, float wd, float c1, float c2) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float gi = g[i];
+  const float mi = b1 * m[i] + (1.f - b1) * gi;
+  const float vi = b2 * v[i] + (1.f - b2) * gi * gi;
+  m[i] = mi;
+  v[i] = vi;
+  const float upd = (mi / c1) / (sqrtf(vi / c2) + eps);
+  p[i] = p[i] * (1.f - lr * wd) - lr * upd;
+}
+
+// Muon momentum (muon.rs:200-204): velocity = g + mu * velocity (g alone on
+// the first step), update = mu * velocity + g.
+__global__ void muon_momentum_kernel(const float* __restrict__ g, float* __restrict__ vel,
+                                     float* __restrict__ upd, int64_t n, float mu, int first) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const float vi = first ? g[i] : g[i] + vel[i] * mu;
+  vel[i] = vi;
+  upd[i] = vi * mu + g[i];
+}
+
+// y = a * x + b * y over n elements
+__global__ void axpby_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n,
+                             float a, float b) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  y[i] = a * x[i] + b * y[i];
+}
+
+// out[0] = max(sqrt(sum x^2), eps) in f64 partial order (one workgroup)
+__global__ __launch_bounds__(1024) void frob_norm_kernel(const float* __restrict__ x, int64_t n,
+                                                          float eps, float* __restrict__ out) {
+  __shared__ double part[16];
+  double s = 0.0;
+  for (int64_t i = threadIdx.x; i < n; i += 1024) s += (double)x[i] * x[i];
+  s = wave_sum_f64(s);
+  if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < 16; ++w) t += part[w];
+    out[0] = fmaxf((float)sqrt(t), eps);
+  }
+}
+
+__global__ void scale_by_kernel(float* __restrict__ x, int64_t n, const float* __restrict__ div) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) x[i] = x[i] / div[0];
+}
+
+inline unsigned g256(int64_t n) { return (unsigned)ceil_div(n, 256); }
+
+}  // namespace
+}  // namespace sm
+
+using namespace sm;
+
+extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                          const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                          float* C, int64_t ldc, void* stream) {
+  SM_REQUIRE(A && B && C, "sm_gemm_ex: null buffer");
+  SM_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1 << 30) && N < (1 << 30) && K < (1 << 30),
+             "sm_gemm_ex: bad shape");
+  SM_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N,
+             "sm_gemm_ex: leading dimension too small");
+  if (M == 0 || N == 0) return SM_OK;
+  const dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
+  hipStream_t st = as_stream(stream);
+#define SM_GX(TA, TB)                                                                        \
+  gemm_ex_kernel<TA, TB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, \
+                                               alpha, beta)
+  if (trans_a && trans_b) SM_GX(true, true);
+  else if (trans_a) SM_GX(true, false);
+  else if (trans_b) SM_GX(false, true);
+  else SM_GX(false, false);
+#undef SM_GX
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy,
+                                   int64_t rows, int64_t d, float eps, int accumulate, float* dx,
+                                   float* dgamma, float* rinv_scratch, void* stream) {
+  SM_REQUIRE(x && gamma && dy && dx && rinv_scratch, "sm_rmsnorm_backward: null buffer");
+  SM_REQUIRE(rows >= 0 && d > 0, "sm_rmsnorm_backward: bad shape");
+  if (rows == 0) return SM_OK;
+  hipStream_t st = as_stream(stream);
+  rmsnorm_bwd_kernel<<<(unsigned)rows, 256, 0, st>>>(x, gamma, dy, (int)d, eps, accumulate, dx,
+                                                     rinv_scratch);
+  if (dgamma)
+    rmsnorm_dgamma_kernel<<<g256(d), 256, 0, st>>>(x, dy, rinv_scratch, rows, (int)d, accumulate,
+                                                   dgamma);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_rope_qk(float* qkv, const float* rope_table, const int32_t* pos0, int64_t S,
+                          int64_t L, int64_t H, int64_t KVH, int64_t head_dim, int backward,
+                          void* stream) {
+  SM_REQUIRE(qkv && rope_table && pos0, "sm_rope_qk: null buffer");
+  SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && head_dim > 0 && head_dim % 2 == 0,
+             "sm_rope_qk: bad shape");
+  const int64_t rows = S * L, n = rows * (H + KVH) * (head_dim / 2);
+  if (n == 0) return SM_OK;
+  hipStream_t st = as_stream(stream);
+  const float2* rt = reinterpret_cast<const float2*>(rope_table);
+  if (backward)
+    rope_qk_kernel<-1><<<g256(n), 256, 0, st>>>(qkv, rt, pos0, (int)L, (int)H, (int)KVH,
+                                                (int)head_dim, rows);
+  else
+    rope_qk_kernel<1><<<g256(n), 256, 0, st>>>(qkv, rt, pos0, (int)L, (int)H, (int)KVH,
+                                               (int)head_dim, rows);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_attn_backward_f32(const float* q, const float* k, const float* v, const float* o,
+                                    const float* dout, const float* lse, int64_t S, int64_t L,
+                                    int64_t H, int64_t KVH, int64_t head_dim, float* dq,
+                                    float* dk, float* dv, float* delta_scratch, void* stream) {
+  SM_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta_scratch,
+             "sm_attn_backward_f32: null buffer");
+  SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && H % KVH == 0, "sm_attn_backward_f32: bad shape");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128, "sm_attn_backward_f32: head_dim must be 64 or 128");
+  if (S == 0 || L == 0) return SM_OK;
+  hipStream_t st = as_stream(stream);
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  const int64_t nq = S * L * H, nk = S * KVH * L;
+  if (head_dim == 64) {
+    attn_bwd_dq_kernel<64><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L, (int)H,
+                                                     (int)KVH, scale, dq, delta_scratch);
+    attn_bwd_dkv_kernel<64><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
+                                                      (int)L, (int)H, (int)KVH, scale, dk, dv);
+  } else {
+    attn_bwd_dq_kernel<128><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L,
+                                                      (int)H, (int)KVH, scale, dq, delta_scratch);
+    attn_bwd_dkv_kernel<128><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
+                                                       (int)L, (int)H, (int)KVH, scale, dk, dv);
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_embed_backward(const int32_t* ids, const float* dx, int64_t rows, int64_t d,
+                                 int64_t vocab, float* dtable, void* stream) {
+  SM_REQUIRE(ids && dx && dtable, "sm_embed_backward: null buffer");
+  SM_REQUIRE(rows >= 0 && d > 0 && vocab > 0, "sm_embed_backward: bad shape");
+  if (rows == 0) return SM_OK;
+  embed_bwd_kernel<<<g256(rows * d), 256, 0, as_stream(stream)>>>(ids, dx, rows, (int)d,
+                                                                  (int)vocab, dtable);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n,
+                             float lr, float beta1, float beta2, float eps, float weight_decay,
+                             int64_t step, void* stream) {
+  SM_REQUIRE(param && grad && m && v, "sm_adamw_step: null buffer");
+  SM_REQUIRE(n >= 0 && step >= 1, "sm_adamw_step: step counts from 1");
+  SM_REQUIRE(std::isfinite(lr) && beta1 >= 0.f && beta1 < 1.f && beta2 >= 0.f && beta2 < 1.f &&
+                 eps > 0.f && weight_decay >= 0.f,
+             "sm_adamw_step: invalid hyperparameters");
+  if (n == 0) return SM_OK;
+  const float c1 = 1.f - powf(beta1, (float)step), c2 = 1.f - powf(beta2, (float)step);
+  adamw_kernel<<<g256(n), 256, 0, as_stream(stream)>>>(param, grad, m, v, n, lr, beta1, beta2,
+                                                       eps, weight_decay, c1, c2);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_muon_momentum(const float* grad, float* velocity, float* update, int64_t n,
+                                float momentum, int first_step, void* stream) {
+  SM_REQUIRE(grad && velocity && update, "sm_muon_momentum: null buffer");
+  if (n <= 0) return SM_OK;
+  muon_momentum_kernel<<<g256(n), 256, 0, as_stream(stream)>>>(grad, velocity, update, n, momentum,
+                                                               first_step);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_axpby(const float* x, float* y, int64_t n, float a, float b, void* stream) {
+  SM_REQUIRE(x && y, "sm_axpby: null buffer");
+  if (n <= 0) return SM_OK;
+  axpby_kernel<<<g256(n), 256, 0, as_stream(stream)>>>(x, y, n, a, b);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_frobenius_normalize(float* x, int64_t n, float eps, float* norm_out,
+                                      void* stream) {
+  SM_REQUIRE(x && norm_out, "sm_frobenius_normalize: null buffer");
+  if (n <= 0) return SM_OK;
+  hipStream_t st = as_stream(stream);
+  frob_norm_kernel<<<1, 1024, 0, st>>>(x, n, eps, norm_out);
+  scale_by_kernel<<<g256(n), 256, 0, st>>>(x, n, norm_out);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}

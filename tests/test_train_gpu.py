@@ -1,0 +1,247 @@
+"""Policy-update path for fp32 models (summa_amd/train.py over the train.hip
+kernels) against torch.autograd in float64 on the CPU: each backward kernel,
+the whole policy gradient of sum(dlp * lp) through an independent torch
+restatement of the decoder, AdamW against torch.optim.AdamW, and Muon's
+Newton-Schulz against its formula and the orthogonality it aims for."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from summa_amd import ops, train
+from summa_amd._lib import call
+from summa_amd.model import Model, ModelConfig
+
+pytestmark = pytest.mark.gpu
+
+
+def _st():
+    return torch.cuda.current_stream().cuda_stream
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+def test_gemm_ex_transposes(dev, ta, tb):
+    M, N, K = 77, 130, 45
+    rng = np.random.default_rng(ta * 2 + tb)
+    A = rng.normal(0, 1, (K, M) if ta else (M, K))
+    B = rng.normal(0, 1, (N, K) if tb else (K, N))
+    C = rng.normal(0, 1, (M, N))
+    ref = 0.5 * ((A.T if ta else A) @ (B.T if tb else B)) + 2.0 * C
+    out = torch.from_numpy(C.astype(np.float32)).to(dev)
+    train.gemm(torch.from_numpy(A.astype(np.float32)).to(dev), torch.from_numpy(B.astype(np.float32)).to(dev),
+               ta=bool(ta), tb=bool(tb), out=out, alpha=0.5, beta=2.0)
+    np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-4)
+
+
+def test_rmsnorm_backward_matches_autograd(dev):
+    rows, d, eps = 33, 300, 1e-5
+    x = torch.randn(rows, d, dtype=torch.float64, requires_grad=True)
+    g = torch.rand(d, dtype=torch.float64, requires_grad=True)
+    y = x / torch.sqrt((x * x).mean(1, keepdim=True) + eps) * g
+    dy = torch.randn(rows, d, dtype=torch.float64)
+    y.backward(dy)
+    dx = torch.full((rows, d), 0.5, device=dev)
+    dg = torch.zeros(d, device=dev)
+    rinv = torch.empty(rows, device=dev)
+    xd, gd, dyd = (t.detach().float().to(dev) for t in (x, g, dy))
+    call("sm_rmsnorm_backward", xd.data_ptr(), gd.data_ptr(), dyd.data_ptr(), rows, d, eps, 1,
+         dx.data_ptr(), dg.data_ptr(), rinv.data_ptr(), _st())
+    torch.testing.assert_close(dx.cpu().double(), x.grad + 0.5, rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(dg.cpu().double(), g.grad, rtol=1e-4, atol=1e-4)
+
+
+def _rope_t(x, tab, pos):
+    """adjacent-pair rotation of x [.., L, heads, hd] at positions pos [L] (f64)."""
+    c = tab[pos][:, None, :, 0]
+    s = tab[pos][:, None, :, 1]
+    a, b = x[..., 0::2], x[..., 1::2]
+    out = torch.stack([a * c - b * s, b * c + a * s], -1)
+    return out.flatten(-2)
+
+
+def test_rope_qk_forward_and_backward(dev):
+    cfg = ModelConfig(layers=1, d_model=128, heads=4, kv_heads=2, head_dim=64, ffn=128,
+                      vocab=10, max_seq=32, quantized=False)
+    S, L, H, KVH, hd = 2, 9, 4, 2, 64
+    tab = train.rope_table(cfg, dev)
+    pos0 = torch.tensor([0, 5], dtype=torch.int32, device=dev)
+    qkv = torch.randn(S * L, (H + 2 * KVH) * hd, dtype=torch.float64)
+    x = qkv.clone().requires_grad_(True)
+    t64 = tab.cpu().double()
+    parts = []
+    for s in range(S):
+        pos = torch.arange(L) + int(pos0[s])
+        row = x[s * L:(s + 1) * L]
+        q = _rope_t(row[:, :H * hd].view(L, H, hd), t64, pos).reshape(L, -1)
+        k = _rope_t(row[:, H * hd:(H + KVH) * hd].view(L, KVH, hd), t64, pos).reshape(L, -1)
+        parts.append(torch.cat([q, k, row[:, (H + KVH) * hd:]], 1))
+    y = torch.cat(parts)
+    dy = torch.randn_like(y)
+    y.backward(dy)
+    d = qkv.float().to(dev)
+    call("sm_rope_qk", d.data_ptr(), tab.data_ptr(), pos0.data_ptr(), S, L, H, KVH, hd, 0, _st())
+    torch.testing.assert_close(d.cpu().double(), y.detach(), rtol=1e-5, atol=1e-5)
+    g = dy.float().to(dev)
+    call("sm_rope_qk", g.data_ptr(), tab.data_ptr(), pos0.data_ptr(), S, L, H, KVH, hd, 1, _st())
+    torch.testing.assert_close(g.cpu().double(), x.grad, rtol=1e-5, atol=1e-5)
+
+
+def _attn_t(q, k, v, H, KVH):
+    """causal GQA attention, q [S, L, H, hd], k/v [S, KVH, L, hd] (f64)."""
+    S, L, _, hd = q.shape
+    kk = k.repeat_interleave(H // KVH, dim=1)
+    vv = v.repeat_interleave(H // KVH, dim=1)
+    sc = torch.einsum("slhd,shtd->shlt", q, kk) / math.sqrt(hd)
+    mask = torch.ones(L, L, dtype=torch.bool).triu(1)
+    sc = sc.masked_fill(mask, float("-inf"))
+    p = torch.softmax(sc, -1)
+    return torch.einsum("shlt,shtd->slhd", p, vv), torch.logsumexp(sc, -1)
+
+
+@pytest.mark.parametrize("hd,H,KVH", [(64, 4, 2), (128, 4, 4)])
+def test_attention_backward_matches_autograd(dev, hd, H, KVH):
+    S, L = 2, 21
+    q = torch.randn(S, L, H, hd, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(S, KVH, L, hd, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(S, KVH, L, hd, dtype=torch.float64, requires_grad=True)
+    o, lse = _attn_t(q, k, v, H, KVH)
+    do = torch.randn_like(o)
+    o.backward(do)
+    qd, kd, vd, od, dod = (t.detach().float().contiguous().to(dev) for t in (q, k, v, o, do))
+    lsed = lse.detach().float().contiguous().to(dev)
+    dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+    delta = torch.empty(S * H * L, device=dev)
+    call("sm_attn_backward_f32", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), od.data_ptr(),
+         dod.data_ptr(), lsed.data_ptr(), S, L, H, KVH, hd, dq.data_ptr(), dk.data_ptr(),
+         dv.data_ptr(), delta.data_ptr(), _st())
+    for got, want in ((dq, q.grad), (dk, k.grad), (dv, v.grad)):
+        torch.testing.assert_close(got.cpu().double(), want, rtol=1e-4, atol=1e-4)
+
+
+CFG = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
+                  max_seq=32, quantized=False)
+
+
+def _torch_lp(w, cfg, prompts, tokens):
+    """Independent float64 restatement of the decoder's recompute."""
+    S, P = prompts.shape
+    N = tokens.shape[1]
+    L = P + N - 1
+    H, KVH, hd, F, eps = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.ffn, cfg.norm_eps
+    ids = torch.cat([prompts, tokens[:, :N - 1]], 1).long()
+    rms = lambda x, g: x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * g
+    half = hd // 2
+    freq = float(cfg.rope_theta) ** (-2.0 * torch.arange(half, dtype=torch.float64) / hd)
+    ang = torch.arange(L, dtype=torch.float64)[:, None] * freq[None, :]
+    tab = torch.stack([torch.cos(ang), torch.sin(ang)], -1).float().double()
+    pos = torch.arange(L)
+    x = w["embed"][ids]
+    for i in range(cfg.layers):
+        h = rms(x, w["attn_norm"][i])
+        qkv = h @ w["qkv"][i].T
+        q = _rope_t(qkv[..., :H * hd].reshape(S, L, H, hd), tab, pos)
+        k = _rope_t(qkv[..., H * hd:(H + KVH) * hd].reshape(S, L, KVH, hd), tab, pos)
+        v = qkv[..., (H + KVH) * hd:].reshape(S, L, KVH, hd)
+        o, _ = _attn_t(q, k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), H, KVH)
+        x = x + o.reshape(S, L, H * hd) @ w["o"][i].T
+        u = rms(x, w["ffn_norm"][i]) @ w["in"][i].T
+        x = x + (torch.nn.functional.silu(u[..., :F]) * u[..., F:]) @ w["down"][i].T
+    hf = rms(x, w["final_norm"])[:, P - 1:P - 1 + N]
+    logits = hf @ w["lm_head"].T
+    return torch.log_softmax(logits, -1).gather(-1, tokens.long()[..., None])[..., 0]
+
+
+def test_policy_gradient_matches_autograd(dev):
+    cfg = CFG.oracle_cfg()
+    w = oracle.random_weights(cfg, seed=11, std=0.05)
+    rng = np.random.default_rng(2)
+    prompts = torch.from_numpy(rng.integers(0, CFG.vocab, (4, 8)).astype(np.int32))
+    tokens = torch.from_numpy(rng.integers(0, CFG.vocab, (4, 6)).astype(np.int32))
+    pol = train.Fp32Policy(CFG, w, dev)
+    lp = pol.forward(prompts.to(dev), tokens.to(dev))
+    m = Model(CFG)
+    m.load_host_weights(w, dev)
+    np.testing.assert_allclose(lp.cpu().numpy(), m.logprobs(prompts.to(dev), tokens.to(dev)).cpu().numpy(),
+                               atol=1e-5)
+    dlp = torch.randn(4, 6, dtype=torch.float64)
+    grads = pol.backward(dlp.float().to(dev))
+    wt = {k: torch.from_numpy(np.asarray(v, dtype=np.float64)).requires_grad_(True) for k, v in w.items()}
+    lp_t = _torch_lp(wt, CFG, prompts, tokens)
+    np.testing.assert_allclose(lp.cpu().numpy(), lp_t.detach().numpy(), atol=2e-5)
+    (dlp * lp_t).sum().backward()
+    for k, t in wt.items():
+        got = grads[k].cpu().double()
+        scale = t.grad.abs().max().item() + 1e-12
+        err = (got - t.grad).abs().max().item() / scale
+        assert err < 2e-4, (k, err)
+
+
+def test_adamw_matches_torch(dev):
+    rng = np.random.default_rng(3)
+    p0 = rng.normal(0, 1, 1000)
+    tp = torch.tensor(p0, dtype=torch.float64, requires_grad=True)
+    opt = torch.optim.AdamW([tp], lr=1e-2, betas=(0.9, 0.95), eps=1e-8, weight_decay=0.1)
+    p = torch.tensor(p0, dtype=torch.float32, device=dev)
+    m, v = torch.zeros_like(p), torch.zeros_like(p)
+    for step in range(1, 6):
+        gr = rng.normal(0, 1, 1000)
+        tp.grad = torch.tensor(gr)
+        opt.step()
+        gd = torch.tensor(gr, dtype=torch.float32, device=dev)
+        call("sm_adamw_step", p.data_ptr(), gd.data_ptr(), m.data_ptr(), v.data_ptr(), 1000,
+             1e-2, 0.9, 0.95, 1e-8, 0.1, step, _st())
+    np.testing.assert_allclose(p.cpu().numpy(), tp.detach().numpy(), rtol=1e-5, atol=1e-6)
+
+
+@pytest.mark.parametrize("shape", [(96, 256), (256, 96)])
+def test_newton_schulz_formula_and_orthogonality(dev, shape):
+    g = torch.randn(*shape, dtype=torch.float64)
+    got = train.newton_schulz(g.float().to(dev)).cpu().double()
+    # muon.rs:257-285 in float64, on the Burn orientation of this [out, in] matrix
+    x = g.t()
+    tr = x.shape[0] > x.shape[1]
+    if tr:
+        x = x.t()
+    x = x / x.norm().clamp_min(1e-7)
+    a, b, c = train.NS_COEFFICIENTS
+    for _ in range(train.NS_STEPS):
+        gram = x @ x.t()
+        x = a * x + (b * gram + c * gram @ gram) @ x
+    want = (x.t() if tr else x).t()
+    torch.testing.assert_close(got, want, rtol=1e-3, atol=1e-4)
+    sv = torch.linalg.svdvals(got)
+    assert sv.min() > 0.5 and sv.max() < 1.3, sv  # near-orthogonal: the point of the iteration
+
+
+def test_grpo_update_lowers_the_surrogate_loss(dev):
+    """One GRPO step end to end: rollouts from the inference model, the
+    device loss and its dlp, the policy gradient, an AdamW step on every
+    weight, and the updated weights back in the model: the same batch's loss
+    drops."""
+    cfg = CFG.oracle_cfg()
+    w = oracle.random_weights(cfg, seed=12, std=0.05)
+    m = Model(CFG)
+    m.load_host_weights(w, dev)
+    G, B = 8, 2
+    prompts = torch.from_numpy(np.random.default_rng(4).integers(0, CFG.vocab, (B * G, 8)).astype(np.int32)).to(dev)
+    tok, beh = m.generate(prompts, 6, temperature=1.0, seed=9)
+    rewards = torch.from_numpy(np.random.default_rng(5).random((B, G)).astype(np.float32)).to(dev)
+    pol = train.Fp32Policy(CFG, w, dev)
+
+    def loss_and_dlp():
+        lp = pol.forward(prompts, tok)
+        out = ops.grpo_loss_batched(rewards, lp.view(B, G, 6), beh.view(B, G, 6), None, None,
+                                    kl_coefficient=0.0)
+        return float(out["stats"][:, 0].sum()), out["dlp"].view(B * G, 6)
+
+    l0, dlp = loss_and_dlp()
+    grads = pol.backward(dlp)
+    pol.adamw_step(grads, list(pol.p), lr=1e-3, wd=0.0)
+    l1, _ = loss_and_dlp()
+    assert l1 < l0, (l0, l1)
+    pol.to_model(m)
+    lp_m = m.logprobs(prompts, tok).cpu().numpy()
+    lp_p = pol.forward(prompts, tok).cpu().numpy()
+    np.testing.assert_allclose(lp_m, lp_p, atol=1e-5)
