@@ -350,6 +350,11 @@ extern "C" int sm_attn_prefill_lse(const void* q, const void* kcache, const void
              "sm_attn_prefill: dtype must be SM_BF16, SM_F16 or SM_F32");
   const int om = out_mode(out_dtype);
   SM_REQUIRE(om >= 0, "sm_attn_prefill: 16-bit attention writes bf16, f16 or f16 pairs");
+  SM_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(kcache) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(vcache) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(out) % 8 == 0,
+             "sm_attn_prefill: q and the caches must be 16-byte aligned, out 8-byte aligned");
   return attn_prefill_16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
                          pos0, out, lse, dtype == SM_F16, om, (int)S, (int)L, (int)H, (int)KVH,
                          (int)cap, (int)head_dim, st);

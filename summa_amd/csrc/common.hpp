@@ -165,6 +165,7 @@ __host__ __device__ inline uint32_t q4_prepare_word(uint32_t w) {
 }
 
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 
 __device__ inline h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
@@ -172,6 +173,12 @@ __device__ inline h2 as_h2(uint32_t u) { return __builtin_bit_cast(h2, u); }
 // fp32 -> f16 pair (the SM_F16X2 activation format): hi = f16(x),
 // lo = f16(x - hi), so hi + lo carries x to about 22 significant bits.
 __device__ inline void split_f16(float x, _Float16& hi, _Float16& lo) {
+  // Both halves must come from one rounded f32 value. Without the empty asm
+  // the compiler may fold the multiply that produced x into the f16
+  // conversions (v_fma_mix*), rounding hi from the f32 product for the store
+  // but from the exact product for the subtraction: when the f32 rounding lands
+  // on an f16 midpoint the pair is then off by one f16 ulp (~1 value in 8000).
+  asm volatile("" : "+v"(x));
   hi = (_Float16)x;
   lo = (_Float16)(x - (float)hi);
 }

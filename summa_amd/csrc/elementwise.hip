@@ -63,6 +63,56 @@ __global__ __launch_bounds__(256) void rmsnorm_kernel(const float* __restrict__ 
   }
 }
 
+// One wave per row for d = 256 * V (the models' widths): the row stays in
+// registers (V float4 per lane, lane l holding columns 4*(64*i + l) + 0..3, so
+// every load and store instruction covers a contiguous 1 KB of the row), one
+// read of x, a shuffle reduction, no barrier. Four rows per workgroup.
+template <typename TO, bool PAIR, int V>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const float* __restrict__ x,
+                                                           const float* __restrict__ gamma,
+                                                           int64_t rows, float eps,
+                                                           TO* __restrict__ y) {
+  constexpr int D = 256 * V;
+  const int64_t r = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  if (r >= rows) return;  // uniform per wave
+  const int lane = threadIdx.x % kWave;
+  const float4* xr = reinterpret_cast<const float4*>(x + r * D);
+  float4 v[V];
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < V; ++i) v[i] = xr[i * kWave + lane];
+#pragma unroll
+  for (int i = 0; i < V; ++i)
+    ss = fmaf(v[i].w, v[i].w, fmaf(v[i].z, v[i].z, fmaf(v[i].y, v[i].y, fmaf(v[i].x, v[i].x, ss))));
+  ss = wave_sum(ss);
+  const float rms = sqrtf(ss / (float)D + eps);
+  const float4* gr = reinterpret_cast<const float4*>(gamma);
+#pragma unroll
+  for (int i = 0; i < V; ++i) {
+    const float4 gm = gr[i * kWave + lane];
+    const float o[4] = {v[i].x / rms * gm.x, v[i].y / rms * gm.y, v[i].z / rms * gm.z,
+                        v[i].w / rms * gm.w};
+    const int c = 4 * (i * kWave + lane);
+    if constexpr (PAIR) {
+      _Float16 hi[4], lo[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) split_f16(o[e], hi[e], lo[e]);
+      _Float16* yr = reinterpret_cast<_Float16*>(y) + r * 2 * D;
+      *reinterpret_cast<h4*>(yr + c) = h4{hi[0], hi[1], hi[2], hi[3]};
+      *reinterpret_cast<h4*>(yr + D + c) = h4{lo[0], lo[1], lo[2], lo[3]};
+    } else if constexpr (sizeof(TO) == 4) {
+      *reinterpret_cast<float4*>(y + r * D + c) = float4{o[0], o[1], o[2], o[3]};
+    } else {
+      TO t[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t[e] = from_f<TO>(o[e]);
+      uint2 u;
+      __builtin_memcpy(&u, t, 8);
+      *reinterpret_cast<uint2*>(y + r * D + c) = u;
+    }
+  }
+}
+
 // qkv: [rows, (H + 2*KVH) * hd] f32, row = s*L + i at position pos0[s] + i.
 // One thread per (row, head slot, pair).
 template <typename TA, typename TC>
@@ -185,20 +235,42 @@ extern "C" int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int6
                           void* y, int out_dtype, void* stream) {
   SM_REQUIRE(x && gamma && y, "sm_rmsnorm: null buffer");
   SM_REQUIRE(rows >= 0 && d > 0, "sm_rmsnorm: bad shape");
+  SM_REQUIRE(out_dtype == SM_BF16 || out_dtype == SM_F16 || out_dtype == SM_F16X2 ||
+                 out_dtype == SM_F32,
+             "sm_rmsnorm: out_dtype must be SM_F32, SM_BF16, SM_F16 or SM_F16X2");
   if (rows == 0) return SM_OK;
-  if (out_dtype == SM_BF16)
-    rmsnorm_kernel<uint16_t><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
-                                                                           (uint16_t*)y);
+  hipStream_t st = as_stream(stream);
+  const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
+                       reinterpret_cast<uintptr_t>(y) % 16 == 0;
+  const int v = (d % 256 == 0 && aligned) ? (int)(d / 256) : 0;
+  if (v == 3 || v == 4 || v == 8 || v == 12 || v == 16) {
+    const unsigned blocks = (unsigned)ceil_div(rows, 4);
+#define SM_RMSW(TO, PAIR, V) \
+  rmsnorm_wave_kernel<TO, PAIR, V><<<blocks, 256, 0, st>>>(x, gamma, rows, eps, (TO*)y)
+#define SM_RMSW_V(TO, PAIR)            \
+  do {                                 \
+    if (v == 3) SM_RMSW(TO, PAIR, 3);  \
+    else if (v == 4) SM_RMSW(TO, PAIR, 4);   \
+    else if (v == 8) SM_RMSW(TO, PAIR, 8);   \
+    else if (v == 12) SM_RMSW(TO, PAIR, 12); \
+    else SM_RMSW(TO, PAIR, 16);        \
+  } while (0)
+    if (out_dtype == SM_BF16) SM_RMSW_V(uint16_t, false);
+    else if (out_dtype == SM_F16) SM_RMSW_V(_Float16, false);
+    else if (out_dtype == SM_F16X2) SM_RMSW_V(_Float16, true);
+    else SM_RMSW_V(float, false);
+#undef SM_RMSW_V
+#undef SM_RMSW
+  } else if (out_dtype == SM_BF16)
+    rmsnorm_kernel<uint16_t><<<(unsigned)rows, 256, 0, st>>>(x, gamma, (int)d, eps, (uint16_t*)y);
   else if (out_dtype == SM_F16)
-    rmsnorm_kernel<_Float16><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
-                                                                           (_Float16*)y);
+    rmsnorm_kernel<_Float16><<<(unsigned)rows, 256, 0, st>>>(x, gamma, (int)d, eps, (_Float16*)y);
   else if (out_dtype == SM_F16X2)
-    rmsnorm_kernel<_Float16, true><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(
-        x, gamma, (int)d, eps, (_Float16*)y);
-  else if (out_dtype == SM_F32)
-    rmsnorm_kernel<float><<<(unsigned)rows, 256, 0, as_stream(stream)>>>(x, gamma, (int)d, eps,
-                                                                        (float*)y);
-  else SM_REQUIRE(false, "sm_rmsnorm: out_dtype must be SM_F32, SM_BF16, SM_F16 or SM_F16X2");
+    rmsnorm_kernel<_Float16, true><<<(unsigned)rows, 256, 0, st>>>(x, gamma, (int)d, eps,
+                                                                  (_Float16*)y);
+  else
+    rmsnorm_kernel<float><<<(unsigned)rows, 256, 0, st>>>(x, gamma, (int)d, eps, (float*)y);
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

@@ -207,6 +207,28 @@ def test_rmsnorm_and_embed(dev):
                   <= np.abs(hi) * 2.0 ** -11 + 2.0 ** -24)
 
 
+@pytest.mark.parametrize("d", [768, 1024, 2048, 3072, 4096, 320, 1000])
+def test_rmsnorm_widths_and_dtypes(dev, d):
+    """Wave-per-row kernel (d = 256 * {3, 4, 8, 12, 16}) and the generic
+    kernel (other widths) against float64, every output dtype, a row count
+    that leaves a partial workgroup."""
+    rows = 7
+    rng = np.random.default_rng(d)
+    x = rng.normal(0, 1.5, (rows, d)).astype(np.float32)
+    g = rng.uniform(0.5, 1.5, d).astype(np.float32)
+    xd, gd = torch.from_numpy(x).to(dev), torch.from_numpy(g).to(dev)
+    xr = x.astype(np.float64)
+    ref = xr / np.sqrt((xr ** 2).mean(1, keepdims=True) + 1e-5) * g
+    for dt, tdt, rtol in ((SM_F32, torch.float32, 2e-6), (SM_BF16, torch.bfloat16, 2 ** -8),
+                          (SM_F16, torch.float16, 2 ** -11)):
+        y = torch.full((rows, d), float("nan"), dtype=tdt, device=dev)
+        call("sm_rmsnorm", xd.data_ptr(), gd.data_ptr(), rows, d, 1e-5, y.data_ptr(), dt, _s())
+        np.testing.assert_allclose(y.float().cpu().numpy(), ref, rtol=rtol, atol=1e-6)
+    yp = torch.full((rows, 2 * d), float("nan"), dtype=torch.float16, device=dev)
+    call("sm_rmsnorm", xd.data_ptr(), gd.data_ptr(), rows, d, 1e-5, yp.data_ptr(), SM_F16X2, _s())
+    np.testing.assert_allclose(_unpair(yp, d), ref, rtol=1e-6, atol=1e-7)
+
+
 @pytest.mark.parametrize("temperature", [0.0, 1.0, 0.7])
 def test_sample_matches_oracle(dev, temperature):
     rows, V = 16, 32768
