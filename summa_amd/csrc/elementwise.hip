@@ -77,21 +77,22 @@ __global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const float* __restri
   if (r >= rows) return;  // uniform per wave
   const int lane = threadIdx.x % kWave;
   const float4* xr = reinterpret_cast<const float4*>(x + r * D);
-  float4 v[V];
+  const float4* gr = reinterpret_cast<const float4*>(gamma);
+  float4 v[V], gm[V];  // gamma is loaded with x: one memory round trip
   float ss = 0.f;
 #pragma unroll
   for (int i = 0; i < V; ++i) v[i] = xr[i * kWave + lane];
+#pragma unroll
+  for (int i = 0; i < V; ++i) gm[i] = gr[i * kWave + lane];
 #pragma unroll
   for (int i = 0; i < V; ++i)
     ss = fmaf(v[i].w, v[i].w, fmaf(v[i].z, v[i].z, fmaf(v[i].y, v[i].y, fmaf(v[i].x, v[i].x, ss))));
   ss = wave_sum(ss);
   const float rms = sqrtf(ss / (float)D + eps);
-  const float4* gr = reinterpret_cast<const float4*>(gamma);
 #pragma unroll
   for (int i = 0; i < V; ++i) {
-    const float4 gm = gr[i * kWave + lane];
-    const float o[4] = {v[i].x / rms * gm.x, v[i].y / rms * gm.y, v[i].z / rms * gm.z,
-                        v[i].w / rms * gm.w};
+    const float o[4] = {v[i].x / rms * gm[i].x, v[i].y / rms * gm[i].y, v[i].z / rms * gm[i].z,
+                        v[i].w / rms * gm[i].w};
     const int c = 4 * (i * kWave + lane);
     if constexpr (PAIR) {
       _Float16 hi[4], lo[4];

@@ -182,9 +182,9 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_bl_kernel(BLArgs a) {
       }
   };
 
-  // EPI 6: the epilogue's positions do not depend on the product: load them
-  // before the main loop (one independent load per row) so their latency is
-  // hidden behind it. Even lanes own pairs (e, e+1).
+  // EPI 6: the epilogue's positions and RoPE factors do not depend on the
+  // product: load them before the main loop so their latency is hidden behind
+  // it. Even lanes own pairs (e, e+1).
   int slot_b[NBK], e_b[NBK];
   int srow[MT][4], prow[MT][4];
   float2 cs[MT][4][NBK];
@@ -208,6 +208,20 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_bl_kernel(BLArgs a) {
         prow[mt][r] = (row < mlim && pos >= 0 && pos < a.cap) ? pos : -1;
       }
   }
+  // (cos, sin) pairs: loaded here for one row block per wave, their loads
+  // completing during the main loop; 32-row waves load them in the epilogue
+  // (registers)
+  auto load_rope = [&]() {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float2* rrow = a.rope + (size_t)max(prow[mt][r], 0) * (a.hd / 2);
+#pragma unroll
+        for (int b = 0; b < NBK; ++b) cs[mt][r][b] = rrow[e_b[b] >> 1];
+      }
+  };
+  if constexpr (EPI == 6 && MT == 1) load_rope();
 
   f4 acc[MT][NBK];
 #pragma unroll
@@ -271,14 +285,7 @@ __global__ __launch_bounds__(256, 2) void q4_gemm_bl_kernel(BLArgs a) {
       for (int b = 0; b < NBK; ++b)
 #pragma unroll
         for (int r = 0; r < 4; ++r) partner[mt][b][r] = __shfl_xor(acc[mt][b][r], 1, kWave);
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float2* rrow = a.rope + (size_t)max(prow[mt][r], 0) * (a.hd / 2);
-#pragma unroll
-        for (int b = 0; b < NBK; ++b) cs[mt][r][b] = rrow[e_b[b] >> 1];
-      }
+    if constexpr (MT > 1) load_rope();
     if ((j & 1) == 0) {
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
