@@ -47,19 +47,22 @@ PlanView plan_view(int32_t* plan, int64_t routes, int64_t experts) {
 
 namespace {
 
-constexpr int kRouterThreads = 256;
+constexpr int kRouterThreads = 512;  // 8 waves: four experts each at E = 32
 constexpr int kRouterLds = 64 * 1024;  // dynamic LDS budget (h rows + logits)
 
-// One workgroup per TT tokens: their h rows go to LDS (f32), then each wave
-// takes experts e = wave, wave + 4, ...: its lanes stream W_r[e] once
-// (coalesced, c = lane + 64 u, eight loads in flight) and accumulate the dot
-// products of all TT tokens, reduced across the wave in a fixed order; the
-// router weights are read once per TT tokens instead of once per token. One
+// One workgroup per TT tokens: their h rows go to LDS (f32), then each of the
+// 8 waves takes experts e = wave, wave + 8, ...: its lanes stream W_r[e] once
+// (coalesced, c = lane + 64 u; for d = 768 and 2048 all of the expert's loads
+// in flight together, else eight) and accumulate the dot products of all TT
+// tokens, reduced across the wave in a fixed order; the router weights are
+// read once per TT tokens instead of once per token. (Four waves walking the
+// experts with eight loads in flight waited one L2 round trip per 512 weights:
+// 31 us per call at config[4].) One
 // thread per token then does the strict top-2 scan and the softmax over the
 // pair. Rows past the last token repeat the last token (their results are
 // not stored), so the inner loops carry no per-token branches.
 // TH: f32, f16, or f16 pair (PAIR: row t is hi[d] | lo[d]); VEC: d % 64 == 0.
-template <typename TH, bool PAIR, int TT, bool VEC>
+template <typename TH, bool PAIR, int TT, bool VEC, int CH = 0>
 __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
     const TH* __restrict__ h, const float* __restrict__ wr, int64_t tokens, int d, int E,
     float* __restrict__ logits_out, int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
@@ -94,7 +97,17 @@ __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
 #pragma unroll
     for (int t = 0; t < TT; ++t) acc[t] = 0.f;
     const float* we = wr + (size_t)e * d;
-    if constexpr (VEC) {
+    if constexpr (CH > 0) {
+      // d = 64 * CH: every weight load of the expert in flight at once (one
+      // L2 round trip per expert), then the same FMA order as below
+      float w[CH];
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch) w[ch] = we[ch * kWave + lane];
+#pragma unroll
+      for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+        for (int t = 0; t < TT; ++t) acc[t] = fmaf(hs[t * d + ch * kWave + lane], w[ch], acc[t]);
+    } else if constexpr (VEC) {
       const int chunks = d / kWave;
       int ch = 0;
       for (; ch + 8 <= chunks; ch += 8) {
@@ -154,7 +167,14 @@ void launch_router(const void* h, const float* wr, int64_t tokens, int d, int E,
   const size_t shmem = (size_t)TT * (d + E) * sizeof(float);
   const unsigned grid = (unsigned)ceil_div(tokens, TT);
   const bool vec = d % kWave == 0 && reinterpret_cast<uintptr_t>(h) % 16 == 0;
-  if (vec)
+  // (d = 2048 rows hold at most four tokens in the LDS budget: TT <= 4 there)
+  if (TT <= 4 && vec && d == 32 * kWave)
+    router_top2_kernel<TH, PAIR, TT, true, (TT <= 4 ? 32 : 0)><<<grid, kRouterThreads, shmem, st>>>(
+        static_cast<const TH*>(h), wr, tokens, d, E, lo, idx, w);
+  else if (vec && d == 12 * kWave)
+    router_top2_kernel<TH, PAIR, TT, true, 12><<<grid, kRouterThreads, shmem, st>>>(
+        static_cast<const TH*>(h), wr, tokens, d, E, lo, idx, w);
+  else if (vec)
     router_top2_kernel<TH, PAIR, TT, true><<<grid, kRouterThreads, shmem, st>>>(
         static_cast<const TH*>(h), wr, tokens, d, E, lo, idx, w);
   else
