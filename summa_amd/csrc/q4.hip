@@ -27,8 +27,8 @@
 // with no conversion at all. The small-M kernel accumulates each group's four
 // k-steps unscaled and applies the group scale with one FMA per output; the
 // large-M kernel folds the scale into B (exact in f16 for an f16-normal scale,
-// which sm_q4_quantize checks). The A operand is read by the lanes whose row
-// is < M only. For
+// which sm_q4_quantize checks). Lanes of rows >= M read a clamped valid row
+// and feed only output rows that are not stored. For
 // tiny N the four waves of a workgroup split the K groups and merge their
 // accumulators through LDS in a fixed order (deterministic).
 #include <algorithm>
@@ -136,7 +136,6 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   // serialises the round trips this kernel exists to overlap.
   const int prow = min(m0 + j, mlim - 1);  // activation row this lane feeds to the A operand
   const int arow = a.rowidx ? a.rowidx[prow] : prow;
-  const bool arow_ok = m0 + j < mlim;
   auto load_act = [&](int kg, h8 (&af)[NA][4]) {
     const int kc = min(kg, ngroups - 1);
 #pragma unroll
@@ -182,11 +181,14 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
     for (int u = 0; u < kU; ++u) {
       const int kg = kb0 + u * KSPLIT;
       if (kg >= ngroups) break;
+      // Lanes of rows past mlim hold a clamped valid row: they only feed MFMA
+      // output rows that the epilogue never stores (each D row depends on its
+      // A row alone), so no zeroing is needed.
       h8 af[NA][4];
 #pragma unroll
       for (int h = 0; h < NA; ++h)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) af[h][s] = arow_ok ? an[h][s] : h8{0, 0, 0, 0, 0, 0, 0, 0};
+        for (int s = 0; s < 4; ++s) af[h][s] = an[h][s];
       load_act(kg + KSPLIT, an);  // next group's activations, in flight during this one
       // Per block: the group's 4 k-steps accumulate unscaled codes, then one
       // FMA per output applies the group scale (cheaper than scaling B). f16
