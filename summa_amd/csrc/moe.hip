@@ -273,6 +273,83 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const int32_t*
   }
 }
 
+// The same plan for at most kPlanSmall routes (decode batches): one thread per
+// route and no serial scans. Per expert, a wave ballot gives the wave's count
+// and each route's rank among the wave's routes of that expert (lanes, like
+// waves, are in route order, so the sort stays stable); a 16-step pass per
+// expert turns the wave counts into wave bases, and one wave scans the
+// expert totals and tile counts with shuffles. Output identical to
+// route_plan_kernel.
+constexpr int kPlanSmall = 1024;
+
+__global__ __launch_bounds__(kPlanSmall) void route_plan_small_kernel(
+    const int32_t* __restrict__ idx, int routes, int k, int E, PlanView pv, int max16,
+    int max128, int32_t* __restrict__ error) {
+  constexpr int NW = kPlanSmall / kWave;
+  __shared__ int32_t wc[NW][kMaxExperts];  // wave counts, then wave bases
+  __shared__ int32_t offs[kMaxExperts];
+  const int r = threadIdx.x, wave = r / kWave, lane = r % kWave;
+  int e = -1;
+  if (r < routes) {
+    e = idx[r];
+    if (e < 0 || e >= E) {
+      atomicOr(error, 1);
+      pv.inverse[r] = -1;  // flagged route: combine skips it
+      e = -1;
+    }
+  }
+  const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  int rank = 0;
+  for (int x = 0; x < E; ++x) {
+    const uint64_t m = __ballot(e == x);
+    if (e == x) rank = __popcll(m & below);
+    if (lane == 0) wc[wave][x] = __popcll(m);
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // lane x: expert x's wave bases and total; then the exclusive scans of
+    // the totals and of the 16- / 128-row tile counts across the experts
+    int tot = 0;
+    if (lane < E) {
+      for (int w = 0; w < NW; ++w) {
+        const int c = wc[w][lane];
+        wc[w][lane] = tot;
+        tot += c;
+      }
+    }
+    const int t16 = (tot + 15) / 16, t128 = (tot + 127) / 128;
+    int s0 = tot, s16 = t16, s128 = t128;  // inclusive scans
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int a0 = __shfl_up(s0, o, kWave), a16 = __shfl_up(s16, o, kWave),
+                a128 = __shfl_up(s128, o, kWave);
+      if (lane >= o) { s0 += a0; s16 += a16; s128 += a128; }
+    }
+    if (lane < E) {
+      const int off = s0 - tot;
+      offs[lane] = off;
+      pv.counts[lane] = tot;
+      pv.offsets[lane] = off;
+      if (lane == E - 1) pv.offsets[E] = s0;
+      for (int i = 0, n = s16 - t16; i < t16; ++i, ++n)
+        if (n < max16) { pv.tiles16[2 * n] = lane; pv.tiles16[2 * n + 1] = 16 * i; }
+      for (int i = 0, n = s128 - t128; i < t128; ++i, ++n)
+        if (n < max128) { pv.tiles128[2 * n] = lane; pv.tiles128[2 * n + 1] = 128 * i; }
+      if (lane == E - 1) {
+        pv.ntiles16[0] = min(s16, max16);
+        pv.ntiles128[0] = min(s128, max128);
+      }
+    }
+  }
+  __syncthreads();
+  if (e >= 0) {
+    const int pos = offs[e] + wc[wave][e] + rank;
+    pv.order[pos] = r;
+    pv.inverse[r] = pos;
+    pv.src_rows[pos] = r / k;
+  }
+}
+
 // x[t, c] += sum_j w[t, j] * routed[inverse[t*k + j], c]   (f32); routes the
 // plan flagged (inverse < 0) contribute nothing
 __global__ void combine_kernel(const float* __restrict__ routed, const float* __restrict__ w,
@@ -336,9 +413,14 @@ extern "C" int sm_moe_route_plan(const int32_t* top_idx, int64_t tokens, int64_t
              "sm_moe_route_plan: bad shape");
   const int64_t routes = tokens * top_k;
   PlanView pv = plan_view(plan, routes, experts);
-  route_plan_kernel<<<1, kPlanThreads, 0, as_stream(stream)>>>(
-      top_idx, (int)routes, (int)top_k, (int)experts, pv,
-      (int)moe_max_tiles(routes, experts, 16), (int)moe_max_tiles(routes, experts, 128), error);
+  const int max16 = (int)moe_max_tiles(routes, experts, 16);
+  const int max128 = (int)moe_max_tiles(routes, experts, 128);
+  if (routes <= kPlanSmall)
+    route_plan_small_kernel<<<1, kPlanSmall, 0, as_stream(stream)>>>(
+        top_idx, (int)routes, (int)top_k, (int)experts, pv, max16, max128, error);
+  else
+    route_plan_kernel<<<1, kPlanThreads, 0, as_stream(stream)>>>(
+        top_idx, (int)routes, (int)top_k, (int)experts, pv, max16, max128, error);
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

@@ -78,8 +78,11 @@ def _expected_tiles(counts, rows):
 
 @pytest.mark.parametrize("T,k,E,used", [(1, 2, 2, 2), (7, 2, 8, 3), (128, 2, 32, 32),
                                         (4096, 2, 32, 20), (8192, 2, 64, 64), (1000, 1, 16, 16),
-                                        (0, 2, 8, 8)])
+                                        (0, 2, 8, 8), (512, 2, 64, 40), (300, 2, 64, 64),
+                                        (513, 2, 32, 32)])
 def test_route_plan_is_stable_and_invertible(dev, T, k, E, used):
+    """Up to 1024 routes the one-thread-per-route ballot kernel runs, above it
+    the counting-sort kernel; both must give numpy's stable argsort."""
     print(f"case plan T={T} k={k} E={E}", flush=True)
     rng = np.random.default_rng(T + E)
     experts_used = rng.choice(E, used, replace=False)
