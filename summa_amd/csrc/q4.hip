@@ -260,6 +260,182 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
   }
 }
 
+// Grouped (MoE) decode: the route plan's 16-row tiles with few rows each and
+// wide expert matrices. One workgroup = 8 waves x 16*NB columns of one plan
+// tile. q4_gemm_kernel's four waves each load the tile's activation rows
+// themselves, so at decode size those loads are 2/3 of the memory
+// instructions and the texture addresser, not HBM, sets the pace (~1.6 TB/s of
+// expert weights at config[4]). Here every K group's activation tile (16 rows x
+// 128 k, both halves of f16 pairs) is loaded once per workgroup, one 16-byte
+// chunk per thread, into one of two LDS buffers (one barrier per group), and
+// each wave reads its A fragments from LDS; weight groups stay register-direct
+// and double-buffered. Per block and group the MFMA sequence and the scale
+// FMA are q4_gemm_kernel's, so the results are identical.
+template <int NB, int EPI, int XT>
+__global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
+  constexpr int NA = (XT == X_F16X2) ? 2 : 1;
+  constexpr int AP = NA * 128 + 8;      // LDS row (f16): hi | lo | pad
+  constexpr int STG = 16 * NA * 16;     // 16-byte chunks per group tile
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][16 * AP];
+  if ((int)blockIdx.y >= a.ntiles[0]) return;  // uniform per workgroup
+  const int e = a.tiles[2 * blockIdx.y];
+  const int m0 = a.goff[e] + a.tiles[2 * blockIdx.y + 1];
+  const int mlim = a.goff[e + 1];
+  const uint8_t* codes = a.codes + (size_t)e * a.cstride;
+  const uint16_t* scales = a.scales + (size_t)e * a.sstride;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  const int c0 = (int)blockIdx.x * 8 * 16 * NB + wave * 16 * NB;
+  const int ngroups = a.K / 128;
+  int brow[NB], brow_c[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if constexpr (is_swiglu(EPI)) {
+      const int col = c0 / 2 + (b % (NB / 2)) * 16 + j;
+      brow[b] = (col < a.ncols) ? ((b < NB / 2) ? col : a.ncols + col) : -1;
+    } else {
+      const int col = c0 + b * 16 + j;
+      brow[b] = (col < a.N) ? col : -1;
+    }
+    brow_c[b] = brow[b] >= 0 ? brow[b] : 0;
+  }
+  // staging: thread t < STG copies chunk c of half h of tile row `srow`
+  const int t = threadIdx.x;
+  const bool stager = t < STG;
+  const int srow = t / (NA * 16), sh = (t / 16) % NA, sc16 = t % 16;
+  const int sprow = min(m0 + srow, mlim - 1);  // rows past the tile repeat a valid row
+  const int sarow = a.rowidx ? a.rowidx[sprow] : sprow;
+  const size_t sxo = (size_t)sarow * a.ldx + (size_t)sh * a.K + sc16 * 8;
+  const int sdst = srow * AP + sh * 128 + sc16 * 8;
+  auto aload = [&](int kg) {
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (stager) {
+      const size_t xo = sxo + (size_t)min(kg, ngroups - 1) * 128;
+      if constexpr (XT == X_BF16) {
+        const h8 f = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
+        v = __builtin_bit_cast(u32x4, f);
+      } else {
+        v = *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(a.x) + xo);
+      }
+    }
+    return v;
+  };
+  auto astore = [&](int buf, const u32x4& v) {
+    if (stager) *reinterpret_cast<u32x4*>(&As[buf][sdst]) = v;
+  };
+  auto wload = [&](int kg, u32x4 (&w)[NB], uint16_t (&sr)[NB]) {
+    const int kc = min(kg, ngroups - 1);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          codes + q4t_code_offset(brow_c[b], kc, ngroups) + g * 16));
+      sr[b] = scales[q4t_scale_index(brow_c[b], kc, ngroups)];
+    }
+  };
+  f4 acc[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+  auto group = [&](int kg, const u32x4 (&w)[NB], const uint16_t (&sr)[NB]) {
+    const _Float16* ab = &As[kg & 1][j * AP + g * 32];
+    h8 af[NA][4];
+#pragma unroll
+    for (int h = 0; h < NA; ++h)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) af[h][s4] = *reinterpret_cast<const h8*>(ab + h * 128 + s4 * 8);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      f4 tt = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const h8 bq = q4_unpack(w[b][s4]);
+        tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[0][s4], bq, tt, 0, 0, 0);
+        if constexpr (NA == 2) tt = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[1][s4], bq, tt, 0, 0, 0);
+      }
+      const float scl = brow[b] >= 0 ? bf16_to_f32(sr[b]) : 0.f;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[b][r] = fmaf(tt[r], scl, acc[b][r]);
+    }
+  };
+  // prologue: group 0's activations in LDS, weight groups 0 (and 1 below) in flight
+  u32x4 w0[NB], w1[NB];
+  uint16_t s0[NB], s1[NB];
+  u32x4 av = aload(0);
+  wload(0, w0, s0);
+  astore(0, av);
+  // step kg: issue group kg+1's activations and weights, barrier (group kg's
+  // tile is in LDS), math of group kg, then group kg+1's tile into the other
+  // buffer (last read in step kg-1, before this step's barrier)
+  for (int kg = 0; kg < ngroups; kg += 2) {
+    av = aload(kg + 1);
+    wload(kg + 1, w1, s1);
+    __syncthreads();
+    group(kg, w0, s0);
+    astore((kg + 1) & 1, av);
+    if (kg + 1 >= ngroups) break;
+    av = aload(kg + 2);
+    wload(kg + 2, w0, s0);
+    __syncthreads();
+    group(kg + 1, w1, s1);
+    astore(kg & 1, av);
+  }
+  // epilogue (rows 4g + r, as q4_gemm_kernel)
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = m0 + 4 * g + r;
+    if (row >= mlim) continue;
+    if constexpr (is_swiglu(EPI)) {
+#pragma unroll
+      for (int b = 0; b < NB / 2; ++b) {
+        const int col = c0 / 2 + b * 16 + j;
+        if (col < a.ncols) {
+          const float hv = silu(acc[b][r]) * acc[b + NB / 2][r];
+          if constexpr (EPI == EPI_SWIGLU_F16X2) {
+            _Float16 hi, lo;
+            split_f16(hv, hi, lo);
+            static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = hi;
+            static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + a.ncols + col] = lo;
+          } else if constexpr (EPI == EPI_SWIGLU_F16)
+            static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = (_Float16)hv;
+          else
+            static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(hv);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int col = c0 + b * 16 + j;
+        if (col >= a.N) continue;
+        const size_t o = (size_t)row * a.ldy + col;
+        if constexpr (EPI == EPI_STORE_F32) static_cast<float*>(a.y)[o] = acc[b][r];
+        else static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(acc[b][r]);
+      }
+    }
+  }
+}
+
+template <int XT>
+int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
+  // 256 columns per workgroup: measured against 512 at config[4] decode
+  // (FFN-in 30 vs 32 us, down 17 vs 24 us: the narrower tile gives the down
+  // projection's 2048 columns enough workgroups)
+  constexpr int NB = 2;
+  const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
+  const dim3 grid((unsigned)ceil_div(logical_cols, 8 * 16 * NB), (unsigned)row_tiles);
+  switch (epi) {
+#define SM_GL(E) \
+    case E: q4_grouped_lds_kernel<NB, E, XT><<<grid, 512, 0, st>>>(a); break;
+    SM_GL(EPI_STORE_F32)
+    SM_GL(EPI_STORE_BF16)
+    SM_GL(EPI_SWIGLU_BF16)
+    SM_GL(EPI_SWIGLU_F16)
+    SM_GL(EPI_SWIGLU_F16X2)
+#undef SM_GL
+    default: set_error("sm_q4_grouped_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
 // M = 1 (one sequence's decode step; the LM head at batch 1). One wave owns a
 // 16-row block of W; KS = 1: four blocks per workgroup, each wave over all of
 // K; KS = 4: one block per workgroup, wave w over the K groups w, w + 4, ...,
@@ -628,6 +804,8 @@ extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales
     a.cstride = cstride;
     a.sstride = sstride;
     const int64_t rt = moe_max_tiles(routes, experts, 16);
+    if (xt == X_F16X2) return launch_grouped_lds<X_F16X2>(a, epilogue, st, rt);
+    if (xt == X_F16) return launch_grouped_lds<X_F16>(a, epilogue, st, rt);
     if (is_swiglu(epilogue) || K < 4 * 128) return launch_q4<2, 1>(a, epilogue, xt, st, rt);
     return launch_q4<2, 4>(a, epilogue, xt, st, rt);
   }
