@@ -87,6 +87,13 @@ struct Q4Args {
   const int32_t* goff = nullptr;
   const int32_t* rowidx = nullptr;
   size_t cstride = 0, sstride = 0;
+  // qkv projection + RoPE + KV-cache append (q4_grouped_lds_kernel EPI 6,
+  // dense mode): row = s*rope_L + i sits at position pos0[s] + i; columns are
+  // [q | k | v] heads of hd (as q4_gemm_bl.hip's EPI 6)
+  const float2* rope = nullptr;
+  const int32_t* pos0 = nullptr;
+  int rope_L = 0, cap = 0, H = 0, KVH = 0, hd = 0;
+  _Float16 *q_out = nullptr, *kc = nullptr, *vc = nullptr;
 };
 
 // One workgroup = 16 rows (M tile) x its column tile. NB: 16-column blocks per
@@ -271,18 +278,31 @@ __global__ __launch_bounds__(256) void q4_gemm_kernel(Q4Args a) {
 // each wave reads its A fragments from LDS; weight groups stay register-direct
 // and double-buffered. Per block and group the MFMA sequence and the scale
 // FMA are q4_gemm_kernel's, so the results are identical.
+// Dense mode (tiles == nullptr): row tile y = rows 16y .. 16y+15 of M. Measured
+// faster than the batch kernel for decode batches (M <= 256) with K <= 2048 and
+// 2k-8k output columns (config[2] qkv 27 -> 18 us, o 19 -> 16 us; config[1]
+// qkv 12 -> 10 us): its 64 x 64 tiles re-read every activation row once per
+// 64 columns, here once per 256. EPI 2 adds into y; EPI 6 is the qkv
+// projection with RoPE and the KV-cache append (q4_gemm_bl.hip's EPI 6).
 template <int NB, int EPI, int XT>
 __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
   constexpr int NA = (XT == X_F16X2) ? 2 : 1;
   constexpr int AP = NA * 128 + 8;      // LDS row (f16): hi | lo | pad
   constexpr int STG = 16 * NA * 16;     // 16-byte chunks per group tile
   __shared__ __attribute__((aligned(16))) _Float16 As[2][16 * AP];
-  if ((int)blockIdx.y >= a.ntiles[0]) return;  // uniform per workgroup
-  const int e = a.tiles[2 * blockIdx.y];
-  const int m0 = a.goff[e] + a.tiles[2 * blockIdx.y + 1];
-  const int mlim = a.goff[e + 1];
-  const uint8_t* codes = a.codes + (size_t)e * a.cstride;
-  const uint16_t* scales = a.scales + (size_t)e * a.sstride;
+  int m0, mlim = a.M;
+  const uint8_t* codes = a.codes;
+  const uint16_t* scales = a.scales;
+  if (a.tiles) {
+    if ((int)blockIdx.y >= a.ntiles[0]) return;  // uniform per workgroup
+    const int e = a.tiles[2 * blockIdx.y];
+    m0 = a.goff[e] + a.tiles[2 * blockIdx.y + 1];
+    mlim = a.goff[e + 1];
+    codes += (size_t)e * a.cstride;
+    scales += (size_t)e * a.sstride;
+  } else {
+    m0 = (int)blockIdx.y * 16;
+  }
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
   const int c0 = (int)blockIdx.x * 8 * 16 * NB + wave * 16 * NB;
@@ -335,6 +355,42 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
   f4 acc[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) acc[b] = f4{0.f, 0.f, 0.f, 0.f};
+  // EPI 2 / 6 operands that do not depend on the product, loaded before the
+  // main loop so their latency hides behind it: y for the residual add; the
+  // positions and (cos, sin) pairs for RoPE (even lanes own pairs (e, e+1))
+  float yv[NB][4];
+  int slot_b[NB], e_b[NB], srow_q[4], prow_q[4];
+  float2 csr[4][NB];
+  if constexpr (EPI == EPI_ADD_F32) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = min(m0 + 4 * g + r, mlim - 1), col = min(c0 + b * 16 + j, a.N - 1);
+        yv[b][r] = static_cast<const float*>(a.y)[(size_t)row * a.ldy + col];
+      }
+  }
+  if constexpr (EPI == 6) {
+    const int hd_shift = __builtin_ctz(a.hd);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int col = c0 + b * 16 + j;
+      slot_b[b] = col < a.N ? (col >> hd_shift) : -1;
+      e_b[b] = col & (a.hd - 1);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 4 * g + r;
+      const int rc = min(row, mlim - 1);
+      const int sq = (a.rope_L == 1) ? rc : rc / a.rope_L;
+      const int pos = a.pos0[sq] + (rc - sq * a.rope_L);
+      srow_q[r] = sq;
+      prow_q[r] = (row < mlim && pos >= 0 && pos < a.cap) ? pos : -1;
+      const float2* rrow = a.rope + (size_t)max(prow_q[r], 0) * (a.hd / 2);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) csr[r][b] = rrow[e_b[b] >> 1];
+    }
+  }
   auto group = [&](int kg, const u32x4 (&w)[NB], const uint16_t (&sr)[NB]) {
     const _Float16* ab = &As[kg & 1][j * AP + g * 32];
     h8 af[NA][4];
@@ -379,6 +435,41 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
     astore(kg & 1, av);
   }
   // epilogue (rows 4g + r, as q4_gemm_kernel)
+  if constexpr (EPI == 6) {
+    // RoPE pairs (2p, 2p+1) are adjacent columns, i.e. lanes j and j^1 of the
+    // same rows: swap partners before any lane-dependent branch
+    f4 partner[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) partner[b][r] = __shfl_xor(acc[b][r], 1, kWave);
+    if ((j & 1) != 0) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int pos = prow_q[r];
+      if (pos < 0) continue;
+      const int row = m0 + 4 * g + r, sq = srow_q[r];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int slot = slot_b[b], e = e_b[b];
+        if (slot < 0) continue;
+        const float va = acc[b][r], vb = partner[b][r];  // columns e, e+1
+        h2 out;
+        _Float16* dst;
+        if (slot >= a.H + a.KVH) {  // value: no rotation
+          out = h2{(_Float16)va, (_Float16)vb};
+          dst = a.vc + (((size_t)sq * a.KVH + (slot - a.H - a.KVH)) * a.cap + pos) * a.hd + e;
+        } else {
+          const float2 c = csr[r][b];
+          out = h2{(_Float16)(va * c.x - vb * c.y), (_Float16)(vb * c.x + va * c.y)};
+          dst = (slot < a.H) ? a.q_out + ((size_t)row * a.H + slot) * a.hd + e
+                             : a.kc + (((size_t)sq * a.KVH + (slot - a.H)) * a.cap + pos) * a.hd + e;
+        }
+        *reinterpret_cast<h2*>(dst) = out;
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = m0 + 4 * g + r;
@@ -407,10 +498,17 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
         if (col >= a.N) continue;
         const size_t o = (size_t)row * a.ldy + col;
         if constexpr (EPI == EPI_STORE_F32) static_cast<float*>(a.y)[o] = acc[b][r];
+        else if constexpr (EPI == EPI_ADD_F32) static_cast<float*>(a.y)[o] = yv[b][r] + acc[b][r];
         else static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(acc[b][r]);
       }
     }
   }
+}
+
+// Dense decode shapes that the LDS-shared kernel serves faster (measured).
+inline bool use_dense_lds(int64_t M, int64_t K, int64_t logical_cols, int xt) {
+  return (xt == X_F16X2 || xt == X_F16) && M > 32 && M <= 256 && K <= 2048 &&
+         logical_cols >= 2048 && logical_cols <= 8192;
 }
 
 template <int XT>
@@ -426,6 +524,8 @@ int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_til
     case E: q4_grouped_lds_kernel<NB, E, XT><<<grid, 512, 0, st>>>(a); break;
     SM_GL(EPI_STORE_F32)
     SM_GL(EPI_STORE_BF16)
+    SM_GL(EPI_ADD_F32)
+    SM_GL(6)
     SM_GL(EPI_SWIGLU_BF16)
     SM_GL(EPI_SWIGLU_F16)
     SM_GL(EPI_SWIGLU_F16X2)
@@ -615,6 +715,10 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
     }
     if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xt, st, rt);
     return launch_q4<2, 1>(a, epi, xt, st, rt);
+  }
+  if (!a.tiles && !a.rowidx && use_dense_lds(a.M, a.K, logical_cols, xt)) {
+    if (xt == X_F16X2) return launch_grouped_lds<X_F16X2>(a, epi, st, ceil_div(a.M, 16));
+    return launch_grouped_lds<X_F16>(a, epi, st, ceil_div(a.M, 16));
   }
   return q4_gemm_bl(a.codes, a.scales, a.N, a.K, a.x, xt, a.M, a.ldx, a.y, a.ldy, epi, a.ncols,
                     st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, ws, ws_bytes, nullptr);
@@ -837,6 +941,22 @@ extern "C" int sm_q4_qkv_rope(const uint8_t* codes, const uint16_t* scales, int6
              "sm_q4_qkv_rope: x rows must be 16-byte aligned, >= %lld elements", (long long)xw);
   const int64_t N = (H + 2 * KVH) * head_dim;
   if (S == 0) return SM_OK;
+  if (use_dense_lds(S * L, K, N, xt)) {
+    Q4Args a{codes, scales, x, nullptr, (int)(S * L), (int)N, (int)K, (int)ldx, 0, (int)N};
+    a.rope = reinterpret_cast<const float2*>(rope_table);
+    a.pos0 = pos0;
+    a.rope_L = (int)L;
+    a.cap = (int)cap;
+    a.H = (int)H;
+    a.KVH = (int)KVH;
+    a.hd = (int)head_dim;
+    a.q_out = static_cast<_Float16*>(q_out);
+    a.kc = static_cast<_Float16*>(kcache);
+    a.vc = static_cast<_Float16*>(vcache);
+    const int64_t rt = ceil_div(S * L, 16);
+    if (xt == X_F16X2) return launch_grouped_lds<X_F16X2>(a, 6, as_stream(stream), rt);
+    return launch_grouped_lds<X_F16>(a, 6, as_stream(stream), rt);
+  }
   QkvRope qr{rope_table, pos0, (int)L, (int)cap, (int)H, (int)KVH, (int)head_dim,
              q_out, kcache, vcache};
   return q4_gemm_bl(codes, scales, (int)N, (int)K, x, xt, (int)(S * L), (int)ldx, nullptr, 0, 6,

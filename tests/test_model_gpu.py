@@ -97,10 +97,12 @@ def test_logprob_chunking_is_exact(dev):
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("geom", ["cfg1", "cfg2", "batch"])
+@pytest.mark.parametrize("geom", ["cfg1", "cfg2", "batch", "batch_cfg1"])
 def test_quantized_rollout_and_logprobs(dev, geom):
     """cfg1 / cfg2 geometry at small batch; "batch" decodes 128 sequences at
-    once, so every decode matmul runs the batch kernel (with split-K)."""
+    once, so every decode matmul runs the batch kernel (with split-K);
+    "batch_cfg1" decodes 128 sequences of config[1]'s layer shapes, whose qkv
+    (with RoPE) and SwiGLU projections run the LDS-staged decode kernel."""
     print(f"case quantized {geom}", flush=True)
     if geom == "cfg1":
         mc = ModelConfig(layers=2, d_model=768, heads=12, kv_heads=12, head_dim=64, ffn=3072,
@@ -108,6 +110,10 @@ def test_quantized_rollout_and_logprobs(dev, geom):
         S, P, N = 8, 16, 8
     elif geom == "batch":
         mc = ModelConfig(layers=2, d_model=768, heads=12, kv_heads=4, head_dim=64, ffn=3072,
+                         vocab=4096, max_seq=64, quantized=True)
+        S, P, N = 128, 8, 4
+    elif geom == "batch_cfg1":
+        mc = ModelConfig(layers=2, d_model=768, heads=12, kv_heads=12, head_dim=64, ffn=3072,
                          vocab=4096, max_seq=64, quantized=True)
         S, P, N = 128, 8, 4
     else:

@@ -199,7 +199,7 @@ def test_pair_rejects_short_rows(dev):
                   torch.cuda.current_stream().cuda_stream)
 
 
-@pytest.mark.parametrize("m,n,k,epi", [(256, 2048, 2048, "add"), (256, 2048, 5632, "add"),
+@pytest.mark.parametrize("m,n,k,epi", [(256, 1024, 2048, "add"), (256, 2048, 5632, "add"),
                                        (200, 1024, 2048, "swiglu"), (256, 1024, 4096, "store")])
 def test_split_k_workspace(dev, m, n, k, epi):
     """sm_q4_matmul_ws: with a workspace, batch calls that would underfill the
@@ -290,8 +290,10 @@ WIDE_EPI = [("store", _lib.SM_EPI_STORE_F32), ("bf16", _lib.SM_EPI_STORE_BF16),
 def test_wide_kernel_equals_tile_kernel(dev, m, n, k, pair, epi):
     """Large dense problems (>= 128 workgroups of 256 x 256) run the wide-tile
     kernel; its accumulation order is the 128 x 128 kernel's, which row chunks
-    of <= 256 rows (16 workgroups) still run: results agree bit for bit, for
-    every epilogue, f16 and f16-pair inputs, and ragged M / N edges."""
+    of 512 rows (32 workgroups of 256 x 256, too few for the wide kernel; above
+    the decode sizes that take the LDS-staged kernel) still run: results agree
+    bit for bit, for every epilogue, f16 and f16-pair inputs, and ragged M / N
+    edges."""
     print(f"case wide m={m} n={n} k={k} pair={pair} epi={epi}", flush=True)
     e = dict(WIDE_EPI)[epi]
     w = torch.empty(n, k, device=dev)
@@ -304,18 +306,18 @@ def test_wide_kernel_equals_tile_kernel(dev, m, n, k, pair, epi):
         big = base.clone()
         ops.q4_matmul(qw, xd, out=big, epilogue=e, pair=pair)
         ref = base.clone()
-        for r0 in range(0, m, 256):
-            ops.q4_matmul(qw, xd[r0:r0 + 256], out=ref[r0:r0 + 256], epilogue=e, pair=pair)
+        for r0 in range(0, m, 512):
+            ops.q4_matmul(qw, xd[r0:r0 + 512], out=ref[r0:r0 + 512], epilogue=e, pair=pair)
     else:
         big = ops.q4_matmul(qw, xd, epilogue=e, pair=pair)
-        ref = torch.cat([ops.q4_matmul(qw, xd[r0:r0 + 256], epilogue=e, pair=pair)
-                         for r0 in range(0, m, 256)])
+        ref = torch.cat([ops.q4_matmul(qw, xd[r0:r0 + 512], epilogue=e, pair=pair)
+                         for r0 in range(0, m, 512)])
     assert big.shape == ref.shape
     assert torch.equal(big.view(torch.int16) if big.dtype != torch.float32 else big,
                        ref.view(torch.int16) if ref.dtype != torch.float32 else ref)
 
 
-@pytest.mark.parametrize("S,L,H,KVH", [(8, 256, 32, 16), (10, 300, 32, 8)])
+@pytest.mark.parametrize("S,L,H,KVH", [(8, 320, 32, 16), (10, 300, 32, 8)])
 def test_wide_kernel_qkv_rope_equals_tile_kernel(dev, S, L, H, KVH):
     """sm_q4_qkv_rope over a prefill-sized batch (the wide kernel) writes the
     same q / K / V cache bits as one sequence at a time (the 128 x 128 kernel)."""
@@ -348,3 +350,92 @@ def test_wide_kernel_qkv_rope_equals_tile_kernel(dev, S, L, H, KVH):
         outs.append((q, kc, vc))
     for a, b in zip(*outs):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
+@pytest.mark.parametrize("m,n,k", [(128, 2304, 768), (256, 2048, 2048), (256, 3072, 2048),
+                                   (200, 6144, 768), (33, 4096, 1024), (64, 8192, 256)])
+@pytest.mark.parametrize("pair", [True, False])
+def test_dense_decode_lds_kernel(dev, m, n, k, pair):
+    """Decode-batch shapes (32 < M <= 256, K <= 2048, 2k-8k columns) run the
+    kernel that stages each 16-row activation tile once per workgroup in LDS
+    (dense mode of the grouped decode kernel): store, bf16, residual add and
+    SwiGLU epilogues against float64 on the decoded weights."""
+    print(f"case dense-lds m={m} n={n} k={k} pair={pair}", flush=True)
+    w = _weights(n, k, m + n)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(m + 2).normal(0, 1, (m, k)).astype(np.float32)
+    if pair:
+        xp, xr = _pair_host(x)
+        xd = torch.from_numpy(xp).to(dev)
+    else:
+        xd = torch.from_numpy(x).to(dev).to(torch.float16)
+        xr = xd.float().cpu().numpy()
+    dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+    y_ref = xr.astype(np.float64) @ dense.T
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    y = ops.q4_matmul(qw, xd, pair=pair).cpu().numpy()
+    assert np.all(np.abs(y - y_ref) <= tol), float(np.abs(y - y_ref).max())
+    yb = ops.q4_matmul(qw, xd, pair=pair, epilogue=_lib.SM_EPI_STORE_BF16)
+    assert torch.equal(yb.float().cpu(), torch.from_numpy(y).to(torch.bfloat16).float())
+    base = np.random.default_rng(4).normal(0, 1, (m, n)).astype(np.float32)
+    acc = torch.from_numpy(base.copy()).to(dev)
+    ops.q4_matmul(qw, xd, out=acc, pair=pair, epilogue=_lib.SM_EPI_ADD_F32)
+    np.testing.assert_array_equal(acc.cpu().numpy(), base + y)
+    F = n // 2
+    h = ops.q4_matmul(qw, xd, pair=pair,
+                      epilogue=_lib.SM_EPI_SWIGLU_F16X2 if pair else _lib.SM_EPI_SWIGLU_F16)
+    h = (ops.unpair(h) if pair else h.float()).cpu().numpy()
+    g, v = y_ref[:, :F], y_ref[:, F:]
+    ref_h = g / (1 + np.exp(-g)) * v
+    hb = (np.abs(g) + 1) * (tol[:, F:] + tol[:, :F]) * (np.abs(v) + 1)
+    rel = 1e-6 if pair else 2.0 ** -11
+    assert np.all(np.abs(h - ref_h) <= hb + rel * np.abs(ref_h) + 1e-7)
+
+
+@pytest.mark.parametrize("S,H,KVH,hd,K", [(128, 12, 12, 64, 768), (256, 16, 4, 128, 2048),
+                                          (40, 16, 16, 128, 2048)])
+def test_dense_decode_lds_qkv_rope(dev, S, H, KVH, hd, K):
+    """sm_q4_qkv_rope at decode size (one new token per sequence, the LDS
+    kernel's RoPE epilogue): q and the appended K/V rows against the f32
+    matmul of the same weights with RoPE applied on the host; every other
+    cache slot stays untouched."""
+    from summa_amd._lib import SM_F16, SM_F16X2, call
+    print(f"case dense-lds qkv-rope S={S} H={H} KVH={KVH} hd={hd} K={K}", flush=True)
+    N = (H + 2 * KVH) * hd
+    w = torch.empty(N, K, device=dev)
+    ops.fill_normal(w, 0.0, 0.05, seed=N + K)
+    qw = ops.Q4Weight.quantize(w)
+    xp = ops.f16_pair(torch.randn(S, K, device=dev))
+    cap = 64
+    pos0 = torch.from_numpy(np.random.default_rng(S).integers(0, cap, S).astype(np.int32)).to(dev)
+    half = hd // 2
+    inv = 1.0 / (10000.0 ** (np.arange(half) * 2.0 / hd))
+    ang = np.arange(cap)[:, None] * inv[None, :]
+    tab = torch.from_numpy(np.stack([np.cos(ang), np.sin(ang)], -1).astype(np.float32)).to(dev)
+    q = torch.zeros(S, H, hd, dtype=torch.float16, device=dev)
+    kc = torch.full((S, KVH, cap, hd), 7.0, dtype=torch.float16, device=dev)
+    vc = torch.full((S, KVH, cap, hd), 7.0, dtype=torch.float16, device=dev)
+    call("sm_q4_qkv_rope", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), H, KVH, hd, K,
+         xp.data_ptr(), SM_F16X2, S, 1, xp.stride(0), tab.data_ptr(), pos0.data_ptr(), cap,
+         q.data_ptr(), kc.data_ptr(), vc.data_ptr(), SM_F16, torch.cuda.current_stream().cuda_stream)
+    y = ops.q4_matmul(qw, xp, pair=True).cpu().numpy().astype(np.float64).reshape(S, H + 2 * KVH, hd)
+    p = pos0.cpu().numpy()
+    c, s_ = np.cos(ang[p])[:, None, :], np.sin(ang[p])[:, None, :]
+    def rope(t):
+        a, b = t[..., 0::2], t[..., 1::2]
+        out = np.empty_like(t)
+        out[..., 0::2], out[..., 1::2] = a * c - b * s_, b * c + a * s_
+        return out
+    q_ref, k_ref, v_ref = rope(y[:, :H]), rope(y[:, H:H + KVH]), y[:, H + KVH:]
+    tol = lambda r: 2.0 ** -10 * np.abs(r) + 1e-4
+    qn = q.float().cpu().numpy()
+    assert np.all(np.abs(qn - q_ref) <= tol(q_ref)), float(np.abs(qn - q_ref).max())
+    kn, vn = kc.float().cpu().numpy(), vc.float().cpu().numpy()
+    rows = np.arange(S)
+    kg, vg = kn[rows, :, p], vn[rows, :, p]
+    assert np.all(np.abs(kg - k_ref) <= tol(k_ref)), float(np.abs(kg - k_ref).max())
+    assert np.all(np.abs(vg - v_ref) <= tol(v_ref)), float(np.abs(vg - v_ref).max())
+    mask = np.ones((S, cap), bool)
+    mask[rows, p] = False
+    assert np.all(kn.transpose(0, 2, 1, 3)[mask] == 7.0) and np.all(vn.transpose(0, 2, 1, 3)[mask] == 7.0)
