@@ -94,6 +94,11 @@ struct Q4Args {
   const int32_t* pos0 = nullptr;
   int rope_L = 0, cap = 0, H = 0, KVH = 0, hd = 0;
   _Float16 *q_out = nullptr, *kc = nullptr, *vc = nullptr;
+  // split-K (q4_grouped_lds_kernel dense mode): blockIdx.z = split z covers K
+  // groups [z*gper, min(K/128, (z+1)*gper)) and writes its f32 partial tile to
+  // part[z][row][logical column]; splitk_reduce sums the splits in order
+  float* part = nullptr;
+  int gper = 0;
 };
 
 // One workgroup = 16 rows (M tile) x its column tile. NB: 16-column blocks per
@@ -307,6 +312,8 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
   const int j = lane % 16, g = lane / 16;
   const int c0 = (int)blockIdx.x * 8 * 16 * NB + wave * 16 * NB;
   const int ngroups = a.K / 128;
+  const int g0 = a.part ? (int)blockIdx.z * a.gper : 0;  // host: g0 < g1
+  const int g1 = a.part ? min(ngroups, g0 + a.gper) : ngroups;
   int brow[NB], brow_c[NB];
 #pragma unroll
   for (int b = 0; b < NB; ++b) {
@@ -330,7 +337,7 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
   auto aload = [&](int kg) {
     u32x4 v = u32x4{0u, 0u, 0u, 0u};
     if (stager) {
-      const size_t xo = sxo + (size_t)min(kg, ngroups - 1) * 128;
+      const size_t xo = sxo + (size_t)min(kg, g1 - 1) * 128;
       if constexpr (XT == X_BF16) {
         const h8 f = act_frag(*reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + xo));
         v = __builtin_bit_cast(u32x4, f);
@@ -344,7 +351,7 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
     if (stager) *reinterpret_cast<u32x4*>(&As[buf][sdst]) = v;
   };
   auto wload = [&](int kg, u32x4 (&w)[NB], uint16_t (&sr)[NB]) {
-    const int kc = min(kg, ngroups - 1);
+    const int kc = min(kg, g1 - 1);
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
@@ -392,7 +399,7 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
     }
   }
   auto group = [&](int kg, const u32x4 (&w)[NB], const uint16_t (&sr)[NB]) {
-    const _Float16* ab = &As[kg & 1][j * AP + g * 32];
+    const _Float16* ab = &As[(kg - g0) & 1][j * AP + g * 32];
     h8 af[NA][4];
 #pragma unroll
     for (int h = 0; h < NA; ++h)
@@ -415,24 +422,48 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
   // prologue: group 0's activations in LDS, weight groups 0 (and 1 below) in flight
   u32x4 w0[NB], w1[NB];
   uint16_t s0[NB], s1[NB];
-  u32x4 av = aload(0);
-  wload(0, w0, s0);
+  u32x4 av = aload(g0);
+  wload(g0, w0, s0);
   astore(0, av);
   // step kg: issue group kg+1's activations and weights, barrier (group kg's
   // tile is in LDS), math of group kg, then group kg+1's tile into the other
-  // buffer (last read in step kg-1, before this step's barrier)
-  for (int kg = 0; kg < ngroups; kg += 2) {
+  // buffer (last read in step kg-1, before this step's barrier); buffers by
+  // kg - g0
+  for (int kg = g0; kg < g1; kg += 2) {
     av = aload(kg + 1);
     wload(kg + 1, w1, s1);
     __syncthreads();
     group(kg, w0, s0);
-    astore((kg + 1) & 1, av);
-    if (kg + 1 >= ngroups) break;
+    astore((kg + 1 - g0) & 1, av);
+    if (kg + 1 >= g1) break;
     av = aload(kg + 2);
     wload(kg + 2, w0, s0);
     __syncthreads();
     group(kg + 1, w1, s1);
-    astore(kg & 1, av);
+    astore((kg - g0) & 1, av);
+  }
+  if (a.part) {  // split-K partial tile, logical columns (uniform branch)
+    const int lc_total = is_swiglu(EPI) ? 2 * a.ncols : a.N;
+    float* pp = a.part + (size_t)blockIdx.z * a.M * lc_total;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + 4 * g + r;
+      if (row >= mlim) continue;
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        int lc;
+        if constexpr (is_swiglu(EPI)) {
+          const int hcol = c0 / 2 + (b % (NB / 2)) * 16 + j;
+          if (hcol >= a.ncols) continue;
+          lc = (b < NB / 2) ? hcol : a.ncols + hcol;
+        } else {
+          lc = c0 + b * 16 + j;
+          if (lc >= a.N) continue;
+        }
+        pp[(size_t)row * lc_total + lc] = acc[b][r];
+      }
+    }
+    return;
   }
   // epilogue (rows 4g + r, as q4_gemm_kernel)
   if constexpr (EPI == 6) {
@@ -511,14 +542,21 @@ inline bool use_dense_lds(int64_t M, int64_t K, int64_t logical_cols, int xt) {
          logical_cols >= 2048 && logical_cols <= 8192;
 }
 
+// Decode shapes outside that window (long K, or narrow N) with a split-K
+// workspace: the same kernel over K ranges, partials reduced in order.
+inline bool use_dense_lds_split(int64_t M, int64_t K, int64_t logical_cols, int xt) {
+  return (xt == X_F16X2 || xt == X_F16) && M > 32 && M <= 256 && K >= 6 * 128 &&
+         (K > 2048 || logical_cols < 2048) && logical_cols <= 8192;
+}
+
 template <int XT>
-int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles) {
+int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1) {
   // 256 columns per workgroup: measured against 512 at config[4] decode
   // (FFN-in 30 vs 32 us, down 17 vs 24 us: the narrower tile gives the down
   // projection's 2048 columns enough workgroups)
   constexpr int NB = 2;
   const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
-  const dim3 grid((unsigned)ceil_div(logical_cols, 8 * 16 * NB), (unsigned)row_tiles);
+  const dim3 grid((unsigned)ceil_div(logical_cols, 8 * 16 * NB), (unsigned)row_tiles, (unsigned)ks);
   switch (epi) {
 #define SM_GL(E) \
     case E: q4_grouped_lds_kernel<NB, E, XT><<<grid, 512, 0, st>>>(a); break;
@@ -533,6 +571,7 @@ int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_til
     default: set_error("sm_q4_grouped_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
   }
   SM_LAUNCH_CHECK();
+  if (ks > 1) return splitk_reduce(a.part, ks, a.M, a.N, a.ncols, a.y, a.ldy, epi, st);
   return SM_OK;
 }
 
@@ -719,6 +758,22 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
   if (!a.tiles && !a.rowidx && use_dense_lds(a.M, a.K, logical_cols, xt)) {
     if (xt == X_F16X2) return launch_grouped_lds<X_F16X2>(a, epi, st, ceil_div(a.M, 16));
     return launch_grouped_lds<X_F16>(a, epi, st, ceil_div(a.M, 16));
+  }
+  if (!a.tiles && !a.rowidx && ws && use_dense_lds_split(a.M, a.K, logical_cols, xt)) {
+    // K split over workgroups: >= 3 groups per split, up to ~512 workgroups
+    const int64_t rt = ceil_div(a.M, 16), base = ceil_div(logical_cols, 256) * rt;
+    const int ng = a.K / 128;
+    int ks = (int)std::min<int64_t>(ng / 3, std::max<int64_t>(1, 512 / base));
+    const int64_t lc_total = logical_cols;
+    while (ks > 1 && (int64_t)ks * a.M * lc_total * 4 > ws_bytes) --ks;
+    if (ks > 1) {
+      Q4Args b = a;
+      b.gper = (int)ceil_div(ng, ks);
+      ks = (int)ceil_div(ng, b.gper);  // every split non-empty
+      b.part = static_cast<float*>(ws);
+      if (xt == X_F16X2) return launch_grouped_lds<X_F16X2>(b, epi, st, rt, ks);
+      return launch_grouped_lds<X_F16>(b, epi, st, rt, ks);
+    }
   }
   return q4_gemm_bl(a.codes, a.scales, a.N, a.K, a.x, xt, a.M, a.ldx, a.y, a.ldy, epi, a.ncols,
                     st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, ws, ws_bytes, nullptr);

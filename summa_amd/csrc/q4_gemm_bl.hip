@@ -532,12 +532,18 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
   else s = (tn == 128) ? launch_bl_x<32, 128>(a, epi, xt, grid, st)
                        : launch_bl_x<32, 64>(a, epi, xt, grid, st);
   if (s != SM_OK || ks == 1) return s;
+  return splitk_reduce(a.part, ks, M, N, ncols, y, ldy, epi, st);
+}
+
+int splitk_reduce(const float* part, int ks, int M, int N, int ncols, void* y, int ldy, int epi,
+                  hipStream_t st) {
+  const bool swiglu = epi >= 3 && epi <= 5;
   const int64_t width = swiglu ? ncols : N;
   const unsigned rb = (unsigned)ceil_div((int64_t)M * width, 256);
   switch (epi) {
 #define SM_RED(E)                                                                       \
     case E:                                                                             \
-      splitk_reduce_kernel<E><<<rb, 256, 0, st>>>(a.part, ks, M, N, ncols, y, ldy);      \
+      splitk_reduce_kernel<E><<<rb, 256, 0, st>>>(part, ks, M, N, ncols, y, ldy);        \
       break;
     SM_RED(0)
     SM_RED(1)
@@ -546,6 +552,7 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
     SM_RED(4)
     SM_RED(5)
 #undef SM_RED
+    default: set_error("sm_q4_matmul: split-K reduction of epilogue %d", epi); return SM_ERR_INVALID;
   }
   SM_LAUNCH_CHECK();
   return SM_OK;

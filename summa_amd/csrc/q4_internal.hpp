@@ -26,6 +26,11 @@ int q4_gemm_bl(const uint8_t* codes, const uint16_t* scales, int N, int K, const
                void* ws, int64_t ws_bytes, const QkvRope* qr);
 int64_t bl_counter_bytes();
 
+// Sums split-K partials part[ks][M][cols] (cols = N, or 2*ncols gate | value
+// for SwiGLU) in split order and applies epilogue epi (0..5) into y.
+int splitk_reduce(const float* part, int ks, int M, int N, int ncols, void* y, int ldy, int epi,
+                  hipStream_t st);
+
 // Dense large-M Q4 matmul with 256 x 256 tiles (q4_gemm_wide.hip): f16 (xt 1)
 // or f16-pair (xt 2) activations, epilogues 0..6; the same results as
 // q4_gemm_bl. q4_wide_tiles: its workgroup count for a shape.

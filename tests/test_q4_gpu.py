@@ -201,16 +201,24 @@ def test_pair_rejects_short_rows(dev):
 
 @pytest.mark.parametrize("m,n,k,epi", [(256, 1024, 2048, "add"), (256, 2048, 5632, "add"),
                                        (200, 1024, 2048, "swiglu"), (256, 1024, 4096, "store")])
-def test_split_k_workspace(dev, m, n, k, epi):
+@pytest.mark.parametrize("xdt", ["pair", "bf16"])
+def test_split_k_workspace(dev, m, n, k, epi, xdt):
     """sm_q4_matmul_ws: with a workspace, batch calls that would underfill the
-    GPU split K and reduce fp32 partials in a fixed order (run-to-run exact)."""
-    print(f"case split-k m={m} n={n} k={k} {epi}", flush=True)
+    GPU split K and reduce fp32 partials in a fixed order (run-to-run exact).
+    f16 pairs run the LDS-staged decode kernel over K ranges, bf16 the batch
+    kernel's split."""
+    print(f"case split-k m={m} n={n} k={k} {epi} {xdt}", flush=True)
     w = _weights(n, k, m + n + 3)
     codes, scales = oracle.q4_quantize(w)
     qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
     x = np.random.default_rng(m + 5).normal(0, 1, (m, k)).astype(np.float32)
-    xp, xr = _pair_host(x)
-    xd = torch.from_numpy(xp).to(dev)
+    pair = xdt == "pair"
+    if pair:
+        xp, xr = _pair_host(x)
+        xd = torch.from_numpy(xp).to(dev)
+    else:
+        xd = torch.from_numpy(x).to(dev).to(torch.bfloat16)
+        xr = xd.float().cpu().numpy()
     dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
     y_ref = xr.astype(np.float64) @ dense.T
     tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
@@ -219,7 +227,7 @@ def test_split_k_workspace(dev, m, n, k, epi):
     ws = ops.q4_workspace(m, n, k, e, dev)
     ws.zero_()
     if epi == "swiglu":
-        outs = [ops.unpair(ops.q4_matmul(qw, xd, epilogue=e, pair=True, workspace=ws))
+        outs = [ops.unpair(ops.q4_matmul(qw, xd, epilogue=e, pair=pair, workspace=ws))
                 for _ in range(2)]
         torch.testing.assert_close(outs[0], outs[1], rtol=0, atol=0)
         F = n // 2
@@ -231,16 +239,16 @@ def test_split_k_workspace(dev, m, n, k, epi):
     outs = []
     for _ in range(2):
         acc = torch.from_numpy(base.copy()).to(dev)
-        ops.q4_matmul(qw, xd, out=acc, epilogue=e, pair=True, workspace=ws)
+        ops.q4_matmul(qw, xd, out=acc, epilogue=e, pair=pair, workspace=ws)
         outs.append(acc.cpu().numpy())
     np.testing.assert_array_equal(outs[0], outs[1])
     # a call of another shape on the same workspace leaves nothing behind that
     # changes the next result
     other = torch.zeros((m, 128), device=dev)
     w2 = ops.Q4Weight.from_host(*oracle.q4_quantize(_weights(128, k, 1)), 128, k, dev)
-    ops.q4_matmul(w2, xd, out=other, pair=True, workspace=ws)
+    ops.q4_matmul(w2, xd, out=other, pair=pair, workspace=ws)
     acc = torch.from_numpy(base.copy()).to(dev)
-    ops.q4_matmul(qw, xd, out=acc, epilogue=e, pair=True, workspace=ws)
+    ops.q4_matmul(qw, xd, out=acc, epilogue=e, pair=pair, workspace=ws)
     np.testing.assert_array_equal(acc.cpu().numpy(), outs[0])
     assert int(ws.int().abs().sum().item()) != 0  # the split really ran
     expect = (base + y_ref) if epi == "add" else y_ref
