@@ -209,16 +209,27 @@ __device__ inline void split_f16(float x, _Float16& hi, _Float16& lo) {
 
 // One prepared word -> its 8 codes q in natural k order as f16. Each 16-bit
 // half becomes 1024 + u (or 1024 + 16u) by OR-ing the nibble into the
-// mantissa of 0x6400; one packed add / fma removes the bias. 9 VALU ops.
+// mantissa of 0x6400; one packed add / fma removes the bias. 9 VALU ops: each
+// mask-and-OR is one v_and_or_b32, which (VOP3 on this architecture) takes no
+// literal and at most one scalar operand, so the 0x6400 magic is handed over in
+// a vector register (an empty-effect v_mov the compiler hoists and shares);
+// with both constants as literals it emitted a separate v_and and v_or (13.5
+// VALU per word).
+__device__ inline uint32_t q4_magic() {
+  uint32_t m;
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(m));
+  return m;
+}
 __device__ inline h8 q4_unpack(uint32_t w) {
+  const uint32_t magic = q4_magic();
   const uint32_t w2 = w >> 8;
   const h2 k1032 = {(_Float16)-1032.f, (_Float16)-1032.f};
   const h2 k72 = {(_Float16)-72.f, (_Float16)-72.f};
   const h2 k16 = {(_Float16)0.0625f, (_Float16)0.0625f};
-  const h2 a = as_h2((w & 0x000F000Fu) | 0x64006400u) + k1032;       // k0, k1
-  const h2 b = as_h2((w & 0x00F000F0u) | 0x64006400u) * k16 + k72;   // k2, k3
-  const h2 c = as_h2((w2 & 0x000F000Fu) | 0x64006400u) + k1032;      // k4, k5
-  const h2 d = as_h2((w2 & 0x00F000F0u) | 0x64006400u) * k16 + k72;  // k6, k7
+  const h2 a = as_h2((w & 0x000F000Fu) | magic) + k1032;       // k0, k1
+  const h2 b = as_h2((w & 0x00F000F0u) | magic) * k16 + k72;   // k2, k3
+  const h2 c = as_h2((w2 & 0x000F000Fu) | magic) + k1032;      // k4, k5
+  const h2 d = as_h2((w2 & 0x00F000F0u) | magic) * k16 + k72;  // k6, k7
   return h8{a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
 }
 
