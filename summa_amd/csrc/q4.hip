@@ -651,13 +651,17 @@ __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
 }
 
 // The K-split variant runs where the tile kernel's narrow GEMV splits K (fewer
-// than 512 of its 64-column workgroups): the four-block variant would leave
-// most CUs idle there, and the same choice keeps the two kernels' bits equal.
+// than 512 of its 64-column workgroups; the same choice keeps the two kernels'
+// bits equal) and for rows of 2048 or more: measured on the config[2] LM head
+// (N = 65536, K = 2048), four waves per 16-row block over a quarter of K each
+// take 13.6 us per launch against 14.2 us for one wave over all of K (N = 32768,
+// K = 2048: 9.1 against 9.9 us; at K = 1024 the split gains nothing). The
+// tile kernel keeps 512 there: split, its M = 2..16 calls run 1.2-1.6x slower.
 template <int NA, int EPI>
 int launch_gemv1(const Q4Args& a, hipStream_t st) {
   const int64_t nrb = ceil_div(a.N, 16);
   const size_t lds = (size_t)NA * a.K * 2;
-  if (ceil_div(a.N, 64) < 512 && a.K >= 4 * 128)
+  if ((ceil_div(a.N, 64) < 512 || a.K >= 2048) && a.K >= 4 * 128)
     q4_gemv1_kernel<NA, EPI, 4><<<(unsigned)nrb, 256, lds, st>>>(a);
   else
     q4_gemv1_kernel<NA, EPI, 1><<<(unsigned)ceil_div(nrb, 4), 256, lds, st>>>(a);

@@ -259,9 +259,12 @@ def test_split_k_workspace(dev, m, n, k, epi, xdt):
                                       (1000, 640, True), (300, 256, False), (65536, 2048, False)])
 def test_gemv_m1_equals_tile_kernel(dev, n, k, pair):
     """M = 1 runs the single-row GEMV (activation row in LDS, double-buffered
-    weight groups; K split across waves for small N). Its arithmetic and
-    summation order are the 16-row tile kernel's, so row 0 of an M = 2 call
-    matches bit for bit; the store-bf16 and add epilogues follow the same value."""
+    weight groups; K split across waves for small N and for K >= 2048). Where
+    the 16-row tile kernel splits K the same way (fewer than 512 of its
+    64-column workgroups) the arithmetic and summation order are the same, so
+    row 0 of an M = 2 call matches bit for bit; otherwise (the 65536 x 2048 LM
+    head) only the order of the four K-quarter partial sums differs. The
+    store-bf16 and add epilogues follow the same value."""
     print(f"case gemv1 n={n} k={k} pair={pair}", flush=True)
     w = torch.empty(n, k, device=dev)
     ops.fill_normal(w, 0.0, 0.02, seed=n + k)
@@ -270,7 +273,14 @@ def test_gemv_m1_equals_tile_kernel(dev, n, k, pair):
     xd = ops.f16_pair(x) if pair else x.to(torch.float16)
     y1 = ops.q4_matmul(qw, xd[:1], pair=pair)
     y2 = ops.q4_matmul(qw, xd, pair=pair)
-    assert torch.equal(y1[0], y2[0])
+    tile_split = (n + 63) // 64 < 512
+    if tile_split or k < 2048:
+        assert torch.equal(y1[0], y2[0])
+    else:
+        # |x| ~ 0.8, |w| ~ 0.016: the sum of |x_k w_k| is ~0.013 k, and
+        # reordering four f32 partial sums moves the result by a few ulps of it
+        bound = 1e-6 * 0.013 * k
+        assert float((y1[0] - y2[0]).abs().max()) <= bound
     yb = ops.q4_matmul(qw, xd[:1], pair=pair, epilogue=_lib.SM_EPI_STORE_BF16)
     assert torch.equal(yb.float(), y1.to(torch.bfloat16).float())
     base = torch.randn(1, n, device=dev)
