@@ -587,7 +587,7 @@ int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_til
 // next group's weights too. The arithmetic per group is that of
 // q4_gemm_kernel (codes x activations over 4 k-steps, then one FMA with the
 // group scale), so the two kernels give the same bits.
-template <int NA, int EPI, int KS>
+template <int NA, int EPI, int KS, int ALL = 0>
 __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
   extern __shared__ _Float16 xs[];  // NA * K activations (hi, then lo)
   __shared__ float red[KS][4][16];
@@ -606,9 +606,14 @@ __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
     w = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(cb + (size_t)kc * 1024));
     sc = sb[kc * 16];
   };
-  u32x4 w0, w1;
-  uint16_t s0, s1;
-  load(part, w0, s0);
+  u32x4 w0, w1, wa[ALL > 0 ? ALL : 1];
+  uint16_t s0, s1, sa[ALL > 0 ? ALL : 1];
+  if constexpr (ALL > 0) {
+#pragma unroll
+    for (int i = 0; i < ALL; ++i) load(part + i * KS, wa[i], sa[i]);
+  } else {
+    load(part, w0, s0);
+  }
   const _Float16* x = static_cast<const _Float16*>(a.x);
   for (int i = threadIdx.x * 8; i < NA * a.K; i += 256 * 8)
     *reinterpret_cast<h8*>(xs + i) = *reinterpret_cast<const h8*>(x + i);
@@ -628,12 +633,17 @@ __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
     }
     acc = fmaf(t[0], bf16_to_f32(sc), acc);
   };
-  for (int kb = part; kb < ng; kb += 2 * KS) {
-    load(kb + KS, w1, s1);
-    group(kb, w0, s0);
-    if (kb + KS >= ng) break;
-    load(kb + 2 * KS, w0, s0);
-    group(kb + KS, w1, s1);
+  if constexpr (ALL > 0) {
+#pragma unroll
+    for (int i = 0; i < ALL; ++i) group(part + i * KS, wa[i], sa[i]);
+  } else {
+    for (int kb = part; kb < ng; kb += 2 * KS) {
+      load(kb + KS, w1, s1);
+      group(kb, w0, s0);
+      if (kb + KS >= ng) break;
+      load(kb + 2 * KS, w0, s0);
+      group(kb + KS, w1, s1);
+    }
   }
   if constexpr (KS > 1) {
     if (g == 0) red[part][blk][j] = acc;
@@ -657,11 +667,23 @@ __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
 // take 13.6 us per launch against 14.2 us for one wave over all of K (N = 32768,
 // K = 2048: 9.1 against 9.9 us; at K = 1024 the split gains nothing). The
 // tile kernel keeps 512 there: split, its M = 2..16 calls run 1.2-1.6x slower.
+// Where each wave owns 4, 8 or 11 groups (K = 2048, 4096, 5632) it requests
+// them all before staging the activation row (ALL): 13.0 us on the LM head,
+// 6.5 -> 4.6 us at 2048 x 5632, 5.6 -> 4.3 us at 4096 x 4096. Walking several
+// row blocks per workgroup with the next block's weights in flight (2, 4 or 8
+// blocks) measured 13.7-14.3 us on the LM head, so each workgroup owns one.
 template <int NA, int EPI>
 int launch_gemv1(const Q4Args& a, hipStream_t st) {
   const int64_t nrb = ceil_div(a.N, 16);
   const size_t lds = (size_t)NA * a.K * 2;
-  if ((ceil_div(a.N, 64) < 512 || a.K >= 2048) && a.K >= 4 * 128)
+  const int64_t ng = a.K / 128;
+  if (ng == 16)  // 4, 8 or 11 K groups per wave, all requested at once
+    q4_gemv1_kernel<NA, EPI, 4, 4><<<(unsigned)nrb, 256, lds, st>>>(a);
+  else if (ng == 32)
+    q4_gemv1_kernel<NA, EPI, 4, 8><<<(unsigned)nrb, 256, lds, st>>>(a);
+  else if (ng == 44)
+    q4_gemv1_kernel<NA, EPI, 4, 11><<<(unsigned)nrb, 256, lds, st>>>(a);
+  else if ((ceil_div(a.N, 64) < 512 || a.K >= 2048) && a.K >= 4 * 128)
     q4_gemv1_kernel<NA, EPI, 4><<<(unsigned)nrb, 256, lds, st>>>(a);
   else
     q4_gemv1_kernel<NA, EPI, 1><<<(unsigned)ceil_div(nrb, 4), 256, lds, st>>>(a);
