@@ -16,10 +16,13 @@
 // operand (natural [pos][hd] layout is already k-contiguous per lane). The
 // online softmax runs on the MFMA output registers, probabilities go through a
 // per-wave LDS slice, and P.V is a VALU FMA pass with hd/8 lanes per V row
-// (16-byte loads, several rows per wave instruction). All K and V loads of a
-// 64-key tile are issued together before any math, so a tile costs one HBM
-// round trip. Waves merge (max, sum, O) in LDS
-// at the end in a fixed order.
+// (16-byte loads, several rows per wave instruction). Tiles are 32 keys; all
+// K and V loads of a tile are issued together before its math, so a tile costs
+// one HBM round trip; 32-key tiles keep the kernel at 138 VGPRs, three waves
+// per SIMD (measured on MI355X, config[2] decode S256 H16/4 len 768: 78-80 us
+// against 81-83 us for 64-key tiles at two waves per SIMD, and the same again
+// with 32-key tiles double-buffered in registers at two). Waves merge (max,
+// sum, O) in LDS at the end in a fixed order.
 //
 // Prefill / recompute (many queries, causal) uses the flash-attention kernel
 // in prefill_attention.hip; fp32 models (config[0]) use the simple VALU
@@ -50,7 +53,10 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int len = min(lens[s], cap);
   const size_t kv_base = ((size_t)s * KVH + kvh) * cap * HD;
 
-  __shared__ float pbuf[4][QM][64];
+  constexpr int TK = 32;         // keys per tile
+  constexpr int VR = TK / PPI;   // V rows of a tile held by each lane
+  constexpr int KB = TK / 16;    // 16-key MFMA blocks per tile
+  __shared__ float pbuf[4][QM][TK];
   __shared__ float mrg_m[4][QM], mrg_l[4][QM];
   __shared__ float mrg_o[4][QM][HD];
 
@@ -78,35 +84,37 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int sub = lane / LPK;          // which key of the PPI group this lane handles
   const int dl = (lane % LPK) * 8;     // first of the eight dims this lane owns
 
-  constexpr int VR = 64 / PPI;  // V rows of a 64-key tile held by each lane
-  for (int t0 = wave * 64; t0 < len; t0 += 256) {
-    // ---- issue every load of the tile up front (K fragments for the score
-    //      MFMAs and this lane's V rows for P.V), branch-free: rows past the
-    //      end are clamped to a valid row and masked out below. One round trip
-    //      per tile instead of one per dependent phase.
-    op8 kf[4][STEPS];
+  // One tile's loads: K fragments for the score MFMAs and this lane's V rows.
+  // Rows past the end are clamped to the last valid row (masked below; a
+  // tile wholly past the end reads one row, from cache).
+  struct Tile {
+    op8 kf[KB][STEPS];
     u32x4 vr[VR];
+  };
+  const int last = max(len - 1, 0);  // every load stays inside the sequence's cache rows
+  auto load = [&](int t0, Tile& T) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      const int key = min(t0 + kb * 16 + j, len - 1);
+    for (int kb = 0; kb < KB; ++kb) {
+      const int key = min(t0 + kb * 16 + j, last);
 #pragma unroll
       for (int st = 0; st < STEPS; ++st)
-        kf[kb][st] = *reinterpret_cast<const op8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
+        T.kf[kb][st] = *reinterpret_cast<const op8*>(kc + kv_base + (size_t)key * HD + st * 32 + g * 8);
     }
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
-      const int key = min(t0 + sub + i * PPI, len - 1);
-      vr[i] = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)key * HD + dl);
+      const int key = min(t0 + sub + i * PPI, last);
+      T.vr[i] = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)key * HD + dl);
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // ---- scores for 64 keys: 4 MFMA blocks of 16 keys
+  };
+  auto compute = [&](int t0, const Tile& T) {
+    // ---- scores for TK keys: KB MFMA blocks of 16 keys
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < KB; ++kb) {
       const int key = t0 + kb * 16 + j;
       f4 acc = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < STEPS; ++st)
-        acc = Op8<KF16>::mfma(qa[st], kf[kb][st], acc);
+        acc = Op8<KF16>::mfma(qa[st], T.kf[kb][st], acc);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 4 * g + r;
@@ -120,7 +128,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int i = 0; i < QM; ++i) {
       if (i >= qpk) break;
-      const float v = pbuf[wave][i][lane];
+      const float v = lane < TK ? pbuf[wave][i][lane] : -INFINITY;
       const float mnew = fmaxf(m_i[i], wave_max(v));
       const float alpha = (m_i[i] == -INFINITY) ? 0.f : __expf(m_i[i] - mnew);
       const float p = (v == -INFINITY) ? 0.f : __expf(v - mnew);
@@ -128,7 +136,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       m_i[i] = mnew;
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[i][e] *= alpha;
-      pbuf[wave][i][lane] = p;
+      if (lane < TK) pbuf[wave][i][lane] = p;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
@@ -138,7 +146,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     for (int vi = 0; vi < VR; ++vi) {
       const int tt = sub + vi * PPI;
       float v[8];
-      unpack8<KF16>(vr[vi], v);
+      unpack8<KF16>(T.vr[vi], v);
 #pragma unroll
       for (int i = 0; i < QM; ++i) {
         if (i >= qpk) break;
@@ -148,6 +156,14 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       }
     }
     __builtin_amdgcn_wave_barrier();
+  };
+
+  // Wave w takes tiles w, w + 4, ...
+  constexpr int STRIDE = 4 * TK;
+  for (int t0 = wave * TK; t0 < len; t0 += STRIDE) {
+    Tile ta;
+    load(t0, ta);
+    compute(t0, ta);
   }
   // combine the PPI key-subsets inside the wave
   if constexpr (PPI > 1) {
