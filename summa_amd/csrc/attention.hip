@@ -85,8 +85,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   const int dl = (lane % LPK) * 8;     // first of the eight dims this lane owns
 
   // One tile's loads: K fragments for the score MFMAs and this lane's V rows.
-  // Rows past the end are clamped to the last valid row (masked below; a
-  // tile wholly past the end reads one row, from cache).
+  // Rows past the end are clamped to the last valid row and masked below.
   struct Tile {
     op8 kf[KB][STEPS];
     u32x4 vr[VR];
