@@ -84,6 +84,30 @@ def test_attn_decode_f16_cache_pair_out(dev, S, H, KVH, hd, cap):
     np.testing.assert_allclose(_unpair(out, H * hd).reshape(S, H, hd), ref, rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("H,KVH,hd", [(16, 4, 128), (12, 12, 64), (8, 1, 128)])
+def test_attn_decode_tile_edges(dev, H, KVH, hd):
+    """Lengths around the 32-key tile and the 4-wave stride (1, 31-33, 127-129,
+    255-257 keys): the clamped loads past the end and the masked keys of a
+    partial tile must not reach the result."""
+    lens = np.array([1, 31, 32, 33, 127, 128, 129, 255, 256, 257], dtype=np.int32)
+    S, cap = len(lens), 300
+    print(f"case tile edges H={H} KVH={KVH} hd={hd} lens={lens.tolist()}", flush=True)
+    rng = np.random.default_rng(hd + H)
+    q, k, v = (rng.normal(0, 1, sh).astype(np.float16)
+               for sh in ((S, H, hd), (S, KVH, cap, hd), (S, KVH, cap, hd)))
+    # poison the rows past each length: a read of them would show in the result
+    for s_, n in enumerate(lens):
+        k[s_, :, n:] = 60.0
+        v[s_, :, n:] = 1000.0
+    out = torch.empty(S, 2 * H * hd, dtype=torch.float16, device=dev)
+    L = torch.from_numpy(lens).to(dev)
+    qd, kd, vd = _f16(q, dev), _f16(k, dev), _f16(v, dev)
+    call("sm_attn_decode", qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), L.data_ptr(),
+         out.data_ptr(), SM_F16, SM_F16X2, S, H, KVH, cap, hd, _s())
+    ref = _attn_ref(q.astype(np.float32), k.astype(np.float32), v.astype(np.float32), lens)
+    np.testing.assert_allclose(_unpair(out, H * hd).reshape(S, H, hd), ref, rtol=2e-5, atol=2e-6)
+
+
 @pytest.mark.parametrize("S,L,p0,H,KVH,hd", [(2, 100, 0, 4, 4, 64), (2, 64, 0, 16, 4, 128),
                                              (1, 130, 3, 8, 2, 128)])
 def test_attn_prefill_f16_cache_pair_out(dev, S, L, p0, H, KVH, hd):
