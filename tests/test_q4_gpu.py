@@ -257,7 +257,8 @@ def test_split_k_workspace(dev, m, n, k, epi, xdt):
 
 @pytest.mark.parametrize("n,k,pair", [(16400, 2048, False), (16400, 1024, True), (1000, 640, False),
                                       (1000, 640, True), (300, 256, False), (65536, 2048, False),
-                                      (2048, 5632, True), (4096, 4096, False), (40000, 4096, True)])
+                                      (2048, 5632, True), (4096, 4096, False), (40000, 4096, True),
+                                      (1000, 2048, True), (1003, 5632, False), (65533, 2048, True)])
 def test_gemv_m1_equals_tile_kernel(dev, n, k, pair):
     """M = 1 runs the single-row GEMV (activation row in LDS, double-buffered
     weight groups; K split across waves for small N and for K >= 2048). Where
