@@ -581,10 +581,10 @@ int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_til
 // merged in LDS in wave order (for N too small to fill the GPU otherwise). The activation
 // row is staged in LDS once per workgroup, after the first weight group has
 // been requested, and feeds every A row of the MFMA (so every D row is the
-// result and no lane is masked). With every group of a wave requested up
-// front (ALL) each wave copies only its own groups of the row and waits on no
-// other wave (measured: 3072 x 2048 3.0 -> 2.7 us, 4096 x 4096 4.4 -> 3.65 us,
-// LM head 12.9 -> 12.7 us). Weight groups are double-buffered in
+// result and no lane is masked). With K split over the waves each wave copies
+// only its own groups of the row and waits on no other wave (measured with
+// every group of a wave requested up front: 3072 x 2048 3.0 -> 2.7 us,
+// 4096 x 4096 4.4 -> 3.65 us, LM head 12.9 -> 12.7 us). Weight groups are double-buffered in
 // registers, which leaves the weight stream alone on the vector-memory
 // counter: activation loads interleaved with it made every wait drain the
 // next group's weights too. The arithmetic per group is that of
@@ -618,14 +618,23 @@ __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
     load(part, w0, s0);
   }
   const _Float16* x = static_cast<const _Float16*>(a.x);
-  if constexpr (ALL > 0 && KS == 4) {
+  if constexpr (KS == 4) {
     // each wave copies only its own K groups (part + 4i) of the activation row
     // into their places in LDS; no workgroup barrier before the math
+    if constexpr (ALL > 0) {  // trip count known: fully unrolled
 #pragma unroll
-    for (int c = lane; c < NA * ALL * 16; c += kWave) {
-      const int h = c / (ALL * 16), i = (c / 16) % ALL, ch = c % 16;
-      const int off = h * a.K + (part + 4 * i) * 128 + ch * 8;
-      *reinterpret_cast<h8*>(xs + off) = *reinterpret_cast<const h8*>(x + off);
+      for (int c = lane; c < NA * ALL * 16; c += kWave) {
+        const int h = c / (ALL * 16), i = (c / 16) % ALL, ch = c % 16;
+        const int off = h * a.K + (part + 4 * i) * 128 + ch * 8;
+        *reinterpret_cast<h8*>(xs + off) = *reinterpret_cast<const h8*>(x + off);
+      }
+    } else {
+      const int mine = (ng - part + 3) / 4;
+      for (int c = lane; c < NA * mine * 16; c += kWave) {
+        const int h = c / (mine * 16), i = (c / 16) % mine, ch = c % 16;
+        const int off = h * a.K + (part + 4 * i) * 128 + ch * 8;
+        *reinterpret_cast<h8*>(xs + off) = *reinterpret_cast<const h8*>(x + off);
+      }
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
