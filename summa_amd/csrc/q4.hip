@@ -611,23 +611,35 @@ __global__ __launch_bounds__(256) void q4_gemv1_kernel(Q4Args a) {
   };
   u32x4 w0, w1, wa[ALL > 0 ? ALL : 1];
   uint16_t s0, s1, sa[ALL > 0 ? ALL : 1];
+  const _Float16* x = static_cast<const _Float16*>(a.x);
+  // With every group requested up front, this wave's activation chunks are
+  // requested first: loads complete in issue order, so the copy into LDS then
+  // waits for them alone and the math starts as the first weight group lands.
+  constexpr int XN = NA * (ALL > 0 ? ALL : 1) * 16, XC = (XN + kWave - 1) / kWave;
+  h8 xr[XC];
+  int xoff[XC];
+  if constexpr (ALL > 0 && KS == 4) {
+#pragma unroll
+    for (int u = 0; u < XC; ++u) {
+      const int c = lane + u * kWave;
+      const int h = c / (ALL * 16), i = (c / 16) % ALL, ch = c % 16;
+      xoff[u] = h * a.K + (part + 4 * i) * 128 + ch * 8;
+      if (c < XN) xr[u] = *reinterpret_cast<const h8*>(x + xoff[u]);
+    }
+  }
   if constexpr (ALL > 0) {
 #pragma unroll
     for (int i = 0; i < ALL; ++i) load(part + i * KS, wa[i], sa[i]);
   } else {
     load(part, w0, s0);
   }
-  const _Float16* x = static_cast<const _Float16*>(a.x);
   if constexpr (KS == 4) {
     // each wave copies only its own K groups (part + 4i) of the activation row
     // into their places in LDS; no workgroup barrier before the math
-    if constexpr (ALL > 0) {  // trip count known: fully unrolled
+    if constexpr (ALL > 0) {
 #pragma unroll
-      for (int c = lane; c < NA * ALL * 16; c += kWave) {
-        const int h = c / (ALL * 16), i = (c / 16) % ALL, ch = c % 16;
-        const int off = h * a.K + (part + 4 * i) * 128 + ch * 8;
-        *reinterpret_cast<h8*>(xs + off) = *reinterpret_cast<const h8*>(x + off);
-      }
+      for (int u = 0; u < XC; ++u)
+        if (lane + u * kWave < XN) *reinterpret_cast<h8*>(xs + xoff[u]) = xr[u];
     } else {
       const int mine = (ng - part + 3) / 4;
       for (int c = lane; c < NA * mine * 16; c += kWave) {
