@@ -53,6 +53,8 @@ def _declare(L: C.CDLL) -> None:
         getattr(L, name).restype = None
     L.or_round_f16.argtypes = [C.c_float]
     L.or_round_f16.restype = C.c_float
+    L.or_bf16_bits.argtypes = [vp, i64, vp]
+    L.or_bf16_bits.restype = None
     _declare_model(L)
 
 
@@ -97,11 +99,11 @@ def _ptr(a):
 # ---------------------------------------------------------------- helpers ---
 
 def bf16_bits(x: np.ndarray) -> np.ndarray:
-    """float32 -> bf16 bit patterns, round to nearest even (NaN kept quiet)."""
-    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    nan = ((u & 0x7F800000) == 0x7F800000) & ((u & 0x007FFFFF) != 0)
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    r[nan] = ((u[nan] >> 16) | 0x40).astype(np.uint16)
+    """float32 -> bf16 bit patterns, round to nearest even (NaN kept quiet):
+    ``or_f32_to_bf16`` per element."""
+    a = np.ascontiguousarray(x, dtype=np.float32)
+    r = np.empty(a.shape, np.uint16)
+    lib().or_bf16_bits(a.ctypes.data, a.size, r.ctypes.data)
     return r
 
 
@@ -283,6 +285,29 @@ class HostModel:
                           lp.ctypes.data)
         return lp
 
+    def continuation(self, prompts, tokens):
+        """Teacher-forced recompute of ``or_logprobs`` that also returns the
+        logits: (lp [S, N] f64, logits [S, N, V] f32), row n being the
+        prediction of tokens[:, n] from prompt ‖ tokens[:, :n]."""
+        prompts = np.ascontiguousarray(prompts, dtype=np.int32)
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        S, P = prompts.shape
+        N = tokens.shape[1]
+        L = P + N - 1
+        c = self.cfg
+        ids = np.ascontiguousarray(np.concatenate([prompts, tokens[:, :N - 1]], 1))
+        kc = np.zeros(c["layers"] * S * c["KVH"] * L * c["hd"], np.float32)
+        vc = np.zeros_like(kc)
+        x = np.empty((S, L, c["d"]), np.float32)
+        lib().or_model_forward(C.byref(self.m), ids.ctypes.data, S, L, 0, kc.ctypes.data,
+                               vc.ctypes.data, L, x.ctypes.data)
+        del kc, vc
+        rows = np.ascontiguousarray(x[:, P - 1:, :]).reshape(S * N, c["d"])
+        logits = np.empty((S * N, c["V"]), np.float32)
+        lib().or_model_logits(C.byref(self.m), rows.ctypes.data, S * N, logits.ctypes.data)
+        lp, _, _ = ce_rows(logits, tokens.reshape(-1))
+        return lp.reshape(S, N), logits.reshape(S, N, c["V"])
+
     def forward_logits(self, ids):
         """Full causal forward over ids [S, L]; returns logits [S, L, V] (float32)."""
         ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -306,9 +331,13 @@ class HostModel:
         S, L = ids.shape
         c = self.cfg
         gaps = np.full((c["layers"], S * L), np.inf, np.float32)
+        kc = np.zeros(c["layers"] * S * c["KVH"] * L * c["hd"], np.float32)
+        vc = np.zeros_like(kc)
+        x = np.empty((S * L, c["d"]), np.float32)
         self.m.router_gap = gaps.ctypes.data
         try:
-            self.forward_logits(ids)
+            lib().or_model_forward(C.byref(self.m), ids.ctypes.data, S, L, 0, kc.ctypes.data,
+                                   vc.ctypes.data, L, x.ctypes.data)
         finally:
             self.m.router_gap = None
         return gaps.reshape(c["layers"], S, L)

@@ -62,27 +62,79 @@ static float q4_at(const uint8_t* codes, const uint16_t* scales, int64_t i) {
   return or_bf16_to_f32(scales[i / 128]) * (float)q;
 }
 
+/* Decode row n ([K] values) of a Q4 tensor whose rows start at n * K. */
+static void q4_row(const uint8_t* c, const uint16_t* s, int64_t n, int64_t K, float* out) {
+  for (int64_t k = 0; k < K; ++k) out[k] = q4_at(c, s, n * K + k);
+}
+
+/* f64 dot product of f32 vectors: the products are exact in f64, and eight
+ * interleaved partial sums (k mod 8) are added at the end. The result differs
+ * from a sequential f64 sum only far below f32 resolution; it stands for the
+ * exactly accumulated value. */
+static double dot64(const float* a, const float* b, int64_t K) {
+  double p[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+  int64_t k = 0;
+  for (; k + 8 <= K; k += 8)
+    for (int j = 0; j < 8; ++j) p[j] += (double)a[k + j] * (double)b[k + j];
+  for (; k < K; ++k) p[0] += (double)a[k] * (double)b[k];
+  return ((p[0] + p[4]) + (p[1] + p[5])) + ((p[2] + p[6]) + (p[3] + p[7]));
+}
+
+/* dot64 of four rows w0..w3 (stride K) with one x, each computed exactly as
+ * dot64 computes it; the four are interleaved only for instruction-level
+ * parallelism. */
+static void dot64x4(const float* w, const float* x, int64_t K, double* out) {
+  double p[4][8] = {{0}};
+  int64_t k = 0;
+  for (; k + 8 <= K; k += 8)
+    for (int r = 0; r < 4; ++r)
+      for (int j = 0; j < 8; ++j) p[r][j] += (double)w[r * K + k + j] * (double)x[k + j];
+  for (; k < K; ++k)
+    for (int r = 0; r < 4; ++r) p[r][0] += (double)w[r * K + k] * (double)x[k];
+  for (int r = 0; r < 4; ++r)
+    out[r] = ((p[r][0] + p[r][4]) + (p[r][1] + p[r][5])) + ((p[r][2] + p[r][6]) + (p[r][3] + p[r][7]));
+}
+
 /* y[r, n] (+)= sum_k x[r, k] * W[n, k]; W dense f32 (w) or Q4 codes/scales
- * (c, s); sequential f32 accumulation, or f64 with acc64. */
+ * (c, s); sequential f32 accumulation, or f64 with acc64. Weight rows are
+ * decoded once, in blocks of 16, and each input row is applied to a whole
+ * block while it sits in cache; every output is still its own dot product. */
+#define OR_NB 16
 static void linear_w(const or_model* m, int64_t N, int64_t K, const float* w, const uint8_t* c,
                      const uint16_t* s, const float* x, int64_t M, float* y, int add) {
-#pragma omp parallel for schedule(static) collapse(2)
-  for (int64_t r = 0; r < M; ++r)
-    for (int64_t n = 0; n < N; ++n) {
-      float acc = 0.f;
-      double acc64 = 0.0;
-      const float* xr = x + r * K;
-      if (w) {
-        const float* wr = w + n * K;
-        if (m->acc64) for (int64_t k = 0; k < K; ++k) acc64 += (double)wr[k] * xr[k];
-        else for (int64_t k = 0; k < K; ++k) acc += wr[k] * xr[k];
-      } else {
-        if (m->acc64) for (int64_t k = 0; k < K; ++k) acc64 += (double)q4_at(c, s, n * K + k) * xr[k];
-        else for (int64_t k = 0; k < K; ++k) acc += q4_at(c, s, n * K + k) * xr[k];
+  const int64_t nblk = (N + OR_NB - 1) / OR_NB;
+#pragma omp parallel
+  {
+    float* buf = w ? NULL : malloc(sizeof(float) * K * OR_NB);
+#pragma omp for schedule(dynamic, 1)
+    for (int64_t b = 0; b < nblk; ++b) {
+      const int64_t n0 = b * OR_NB, nn = N - n0 < OR_NB ? N - n0 : OR_NB;
+      const float* wb = w ? w + n0 * K : buf;
+      if (!w)
+        for (int64_t j = 0; j < nn; ++j) q4_row(c, s, n0 + j, K, buf + j * K);
+      for (int64_t r = 0; r < M; ++r) {
+        const float* xr = x + r * K;
+        int64_t j = 0;
+        if (m->acc64)
+          for (; j + 4 <= nn; j += 4) {
+            double o[4];
+            dot64x4(wb + j * K, xr, K, o);
+            for (int q = 0; q < 4; ++q) {
+              if (add) y[r * N + n0 + j + q] += (float)o[q];
+              else y[r * N + n0 + j + q] = (float)o[q];
+            }
+          }
+        for (; j < nn; ++j) {
+          const float* wr = wb + j * K;
+          float acc = 0.f;
+          if (m->acc64) acc = (float)dot64(wr, xr, K);
+          else for (int64_t k = 0; k < K; ++k) acc += wr[k] * xr[k];
+          if (add) y[r * N + n0 + j] += acc; else y[r * N + n0 + j] = acc;
+        }
       }
-      if (m->acc64) acc = (float)acc64;
-      if (add) y[r * N + n] += acc; else y[r * N + n] = acc;
     }
+    free(buf);
+  }
 }
 
 /* kind: 0 qkv, 1 o, 2 in, 3 down, 4 lm_head */
@@ -109,63 +161,85 @@ static void linear(const or_model* m, int kind, int layer, const float* x, int64
 }
 
 /* x += SparseMoe(h) (ffn.rs:478-711) for M tokens: fp32 router, strict top-2,
- * softmax over the pair, per-route SwiGLU expert MLP, weighted sum. */
+ * softmax over the pair, per-route SwiGLU expert MLP, weighted sum. The routes
+ * are grouped by expert so that each expert's weights are decoded once; every
+ * route's values are computed exactly as for a token on its own. */
 static void moe_ffn(const or_model* m, int layer, const float* h, int64_t M, float* x) {
   const int E = m->experts, Fe = m->expert_ffn, d = m->d;
   const float* wr = m->router + (size_t)layer * E * d;
   const int64_t nin = 2 * (int64_t)Fe * d, ndown = (int64_t)d * Fe;
-  float* gv = malloc(sizeof(float) * 2 * Fe);
-  float* u = malloc(sizeof(float) * Fe);
-  float* yv = malloc(sizeof(float) * 2 * d);
-  float* lg = malloc(sizeof(float) * E);
-  for (int64_t t = 0; t < M; ++t) {
-    const float* ht = h + t * d;
-    for (int e = 0; e < E; ++e) {
-      float acc = 0.f;
-      double acc64 = 0.0;
-      if (m->acc64) { for (int c = 0; c < d; ++c) acc64 += (double)ht[c] * wr[(size_t)e * d + c]; acc = (float)acc64; }
-      else for (int c = 0; c < d; ++c) acc += ht[c] * wr[(size_t)e * d + c];
-      lg[e] = acc;
-    }
-    float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY;
-    int i0 = 0, i1 = 0;
-    for (int e = 0; e < E; ++e) {
-      if (lg[e] > v0) { v2 = v1; v1 = v0; i1 = i0; v0 = lg[e]; i0 = e; }
-      else if (lg[e] > v1) { v2 = v1; v1 = lg[e]; i1 = e; }
-      else if (lg[e] > v2) v2 = lg[e];
-    }
-    if (m->router_gap) m->router_gap[(int64_t)layer * M + t] = v1 - v2;
-    const float e1 = expf(v1 - v0);
-    const float w0 = 1.f / (1.f + e1), w1 = e1 / (1.f + e1);
-    const int sel[2] = {i0, i1};
-    for (int j = 0; j < 2; ++j) {
-      const int e = sel[j];
-      const int64_t base_in = ((int64_t)layer * E + e) * nin, base_down = ((int64_t)layer * E + e) * ndown;
-      if (m->quantized)
-        linear_w(m, 2 * Fe, d, NULL, m->exp_in_c + base_in / 2, m->exp_in_s + base_in / 128, ht, 1, gv, 0);
-      else
-        linear_w(m, 2 * Fe, d, m->exp_in + base_in, NULL, NULL, ht, 1, gv, 0);
-      for (int c = 0; c < Fe; ++c) {
-        const float g = gv[c], v = gv[Fe + c];
-        u[c] = g / (1.0f + expf(-g)) * v;
+  int32_t* sel = malloc(sizeof(int32_t) * M * 2);
+  float* rw = malloc(sizeof(float) * M * 2);
+#pragma omp parallel
+  {
+    float* lg = malloc(sizeof(float) * E);
+#pragma omp for schedule(static)
+    for (int64_t t = 0; t < M; ++t) {
+      const float* ht = h + t * d;
+      for (int e = 0; e < E; ++e) {
+        float acc = 0.f;
+        double acc64 = 0.0;
+        if (m->acc64) { for (int c = 0; c < d; ++c) acc64 += (double)ht[c] * wr[(size_t)e * d + c]; acc = (float)acc64; }
+        else for (int c = 0; c < d; ++c) acc += ht[c] * wr[(size_t)e * d + c];
+        lg[e] = acc;
       }
-      if (m->quantized)
-        linear_w(m, d, Fe, NULL, m->exp_down_c + base_down / 2, m->exp_down_s + base_down / 128, u, 1, yv + j * d, 0);
-      else
-        linear_w(m, d, Fe, m->exp_down + base_down, NULL, NULL, u, 1, yv + j * d, 0);
+      float v0 = -INFINITY, v1 = -INFINITY, v2 = -INFINITY;
+      int i0 = 0, i1 = 0;
+      for (int e = 0; e < E; ++e) {
+        if (lg[e] > v0) { v2 = v1; v1 = v0; i1 = i0; v0 = lg[e]; i0 = e; }
+        else if (lg[e] > v1) { v2 = v1; v1 = lg[e]; i1 = e; }
+        else if (lg[e] > v2) v2 = lg[e];
+      }
+      if (m->router_gap) m->router_gap[(int64_t)layer * M + t] = v1 - v2;
+      const float e1 = expf(v1 - v0);
+      sel[2 * t] = i0;
+      sel[2 * t + 1] = i1;
+      rw[2 * t] = 1.f / (1.f + e1);
+      rw[2 * t + 1] = e1 / (1.f + e1);
     }
+    free(lg);
+  }
+  float* yr = malloc(sizeof(float) * M * 2 * d);   /* expert output per route t*2+j */
+  int64_t* rt = malloc(sizeof(int64_t) * M * 2);   /* routes of one expert */
+  float* hx = malloc(sizeof(float) * M * 2 * d);
+  float* gv = malloc(sizeof(float) * M * 2 * 2 * Fe);
+  float* u = malloc(sizeof(float) * M * 2 * Fe);
+  float* yv = malloc(sizeof(float) * M * 2 * d);
+  for (int e = 0; e < E; ++e) {
+    int64_t cnt = 0;
+    for (int64_t r = 0; r < 2 * M; ++r)
+      if (sel[r] == e) rt[cnt++] = r;
+    if (cnt == 0) continue;
+    for (int64_t i = 0; i < cnt; ++i) memcpy(hx + i * d, h + (rt[i] / 2) * d, sizeof(float) * d);
+    const int64_t base_in = ((int64_t)layer * E + e) * nin, base_down = ((int64_t)layer * E + e) * ndown;
+    if (m->quantized)
+      linear_w(m, 2 * Fe, d, NULL, m->exp_in_c + base_in / 2, m->exp_in_s + base_in / 128, hx, cnt, gv, 0);
+    else
+      linear_w(m, 2 * Fe, d, m->exp_in + base_in, NULL, NULL, hx, cnt, gv, 0);
+    for (int64_t i = 0; i < cnt; ++i)
+      for (int c = 0; c < Fe; ++c) {
+        const float g = gv[i * 2 * Fe + c], v = gv[i * 2 * Fe + Fe + c];
+        u[i * Fe + c] = g / (1.0f + expf(-g)) * v;
+      }
+    if (m->quantized)
+      linear_w(m, d, Fe, NULL, m->exp_down_c + base_down / 2, m->exp_down_s + base_down / 128, u, cnt, yv, 0);
+    else
+      linear_w(m, d, Fe, m->exp_down + base_down, NULL, NULL, u, cnt, yv, 0);
+    for (int64_t i = 0; i < cnt; ++i) memcpy(yr + rt[i] * d, yv + i * d, sizeof(float) * d);
+  }
+  for (int64_t t = 0; t < M; ++t)
     for (int c = 0; c < d; ++c) {
       float sum = 0.f;
-      sum += yv[c] * w0;
-      sum += yv[d + c] * w1;
+      sum += yr[(2 * t) * d + c] * rw[2 * t];
+      sum += yr[(2 * t + 1) * d + c] * rw[2 * t + 1];
       x[t * d + c] += sum;
     }
-  }
-  free(gv); free(u); free(yv); free(lg);
+  free(sel); free(rw); free(yr); free(rt); free(hx); free(gv); free(u); free(yv);
 }
 
 static void rmsnorm(const or_model* m, const float* x, const float* g, int64_t M, float* y) {
   const int d = m->d;
+#pragma omp parallel for schedule(static)
   for (int64_t r = 0; r < M; ++r) {
     float ss = 0.f;
     for (int c = 0; c < d; ++c) ss += x[r * d + c] * x[r * d + c];
@@ -196,6 +270,12 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
   float* gv = malloc(sizeof(float) * rows * 2 * F);
   float* u = malloc(sizeof(float) * rows * F);
   const float scale = 1.0f / sqrtf((float)hd);
+  /* cos / sin of (position pos0 + i, pair p), the same values rope_cs gives */
+  float* rcos = malloc(sizeof(float) * (size_t)L * (hd / 2));
+  float* rsin = malloc(sizeof(float) * (size_t)L * (hd / 2));
+  for (int i = 0; i < L; ++i)
+    for (int p = 0; p < hd / 2; ++p)
+      rope_cs(m, pos0 + i, p, &rcos[(size_t)i * (hd / 2) + p], &rsin[(size_t)i * (hd / 2) + p]);
   for (int64_t r = 0; r < rows; ++r)
     for (int c = 0; c < d; ++c) x[r * d + c] = m->embed[(int64_t)ids[r] * d + c];
   for (int l = 0; l < m->layers; ++l) {
@@ -203,6 +283,7 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
     float* vl = vc + (size_t)l * S * KVH * cap * hd;
     rmsnorm(m, x, m->attn_norm + (size_t)l * d, rows, h);
     linear(m, 0, l, h, rows, qkv, 0);
+#pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; ++r) {
       const int s = (int)(r / L), pos = pos0 + (int)(r % L);
       const float* src = qkv + r * qn;
@@ -211,8 +292,8 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
           const float a = src[slot * hd + 2 * p], b = src[slot * hd + 2 * p + 1];
           float ra = a, rbv = b;
           if (slot < H + KVH) {
-            float cs, sn;
-            rope_cs(m, pos, p, &cs, &sn);
+            const float cs = rcos[(size_t)(pos - pos0) * (hd / 2) + p];
+            const float sn = rsin[(size_t)(pos - pos0) * (hd / 2) + p];
             ra = a * cs - b * sn;
             rbv = b * cs + a * sn;
           }
@@ -263,6 +344,7 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
       continue;
     }
     linear(m, 2, l, h, rows, gv, 0);
+#pragma omp parallel for schedule(static)
     for (int64_t r = 0; r < rows; ++r)
       for (int c = 0; c < F; ++c) {
         const float g = gv[r * 2 * F + c], v = gv[r * 2 * F + F + c];
@@ -270,7 +352,7 @@ void or_model_forward(const or_model* m, const int32_t* ids, int S, int L, int p
       }
     linear(m, 3, l, u, rows, x, 1);
   }
-  free(h); free(qkv); free(q); free(att); free(gv); free(u);
+  free(h); free(qkv); free(q); free(att); free(gv); free(u); free(rcos); free(rsin);
 }
 
 void or_model_logits(const or_model* m, const float* x, int64_t M, float* logits) {

@@ -22,6 +22,11 @@ uint16_t or_f32_to_bf16(float f) {
   return (uint16_t)(u >> 16);
 }
 
+void or_bf16_bits(const float* x, int64_t n, uint16_t* out) {
+#pragma omp parallel for schedule(static)
+  for (int64_t i = 0; i < n; ++i) out[i] = or_f32_to_bf16(x[i]);
+}
+
 float or_round_f16(float f) {
   if (!isfinite(f)) return f;
   const float a = fabsf(f);
@@ -189,6 +194,8 @@ static float round_half_away(float v) { return v >= 0.f ? floorf(v + 0.5f) : -fl
 void or_q4_quantize(const float* w, int64_t n, uint8_t* codes, uint16_t* scales) {
   const int64_t groups = (n + 127) / 128;
   memset(codes, 0, (size_t)(groups * 64));
+  /* groups own disjoint 64-byte code ranges */
+#pragma omp parallel for schedule(static)
   for (int64_t g = 0; g < groups; ++g) {
     const int64_t lo = g * 128, hi = lo + 128 < n ? lo + 128 : n;
     float amax = 0.f;

@@ -23,6 +23,7 @@ extern "C" {
 /* bf16 <-> f32 (round to nearest even), the rounding the device path uses. */
 float or_bf16_to_f32(uint16_t b);
 uint16_t or_f32_to_bf16(float f);
+void or_bf16_bits(const float* x, int64_t n, uint16_t* out); /* elementwise or_f32_to_bf16 */
 /* f32 -> nearest IEEE binary16 value (ties to even, subnormals, overflow to
  * inf), returned as f32. */
 float or_round_f16(float f);

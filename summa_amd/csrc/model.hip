@@ -14,10 +14,11 @@
 // Precision policy. fp32 models: everything fp32 (the reference CPU path).
 // Quantized models: Q4G128 linears (incl. LM head), bf16 embedding table,
 // fp32 residual stream (the reference's decode stream, transformer.rs:588-592),
-// f16 activations into every matmul (the Q4 MFMA operand type; its 11-bit
-// significand keeps the log-prob noise of the activation roundings below the
-// 2e-3 parity bar, which bf16 activations exceed), bf16 q and KV cache, fp32
-// logits.
+// matmul inputs as f16 hi/lo pairs (SM_F16X2: x = hi + lo, about 22
+// significant bits, so activation roundings add no log-prob noise; a single
+// f16 or bf16 rounding per matmul input drifts past the 2e-3 parity bar at
+// 24 layers), f16 q and KV cache (3 more significand bits than bf16 in the
+// same bytes), fp32 logits.
 #include <cmath>
 #include <cstring>
 #include <vector>

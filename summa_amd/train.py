@@ -186,7 +186,10 @@ class Fp32Policy:
         """2-D matrices (per layer) go to Muon, the rest to AdamW (trainer.rs:1974)."""
         return ("qkv", "o", "in", "down")
 
-    def adamw_step(self, grads: dict, keys, lr=1e-3, betas=(0.9, 0.999), eps=1e-8, wd=1e-4):
+    def adamw_step(self, grads: dict, keys, lr=3e-4, betas=(0.9, 0.95), eps=1e-8, wd=0.1):
+        """AdamW with the trainer's settings: beta1 0.9, beta2 0.95, eps 1e-8
+        (summa-train/src/trainer.rs:1124-1129), lr 3e-4 and weight decay 0.1
+        (the CLI defaults, summa-train/src/main.rs:171-174)."""
         self._step += 1
         for k in keys:
             p, gr = self.p[k], grads[k].contiguous()

@@ -238,7 +238,7 @@ def test_grpo_update_lowers_the_surrogate_loss(dev):
 
     l0, dlp = loss_and_dlp()
     grads = pol.backward(dlp)
-    pol.adamw_step(grads, list(pol.p), lr=1e-3, wd=0.0)
+    pol.adamw_step(grads, list(pol.p))  # the trainer's AdamW settings
     l1, _ = loss_and_dlp()
     assert l1 < l0, (l0, l1)
     pol.to_model(m)
