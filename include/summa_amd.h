@@ -437,6 +437,17 @@ int64_t sm_model_weight_bytes(const sm_model* model);
  * load_floating_tensor, quantization.rs:1183-1189). Synchronises `stream`
  * for quantized linears (range check of the scales). */
 int sm_model_set_tensor(sm_model* model, int kind, int layer, const float* src, void* stream);
+/* MoE router trace, a diagnostic with no reference counterpart (the
+ * reference reports router statistics only as training-side auxiliary losses,
+ * ffn.rs:478-711). While a trace is set, every MoE layer of every forward run
+ * on this model appends, per token, its top-2 expert ids (idx [capacity, 2]
+ * int32, device) and its router logits (logits [capacity, experts] f32,
+ * device, nullable), in call order: forward by forward, layer by layer, tokens
+ * in row order (a prefill or recompute chunk: sequence-major; a decode step:
+ * one token per sequence). Entries past `capacity` tokens are dropped and
+ * counted. idx = NULL ends tracing. Setting a trace resets both counts. */
+int sm_model_trace_routes(sm_model* model, int32_t* idx, float* logits, int64_t capacity);
+int sm_model_route_trace_count(const sm_model* model, int64_t* recorded, int64_t* dropped);
 /* Synthetic weights: every linear and the embedding ~ N(0, std) from the
  * counter RNG, norms = 1, router ~ N(0, 1/sqrt(d)) so router logits are
  * ~N(0, 1) (the BASELINE configs' random init). */

@@ -69,7 +69,8 @@ class OrModel(C.Structure):
                                    "qkv_s", "o_s", "in_s", "down_s", "lm_s")] + \
         [("experts", C.c_int32), ("expert_ffn", C.c_int32)] + \
         [(n, C.c_void_p) for n in ("router", "exp_in", "exp_down", "exp_in_c", "exp_down_c",
-                                   "exp_in_s", "exp_down_s", "router_gap")]
+                                   "exp_in_s", "exp_down_s", "router_gap", "route_hint")] + \
+        [("hint_margin", C.c_float), ("hint_conflicts", C.c_void_p)]
 
 
 def _declare_model(L: C.CDLL) -> None:
@@ -285,10 +286,16 @@ class HostModel:
                           lp.ctypes.data)
         return lp
 
-    def continuation(self, prompts, tokens):
+    def continuation(self, prompts, tokens, route_hint=None, hint_margin=0.0):
         """Teacher-forced recompute of ``or_logprobs`` that also returns the
         logits: (lp [S, N] f64, logits [S, N, V] f32), row n being the
-        prediction of tokens[:, n] from prompt ‖ tokens[:, :n]."""
+        prediction of tokens[:, n] from prompt ‖ tokens[:, :n].
+
+        MoE models: ``route_hint`` [layers, S, P + N - 1, 2] expert ids of
+        another computation of the same forward; a token whose top-2 margin
+        (2nd minus 3rd router logit) is below ``hint_margin`` takes the hinted
+        pair. Returns (lp, logits, conflicts): conflicts counts hinted pairs
+        that differ from the oracle's own where its margin is not below it."""
         prompts = np.ascontiguousarray(prompts, dtype=np.int32)
         tokens = np.ascontiguousarray(tokens, dtype=np.int32)
         S, P = prompts.shape
@@ -299,14 +306,27 @@ class HostModel:
         kc = np.zeros(c["layers"] * S * c["KVH"] * L * c["hd"], np.float32)
         vc = np.zeros_like(kc)
         x = np.empty((S, L, c["d"]), np.float32)
-        lib().or_model_forward(C.byref(self.m), ids.ctypes.data, S, L, 0, kc.ctypes.data,
-                               vc.ctypes.data, L, x.ctypes.data)
+        conflicts = np.zeros(1, np.int32)
+        if route_hint is not None:
+            hint = np.ascontiguousarray(route_hint, dtype=np.int32)
+            assert hint.shape == (c["layers"], S, L, 2)
+            self.m.route_hint = hint.ctypes.data
+            self.m.hint_margin = float(hint_margin)
+            self.m.hint_conflicts = conflicts.ctypes.data
+        try:
+            lib().or_model_forward(C.byref(self.m), ids.ctypes.data, S, L, 0, kc.ctypes.data,
+                                   vc.ctypes.data, L, x.ctypes.data)
+        finally:
+            self.m.route_hint = None
+            self.m.hint_conflicts = None
         del kc, vc
         rows = np.ascontiguousarray(x[:, P - 1:, :]).reshape(S * N, c["d"])
         logits = np.empty((S * N, c["V"]), np.float32)
         lib().or_model_logits(C.byref(self.m), rows.ctypes.data, S * N, logits.ctypes.data)
         lp, _, _ = ce_rows(logits, tokens.reshape(-1))
-        return lp.reshape(S, N), logits.reshape(S, N, c["V"])
+        if route_hint is None:
+            return lp.reshape(S, N), logits.reshape(S, N, c["V"])
+        return lp.reshape(S, N), logits.reshape(S, N, c["V"]), int(conflicts[0])
 
     def forward_logits(self, ids):
         """Full causal forward over ids [S, L]; returns logits [S, L, V] (float32)."""

@@ -50,6 +50,13 @@ typedef struct or_model {
   /* optional diagnostics: when set, moe_ffn stores for layer l and row t the
    * router margin (2nd-largest minus 3rd-largest logit) at [l * M + t] */
   float* router_gap;
+  /* optional route hints [layers][M][2] (expert ids of another computation of
+   * the same forward): a token whose margin is below hint_margin is an
+   * ambiguous top-2 decision and takes the hinted pair; elsewhere a hinted
+   * pair that differs from the oracle's own is counted in *hint_conflicts */
+  const int32_t* route_hint;
+  float hint_margin;
+  int32_t* hint_conflicts;
 } or_model;
 
 /* f16 rounding of q, k and v (the 16-bit KV cache) of quantized models. */
@@ -191,6 +198,22 @@ static void moe_ffn(const or_model* m, int layer, const float* h, int64_t M, flo
         else if (lg[e] > v2) v2 = lg[e];
       }
       if (m->router_gap) m->router_gap[(int64_t)layer * M + t] = v1 - v2;
+      if (m->route_hint) {
+        const int32_t* hp = m->route_hint + ((int64_t)layer * M + t) * 2;
+        const int a = hp[0], b = hp[1];
+        const int same = (a == i0 && b == i1) || (a == i1 && b == i0);
+        if (!same && v1 - v2 < m->hint_margin && a >= 0 && a < E && b >= 0 && b < E && a != b) {
+          /* the first of the pair by logit (equal logits: the lower index) */
+          const int first = (lg[a] > lg[b] || (lg[a] == lg[b] && a < b)) ? a : b;
+          i0 = first;
+          i1 = first == a ? b : a;
+          v0 = lg[i0];
+          v1 = lg[i1];
+        } else if (!same && m->hint_conflicts) {
+#pragma omp atomic
+          *m->hint_conflicts += 1;
+        }
+      }
       const float e1 = expf(v1 - v0);
       sel[2 * t] = i0;
       sel[2 * t + 1] = i1;

@@ -71,6 +71,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_model_destroy": (i32, [vp]),
     "sm_model_weight_bytes": (i64, [vp]),
     "sm_model_set_tensor": (i32, [vp, i32, i32, vp, vp]),
+    "sm_model_trace_routes": (i32, [vp, vp, vp, i64]),
+    "sm_model_route_trace_count": (i32, [vp, vp, vp]),
     "sm_fnv1a64": (u64, [vp, i64]),
     "sm_hquant_parse": (i32, [vp, i64, vp]),
     "sm_hquant_bytes": (i64, [vp]),

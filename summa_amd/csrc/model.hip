@@ -180,6 +180,10 @@ struct sm_model {
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
       lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws, seen, done;
   int64_t gen_cap = 0, gen_S = 0;
+  // MoE router trace (sm_model_trace_routes): top-2 ids [cap, 2], logits [cap, E]
+  int32_t* trace_idx = nullptr;
+  float* trace_logits = nullptr;
+  int64_t trace_cap = 0, trace_used = 0, trace_dropped = 0;
 };
 
 namespace sm {
@@ -250,8 +254,22 @@ int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st) {
   SM_TRY(ensure(m->moe_y, (size_t)routes * d * 4));
   SM_TRY(ensure(m->moe_err, 4));
   int32_t* plan = (int32_t*)m->moe_plan.p;
-  SM_TRY(sm_moe_router_top2(m->h.p, m->act, Ly.router, rows, d, E, nullptr,
+  int32_t* trace_idx = nullptr;
+  float* trace_lg = nullptr;
+  if (m->trace_idx) {
+    if (m->trace_used + rows <= m->trace_cap) {
+      trace_idx = m->trace_idx + m->trace_used * 2;
+      if (m->trace_logits) trace_lg = m->trace_logits + m->trace_used * E;
+      m->trace_used += rows;
+    } else {
+      m->trace_dropped += rows;
+    }
+  }
+  SM_TRY(sm_moe_router_top2(m->h.p, m->act, Ly.router, rows, d, E, trace_lg,
                             (int32_t*)m->moe_idx.p, (float*)m->moe_w.p, st));
+  if (trace_idx)
+    SM_HIP(hipMemcpyAsync(trace_idx, m->moe_idx.p, (size_t)routes * 4, hipMemcpyDeviceToDevice,
+                          st));
   SM_TRY(sm_moe_route_plan((const int32_t*)m->moe_idx.p, rows, k, E, plan,
                            (int32_t*)m->moe_err.p, st));
   SM_TRY(sm_q4_grouped_matmul(Ly.exp_in.codes, Ly.exp_in.scales, E, 2 * Fe, d, m->h.p, m->act,
@@ -413,6 +431,26 @@ extern "C" int sm_model_destroy(sm_model* m) {
 }
 
 extern "C" int64_t sm_model_weight_bytes(const sm_model* m) { return m ? (int64_t)m->weight_bytes : 0; }
+
+extern "C" int sm_model_trace_routes(sm_model* m, int32_t* idx, float* logits, int64_t capacity) {
+  SM_REQUIRE(m, "sm_model_trace_routes: null model");
+  SM_REQUIRE(m->cfg.experts > 0 || !idx, "sm_model_trace_routes: the model has no MoE layers");
+  SM_REQUIRE(!idx || capacity >= 0, "sm_model_trace_routes: negative capacity");
+  SM_REQUIRE(idx || !logits, "sm_model_trace_routes: logits need an index buffer");
+  m->trace_idx = idx;
+  m->trace_logits = idx ? logits : nullptr;
+  m->trace_cap = idx ? capacity : 0;
+  m->trace_used = 0;
+  m->trace_dropped = 0;
+  return SM_OK;
+}
+
+extern "C" int sm_model_route_trace_count(const sm_model* m, int64_t* recorded, int64_t* dropped) {
+  SM_REQUIRE(m && recorded && dropped, "sm_model_route_trace_count: null argument");
+  *recorded = m->trace_used;
+  *dropped = m->trace_dropped;
+  return SM_OK;
+}
 
 static int tensor_target(sm_model* m, int kind, int layer, Linear** lin, void** dense,
                          int64_t* n, int64_t* count) {

@@ -117,6 +117,30 @@ class Model:
                 self.set_tensor(name, t)
         torch.cuda.synchronize()
 
+    def trace_routes(self, capacity: int, logits: bool = True):
+        """Start an MoE router trace of ``capacity`` token entries
+        (``sm_model_trace_routes``): returns the device buffers it fills, ids
+        [capacity, 2] int32 and router logits [capacity, experts] f32 (or None).
+        ``stop_trace`` ends it."""
+        dev = torch.device("cuda", torch.cuda.current_device())
+        idx = torch.full((capacity, 2), -1, dtype=torch.int32, device=dev)
+        lg = (torch.zeros((capacity, self.cfg.experts), dtype=torch.float32, device=dev)
+              if logits else None)
+        call("sm_model_trace_routes", self._h, idx.data_ptr(),
+             None if lg is None else lg.data_ptr(), int(capacity))
+        self._trace = (idx, lg)
+        return idx, lg
+
+    def route_trace_count(self):
+        """(recorded, dropped) token entries of the current trace."""
+        rec, drop = C.c_int64(), C.c_int64()
+        call("sm_model_route_trace_count", self._h, C.byref(rec), C.byref(drop))
+        return rec.value, drop.value
+
+    def stop_trace(self) -> None:
+        call("sm_model_trace_routes", self._h, None, None, 0)
+        self._trace = None
+
     def init_random(self, seed: int = 0, std: float = 0.02) -> None:
         call("sm_model_init_random", self._h, int(seed), float(std), _stream())
 

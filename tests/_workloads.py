@@ -94,7 +94,8 @@ def gumbel(seed, row, step, V):
         cnt = np.uint64(step) * np.uint64(V) + np.arange(V, dtype=np.uint64)
         k = mix64(a ^ (cnt * np.uint64(0xd1b54a32d192ed03)))
     u = ((k >> np.uint64(40)).astype(np.float32) + np.float32(0.5)) * np.float32(1.0 / 16777216.0)
-    return -np.log(-np.log(u.astype(np.float64)))
+    with np.errstate(divide="ignore"):  # u rounds to 1 for the top counter value: key +inf
+        return -np.log(-np.log(u.astype(np.float64)))
 
 
 def check_sampled_tokens(tokens, logits, temperature, seed, rows, tol):

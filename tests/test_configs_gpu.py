@@ -18,10 +18,8 @@ its frozen copy, the GRPO loss) and checks:
   the fp32 config[0]), and every sampled token equal to the sampler's choice
   on the oracle's logits up to a near-tie.
 
-The MoE config adds router near-ties: a token whose top-2 expert set is
-decided by less than the two paths' rounding differences can pick different
-experts in the decode and recompute paths (and the oracle). Its checks allow
-that for a few rollouts and name each one.
+The MoE config (test_moe_full_workload_rl_step) adds router near-ties, which
+its checks resolve through the device's traced router decisions.
 """
 import numpy as np
 import pytest
@@ -37,15 +35,11 @@ pytestmark = pytest.mark.gpu
 
 SEED = 7
 # A router near-tie: second- and third-largest router logits closer than
-# ROUTER_TIE in some layer at the first disagreeing token or the one before
-# it. The two device paths (and the oracle) agree on the residual stream to a
-# few 1e-5 relative, but their f16 K/V roundings differ by an ulp here and
-# there, which moves router logits (~N(0, 1)) by up to ~1e-4: a top-2 set can
-# flip only at a margin of that order. A margin under 1e-3 at two given
-# tokens in one of 16 layers has a probability of about 10 %, so a
-# disagreement without one points at a bug.
+# ROUTER_TIE. The two device paths (and the oracle) agree on the residual
+# stream to a few 1e-5 relative, but their f16 K/V roundings differ by an ulp
+# here and there, which moves router logits (~N(0, 1)) by up to ~1e-4: a
+# top-2 set can flip only at a margin of that order.
 ROUTER_TIE = 1e-3
-ROUTER_WINDOW = 1
 
 
 def _run_step(wl, dev):
@@ -77,7 +71,6 @@ def test_full_workload_rl_step(dev, index):
     mc, host_w, a, res = _run_step(wl, dev)
     V = mc.vocab
     tok, lp_beh, lp_cur, lp_ref = a["tokens"], a["lp_beh"], a["lp_cur"], a["lp_ref"]
-    moe = bool(mc.experts)
     lp_tol = 2e-3 if wl.quantized else 1e-5
 
     # ---- whole-batch properties
@@ -87,30 +80,14 @@ def test_full_workload_rl_step(dev, index):
         assert (lp <= 0).all(), f"{name} log-probs > 0: {lp.max()}"
     assert np.array_equal(lp_ref, lp_cur), "frozen copy with equal weights must match bitwise"
     dev_path = np.abs(lp_beh.astype(np.float64) - lp_cur).max(1)
-    off = np.nonzero(dev_path > lp_tol)[0]
     print(f"max |behaviour - recompute| {dev_path.max():.2e} (median rollout "
-          f"{np.median(dev_path):.2e}); rollouts over {lp_tol}: {off.tolist()}", flush=True)
-    if not moe:
-        assert off.size == 0
-    host = oracle.HostModel(mc.oracle_cfg(), host_w, quantized=wl.quantized)
-    del host_w
-    if moe and off.size:
-        # Each such rollout must have a router near-tie at (or just before)
-        # its first token where the two paths disagree: the top-2 expert set
-        # there is decided by less than the paths' rounding differences.
-        assert off.size <= S // 4, f"too many rollouts off: {off.tolist()}"
-        gaps = host.router_gaps(np.concatenate([a["prompts"][off], tok[off, :N - 1]], 1))
-        for i, s in enumerate(off):
-            n0 = int(np.argmax(np.abs(lp_beh[s].astype(np.float64) - lp_cur[s]) > lp_tol))
-            window = gaps[:, i, max(0, P - 1 + n0 - ROUTER_WINDOW):P + n0]
-            print(f"rollout {s}: paths disagree from token {n0}; smallest router gap at and "
-                  f"before it {window.min():.2e}", flush=True)
-            assert window.min() < ROUTER_TIE, f"rollout {s} token {n0}: no router near-tie"
+          f"{np.median(dev_path):.2e})", flush=True)
+    assert dev_path.max() <= lp_tol
     assert (a["flags"] == 0).all()
     stats = a["stats"]
     assert np.isfinite(stats).all()
     assert res["mean_kl_sum"] == 0.0
-    assert res["clipped_fraction_sum"] == 0.0 or moe
+    assert res["clipped_fraction_sum"] == 0.0
 
     # ---- GRPO loss on the full arrays against the f64 oracle
     groups = wl.prompts
@@ -132,33 +109,139 @@ def test_full_workload_rl_step(dev, index):
     np.testing.assert_allclose(adv, expect, rtol=1e-6, atol=1e-9)
 
     # ---- two rollouts at full depth and length against the oracle
+    host = oracle.HostModel(mc.oracle_cfg(), host_w, quantized=wl.quantized)
+    del host_w
     rows = [0, S - 1]
     lp_or, logits_or = host.continuation(a["prompts"][rows], tok[rows])
     err_cur = np.abs(lp_cur[rows] - lp_or).max(1)
     err_beh = np.abs(lp_beh[rows] - lp_or).max(1)
     print(f"oracle rollouts {rows}: max |recompute - oracle| {err_cur.tolist()}, "
           f"|behaviour - oracle| {err_beh.tolist()}", flush=True)
-    # MoE: a rollout may leave the comparison at its first token off the
-    # oracle only at a router near-tie there (as above)
-    upto = [N, N]
-    if moe:
-        gaps = host.router_gaps(np.concatenate([a["prompts"][rows], tok[rows, :N - 1]], 1))
-        for i, s in enumerate(rows):
-            bad = np.nonzero((np.abs(lp_cur[s] - lp_or[i]) > lp_tol) |
-                             (np.abs(lp_beh[s] - lp_or[i]) > lp_tol))[0]
-            if bad.size:
-                n0 = int(bad[0])
-                window = gaps[:, i, max(0, P - 1 + n0 - ROUTER_WINDOW):P + n0]
-                print(f"rollout {s}: off the oracle from token {n0}; smallest router gap at "
-                      f"and before it {window.min():.2e}", flush=True)
-                assert window.min() < ROUTER_TIE, f"rollout {s} token {n0}: no router near-tie"
-                upto[i] = n0
-    else:
-        assert err_cur.max() <= lp_tol and err_beh.max() <= lp_tol
+    assert err_cur.max() <= lp_tol and err_beh.max() <= lp_tol
+    ties = check_sampled_tokens(tok[rows], logits_or, wl.temperature, SEED, rows,
+                                tol=4e-3 if wl.quantized else 1e-4)
+    print(f"sampled tokens: {2 * N} checked, {ties} at near-ties", flush=True)
+
+
+def _margins(logits):
+    """2nd-largest minus 3rd-largest router logit (the top-2 set's margin)."""
+    top3 = np.sort(logits, axis=-1)[..., -3:]
+    return top3[..., 1] - top3[..., 0]
+
+
+@pytest.mark.timeout(600)
+def test_moe_full_workload_rl_step(dev):
+    """Config[4] (16-layer top-2 MoE, 32 experts) at its full workload.
+
+    The decode path, the recompute path and the oracle can each resolve a
+    router near-tie (top-2 set decided by less than their rounding
+    differences, ~1e-4 in router logit) differently, and a flipped expert set
+    changes that token's output outright. The device's router decisions of
+    both paths are therefore traced (``sm_model_trace_routes``):
+    * wherever the two paths pick different top-2 sets, both paths' own
+      margins there must be below ROUTER_TIE;
+    * every token before a rollout's first such flip must agree within 2e-3;
+    * the oracle takes the recompute path's pair wherever its own margin is
+      below ROUTER_TIE and must agree everywhere else; with that, rollouts 0
+      and S-1 must match it within 2e-3 over their whole length (recompute)
+      and up to the first flip (behaviour, sampled tokens)."""
+    wl = RL_WORKLOADS[4]
+    S, P, N, G = wl.rollouts, wl.prompt_len, wl.new_tokens, wl.group
+    L = P + N - 1
+    print(f"case config[4] full workload: S={S} P={P} N={N} layers={wl.model['layers']}",
+          flush=True)
+    mc, (policy, reference), host_w = build_models(wl, dev, seed=wl.index)
+    Lr, E = mc.layers, mc.experts
+    gen = torch.Generator().manual_seed(wl.index)
+    prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
+    rewards = wl.sample_rewards(gen).to(dev)
+    cap = Lr * (S * P + (N - 1) * S)
+    gi, gl = policy.trace_routes(cap)
+    tok, lp_beh = policy.generate(prompts, N, temperature=wl.temperature, seed=SEED)
+    assert policy.route_trace_count() == (cap, 0)
+    gi, gl = gi.cpu().numpy(), gl.cpu().numpy()
+    assert S * L <= 65536  # the recompute runs as one chunk: one trace block per layer
+    ri, rl = policy.trace_routes(Lr * S * L)
+    out = rl_prepare(policy, reference, prompts, tok, lp_beh, rewards, clip_epsilon=CLIP_EPSILON,
+                     advantage_epsilon=ADVANTAGE_EPSILON, kl_coefficient=KL_COEFFICIENT)
+    res = batch_result(out)
+    assert policy.route_trace_count() == (Lr * S * L, 0)
+    policy.stop_trace()
+    ri, rl = ri.cpu().numpy().reshape(Lr, S, L, 2), rl.cpu().numpy().reshape(Lr, S, L, E)
+    # generate trace: prefill [Lr, S, P], then per decode step [Lr, S] (position P + t - 1)
+    pre = Lr * S * P
+    g_ids = np.concatenate([gi[:pre].reshape(Lr, S, P, 2),
+                            gi[pre:].reshape(N - 1, Lr, S, 2).transpose(1, 2, 0, 3)], 2)
+    g_lg = np.concatenate([gl[:pre].reshape(Lr, S, P, E),
+                           gl[pre:].reshape(N - 1, Lr, S, E).transpose(1, 2, 0, 3)], 2)
+    del gi, gl
+    tok, lp_beh = tok.cpu().numpy(), lp_beh.cpu().numpy()
+    lp_cur, lp_ref = out["lp_cur"].cpu().numpy(), out["lp_ref"].cpu().numpy()
+    prompts = prompts.cpu().numpy()
+    del policy, reference
+    torch.cuda.empty_cache()
+
+    assert tok.min() >= 0 and tok.max() < mc.vocab
+    for lp in (lp_beh, lp_cur):
+        assert np.isfinite(lp).all() and (lp <= 0).all()
+    assert np.array_equal(lp_ref, lp_cur)
+    assert (out["flags"].cpu().numpy() == 0).all() and res["mean_kl_sum"] == 0.0
+    st = out["stats"].cpu().numpy()
+    sh = (wl.prompts, G, N)
+    st_or, adv_or, dlp_or, err = oracle.grpo_loss(
+        rewards.cpu().numpy(), lp_cur.reshape(sh), lp_beh.reshape(sh), lp_ref.reshape(sh), None,
+        CLIP_EPSILON, ADVANTAGE_EPSILON, KL_COEFFICIENT)
+    assert err == 0
+    np.testing.assert_allclose(st[:, 0], st_or[:, 0], rtol=1e-4, atol=1e-6)
+    np.testing.assert_allclose(st[:, 1:], st_or[:, 1:], rtol=1e-4, atol=1e-7)
+    np.testing.assert_allclose(out["dlp"].cpu().numpy(), dlp_or.reshape(S, N), rtol=1e-4,
+                               atol=1e-9)
+    assert np.abs(adv_or.sum(1)).max() < 1e-4 * G
+
+    # ---- decode path vs recompute path, through their router decisions. A
+    # flipped pair changes that token's hidden state from that layer on, so its
+    # later layers (and later tokens, through attention) can route differently
+    # by clear margins: only each rollout's first flip, in the first layer
+    # where it shows, must be a near-tie in both paths.
+    flips = (np.sort(g_ids, -1) != np.sort(ri, -1)).any(-1)  # [Lr, S, L]
+    at = flips.any(0)  # [S, L]
+    first = np.where(at.any(1), at.argmax(1), L)
+    mg, mr = _margins(g_lg), _margins(rl)
+    for s in np.nonzero(first < L)[0]:
+        f = int(first[s])
+        lay = int(flips[:, s, f].argmax())
+        print(f"rollout {s}: first flip at position {f} (token {f - (P - 1)}), layer {lay}, "
+              f"margins {mg[lay, s, f]:.1e} / {mr[lay, s, f]:.1e}", flush=True)
+        assert mg[lay, s, f] < ROUTER_TIE and mr[lay, s, f] < ROUTER_TIE, \
+            f"rollout {s} position {f} layer {lay}: a clear router decision flipped"
+    n_lim = np.clip(first - (P - 1), 0, N)  # tokens predicted before the first flip
+    d = np.abs(lp_beh.astype(np.float64) - lp_cur)
+    compared = sum(int(n) for n in n_lim)
+    worst = max(float(d[s, :n_lim[s]].max()) if n_lim[s] else 0.0 for s in range(S))
+    print(f"route flips between the paths: {int(flips.sum())} token-layers in "
+          f"{int(at.any(1).sum())} rollouts; |behaviour - recompute| before the first flip: max "
+          f"{worst:.2e} over {compared}/{S * N} tokens; overall tokens over 2e-3: "
+          f"{int((d > 2e-3).sum())}", flush=True)
+    assert worst <= 2e-3
+    assert compared >= S * N // 2
+
+    # ---- two rollouts against the oracle, which follows the recompute path's
+    # choice where its own top-2 margin is below ROUTER_TIE
+    host = oracle.HostModel(mc.oracle_cfg(), host_w, quantized=True)
+    del host_w
+    rows = [0, S - 1]
+    lp_or, logits_or, conflicts = host.continuation(prompts[rows], tok[rows],
+                                                    route_hint=ri[:, rows], hint_margin=ROUTER_TIE)
+    assert conflicts == 0, f"{conflicts} clear router decisions differ from the oracle's"
+    err_cur = np.abs(lp_cur[rows] - lp_or).max(1)
+    print(f"oracle rollouts {rows}: max |recompute - oracle| {err_cur.tolist()}", flush=True)
+    assert err_cur.max() <= 2e-3
     ties = 0
-    for i in range(2):
-        if upto[i]:
-            ties += check_sampled_tokens(tok[rows[i]:rows[i] + 1, :upto[i]],
-                                         logits_or[i:i + 1, :upto[i]], wl.temperature, SEED,
-                                         [rows[i]], tol=4e-3 if wl.quantized else 1e-4)
-    print(f"sampled tokens: {sum(upto)} checked, {ties} at near-ties", flush=True)
+    for i, s in enumerate(rows):
+        n = int(n_lim[s])
+        if n:
+            assert np.abs(lp_beh[s, :n] - lp_or[i, :n]).max() <= 2e-3
+            ties += check_sampled_tokens(tok[s:s + 1, :n], logits_or[i:i + 1, :n], wl.temperature,
+                                         SEED, [s], tol=4e-3)
+    print(f"behaviour / sampled tokens checked before the first flip: {n_lim[rows].tolist()}, "
+          f"{ties} at near-ties", flush=True)
