@@ -2,20 +2,30 @@
 """Benchmark of the GRPO RL-step hot path on one MI355X.
 
 Prints ONE JSON line (the driver's contract). Workloads:
-  rl_step    config[1] (default): 12-layer d768 Q4G128 decoder, 16 prompts x 8
-             rollouts, 128-token prompts, 256 sampled tokens at T=1.0, then the
-             log-prob recompute of policy + frozen reference and the GRPO loss.
-             value = rollout tok/s; ms_per_step = whole RL step.
-  ce_stress  config[3]: fused log-softmax/CE/token-logprob over bf16
-             [65536 x 131072] logits (HBM-bound).
-Timing: W warmup steps, then K timed steps bracketed by synchronisation; kernel
-durations come from HIP events recorded on the stream the kernels run on.
+  rl_step         (default) one GRPO step of a BASELINE config (--config, default
+                  2: the 24-layer d2048 GQA Q4G128 decoder, 32 prompts x 8
+                  rollouts, 512-token prompts, 512 sampled tokens at T = 1, then
+                  the log-prob recompute of the policy and its frozen copy over
+                  all 1023 positions and the GRPO loss). value = rollout tok/s
+                  (S * N / rollout time); ms_per_step = the whole RL step.
+                  Sub-results: decode HBM fraction, recompute MFMA fraction,
+                  the dominant kernel's roofline, the config[3] fused CE, the
+                  whole-model Q4 GEMV sweep at M = 1, 2, 4, 8, 16, config[0].
+  ce_stress       config[3]: fused log-softmax/CE/token-logprob over bf16
+                  [65536 x 131072] logits (lp + loss, and grad in place).
+  q4_gemv         the whole-model M = 1 Q4 GEMV sweep (config[2] weights).
+  recompute_gemm  the dominant kernel alone: the config[2] recompute FFN-in
+                  GEMM (wide-tile kernel), for counter runs.
+Timing: W warmup steps, then K timed steps bracketed by synchronisation; GPU
+durations come from HIP events recorded on the stream the work runs on.
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import platform
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -23,132 +33,137 @@ from pathlib import Path
 ROOT = Path(__file__).resolve().parent
 sys.path.insert(0, str(ROOT))
 
-HBM_PEAK_GBS = 8000.0
-
-
-def measured_gemv_traffic():
-    """HBM bytes per launch of the LM-head GEMV from the committed rocprofv3
-    --pmc summary (FETCH_SIZE / WRITE_SIZE, copy-calibrated), or None."""
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "q4_gemv_lm_head_traffic.md")
-    try:
-        for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":")[1])
-    except OSError:
-        return None
-    return None
+HBM_PEAK_GBS = 8000.0        # MI355X HBM3E
+MFMA_F16_PEAK_TFS = 2500.0   # MI355X dense f16 / bf16 MFMA
 
 
 def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
-def cpu_baseline_ce(rows: int, vocab: int, seconds: float = 10.0) -> dict:
-    """Oracle (f64 two-pass C port, all host threads) on a bounded sample of config[3] rows."""
-    import numpy as np
-
-    import oracle
-
-    rng = np.random.default_rng(0)
-    sample_rows = 256
-    x = oracle.bf16_bits(rng.normal(0, 3, (sample_rows, vocab)).astype(np.float32))
-    t = rng.integers(0, vocab, sample_rows).astype(np.int32)
-    oracle.ce_rows(x[:8], t[:8])
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds:
-        oracle.ce_rows(x, t)
-        n += 1
-    dt = (time.perf_counter() - t0) / n
-    gbs = sample_rows * vocab * 2 / dt / 1e9
-    return {"value": round(gbs, 3), "unit": "GB/s", "cores": os.cpu_count(), "kind": "port",
-            "sample": f"{sample_rows} rows x {vocab} bf16, lp only, {n} reps"}
+def profile_figure(name: str, key: str):
+    """An integer figure (``key: value`` line) from a committed profiles/ summary."""
+    try:
+        for line in open(ROOT / "profiles" / name):
+            if line.startswith(key + ":"):
+                return int(line.split(":")[1])
+    except OSError:
+        return None
+    return None
 
 
-def bench_ce_stress(args) -> dict:
+def _events(n):
     import torch
+    return [torch.cuda.Event(enable_timing=True) for _ in range(n)]
 
-    from summa_amd import ops
 
-    rows, vocab = args.rows, 131072
-    dev = torch.device("cuda:0")
-    x = torch.empty(rows, vocab, dtype=torch.bfloat16, device=dev)
-    t = torch.empty(rows, dtype=torch.int32, device=dev)
-    ops.fill_ce_stress(x, t, 3.0, 8.0, seed=0)
-    torch.cuda.synchronize()
-    for _ in range(args.warmup):
-        ops.ce_rows(x, t)
-    torch.cuda.synchronize()
+def _time_launches(fn, reps: int) -> float:
+    """Average GPU ms per call of ``fn`` (events on the current stream)."""
+    import torch
     st = torch.cuda.current_stream()
-    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-           for _ in range(args.steps)]
-    t0 = time.perf_counter()
-    for a, b in evs:
-        a.record(st)
-        ops.ce_rows(x, t)
-        b.record(st)
+    fn()
     torch.cuda.synchronize()
-    wall = time.perf_counter() - t0
-    kms = sum(a.elapsed_time(b) for a, b in evs) / len(evs)
-    algo_bytes = rows * vocab * 2 + rows * 8
-    achieved = algo_bytes / (kms * 1e-3) / 1e9
-    res = {
-        "metric": "fused CE/log-prob rows/s (config[3] bf16 65536x131072)",
-        "value": rows / (wall / args.steps), "unit": "rows/s",
-        "ms_per_step": wall / args.steps * 1e3, "dtype": "bf16",
-        "config": {"workload": "ce_stress", "rows": rows, "vocab": vocab, "outputs": "lp+loss"},
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None},
-    }
-    # grad-in-place variant (1 read + 1 write)
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a, b = _events(2)
     a.record(st)
-    ops.ce_rows(x, t, grad_in_place=True, grad_scale=1.0 / rows)
+    for _ in range(reps):
+        fn()
     b.record(st)
     torch.cuda.synchronize()
-    gms = a.elapsed_time(b)
-    res["grad_in_place"] = {"ms": round(gms, 4),
-                            "GB/s": round(2 * rows * vocab * 2 / (gms * 1e-3) / 1e9, 1)}
-    return res
+    return a.elapsed_time(b) / reps
 
 
-CFG1 = dict(layers=12, d_model=768, heads=12, kv_heads=12, head_dim=64, ffn=3072, vocab=32768)
+# --------------------------------------------------------------- analysis ---
+
+def linear_shapes(m: dict) -> list:
+    """(N, K) of every per-layer linear of a dense model (out x in)."""
+    d, qn = m["d_model"], (m["heads"] + 2 * m["kv_heads"]) * m["head_dim"]
+    return [(qn, d), (d, m["heads"] * m["head_dim"]), (2 * m["ffn"], d), (d, m["ffn"])]
 
 
-CFG2 = dict(layers=24, d_model=2048, heads=16, kv_heads=4, head_dim=128, ffn=5632, vocab=65536)
+def q4_bytes(n: int, k: int) -> int:
+    return n * k // 2 + n * k // 128 * 2  # 4-bit codes + one bf16 scale per 128
 
 
-# config[4]: attention geometry is not specified by the config; H16 = KVH16,
-# head_dim 128 (d_model / heads). The dense FFN width is unused (all layers MoE).
-CFG4 = dict(layers=16, d_model=2048, heads=16, kv_heads=16, head_dim=128, ffn=1408, vocab=65536,
-            experts=32, expert_ffn=1408)
+def recompute_flops(wl) -> float:
+    """Algorithmic flops of one model's log-prob recompute over S x (P + N - 1)
+    positions: 2 * tokens * per-layer linear params, the LM head over the S * N
+    scored rows, causal attention (Q.K^T and P.V over the lower triangle)."""
+    m = wl.model
+    L = wl.prompt_len + wl.new_tokens - 1
+    tokens = wl.rollouts * L
+    lin = sum(n * k for n, k in linear_shapes(m)) * m["layers"]
+    head = m["vocab"] * m["d_model"]
+    attn = 4 * m["head_dim"] * (L * (L + 1) / 2) * m["heads"] * wl.rollouts * m["layers"]
+    return 2.0 * tokens * lin + 2.0 * wl.rollouts * wl.new_tokens * head + attn
 
-# (model, prompts, group, prompt_len, new_tokens, reward sampler)
-RL_CONFIGS = {
-    1: (CFG1, 16, 8, 128, 256, "bernoulli0.3"),
-    2: (CFG2, 32, 8, 512, 512, "uniform"),
-    4: (CFG4, 16, 8, 256, 256, "bernoulli0.3"),
-}
+
+def decode_bytes(wl) -> float:
+    """Algorithmic HBM bytes of the N - 1 cached decode steps: every packed
+    weight once per step plus each sequence's K/V cache (f16) read once per
+    KV head per layer at its context length P + t."""
+    m = wl.model
+    S, P, N = wl.rollouts, wl.prompt_len, wl.new_tokens
+    w = sum(q4_bytes(n, k) for n, k in linear_shapes(m)) * m["layers"]
+    w += q4_bytes(m["vocab"], m["d_model"])
+    kv_tok = m["layers"] * S * m["kv_heads"] * m["head_dim"] * 2 * 2
+    ctx = sum(P + t for t in range(1, N))
+    return (N - 1) * w + kv_tok * ctx
 
 
-def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 10) -> dict:
-    """M=1 Q4G128 GEMV over every linear of a model (whole-model weight sweep).
+# --------------------------------------------------------------- kernels ---
 
-    All launches are captured once in a HIP graph and replayed, so the timing is
-    GPU time, not Python launch overhead; HIP events on the capture/replay
-    stream. The config[2] sweep (~627 MB of packed weights) exceeds the 256 MB
-    MALL, so every matrix streams from HBM. Algorithmic bytes per launch =
-    N*K*(0.5 + 2/128) + K*2 (x) + N*4 (y)."""
+def recompute_gemm(wl, dev, reps: int = 10) -> dict:
+    """The dominant kernel of the config[2] step: the FFN-in projection of the
+    log-prob recompute (SwiGLU f16-pair epilogue) at its chunk shape
+    M = 64 rollouts x 1023 positions, N = 2F = 11264, K = 2048, on the
+    wide-tile kernel. flops = 2 M N K per launch."""
+    import torch
+
+    from summa_amd import _lib, ops
+
+    m = wl.model
+    L = wl.prompt_len + wl.new_tokens - 1
+    M = max(1, 65536 // L) * L
+    N, K = 2 * m["ffn"], m["d_model"]
+    w = torch.empty(N, K, device=dev)
+    ops.fill_normal(w, 0.0, 0.02, seed=5)
+    qw = ops.Q4Weight.quantize(w)
+    qw.drop_rowmajor()
+    del w
+    x = torch.empty(M, K, device=dev)
+    ops.fill_normal(x, 0.0, 1.0, seed=6)
+    xp = ops.f16_pair(x)
+    del x
+    out = torch.empty(M, 2 * (N // 2), dtype=torch.float16, device=dev)
+
+    def run():
+        ops.q4_matmul(qw, xp, out=out, epilogue=_lib.SM_EPI_SWIGLU_F16X2, pair=True)
+
+    ms = _time_launches(run, reps)
+    flops = 2.0 * M * N * K
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"kernel": "q4_gemm_wide_kernel<2,5> (recompute FFN-in, SwiGLU f16-pair epilogue)",
+            "shape": [M, N, K], "us": round(ms * 1e3, 2), "flops": flops,
+            "TFLOPs": round(achieved, 1), "frac": round(achieved / MFMA_F16_PEAK_TFS, 4)}
+
+
+def q4_gemv_sweep(model_cfg: dict, dev, ms=(1, 2, 4, 8, 16), reps: int = 10) -> dict:
+    """Q4G128 GEMV over every linear of a model (whole-model weight sweep), at
+    M = 1, 2, 4, 8, 16 activation rows (f16).
+
+    All launches of one M are captured in a HIP graph and replayed, so the
+    time is GPU time, not Python launch overhead (HIP events on the replay
+    stream). The config[2] sweep (~627 MB of packed weights) exceeds the
+    256 MB MALL, so every matrix streams from HBM. Algorithmic bytes per
+    launch = N*K*(0.5 + 2/128) + M*K*2 (x) + M*N*4 (y, f32)."""
     import torch
 
     from summa_amd import ops
 
-    d, F, V = model_cfg["d_model"], model_cfg["ffn"], model_cfg["vocab"]
-    qn = (model_cfg["heads"] + 2 * model_cfg["kv_heads"]) * model_cfg["head_dim"]
-    shapes = [(qn, d), (d, model_cfg["heads"] * model_cfg["head_dim"]), (2 * F, d), (d, F)]
+    d, V = model_cfg["d_model"], model_cfg["vocab"]
     mats = []
     for layer in range(model_cfg["layers"]):
-        for n, k in shapes:
+        for n, k in linear_shapes(model_cfg):
             w = torch.empty(n, k, device=dev)
             ops.fill_normal(w, 0.0, 0.02, seed=layer * 10 + n)
             mats.append(ops.Q4Weight.quantize(w))
@@ -157,30 +172,37 @@ def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 10) -> dict:
     w = torch.empty(V, d, device=dev)
     ops.fill_normal(w, 0.0, 0.02, seed=99)
     mats.append(ops.Q4Weight.quantize(w))
+    mats[-1].drop_rowmajor()
     del w
     kmax = max(m.k for m in mats)
-    x = torch.randn(1, kmax, device=dev).to(torch.float16)  # model activations are f16
-    xs = [x[:, :m.k].contiguous() for m in mats]
-    ys = [torch.empty(1, m.n, device=dev) for m in mats]
-    torch.cuda.synchronize()
-    for m, xi, y in zip(mats, xs, ys):  # warm (module load, first launch)
-        ops.q4_matmul(m, xi, out=y)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for m, xi, y in zip(mats, xs, ys):
-            ops.q4_matmul(m, xi, out=y)
-    graph.replay()
-    torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    a.record(st)
-    for _ in range(reps):
+    res = {"model": f"{model_cfg['layers']}L d{d} F{model_cfg['ffn']} V{V}",
+           "launches": len(mats), "weight_bytes": sum(m.nbytes for m in mats), "by_M": {}}
+    for M in ms:
+        x = torch.randn(M, kmax, device=dev).to(torch.float16)
+        xs = [x[:, :m.k].contiguous() for m in mats]
+        ys = [torch.empty(M, m.n, device=dev) for m in mats]
+        for m, xi, y in zip(mats, xs, ys):  # warm (module load, first launch)
+            ops.q4_matmul(m, xi, out=y)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for m, xi, y in zip(mats, xs, ys):
+                ops.q4_matmul(m, xi, out=y)
         graph.replay()
-    b.record(st)
-    torch.cuda.synchronize()
-    sweep_ms = a.elapsed_time(b) / reps
-    nbytes = sum(m.nbytes + m.k * 2 + m.n * 4 for m in mats)
+        torch.cuda.synchronize()
+        a, b = _events(2)
+        a.record(st)
+        for _ in range(reps):
+            graph.replay()
+        b.record(st)
+        torch.cuda.synchronize()
+        sweep_ms = a.elapsed_time(b) / reps
+        nbytes = sum(m.nbytes + M * m.k * 2 + M * m.n * 4 for m in mats)
+        gbs = nbytes / sweep_ms / 1e6
+        res["by_M"][str(M)] = {"sweep_ms": round(sweep_ms, 4), "bytes": nbytes,
+                               "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        del graph, xs, ys, x
     # The largest GEMV (LM head) sustained: 4 distinct copies (> 256 MB MALL)
     # replayed back to back, so each launch streams its matrix from HBM.
     heads = [mats[-1]]
@@ -190,15 +212,17 @@ def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 10) -> dict:
         heads.append(ops.Q4Weight.quantize(w))
         heads[-1].drop_rowmajor()
         del w
+    xh = torch.randn(1, d, device=dev).to(torch.float16)
     y_head = torch.empty(1, V, device=dev)
     torch.cuda.synchronize()
     g2 = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g2):
         for _ in range(2):
             for m in heads:
-                ops.q4_matmul(m, xs[-1], out=y_head)
+                ops.q4_matmul(m, xh, out=y_head)
     g2.replay()
     torch.cuda.synchronize()
+    a, b = _events(2)
     a.record(st)
     for _ in range(reps):
         g2.replay()
@@ -206,139 +230,395 @@ def q4_gemv_sweep(model_cfg: dict, dev, reps: int = 10) -> dict:
     torch.cuda.synchronize()
     head_us = a.elapsed_time(b) * 1e3 / (reps * 8)
     head_bytes = heads[0].nbytes + d * 2 + V * 4
-    return {"sweep_ms": sweep_ms, "sweep_bytes": nbytes, "sweep_GBs": nbytes / sweep_ms / 1e6,
-            "launches": len(mats), "avg_launch_us": sweep_ms * 1e3 / len(mats),
-            "model": f"{model_cfg['layers']}L d{d} F{F} V{V}",
-            "lm_head_shape": [V, d], "lm_head_us": head_us, "lm_head_bytes": head_bytes,
-            "lm_head_GBs": head_bytes / head_us / 1e3}
+    res.update(lm_head_shape=[V, d], lm_head_us=round(head_us, 3), lm_head_bytes=head_bytes,
+               lm_head_GBs=round(head_bytes / head_us / 1e3, 1))
+    return res
 
 
-def cpu_baseline_rl(config: int) -> dict:
-    """Oracle (C restatement, OpenMP over the host cores) rollout on a bounded
-    sample of the workload: 2 rollouts x (full-length prompt + 8 sampled tokens)
-    for config[1], 1 x (prompt + 2) for the larger configs."""
-    import numpy as np
-
-    import oracle
-
-    mcfg, _, _, P, _, _ = RL_CONFIGS[config]
-    cfg = {"layers": mcfg["layers"], "d": mcfg["d_model"], "H": mcfg["heads"],
-           "KVH": mcfg["kv_heads"], "hd": mcfg["head_dim"], "F": mcfg["ffn"], "V": mcfg["vocab"]}
-    if mcfg.get("experts"):
-        cfg.update(E=mcfg["experts"], Fe=mcfg["expert_ffn"])
-    w = oracle.random_weights(cfg, seed=0, std=0.02)
-    host = oracle.HostModel(cfg, w, quantized=True)
-    del w
-    S, N = (2, 8) if config == 1 else (1, 2)
-    prompts = np.random.default_rng(0).integers(0, cfg["V"], (S, P)).astype(np.int32)
-    t0 = time.perf_counter()
-    host.generate(prompts, N, 1.0, 0)
-    dt = time.perf_counter() - t0
-    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count()))
-    return {"value": round(S * N / dt, 4), "unit": "rollout tok/s", "cores": threads,
-            "kind": "port",
-            "sample": f"config[{config}] Q4 model, {S} rollouts x ({P}-token prompt + {N} "
-                      f"sampled), {dt:.1f} s (prefill included, as in the rollout)"}
-
-
-def bench_rl_step(args) -> dict:
+def ce_stress(dev, rows: int, reps: int = 5) -> dict:
+    """config[3]: fused log-softmax / CE / token log-prob over bf16
+    [rows, 131072] logits ~ N(0, 3) with a +8 spike at the target. lp + loss
+    read the logits once (algorithmic bytes rows * V * 2); grad in place reads
+    and writes them once (2 * rows * V * 2)."""
     import torch
 
-    from summa_amd.model import Model, ModelConfig, batch_result, rl_prepare
+    from summa_amd import ops
+    from summa_amd.configs import CE_STRESS
 
-    mcfg, groups, G, P, N, reward_kind = RL_CONFIGS[args.config]
-    S = groups * G
-    dev = torch.device("cuda:0")
-    mc = ModelConfig(**mcfg, max_seq=P + N, quantized=True)
-    policy = Model(mc)
-    policy.init_random(seed=0, std=0.02)
-    reference = Model(mc)
-    reference.init_random(seed=0, std=0.02)  # frozen copy of the initial policy
-    gen = torch.Generator().manual_seed(0)
-    prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
-    if reward_kind == "uniform":
-        rewards = torch.rand((groups, G), generator=gen).to(dev)
-    else:
-        rewards = torch.bernoulli(torch.full((groups, G), 0.3), generator=gen).to(dev)
+    vocab = CE_STRESS["vocab"]
+    x = torch.empty(rows, vocab, dtype=torch.bfloat16, device=dev)
+    t = torch.empty(rows, dtype=torch.int32, device=dev)
+    ops.fill_ce_stress(x, t, CE_STRESS["std"], CE_STRESS["spike"], seed=0)
     torch.cuda.synchronize()
+    lp_ms = _time_launches(lambda: ops.ce_rows(x, t), reps)
+    g_ms = _time_launches(lambda: ops.ce_rows(x, t, grad_in_place=True, grad_scale=1.0 / rows),
+                          reps)
+    rb = rows * vocab * 2
+    del x, t
+    torch.cuda.empty_cache()
+    return {"shape": [rows, vocab], "dtype": "bf16",
+            "lp_loss": {"ms": round(lp_ms, 4), "bytes": rb,
+                        "GBs": round(rb / lp_ms / 1e6, 1),
+                        "frac": round(rb / lp_ms / 1e6 / HBM_PEAK_GBS, 4)},
+            "grad_in_place": {"ms": round(g_ms, 4), "bytes": 2 * rb,
+                              "GBs": round(2 * rb / g_ms / 1e6, 1),
+                              "frac": round(2 * rb / g_ms / 1e6 / HBM_PEAK_GBS, 4)}}
+
+
+# ---------------------------------------------------------------- RL step ---
+
+def rl_inputs(wl, mc, dev):
+    import torch
+    gen = torch.Generator().manual_seed(0)
+    prompts = torch.randint(0, mc.vocab, (wl.rollouts, wl.prompt_len), generator=gen,
+                            dtype=torch.int32).to(dev)
+    rewards = wl.sample_rewards(gen).to(dev)
+    return prompts, rewards
+
+
+def run_rl_step(wl, policy, reference, prompts, rewards, steps, warmup, tag=""):
+    """W + K GRPO steps; returns per-step rollout / prepare / step ms (events)
+    and the last step's outputs."""
+    import torch
+
+    from summa_amd.configs import ADVANTAGE_EPSILON, CLIP_EPSILON, KL_COEFFICIENT
+    from summa_amd.model import rl_prepare
+
     st = torch.cuda.current_stream()
+    e0, e_mid, e1 = _events(3)
 
     def step(seed):
-        tok, lp_beh = policy.generate(prompts, N, temperature=1.0, seed=seed)
+        tok, lp_beh = policy.generate(prompts, wl.new_tokens, temperature=wl.temperature,
+                                      seed=seed)
         e_mid.record(st)
-        out = rl_prepare(policy, reference, prompts, tok, lp_beh, rewards, clip_epsilon=0.2,
-                         advantage_epsilon=1e-6, kl_coefficient=0.04)
+        out = rl_prepare(policy, reference, prompts, tok, lp_beh, rewards,
+                         clip_epsilon=CLIP_EPSILON, advantage_epsilon=ADVANTAGE_EPSILON,
+                         kl_coefficient=KL_COEFFICIENT)
+        out["tokens"], out["lp_beh"] = tok, lp_beh
         return out
 
-    e0, e_mid, e1 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-    log("bench: warmup")
-    for i in range(args.warmup):
+    for i in range(warmup):
         step(1000 + i)
     torch.cuda.synchronize()
-    roll_ms, step_ms = [], []
+    roll, full = [], []
     t0 = time.perf_counter()
-    for i in range(args.steps):
+    for i in range(steps):
         e0.record(st)
         out = step(i)
         e1.record(st)
         torch.cuda.synchronize()
-        roll_ms.append(e0.elapsed_time(e_mid))
-        step_ms.append(e0.elapsed_time(e1))
-        log(f"bench: step {i} rollout {roll_ms[-1]:.1f} ms, RL step {step_ms[-1]:.1f} ms")
+        roll.append(e0.elapsed_time(e_mid))
+        full.append(e0.elapsed_time(e1))
+        if tag:
+            log(f"bench: {tag} step {i} rollout {roll[-1]:.1f} ms, RL step {full[-1]:.1f} ms")
     wall = time.perf_counter() - t0
+    return roll, full, wall, out
+
+
+def prefill_ms(wl, policy, prompts, reps: int = 3) -> float:
+    """The rollout's prefill (plus its first sample): generate with N = 1."""
+    return _time_launches(lambda: policy.generate(prompts, 1, temperature=wl.temperature,
+                                                  seed=3), reps)
+
+
+def config0_leg(dev, steps: int = 5) -> dict:
+    """config[0] (2-layer fp32 decoder, 32 rollouts, greedy): the latency leg
+    (median of ``steps`` RL steps after 2 warm-up steps)."""
+    from summa_amd.configs import RL_WORKLOADS
+    from summa_amd.model import Model
+    wl = RL_WORKLOADS[0]
+    mc = wl.model_config()
+    policy, reference = Model(mc), Model(mc)
+    w = draw_weights(wl, [policy, reference], dev, seed=1)
+    prompts, rewards = rl_inputs(wl, mc, dev)
+    roll, full, _, out = run_rl_step(wl, policy, reference, prompts, rewards, steps, 2)
+    r, f = statistics.median(roll), statistics.median(full)
+    return {"rl_step_ms": round(f, 3), "rollout_ms": round(r, 3),
+            "rollout_tok_s": round(wl.rollouts * wl.new_tokens / (r * 1e-3), 1),
+            "prepare_ms": round(f - r, 3), "steps": steps,
+            "_out": out, "_prompts": prompts, "_weights": w}
+
+
+# -------------------------------------------------------------- baseline ---
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline_rl(wl, host_weights, c0=None) -> dict:
+    """The C oracle (the reference CPU path restated: fp32, batch 1 per
+    rollout, generate.rs:68-124) on the GPU box's host cores, on a bounded
+    sample of the workload: one rollout, a 64-token prompt prefilled untimed,
+    then cached decode steps (rollout tok/s = 1 / time per step, the rate of
+    the reference's per-rollout loop); warm-up, then the median of 5 reps, at
+    1 thread and at every core. Plus the GRPO loss over the full [S, N]
+    arrays, and config[0]'s full RL step with its oracle parity verdict."""
+    import numpy as np
+
+    import oracle
+    from summa_amd.configs import ADVANTAGE_EPSILON, CLIP_EPSILON, KL_COEFFICIENT
+
+    cfg = wl.model_config().oracle_cfg()
+    host = oracle.HostModel(cfg, host_weights, quantized=wl.quantized)
+    prompt = np.random.default_rng(0).integers(0, cfg["V"], 64).astype(np.int32)
+    out = {}
+    for label, threads in (("1_thread", 1), ("all_threads", 0)):
+        n = oracle.set_threads(threads)
+        per_rep = 1 if threads == 1 else 2
+        stamps = []
+        host.decode_steps(prompt, 1 + 5 * per_rep, wl.temperature, 0,
+                          on_step=lambda i: stamps.append(time.perf_counter()))
+        stamps.append(time.perf_counter())
+        # stamps[i] .. stamps[i + 1] is decode step i; step 0 is the warm-up
+        reps = [(stamps[1 + r * per_rep + per_rep] - stamps[1 + r * per_rep]) / per_rep
+                for r in range(5)]
+        med = statistics.median(reps)
+        out[label] = {"threads": n, "s_per_token": round(med, 4),
+                      "rollout_tok_s": round(1.0 / med, 4)}
+    oracle.set_threads(0)
+    # GRPO loss over the whole batch's [S, N] arrays (f64 oracle)
+    rng = np.random.default_rng(1)
+    sh = (wl.prompts, wl.group, wl.new_tokens)
+    cur = rng.normal(-5, 1, sh)
+    beh = cur + rng.normal(0, 1e-3, sh)
+    t0 = time.perf_counter()
+    for _ in range(5):
+        oracle.grpo_loss(rng.random(sh[:2]), cur, beh, cur, None, CLIP_EPSILON,
+                         ADVANTAGE_EPSILON, KL_COEFFICIENT)
+    out["grpo_loss_ms"] = round((time.perf_counter() - t0) / 5 * 1e3, 3)
+    res = {"value": out["all_threads"]["rollout_tok_s"], "unit": "rollout tok/s",
+           "cores": out["all_threads"]["threads"], "kind": "port",
+           "sample": (f"config[{wl.index}] Q4 model, 1 rollout: 64-token prompt prefilled "
+                      f"untimed, then median of 5 reps of cached decode steps (1 thread: 1 "
+                      f"step per rep, all threads: 2); GRPO loss over the full "
+                      f"{list(sh)} arrays"),
+           "cpu_model": _cpu_model(), "nproc": os.cpu_count(), **out}
+    if c0 is not None:
+        res["config0"] = c0
+    return res
+
+
+def cpu_config0(c0_gpu) -> dict:
+    """config[0] on the oracle at every core: the full RL step's rollouts and
+    recompute (median of 3), and the GPU's log-probs against it (1e-5)."""
+    import numpy as np
+
+    import oracle
+    from summa_amd.configs import RL_WORKLOADS
+
+    wl = RL_WORKLOADS[0]
+    mc = wl.model_config()
+    weights = _model_host_weights(c0_gpu["_weights"])
+    host = oracle.HostModel(mc.oracle_cfg(), weights, quantized=False)
+    prompts = c0_gpu["_prompts"].cpu().numpy()
+    times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        tok, _ = host.generate(prompts, wl.new_tokens, 0.0, 0)
+        lp = host.logprobs(prompts, tok)
+        times.append(time.perf_counter() - t0)
+    out = c0_gpu["_out"]
+    gtok = out["tokens"].cpu().numpy()
+    lp_or = host.logprobs(prompts, gtok)
+    err_cur = float(np.abs(out["lp_cur"].cpu().numpy() - lp_or).max())
+    err_beh = float(np.abs(out["lp_beh"].cpu().numpy() - lp_or).max())
+    same = float((gtok == tok).mean())
+    return {"cpu_rl_step_ms": round(statistics.median(times) * 1e3, 1),
+            "parity": {"max_abs_lp_recompute": err_cur, "max_abs_lp_behaviour": err_beh,
+                       "tolerance": 1e-5, "greedy_tokens_equal": same,
+                       "verdict": "pass" if max(err_cur, err_beh) <= 1e-5 else "fail"}}
+
+
+def _model_host_weights(dev_weights: dict) -> dict:
+    return {k: v.cpu().numpy() for k, v in dev_weights.items()}
+
+
+def draw_weights(wl, models, dev, seed: int = 0) -> dict:
+    """Seeded N(0, 0.02) weights drawn on the device and installed into every
+    model of ``models``; returns the device tensors (for the CPU baseline)."""
+    import torch
+
+    from summa_amd import ops
+
+    mc = wl.model_config()
+    Lr, d = mc.layers, mc.d_model
+    out = {"attn_norm": torch.ones(Lr, d, device=dev), "ffn_norm": torch.ones(Lr, d, device=dev),
+           "final_norm": torch.ones(d, device=dev)}
+    n = [0]
+
+    def draw(shape, sd=0.02):
+        t = torch.empty(shape, device=dev)
+        n[0] += 1
+        ops.fill_normal(t, 0.0, sd, seed=seed * 1000003 + n[0])
+        return t
+
+    out["embed"], out["lm_head"] = draw((mc.vocab, d)), draw((mc.vocab, d))
+    shapes = dict(zip(("qkv", "o", "in", "down"), linear_shapes(wl.model)))
+    if mc.experts:
+        del shapes["in"], shapes["down"]
+        shapes.update(exp_in=(mc.experts, 2 * mc.expert_ffn, d),
+                      exp_down=(mc.experts, d, mc.expert_ffn), router=(mc.experts, d))
+    for k, shp in shapes.items():
+        out[k] = draw((Lr, *shp), 1.0 / d ** 0.5 if k == "router" else 0.02)
+    per_layer = ("attn_norm", "ffn_norm", "qkv", "o", "in", "down", "router", "exp_in",
+                 "exp_down")
+    for m in models:
+        for k, t in out.items():
+            if k in per_layer:
+                for layer in range(Lr):
+                    m.set_tensor(k, t[layer], layer)
+            else:
+                m.set_tensor(k, t)
+    torch.cuda.synchronize()
+    return out
+
+
+# ------------------------------------------------------------- workloads ---
+
+def bench_rl_step(args) -> dict:
+    import torch
+
+    from summa_amd.configs import CE_STRESS, RL_WORKLOADS
+    from summa_amd.model import Model, batch_result
+
+    wl = RL_WORKLOADS[args.config]
+    dev = torch.device("cuda:0")
+    mc = wl.model_config()
+    policy, reference = Model(mc), Model(mc)
+    dweights = draw_weights(wl, [policy, reference], dev)  # the frozen copy equals the policy
+    prompts, rewards = rl_inputs(wl, mc, dev)
+    S, N = wl.rollouts, wl.new_tokens
+    log("bench: warmup")
+    roll, full, wall, out = run_rl_step(wl, policy, reference, prompts, rewards, args.steps,
+                                        args.warmup, tag=f"config[{wl.index}]")
     res = batch_result(out)
-    roll = sum(roll_ms) / len(roll_ms)
-    full = sum(step_ms) / len(step_ms)
+    lp_gap = float((out["lp_beh"] - out["lp_cur"]).abs().max())
+    r_ms, f_ms = sum(roll) / len(roll), sum(full) / len(full)
+    pre_ms = prefill_ms(wl, policy, prompts)
+    dec_ms = r_ms - pre_ms
+    dec_bytes = decode_bytes(wl)
+    rec_flops = 2 * recompute_flops(wl)  # policy + frozen reference
+    prep_ms = f_ms - r_ms
+    line = {
+        "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
+        "value": S * N / (r_ms * 1e-3), "unit": "rollout tok/s", "ms_per_step": f_ms,
+        "dtype": ("q4g128 weights, f16-pair (fp32-grade) matmul inputs, f16 KV, f32 accumulate"
+                  if wl.quantized else "f32"),
+        "config": {"workload": f"rl_step config[{wl.index}]", **wl.model, "prompts": wl.prompts,
+                   "group": wl.group, "prompt_len": wl.prompt_len, "new_tokens": N,
+                   "temperature": wl.temperature,
+                   "weights": "Q4G128 (bf16 scales)" if wl.quantized else "f32",
+                   "rewards": wl.reward_label()},
+        "rl_step_ms": round(f_ms, 3), "rollout_ms": round(r_ms, 3), "prepare_ms": round(prep_ms, 3),
+        "wall_s": round(wall, 3),
+        "grpo": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()},
+        "check": {"max_abs_lp_behaviour_minus_recompute": lp_gap},
+        "phases": {
+            "prefill_ms": round(pre_ms, 3),
+            "decode": {"ms": round(dec_ms, 3), "steps": N - 1,
+                       "us_per_step": round(dec_ms * 1e3 / (N - 1), 1),
+                       "algorithmic_bytes": dec_bytes,
+                       "floor_ms": round(dec_bytes / HBM_PEAK_GBS / 1e6, 3),
+                       "hbm_frac": round(dec_bytes / HBM_PEAK_GBS / 1e6 / dec_ms, 4)},
+            "recompute_and_loss": {"ms": round(prep_ms, 3), "algorithmic_flops": rec_flops,
+                                   "TFLOPs": round(rec_flops / (prep_ms * 1e-3) / 1e12, 1),
+                                   "mfma_frac": round(rec_flops / (prep_ms * 1e-3) / 1e12
+                                                      / MFMA_F16_PEAK_TFS, 4)}},
+    }
     del policy, reference
     torch.cuda.empty_cache()
-    log("bench: q4 gemv sweep (config[2] weights, graph replay)")
-    sweep = q4_gemv_sweep(CFG2, dev)
-    achieved = sweep["lm_head_GBs"]
-    return {
-        "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
-        "value": S * N / (roll * 1e-3), "unit": "rollout tok/s",
-        "ms_per_step": full, "dtype": "q4g128 weights, f16-pair (fp32-grade) matmul inputs, f16 KV, f32 accumulate",
-        "config": {"workload": f"rl_step config[{args.config}]", **mcfg, "prompts": groups,
-                   "group": G, "prompt_len": P, "new_tokens": N, "temperature": 1.0,
-                   "weights": "Q4G128 (bf16 scales)",
-                   "rewards": "U[0,1]" if reward_kind == "uniform" else "Bernoulli(0.3)"},
-        "rl_step_ms": round(full, 3), "rollout_ms": round(roll, 3),
-        "prepare_ms": round(full - roll, 3), "wall_s": round(wall, 3),
-        "grpo": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()},
-        "roofline": {"bound": "hbm",
-                     "kernel": "q4g128 GEMV M=1, config[2] LM head 65536x2048 (4 copies > MALL, "
-                               "graph replay); whole-model sweep in q4_gemv",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_gemv_traffic()},
-        "q4_gemv": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sweep.items()},
-    }
+    log("bench: dominant kernel (recompute FFN-in GEMM)")
+    k = recompute_gemm(RL_WORKLOADS[2], dev)
+    line["roofline"] = {"bound": "mfma", "kernel": k["kernel"], "shape": k["shape"],
+                        "achieved": k["TFLOPs"], "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s",
+                        "frac": k["frac"], "us": k["us"],
+                        "traffic": profile_figure("recompute_gemm_ffn_in_traffic.md",
+                                                  "traffic_bytes_per_launch")}
+    log("bench: q4 gemv sweep (config[2] weights, M = 1..16, graph replay)")
+    sweep = q4_gemv_sweep(RL_WORKLOADS[2].model, dev)
+    sweep["lm_head_traffic"] = profile_figure("q4_gemv_lm_head_traffic.md",
+                                              "traffic_bytes_per_launch")
+    line["q4_gemv"] = sweep
+    log("bench: fused CE (config[3])")
+    line["ce_config3"] = ce_stress(dev, CE_STRESS["rows"])
+    log("bench: config[0]")
+    c0 = config0_leg(dev)
+    line["config0"] = {k: v for k, v in c0.items() if not k.startswith("_")}
+    line["_cpu"] = (dweights, c0)
+    return line
+
+
+def bench_ce_stress(args) -> dict:
+    import torch
+
+    from summa_amd.configs import CE_STRESS
+    dev = torch.device("cuda:0")
+    r = ce_stress(dev, args.rows, reps=max(args.steps, 1))
+    gbs = r["grad_in_place"]["GBs"]
+    return {"metric": "fused CE grad-in-place GB/s (config[3] bf16 65536x131072)",
+            "value": gbs, "unit": "GB/s", "ms_per_step": r["grad_in_place"]["ms"],
+            "dtype": "bf16", "config": {"workload": "ce_stress", **CE_STRESS},
+            "roofline": {"bound": "hbm", "kernel": "ce_grad (lp + loss + grad in place)",
+                         "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": r["grad_in_place"]["frac"],
+                         "traffic": profile_figure("ce_config3_traffic.md",
+                                                   "traffic_bytes_per_launch")},
+            "ce_config3": r}
 
 
 def bench_q4_gemv(args) -> dict:
-    """The 4-bit GEMV alone (the metric's roofline part): config[2] weights,
-    M=1, graph replay; see q4_gemv_sweep."""
     import torch
 
+    from summa_amd.configs import RL_WORKLOADS
     dev = torch.device("cuda:0")
-    sweep = q4_gemv_sweep(CFG2, dev, reps=max(args.steps, 1) * 10)
+    sweep = q4_gemv_sweep(RL_WORKLOADS[2].model, dev, reps=max(args.steps, 1) * 10)
     achieved = sweep["lm_head_GBs"]
     # a plain device copy of known size (256 MiB read + 256 MiB written): the
     # calibration dispatch for the HBM byte counters of a rocprofv3 --pmc run
     src = torch.empty(64 << 20, dtype=torch.float32, device=dev)
     torch.empty_like(src).copy_(src)
     torch.cuda.synchronize()
-    return {
-        "metric": "4-bit GEMV GB/s (config[2] LM head, M=1)", "value": achieved, "unit": "GB/s",
-        "ms_per_step": sweep["sweep_ms"], "dtype": "q4g128 weights, f16 x, f32 accumulate",
-        "config": {"workload": "q4_gemv config[2]", "lm_head": [CFG2["vocab"], CFG2["d_model"]]},
-        "roofline": {"bound": "hbm", "kernel": "q4g128 GEMV M=1 (LM head 65536x2048)",
-                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_gemv_traffic()},
-        "q4_gemv": {k: (round(v, 4) if isinstance(v, float) else v) for k, v in sweep.items()},
-    }
+    return {"metric": "4-bit GEMV GB/s (config[2] LM head, M=1)", "value": achieved,
+            "unit": "GB/s", "ms_per_step": sweep["by_M"]["1"]["sweep_ms"],
+            "dtype": "q4g128 weights, f16 x, f32 accumulate",
+            "config": {"workload": "q4_gemv config[2]",
+                       "lm_head": [RL_WORKLOADS[2].model["vocab"],
+                                   RL_WORKLOADS[2].model["d_model"]]},
+            "roofline": {"bound": "hbm", "kernel": "q4g128 GEMV M=1 (LM head 65536x2048)",
+                         "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4),
+                         "traffic": profile_figure("q4_gemv_lm_head_traffic.md",
+                                                   "traffic_bytes_per_launch")},
+            "q4_gemv": sweep}
 
 
-WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress, "q4_gemv": bench_q4_gemv}
+def bench_recompute_gemm(args) -> dict:
+    import torch
+
+    from summa_amd.configs import RL_WORKLOADS
+    dev = torch.device("cuda:0")
+    k = recompute_gemm(RL_WORKLOADS[2], dev, reps=max(args.steps, 1))
+    # calibration copy for the counter runs (256 MiB read + 256 MiB written)
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+    torch.empty_like(src).copy_(src)
+    torch.cuda.synchronize()
+    return {"metric": "recompute FFN-in GEMM TFLOP/s (config[2])", "value": k["TFLOPs"],
+            "unit": "TFLOP/s", "ms_per_step": k["us"] / 1e3, "dtype": "q4g128 x f16 pairs",
+            "config": {"workload": "recompute_gemm config[2]", "shape": k["shape"]},
+            "roofline": {"bound": "mfma", "kernel": k["kernel"], "achieved": k["TFLOPs"],
+                         "peak": MFMA_F16_PEAK_TFS, "unit": "TFLOP/s", "frac": k["frac"],
+                         "traffic": profile_figure("recompute_gemm_ffn_in_traffic.md",
+                                                   "traffic_bytes_per_launch")}}
+
+
+WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress, "q4_gemv": bench_q4_gemv,
+             "recompute_gemm": bench_recompute_gemm}
 
 
 def main() -> int:
@@ -348,8 +628,8 @@ def main() -> int:
     p.add_argument("--warmup", type=int, default=1)
     p.add_argument("--workload", default="rl_step", choices=sorted(WORKLOADS))
     p.add_argument("--rows", type=int, default=65536)
-    p.add_argument("--config", type=int, default=1, choices=sorted(RL_CONFIGS),
-                   help="rl_step: BASELINE config index (1 = the headline line)")
+    p.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 4],
+                   help="rl_step: BASELINE config index (2 = the headline line)")
     p.add_argument("--no-cpu-baseline", action="store_true")
     args = p.parse_args()
     if args.gpus != 1:
@@ -359,18 +639,20 @@ def main() -> int:
         return 2
     log(f"bench: workload={args.workload} steps={args.steps} warmup={args.warmup}")
     res = WORKLOADS[args.workload](args)
+    cpu = res.pop("_cpu", None)
     out = {"metric": res.pop("metric"), "value": round(res.pop("value"), 3), "unit": res.pop("unit"),
            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
            "ms_per_step": round(res.pop("ms_per_step"), 4), "higher_is_better": True,
            "scaling": "weak", "vs_baseline": None, "dtype": res.pop("dtype"), "data": "synthetic",
            "config": res.pop("config")}
     out.update(res)
-    if not args.no_cpu_baseline:
-        log("bench: cpu baseline")
-        if args.workload == "rl_step":
-            out["cpu_baseline"] = cpu_baseline_rl(args.config)
-        elif args.workload == "ce_stress":
-            out["cpu_baseline"] = cpu_baseline_ce(256, 131072)
+    if not args.no_cpu_baseline and cpu is not None:
+        log("bench: cpu baseline (oracle on the host cores)")
+        from summa_amd.configs import RL_WORKLOADS
+        dweights, c0 = cpu
+        host_w = _model_host_weights(dweights)
+        del dweights
+        out["cpu_baseline"] = cpu_baseline_rl(RL_WORKLOADS[args.config], host_w, cpu_config0(c0))
     print(json.dumps(out), flush=True)
     return 0
 

@@ -55,6 +55,10 @@ def _declare(L: C.CDLL) -> None:
     L.or_round_f16.restype = C.c_float
     L.or_bf16_bits.argtypes = [vp, i64, vp]
     L.or_bf16_bits.restype = None
+    L.or_set_threads.argtypes = [C.c_int]
+    L.or_set_threads.restype = None
+    L.or_max_threads.argtypes = []
+    L.or_max_threads.restype = C.c_int
     _declare_model(L)
 
 
@@ -328,6 +332,36 @@ class HostModel:
             return lp.reshape(S, N), logits.reshape(S, N, c["V"])
         return lp.reshape(S, N), logits.reshape(S, N, c["V"]), int(conflicts[0])
 
+    def decode_steps(self, prompt, steps, temperature=1.0, seed=0, on_step=None):
+        """One rollout as ``or_generate`` runs it (generate.rs:68-124): a
+        prefill over ``prompt`` [P], then ``steps`` cached single-token steps.
+        ``on_step(i)`` is called before decode step i (timing hooks); returns
+        the sampled tokens [steps + 1]."""
+        c = self.cfg
+        P = len(prompt)
+        cap = P + steps
+        kc = np.zeros(c["layers"] * c["KVH"] * cap * c["hd"], np.float32)
+        vc = np.zeros_like(kc)
+        ids = np.ascontiguousarray(prompt, dtype=np.int32)
+        x = np.empty((P, c["d"]), np.float32)
+        lib().or_model_forward(C.byref(self.m), ids.ctypes.data, 1, P, 0, kc.ctypes.data,
+                               vc.ctypes.data, cap, x.ctypes.data)
+        last = np.ascontiguousarray(x[P - 1:])
+        logits = np.empty((1, c["V"]), np.float32)
+        toks = np.empty(steps + 1, np.int32)
+        lp = np.empty(1, np.float64)
+        for t in range(steps + 1):
+            if t > 0:
+                if on_step is not None:
+                    on_step(t - 1)
+                one = np.array([toks[t - 1]], np.int32)
+                lib().or_model_forward(C.byref(self.m), one.ctypes.data, 1, 1, P + t - 1,
+                                       kc.ctypes.data, vc.ctypes.data, cap, last.ctypes.data)
+            lib().or_model_logits(C.byref(self.m), last.ctypes.data, 1, logits.ctypes.data)
+            lib().or_sample(logits.ctypes.data, 1, c["V"], temperature, seed, t,
+                            toks[t:].ctypes.data, 1, lp.ctypes.data, 1)
+        return toks
+
     def forward_logits(self, ids):
         """Full causal forward over ids [S, L]; returns logits [S, L, V] (float32)."""
         ids = np.ascontiguousarray(ids, dtype=np.int32)
@@ -361,6 +395,12 @@ class HostModel:
         finally:
             self.m.router_gap = None
         return gaps.reshape(c["layers"], S, L)
+
+
+def set_threads(n: int) -> int:
+    """OpenMP threads for the oracle (n <= 0: every core); returns the count."""
+    lib().or_set_threads(int(n))
+    return int(lib().or_max_threads())
 
 
 def sample(logits, temperature, seed, step):

@@ -5,7 +5,12 @@
 #include "oracle.h"
 
 #include <math.h>
+#include <omp.h>
 #include <string.h>
+
+/* OpenMP thread count of the oracle's parallel loops (n <= 0: every core). */
+void or_set_threads(int n) { omp_set_num_threads(n > 0 ? n : omp_get_num_procs()); }
+int or_max_threads(void) { return omp_get_max_threads(); }
 
 float or_bf16_to_f32(uint16_t b) {
   uint32_t u = (uint32_t)b << 16;

@@ -20,6 +20,10 @@
 extern "C" {
 #endif
 
+/* OpenMP thread count of the oracle's parallel loops (n <= 0: every core). */
+void or_set_threads(int n);
+int or_max_threads(void);
+
 /* bf16 <-> f32 (round to nearest even), the rounding the device path uses. */
 float or_bf16_to_f32(uint16_t b);
 uint16_t or_f32_to_bf16(float f);
