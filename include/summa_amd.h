@@ -163,6 +163,20 @@ int64_t sm_q4_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilog
 int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
                     const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
                     int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
+/* sm_q4_matmul_ws without a caller workspace and without any allocation, for
+ * callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference. The split-K partials live in a static device array of
+ * SM_Q4_NOALLOC_SCRATCH_BYTES per GPU (held until the process ends); results
+ * are bit-identical to sm_q4_matmul_ws given a workspace of
+ * sm_q4_matmul_workspace_bytes(M, N, K, epilogue) bytes. A call whose query
+ * exceeds the scratch is rejected (SM_ERR_INVALID) before any launch. All
+ * calls on one GPU share its scratch: calls that overlap on one GPU race. */
+#define SM_Q4_NOALLOC_SCRATCH_BYTES (96LL * 1024 * 1024)
+int64_t sm_q4_noalloc_scratch_bytes(void);
+int sm_q4_matmul_noalloc(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                         const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
+                         int epilogue, void* stream);
 
 /* qkv projection fused with RoPE and the KV-cache append: y = x . W^T over
  * the Q4 qkv weight (rows [q heads | k heads | v heads], N = (H + 2 KVH) hd)

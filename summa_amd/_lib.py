@@ -34,6 +34,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_q4_qkv_rope": (i32, [vp, vp, i64, i64, i64, i64, vp, i32, i64, i64, i64, vp, vp, i64, vp,
                              vp, vp, i32, vp]),
     "sm_q4_matmul_ws": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp, i64, vp]),
+    "sm_q4_noalloc_scratch_bytes": (i64, []),
+    "sm_q4_matmul_noalloc": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
     "sm_gemm_f32": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
     "sm_swiglu_f32": (i32, [vp, i64, i64, vp, vp]),
     "sm_embed": (i32, [vp, i32, vp, i64, i64, i64, f32, vp, vp]),
