@@ -247,6 +247,29 @@ int sm_attn_prefill_lse(const void* q, const void* kcache, const void* vcache,
                         int64_t S, int64_t L, int64_t H, int64_t KVH, int64_t cap,
                         int64_t head_dim, void* stream);
 
+/* Full-sequence attention in the reference's tensor layout: the
+ * AttentionBackend::attention_inner / attention_backward pair
+ * (summa-llm/src/model/fused_attention.rs:37-74; portable definitions
+ * reference_attention :177-217 and reference_attention_backward :219-261)
+ * that Dispatch::attention_inner calls (:103-110).
+ * q, out [B, H, S, hd]; k, v [B, KVH, S, hd] with KVH dividing H (KVH == H is
+ * the repeat_kv'd form the reference hands over; a smaller KVH is read in
+ * place, query head h using key/value head h / (H / KVH)); scale 1/sqrt(hd);
+ * causal = 1 masks keys after the query's position. lse (nullable) [B*H, S]
+ * f32: the per-row log-sum-exp of the scaled, masked scores (natural log).
+ * sm_attention: dtype SM_F32 (VALU), SM_BF16 or SM_F16 (MFMA; out in the
+ *   same dtype); head_dim 64 or 128.
+ * sm_attention_backward: f32; from the forward's output and lse; dq [B, H,
+ *   S, hd], dk / dv [B, KVH, S, hd] (summed over each head group, as
+ *   reduce_kv_grad :127-138); delta_scratch [B*H*S] f32. */
+int sm_attention(const void* q, const void* k, const void* v, int dtype, int64_t B, int64_t H,
+                 int64_t KVH, int64_t S, int64_t head_dim, int causal, void* out, float* lse,
+                 void* stream);
+int sm_attention_backward(const float* q, const float* k, const float* v, const float* out,
+                          const float* grad_out, const float* lse, int64_t B, int64_t H,
+                          int64_t KVH, int64_t S, int64_t head_dim, int causal, float* dq,
+                          float* dk, float* dv, float* delta_scratch, void* stream);
+
 /* Next-token selection for `rows` logits rows (select_next_token /
  * sample_from_logits, summa-llm/src/generate.rs:127-202). temperature <= 0:
  * greedy, first max wins ties; otherwise Gumbel-max sampling from

@@ -44,6 +44,9 @@ SIGNATURES: dict[str, tuple] = {
     "sm_attn_decode": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, vp]),
     "sm_attn_prefill": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_attn_prefill_lse": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
+    "sm_attention": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp, vp, vp]),
+    "sm_attention_backward": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, vp,
+                                    vp, vp, vp]),
     "sm_sample": (i32, [vp, i64, i64, i64, f32, u64, i64, vp, i64, vp, i64, vp, vp]),
     "sm_sample_ex": (i32, [vp, i64, i64, i64, vp, u64, i64, vp, i64, vp, vp, vp, i64, vp, i64, vp,
                            vp]),

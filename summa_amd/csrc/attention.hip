@@ -203,13 +203,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 
 // Generic VALU attention (fp32 models): one thread per (query row, head);
 // query row r of sequence s sits at position pos0[s] + r + pos_off and attends
-// keys 0..=pos. q [S, L, H, hd] f32; cache [S, KVH, cap, hd] f32; out like q.
+// keys 0..=pos (causal; without the mask keys 0..L-1). q / out addressed by
+// element strides (the model's [S, L, H, hd] rows or the reference's
+// [B, H, S, hd]); cache [S, KVH, cap, hd] f32.
 template <int HD>
 __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ pos0, int pos_off, float* __restrict__ out,
     float* __restrict__ lse, int S, int L, int H,
-    int KVH, int cap, float scale) {
+    int KVH, int cap, float scale, AttnStrides qs, AttnStrides os, int causal) {
   constexpr int hd = HD;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= (int64_t)S * L * H) return;
@@ -217,11 +219,11 @@ __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
   const int r = (idx / H) % L;
   const int s = idx / ((int64_t)H * L);
   const int kvh = h / (H / KVH);
-  const int pos = pos0[s] + r + pos_off;
-  const float* qp = q + idx * hd;
+  const int pos = causal ? (pos0 ? pos0[s] : 0) + r + pos_off : L - 1;
+  const float* qp = q + qs.at(s, r, h);
   const float* kb = kc + ((size_t)s * KVH + kvh) * cap * hd;
   const float* vb = vc + ((size_t)s * KVH + kvh) * cap * hd;
-  float* op = out + idx * hd;
+  float* op = out + os.at(s, r, h);
   float m = -INFINITY, l = 0.f;
   float acc[HD];
 #pragma unroll
@@ -246,15 +248,21 @@ __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
 
 int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_t* pos0,
                   int pos_off, float* out, float* lse, int S, int L, int H, int KVH, int cap,
-                  int hd, hipStream_t st) {
+                  int hd, hipStream_t st, const AttnStrides* qs_in = nullptr,
+                  const AttnStrides* os_in = nullptr, bool causal = true) {
   const int64_t n = (int64_t)S * L * H;
   if (n == 0) return SM_OK;
   const unsigned blocks = (unsigned)ceil_div(n, 256);
   const float scale = 1.0f / sqrtf((float)hd);
+  const AttnStrides rows = AttnStrides::rows(L, H, hd);
+  const AttnStrides qs = qs_in ? *qs_in : rows, os = os_in ? *os_in : rows;
+  const int cz = causal ? 1 : 0;
   if (hd == 64)
-    attn_valu_f32_kernel<64><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, H, KVH, cap, scale);
+    attn_valu_f32_kernel<64><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, H,
+                                                     KVH, cap, scale, qs, os, cz);
   else if (hd == 128)
-    attn_valu_f32_kernel<128><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, H, KVH, cap, scale);
+    attn_valu_f32_kernel<128><<<blocks, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, H,
+                                                      KVH, cap, scale, qs, os, cz);
   else {
     set_error("f32 attention: head_dim must be 64 or 128 (got %d)", hd);
     return SM_ERR_UNSUPPORTED;
@@ -267,7 +275,9 @@ int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_
 
 int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                     const int32_t* pos0, void* out, float* lse, bool kf16, int om, int S, int L,
-                    int H, int KVH, int cap, int hd, hipStream_t st);
+                    int H, int KVH, int cap, int hd, hipStream_t st,
+                    const AttnStrides* qs = nullptr, const AttnStrides* os = nullptr,
+                    bool causal = true);
 
 inline int out_mode(int out_dtype) {
   return out_dtype == SM_BF16 ? 0 : out_dtype == SM_F16 ? 1 : out_dtype == SM_F16X2 ? 2 : -1;
@@ -373,4 +383,32 @@ extern "C" int sm_attn_prefill_lse(const void* q, const void* kcache, const void
   return attn_prefill_16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
                          pos0, out, lse, dtype == SM_F16, om, (int)S, (int)L, (int)H, (int)KVH,
                          (int)cap, (int)head_dim, st);
+}
+
+extern "C" int sm_attention(const void* q, const void* k, const void* v, int dtype, int64_t B,
+                            int64_t H, int64_t KVH, int64_t S, int64_t head_dim, int causal,
+                            void* out, float* lse, void* stream) {
+  using namespace sm;
+  SM_REQUIRE(q && k && v && out, "sm_attention: null buffer");
+  SM_REQUIRE(B >= 0 && B <= 65535 && S >= 0 && S <= (1 << 24) && H > 0 && H <= 65535 &&
+                 KVH > 0 && H % KVH == 0,
+             "sm_attention: bad shape (query heads must be a multiple of key/value heads)");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128, "sm_attention: head_dim must be 64 or 128");
+  SM_REQUIRE(causal == 0 || causal == 1, "sm_attention: causal must be 0 or 1");
+  if (B == 0 || S == 0) return SM_OK;
+  hipStream_t st = as_stream(stream);
+  const AttnStrides ts = AttnStrides::bhsd(S, H, head_dim);
+  if (dtype == SM_F32)
+    return attn_valu_f32((const float*)q, (const float*)k, (const float*)v, nullptr, 0,
+                         (float*)out, lse, (int)B, (int)S, (int)H, (int)KVH, (int)S,
+                         (int)head_dim, st, &ts, &ts, causal != 0);
+  SM_REQUIRE(dtype == SM_BF16 || dtype == SM_F16,
+             "sm_attention: dtype must be SM_F32, SM_BF16 or SM_F16");
+  SM_REQUIRE(reinterpret_cast<uintptr_t>(q) % 16 == 0 && reinterpret_cast<uintptr_t>(k) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(v) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(out) % 8 == 0,
+             "sm_attention: q, k and v must be 16-byte aligned, out 8-byte aligned");
+  return attn_prefill_16((const uint16_t*)q, (const uint16_t*)k, (const uint16_t*)v, nullptr, out,
+                         lse, dtype == SM_F16, dtype == SM_F16 ? 1 : 0, (int)B, (int)S, (int)H,
+                         (int)KVH, (int)S, (int)head_dim, st, &ts, &ts, causal != 0);
 }

@@ -42,6 +42,23 @@ __device__ inline void unpack8(u32x4 v, float (&f)[8]) {
   }
 }
 
+// Element strides of a q / output tensor over (sequence, position, head); the
+// head_dim values of one (sequence, position, head) are contiguous.
+struct AttnStrides {
+  int64_t seq, pos, head;
+  __host__ __device__ inline size_t at(int s, int r, int h) const {
+    return (size_t)((int64_t)s * seq + (int64_t)r * pos + (int64_t)h * head);
+  }
+  // the model's rows [S, L, H, hd]
+  static inline AttnStrides rows(int64_t L, int64_t H, int64_t hd) {
+    return AttnStrides{L * H * hd, H * hd, hd};
+  }
+  // the reference's tensors [B, H, S, hd] (AttentionBackend, fused_attention.rs:37-55)
+  static inline AttnStrides bhsd(int64_t S, int64_t H, int64_t hd) {
+    return AttnStrides{H * S * hd, hd, S * hd};
+  }
+};
+
 // Output modes: 0 bf16, 1 f16, 2 f16 pair (a row of `width` values is
 // hi[width] | lo[width], the SM_F16X2 layout).
 template <int OM>

@@ -28,7 +28,11 @@
 //                query j, so rescaling by the softmax correction needs no
 //                cross-lane traffic and the epilogue stores 8 bytes at a time.
 // A wave skips the key tiles past its last row's position (fully masked for
-// it). The f16 pair keeps P.V at fp32-like precision, so the prefill path
+// it). Without the causal mask (AttentionBackend::attention_inner with
+// causal = false) every query attends keys 0..L-1. q and out are addressed
+// through element strides (sequence, position, head), so the same kernel
+// serves the model's [S, L, H, hd] rows and the reference's [B, H, S, hd]
+// tensors. The f16 pair keeps P.V at fp32-like precision, so the prefill path
 // matches the decode path's fp32 probabilities; a single bf16 or f16 P costs
 // measurable log-prob accuracy.
 #include <cmath>
@@ -44,7 +48,7 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ pos0,
     void* __restrict__ out, float* __restrict__ lse, int L, int H, int KVH, int cap,
-    float scale) {
+    float scale, AttnStrides qs, AttnStrides os, int causal) {
   typedef typename Op8<KF16>::T op8;
   constexpr int NW = 8;                  // waves, 16 query rows each
   constexpr int NT = NW * kWave;         // threads
@@ -70,7 +74,7 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
   const int kvh = h / (H / KVH);
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
-  const int p0 = pos0[s];
+  const int p0 = pos0 ? pos0[s] : 0;
   const int r0 = qt * (16 * NW) + wave * 16;  // first query row of this wave
   const size_t kv_base = ((size_t)s * KVH + kvh) * cap * HD;
 
@@ -81,7 +85,7 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
 #pragma unroll
     for (int st = 0; st < STEPS; ++st) {
       if (r < L)
-        qa[st] = *reinterpret_cast<const op8*>(q + (((size_t)s * L + r) * H + h) * HD + st * 32 + g * 8);
+        qa[st] = *reinterpret_cast<const op8*>(q + qs.at(s, r, h) + st * 32 + g * 8);
       else
         qa[st] = op8{};
     }
@@ -97,10 +101,11 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
   const int qpos = p0 + r0 + j;                       // this lane's query position
 
   const int last_row = min(qt * (16 * NW) + 16 * NW - 1, L - 1);
-  const int kend = p0 + last_row + 1;  // keys [0, kend) needed by this workgroup
+  // keys [0, kend) needed by this workgroup (all L of them without the mask)
+  const int kend = causal ? p0 + last_row + 1 : L;
   // keys this wave attends to: [0, p0 + its last row]; later tiles are fully
   // masked for it (they would leave m, l and o bit-for-bit unchanged) and skipped
-  const int wave_kmax = (r0 < L) ? p0 + min(r0 + 15, L - 1) : -1;
+  const int wave_kmax = (r0 < L) ? (causal ? p0 + min(r0 + 15, L - 1) : L - 1) : -1;
 
   // ---- K/V tile staging: the next tile's global loads are issued into
   //      registers before the current tile's math and written to LDS after
@@ -169,12 +174,12 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
       sc[kb] = acc;
     }
     // ---- causal mask (only tiles that reach past the wave's first query)
-    if (kt + 63 > p0 + r0) {
+    if (kt + 63 > (causal ? p0 + r0 : L - 1)) {
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
-          if (kt + kb * 16 + 4 * g + r > qpos) sc[kb][r] = -INFINITY;
+          if (kt + kb * 16 + 4 * g + r > (causal ? qpos : L - 1)) sc[kb][r] = -INFINITY;
     }
     // ---- online softmax of query j over the 64 keys (16 here, 48 in the
     //      lanes j + 16, j + 32, j + 48)
@@ -249,8 +254,9 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
   if (lse && g == 0) lse[((size_t)s * H + h) * L + row] = m * scale + logf(l);
   const float inv = 1.f / l;
   // lane (j, g) holds dims d*16 + 4g .. +3 of its query: 8-byte stores
-  const size_t orow = (size_t)s * L + row;
+  const size_t orow = (size_t)s * L + row;  // f16-pair rows: [S * L, 2 * H * hd]
   const int width = H * HD;
+  const size_t obase = os.at(s, row, h);
 #pragma unroll
   for (int d = 0; d < HD / 16; ++d) {
     const int col = h * HD + d * 16 + 4 * g;
@@ -269,13 +275,13 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
     } else if constexpr (OM == 1) {
       const h4 v = h4{(_Float16)(o[d][0] * inv), (_Float16)(o[d][1] * inv),
                       (_Float16)(o[d][2] * inv), (_Float16)(o[d][3] * inv)};
-      *reinterpret_cast<h4*>(static_cast<_Float16*>(out) + orow * width + col) = v;
+      *reinterpret_cast<h4*>(static_cast<_Float16*>(out) + obase + d * 16 + 4 * g) = v;
     } else {
       const uint2 v = uint2{(uint32_t)f32_to_bf16(o[d][0] * inv) |
                                 ((uint32_t)f32_to_bf16(o[d][1] * inv) << 16),
                             (uint32_t)f32_to_bf16(o[d][2] * inv) |
                                 ((uint32_t)f32_to_bf16(o[d][3] * inv) << 16)};
-      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + orow * width + col) = v;
+      *reinterpret_cast<uint2*>(static_cast<uint16_t*>(out) + obase + d * 16 + 4 * g) = v;
     }
   }
 }
@@ -284,16 +290,20 @@ __global__ __launch_bounds__(512) void attn_prefill_kernel(
 
 int attn_prefill_16(const uint16_t* q, const uint16_t* kc, const uint16_t* vc,
                     const int32_t* pos0, void* out, float* lse, bool kf16, int om, int S, int L,
-                    int H, int KVH, int cap, int hd, hipStream_t st) {
+                    int H, int KVH, int cap, int hd, hipStream_t st, const AttnStrides* qs_in,
+                    const AttnStrides* os_in, bool causal) {
   if (S > 65535 || H > 65535) {
     set_error("sm_attn_prefill: S and H must be <= 65535");
     return SM_ERR_UNSUPPORTED;
   }
   const dim3 grid((unsigned)ceil_div(L, 128), (unsigned)H, (unsigned)S);
   const float scale = 1.0f / sqrtf((float)hd);
+  const AttnStrides rows = AttnStrides::rows(L, H, hd);  // [S, L, H, hd]
+  const AttnStrides qs = qs_in ? *qs_in : rows, os = os_in ? *os_in : rows;
+  const int cz = causal ? 1 : 0;
 #define SM_PF3(HD, KF, OM)                                                                \
   attn_prefill_kernel<HD, KF, OM><<<grid, 512, 0, st>>>(q, kc, vc, pos0, out, lse, L, H, KVH, cap, \
-                                                        scale)
+                                                        scale, qs, os, cz)
 #define SM_PF2(HD, KF)                          \
   do {                                          \
     if (om == 2) SM_PF3(HD, KF, 2);             \

@@ -15,6 +15,7 @@
 // All f32 with f32 accumulation: the precision of the reference CPU path.
 #include <cmath>
 
+#include "attn_common.hpp"
 #include "common.hpp"
 
 namespace sm {
@@ -152,22 +153,25 @@ __global__ void rope_qk_kernel(float* __restrict__ qkv, const float2* __restrict
 }
 
 // ------------------------------------------------------------- attention ---
-// Forward inputs: q [S*L, H, hd], k / v [S, KVH, L, hd] (positions 0..L-1,
-// causal), o [S*L, H, hd], lse [S*H, L]; dO like o.
+// Forward inputs: q, o and dO addressed by element strides (the model's
+// [S*L, H, hd] rows or the reference's [B, H, S, hd] tensors), k / v
+// [S, KVH, L, hd] (positions 0..L-1, causal or not), lse [S*H, L].
 // delta[s,h,r] = <dO, O>; dq = scale sum_t ds_t k_t with
 // ds_t = p_t (<dO, v_t> - delta), p_t = exp(scale <q, k_t> - lse).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ o, const float* __restrict__ dout, const float* __restrict__ lse,
-    int S, int L, int H, int KVH, float scale, float* __restrict__ dq, float* __restrict__ delta) {
+    int S, int L, int H, int KVH, float scale, float* __restrict__ dq, float* __restrict__ delta,
+    AttnStrides qs, int causal) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (s, r, h)
   if (idx >= (int64_t)S * L * H) return;
   const int h = idx % H, r = (idx / H) % L, s = (int)(idx / ((int64_t)H * L));
   const int kvh = h / (H / KVH);
-  const float* qp = q + idx * HD;
-  const float* op = o + idx * HD;
-  const float* gp = dout + idx * HD;
+  const size_t at = qs.at(s, r, h);
+  const float* qp = q + at;
+  const float* op = o + at;
+  const float* gp = dout + at;
   const float* kb = k + ((size_t)s * KVH + kvh) * L * HD;
   const float* vb = v + ((size_t)s * KVH + kvh) * L * HD;
   float dlt = 0.f;
@@ -176,7 +180,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
   float acc[HD];
 #pragma unroll
   for (int d = 0; d < HD; ++d) acc[d] = 0.f;
-  for (int t = 0; t <= r; ++t) {
+  const int tmax = causal ? r : L - 1;
+  for (int t = 0; t <= tmax; ++t) {
     float sc = 0.f, dp = 0.f;
 #pragma unroll
     for (int d = 0; d < HD; ++d) {
@@ -189,7 +194,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
     for (int d = 0; d < HD; ++d) acc[d] = fmaf(ds, kb[(size_t)t * HD + d], acc[d]);
   }
 #pragma unroll
-  for (int d = 0; d < HD; ++d) dq[idx * HD + d] = acc[d];
+  for (int d = 0; d < HD; ++d) dq[at + d] = acc[d];
   delta[((size_t)s * H + h) * L + r] = dlt;
 }
 
@@ -198,7 +203,8 @@ template <int HD>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
-    int S, int L, int H, int KVH, float scale, float* __restrict__ dk, float* __restrict__ dv) {
+    int S, int L, int H, int KVH, float scale, float* __restrict__ dk, float* __restrict__ dv,
+    AttnStrides qs, int causal) {
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (s, kvh, t)
   if (idx >= (int64_t)S * KVH * L) return;
   const int t = idx % L, kvh = (idx / L) % KVH, s = (int)(idx / ((int64_t)L * KVH));
@@ -210,10 +216,10 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(
   for (int d = 0; d < HD; ++d) ak[d] = av[d] = 0.f;
   for (int hh = 0; hh < group; ++hh) {
     const int h = kvh * group + hh;
-    for (int r = t; r < L; ++r) {
-      const int64_t row = ((int64_t)s * L + r) * H + h;
-      const float* qp = q + row * HD;
-      const float* gp = dout + row * HD;
+    for (int r = causal ? t : 0; r < L; ++r) {
+      const size_t at = qs.at(s, r, h);
+      const float* qp = q + at;
+      const float* gp = dout + at;
       float sc = 0.f, dp = 0.f;
 #pragma unroll
       for (int d = 0; d < HD; ++d) {
@@ -369,6 +375,35 @@ extern "C" int sm_rope_qk(float* qkv, const float* rope_table, const int32_t* po
   return SM_OK;
 }
 
+namespace sm {
+namespace {
+int attn_backward_f32(const float* q, const float* k, const float* v, const float* o,
+                      const float* dout, const float* lse, int64_t S, int64_t L, int64_t H,
+                      int64_t KVH, int64_t head_dim, float* dq, float* dk, float* dv,
+                      float* delta_scratch, const AttnStrides& qs, bool causal, hipStream_t st) {
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  const int64_t nq = S * L * H, nk = S * KVH * L;
+  const int cz = causal ? 1 : 0;
+  if (head_dim == 64) {
+    attn_bwd_dq_kernel<64><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L, (int)H,
+                                                     (int)KVH, scale, dq, delta_scratch, qs, cz);
+    attn_bwd_dkv_kernel<64><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
+                                                      (int)L, (int)H, (int)KVH, scale, dk, dv, qs,
+                                                      cz);
+  } else {
+    attn_bwd_dq_kernel<128><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L,
+                                                      (int)H, (int)KVH, scale, dq, delta_scratch,
+                                                      qs, cz);
+    attn_bwd_dkv_kernel<128><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
+                                                       (int)L, (int)H, (int)KVH, scale, dk, dv, qs,
+                                                       cz);
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+}  // namespace
+}  // namespace sm
+
 extern "C" int sm_attn_backward_f32(const float* q, const float* k, const float* v, const float* o,
                                     const float* dout, const float* lse, int64_t S, int64_t L,
                                     int64_t H, int64_t KVH, int64_t head_dim, float* dq,
@@ -378,22 +413,26 @@ extern "C" int sm_attn_backward_f32(const float* q, const float* k, const float*
   SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && H % KVH == 0, "sm_attn_backward_f32: bad shape");
   SM_REQUIRE(head_dim == 64 || head_dim == 128, "sm_attn_backward_f32: head_dim must be 64 or 128");
   if (S == 0 || L == 0) return SM_OK;
-  hipStream_t st = as_stream(stream);
-  const float scale = 1.0f / sqrtf((float)head_dim);
-  const int64_t nq = S * L * H, nk = S * KVH * L;
-  if (head_dim == 64) {
-    attn_bwd_dq_kernel<64><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L, (int)H,
-                                                     (int)KVH, scale, dq, delta_scratch);
-    attn_bwd_dkv_kernel<64><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
-                                                      (int)L, (int)H, (int)KVH, scale, dk, dv);
-  } else {
-    attn_bwd_dq_kernel<128><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L,
-                                                      (int)H, (int)KVH, scale, dq, delta_scratch);
-    attn_bwd_dkv_kernel<128><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
-                                                       (int)L, (int)H, (int)KVH, scale, dk, dv);
-  }
-  SM_LAUNCH_CHECK();
-  return SM_OK;
+  return attn_backward_f32(q, k, v, o, dout, lse, S, L, H, KVH, head_dim, dq, dk, dv,
+                           delta_scratch, AttnStrides::rows(L, H, head_dim), true,
+                           as_stream(stream));
+}
+
+extern "C" int sm_attention_backward(const float* q, const float* k, const float* v,
+                                     const float* out, const float* grad_out, const float* lse,
+                                     int64_t B, int64_t H, int64_t KVH, int64_t S,
+                                     int64_t head_dim, int causal, float* dq, float* dk, float* dv,
+                                     float* delta_scratch, void* stream) {
+  SM_REQUIRE(q && k && v && out && grad_out && lse && dq && dk && dv && delta_scratch,
+             "sm_attention_backward: null buffer");
+  SM_REQUIRE(B >= 0 && S >= 0 && H > 0 && KVH > 0 && H % KVH == 0,
+             "sm_attention_backward: bad shape (query heads must be a multiple of key/value heads)");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128, "sm_attention_backward: head_dim must be 64 or 128");
+  SM_REQUIRE(causal == 0 || causal == 1, "sm_attention_backward: causal must be 0 or 1");
+  if (B == 0 || S == 0) return SM_OK;
+  return attn_backward_f32(q, k, v, out, grad_out, lse, B, S, H, KVH, head_dim, dq, dk, dv,
+                           delta_scratch, AttnStrides::bhsd(S, H, head_dim), causal != 0,
+                           as_stream(stream));
 }
 
 extern "C" int sm_embed_backward(const int32_t* ids, const float* dx, int64_t rows, int64_t d,

@@ -454,3 +454,38 @@ def swiglu_backward(gate_value: torch.Tensor, grad: torch.Tensor) -> torch.Tenso
     call("sm_swiglu_backward", gv.data_ptr(), g.data_ptr(), dt, gv.shape[0], gv.shape[1] // 2,
          out.data_ptr(), _stream())
     return out
+
+
+# ------------------------------------------------------------- attention ---
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
+              want_lse: bool = False):
+    """AttentionBackend::attention_inner (fused_attention.rs:37-55) in the
+    reference's layout: q [B, H, S, hd], k / v [B, KVH, S, hd] (KVH divides H)
+    of one dtype (f32, bf16 or f16) -> out [B, H, S, hd] (and lse [B*H, S] f32)."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v")):
+        _dev(t, n)
+    B, H, S, hd = q.shape
+    KVH = k.shape[1]
+    if k.shape != (B, KVH, S, hd) or v.shape != k.shape or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("attention: k and v must be [B, KVH, S, hd] in q's dtype")
+    out = torch.empty_like(q)
+    lse = torch.empty(B * H, S, dtype=torch.float32, device=q.device) if want_lse else None
+    call("sm_attention", q.data_ptr(), k.data_ptr(), v.data_ptr(), _dt(q), B, H, KVH, S, hd,
+         int(causal), out.data_ptr(), _p(lse), _stream())
+    return (out, lse) if want_lse else out
+
+
+def attention_backward(q, k, v, out, grad_out, lse, causal: bool = True):
+    """AttentionBackend::attention_backward (fused_attention.rs:57-68), f32:
+    (dq [B, H, S, hd], dk [B, KVH, S, hd], dv [B, KVH, S, hd])."""
+    for t, n in ((q, "q"), (k, "k"), (v, "v"), (out, "out"), (grad_out, "grad_out"), (lse, "lse")):
+        _dev(t, n)
+    B, H, S, hd = q.shape
+    KVH = k.shape[1]
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    delta = torch.empty(B * H * S, dtype=torch.float32, device=q.device)
+    call("sm_attention_backward", q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+         grad_out.data_ptr(), lse.data_ptr(), B, H, KVH, S, hd, int(causal), dq.data_ptr(),
+         dk.data_ptr(), dv.data_ptr(), delta.data_ptr(), _stream())
+    return dq, dk, dv
