@@ -492,6 +492,8 @@ def bench_rl_step(args) -> dict:
     mc = wl.model_config()
     policy, reference = Model(mc), Model(mc)
     dweights = draw_weights(wl, [policy, reference], dev)  # the frozen copy equals the policy
+    for m in (policy, reference):  # hot calls carve their buffers from a bound workspace
+        m.bind_workspace(wl.rollouts, wl.prompt_len, wl.new_tokens)
     prompts, rewards = rl_inputs(wl, mc, dev)
     S, N = wl.rollouts, wl.new_tokens
     log("bench: warmup")

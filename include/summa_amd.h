@@ -539,6 +539,24 @@ int sm_hquant_decode(const sm_hquant* t, float* out, int transpose, void* stream
 int sm_model_load_packed(sm_model* model, int kind, int layer, const sm_hquant* tensor,
                          int layout, void* stream);
 
+/* Device workspace of the RL calls (no hidden allocation in hot calls, the
+ * workspace-query convention the Burn kernels lack). sm_rl_workspace_bytes:
+ * bytes that sm_rl_generate / sm_rl_generate_ex of S rollouts with P prompt
+ * and N new tokens, and sm_rl_logprobs / sm_rl_prepare of the same shapes
+ * (max_tokens_per_forward as they are given it), need at most; -1 on bad
+ * arguments. sm_model_bind_workspace hands the model a caller-owned device
+ * buffer of at least that many bytes (256-byte aligned) sized for those
+ * bounds: every later hot call on this model carves its buffers from it and
+ * never allocates, and a call with larger shapes fails with SM_ERR_INVALID.
+ * ws = NULL returns the model to its own grow-only buffers (the default,
+ * which allocates on the first call at a new size). Binding synchronises the
+ * device. Weight loading (sm_model_set_tensor, sm_model_load_packed,
+ * sm_model_init_random) allocates temporaries either way. */
+int64_t sm_rl_workspace_bytes(sm_model* model, int64_t S, int64_t P, int64_t N,
+                              int64_t max_tokens_per_forward);
+int sm_model_bind_workspace(sm_model* model, void* ws, int64_t bytes, int64_t S, int64_t P,
+                            int64_t N, int64_t max_tokens_per_forward);
+
 /* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout
  * the semantics of TextGenerator::generate, generate.rs:68-124, with no EOS):
  * prompts [S, P] int32 -> tokens [S, N] int32 and behavior_lp [S, N] f32

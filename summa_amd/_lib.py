@@ -85,6 +85,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_hquant_decode": (i32, [vp, vp, i32, vp]),
     "sm_model_load_packed": (i32, [vp, i32, i32, vp, i32, vp]),
     "sm_model_init_random": (i32, [vp, u64, f32, vp]),
+    "sm_rl_workspace_bytes": (i64, [vp, i64, i64, i64, i64]),
+    "sm_model_bind_workspace": (i32, [vp, vp, i64, i64, i64, i64, i64]),
     "sm_rl_generate": (i32, [vp, vp, i64, i64, i64, f32, u64, vp, vp, vp]),
     "sm_rl_generate_ex": (i32, [vp, vp, i64, i64, i64, vp, u64, vp, vp, vp, vp]),
     "sm_rl_logprobs": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),

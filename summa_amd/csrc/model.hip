@@ -69,13 +69,21 @@ int sm_moe_combine(const float*, const float*, const int32_t*, int64_t, int64_t,
 namespace sm {
 namespace {
 
+// A workspace buffer of the model: grow-only device memory the model
+// allocates itself, or (fixed) a slice of a caller-bound workspace, which is
+// never reallocated: a call that needs more fails instead.
 struct DevBuf {
   void* p = nullptr;
   size_t n = 0;
+  bool fixed = false;
 };
 
 int ensure(DevBuf& b, size_t bytes) {
   if (b.n >= bytes) return SM_OK;
+  SM_REQUIRE(!b.fixed,
+             "the bound workspace holds %zu bytes for a buffer this call needs %zu of: query "
+             "sm_rl_workspace_bytes for the larger shape and bind again",
+             b.n, bytes);
   if (b.p) SM_HIP(hipFree(b.p));
   b.p = nullptr;
   b.n = 0;
@@ -180,6 +188,10 @@ struct sm_model {
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
       lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws, seen, done;
   int64_t gen_cap = 0, gen_S = 0;
+  // caller-bound workspace (sm_model_bind_workspace): the buffers above are
+  // fixed slices of it
+  void* ws_base = nullptr;
+  int64_t ws_bytes = 0;
   // MoE router trace (sm_model_trace_routes): top-2 ids [cap, 2], logits [cap, E]
   int32_t* trace_idx = nullptr;
   float* trace_logits = nullptr;
@@ -416,17 +428,164 @@ extern "C" int sm_model_create(const sm_model_config* cfg, sm_model** out) {
   return SM_OK;
 }
 
+namespace sm {
+namespace {
+
+// Every workspace buffer of a model, in the order a bound workspace lays
+// them out.
+std::vector<DevBuf*> model_bufs(sm_model* m) {
+  return {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits, &m->rows,
+          &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc, &m->rkc, &m->rvc,
+          &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w, &m->moe_plan, &m->moe_u, &m->moe_y,
+          &m->moe_err, &m->mmws, &m->seen, &m->done};
+}
+
+void release_bufs(sm_model* m) {
+  for (DevBuf* b : model_bufs(m)) {
+    if (b->p && !b->fixed) hipFree(b->p);
+    *b = DevBuf{};
+  }
+  m->ws_base = nullptr;
+  m->ws_bytes = 0;
+}
+
+// Largest size each buffer reaches in sm_rl_generate(_ex) of S rollouts with
+// P prompt and N new tokens, and in sm_rl_logprobs / sm_rl_prepare of the
+// same shapes, for any smaller shape too (each entry is monotone in S, P, N
+// and max_tokens_per_forward); the same expressions the calls pass to ensure().
+struct WsPlan {
+  std::vector<size_t> bytes;  // parallel to model_bufs()
+};
+
+void plan_max(size_t& slot, size_t v) { slot = std::max(slot, v); }
+
+WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf) {
+  const auto& c = m->cfg;
+  auto bufs = model_bufs(m);
+  WsPlan plan;
+  plan.bytes.assign(bufs.size(), 0);
+  auto at = [&](DevBuf& b) -> size_t& {
+    for (size_t i = 0; i < bufs.size(); ++i)
+      if (bufs[i] == &b) return plan.bytes[i];
+    return plan.bytes[0];  // unreachable: every buffer is listed
+  };
+  const int64_t d = c.d_model;
+  auto mm = [&](int64_t M, int64_t Nn, int64_t K, int epi) {
+    if (!c.quantized) return;
+    const int64_t want = std::min(kMatmulWs, sm_q4_matmul_workspace_bytes(M, Nn, K, epi));
+    if (want > 0) plan_max(at(m->mmws), (size_t)want);
+  };
+  auto layers = [&](int64_t rows) {  // run_layers over `rows` tokens
+    plan_max(at(m->x), (size_t)rows * d * 4);
+    plan_max(at(m->h), (size_t)rows * std::max<int64_t>(d, m->qdim) * m->act_size);
+    if (!c.quantized) plan_max(at(m->qkv), (size_t)rows * m->qkv_n * 4);
+    plan_max(at(m->qb), (size_t)rows * m->qdim * m->kv_size);
+    plan_max(at(m->attn), (size_t)rows * m->qdim * m->act_size);
+    plan_max(at(m->u), (size_t)rows * c.ffn * m->act_size);
+    if (!c.quantized) plan_max(at(m->gv), (size_t)rows * 2 * c.ffn * 4);
+    mm(rows, d, m->qdim, SM_EPI_ADD_F32);
+    if (c.experts > 0) {
+      const int64_t routes = rows * 2;
+      plan_max(at(m->moe_idx), (size_t)routes * 4);
+      plan_max(at(m->moe_w), (size_t)routes * 4);
+      plan_max(at(m->moe_plan), (size_t)sm_moe_plan_words(rows, 2, c.experts) * 4);
+      plan_max(at(m->moe_u), (size_t)routes * c.expert_ffn * m->act_size);
+      plan_max(at(m->moe_y), (size_t)routes * d * 4);
+      plan_max(at(m->moe_err), 4);
+    } else {
+      mm(rows, 2 * (int64_t)c.ffn, d, SM_EPI_SWIGLU_F16X2);
+      mm(rows, d, c.ffn, SM_EPI_ADD_F32);
+    }
+  };
+  auto head = [&](int64_t M) {
+    plan_max(at(m->h), (size_t)M * std::max<int64_t>(d, m->qdim) * m->act_size);
+    mm(M, c.vocab, d, SM_EPI_STORE_F32);
+  };
+  // generation: prefill S*P rows, decode steps S rows, head S rows
+  const int64_t cap = P + N - 1;
+  layers(S * P);
+  layers(S);
+  head(S);
+  const size_t cache = (size_t)S * c.kv_heads * cap * c.head_dim * c.layers * m->kv_size;
+  plan_max(at(m->kc), cache);
+  plan_max(at(m->vc), cache);
+  plan_max(at(m->pos), (size_t)S * 4);
+  plan_max(at(m->lens), (size_t)S * 4);
+  plan_max(at(m->next_ids), (size_t)S * 4);
+  plan_max(at(m->rows), (size_t)S * d * 4);
+  plan_max(at(m->logits), (size_t)S * c.vocab * 4);
+  plan_max(at(m->seen), (size_t)S * ceil_div(c.vocab, 32) * 4);
+  plan_max(at(m->done), (size_t)(S + 1) * 4);
+  // recompute: chunks of at most max(budget, L) token rows (one sequence when
+  // a sequence is longer than the budget)
+  const int64_t L = P + N - 1;
+  const int64_t budget = mtpf > 0 ? mtpf : 65536;
+  const int64_t rows = std::min<int64_t>(S * L, std::max<int64_t>(budget, L));
+  layers(rows);
+  plan_max(at(m->rkc), (size_t)rows * c.kv_heads * c.head_dim * m->kv_size);
+  plan_max(at(m->rvc), (size_t)rows * c.kv_heads * c.head_dim * m->kv_size);
+  plan_max(at(m->ids), (size_t)rows * 4);
+  plan_max(at(m->pos), (size_t)S * 4);
+  plan_max(at(m->lens), (size_t)S * 4);
+  plan_max(at(m->rows), (size_t)rows * d * 4);
+  const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 29) / c.vocab);
+  head(std::min(rows, rchunk));
+  plan_max(at(m->logits), (size_t)std::min(rows, rchunk) * c.vocab * 4);
+  return plan;
+}
+
+constexpr size_t kWsAlign = 256;
+size_t align_up(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+size_t plan_total(const WsPlan& p) {
+  size_t t = 0;
+  for (size_t b : p.bytes) t += align_up(b);
+  return t;
+}
+
+}  // namespace
+}  // namespace sm
+
 extern "C" int sm_model_destroy(sm_model* m) {
   if (!m) return SM_OK;
   hipDeviceSynchronize();
   for (void* p : m->owned) hipFree(p);
-  DevBuf* bufs[] = {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits,
-                    &m->rows, &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc,
-                    &m->rkc, &m->rvc, &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w,
-                    &m->moe_plan, &m->moe_u, &m->moe_y, &m->moe_err, &m->mmws};
-  for (DevBuf* b : bufs)
-    if (b->p) hipFree(b->p);
+  release_bufs(m);
   delete m;
+  return SM_OK;
+}
+
+extern "C" int64_t sm_rl_workspace_bytes(sm_model* m, int64_t S, int64_t P, int64_t N,
+                                         int64_t max_tokens_per_forward) {
+  if (!m || S <= 0 || P <= 0 || N <= 0 || max_tokens_per_forward < 0) return -1;
+  return (int64_t)plan_total(plan_workspace(m, S, P, N, max_tokens_per_forward));
+}
+
+extern "C" int sm_model_bind_workspace(sm_model* m, void* ws, int64_t bytes, int64_t S,
+                                       int64_t P, int64_t N, int64_t max_tokens_per_forward) {
+  SM_REQUIRE(m, "sm_model_bind_workspace: null model");
+  SM_HIP(hipDeviceSynchronize());  // no call may still use the old buffers
+  release_bufs(m);
+  if (!ws) return SM_OK;  // back to the model's own grow-only buffers
+  SM_REQUIRE(S > 0 && P > 0 && N > 0 && max_tokens_per_forward >= 0,
+             "sm_model_bind_workspace: bad shape");
+  SM_REQUIRE(reinterpret_cast<uintptr_t>(ws) % kWsAlign == 0,
+             "sm_model_bind_workspace: the workspace must be 256-byte aligned");
+  const WsPlan plan = plan_workspace(m, S, P, N, max_tokens_per_forward);
+  const size_t need = plan_total(plan);
+  SM_REQUIRE(bytes >= 0 && (size_t)bytes >= need,
+             "sm_model_bind_workspace: %lld bytes given, %zu needed (sm_rl_workspace_bytes)",
+             (long long)bytes, need);
+  auto bufs = model_bufs(m);
+  size_t off = 0;
+  for (size_t i = 0; i < bufs.size(); ++i) {
+    bufs[i]->fixed = true;
+    bufs[i]->n = plan.bytes[i];
+    bufs[i]->p = plan.bytes[i] ? static_cast<char*>(ws) + off : nullptr;
+    off += align_up(plan.bytes[i]);
+  }
+  m->ws_base = ws;
+  m->ws_bytes = bytes;
   return SM_OK;
 }
 

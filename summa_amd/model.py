@@ -141,6 +141,29 @@ class Model:
         call("sm_model_trace_routes", self._h, None, None, 0)
         self._trace = None
 
+    def workspace_bytes(self, S: int, P: int, N: int, max_tokens_per_forward: int = 0) -> int:
+        """sm_rl_workspace_bytes: device bytes the RL calls need for these shapes."""
+        n = int(_lib.lib().sm_rl_workspace_bytes(self._h, S, P, N, int(max_tokens_per_forward)))
+        if n < 0:
+            raise ValueError("sm_rl_workspace_bytes: bad shape")
+        return n
+
+    def bind_workspace(self, S: int, P: int, N: int, max_tokens_per_forward: int = 0):
+        """Allocate a workspace for RL calls of up to these shapes and bind it
+        (sm_model_bind_workspace): later generate / logprobs / rl_prepare calls
+        on this model allocate nothing. Returns the workspace tensor."""
+        n = self.workspace_bytes(S, P, N, max_tokens_per_forward)
+        dev = torch.device("cuda", torch.cuda.current_device())
+        ws = torch.empty(n + 256, dtype=torch.uint8, device=dev)
+        base = (ws.data_ptr() + 255) // 256 * 256
+        call("sm_model_bind_workspace", self._h, base, n, S, P, N, int(max_tokens_per_forward))
+        self._ws = ws
+        return ws
+
+    def unbind_workspace(self) -> None:
+        call("sm_model_bind_workspace", self._h, None, 0, 0, 0, 0, 0)
+        self._ws = None
+
     def init_random(self, seed: int = 0, std: float = 0.02) -> None:
         call("sm_model_init_random", self._h, int(seed), float(std), _stream())
 
