@@ -592,6 +592,53 @@ int sm_rl_prepare(sm_model* policy, sm_model* reference, const int32_t* prompts,
                   float* group_stats, float* dlp, int32_t* flags, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Trainable policy: the gradient and optimizer half of GrpoDeviceBatchRuntime
+ * (posttrain.rs:1288-1305): prepare_device_batch stages gradients,
+ * optimizer_step(learning_rate_scale) applies them. f32 master weights of a
+ * dense decoder ([out, in] rows, tensor kinds SM_W_EMBED .. SM_W_LM_HEAD); a
+ * quantized config runs its forward on fake-quantized weights (Q4G128
+ * linears, bf16 embedding: what sm_policy_install puts into a quantized
+ * model) with straight-through gradients (trainer.rs:312-318).
+ * sm_optimizer_config: AdamW (lr, beta1, beta2, eps, weight_decay; the
+ * trainer's 3e-4, 0.9, 0.95, 1e-8, 0.1: trainer.rs:1124-1129, main.rs:171-174)
+ * for every tensor, or with muon_lr > 0 Muon for the per-layer projections
+ * (BatchedMuon, muon.rs:196-285; trainer.rs:1974-1975); grad_clip > 0 clips the
+ * global gradient norm (gradient_norm_and_clip, main.rs:667-694; default 1.0).
+ * sm_policy_prepare: the recompute with activations kept (lp_cur), the
+ *   frozen reference's log-probs (sm_rl_logprobs on `reference`), the GRPO
+ *   loss (as sm_grpo_loss) and the backward of sum(dlp * lp_cur), added to the
+ *   staged gradients. Arguments as sm_rl_prepare.
+ * sm_policy_optimizer_step: clip, optimizer update at lr * scale, staged
+ *   gradients cleared; grad_norm (nullable, host) gets the pre-clip norm; a
+ *   non-finite norm fails with the reference's message (trainer.rs:1959-1964).
+ *   Synchronises the stream once (the norm readback).
+ * sm_policy_install: the master weights into an inference model
+ *   (sm_model_set_tensor per tensor: quantized models re-quantize).
+ * sm_policy_get_tensor: a master weight (gradient = 0) or its staged
+ *   gradient (gradient = 1) into dst. */
+typedef struct sm_policy sm_policy;
+typedef struct sm_optimizer_config {
+  float lr, beta1, beta2, eps, weight_decay;
+  float muon_lr;   /* 0: AdamW for every tensor */
+  float grad_clip; /* <= 0: no clipping */
+} sm_optimizer_config;
+int sm_policy_create(const sm_model_config* cfg, const sm_optimizer_config* opt,
+                     sm_policy** out);
+int sm_policy_destroy(sm_policy* policy);
+int sm_policy_set_tensor(sm_policy* policy, int kind, int layer, const float* src, void* stream);
+int sm_policy_get_tensor(const sm_policy* policy, int kind, int layer, float* dst, int gradient,
+                         void* stream);
+int sm_policy_install(const sm_policy* policy, sm_model* model, void* stream);
+int sm_policy_prepare(sm_policy* policy, sm_model* reference, const int32_t* prompts,
+                      const int32_t* tokens, const float* behavior_lp, const float* rewards,
+                      const float* mask, int64_t groups, int64_t group_size, int64_t P, int64_t N,
+                      double clip_epsilon, double advantage_epsilon, double kl_coefficient,
+                      float* lp_cur, float* lp_ref, float* group_stats, float* dlp,
+                      int32_t* flags, void* stream);
+int sm_policy_optimizer_step(sm_policy* policy, double learning_rate_scale, float* grad_norm,
+                             void* stream);
+
+/* ------------------------------------------------------------------------
  * Seeded synthetic data (no reference counterpart; bench/test inputs).
  * Values are a pure function of (seed, index), identical for any launch shape.
  */

@@ -92,6 +92,14 @@ SIGNATURES: dict[str, tuple] = {
     "sm_rl_logprobs": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "sm_rl_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64, i64,
                             vp, vp, vp, vp, vp, vp]),
+    "sm_policy_create": (i32, [vp, vp, vp]),
+    "sm_policy_destroy": (i32, [vp]),
+    "sm_policy_set_tensor": (i32, [vp, i32, i32, vp, vp]),
+    "sm_policy_get_tensor": (i32, [vp, i32, i32, vp, i32, vp]),
+    "sm_policy_install": (i32, [vp, vp, vp]),
+    "sm_policy_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64,
+                                vp, vp, vp, vp, vp, vp]),
+    "sm_policy_optimizer_step": (i32, [vp, f64, vp, vp]),
     "sm_fill_normal": (i32, [vp, i32, i64, f32, f32, u64, vp]),
     "sm_fill_ce_stress": (i32, [vp, i32, vp, i64, i64, f32, f32, u64, vp]),
 }

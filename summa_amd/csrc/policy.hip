@@ -1,0 +1,640 @@
+// Trainable policy: the gradient and optimizer half of GrpoDeviceBatchRuntime
+// (summa-train/src/posttrain.rs:1288-1305). prepare_device_batch recomputes
+// the policy's token log-probs with its activations kept, evaluates the GRPO
+// loss (grpo_loss_tensor, posttrain.rs:874-1028) and stages the gradient of
+// every parameter; optimizer_step(learning_rate_scale) clips the global
+// gradient norm and applies the trainer's optimizers (gradient_norm_and_clip,
+// summa-train/src/main.rs:667-694; Muon for the per-layer projections and
+// AdamW for the rest, trainer.rs:1124-1129, 1974-1975; muon.rs:196-285).
+//
+// Weights are f32 master copies of a dense decoder in the model's [out, in]
+// rows. For a quantized configuration the forward runs on fake-quantized
+// weights (Q4G128 linears, bf16 embedding: the values the inference model
+// holds after sm_policy_install) and the gradient passes straight through to
+// the masters (the fake-quantized parameter leaves of trainer.rs:312-318), so
+// the recomputed log-probs are those of the model that produced the rollouts.
+//
+// Host composition over the library's kernels (the same steps as the Python
+// composition in summa_amd/train.py): embedding, RMSNorm, GEMMs, RoPE,
+// attention with its log-sum-exp, SwiGLU, fused CE; backward through the CE
+// gradient, GEMM data / weight gradients, RMSNorm, RoPE, attention, SwiGLU and
+// embedding backward kernels.
+#include <cmath>
+#include <vector>
+
+#include "common.hpp"
+
+extern "C" {
+int sm_embed(const void*, int, const int32_t*, int64_t, int64_t, int64_t, float, float*, void*);
+int sm_rmsnorm(const float*, const float*, int64_t, int64_t, float, void*, int, void*);
+int sm_gemm_ex(int, int, int64_t, int64_t, int64_t, float, const float*, int64_t, const float*,
+               int64_t, float, float*, int64_t, void*);
+int sm_rope_qk(float*, const float*, const int32_t*, int64_t, int64_t, int64_t, int64_t, int64_t,
+               int, void*);
+int sm_attn_prefill_lse(const void*, const void*, const void*, const int32_t*, void*, float*, int,
+                        int, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void*);
+int sm_swiglu(const void*, int, int64_t, int64_t, void*, void*);
+int sm_swiglu_backward(const void*, const void*, int, int64_t, int64_t, void*, void*);
+int sm_ce_rows(const void*, int, const int32_t*, int64_t, int64_t, int64_t, float*, float*, void*,
+               float, const float*, float*, void*);
+int sm_rmsnorm_backward(const float*, const float*, const float*, int64_t, int64_t, float, int,
+                        float*, float*, float*, void*);
+int sm_attn_backward_f32(const float*, const float*, const float*, const float*, const float*,
+                         const float*, int64_t, int64_t, int64_t, int64_t, int64_t, float*, float*,
+                         float*, float*, void*);
+int sm_embed_backward(const int32_t*, const float*, int64_t, int64_t, int64_t, float*, void*);
+int sm_adamw_step(float*, const float*, float*, float*, int64_t, float, float, float, float, float,
+                  int64_t, void*);
+int sm_muon_momentum(const float*, float*, float*, int64_t, float, int, void*);
+int sm_axpby(const float*, float*, int64_t, float, float, void*);
+int sm_frobenius_normalize(float*, int64_t, float, float*, void*);
+int sm_grpo_loss(const float*, const float*, const float*, const float*, const float*, int64_t,
+                 int64_t, int64_t, double, double, double, float*, float*, float*, int32_t*, void*);
+int sm_rl_logprobs(sm_model*, const int32_t*, const int32_t*, int64_t, int64_t, int64_t, int64_t,
+                   float*, void*);
+int sm_model_set_tensor(sm_model*, int, int, const float*, void*);
+int sm_q4_quantize(const void*, int, int64_t, uint8_t*, uint16_t*, int32_t*, void*);
+}
+
+namespace sm {
+namespace {
+
+constexpr int kKinds = 9;  // SM_W_EMBED .. SM_W_LM_HEAD
+constexpr float kMuonMomentum = 0.95f;                          // muon.rs:10
+constexpr float kNsA = 3.4445f, kNsB = -4.775f, kNsC = 2.0315f;  // muon.rs:11
+constexpr int kNsSteps = 5;                                     // muon.rs:12
+constexpr float kMuonEps = 1e-7f;                               // muon.rs:13
+
+bool is_layer_kind(int k) {
+  return k == SM_W_ATTN_NORM || k == SM_W_QKV || k == SM_W_O || k == SM_W_FFN_NORM ||
+         k == SM_W_IN || k == SM_W_DOWN;
+}
+bool is_linear_kind(int k) {
+  return k == SM_W_QKV || k == SM_W_O || k == SM_W_IN || k == SM_W_DOWN || k == SM_W_LM_HEAD;
+}
+bool is_muon_kind(int k) {  // the per-layer 2-D projections (trainer.rs:1974)
+  return k == SM_W_QKV || k == SM_W_O || k == SM_W_IN || k == SM_W_DOWN;
+}
+
+__global__ void gather_rows_f32(const float* __restrict__ src, const int64_t* __restrict__ rows,
+                                int64_t n, int d, float* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n * d) dst[i] = src[rows[i / d] * d + i % d];
+}
+__global__ void scatter_rows_f32(const float* __restrict__ src, const int64_t* __restrict__ rows,
+                                 int64_t n, int d, float* __restrict__ dst) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n * d) dst[rows[i / d] * d + i % d] = src[i];
+}
+// rows [S*L, (H + 2 KVH) hd] -> q [S*L, H*hd], k / v [S, KVH, L, hd]
+__global__ void split_qkv_f32(const float* __restrict__ qkv, int S, int L, int H, int KVH, int hd,
+                              float* __restrict__ q, float* __restrict__ k, float* __restrict__ v) {
+  const int qn = (H + 2 * KVH) * hd;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * L * qn) return;
+  const int64_t row = i / qn;
+  const int c = i % qn;
+  const float x = qkv[i];
+  if (c < H * hd) { q[row * H * hd + c] = x; return; }
+  const int s = row / L, r = row % L;
+  const int c2 = c - H * hd;
+  const int which = c2 / (KVH * hd), kh = (c2 % (KVH * hd)) / hd, e = c2 % hd;
+  (which ? v : k)[(((size_t)s * KVH + kh) * L + r) * hd + e] = x;
+}
+// the inverse: dq, dk, dv -> dqkv rows
+__global__ void merge_qkv_f32(const float* __restrict__ q, const float* __restrict__ k,
+                              const float* __restrict__ v, int S, int L, int H, int KVH, int hd,
+                              float* __restrict__ qkv) {
+  const int qn = (H + 2 * KVH) * hd;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)S * L * qn) return;
+  const int64_t row = i / qn;
+  const int c = i % qn;
+  if (c < H * hd) { qkv[i] = q[row * H * hd + c]; return; }
+  const int s = row / L, r = row % L;
+  const int c2 = c - H * hd;
+  const int which = c2 / (KVH * hd), kh = (c2 % (KVH * hd)) / hd, e = c2 % hd;
+  qkv[i] = (which ? v : k)[(((size_t)s * KVH + kh) * L + r) * hd + e];
+}
+// ids [S, L] = prompt ‖ tokens[:, :N-1]; scored rows s*L + P-1+n
+__global__ void build_ids_rows(const int32_t* __restrict__ prompts,
+                               const int32_t* __restrict__ tokens, int S, int P, int N,
+                               int32_t* __restrict__ ids, int64_t* __restrict__ rows) {
+  const int L = P + N - 1;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < (int64_t)S * L) {
+    const int64_t s = i / L;
+    const int t = i % L;
+    ids[i] = (t < P) ? prompts[s * P + t] : tokens[s * N + (t - P)];
+  }
+  if (i < (int64_t)S * N) rows[i] = (i / N) * L + P - 1 + i % N;
+}
+__global__ void neg_f32(const float* __restrict__ a, int64_t n, float* __restrict__ b) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) b[i] = -a[i];
+}
+__global__ void transpose_f32(const float* __restrict__ a, int R, int C, float* __restrict__ b) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // a [R, C] -> b [C, R]
+  if (i < (int64_t)R * C) b[(i % C) * R + i / C] = a[i];
+}
+__global__ void zero_f32(float* p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0.f;
+}
+__global__ void round_bf16_f32(const float* __restrict__ a, int64_t n, float* __restrict__ b) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) b[i] = bf16_to_f32(f32_to_bf16(a[i]));
+}
+// Q4G128 codec decode (row-major codes, bf16 scales): value = scale * code
+__global__ void q4_decode_f32(const uint8_t* __restrict__ codes, const uint16_t* __restrict__ sc,
+                              int64_t n, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int q = (codes[i / 2] >> ((i & 1) * 4)) & 0xf;
+  if (q >= 8) q -= 16;
+  out[i] = bf16_to_f32(sc[i / 128]) * (float)q;
+}
+// sum of squares (f64) of each 64 K-value chunk of `a` -> part[blockIdx.x]
+constexpr int64_t kSumChunk = 65536;
+__global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ a, int64_t n,
+                                                    double* __restrict__ part) {
+  __shared__ double wp[256 / kWave];
+  double s = 0.0;
+  const int64_t base = (int64_t)blockIdx.x * kSumChunk;
+  const int64_t end = std::min<int64_t>(n, base + kSumChunk);
+  for (int64_t i = base + threadIdx.x; i < end; i += 256) s += (double)a[i] * a[i];
+  s = wave_sum_f64(s);
+  if (threadIdx.x % kWave == 0) wp[threadIdx.x / kWave] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double t = 0.0;
+    for (int w = 0; w < 256 / kWave; ++w) t += wp[w];
+    part[blockIdx.x] = t;
+  }
+}
+// acc[0] = sum of part[0..n) in order (deterministic)
+__global__ void sum_parts_kernel(const double* __restrict__ part, int64_t n,
+                                 double* __restrict__ acc) {
+  double t = 0.0;
+  for (int64_t i = 0; i < n; ++i) t += part[i];
+  acc[0] = t;
+}
+// g *= max_norm / norm when the norm (sqrt(acc[0])) exceeds max_norm > 0
+__global__ void clip_scale_kernel(float* __restrict__ g, int64_t n, const double* __restrict__ acc,
+                                  float max_norm) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const float norm = (float)sqrt(acc[0]);
+  if (i < n && max_norm > 0.f && norm > max_norm) g[i] *= max_norm / norm;
+}
+
+unsigned blocks256(int64_t n) { return (unsigned)ceil_div(n > 0 ? n : 1, 256); }
+
+struct Buf {
+  void* p = nullptr;
+  size_t n = 0;
+};
+int grow(Buf& b, size_t bytes) {
+  if (b.n >= bytes) return SM_OK;
+  if (b.p) SM_HIP(hipFree(b.p));
+  b.p = nullptr;
+  b.n = 0;
+  SM_HIP(hipMalloc(&b.p, bytes ? bytes : 16));
+  b.n = bytes;
+  return SM_OK;
+}
+
+}  // namespace
+}  // namespace sm
+
+struct sm_policy {
+  sm_model_config cfg;
+  sm_optimizer_config opt;
+  int64_t qdim = 0, kvdim = 0, qn = 0;
+  int64_t rows_per_layer[sm::kKinds] = {};  // per-layer tensor shape [N, K]
+  int64_t cols[sm::kKinds] = {};
+  int64_t count[sm::kKinds] = {};           // elements over all layers
+  float* w[sm::kKinds] = {};    // f32 masters
+  float* g[sm::kKinds] = {};    // staged gradients
+  float* wq[sm::kKinds] = {};   // fake-quantized copies (quantized configs)
+  float* m1[sm::kKinds] = {};   // AdamW moments / Muon velocity in m1
+  float* m2[sm::kKinds] = {};
+  int64_t adam_step = 0, muon_step = 0;
+  float* rope = nullptr;
+  std::vector<void*> owned;
+  // forward activations and scratch (grow-only)
+  sm::Buf act, scratch;
+  int64_t fS = 0, fP = 0, fN = 0;
+  bool staged = false;
+};
+
+namespace sm {
+namespace {
+
+int palloc(sm_policy* p, float** out, int64_t n) {
+  SM_HIP(hipMalloc((void**)out, (size_t)std::max<int64_t>(n, 1) * 4));
+  p->owned.push_back(*out);
+  zero_f32<<<blocks256(n), 256>>>(*out, n);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+// the weights the forward uses: masters, or their fake-quantized copies
+const float* fw(const sm_policy* p, int kind) {
+  return (p->cfg.quantized && p->wq[kind]) ? p->wq[kind] : p->w[kind];
+}
+const float* fwl(const sm_policy* p, int kind, int layer) {
+  return fw(p, kind) + (size_t)layer * p->rows_per_layer[kind] * p->cols[kind];
+}
+float* gl(const sm_policy* p, int kind, int layer) {
+  return p->g[kind] + (size_t)layer * p->rows_per_layer[kind] * p->cols[kind];
+}
+
+// Refresh the fake-quantized copies from the masters: Q4G128 per [N, K]
+// linear (the inference model's quantizer, sm_q4_quantize) and bf16 for the
+// embedding table.
+int fake_quantize(sm_policy* p, hipStream_t st) {
+  const auto& c = p->cfg;
+  int64_t maxn = 0;
+  for (int k = 0; k < kKinds; ++k)
+    if (is_linear_kind(k)) maxn = std::max(maxn, p->rows_per_layer[k] * p->cols[k]);
+  const int64_t groups = ceil_div(maxn, 128);
+  SM_TRY(grow(p->scratch, (size_t)groups * 64 + (size_t)groups * 2 + 64));
+  uint8_t* codes = (uint8_t*)p->scratch.p;
+  uint16_t* scales = (uint16_t*)(codes + groups * 64);
+  for (int k = 0; k < kKinds; ++k) {
+    if (!is_linear_kind(k)) continue;
+    const int64_t n = p->rows_per_layer[k] * p->cols[k];
+    const int layers = (k == SM_W_LM_HEAD) ? 1 : c.layers;
+    for (int l = 0; l < layers; ++l) {
+      SM_TRY(sm_q4_quantize(p->w[k] + (size_t)l * n, SM_F32, n, codes, scales, nullptr, st));
+      q4_decode_f32<<<blocks256(n), 256, 0, st>>>(codes, scales, n, p->wq[k] + (size_t)l * n);
+    }
+  }
+  round_bf16_f32<<<blocks256(p->count[SM_W_EMBED]), 256, 0, st>>>(
+      p->w[SM_W_EMBED], p->count[SM_W_EMBED], p->wq[SM_W_EMBED]);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+// zeropower_via_newton_schulz (muon.rs:257-285) of one [N, K] matrix in place
+// of `upd`, in the orientation the reference sees it (Burn's [d_in, d_out] =
+// this matrix transposed): the short side first, Frobenius-normalised, five
+// quintic steps. tmp holds 2 N K + 2 min(N, K)^2 + 1 floats.
+int newton_schulz(float* upd, int64_t N, int64_t K, float* tmp, hipStream_t st) {
+  // Burn orientation X0 = upd^T [K, N]; with K > N iterate on X0^T = upd.
+  const bool as_is = K > N;
+  const int64_t r = as_is ? N : K, cdim = as_is ? K : N;
+  float* x = tmp;
+  float* x2 = x + N * K;
+  float* gram = x2 + N * K;
+  float* poly = gram + r * r;
+  float* norm = poly + r * r;
+  if (as_is) SM_HIP(hipMemcpyAsync(x, upd, (size_t)N * K * 4, hipMemcpyDeviceToDevice, st));
+  else transpose_f32<<<blocks256(N * K), 256, 0, st>>>(upd, (int)N, (int)K, x);
+  SM_TRY(sm_frobenius_normalize(x, r * cdim, kMuonEps, norm, st));
+  for (int i = 0; i < kNsSteps; ++i) {
+    SM_TRY(sm_gemm_ex(0, 1, r, r, cdim, 1.f, x, cdim, x, cdim, 0.f, gram, r, st));  // X X^T
+    SM_TRY(sm_gemm_ex(0, 0, r, r, r, kNsC, gram, r, gram, r, 0.f, poly, r, st));    // c A A
+    SM_TRY(sm_axpby(gram, poly, r * r, kNsB, 1.f, st));                              // + b A
+    SM_HIP(hipMemcpyAsync(x2, x, (size_t)r * cdim * 4, hipMemcpyDeviceToDevice, st));
+    SM_TRY(sm_gemm_ex(0, 0, r, cdim, r, 1.f, poly, r, x2, cdim, kNsA, x, cdim, st));  // a X + B X
+  }
+  if (as_is) SM_HIP(hipMemcpyAsync(upd, x, (size_t)N * K * 4, hipMemcpyDeviceToDevice, st));
+  else transpose_f32<<<blocks256(N * K), 256, 0, st>>>(x, (int)K, (int)N, upd);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+}  // namespace
+}  // namespace sm
+
+using namespace sm;
+
+extern "C" int sm_policy_create(const sm_model_config* cfg, const sm_optimizer_config* opt,
+                                sm_policy** out) {
+  SM_REQUIRE(cfg && opt && out, "sm_policy_create: null argument");
+  const sm_model_config& c = *cfg;
+  SM_REQUIRE(c.layers > 0 && c.d_model > 0 && c.heads > 0 && c.kv_heads > 0 &&
+                 c.heads % c.kv_heads == 0 && c.ffn > 0 && c.vocab > 0 && c.max_seq > 0,
+             "sm_policy_create: invalid model config");
+  SM_REQUIRE(c.head_dim == 64 || c.head_dim == 128, "sm_policy_create: head_dim must be 64 or 128");
+  SM_REQUIRE(c.experts == 0, "sm_policy_create: the trainable policy is a dense decoder");
+  if (c.quantized)
+    SM_REQUIRE(c.d_model % 128 == 0 && c.ffn % 128 == 0 && (c.heads * c.head_dim) % 128 == 0,
+               "sm_policy_create: quantized models need d_model, ffn and heads*head_dim % 128 == 0");
+  SM_REQUIRE(std::isfinite(opt->lr) && opt->lr >= 0.f && opt->beta1 >= 0.f && opt->beta1 < 1.f &&
+                 opt->beta2 >= 0.f && opt->beta2 < 1.f && opt->eps > 0.f &&
+                 opt->weight_decay >= 0.f && opt->muon_lr >= 0.f && std::isfinite(opt->grad_clip),
+             "sm_policy_create: invalid optimizer settings");
+  sm_policy* p = new sm_policy();
+  p->cfg = c;
+  p->opt = *opt;
+  p->qdim = (int64_t)c.heads * c.head_dim;
+  p->kvdim = (int64_t)c.kv_heads * c.head_dim;
+  p->qn = p->qdim + 2 * p->kvdim;
+  const int64_t d = c.d_model, F = c.ffn;
+  const int64_t shape[kKinds][2] = {{c.vocab, d}, {1, d}, {p->qn, d}, {d, p->qdim}, {1, d},
+                                    {2 * F, d},  {d, F}, {1, d},     {c.vocab, d}};
+  auto fail = [&](int s) { sm_policy_destroy(p); return s; };
+  for (int k = 0; k < kKinds; ++k) {
+    p->rows_per_layer[k] = shape[k][0];
+    p->cols[k] = shape[k][1];
+    p->count[k] = shape[k][0] * shape[k][1] * (is_layer_kind(k) ? c.layers : 1);
+    int s;
+    if ((s = palloc(p, &p->w[k], p->count[k])) || (s = palloc(p, &p->g[k], p->count[k])) ||
+        (s = palloc(p, &p->m1[k], p->count[k])) || (s = palloc(p, &p->m2[k], p->count[k])))
+      return fail(s);
+    if (c.quantized && (is_linear_kind(k) || k == SM_W_EMBED))
+      if ((s = palloc(p, &p->wq[k], p->count[k]))) return fail(s);
+  }
+  const int half = c.head_dim / 2;
+  std::vector<float> tab((size_t)c.max_seq * half * 2);
+  for (int pos = 0; pos < c.max_seq; ++pos)
+    for (int q = 0; q < half; ++q) {
+      const double ang = (double)pos * std::pow((double)c.rope_theta, -2.0 * q / c.head_dim);
+      tab[((size_t)pos * half + q) * 2] = (float)std::cos(ang);
+      tab[((size_t)pos * half + q) * 2 + 1] = (float)std::sin(ang);
+    }
+  int s;
+  if ((s = palloc(p, &p->rope, (int64_t)tab.size()))) return fail(s);
+  if (hipMemcpy(p->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess) {
+    set_error("sm_policy_create: rope upload failed");
+    return fail(SM_ERR_HIP);
+  }
+  if (hipDeviceSynchronize() != hipSuccess) {
+    set_error("sm_policy_create: initialisation failed");
+    return fail(SM_ERR_HIP);
+  }
+  *out = p;
+  return SM_OK;
+}
+
+extern "C" int sm_policy_destroy(sm_policy* p) {
+  if (!p) return SM_OK;
+  hipDeviceSynchronize();
+  for (void* q : p->owned) hipFree(q);
+  if (p->act.p) hipFree(p->act.p);
+  if (p->scratch.p) hipFree(p->scratch.p);
+  delete p;
+  return SM_OK;
+}
+
+extern "C" int sm_policy_set_tensor(sm_policy* p, int kind, int layer, const float* src,
+                                    void* stream) {
+  SM_REQUIRE(p && src, "sm_policy_set_tensor: null argument");
+  SM_REQUIRE(kind >= 0 && kind < kKinds, "sm_policy_set_tensor: tensor kind %d", kind);
+  const int64_t n = p->rows_per_layer[kind] * p->cols[kind];
+  float* dst = p->w[kind];
+  if (is_layer_kind(kind)) {
+    SM_REQUIRE(layer >= 0 && layer < p->cfg.layers, "layer %d out of range", layer);
+    dst += (size_t)layer * n;
+  }
+  SM_HIP(hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice, as_stream(stream)));
+  return SM_OK;
+}
+
+extern "C" int sm_policy_get_tensor(const sm_policy* p, int kind, int layer, float* dst,
+                                    int gradient, void* stream) {
+  SM_REQUIRE(p && dst, "sm_policy_get_tensor: null argument");
+  SM_REQUIRE(kind >= 0 && kind < kKinds, "sm_policy_get_tensor: tensor kind %d", kind);
+  const int64_t n = p->rows_per_layer[kind] * p->cols[kind];
+  const float* src = gradient ? p->g[kind] : p->w[kind];
+  if (is_layer_kind(kind)) {
+    SM_REQUIRE(layer >= 0 && layer < p->cfg.layers, "layer %d out of range", layer);
+    src += (size_t)layer * n;
+  }
+  SM_HIP(hipMemcpyAsync(dst, src, (size_t)n * 4, hipMemcpyDeviceToDevice, as_stream(stream)));
+  return SM_OK;
+}
+
+extern "C" int sm_policy_install(const sm_policy* p, sm_model* model, void* stream) {
+  SM_REQUIRE(p && model, "sm_policy_install: null argument");
+  for (int k = 0; k < kKinds; ++k) {
+    const int64_t n = p->rows_per_layer[k] * p->cols[k];
+    const int layers = is_layer_kind(k) ? p->cfg.layers : 1;
+    for (int l = 0; l < layers; ++l)
+      SM_TRY(sm_model_set_tensor(model, k, is_layer_kind(k) ? l : -1, p->w[k] + (size_t)l * n,
+                                 stream));
+  }
+  return SM_OK;
+}
+
+extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_t* prompts,
+                                 const int32_t* tokens, const float* behavior_lp,
+                                 const float* rewards, const float* mask, int64_t groups,
+                                 int64_t group_size, int64_t P, int64_t N, double clip_epsilon,
+                                 double advantage_epsilon, double kl_coefficient, float* lp_cur,
+                                 float* lp_ref, float* group_stats, float* dlp, int32_t* flags,
+                                 void* stream) {
+  SM_REQUIRE(p && prompts && tokens && behavior_lp && rewards && lp_cur && dlp,
+             "sm_policy_prepare: null argument");
+  SM_REQUIRE(kl_coefficient == 0.0 || (reference && lp_ref),
+             "GRPO rollout needs reference log-probs for positive KL coefficient");
+  SM_REQUIRE(groups > 0 && group_size > 0 && P > 0 && N > 0, "sm_policy_prepare: bad shape");
+  const auto& c = p->cfg;
+  const int64_t S = groups * group_size, L = P + N - 1, M = S * L, R = S * N;
+  SM_REQUIRE(L <= c.max_seq, "sequence length %lld exceeds max_seq_len %d", (long long)L,
+             c.max_seq);
+  hipStream_t st = as_stream(stream);
+  const int64_t d = c.d_model, H = c.heads, KVH = c.kv_heads, hd = c.head_dim, F = c.ffn;
+  const int64_t V = c.vocab, qn = p->qn, qdim = p->qdim;
+  if (c.quantized) SM_TRY(fake_quantize(p, st));
+  // ---- activation arena: per layer x0, h, qkv, q, k, v, o, lse, x1, h2, u, a
+  const int64_t per_layer = M * (d + d + qn + qdim + 2 * p->kvdim + qdim + H + d + d + 2 * F + F);
+  const int64_t fixed = M * d /*x*/ + M * d /*hf*/ + R * d /*hr*/ + R * V /*logits*/ +
+                        M * d /*dx*/ + M * d /*dhf*/ + R * d /*dhr*/ + M * 2 * F /*du*/ +
+                        M * F /*da*/ + M * d /*dh*/ + M * qdim /*do*/ + M * qdim /*dq*/ +
+                        2 * S * KVH * L * hd /*dk dv*/ + M * qn /*dqkv*/ + M /*rinv*/ +
+                        S * H * L /*delta*/ + R /*row scale*/ + d /*dgamma final*/ + S /*pos0*/;
+  const size_t bytes = (size_t)(per_layer * c.layers + fixed) * 4 + (size_t)M * 4 /*ids*/ +
+                       (size_t)R * 8 /*rows*/ + (size_t)(12 * c.layers + 32) * 256;
+  SM_TRY(grow(p->act, bytes));
+  char* cur = (char*)p->act.p;
+  auto take = [&](int64_t n, size_t elem = 4) {
+    char* r = cur;
+    cur += ((size_t)n * elem + 255) / 256 * 256;
+    return (void*)r;
+  };
+  struct Saved { float *x0, *h, *qkv, *q, *k, *v, *o, *lse, *x1, *h2, *u, *a; };
+  std::vector<Saved> sv(c.layers);
+  for (auto& s : sv) {
+    s.x0 = (float*)take(M * d); s.h = (float*)take(M * d); s.qkv = (float*)take(M * qn);
+    s.q = (float*)take(M * qdim); s.k = (float*)take(S * KVH * L * hd);
+    s.v = (float*)take(S * KVH * L * hd); s.o = (float*)take(M * qdim);
+    s.lse = (float*)take(S * H * L); s.x1 = (float*)take(M * d); s.h2 = (float*)take(M * d);
+    s.u = (float*)take(M * 2 * F); s.a = (float*)take(M * F);
+  }
+  float* x = (float*)take(M * d);
+  float* hf = (float*)take(M * d);
+  float* hr = (float*)take(R * d);
+  float* logits = (float*)take(R * V);
+  float* dx = (float*)take(M * d);
+  float* dhf = (float*)take(M * d);
+  float* dhr = (float*)take(R * d);
+  float* du = (float*)take(M * 2 * F);
+  float* da = (float*)take(M * F);
+  float* dh = (float*)take(M * d);
+  float* dO = (float*)take(M * qdim);
+  float* dq = (float*)take(M * qdim);
+  float* dk = (float*)take(S * KVH * L * hd);
+  float* dv = (float*)take(S * KVH * L * hd);
+  float* dqkv = (float*)take(M * qn);
+  float* rinv = (float*)take(M);
+  float* delta = (float*)take(S * H * L);
+  float* rscale = (float*)take(R);
+  float* dgf = (float*)take(d);
+  int32_t* pos0 = (int32_t*)take(S);
+  int32_t* ids = (int32_t*)take(M);
+  int64_t* rows = (int64_t*)take(R, 8);
+  SM_HIP(hipMemsetAsync(pos0, 0, (size_t)S * 4, st));
+  build_ids_rows<<<blocks256(std::max(M, R)), 256, 0, st>>>(prompts, tokens, (int)S, (int)P,
+                                                            (int)N, ids, rows);
+  // ---- forward (recompute with activations kept)
+  SM_TRY(sm_embed(fw(p, SM_W_EMBED), SM_F32, ids, M, d, V, 1.0f, x, stream));
+  for (int l = 0; l < c.layers; ++l) {
+    Saved& s = sv[l];
+    SM_HIP(hipMemcpyAsync(s.x0, x, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
+    SM_TRY(sm_rmsnorm(s.x0, fwl(p, SM_W_ATTN_NORM, l), M, d, c.norm_eps, s.h, SM_F32, stream));
+    SM_TRY(sm_gemm_ex(0, 1, M, qn, d, 1.f, s.h, d, fwl(p, SM_W_QKV, l), d, 0.f, s.qkv, qn, stream));
+    SM_TRY(sm_rope_qk(s.qkv, p->rope, pos0, S, L, H, KVH, hd, 0, stream));
+    split_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(s.qkv, (int)S, (int)L, (int)H, (int)KVH,
+                                                     (int)hd, s.q, s.k, s.v);
+    SM_TRY(sm_attn_prefill_lse(s.q, s.k, s.v, pos0, s.o, s.lse, SM_F32, SM_F32, S, L, H, KVH, L,
+                               hd, stream));
+    SM_HIP(hipMemcpyAsync(s.x1, s.x0, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
+    SM_TRY(sm_gemm_ex(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
+                      stream));
+    SM_TRY(sm_rmsnorm(s.x1, fwl(p, SM_W_FFN_NORM, l), M, d, c.norm_eps, s.h2, SM_F32, stream));
+    SM_TRY(sm_gemm_ex(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
+                      stream));
+    SM_TRY(sm_swiglu(s.u, SM_F32, M, F, s.a, stream));
+    SM_HIP(hipMemcpyAsync(x, s.x1, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
+    SM_TRY(sm_gemm_ex(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
+  }
+  SM_TRY(sm_rmsnorm(x, fw(p, SM_W_FINAL_NORM), M, d, c.norm_eps, hf, SM_F32, stream));
+  gather_rows_f32<<<blocks256(R * d), 256, 0, st>>>(hf, rows, R, (int)d, hr);
+  SM_TRY(sm_gemm_ex(0, 1, R, V, d, 1.f, hr, d, fw(p, SM_W_LM_HEAD), d, 0.f, logits, V, stream));
+  SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, lp_cur, nullptr, nullptr, 1.f, nullptr,
+                    nullptr, stream));
+  // ---- the frozen reference and the loss
+  const bool use_ref = reference && lp_ref;
+  if (use_ref) SM_TRY(sm_rl_logprobs(reference, prompts, tokens, S, P, N, 0, lp_ref, stream));
+  SM_TRY(sm_grpo_loss(rewards, lp_cur, behavior_lp, use_ref ? lp_ref : nullptr, mask, groups,
+                      group_size, N, clip_epsilon, advantage_epsilon, kl_coefficient, group_stats,
+                      nullptr, dlp, flags, stream));
+  // ---- backward of sum(dlp * lp), gradients added to the staged ones.
+  // d lp / d logits = onehot - softmax: the CE gradient with scale -dlp per row
+  neg_f32<<<blocks256(R), 256, 0, st>>>(dlp, R, rscale);
+  SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, nullptr, nullptr, logits, 1.f, rscale,
+                    nullptr, stream));
+  SM_TRY(sm_gemm_ex(1, 0, V, d, R, 1.f, logits, V, hr, d, 1.f, p->g[SM_W_LM_HEAD], d, stream));
+  SM_TRY(sm_gemm_ex(0, 0, R, d, V, 1.f, logits, V, fw(p, SM_W_LM_HEAD), d, 0.f, dhr, d, stream));
+  SM_HIP(hipMemsetAsync(dhf, 0, (size_t)M * d * 4, st));
+  scatter_rows_f32<<<blocks256(R * d), 256, 0, st>>>(dhr, rows, R, (int)d, dhf);
+  SM_TRY(sm_rmsnorm_backward(x, fw(p, SM_W_FINAL_NORM), dhf, M, d, c.norm_eps, 0, dx, dgf, rinv,
+                             stream));
+  SM_TRY(sm_axpby(dgf, p->g[SM_W_FINAL_NORM], d, 1.f, 1.f, stream));
+  for (int l = c.layers - 1; l >= 0; --l) {
+    Saved& s = sv[l];
+    // FFN: x = x1 + swiglu(h2 W_in^T) W_down^T
+    SM_TRY(sm_gemm_ex(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
+    SM_TRY(sm_gemm_ex(1, 0, d, F, M, 1.f, dx, d, s.a, F, 1.f, gl(p, SM_W_DOWN, l), F, stream));
+    SM_TRY(sm_swiglu_backward(s.u, da, SM_F32, M, F, du, stream));
+    SM_TRY(sm_gemm_ex(1, 0, 2 * F, d, M, 1.f, du, 2 * F, s.h2, d, 1.f, gl(p, SM_W_IN, l), d,
+                      stream));
+    SM_TRY(sm_gemm_ex(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
+                      stream));
+    SM_TRY(sm_rmsnorm_backward(s.x1, fwl(p, SM_W_FFN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
+                               gl(p, SM_W_FFN_NORM, l), rinv, stream));
+    // attention: x1 = x0 + attn(rope(h W_qkv^T)) W_o^T
+    SM_TRY(sm_gemm_ex(0, 0, M, qdim, d, 1.f, dx, d, fwl(p, SM_W_O, l), qdim, 0.f, dO, qdim,
+                      stream));
+    SM_TRY(sm_gemm_ex(1, 0, d, qdim, M, 1.f, dx, d, s.o, qdim, 1.f, gl(p, SM_W_O, l), qdim,
+                      stream));
+    SM_TRY(sm_attn_backward_f32(s.q, s.k, s.v, s.o, dO, s.lse, S, L, H, KVH, hd, dq, dk, dv,
+                                delta, stream));
+    merge_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(dq, dk, dv, (int)S, (int)L, (int)H,
+                                                     (int)KVH, (int)hd, dqkv);
+    SM_TRY(sm_rope_qk(dqkv, p->rope, pos0, S, L, H, KVH, hd, 1, stream));
+    SM_TRY(sm_gemm_ex(1, 0, qn, d, M, 1.f, dqkv, qn, s.h, d, 1.f, gl(p, SM_W_QKV, l), d, stream));
+    SM_TRY(sm_gemm_ex(0, 0, M, d, qn, 1.f, dqkv, qn, fwl(p, SM_W_QKV, l), d, 0.f, dh, d, stream));
+    SM_TRY(sm_rmsnorm_backward(s.x0, fwl(p, SM_W_ATTN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
+                               gl(p, SM_W_ATTN_NORM, l), rinv, stream));
+  }
+  SM_TRY(sm_embed_backward(ids, dx, M, d, V, p->g[SM_W_EMBED], stream));
+  SM_LAUNCH_CHECK();
+  p->staged = true;
+  return SM_OK;
+}
+
+extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale,
+                                        float* grad_norm, void* stream) {
+  SM_REQUIRE(p, "sm_policy_optimizer_step: null policy");
+  SM_REQUIRE(std::isfinite(learning_rate_scale) && learning_rate_scale >= 0.0,
+             "learning rate scale must be finite and non-negative");
+  hipStream_t st = as_stream(stream);
+  // global gradient norm over every staged gradient, then the clip
+  int64_t maxn = 0;
+  for (int k = 0; k < kKinds; ++k) maxn = std::max(maxn, p->rows_per_layer[k] * p->cols[k]);
+  int64_t ns_floats = 0;  // Newton-Schulz scratch: 2 N K + 2 min(N, K)^2 + 1 per projection
+  for (int k = 0; k < kKinds; ++k)
+    if (is_muon_kind(k)) {
+      const int64_t n = p->rows_per_layer[k], kk = p->cols[k], r = std::min(n, kk);
+      ns_floats = std::max(ns_floats, 2 * n * kk + 2 * r * r + 1);
+    }
+  int64_t nparts = 0;
+  for (int k = 0; k < kKinds; ++k) nparts += ceil_div(p->count[k], kSumChunk);
+  const size_t head = ((size_t)(nparts + 1) * 8 + 255) / 256 * 256;
+  SM_TRY(grow(p->scratch, head + (size_t)(ns_floats + maxn) * 4));
+  double* acc = (double*)p->scratch.p;
+  double* parts = acc + 1;
+  float* upd = (float*)((char*)p->scratch.p + head);
+  float* ns_tmp = upd + maxn;
+  for (int k = 0, off = 0; k < kKinds; ++k) {
+    const int64_t nb = ceil_div(p->count[k], kSumChunk);
+    sumsq_kernel<<<(unsigned)nb, 256, 0, st>>>(p->g[k], p->count[k], parts + off);
+    off += (int)nb;
+  }
+  sum_parts_kernel<<<1, 1, 0, st>>>(parts, nparts, acc);
+  SM_LAUNCH_CHECK();
+  double sumsq = 0.0;
+  SM_HIP(hipMemcpyAsync(&sumsq, acc, 8, hipMemcpyDeviceToHost, st));
+  SM_HIP(hipStreamSynchronize(st));
+  const float norm = (float)std::sqrt(sumsq);
+  if (grad_norm) *grad_norm = norm;
+  SM_REQUIRE(std::isfinite(norm), "non-finite gradient norm at optimizer step %lld: %g",
+             (long long)(p->adam_step + 1), (double)norm);
+  for (int k = 0; k < kKinds; ++k)
+    clip_scale_kernel<<<blocks256(p->count[k]), 256, 0, st>>>(p->g[k], p->count[k], acc,
+                                                              p->opt.grad_clip);
+  SM_LAUNCH_CHECK();
+  const auto& o = p->opt;
+  const float lr = (float)(o.lr * learning_rate_scale);
+  const float muon_lr = (float)(o.muon_lr * learning_rate_scale);
+  const bool muon = o.muon_lr > 0.f;
+  ++p->adam_step;
+  if (muon) ++p->muon_step;
+  for (int k = 0; k < kKinds; ++k) {
+    if (muon && is_muon_kind(k)) {
+      // BatchedMuon::step (muon.rs:196-215): momentum, Newton-Schulz, and the
+      // learning rate scaled by sqrt(max(1, d_in / d_out)) of Burn's [d_in, d_out]
+      const int64_t N = p->rows_per_layer[k], K = p->cols[k], n = N * K;
+      const float adj = muon_lr * std::sqrt(std::max(1.0f, (float)K / (float)N));
+      for (int l = 0; l < p->cfg.layers; ++l) {
+        float* w = p->w[k] + (size_t)l * n;
+        float* gr = p->g[k] + (size_t)l * n;
+        float* vel = p->m1[k] + (size_t)l * n;
+        SM_TRY(sm_muon_momentum(gr, vel, upd, n, kMuonMomentum, p->muon_step == 1 ? 1 : 0, stream));
+        SM_TRY(newton_schulz(upd, N, K, ns_tmp, st));
+        SM_TRY(sm_axpby(upd, w, n, -adj, 1.f, stream));
+      }
+    } else {
+      SM_TRY(sm_adamw_step(p->w[k], p->g[k], p->m1[k], p->m2[k], p->count[k], lr, o.beta1,
+                           o.beta2, o.eps, o.weight_decay, p->adam_step, stream));
+    }
+    zero_f32<<<blocks256(p->count[k]), 256, 0, st>>>(p->g[k], p->count[k]);
+  }
+  SM_LAUNCH_CHECK();
+  p->staged = false;
+  return SM_OK;
+}

@@ -15,6 +15,8 @@ optimizers are ``sm_adamw_step`` and Muon's momentum / Newton-Schulz over
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import numpy as np
 import torch
 
@@ -248,3 +250,98 @@ def newton_schulz(g: torch.Tensor) -> torch.Tensor:
     if transpose:
         x = x.t().contiguous()
     return x.t().contiguous()  # back to [out, in]
+
+
+# ------------------------------------------------------- native policy ---
+
+class OptimizerConfigC(C.Structure):
+    _fields_ = [(n, C.c_float) for n in ("lr", "beta1", "beta2", "eps", "weight_decay",
+                                         "muon_lr", "grad_clip")]
+
+
+_POLICY_KINDS = {"embed": 0, "attn_norm": 1, "qkv": 2, "o": 3, "ffn_norm": 4, "in": 5,
+                 "down": 6, "final_norm": 7, "lm_head": 8}
+
+
+class Policy:
+    """The library's trainable policy (``sm_policy``): prepare_device_batch's
+    recompute, GRPO loss and staged backward in one call, optimizer_step in
+    another (posttrain.rs:1288-1305), with the trainer's optimizer settings as
+    defaults (AdamW 3e-4 / 0.9 / 0.95 / 1e-8 / wd 0.1, global-norm clip 1.0;
+    ``muon_lr > 0`` adds Muon for the per-layer projections)."""
+
+    def __init__(self, cfg: ModelConfig, weights: dict, device, lr=3e-4, betas=(0.9, 0.95),
+                 eps=1e-8, weight_decay=0.1, muon_lr=0.0, grad_clip=1.0):
+        from . import _lib
+        self.cfg, self.dev = cfg, device
+        self._h = C.c_void_p()
+        oc = OptimizerConfigC(lr, betas[0], betas[1], eps, weight_decay, muon_lr, grad_clip)
+        cc = cfg.c()
+        _lib.check(_lib.lib().sm_policy_create(C.byref(cc), C.byref(oc), C.byref(self._h)))
+        for name, arr in weights.items():
+            t = torch.as_tensor(np.ascontiguousarray(arr, dtype=np.float32)).to(device)
+            if name in LAYER_KEYS:
+                for i in range(cfg.layers):
+                    call("sm_policy_set_tensor", self._h, _POLICY_KINDS[name], i,
+                         t[i].contiguous().data_ptr(), _st())
+            else:
+                call("sm_policy_set_tensor", self._h, _POLICY_KINDS[name], -1, t.data_ptr(),
+                     _st())
+        torch.cuda.synchronize()
+
+    def close(self):
+        if self._h.value:
+            from . import _lib
+            _lib.lib().sm_policy_destroy(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def tensor(self, name: str, layer: int = -1, gradient: bool = False) -> torch.Tensor:
+        """A master weight (or its staged gradient), [out, in] rows."""
+        c = self.cfg
+        d, F, qn = c.d_model, c.ffn, (c.heads + 2 * c.kv_heads) * c.head_dim
+        shape = {"embed": (c.vocab, d), "lm_head": (c.vocab, d), "attn_norm": (d,),
+                 "ffn_norm": (d,), "final_norm": (d,), "qkv": (qn, d),
+                 "o": (d, c.heads * c.head_dim), "in": (2 * F, d), "down": (d, F)}[name]
+        out = torch.empty(shape, dtype=torch.float32, device=self.dev)
+        call("sm_policy_get_tensor", self._h, _POLICY_KINDS[name], layer, out.data_ptr(),
+             int(gradient), _st())
+        return out
+
+    def prepare(self, reference, prompts, tokens, behavior_lp, rewards, mask=None,
+                clip_epsilon=0.2, advantage_epsilon=1e-6, kl_coefficient=0.04):
+        """sm_policy_prepare: like ``model.rl_prepare`` for the trainable
+        policy; the gradient of the loss is added to the staged gradients."""
+        groups, G = rewards.shape
+        S, P = prompts.shape
+        N = tokens.shape[1]
+        dev = prompts.device
+        lp_cur = torch.empty(S, N, dtype=torch.float32, device=dev)
+        lp_ref = (torch.empty(S, N, dtype=torch.float32, device=dev)
+                  if reference is not None else None)
+        stats = torch.empty(groups, 5, dtype=torch.float32, device=dev)
+        dlp = torch.empty(S, N, dtype=torch.float32, device=dev)
+        flags = torch.empty(groups, dtype=torch.int32, device=dev)
+        call("sm_policy_prepare", self._h, reference.handle if reference is not None else None,
+             prompts.data_ptr(), tokens.data_ptr(), behavior_lp.data_ptr(), rewards.data_ptr(),
+             None if mask is None else mask.data_ptr(), groups, G, P, N, float(clip_epsilon),
+             float(advantage_epsilon), float(kl_coefficient), lp_cur.data_ptr(),
+             None if lp_ref is None else lp_ref.data_ptr(), stats.data_ptr(), dlp.data_ptr(),
+             flags.data_ptr(), _st())
+        return {"lp_cur": lp_cur, "lp_ref": lp_ref, "stats": stats, "dlp": dlp, "flags": flags}
+
+    def optimizer_step(self, learning_rate_scale: float = 1.0) -> float:
+        """sm_policy_optimizer_step; returns the pre-clip global gradient norm."""
+        norm = C.c_float()
+        call("sm_policy_optimizer_step", self._h, float(learning_rate_scale), C.byref(norm),
+             _st())
+        return norm.value
+
+    def install(self, model: Model) -> None:
+        call("sm_policy_install", self._h, model.handle, _st())
+        torch.cuda.synchronize()

@@ -1,0 +1,168 @@
+"""The library's trainable policy (sm_policy_*): prepare_device_batch's
+recompute + GRPO loss + staged backward in one C call and optimizer_step in
+another (posttrain.rs:1288-1305), checked against float64 autograd of an
+independent torch restatement of the decoder, against torch.optim.AdamW, the
+global-norm clip of gradient_norm_and_clip (main.rs:667-694), the Python
+composition of Muon, and end to end (a GRPO update lowers the loss; a
+quantized policy's recompute equals the quantized rollout model's)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from summa_amd import _lib, train
+from summa_amd.model import Model, ModelConfig, rl_prepare
+
+from test_train_gpu import CFG, _torch_lp
+
+pytestmark = pytest.mark.gpu
+
+
+def _batch(cfg, seed, dev, B=2, G=4, P=8, N=6):
+    rng = np.random.default_rng(seed)
+    prompts = torch.from_numpy(rng.integers(0, cfg.vocab, (B * G, P)).astype(np.int32)).to(dev)
+    tokens = torch.from_numpy(rng.integers(0, cfg.vocab, (B * G, N)).astype(np.int32)).to(dev)
+    rewards = torch.from_numpy(rng.random((B, G)).astype(np.float32)).to(dev)
+    return prompts, tokens, rewards
+
+
+def test_native_policy_gradient_matches_autograd(dev):
+    w = oracle.random_weights(CFG.oracle_cfg(), seed=11, std=0.05)
+    pol = train.Policy(CFG, w, dev)
+    prompts, tokens, rewards = _batch(CFG, 2, dev)
+    beh = torch.full(tokens.shape, -7.0, device=dev)  # off-policy rollouts: rho != 1
+    out = pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
+    assert int(out["flags"].abs().sum()) == 0
+    lp = out["lp_cur"].cpu()
+    dlp = out["dlp"].cpu().double()
+    wt = {k: torch.from_numpy(np.asarray(v, dtype=np.float64)).requires_grad_(True)
+          for k, v in w.items()}
+    lp_t = _torch_lp(wt, CFG, prompts.cpu(), tokens.cpu())
+    np.testing.assert_allclose(lp.numpy(), lp_t.detach().numpy(), atol=2e-5)
+    # the GRPO loss and dlp are the oracle's on these log-probs
+    st_or, _, dlp_or, err = oracle.grpo_loss(rewards.cpu().numpy(),
+                                             lp.numpy().reshape(2, 4, 6),
+                                             beh.cpu().numpy().reshape(2, 4, 6), None, None,
+                                             0.2, 1e-6, 0.0)
+    assert err == 0
+    np.testing.assert_allclose(dlp.numpy(), dlp_or.reshape(8, 6), rtol=1e-4, atol=1e-9)
+    (dlp * lp_t).sum().backward()
+    for k, t in wt.items():
+        layers = range(CFG.layers) if k in train.LAYER_KEYS else [-1]
+        for layer in layers:
+            got = pol.tensor(k, layer, gradient=True).cpu().double()
+            want = t.grad[layer] if layer >= 0 else t.grad
+            scale = want.abs().max().item() + 1e-12
+            assert (got - want).abs().max().item() / scale < 2e-4, (k, layer)
+    # a second prepare adds the same gradient again (staged accumulation)
+    g1 = pol.tensor("qkv", 1, gradient=True)
+    pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
+    torch.testing.assert_close(pol.tensor("qkv", 1, gradient=True), 2 * g1, rtol=1e-5, atol=1e-7)
+
+
+def test_native_optimizer_step_adamw_and_clip(dev):
+    """AdamW on every tensor after the global-norm clip, against torch in f64
+    fed with the policy's own staged gradients."""
+    w = oracle.random_weights(CFG.oracle_cfg(), seed=13, std=0.05)
+    clip = 1e-3  # well below the batch's gradient norm: the clip engages
+    pol = train.Policy(CFG, w, dev, lr=1e-2, weight_decay=0.1, grad_clip=clip)
+    prompts, tokens, rewards = _batch(CFG, 3, dev)
+    beh = torch.full(tokens.shape, -7.0, device=dev)
+    pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
+    names = list(w)
+    grads = {}
+    for k in names:
+        if k in train.LAYER_KEYS:
+            grads[k] = torch.stack([pol.tensor(k, i, gradient=True) for i in range(CFG.layers)])
+        else:
+            grads[k] = pol.tensor(k, gradient=True)
+    norm = float(torch.sqrt(sum((g.double() ** 2).sum() for g in grads.values())))
+    got_norm = pol.optimizer_step(0.5)  # learning-rate scale 0.5
+    assert abs(got_norm - norm) <= 1e-5 * norm
+    assert norm > clip
+    for k in names:
+        tp = torch.tensor(np.asarray(w[k], dtype=np.float64), requires_grad=True)
+        opt = torch.optim.AdamW([tp], lr=1e-2 * 0.5, betas=(0.9, 0.95), eps=1e-8,
+                                weight_decay=0.1)
+        tp.grad = grads[k].cpu().double() * (clip / norm)
+        opt.step()
+        if k in train.LAYER_KEYS:
+            got = torch.stack([pol.tensor(k, i) for i in range(CFG.layers)])
+        else:
+            got = pol.tensor(k)
+        np.testing.assert_allclose(got.cpu().numpy(), tp.detach().numpy(), rtol=1e-5, atol=1e-6)
+        assert float(pol.tensor(k, 0 if k in train.LAYER_KEYS else -1,
+                                gradient=True).abs().max()) == 0.0  # cleared
+
+
+def test_native_muon_matches_python_composition(dev):
+    w = oracle.random_weights(CFG.oracle_cfg(), seed=14, std=0.05)
+    pol = train.Policy(CFG, w, dev, lr=1e-3, muon_lr=0.02, grad_clip=0.0)
+    prompts, tokens, rewards = _batch(CFG, 4, dev)
+    beh = torch.full(tokens.shape, -7.0, device=dev)
+    pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
+    ref = train.Fp32Policy(CFG, w, dev)
+    grads = {k: torch.stack([pol.tensor(k, i, gradient=True) for i in range(CFG.layers)])
+             for k in ref.muon_keys()}
+    pol.optimizer_step(1.0)
+    ref.muon_step(grads, ref.muon_keys(), lr=0.02)
+    for k in ref.muon_keys():
+        for i in range(CFG.layers):
+            torch.testing.assert_close(pol.tensor(k, i), ref.p[k][i], rtol=1e-5, atol=1e-6)
+
+
+def test_native_grpo_update_lowers_the_loss(dev):
+    """Rollouts from the inference model, prepare (reference = the frozen
+    initial model), an optimizer step, install: the same batch's GRPO loss
+    drops and the model now holds the policy's weights."""
+    w = oracle.random_weights(CFG.oracle_cfg(), seed=15, std=0.05)
+    model, frozen = Model(CFG), Model(CFG)
+    model.load_host_weights(w, dev)
+    frozen.load_host_weights(w, dev)
+    pol = train.Policy(CFG, w, dev)
+    G, B = 8, 2
+    prompts = torch.from_numpy(np.random.default_rng(4).integers(0, CFG.vocab, (B * G, 8))
+                               .astype(np.int32)).to(dev)
+    tok, beh = model.generate(prompts, 6, temperature=1.0, seed=9)
+    rewards = torch.from_numpy(np.random.default_rng(5).random((B, G)).astype(np.float32)).to(dev)
+    out0 = pol.prepare(frozen, prompts, tok, beh, rewards)
+    l0 = float(out0["stats"][:, 0].sum())
+    np.testing.assert_allclose(out0["lp_cur"].cpu().numpy(), beh.cpu().numpy(), atol=1e-5)
+    pol.optimizer_step(1.0)
+    pol.install(model)
+    out1 = rl_prepare(model, frozen, prompts, tok, beh, rewards)
+    l1 = float(out1["stats"][:, 0].sum())
+    assert l1 < l0, (l0, l1)
+    probe = pol.prepare(frozen, prompts, tok, beh, rewards)
+    np.testing.assert_allclose(out1["lp_cur"].cpu().numpy(), probe["lp_cur"].cpu().numpy(),
+                               atol=1e-5)
+
+
+def test_quantized_policy_recompute_equals_rollout_model(dev):
+    """A quantized config trains f32 masters with fake-quantized forward
+    weights: its recompute equals the installed Q4 model's log-probs (2e-3,
+    the 16-bit KV cache of the model being the only difference), and an
+    update moves the installed model."""
+    qc = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
+                     vocab=1024, max_seq=32, quantized=True)
+    w = oracle.random_weights(qc.oracle_cfg(), seed=16, std=0.05)
+    pol = train.Policy(qc, w, dev)
+    model = Model(qc)
+    pol.install(model)
+    prompts, _, rewards = _batch(qc, 6, dev)
+    tok, beh = model.generate(prompts, 6, temperature=1.0, seed=3)
+    out = pol.prepare(None, prompts, tok, beh, rewards, kl_coefficient=0.0)
+    err = float((out["lp_cur"] - beh).abs().max())
+    print(f"quantized policy recompute vs Q4 rollout log-probs: {err:.2e}", flush=True)
+    assert err <= 2e-3
+    before = model.logprobs(prompts, tok)
+    pol.optimizer_step(1.0)
+    pol.install(model)
+    assert float((model.logprobs(prompts, tok) - before).abs().max()) > 1e-4
+
+
+def test_policy_rejects_bad_config(dev):
+    bad = ModelConfig(layers=1, d_model=256, heads=4, kv_heads=4, head_dim=64, ffn=512,
+                      vocab=100, max_seq=16, quantized=True, experts=4, expert_ffn=256)
+    with pytest.raises(_lib.SummaError, match="dense decoder"):
+        train.Policy(bad, {}, dev)
