@@ -573,6 +573,11 @@ int sm_rl_generate(sm_model* model, const int32_t* prompts, int64_t S, int64_t P
 int sm_rl_generate_ex(sm_model* model, const int32_t* prompts, int64_t S, int64_t P, int64_t N,
                       const sm_sampling* sampling, uint64_t seed, int32_t* tokens,
                       float* behavior_lp, int32_t* lengths, void* stream);
+/* The completion mask of rollouts that stop at EOS: mask[s, n] = 1 while
+ * n < lengths[s] (the tokens generated, EOS included, as sm_rl_generate_ex
+ * reports them), else 0, f32 [S, N] (the active mask grpo_loss_tensor takes,
+ * posttrain.rs:874-1028; the padded tail must not enter the loss). */
+int sm_completion_mask(const int32_t* lengths, int64_t S, int64_t N, float* mask, void* stream);
 /* Log-prob recompute (padded_group_log_probabilities /
  * equal_length_continuation_log_probabilities, tensor_sleep.rs:2531-2689):
  * lp_out[s, n] = log_softmax(model(prompt ‖ tokens[:, :N-1]))[P-1+n][tokens[s, n]].

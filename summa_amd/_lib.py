@@ -89,6 +89,7 @@ SIGNATURES: dict[str, tuple] = {
     "sm_model_bind_workspace": (i32, [vp, vp, i64, i64, i64, i64, i64]),
     "sm_rl_generate": (i32, [vp, vp, i64, i64, i64, f32, u64, vp, vp, vp]),
     "sm_rl_generate_ex": (i32, [vp, vp, i64, i64, i64, vp, u64, vp, vp, vp, vp]),
+    "sm_completion_mask": (i32, [vp, i64, i64, vp, vp]),
     "sm_rl_logprobs": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "sm_rl_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64, i64,
                             vp, vp, vp, vp, vp, vp]),

@@ -318,3 +318,25 @@ extern "C" int sm_sample(const float* logits, int64_t rows, int64_t ld, int64_t 
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
+
+namespace sm {
+namespace {
+__global__ void completion_mask_kernel(const int32_t* __restrict__ lengths, int64_t S, int64_t N,
+                                       float* __restrict__ mask) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < S * N) mask[i] = (i % N) < (int64_t)lengths[i / N] ? 1.f : 0.f;
+}
+}  // namespace
+}  // namespace sm
+
+extern "C" int sm_completion_mask(const int32_t* lengths, int64_t S, int64_t N, float* mask,
+                                  void* stream) {
+  using namespace sm;
+  SM_REQUIRE(lengths && mask, "sm_completion_mask: null buffer");
+  SM_REQUIRE(S >= 0 && N > 0, "sm_completion_mask: bad shape");
+  if (S == 0) return SM_OK;
+  completion_mask_kernel<<<(unsigned)ceil_div(S * N, 256), 256, 0, as_stream(stream)>>>(
+      lengths, S, N, mask);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}

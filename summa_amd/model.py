@@ -203,15 +203,29 @@ class Model:
         return lp
 
 
+def completion_mask(lengths: torch.Tensor, N: int) -> torch.Tensor:
+    """sm_completion_mask: f32 [S, N], 1 for n < lengths[s] (EOS included)."""
+    S = lengths.shape[0]
+    mask = torch.empty(S, N, dtype=torch.float32, device=lengths.device)
+    call("sm_completion_mask", lengths.data_ptr(), S, N, mask.data_ptr(), _stream())
+    return mask
+
+
 def rl_prepare(policy: Model, reference: Model | None, prompts, tokens, behavior_lp, rewards,
                mask=None, clip_epsilon=0.2, advantage_epsilon=1e-6, kl_coefficient=0.04,
-               max_tokens_per_forward=0):
+               max_tokens_per_forward=0, lengths=None):
     """prepare_device_batch numerics: returns dict of device tensors (lp_cur, lp_ref,
-    stats [groups, 5], dlp [S, N], flags [groups]) and the GrpoDeviceBatchResult sums."""
+    stats [groups, 5], dlp [S, N], flags [groups]) and the GrpoDeviceBatchResult sums.
+    Rollouts from ``generate_ex`` that stopped at EOS pass their ``lengths``
+    (the completion mask is built from them) or an explicit ``mask``."""
     groups, G = rewards.shape
     S, P = prompts.shape
     N = tokens.shape[1]
     dev = prompts.device
+    if lengths is not None:
+        if mask is not None:
+            raise ValueError("rl_prepare: pass either mask or lengths")
+        mask = completion_mask(lengths, N)
     lp_cur = torch.empty(S, N, dtype=torch.float32, device=dev)
     lp_ref = torch.empty(S, N, dtype=torch.float32, device=dev) if reference is not None else None
     stats = torch.empty(groups, 5, dtype=torch.float32, device=dev)

@@ -190,3 +190,43 @@ def test_generate_ex_teacher_forced_against_oracle(dev, case):
                 assert abs(key[a] - key[b]) < 1e-4, f"seq {s} step {n}: {key[a]} vs {key[b]}"
                 near += 1
     print(f"near-tie positions: {near}", flush=True)
+
+
+def test_eos_stopped_rollouts_through_rl_prepare(dev):
+    """Rollouts that stop at EOS enter the GRPO loss through their completion
+    mask (n < lengths[s]): rl_prepare(lengths=...) equals the oracle's loss on
+    the masked rows, and the padded tail gets no gradient."""
+    from summa_amd.model import completion_mask, rl_prepare
+    cfg = CFG0.oracle_cfg()
+    w = oracle.random_weights(cfg, seed=7, std=0.05)
+    m, ref = Model(CFG0), Model(CFG0)
+    m.load_host_weights(w, dev)
+    ref.load_host_weights(oracle.random_weights(cfg, seed=8, std=0.05), dev)
+    groups, G, P, N, seed = 2, 8, 8, 24, 99
+    S = groups * G
+    prompts = torch.from_numpy(np.random.default_rng(3).integers(0, cfg["V"], (S, P))
+                               .astype(np.int32)).to(dev)
+    kw = dict(max_new_tokens=N, temperature=0.9, top_k=20)
+    # an EOS that rollout 0 emits at its third step at the latest: the token it
+    # samples there without one (the draws do not depend on the EOS option)
+    t0, _, _ = m.generate_ex(prompts, SamplingConfig(**kw), seed=seed)
+    eos = int(t0[0, 2])
+    tok, beh, lens = m.generate_ex(prompts, SamplingConfig(eos_token=eos, **kw), seed=seed)
+    L = lens.cpu().numpy()
+    assert (L < N).any(), "no rollout stopped at EOS"
+    mask_h = (np.arange(N)[None, :] < L[:, None]).astype(np.float64)
+    np.testing.assert_array_equal(completion_mask(lens, N).cpu().numpy(), mask_h)
+    rewards = torch.from_numpy(np.random.default_rng(4).random((groups, G)).astype(np.float32)).to(dev)
+    out = rl_prepare(m, ref, prompts, tok, beh, rewards, lengths=lens)
+    with pytest.raises(ValueError, match="either mask or lengths"):
+        rl_prepare(m, ref, prompts, tok, beh, rewards, mask=completion_mask(lens, N), lengths=lens)
+    sh = (groups, G, N)
+    st_or, _, dlp_or, err = oracle.grpo_loss(
+        rewards.cpu().numpy(), out["lp_cur"].cpu().numpy().reshape(sh),
+        beh.cpu().numpy().reshape(sh), out["lp_ref"].cpu().numpy().reshape(sh),
+        mask_h.reshape(sh), 0.2, 1e-6, 0.04)
+    assert err == 0
+    np.testing.assert_allclose(out["stats"].cpu().numpy(), st_or, rtol=1e-4, atol=1e-6)
+    dlp = out["dlp"].cpu().numpy()
+    np.testing.assert_allclose(dlp, dlp_or.reshape(S, N), rtol=1e-4, atol=1e-9)
+    assert (dlp[mask_h == 0] == 0).all()
