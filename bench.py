@@ -158,7 +158,7 @@ def q4_gemv_sweep(model_cfg: dict, dev, ms=(1, 2, 4, 8, 16), reps: int = 10) -> 
     launch = N*K*(0.5 + 2/128) + M*K*2 (x) + M*N*4 (y, f32)."""
     import torch
 
-    from summa_amd import ops
+    from summa_amd import _lib, ops
 
     d, V = model_cfg["d_model"], model_cfg["vocab"]
     mats = []
@@ -202,6 +202,25 @@ def q4_gemv_sweep(model_cfg: dict, dev, ms=(1, 2, 4, 8, 16), reps: int = 10) -> 
         gbs = nbytes / sweep_ms / 1e6
         res["by_M"][str(M)] = {"sweep_ms": round(sweep_ms, 4), "bytes": nbytes,
                                "GBs": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        if M == 1:
+            # the same GEMVs as one sm_q4_gemv_multi launch (every matrix is
+            # independent here), replayed the same way
+            batch = ops.GemvBatch([(m, xi, y, _lib.SM_EPI_STORE_F32)
+                                   for m, xi, y in zip(mats, xs, ys)])
+            batch.launch()
+            torch.cuda.synchronize()
+            a, b = _events(2)
+            a.record(st)
+            for _ in range(reps):
+                batch.launch()
+            b.record(st)
+            torch.cuda.synchronize()
+            one_ms = a.elapsed_time(b) / reps
+            res["by_M"]["1"].update(
+                launches_ms=res["by_M"]["1"]["sweep_ms"], single_launch_ms=round(one_ms, 4),
+                single_launch_GBs=round(nbytes / one_ms / 1e6, 1),
+                single_launch_frac=round(nbytes / one_ms / 1e6 / HBM_PEAK_GBS, 4))
+            del batch
         del graph, xs, ys, x
     # The largest GEMV (LM head) sustained: 4 distinct copies (> 256 MB MALL)
     # replayed back to back, so each launch streams its matrix from HBM.

@@ -178,6 +178,32 @@ int sm_q4_matmul_noalloc(const uint8_t* codes, const uint16_t* scales, int64_t N
                          const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
                          int epilogue, void* stream);
 
+/* Many independent one-row Q4 GEMVs in one launch: job i computes
+ * y_i[N_i] (=, or +=) x_i[K_i] . W_i^T, i.e. one decode-step Linear::forward
+ * (summa-llm/src/model/matmul.rs:57-66) per job, for inputs that are ready
+ * together (independent projections, a whole-model weight sweep). No
+ * single-call counterpart in the reference (it launches one matmul per
+ * linear). Each job's y equals sm_q4_matmul at M = 1 bit for bit when K >=
+ * 512. Use: fill a host array of jobs, call sm_q4_gemv_multi_plan (checks
+ * every job, sets first_block, returns the total number of 16-row blocks and,
+ * given a host int32 array of that size, fills the block -> job table), copy
+ * both arrays to device memory, then launch sm_q4_gemv_multi with the device
+ * copies (no allocation; the tables can be reused for every launch while
+ * the buffers they name stay valid). max_k >= every job's K, with
+ * (1 or 2) * max_k * 2 bytes <= 64 KB. */
+typedef struct sm_q4_gemv_job {
+  const uint8_t* codes;    /* prepared tiled codes (sm_q4_pack), 16-byte aligned */
+  const uint16_t* scales;  /* prepared tiled scales */
+  const void* x;           /* K f16 (x_dtype SM_F16) or 2K (SM_F16X2: hi then lo), 16-byte aligned */
+  void* y;                 /* N outputs: f32, or bf16 for SM_EPI_STORE_BF16 */
+  int64_t N, K;            /* K a positive multiple of 128 */
+  int32_t epilogue;        /* SM_EPI_STORE_F32, SM_EPI_STORE_BF16 or SM_EPI_ADD_F32 */
+  int32_t first_block;     /* set by sm_q4_gemv_multi_plan */
+} sm_q4_gemv_job;
+int64_t sm_q4_gemv_multi_plan(sm_q4_gemv_job* jobs, int64_t njobs, int32_t* block_job);
+int sm_q4_gemv_multi(const sm_q4_gemv_job* jobs, int64_t njobs, const int32_t* block_job,
+                     int64_t nblocks, int64_t max_k, int x_dtype, void* stream);
+
 /* qkv projection fused with RoPE and the KV-cache append: y = x . W^T over
  * the Q4 qkv weight (rows [q heads | k heads | v heads], N = (H + 2 KVH) hd)
  * for S sequences x L rows (row s*L + i at position pos0[s] + i), then q and

@@ -18,6 +18,13 @@ SM_F32, SM_BF16, SM_F16, SM_F16X2 = 0, 1, 2, 3
 
 _lib = None
 
+
+class GemvJob(C.Structure):
+    """sm_q4_gemv_job (include/summa_amd.h)."""
+    _fields_ = [("codes", C.c_void_p), ("scales", C.c_void_p), ("x", C.c_void_p),
+                ("y", C.c_void_p), ("N", C.c_int64), ("K", C.c_int64),
+                ("epilogue", C.c_int32), ("first_block", C.c_int32)]
+
 vp, i32, i64, u64, f32, f64 = C.c_void_p, C.c_int, C.c_int64, C.c_uint64, C.c_float, C.c_double
 
 # name -> (restype, argtypes). Kept in the order of include/summa_amd.h.
@@ -36,6 +43,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_q4_matmul_ws": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp, i64, vp]),
     "sm_q4_noalloc_scratch_bytes": (i64, []),
     "sm_q4_matmul_noalloc": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
+    "sm_q4_gemv_multi_plan": (i64, [vp, i64, vp]),
+    "sm_q4_gemv_multi": (i32, [vp, i64, vp, i64, i64, i32, vp]),
     "sm_gemm_f32": (i32, [vp, i64, i64, vp, i64, i64, vp, i64, i32, vp]),
     "sm_swiglu_f32": (i32, [vp, i64, i64, vp, vp]),
     "sm_embed": (i32, [vp, i32, vp, i64, i64, i64, f32, vp, vp]),

@@ -6,6 +6,8 @@ argument meaning follow the reference interfaces cited in each docstring.
 """
 from __future__ import annotations
 
+import ctypes as C
+
 import torch
 
 from . import _lib
@@ -270,6 +272,51 @@ def q4_matmul(w: Q4Weight, x: torch.Tensor, out: torch.Tensor | None = None,
              x.data_ptr(), xdt, M, x.stride(0), out.data_ptr(), out.stride(0), int(epilogue),
              workspace.data_ptr(), workspace.numel() * workspace.element_size(), _stream())
     return out
+
+
+class GemvBatch:
+    """Independent one-row Q4 GEMVs launched together (sm_q4_gemv_multi).
+
+    ``jobs``: (Q4Weight, x [K] or [1, K] f16 — [2K] f16 pairs with ``pair`` —,
+    y [N] f32/bf16, epilogue). The plan (job table and block -> job table) is
+    built once on the host and kept in device memory; ``launch()`` then runs
+    every job in one kernel, as often as needed, while the tensors stay
+    alive."""
+
+    def __init__(self, jobs, *, pair: bool = False):
+        import numpy as np
+        n = len(jobs)
+        host = (_lib.GemvJob * n)()
+        kmax = 0
+        self._keep = []  # the tensors the table points at
+        for i, (w, x, y, epi) in enumerate(jobs):
+            _dev(x, "x")
+            _dev(y, "y")
+            if w.tcodes is None:
+                raise ValueError(f"Q4 GEMV needs K % 128 == 0 (K={w.k})")
+            if x.numel() != (2 if pair else 1) * w.k or y.numel() != w.n:
+                raise ValueError(f"job {i}: x / y sizes do not match the weight [{w.n}, {w.k}]")
+            host[i] = _lib.GemvJob(w.tcodes.data_ptr(), w.tscales.data_ptr(), x.data_ptr(),
+                                   y.data_ptr(), w.n, w.k, int(epi), 0)
+            kmax = max(kmax, w.k)
+            self._keep += [w, x, y]
+        L = _lib.lib()
+        total = L.sm_q4_gemv_multi_plan(C.byref(host), n, None)
+        if total < 0:
+            raise _lib.SummaError(L.sm_last_error().decode())
+        table = np.empty(total, dtype=np.int32)
+        L.sm_q4_gemv_multi_plan(C.byref(host), n, table.ctypes.data_as(C.c_void_p))
+        dev = jobs[0][1].device
+        raw = bytes(memoryview(host))
+        self.jobs_dev = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(dev)
+        self.table_dev = torch.from_numpy(table).to(dev)
+        self.njobs, self.nblocks, self.max_k = n, int(total), kmax
+        self.x_dtype = _lib.SM_F16X2 if pair else _lib.SM_F16
+        self.weight_bytes = sum(w.nbytes for w, _, _, _ in jobs)
+
+    def launch(self) -> None:
+        call("sm_q4_gemv_multi", self.jobs_dev.data_ptr(), self.njobs, self.table_dev.data_ptr(),
+             self.nblocks, self.max_k, self.x_dtype, _stream())
 
 
 # ------------------------------------------------------------------ MoE ---

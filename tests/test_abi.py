@@ -85,3 +85,26 @@ def test_rollout_sampling_validate_messages():
         with pytest.raises(ValueError, match=msg.replace("(", r"\(").replace(")", r"\)")
                            .replace("[", r"\[").replace("]", r"\]").replace(".", r"\.")):
             RolloutSampling(**kw).validate()
+
+
+def test_gemv_multi_plan_host_checks():
+    """sm_q4_gemv_multi_plan validates every job and fills first_block and the
+    block -> job table on the host (no device memory is touched)."""
+    import numpy as np
+    L = _lib.lib()
+    jobs = (_lib.GemvJob * 3)()
+    for i, (n, k) in enumerate([(40, 256), (16, 128), (1, 512)]):
+        jobs[i] = _lib.GemvJob(4096, 8192, 16384, 32768, n, k, _lib.SM_EPI_STORE_F32, -1)
+    total = L.sm_q4_gemv_multi_plan(ctypes.byref(jobs), 3, None)
+    assert total == 3 + 1 + 1
+    table = np.full(total, -1, dtype=np.int32)
+    L.sm_q4_gemv_multi_plan(ctypes.byref(jobs), 3, table.ctypes.data_as(ctypes.c_void_p))
+    assert [j.first_block for j in jobs] == [0, 3, 4]
+    assert table.tolist() == [0, 0, 0, 1, 2]
+    jobs[1].K = 100
+    assert L.sm_q4_gemv_multi_plan(ctypes.byref(jobs), 3, None) == -1
+    assert b"job 1" in L.sm_last_error()
+    jobs[1].K = 128
+    jobs[2].epilogue = _lib.SM_EPI_SWIGLU_F16
+    assert L.sm_q4_gemv_multi_plan(ctypes.byref(jobs), 3, None) == -1
+    assert b"job 2" in L.sm_last_error()

@@ -518,3 +518,41 @@ def test_wide_kernel_recompute_shapes_vs_f64(dev, m, n, k, pair):
         h = conv(ops.q4_matmul(qw, xd, pair=pair, epilogue=e)[ridx]).cpu().numpy()
         assert np.all(np.abs(h - ref_h) <= hb + rel * np.abs(ref_h) + 1e-7), \
             (e, float(np.abs(h - ref_h).max()))
+
+
+GEMV_JOBS = [(3072, 2048), (2048, 2048), (11264, 2048), (2048, 5632), (2304, 768), (768, 3072),
+             (1000, 640), (65536, 2048)]
+
+
+@pytest.mark.parametrize("pair", [False, True])
+def test_gemv_multi_equals_single_launches(dev, pair):
+    """sm_q4_gemv_multi over jobs of different N, K and epilogues (ragged N,
+    K from 640 to 5632, the LM head) gives each job's sm_q4_matmul M = 1
+    result bit for bit, and a second launch of the same plan repeats it."""
+    print(f"case gemv-multi pair={pair}", flush=True)
+    g = torch.Generator().manual_seed(3)
+    epis = [_lib.SM_EPI_STORE_F32, _lib.SM_EPI_ADD_F32, _lib.SM_EPI_STORE_BF16]
+    jobs, refs = [], []
+    for i, (n, k) in enumerate(GEMV_JOBS):
+        w = torch.empty(n, k, device=dev)
+        ops.fill_normal(w, 0.0, 0.05, seed=10 + i)
+        qw = ops.Q4Weight.quantize(w)
+        x = torch.randn(1, k, generator=g).to(dev)
+        xd = ops.f16_pair(x) if pair else x.to(torch.float16)
+        epi = epis[i % 3]
+        dt = torch.bfloat16 if epi == _lib.SM_EPI_STORE_BF16 else torch.float32
+        base = torch.randn(1, n, generator=g).to(dev).to(dt)
+        y, ref = base.clone(), base.clone()
+        ops.q4_matmul(qw, xd, out=ref, epilogue=epi, pair=pair)
+        jobs.append((qw, xd, y, epi))
+        refs.append((base, ref))
+    batch = ops.GemvBatch(jobs, pair=pair)
+    assert batch.nblocks == sum((n + 15) // 16 for n, _ in GEMV_JOBS)
+    batch.launch()
+    for (qw, xd, y, epi), (base, ref) in zip(jobs, refs):
+        assert torch.equal(y.view(torch.int16) if y.dtype != torch.float32 else y,
+                           ref.view(torch.int16) if ref.dtype != torch.float32 else ref), qw.n
+        y.copy_(base)
+    batch.launch()
+    for (qw, xd, y, epi), (base, ref) in zip(jobs, refs):
+        assert torch.equal(y.float(), ref.float()), qw.n
