@@ -201,58 +201,100 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   }
 }
 
-// Generic VALU attention (fp32 models): one thread per (query row, head);
-// query row r of sequence s sits at position pos0[s] + r + pos_off and attends
-// keys 0..=pos (causal; without the mask keys 0..L-1). q / out addressed by
-// element strides (the model's [S, L, H, hd] rows or the reference's
-// [B, H, S, hd]); cache [S, KVH, cap, hd] f32.
+// fp32 attention (fp32 models: decode, prefill and recompute; any strides of
+// q / out, causal or not): one wave per query (sequence s, query row r, head
+// h), over keys in chunks of 64. Scores: lane l takes key t0 + l and reads
+// its K row itself (float4 loads, all in flight together), q sits in
+// registers; the chunk's max and sum are wave reductions (online softmax
+// across chunks). P.V: the chunk's probabilities go through a per-wave LDS
+// slice and lane l owns output dims l (and l + 64 for hd 128), reading each
+// V row coalesced. q [S, L, H, hd] at qs (or [B, H, S, hd]); cache
+// [S, KVH, cap, hd] f32; keys 0..pos (pos = pos0[s] + r + pos_off, or L - 1
+// without the causal mask).
 template <int HD>
 __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ pos0, int pos_off, float* __restrict__ out,
     float* __restrict__ lse, int S, int L, int H,
     int KVH, int cap, float scale, AttnStrides qs, AttnStrides os, int causal) {
-  constexpr int hd = HD;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= (int64_t)S * L * H) return;
-  const int h = idx % H;
-  const int r = (idx / H) % L;
-  const int s = idx / ((int64_t)H * L);
+  constexpr int DL = HD / 64;  // output dims per lane
+  __shared__ float pbuf[4][64];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int64_t wid = (int64_t)blockIdx.x * 4 + wave;
+  if (wid >= (int64_t)S * L * H) return;  // uniform per wave; no workgroup barrier below
+  const int h = wid % H;
+  const int r = (wid / H) % L;
+  const int s = wid / ((int64_t)H * L);
   const int kvh = h / (H / KVH);
   const int pos = causal ? (pos0 ? pos0[s] : 0) + r + pos_off : L - 1;
   const float* qp = q + qs.at(s, r, h);
-  const float* kb = kc + ((size_t)s * KVH + kvh) * cap * hd;
-  const float* vb = vc + ((size_t)s * KVH + kvh) * cap * hd;
-  float* op = out + os.at(s, r, h);
-  float m = -INFINITY, l = 0.f;
-  float acc[HD];
+  const float* kb = kc + ((size_t)s * KVH + kvh) * cap * HD;
+  const float* vb = vc + ((size_t)s * KVH + kvh) * cap * HD;
+  float qv[HD];
 #pragma unroll
-  for (int d = 0; d < hd; ++d) acc[d] = 0.f;
-  for (int t = 0; t <= pos; ++t) {
+  for (int d = 0; d < HD; d += 4) {
+    const float4 t = *reinterpret_cast<const float4*>(qp + d);
+    qv[d] = t.x; qv[d + 1] = t.y; qv[d + 2] = t.z; qv[d + 3] = t.w;
+  }
+  float m = -INFINITY, l = 0.f, o[DL];
+#pragma unroll
+  for (int e = 0; e < DL; ++e) o[e] = 0.f;
+  for (int t0 = 0; t0 <= pos; t0 += 64) {
+    const int t = t0 + lane;
+    const bool ok = t <= pos;
+    const float* kr = kb + (size_t)(ok ? t : t0) * HD;
     float sc = 0.f;
 #pragma unroll
-    for (int d = 0; d < hd; ++d) sc = fmaf(qp[d], kb[(size_t)t * hd + d], sc);
-    sc *= scale;
-    const float mnew = fmaxf(m, sc);
+    for (int d = 0; d < HD; d += 4) {
+      const float4 k4 = *reinterpret_cast<const float4*>(kr + d);
+      sc = fmaf(qv[d], k4.x, sc);
+      sc = fmaf(qv[d + 1], k4.y, sc);
+      sc = fmaf(qv[d + 2], k4.z, sc);
+      sc = fmaf(qv[d + 3], k4.w, sc);
+    }
+    sc = ok ? sc * scale : -INFINITY;
+    const float mnew = fmaxf(m, wave_max(sc));
     const float alpha = (m == -INFINITY) ? 0.f : expf(m - mnew);
-    const float p = expf(sc - mnew);
-    l = l * alpha + p;
-#pragma unroll
-    for (int d = 0; d < hd; ++d) acc[d] = acc[d] * alpha + p * vb[(size_t)t * hd + d];
+    const float p = ok ? expf(sc - mnew) : 0.f;
+    l = l * alpha + wave_sum(p);
     m = mnew;
-  }
+    pbuf[wave][lane] = p;
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const int nt = min(64, pos + 1 - t0);
+    float acc[DL];
 #pragma unroll
-  for (int d = 0; d < hd; ++d) op[d] = acc[d] / l;
-  if (lse) lse[((size_t)s * H + h) * L + r] = m + logf(l);
+    for (int e = 0; e < DL; ++e) acc[e] = 0.f;
+#pragma unroll 8
+    for (int tt = 0; tt < nt; ++tt) {
+      const float pt = pbuf[wave][tt];
+      const float* vr = vb + (size_t)(t0 + tt) * HD + lane;
+#pragma unroll
+      for (int e = 0; e < DL; ++e) acc[e] = fmaf(pt, vr[e * 64], acc[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < DL; ++e) o[e] = fmaf(o[e], alpha, acc[e]);
+    __builtin_amdgcn_wave_barrier();  // the next chunk rewrites pbuf
+  }
+  float* op = out + os.at(s, r, h);
+#pragma unroll
+  for (int e = 0; e < DL; ++e) op[lane + e * 64] = o[e] / l;
+  if (lse && lane == 0) lse[((size_t)s * H + h) * L + r] = m + logf(l);
 }
 
 int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_t* pos0,
                   int pos_off, float* out, float* lse, int S, int L, int H, int KVH, int cap,
                   int hd, hipStream_t st, const AttnStrides* qs_in = nullptr,
                   const AttnStrides* os_in = nullptr, bool causal = true) {
-  const int64_t n = (int64_t)S * L * H;
+  const int64_t n = (int64_t)S * L * H;  // queries, one wave each
   if (n == 0) return SM_OK;
-  const unsigned blocks = (unsigned)ceil_div(n, 256);
+  if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
+       reinterpret_cast<uintptr_t>(vc) | reinterpret_cast<uintptr_t>(out)) % 16 != 0) {
+    set_error("f32 attention: q, the caches and out must be 16-byte aligned");
+    return SM_ERR_INVALID;
+  }
+  const unsigned blocks = (unsigned)ceil_div(n, 4);
   const float scale = 1.0f / sqrtf((float)hd);
   const AttnStrides rows = AttnStrides::rows(L, H, hd);
   const AttnStrides qs = qs_in ? *qs_in : rows, os = os_in ? *os_in : rows;

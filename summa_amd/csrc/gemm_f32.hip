@@ -2,9 +2,13 @@
 // path's precision, summa-llm/src/model/matmul.rs:57-66 with F32 weights),
 // plus the SwiGLU combine of a [gate | value] projection (ffn.rs:854-886).
 //
-// Tiled 64x64 output per 256-thread workgroup, K staged through LDS in steps
-// of 16, 4x4 outputs per thread. Used for the tiny fp32 model only, where the
-// whole step is launch-latency bound; the quantized path uses q4.hip.
+// Tiled 64x64 output per 256-thread workgroup, 4x4 outputs per thread, K in
+// steps of 32 through two LDS buffers: the next step's tiles are loaded into
+// registers before the current step's math and stored to the other buffer
+// after it, so each step's global loads overlap a step of FMAs (one barrier
+// per step). Used for the tiny fp32 model, where a launch has only a handful
+// of workgroups and a load round trip per K step would set the pace; the
+// quantized path uses q4.hip.
 #include "common.hpp"
 
 namespace sm {
@@ -15,29 +19,48 @@ __global__ __launch_bounds__(256) void gemm_f32_kernel(const float* __restrict__
                                                        const float* __restrict__ x,
                                                        float* __restrict__ y, int M, int N,
                                                        int K, int ldx, int ldy) {
-  __shared__ float xs[16][64 + 4];
-  __shared__ float ws[16][64 + 4];
+  constexpr int KT = 32;
+  __shared__ float xs[2][KT][64 + 4];
+  __shared__ float ws[2][KT][64 + 4];
   const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
   const int m0 = blockIdx.y * 64, n0 = blockIdx.x * 64;
-  float acc[4][4] = {};
-  for (int k0 = 0; k0 < K; k0 += 16) {
-    for (int e = threadIdx.x; e < 64 * 16; e += 256) {
-      const int r = e / 16, kk = e % 16;
-      const int gm = m0 + r, gn = n0 + r, gk = k0 + kk;
-      xs[kk][r] = (gm < M && gk < K) ? x[(size_t)gm * ldx + gk] : 0.f;
-      ws[kk][r] = (gn < N && gk < K) ? w[(size_t)gn * K + gk] : 0.f;
-    }
-    __syncthreads();
+  // loader: element e = i * 256 + t of a 64 x 32 tile is row e / 32, k e % 32
+  float rx[8], rw[8];
+  auto gload = [&](int k0) {
 #pragma unroll
-    for (int kk = 0; kk < 16; ++kk) {
+    for (int i = 0; i < 8; ++i) {
+      const int e = i * 256 + threadIdx.x, r = e / KT, kk = e % KT;
+      const int gm = m0 + r, gn = n0 + r, gk = k0 + kk;
+      rx[i] = (gm < M && gk < K) ? x[(size_t)gm * ldx + gk] : 0.f;
+      rw[i] = (gn < N && gk < K) ? w[(size_t)gn * K + gk] : 0.f;
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int e = i * 256 + threadIdx.x, r = e / KT, kk = e % KT;
+      xs[buf][kk][r] = rx[i];
+      ws[buf][kk][r] = rw[i];
+    }
+  };
+  float acc[4][4] = {};
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  for (int k0 = 0, buf = 0; k0 < K; k0 += KT, buf ^= 1) {
+    const bool more = k0 + KT < K;  // uniform
+    if (more) gload(k0 + KT);
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
       float a[4], b[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) { a[i] = xs[kk][ty * 4 + i]; b[i] = ws[kk][tx * 4 + i]; }
+      for (int i = 0; i < 4; ++i) { a[i] = xs[buf][kk][ty * 4 + i]; b[i] = ws[buf][kk][tx * 4 + i]; }
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) acc[i][jj] = fmaf(a[i], b[jj], acc[i][jj]);
     }
+    if (more) lstore(buf ^ 1);  // the other buffer was last read before the previous barrier
     __syncthreads();
   }
 #pragma unroll
