@@ -15,8 +15,11 @@
 // as the 16-row A operand (padded) and K rows read straight from HBM as the B
 // operand (natural [pos][hd] layout is already k-contiguous per lane). The
 // online softmax runs on the MFMA output registers, probabilities go through a
-// per-wave LDS slice, and P.V is a VALU FMA pass with hd/8 lanes per V row
-// (16-byte loads, several rows per wave instruction). Tiles are 32 keys; all
+// per-wave LDS slice, and P.V is a VALU FMA pass with hd/DPL lanes per V row,
+// each lane owning DPL dims (DPL = 8: 16-byte loads; DPL = 4, 8-byte loads, for
+// groups of 4 or more query heads, which halves the per-head accumulators:
+// config[2]'s kernel 138 -> 133 VGPRs, 82 -> 80 us, and 16 heads per KV head
+// no longer spill, 225 -> 52 us at S 64, KVH 2, len 512-1023). Tiles are 32 keys; all
 // K and V loads of a tile are issued together before its math, so a tile costs
 // one HBM round trip; 32-key tiles keep the kernel at 138 VGPRs, three waves
 // per SIMD (measured on MI355X, config[2] decode S256 H16/4 len 768: 78-80 us
@@ -28,6 +31,7 @@
 // in prefill_attention.hip; fp32 models (config[0]) use the simple VALU
 // kernel below for both.
 #include <cmath>
+#include <type_traits>
 
 #include "attn_common.hpp"
 #include "common.hpp"
@@ -37,17 +41,21 @@ namespace {
 
 constexpr int kMaxQpk = 16;  // query heads per KV head handled by one WG
 
-template <int HD, int QM, bool KF16, int OM>
+// QM: query heads per KV head the kernel is built for (>= H / KVH); EX: exactly
+// QM, so the per-head bounds are compile-time; DPL: V dims per lane in P.V.
+template <int HD, int QM, bool KF16, int OM, bool EX, int DPL>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ lens,
     void* __restrict__ out, int H, int KVH, int cap, float scale) {
   typedef typename Op8<KF16>::T op8;
-  constexpr int LPK = HD / 8;      // lanes per V row in the P.V pass (8 dims = 16 B each)
+  static_assert(DPL == 4 || DPL == 8, "DPL is 4 or 8");
+  constexpr int LPK = HD / DPL;    // lanes per V row in the P.V pass (DPL dims each)
+  typedef typename std::conditional<DPL == 8, u32x4, u32x2>::type vrow;
   constexpr int PPI = 64 / LPK;    // keys per P.V iteration per wave
   constexpr int STEPS = HD / 32;   // MFMA k-steps over head_dim
   const int kvh = blockIdx.x, s = blockIdx.y;
-  const int qpk = H / KVH;
+  const int qpk = EX ? QM : H / KVH;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int j = lane % 16, g = lane / 16;
   const int len = min(lens[s], cap);
@@ -72,23 +80,23 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
   }
 
-  float m_i[QM], l_i[QM], o[QM][8];
+  float m_i[QM], l_i[QM], o[QM][DPL];
 #pragma unroll
   for (int i = 0; i < QM; ++i) {
     m_i[i] = -INFINITY;
     l_i[i] = 0.f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[i][e] = 0.f;
+    for (int e = 0; e < DPL; ++e) o[i][e] = 0.f;
   }
 
   const int sub = lane / LPK;          // which key of the PPI group this lane handles
-  const int dl = (lane % LPK) * 8;     // first of the eight dims this lane owns
+  const int dl = (lane % LPK) * DPL;   // first of the dims this lane owns
 
   // One tile's loads: K fragments for the score MFMAs and this lane's V rows.
   // Rows past the end are clamped to the last valid row and masked below.
   struct Tile {
     op8 kf[KB][STEPS];
-    u32x4 vr[VR];
+    vrow vr[VR];
   };
   const int last = max(len - 1, 0);  // every load stays inside the sequence's cache rows
   auto load = [&](int t0, Tile& T) {
@@ -102,7 +110,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int i = 0; i < VR; ++i) {
       const int key = min(t0 + sub + i * PPI, last);
-      T.vr[i] = *reinterpret_cast<const u32x4*>(vc + kv_base + (size_t)key * HD + dl);
+      T.vr[i] = *reinterpret_cast<const vrow*>(vc + kv_base + (size_t)key * HD + dl);
     }
   };
   auto compute = [&](int t0, const Tile& T) {
@@ -134,7 +142,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       l_i[i] = l_i[i] * alpha + wave_sum(p);
       m_i[i] = mnew;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) o[i][e] *= alpha;
+      for (int e = 0; e < DPL; ++e) o[i][e] *= alpha;
       if (lane < TK) pbuf[wave][i][lane] = p;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -144,14 +152,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
     for (int vi = 0; vi < VR; ++vi) {
       const int tt = sub + vi * PPI;
-      float v[8];
-      unpack8<KF16>(T.vr[vi], v);
+      float v[DPL];
+      if constexpr (DPL == 8) unpack8<KF16>(T.vr[vi], v);
+      else unpack4<KF16>(T.vr[vi], v);
 #pragma unroll
       for (int i = 0; i < QM; ++i) {
         if (i >= qpk) break;
         const float p = pbuf[wave][i][tt];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[i][e] = fmaf(p, v[e], o[i][e]);
+        for (int e = 0; e < DPL; ++e) o[i][e] = fmaf(p, v[e], o[i][e]);
       }
     }
     __builtin_amdgcn_wave_barrier();
@@ -171,7 +180,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
 #pragma unroll
       for (int off = LPK; off < 64; off <<= 1)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) o[i][e] += __shfl_xor(o[i][e], off, kWave);
+        for (int e = 0; e < DPL; ++e) o[i][e] += __shfl_xor(o[i][e], off, kWave);
   }
 #pragma unroll
   for (int i = 0; i < QM; ++i) {
@@ -179,7 +188,7 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     if (lane == 0) { mrg_m[wave][i] = m_i[i]; mrg_l[wave][i] = l_i[i]; }
     if (lane < LPK) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) mrg_o[wave][i][dl + e] = o[i][e];
+      for (int e = 0; e < DPL; ++e) mrg_o[wave][i][dl + e] = o[i][e];
     }
   }
   __syncthreads();
@@ -354,22 +363,27 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
   const dim3 grid((unsigned)KVH, (unsigned)S);
   const uint16_t *qq = (const uint16_t*)q, *kk = (const uint16_t*)kcache,
                  *vv = (const uint16_t*)vcache;
-#define SM_DEC_K(HD, QM, KF)                                                                   \
+#define SM_DEC_K(HD, QM, KF, EX, DPL)                                                         \
   do {                                                                                         \
     if (om == 2)                                                                               \
-      attn_decode_kernel<HD, QM, KF, 2><<<grid, 256, 0, st>>>(qq, kk, vv, lens, out, (int)H,   \
-                                                             (int)KVH, (int)cap, scale);       \
+      attn_decode_kernel<HD, QM, KF, 2, EX, DPL><<<grid, 256, 0, st>>>(                        \
+          qq, kk, vv, lens, out, (int)H, (int)KVH, (int)cap, scale);                           \
     else if (om == 1)                                                                          \
-      attn_decode_kernel<HD, QM, KF, 1><<<grid, 256, 0, st>>>(qq, kk, vv, lens, out, (int)H,   \
-                                                             (int)KVH, (int)cap, scale);       \
+      attn_decode_kernel<HD, QM, KF, 1, EX, DPL><<<grid, 256, 0, st>>>(                        \
+          qq, kk, vv, lens, out, (int)H, (int)KVH, (int)cap, scale);                           \
     else                                                                                       \
-      attn_decode_kernel<HD, QM, KF, 0><<<grid, 256, 0, st>>>(qq, kk, vv, lens, out, (int)H,   \
-                                                             (int)KVH, (int)cap, scale);       \
+      attn_decode_kernel<HD, QM, KF, 0, EX, DPL><<<grid, 256, 0, st>>>(                        \
+          qq, kk, vv, lens, out, (int)H, (int)KVH, (int)cap, scale);                           \
   } while (0)
-#define SM_DEC(HD, QM)                                   \
-  do {                                                   \
-    if (dtype == SM_F16) SM_DEC_K(HD, QM, true);         \
-    else SM_DEC_K(HD, QM, false);                        \
+#define SM_DEC_X(HD, QM, EX)                                          \
+  do {                                                                \
+    if (dtype == SM_F16) SM_DEC_K(HD, QM, true, EX, (QM >= 4 ? 4 : 8)); \
+    else SM_DEC_K(HD, QM, false, EX, (QM >= 4 ? 4 : 8));              \
+  } while (0)
+#define SM_DEC(HD, QM)                     \
+  do {                                     \
+    if (qpk == QM) SM_DEC_X(HD, QM, true); \
+    else SM_DEC_X(HD, QM, false);          \
   } while (0)
   if (head_dim == 64) {
     if (qpk == 1) SM_DEC(64, 1); else if (qpk <= 4) SM_DEC(64, 4); else SM_DEC(64, 16);
@@ -377,6 +391,7 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
     if (qpk == 1) SM_DEC(128, 1); else if (qpk <= 4) SM_DEC(128, 4); else SM_DEC(128, 16);
   }
 #undef SM_DEC
+#undef SM_DEC_X
 #undef SM_DEC_K
   SM_LAUNCH_CHECK();
   return SM_OK;

@@ -42,6 +42,17 @@ __device__ inline void unpack8(u32x4 v, float (&f)[8]) {
   }
 }
 
+// 4 cache values (one 8-byte load) -> f32.
+template <bool KF16>
+__device__ inline void unpack4(u32x2 v, float (&f)[4]) {
+  if constexpr (KF16) {
+    const h2 a = as_h2(v.x), b = as_h2(v.y);
+    f[0] = (float)a[0]; f[1] = (float)a[1]; f[2] = (float)b[0]; f[3] = (float)b[1];
+  } else {
+    f[0] = bf16lo(v.x); f[1] = bf16hi(v.x); f[2] = bf16lo(v.y); f[3] = bf16hi(v.y);
+  }
+}
+
 // Element strides of a q / output tensor over (sequence, position, head); the
 // head_dim values of one (sequence, position, head) are contiguous.
 struct AttnStrides {

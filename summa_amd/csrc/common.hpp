@@ -49,6 +49,7 @@ void clear_error();
 
 // Native 16-byte vector (usable with the nontemporal load/store builtins).
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 

@@ -45,7 +45,9 @@ def _attn_ref(q, k, v, lens):
 
 
 @pytest.mark.parametrize("S,H,KVH,hd,cap", [(3, 12, 12, 64, 300), (4, 16, 4, 128, 1100),
-                                            (2, 4, 4, 64, 70), (5, 8, 1, 128, 257)])
+                                            (2, 4, 4, 64, 70), (5, 8, 1, 128, 257),
+                                            (3, 12, 4, 64, 200), (2, 16, 8, 128, 300),
+                                            (2, 32, 2, 128, 400)])
 def test_attn_decode_bf16(dev, S, H, KVH, hd, cap):
     print(f"case S={S} H={H} KVH={KVH} hd={hd} cap={cap}", flush=True)
     rng = np.random.default_rng(S * H + cap)
@@ -65,7 +67,8 @@ def test_attn_decode_bf16(dev, S, H, KVH, hd, cap):
 
 
 @pytest.mark.parametrize("S,H,KVH,hd,cap", [(3, 12, 12, 64, 300), (4, 16, 4, 128, 1100),
-                                            (5, 8, 1, 128, 257)])
+                                            (5, 8, 1, 128, 257), (3, 12, 4, 64, 200),
+                                            (2, 16, 8, 128, 300), (2, 32, 2, 128, 400)])
 def test_attn_decode_f16_cache_pair_out(dev, S, H, KVH, hd, cap):
     """f16 q / cache (the quantized models' KV dtype), f16-pair output: only the
     fp32 accumulation separates the result from the exact attention."""
