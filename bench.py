@@ -642,8 +642,68 @@ def bench_recompute_gemm(args) -> dict:
                                                    "traffic_bytes_per_launch")}}
 
 
+def bench_policy_update(args) -> dict:
+    """The GRPO policy update at config[2] scale (sm_policy_prepare +
+    sm_policy_optimizer_step): one group of 8 rollouts x (512 + 512) per call,
+    recompute with activations kept, the frozen reference's log-probs, the
+    loss and the whole backward into f32 master gradients, then AdamW with the
+    global-norm clip. The rollouts come from the installed Q4 model."""
+    import torch
+
+    from summa_amd import train
+    from summa_amd.configs import RL_WORKLOADS
+    from summa_amd.model import Model
+    wl = RL_WORKLOADS[2]
+    mc = wl.model_config()
+    dev = torch.device("cuda:0")
+    d, F, V, Ly = mc.d_model, mc.ffn, mc.vocab, mc.layers
+    qn = (mc.heads + 2 * mc.kv_heads) * mc.head_dim
+    gen = torch.Generator(device=dev).manual_seed(0)
+    nrm = lambda *sh: torch.randn(*sh, generator=gen, device=dev) * 0.02  # noqa: E731
+    w = {"embed": nrm(V, d), "lm_head": nrm(V, d), "final_norm": torch.ones(d, device=dev),
+         "attn_norm": torch.ones(Ly, d, device=dev), "ffn_norm": torch.ones(Ly, d, device=dev),
+         "qkv": nrm(Ly, qn, d), "o": nrm(Ly, d, mc.heads * mc.head_dim), "in": nrm(Ly, 2 * F, d),
+         "down": nrm(Ly, d, F)}
+    pol = train.Policy(mc, w, dev)
+    del w
+    ref = Model(mc)
+    pol.install(ref)
+    G, P, N = wl.group, wl.prompt_len, wl.new_tokens
+    prompts = torch.randint(0, V, (G, P), dtype=torch.int32, device=dev)
+    tok, beh = ref.generate(prompts, N, temperature=wl.temperature, seed=1)
+    rewards = torch.rand(1, G, device=dev)
+    st = torch.cuda.current_stream()
+    e0, e1, e2 = _events(3)
+    prep, step = [], []
+    for i in range(args.warmup + args.steps):
+        e0.record(st)
+        out = pol.prepare(ref, prompts, tok, beh, rewards)
+        e1.record(st)
+        pol.optimizer_step(1.0)
+        e2.record(st)
+        torch.cuda.synchronize()
+        if i == 0:  # the policy still equals the model that rolled out
+            lp_gap = float((out["lp_cur"] - beh).abs().max())
+        if i >= args.warmup:
+            prep.append(e0.elapsed_time(e1))
+            step.append(e1.elapsed_time(e2))
+        log(f"bench: policy update {i}: prepare {e0.elapsed_time(e1):.1f} ms, "
+            f"optimizer step {e1.elapsed_time(e2):.1f} ms")
+    p_ms, s_ms = sum(prep) / len(prep), sum(step) / len(step)
+    positions = G * (P + N - 1)
+    return {"metric": "GRPO policy update positions/s (config[2], one group per call)",
+            "value": positions / ((p_ms + s_ms) / 1e3), "unit": "positions/s",
+            "ms_per_step": p_ms + s_ms, "dtype": "f32 masters, Q4G128 fake-quantized forward",
+            "config": {"workload": "policy_update config[2]", "rollouts": G, "prompt_len": P,
+                       "new_tokens": N},
+            "prepare_ms": round(p_ms, 2), "optimizer_step_ms": round(s_ms, 2),
+            "parameters": int(Ly * (qn * d + d * mc.heads * mc.head_dim + 3 * F * d + 2 * d)
+                              + 2 * V * d + d),
+            "first_prepare_lp_vs_rollout_max_abs": lp_gap}
+
+
 WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress, "q4_gemv": bench_q4_gemv,
-             "recompute_gemm": bench_recompute_gemm}
+             "recompute_gemm": bench_recompute_gemm, "policy_update": bench_policy_update}
 
 
 def main() -> int:

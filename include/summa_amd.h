@@ -417,6 +417,13 @@ int sm_swiglu_backward(const void* gate_value, const void* grad, int dtype, int6
  * sm_gemm_ex: C = alpha op(A) op(B) + beta C, op(A) [M, K] (A stored [M, K],
  *   or [K, M] when trans_a), op(B) [K, N] (B stored [K, N], or [N, K] when
  *   trans_b): the data / weight gradients of Linear::forward (matmul.rs:57-66).
+ *   Problems of at least 2^27 multiply-adds run on the matrix cores as
+ *   sm_gemm_mfma does; smaller ones on an f32 FMA kernel.
+ * sm_gemm_mfma: the same contract (K > 0) always on the matrix cores: each f32
+ *   operand is split exactly into three bf16 planes and the six plane
+ *   products of weight >= 2^-16 are accumulated in f32, an f32 GEMM up to the
+ *   order of its additions (the bf16 operands of matmul_2 / linear on the
+ *   reference's CUDA path, matmul.rs:73-82, 132-143, with f32 results).
  * sm_rmsnorm_backward: dx (= or += with accumulate) and dgamma (nullable; =
  *   or += ; summed over rows in order) of y = x / sqrt(mean x^2 + eps) * gamma
  *   (norm.rs:36-50); rinv_scratch [rows].
@@ -437,6 +444,9 @@ int sm_swiglu_backward(const void* gate_value, const void* grad, int dtype, int6
 int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
                int64_t ldc, void* stream);
+int sm_gemm_mfma(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                 const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+                 int64_t ldc, void* stream);
 int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy, int64_t rows,
                         int64_t d, float eps, int accumulate, float* dx, float* dgamma,
                         float* rinv_scratch, void* stream);

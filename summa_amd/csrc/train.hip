@@ -116,14 +116,34 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_kernel(const float* __restric
 }
 
 // dgamma_c = sum over rows in order (deterministic), one thread per column
-__global__ void rmsnorm_dgamma_kernel(const float* __restrict__ x, const float* __restrict__ dy,
-                                      const float* __restrict__ rinv, int64_t rows, int d,
-                                      int accumulate, float* __restrict__ dgamma) {
-  const int c = blockIdx.x * blockDim.x + threadIdx.x;
-  if (c >= d) return;
-  float s = 0.f;
-  for (int64_t r = 0; r < rows; ++r) s = fmaf(dy[r * d + c] * x[r * d + c], rinv[r], s);
-  dgamma[c] = accumulate ? dgamma[c] + s : s;
+// dgamma[c] (=, or += with accumulate) = sum_r dy[r, c] x[r, c] rinv[r]: one
+// workgroup per 64 columns; thread t sums columns 4 (t % 16) + j over rows
+// t / 16, t / 16 + 16, ... (a wave reads four 256-byte row segments per
+// step), and the 16 row-lane partials are added in order.
+__global__ __launch_bounds__(256) void rmsnorm_dgamma_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ dy,
+                                                             const float* __restrict__ rinv,
+                                                             int64_t rows, int d, int accumulate,
+                                                             float* __restrict__ dgamma) {
+  __shared__ float part[16][64];
+  const int cg = threadIdx.x % 16, rl = threadIdx.x / 16;
+  const int c0 = blockIdx.x * 64 + 4 * cg;
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t r = rl; r < rows; r += 16) {
+    const float ri = rinv[r];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (c0 + j < d) s[j] = fmaf(dy[r * d + c0 + j] * x[r * d + c0 + j], ri, s[j]);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part[rl][4 * cg + j] = s[j];
+  __syncthreads();
+  const int c = blockIdx.x * 64 + (int)threadIdx.x;
+  if (threadIdx.x >= 64 || c >= d) return;
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tot += part[i][threadIdx.x];
+  dgamma[c] = accumulate ? dgamma[c] + tot : tot;
 }
 
 // ------------------------------------------------------------------ RoPE ---
@@ -156,90 +176,240 @@ __global__ void rope_qk_kernel(float* __restrict__ qkv, const float2* __restrict
 // Forward inputs: q, o and dO addressed by element strides (the model's
 // [S*L, H, hd] rows or the reference's [B, H, S, hd] tensors), k / v
 // [S, KVH, L, hd] (positions 0..L-1, causal or not), lse [S*H, L].
-// delta[s,h,r] = <dO, O>; dq = scale sum_t ds_t k_t with
-// ds_t = p_t (<dO, v_t> - delta), p_t = exp(scale <q, k_t> - lse).
+// delta[s,h,r] = <dO, O>; with p_t = exp(scale <q, k_t> - lse) and
+// ds_t = p_t (<dO, v_t> - delta) scale: dq = sum_t ds_t k_t, and for a key t
+// of KV head g, dk_t = sum over the group's heads and rows r of ds q_r,
+// dv_t = the same sum of p dO_r (fused_attention.rs:219-405).
+//
+// FlashAttention-2 style, f32 FMAs on 32 x 32 tiles staged in LDS: the dK / dV
+// kernel holds one 32-key block of K and V and walks the query blocks of
+// every head of its group (rows >= the block's first key under the causal
+// mask), recomputing the scores and dP = dO V^T per tile; the dQ kernel holds
+// one 32-row block of Q and dO and walks the key blocks. Each output has one
+// owner and a fixed order of additions (deterministic, no atomics). Rows
+// padded to hd + 4 floats; 77 KB of LDS, two workgroups per CU. Under the
+// causal mask the heaviest blocks are dispatched first.
+constexpr int kAB = 32;  // query rows and keys per tile
+
+// delta = <dO, O> per (s, h, r), row (s H + h) L + r; one wave per row
 template <int HD>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
-    const float* __restrict__ o, const float* __restrict__ dout, const float* __restrict__ lse,
-    int S, int L, int H, int KVH, float scale, float* __restrict__ dq, float* __restrict__ delta,
-    AttnStrides qs, int causal) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (s, r, h)
-  if (idx >= (int64_t)S * L * H) return;
-  const int h = idx % H, r = (idx / H) % L, s = (int)(idx / ((int64_t)H * L));
-  const int kvh = h / (H / KVH);
-  const size_t at = qs.at(s, r, h);
-  const float* qp = q + at;
-  const float* op = o + at;
-  const float* gp = dout + at;
-  const float* kb = k + ((size_t)s * KVH + kvh) * L * HD;
-  const float* vb = v + ((size_t)s * KVH + kvh) * L * HD;
-  float dlt = 0.f;
-  for (int d = 0; d < HD; ++d) dlt = fmaf(gp[d], op[d], dlt);
-  const float ls = lse[((size_t)s * H + h) * L + r];
-  float acc[HD];
+__global__ __launch_bounds__(256) void attn_bwd_delta_kernel(const float* __restrict__ o,
+                                                             const float* __restrict__ dout,
+                                                             int S, int L, int H, AttnStrides qs,
+                                                             float* __restrict__ delta) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + threadIdx.x / kWave;
+  const int lane = threadIdx.x % kWave;
+  if (row >= (int64_t)S * H * L) return;  // uniform per wave
+  const int r = (int)(row % L), sh = (int)(row / L);
+  const size_t at = qs.at(sh / H, r, sh % H);
+  float acc = 0.f;
 #pragma unroll
-  for (int d = 0; d < HD; ++d) acc[d] = 0.f;
-  const int tmax = causal ? r : L - 1;
-  for (int t = 0; t <= tmax; ++t) {
-    float sc = 0.f, dp = 0.f;
-#pragma unroll
-    for (int d = 0; d < HD; ++d) {
-      sc = fmaf(qp[d], kb[(size_t)t * HD + d], sc);
-      dp = fmaf(gp[d], vb[(size_t)t * HD + d], dp);
-    }
-    const float p = expf(sc * scale - ls);
-    const float ds = p * (dp - dlt) * scale;
-#pragma unroll
-    for (int d = 0; d < HD; ++d) acc[d] = fmaf(ds, kb[(size_t)t * HD + d], acc[d]);
-  }
-#pragma unroll
-  for (int d = 0; d < HD; ++d) dq[at + d] = acc[d];
-  delta[((size_t)s * H + h) * L + r] = dlt;
+  for (int d = lane; d < HD; d += kWave) acc = fmaf(dout[at + d], o[at + d], acc);
+  acc = wave_sum(acc);
+  if (lane == 0) delta[row] = acc;
 }
 
-// dk_t = scale sum_{h in group, r >= t} ds q_r ; dv_t = sum p dO_r (GQA groups summed)
+// T rows of HD floats (row i at src(i), or 0 past `valid`) -> LDS rows of stride RS
+template <int HD, int RS, typename Src>
+__device__ inline void stage_rows(float* __restrict__ dst, int valid, Src src) {
+  constexpr int C4 = HD / 4;
+  for (int e = threadIdx.x; e < kAB * C4; e += 256) {
+    const int i = e / C4, c = e % C4;
+    f4 x = f4{0.f, 0.f, 0.f, 0.f};
+    if (i < valid) x = *reinterpret_cast<const f4*>(src(i) + 4 * c);
+    *reinterpret_cast<f4*>(dst + i * RS + 4 * c) = x;
+  }
+}
+
+// S = A B^T and dP = G W^T for a 32 x 32 tile: rows 2 ty + i of A / G, rows
+// tx + 16 j of B / W (LDS rows of stride RS)
+template <int HD, int RS>
+__device__ inline void tile_scores(const float* A, const float* G, const float* B,
+                                   const float* W, int ty, int tx, float (&sc)[2][2],
+                                   float (&dp)[2][2]) {
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) sc[i][j] = dp[i][j] = 0.f;
+#pragma unroll 4
+  for (int d = 0; d < HD; d += 4) {
+    f4 a[2], g[2], b[2], w[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      a[i] = *reinterpret_cast<const f4*>(A + (2 * ty + i) * RS + d);
+      g[i] = *reinterpret_cast<const f4*>(G + (2 * ty + i) * RS + d);
+      b[i] = *reinterpret_cast<const f4*>(B + (tx + 16 * i) * RS + d);
+      w[i] = *reinterpret_cast<const f4*>(W + (tx + 16 * i) * RS + d);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          sc[i][j] = fmaf(a[i][e], b[j][e], sc[i][j]);
+          dp[i][j] = fmaf(g[i][e], w[j][e], dp[i][j]);
+        }
+  }
+}
+
 template <int HD>
-__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkv_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
     int S, int L, int H, int KVH, float scale, float* __restrict__ dk, float* __restrict__ dv,
     AttnStrides qs, int causal) {
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // (s, kvh, t)
-  if (idx >= (int64_t)S * KVH * L) return;
-  const int t = idx % L, kvh = (idx / L) % KVH, s = (int)(idx / ((int64_t)L * KVH));
-  const int group = H / KVH;
-  const float* kt = k + idx * HD;
-  const float* vt = v + idx * HD;
-  float ak[HD], av[HD];
+  constexpr int T = kAB, RS = HD + 4, PS = T + 4, DPT = HD / 32;
+  __shared__ __attribute__((aligned(16))) float Ks[T * RS], Vs[T * RS], Qs[T * RS], Gs[T * RS];
+  __shared__ __attribute__((aligned(16))) float Ps[T * PS], Ds[T * PS];
+  __shared__ float ls_s[T], dl_s[T];
+  const int sk = (int)blockIdx.x, s = sk / KVH, kvh = sk % KVH;  // (sequence, KV head)
+  const int k0 = (int)blockIdx.y * T;                            // heaviest (first) keys first
+  const int t = (int)threadIdx.x, group = H / KVH;
+  const float* kb = k + (size_t)sk * L * HD;
+  const float* vb = v + (size_t)sk * L * HD;
+  stage_rows<HD, RS>(Ks, L - k0, [&](int i) { return kb + (size_t)(k0 + i) * HD; });
+  stage_rows<HD, RS>(Vs, L - k0, [&](int i) { return vb + (size_t)(k0 + i) * HD; });
+  const int ty = t / 16, tx = t % 16;  // score tile: rows 2 ty + i, keys tx + 16 j
+  const int kg = t / 32, dg = t % 32;  // dK / dV: keys 4 kg + a, dims DPT dg + b
+  float ak[4][DPT], av[4][DPT];
 #pragma unroll
-  for (int d = 0; d < HD; ++d) ak[d] = av[d] = 0.f;
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < DPT; ++b) ak[a][b] = av[a][b] = 0.f;
+  const int nqb = (L + T - 1) / T;
   for (int hh = 0; hh < group; ++hh) {
     const int h = kvh * group + hh;
-    for (int r = causal ? t : 0; r < L; ++r) {
-      const size_t at = qs.at(s, r, h);
-      const float* qp = q + at;
-      const float* gp = dout + at;
-      float sc = 0.f, dp = 0.f;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) {
-        sc = fmaf(qp[d], kt[d], sc);
-        dp = fmaf(gp[d], vt[d], dp);
+    for (int qb = causal ? k0 / T : 0; qb < nqb; ++qb) {
+      const int r0 = qb * T;
+      __syncthreads();  // the previous tile's readers are done
+      stage_rows<HD, RS>(Qs, L - r0, [&](int i) { return q + qs.at(s, r0 + i, h); });
+      stage_rows<HD, RS>(Gs, L - r0, [&](int i) { return dout + qs.at(s, r0 + i, h); });
+      if (t < T) {
+        const bool in = r0 + t < L;
+        const size_t li = ((size_t)s * H + h) * L + r0 + t;
+        ls_s[t] = in ? lse[li] : 0.f;
+        dl_s[t] = in ? delta[li] : 0.f;
       }
-      const size_t li = ((size_t)s * H + h) * L + r;
-      const float p = expf(sc * scale - lse[li]);
-      const float ds = p * (dp - delta[li]) * scale;
+      __syncthreads();
+      float sc[2][2], dp[2][2];
+      tile_scores<HD, RS>(Qs, Gs, Ks, Vs, ty, tx, sc, dp);
 #pragma unroll
-      for (int d = 0; d < HD; ++d) {
-        av[d] = fmaf(p, gp[d], av[d]);
-        ak[d] = fmaf(ds, qp[d], ak[d]);
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const int r = 2 * ty + i, c = tx + 16 * j;
+          const int qr = r0 + r, kc = k0 + c;
+          float p = 0.f;
+          if (qr < L && kc < L && (!causal || kc <= qr)) p = expf(sc[i][j] * scale - ls_s[r]);
+          Ps[r * PS + c] = p;
+          Ds[r * PS + c] = p * (dp[i][j] - dl_s[r]) * scale;
+        }
+      __syncthreads();
+#pragma unroll 4
+      for (int r = 0; r < T; ++r) {
+        const f4 p4 = *reinterpret_cast<const f4*>(Ps + r * PS + 4 * kg);
+        const f4 d4 = *reinterpret_cast<const f4*>(Ds + r * PS + 4 * kg);
+        float g[DPT], qv[DPT];
+#pragma unroll
+        for (int b = 0; b < DPT; ++b) {
+          g[b] = Gs[r * RS + DPT * dg + b];
+          qv[b] = Qs[r * RS + DPT * dg + b];
+        }
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+          for (int b = 0; b < DPT; ++b) {
+            av[a][b] = fmaf(p4[a], g[b], av[a][b]);
+            ak[a][b] = fmaf(d4[a], qv[b], ak[a][b]);
+          }
       }
     }
   }
 #pragma unroll
-  for (int d = 0; d < HD; ++d) {
-    dk[idx * HD + d] = ak[d];
-    dv[idx * HD + d] = av[d];
+  for (int a = 0; a < 4; ++a) {
+    const int key = k0 + 4 * kg + a;
+    if (key >= L) continue;
+    const size_t o = ((size_t)sk * L + key) * HD + DPT * dg;
+#pragma unroll
+    for (int b = 0; b < DPT; ++b) {
+      dk[o + b] = ak[a][b];
+      dv[o + b] = av[a][b];
+    }
+  }
+}
+
+template <int HD>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
+    int S, int L, int H, int KVH, float scale, float* __restrict__ dq, AttnStrides qs,
+    int causal) {
+  constexpr int T = kAB, RS = HD + 4, PS = T + 4, DPT = HD / 32;
+  __shared__ __attribute__((aligned(16))) float Qs[T * RS], Gs[T * RS], Ks[T * RS], Vs[T * RS];
+  __shared__ __attribute__((aligned(16))) float DsT[T * PS];  // [key][row]
+  __shared__ float ls_s[T], dl_s[T];
+  const int sh = (int)blockIdx.x, s = sh / H, h = sh % H;
+  const int sk = s * KVH + h / (H / KVH);
+  const int nqb = (L + T - 1) / T;
+  const int qb = causal ? nqb - 1 - (int)blockIdx.y : (int)blockIdx.y;  // heaviest first
+  const int r0 = qb * T, t = (int)threadIdx.x;
+  stage_rows<HD, RS>(Qs, L - r0, [&](int i) { return q + qs.at(s, r0 + i, h); });
+  stage_rows<HD, RS>(Gs, L - r0, [&](int i) { return dout + qs.at(s, r0 + i, h); });
+  if (t < T) {
+    const bool in = r0 + t < L;
+    const size_t li = ((size_t)s * H + h) * L + r0 + t;
+    ls_s[t] = in ? lse[li] : 0.f;
+    dl_s[t] = in ? delta[li] : 0.f;
+  }
+  const float* kb = k + (size_t)sk * L * HD;
+  const float* vb = v + (size_t)sk * L * HD;
+  const int ty = t / 16, tx = t % 16;  // score tile: rows 2 ty + i, keys tx + 16 j
+  const int rg = t / 32, dg = t % 32;  // dQ: rows 4 rg + a, dims DPT dg + b
+  float aq[4][DPT];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < DPT; ++b) aq[a][b] = 0.f;
+  const int nkb = causal ? qb + 1 : nqb;  // key blocks holding keys <= the block's last row
+  for (int kbk = 0; kbk < nkb; ++kbk) {
+    const int k0 = kbk * T;
+    __syncthreads();  // Q staged (first pass); the previous tile's readers are done
+    stage_rows<HD, RS>(Ks, L - k0, [&](int i) { return kb + (size_t)(k0 + i) * HD; });
+    stage_rows<HD, RS>(Vs, L - k0, [&](int i) { return vb + (size_t)(k0 + i) * HD; });
+    __syncthreads();
+    float sc[2][2], dp[2][2];
+    tile_scores<HD, RS>(Qs, Gs, Ks, Vs, ty, tx, sc, dp);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int r = 2 * ty + i, c = tx + 16 * j;
+        const int qr = r0 + r, kc = k0 + c;
+        float p = 0.f;
+        if (qr < L && kc < L && (!causal || kc <= qr)) p = expf(sc[i][j] * scale - ls_s[r]);
+        DsT[c * PS + r] = p * (dp[i][j] - dl_s[r]) * scale;
+      }
+    __syncthreads();
+#pragma unroll 4
+    for (int c = 0; c < T; ++c) {
+      const f4 d4 = *reinterpret_cast<const f4*>(DsT + c * PS + 4 * rg);
+      float kv[DPT];
+#pragma unroll
+      for (int b = 0; b < DPT; ++b) kv[b] = Ks[c * RS + DPT * dg + b];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < DPT; ++b) aq[a][b] = fmaf(d4[a], kv[b], aq[a][b]);
+    }
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const int r = r0 + 4 * rg + a;
+    if (r >= L) continue;
+    float* o = dq + qs.at(s, r, h) + DPT * dg;
+#pragma unroll
+    for (int b = 0; b < DPT; ++b) o[b] = aq[a][b];
   }
 }
 
@@ -312,6 +482,10 @@ __global__ void scale_by_kernel(float* __restrict__ x, int64_t n, const float* _
 inline unsigned g256(int64_t n) { return (unsigned)ceil_div(n, 256); }
 
 }  // namespace
+
+int gemm_bf16x3(bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
+                int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                hipStream_t st);  // gemm_mfma.hip
 }  // namespace sm
 
 using namespace sm;
@@ -325,8 +499,13 @@ extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_
   SM_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N,
              "sm_gemm_ex: leading dimension too small");
   if (M == 0 || N == 0) return SM_OK;
-  const dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
   hipStream_t st = as_stream(stream);
+  // large problems on the matrix cores (f32-grade three-plane bf16 products,
+  // gemm_mfma.hip); small ones, where a launch has few 128 x 128 tiles, here
+  if (K >= 32 && M * N >= (int64_t)128 * 128 * 16 && M * N * K >= ((int64_t)1 << 27))
+    return gemm_bf16x3(trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
+                       st);
+  const dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
 #define SM_GX(TA, TB)                                                                        \
   gemm_ex_kernel<TA, TB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, \
                                                alpha, beta)
@@ -349,8 +528,8 @@ extern "C" int sm_rmsnorm_backward(const float* x, const float* gamma, const flo
   rmsnorm_bwd_kernel<<<(unsigned)rows, 256, 0, st>>>(x, gamma, dy, (int)d, eps, accumulate, dx,
                                                      rinv_scratch);
   if (dgamma)
-    rmsnorm_dgamma_kernel<<<g256(d), 256, 0, st>>>(x, dy, rinv_scratch, rows, (int)d, accumulate,
-                                                   dgamma);
+    rmsnorm_dgamma_kernel<<<(unsigned)ceil_div(d, 64), 256, 0, st>>>(x, dy, rinv_scratch, rows,
+                                                                     (int)d, accumulate, dgamma);
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
@@ -381,23 +560,28 @@ int attn_backward_f32(const float* q, const float* k, const float* v, const floa
                       const float* dout, const float* lse, int64_t S, int64_t L, int64_t H,
                       int64_t KVH, int64_t head_dim, float* dq, float* dk, float* dv,
                       float* delta_scratch, const AttnStrides& qs, bool causal, hipStream_t st) {
+  auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+  SM_REQUIRE(al16(q) && al16(k) && al16(v) && al16(dout) && qs.seq % 4 == 0 && qs.pos % 4 == 0 &&
+                 qs.head % 4 == 0,
+             "attention backward: q, k, v and grad_out need 16-byte aligned rows");
   const float scale = 1.0f / sqrtf((float)head_dim);
-  const int64_t nq = S * L * H, nk = S * KVH * L;
   const int cz = causal ? 1 : 0;
-  if (head_dim == 64) {
-    attn_bwd_dq_kernel<64><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L, (int)H,
-                                                     (int)KVH, scale, dq, delta_scratch, qs, cz);
-    attn_bwd_dkv_kernel<64><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
-                                                      (int)L, (int)H, (int)KVH, scale, dk, dv, qs,
-                                                      cz);
-  } else {
-    attn_bwd_dq_kernel<128><<<g256(nq), 256, 0, st>>>(q, k, v, o, dout, lse, (int)S, (int)L,
-                                                      (int)H, (int)KVH, scale, dq, delta_scratch,
-                                                      qs, cz);
-    attn_bwd_dkv_kernel<128><<<g256(nk), 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,
-                                                       (int)L, (int)H, (int)KVH, scale, dk, dv, qs,
-                                                       cz);
-  }
+  const unsigned rows_blocks = (unsigned)ceil_div(S * H * L, 4);
+  const dim3 gkv((unsigned)(S * KVH), (unsigned)ceil_div(L, kAB));
+  const dim3 gq((unsigned)(S * H), (unsigned)ceil_div(L, kAB));
+#define SM_AB(HD)                                                                              \
+  do {                                                                                         \
+    attn_bwd_delta_kernel<HD><<<rows_blocks, 256, 0, st>>>(o, dout, (int)S, (int)L, (int)H, qs, \
+                                                           delta_scratch);                     \
+    attn_bwd_dkv_kernel<HD><<<gkv, 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,     \
+                                                 (int)L, (int)H, (int)KVH, scale, dk, dv, qs,  \
+                                                 cz);                                          \
+    attn_bwd_dq_kernel<HD><<<gq, 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S,       \
+                                               (int)L, (int)H, (int)KVH, scale, dq, qs, cz);   \
+  } while (0)
+  if (head_dim == 64) SM_AB(64);
+  else SM_AB(128);
+#undef SM_AB
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

@@ -35,8 +35,9 @@ def _st() -> int:
     return torch.cuda.current_stream().cuda_stream
 
 
-def gemm(a, b, *, ta=False, tb=False, out=None, alpha=1.0, beta=0.0):
-    """out = alpha op(a) op(b) + beta out (sm_gemm_ex), f32 2-D tensors."""
+def gemm(a, b, *, ta=False, tb=False, out=None, alpha=1.0, beta=0.0, entry="sm_gemm_ex"):
+    """out = alpha op(a) op(b) + beta out (sm_gemm_ex, or ``entry`` =
+    "sm_gemm_mfma" for the matrix-core kernel at any size), f32 2-D tensors."""
     M = a.shape[1] if ta else a.shape[0]
     K = a.shape[0] if ta else a.shape[1]
     N = b.shape[0] if tb else b.shape[1]
@@ -45,7 +46,7 @@ def gemm(a, b, *, ta=False, tb=False, out=None, alpha=1.0, beta=0.0):
     if out is None:
         out = torch.empty(M, N, dtype=torch.float32, device=a.device)
         beta = 0.0
-    call("sm_gemm_ex", int(ta), int(tb), M, N, K, float(alpha), a.data_ptr(), a.stride(0),
+    call(entry, int(ta), int(tb), M, N, K, float(alpha), a.data_ptr(), a.stride(0),
          b.data_ptr(), b.stride(0), float(beta), out.data_ptr(), out.stride(0), _st())
     return out
 
@@ -279,7 +280,10 @@ class Policy:
         cc = cfg.c()
         _lib.check(_lib.lib().sm_policy_create(C.byref(cc), C.byref(oc), C.byref(self._h)))
         for name, arr in weights.items():
-            t = torch.as_tensor(np.ascontiguousarray(arr, dtype=np.float32)).to(device)
+            if isinstance(arr, torch.Tensor):  # host or device tensors
+                t = arr.to(device=device, dtype=torch.float32).contiguous()
+            else:
+                t = torch.as_tensor(np.ascontiguousarray(arr, dtype=np.float32)).to(device)
             if name in LAYER_KEYS:
                 for i in range(cfg.layers):
                     call("sm_policy_set_tensor", self._h, _POLICY_KINDS[name], i,

@@ -60,6 +60,37 @@ def test_native_policy_gradient_matches_autograd(dev):
     torch.testing.assert_close(pol.tensor("qkv", 1, gradient=True), 2 * g1, rtol=1e-5, atol=1e-7)
 
 
+def test_native_policy_gradient_on_matrix_cores(dev):
+    """A policy large enough that every linear's forward, data-gradient and
+    weight-gradient GEMM crosses sm_gemm_ex's matrix-core threshold (2^27
+    multiply-adds, 128 x 128 x 16 outputs) and attention spans several 32 x 32
+    backward tiles (127 positions): the staged gradient against float64
+    autograd, as for the small policy."""
+    cfg = ModelConfig(layers=1, d_model=512, heads=4, kv_heads=2, head_dim=128, ffn=1024,
+                      vocab=2048, max_seq=160, quantized=False)
+    w = oracle.random_weights(cfg.oracle_cfg(), seed=21, std=0.05)
+    pol = train.Policy(cfg, w, dev)
+    prompts, tokens, rewards = _batch(cfg, 5, dev, P=64, N=64)
+    beh = torch.full(tokens.shape, -9.0, device=dev)
+    out = pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
+    assert int(out["flags"].abs().sum()) == 0
+    wt = {k: torch.from_numpy(np.asarray(v, dtype=np.float64)).requires_grad_(True)
+          for k, v in w.items()}
+    lp_t = _torch_lp(wt, cfg, prompts.cpu(), tokens.cpu())
+    lp_err = float((out["lp_cur"].cpu().double() - lp_t.detach()).abs().max())
+    print(f"matrix-core policy: max |lp - f64| {lp_err:.2e}", flush=True)
+    assert lp_err < 2e-5
+    (out["dlp"].cpu().double() * lp_t).sum().backward()
+    for k, t in wt.items():
+        layers = range(cfg.layers) if k in train.LAYER_KEYS else [-1]
+        for layer in layers:
+            got = pol.tensor(k, layer, gradient=True).cpu().double()
+            want = t.grad[layer] if layer >= 0 else t.grad
+            err = (got - want).abs().max().item() / (want.abs().max().item() + 1e-12)
+            print(f"  {k}[{layer}] relative gradient error {err:.2e}", flush=True)
+            assert err < 2e-4, (k, layer)
+
+
 def test_native_optimizer_step_adamw_and_clip(dev):
     """AdamW on every tensor after the global-norm clip, against torch in f64
     fed with the policy's own staged gradients."""

@@ -35,6 +35,63 @@ def test_gemm_ex_transposes(dev, ta, tb):
     np.testing.assert_allclose(out.cpu().numpy(), ref, rtol=1e-5, atol=1e-4)
 
 
+def _gemm_case(rng, ta, tb, M, N, K, pad):
+    """A, B (f64) in the stored layouts, as f32 device views whose leading
+    dimension is padded by `pad` (pad 1: odd strides, no 16-byte rows)."""
+    def dev_view(x):
+        r, c = x.shape
+        buf = torch.zeros(r, c + pad, dtype=torch.float32)
+        buf[:, :c] = torch.from_numpy(x.astype(np.float32))
+        return buf.cuda()[:, :c]
+    A = rng.normal(0, 1, (K, M) if ta else (M, K))
+    B = rng.normal(0, 1, (N, K) if tb else (K, N))
+    A32, B32 = A.astype(np.float32).astype(np.float64), B.astype(np.float32).astype(np.float64)
+    ref = (A32.T if ta else A32) @ (B32.T if tb else B32)
+    return dev_view(A), dev_view(B), ref, A32, B32
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K,pad", [(77, 130, 45, 0), (300, 260, 333, 0), (256, 384, 512, 0),
+                                       (129, 257, 100, 1), (1, 5, 1, 0)])
+def test_gemm_mfma_f32_grade(dev, ta, tb, M, N, K, pad):
+    """The three-plane bf16 matrix-core GEMM against f64: its error stays
+    within 4x that of torch's own f32 matmul of the same f32 inputs (a kernel
+    that dropped the third plane, or the cross terms, would be ~2^-17 or
+    ~2^-9 relative, far outside), for every transpose pair, ragged tiles and
+    unaligned leading dimensions; beta = 0 never reads C (NaN there)."""
+    print(f"case gemm_mfma ta={ta} tb={tb} M={M} N={N} K={K} pad={pad}", flush=True)
+    rng = np.random.default_rng(1000 + 4 * ta + 2 * tb + M)
+    a, b, ref, A32, B32 = _gemm_case(rng, ta, tb, M, N, K, pad)
+    out = torch.full((M, N), float("nan"), device=dev)
+    train.gemm(a, b, ta=bool(ta), tb=bool(tb), out=out, alpha=1.0, beta=0.0, entry="sm_gemm_mfma")
+    t32 = ((torch.from_numpy(A32).float().T if ta else torch.from_numpy(A32).float())
+           @ (torch.from_numpy(B32).float().T if tb else torch.from_numpy(B32).float()))
+    err = float(np.abs(out.cpu().double().numpy() - ref).max())
+    err32 = float(np.abs(t32.double().numpy() - ref).max())
+    print(f"  max |err| {err:.3g} vs torch f32 {err32:.3g}", flush=True)
+    assert err <= 4 * err32 + 1e-6
+    # alpha / beta
+    C = rng.normal(0, 1, (M, N))
+    out2 = torch.from_numpy(C.astype(np.float32)).to(dev)
+    train.gemm(a, b, ta=bool(ta), tb=bool(tb), out=out2, alpha=0.5, beta=2.0, entry="sm_gemm_mfma")
+    np.testing.assert_allclose(out2.cpu().numpy(), 0.5 * ref + 2.0 * C.astype(np.float32),
+                               rtol=1e-5, atol=1e-4)
+
+
+def test_gemm_ex_large_runs_on_matrix_cores(dev):
+    """Above its size threshold sm_gemm_ex is the matrix-core kernel (same
+    bits as sm_gemm_mfma); below it, the f32 FMA kernel (within f32 rounding)."""
+    rng = np.random.default_rng(7)
+    for (M, N, K) in [(512, 512, 512), (64, 96, 80)]:
+        print(f"case gemm_ex dispatch M={M} N={N} K={K}", flush=True)
+        a, b, ref, _, _ = _gemm_case(rng, 0, 1, M, N, K, 0)
+        o1 = train.gemm(a, b, tb=True)
+        o2 = train.gemm(a, b, tb=True, entry="sm_gemm_mfma")
+        if M * N * K >= 1 << 27:
+            assert torch.equal(o1, o2)
+        np.testing.assert_allclose(o1.cpu().numpy(), ref, rtol=1e-5, atol=1e-4)
+
+
 def test_rmsnorm_backward_matches_autograd(dev):
     rows, d, eps = 33, 300, 1e-5
     x = torch.randn(rows, d, dtype=torch.float64, requires_grad=True)
@@ -100,9 +157,13 @@ def _attn_t(q, k, v, H, KVH):
     return torch.einsum("shlt,shtd->slhd", p, vv), torch.logsumexp(sc, -1)
 
 
-@pytest.mark.parametrize("hd,H,KVH", [(64, 4, 2), (128, 4, 4)])
-def test_attention_backward_matches_autograd(dev, hd, H, KVH):
-    S, L = 2, 21
+@pytest.mark.parametrize("hd,H,KVH,L", [(64, 4, 2, 21), (128, 4, 4, 21), (128, 8, 2, 100),
+                                        (64, 4, 1, 70), (128, 2, 2, 64)])
+def test_attention_backward_matches_autograd(dev, hd, H, KVH, L):
+    """Causal GQA backward (32 x 32 tiles: one partial tile, several tiles with
+    a partial last one, exact tiles) against float64 autograd."""
+    print(f"case attention backward hd={hd} H={H} KVH={KVH} L={L}", flush=True)
+    S = 2
     q = torch.randn(S, L, H, hd, dtype=torch.float64, requires_grad=True)
     k = torch.randn(S, KVH, L, hd, dtype=torch.float64, requires_grad=True)
     v = torch.randn(S, KVH, L, hd, dtype=torch.float64, requires_grad=True)
