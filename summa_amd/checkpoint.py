@@ -181,13 +181,14 @@ def load_archive(model: Model, root) -> dict:
             f = arc.floating[name]
             if f.shape != burn_shape:
                 raise CheckpointError(f"{name}: shape {f.shape}, expected {burn_shape}")
-            a = _to_model_layout(f.to_f32(), rule)
+            a = np.require(_to_model_layout(f.to_f32(), rule), requirements="W")
             model.set_tensor(kind, torch.from_numpy(a).to(dev), layer)
     if tied:
         if "embedding.weight" in arc.matrices:
             emb = arc.matrices["embedding.weight"].decode(dev)
         else:
-            emb = torch.from_numpy(arc.floating["embedding.weight"].to_f32()).to(dev)
+            emb = torch.from_numpy(np.require(arc.floating["embedding.weight"].to_f32(),
+                                              requirements="W")).to(dev)
         model.set_tensor("lm_head", emb)
     torch.cuda.synchronize()
     return {"format": arc.manifest["recipe"]["format"], "tied": tied,
