@@ -268,7 +268,8 @@ class Policy:
     """The library's trainable policy (``sm_policy``): prepare_device_batch's
     recompute, GRPO loss and staged backward in one call, optimizer_step in
     another (posttrain.rs:1288-1305), with the trainer's optimizer settings as
-    defaults (AdamW 3e-4 / 0.9 / 0.95 / 1e-8 / wd 0.1, global-norm clip 1.0;
+    defaults (AdamW 3e-4 / 0.9 / 0.95 / 1e-8 / wd 0.1, global-norm clip 1.0: the
+    CLI defaults of summa-train/src/main.rs:171-176 and trainer.rs:1124-1129;
     ``muon_lr > 0`` adds Muon for the per-layer projections)."""
 
     def __init__(self, cfg: ModelConfig, weights: dict, device, lr=3e-4, betas=(0.9, 0.95),
