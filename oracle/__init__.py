@@ -74,7 +74,7 @@ class OrModel(C.Structure):
         [("experts", C.c_int32), ("expert_ffn", C.c_int32)] + \
         [(n, C.c_void_p) for n in ("router", "exp_in", "exp_down", "exp_in_c", "exp_down_c",
                                    "exp_in_s", "exp_down_s", "router_gap", "route_hint")] + \
-        [("hint_margin", C.c_float), ("hint_conflicts", C.c_void_p)]
+        [("hint_margin", C.c_float), ("hint_conflicts", C.c_void_p), ("kv_f32", C.c_int32)]
 
 
 def _declare_model(L: C.CDLL) -> None:
@@ -202,9 +202,12 @@ class HostModel:
     instead of in / down, each expert quantized as its own tensor. When ``quantized`` the linears are
     packed with the Q4G128 oracle codec and the embedding is rounded to bf16.
     ``acc64`` (default: on for quantized models) accumulates matmuls in f64.
+    ``kv_f32`` keeps a quantized model's q, k and v in f32 (the trainable
+    policy's forward) instead of rounding them to f16 (the inference cache).
     """
 
-    def __init__(self, cfg: dict, weights: dict, quantized: bool, acc64: bool | None = None):
+    def __init__(self, cfg: dict, weights: dict, quantized: bool, acc64: bool | None = None,
+                 kv_f32: bool = False):
         self.cfg, self.quantized = cfg, quantized
         self._keep = []
         w = {k: np.ascontiguousarray(v, dtype=np.float32) for k, v in weights.items()}
@@ -216,6 +219,7 @@ class HostModel:
             setattr(m, k, int(cfg[k]))
         m.quantized = int(quantized)
         m.acc64 = int(quantized if acc64 is None else acc64)
+        m.kv_f32 = int(kv_f32)
         m.eps, m.theta = float(cfg.get("eps", 1e-5)), float(cfg.get("theta", 1e4))
         for k in ("embed", "attn_norm", "ffn_norm", "final_norm"):
             setattr(m, k, self._ptr(w[k]))

@@ -14,7 +14,8 @@
  *   log-prob recompute    summa-train/src/tensor_sleep.rs:2531-2689
  * in fp32, as the reference's CPU path computes, with one storage rounding
  * for quantized models: q, k and v are rounded to f16 (the device's 16-bit KV
- * cache and query); the embedding table is bf16 (rounded by the caller). The
+ * cache and query; kv_f32 keeps them f32, the policy's training forward); the
+ * embedding table is bf16 (rounded by the caller). The
  * device keeps matmul inputs at fp32-grade precision (f16 hi + lo pairs), so
  * no activation rounding is modelled here. Matmul dot products accumulate
  * sequentially in fp32 (the order PackedTensor::matrix_vector uses,
@@ -57,10 +58,16 @@ typedef struct or_model {
   const int32_t* route_hint;
   float hint_margin;
   int32_t* hint_conflicts;
+  /* 1: keep q, k and v in f32 for a quantized model (the trainable policy's
+   * forward, whose attention runs in f32 over f32 K / V); 0: round them to
+   * f16 as the device's inference path stores them */
+  int32_t kv_f32;
 } or_model;
 
 /* f16 rounding of q, k and v (the 16-bit KV cache) of quantized models. */
-static float rkv(const or_model* m, float v) { return m->quantized ? or_round_f16(v) : v; }
+static float rkv(const or_model* m, float v) {
+  return (m->quantized && !m->kv_f32) ? or_round_f16(v) : v;
+}
 
 static float q4_at(const uint8_t* codes, const uint16_t* scales, int64_t i) {
   const uint8_t byte = codes[i / 2];

@@ -205,6 +205,26 @@ def test_quantized_oracle_close_to_dequantized_f32():
     assert np.abs(a - b).max() > 0  # the f16 q/k/v rounding is really applied
 
 
+def test_quantized_oracle_with_f32_kv_equals_dequantized_f32():
+    """kv_f32 removes the only rounding the quantized path adds: with q, k and
+    v kept in f32 it equals the f32 model on the decoded Q4 weights (both
+    accumulating in f64), while the default rounds them to f16."""
+    cfg = dict(TINY, d=128, F=128, hd=32, H=4, KVH=2)
+    w = oracle.random_weights(cfg, seed=10, std=0.05)
+    q = oracle.HostModel(cfg, w, quantized=True)
+    qf = oracle.HostModel(cfg, w, quantized=True, kv_f32=True)
+    wd = dict(w)
+    for k in ("qkv", "o", "in", "down", "lm_head"):
+        codes, scales = q.packed[k]
+        wd[k] = oracle.q4_decode(codes, scales, w[k].size).reshape(w[k].shape)
+    wd["embed"] = oracle.round_bf16(w["embed"])
+    f = oracle.HostModel(cfg, wd, quantized=False, acc64=True)
+    ids = np.random.default_rng(11).integers(0, cfg["V"], (2, 9)).astype(np.int32)
+    a, b, c = qf.forward_logits(ids), f.forward_logits(ids), q.forward_logits(ids)
+    assert np.abs(a - b).max() <= 1e-6 * max(1.0, np.abs(b).max())
+    assert np.abs(c - b).max() > 10 * np.abs(a - b).max()
+
+
 def test_moe_quantized_oracle_close_to_dequantized_f32():
     # per-expert Q4G128 packing: decoding each expert's codes gives the f32
     # model the quantized MoE path approximates (f16 q/k/v rounding only)

@@ -13,6 +13,8 @@ import oracle
 from summa_amd import _lib, train
 from summa_amd.model import Model, ModelConfig, rl_prepare
 
+from _workloads import build_models
+from summa_amd.configs import RL_WORKLOADS
 from test_train_gpu import CFG, _torch_lp
 
 pytestmark = pytest.mark.gpu
@@ -89,6 +91,43 @@ def test_native_policy_gradient_on_matrix_cores(dev):
             err = (got - want).abs().max().item() / (want.abs().max().item() + 1e-12)
             print(f"  {k}[{layer}] relative gradient error {err:.2e}", flush=True)
             assert err < 2e-4, (k, layer)
+
+
+@pytest.mark.timeout(600)
+def test_policy_at_config2_geometry_against_oracle(dev):
+    """The trainable policy at config[2]'s full geometry (24 layers, d 2048,
+    16 / 4 heads, F 5632, V 65536: 1.35 G f32 masters, fake-quantized Q4G128
+    forward) on a small batch rolled out by the installed Q4 model: its
+    recompute (f32 activations, matrix-core GEMMs at these shapes, tiled
+    attention) against the CPU oracle's quantized model with q, k and v kept
+    in f32 as the policy keeps them (an f32 computation: 5e-5 after 24
+    layers; measured 1e-5), then one optimizer step (finite norm) after which the installed
+    model's log-probs move."""
+    wl = RL_WORKLOADS[2]
+    mc, (model,), host_w = build_models(wl, dev, seed=3, count=1)
+    print(f"case policy at config[2] geometry: layers={mc.layers} d={mc.d_model}", flush=True)
+    pol = train.Policy(mc, host_w, dev)
+    G, P, N = 4, 24, 8
+    gen = torch.Generator().manual_seed(11)
+    prompts = torch.randint(0, mc.vocab, (G, P), generator=gen, dtype=torch.int32).to(dev)
+    tok, beh = model.generate(prompts, N, temperature=1.0, seed=5)
+    rewards = torch.rand(1, G, generator=gen).to(dev)
+    out = pol.prepare(None, prompts, tok, beh, rewards, kl_coefficient=0.0)
+    assert int(out["flags"].abs().sum()) == 0
+    host = oracle.HostModel(mc.oracle_cfg(), host_w, quantized=True, kv_f32=True)
+    del host_w
+    lp_or, _ = host.continuation(prompts.cpu().numpy(), tok.cpu().numpy())
+    lp = out["lp_cur"].cpu().numpy()
+    err = float(np.abs(lp - lp_or).max())
+    gap = float((out["lp_cur"] - beh).abs().max())
+    print(f"policy recompute vs oracle (f32 q/k/v) {err:.2e}; vs the Q4 rollout (f16 KV "
+          f"cache) {gap:.2e}", flush=True)
+    assert err <= 5e-5
+    norm = pol.optimizer_step(1.0)
+    assert np.isfinite(norm) and norm > 0
+    before = model.logprobs(prompts, tok)
+    pol.install(model)
+    assert float((model.logprobs(prompts, tok) - before).abs().max()) > 0
 
 
 def test_native_optimizer_step_adamw_and_clip(dev):
