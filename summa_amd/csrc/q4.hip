@@ -549,17 +549,19 @@ inline bool use_dense_lds_split(int64_t M, int64_t K, int64_t logical_cols, int 
          (K > 2048 || logical_cols < 2048) && logical_cols <= 8192;
 }
 
-template <int XT>
-int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1) {
-  // 256 columns per workgroup: measured against 512 at config[4] decode
-  // (FFN-in 30 vs 32 us, down 17 vs 24 us: the narrower tile gives the down
-  // projection's 2048 columns enough workgroups)
-  constexpr int NB = 2;
+// SwiGLU tiles pair gate and value blocks, so they need an even NB
+template <int NB, int E, int XT>
+void launch_gl(dim3 grid, hipStream_t st, const Q4Args& a) {
+  if constexpr (!is_swiglu(E) || NB % 2 == 0) q4_grouped_lds_kernel<NB, E, XT><<<grid, 512, 0, st>>>(a);
+}
+
+template <int XT, int NB>
+int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks) {
   const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
   const dim3 grid((unsigned)ceil_div(logical_cols, 8 * 16 * NB), (unsigned)row_tiles, (unsigned)ks);
   switch (epi) {
 #define SM_GL(E) \
-    case E: q4_grouped_lds_kernel<NB, E, XT><<<grid, 512, 0, st>>>(a); break;
+    case E: launch_gl<NB, E, XT>(grid, st, a); break;
     SM_GL(EPI_STORE_F32)
     SM_GL(EPI_STORE_BF16)
     SM_GL(EPI_ADD_F32)
@@ -573,6 +575,19 @@ int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_til
   SM_LAUNCH_CHECK();
   if (ks > 1) return splitk_reduce(a.part, ks, a.M, a.N, a.ncols, a.y, a.ldy, epi, st);
   return SM_OK;
+}
+
+// 256 columns per workgroup: measured against 512 at config[4] decode
+// (FFN-in 30 vs 32 us, down 17 vs 24 us: the narrower tile gives the down
+// projection's 2048 columns enough workgroups). Dense non-SwiGLU launches of
+// at most 128 rows take 128 columns (one 16-column block per wave; the same
+// bits): config[1] rollout 213.4 -> 206.8 ms, config[4] 844 -> 837 ms, while
+// config[2]'s 256-row decode is 0.8 % slower that way and keeps 256.
+template <int XT>
+int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1) {
+  if (!a.tiles && !is_swiglu(epi) && a.M <= 128)
+    return launch_grouped_lds_nb<XT, 1>(a, epi, st, row_tiles, ks);
+  return launch_grouped_lds_nb<XT, 2>(a, epi, st, row_tiles, ks);
 }
 
 // M = 1 (one sequence's decode step; the LM head at batch 1). One wave owns a
