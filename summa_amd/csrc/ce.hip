@@ -13,16 +13,19 @@
 //   * lp / loss only: one 256-thread workgroup per row, 4 x 16 B loads in
 //     flight per lane, online max/sum in registers, wave shuffles + LDS merge.
 //     Traffic = one read of the logits.
-//   * lp + grad in place: one 1024-thread workgroup per row streams the row
+//   * lp + grad in place: one 512-thread workgroup per row streams the row
 //     twice: a statistics pass with ordinary (cached) loads, then a gradient
-//     pass whose loads and stores are nontemporal (last use). Between the two
-//     passes the row (256 KB at config[3]) stays in the 256 MB MALL, so HBM
-//     sees about one read and one write. Measured on config[3] (bf16
-//     65536 x 131072) this runs at the speed of a plain in-place streaming
-//     copy of the same bytes (7.0 ms, 4.9 TB/s read + write); keeping each row
-//     in VGPRs (read once, write once) was 9.9 ms: a 1024-thread workgroup
-//     holding 256 KB in registers fits once per CU, so its read, reduce and
-//     write phases never overlap with another row's.
+//     pass whose loads and stores are nontemporal (last use), 8 vectors per
+//     lane in flight. The second read of a row (256 KB at config[3]) misses
+//     L2: the L2-miss read counter shows 1.76x the algorithmic read, served by
+//     the 256 MB MALL or by HBM. Config[3] (bf16 65536 x 131072): 7.2 ms for
+//     34 GB of algorithmic traffic; a plain elementwise in-place pass over the
+//     same bytes (one read, one write, no statistics pass) runs at 5.9 TB/s.
+//     Plain or mixed load / store kinds in the second pass: 7.4-7.6 ms; 1024
+//     threads x 4 vectors: 7.3-7.4 ms. Keeping each row in VGPRs
+//     (read once, write once) was 9.9 ms: a 1024-thread workgroup holding
+//     256 KB in registers fits once per CU, so its read, reduce and write
+//     phases never overlap with another row's.
 #include <cfloat>
 #include <cmath>
 
@@ -309,8 +312,8 @@ int launch_ce(const void* logits, const int32_t* targets, int64_t rows, int64_t 
     return SM_OK;
   }
   if (vec) {
-    ce_grad_stream_kernel<1024, 4, BF16><<<grid, 1024, 0, st>>>(grad, targets, ld, vl, lp, lse,
-                                                                 grad_scale, row_scale);
+    ce_grad_stream_kernel<512, 8, BF16><<<grid, 512, 0, st>>>(grad, targets, ld, vl, lp, lse,
+                                                               grad_scale, row_scale);
   } else {
     ce_grad_2pass_kernel<256, BF16, false><<<grid, 256, 0, st>>>(grad, targets, ld, vl, lp, lse,
                                                                  grad_scale, row_scale);
