@@ -452,7 +452,7 @@ int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_
   const AttnStrides rows = AttnStrides::rows(L, H, hd);
   const AttnStrides qs = qs_in ? *qs_in : rows, os = os_in ? *os_in : rows;
   const int cz = causal ? 1 : 0;
-  if (L >= 32 && (hd == 64 || hd == 128)) {  // many queries per (sequence, head): tiled
+  if (L >= 32 && ceil_div(L, 32) <= 65535 && (hd == 64 || hd == 128)) {  // many queries: tiled
     const dim3 grid((unsigned)((int64_t)S * H), (unsigned)ceil_div(L, 32));
     if (hd == 64)
       attn_f32_tiled_kernel<64><<<grid, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L,

@@ -228,6 +228,7 @@ extern "C" int sm_gemm_mfma(int trans_a, int trans_b, int64_t M, int64_t N, int6
              "sm_gemm_mfma: leading dimension too small");
   if (M == 0 || N == 0) return SM_OK;
   SM_REQUIRE(K > 0, "sm_gemm_mfma: K must be positive");
+  SM_REQUIRE(ceil_div(M, 128) <= 65535, "sm_gemm_mfma: M above 65535 x 128 rows");
   return gemm_bf16x3(trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
                      as_stream(stream));
 }

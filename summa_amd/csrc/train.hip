@@ -499,6 +499,7 @@ extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_
   SM_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N,
              "sm_gemm_ex: leading dimension too small");
   if (M == 0 || N == 0) return SM_OK;
+  SM_REQUIRE(ceil_div(M, 64) <= 65535, "sm_gemm_ex: M above 65535 x 64 rows");
   hipStream_t st = as_stream(stream);
   // large problems on the matrix cores (f32-grade three-plane bf16 products,
   // gemm_mfma.hip); small ones, where a launch has few 128 x 128 tiles, here
@@ -564,6 +565,8 @@ int attn_backward_f32(const float* q, const float* k, const float* v, const floa
   SM_REQUIRE(al16(q) && al16(k) && al16(v) && al16(dout) && qs.seq % 4 == 0 && qs.pos % 4 == 0 &&
                  qs.head % 4 == 0,
              "attention backward: q, k, v and grad_out need 16-byte aligned rows");
+  SM_REQUIRE(ceil_div(L, kAB) <= 65535, "attention backward: sequence longer than %d",
+             65535 * kAB);
   const float scale = 1.0f / sqrtf((float)head_dim);
   const int cz = causal ? 1 : 0;
   const unsigned rows_blocks = (unsigned)ceil_div(S * H * L, 4);
