@@ -593,6 +593,21 @@ int64_t sm_rl_workspace_bytes(sm_model* model, int64_t S, int64_t P, int64_t N,
 int sm_model_bind_workspace(sm_model* model, void* ws, int64_t bytes, int64_t S, int64_t P,
                             int64_t N, int64_t max_tokens_per_forward);
 
+/* Prompt groups (GrpoGenerationBatchRequest: one example per group of
+ * group_size rollouts, posttrain.rs:1206-1216; padded_group_log_probabilities
+ * takes one prefix per group, summa-train/src/tensor_sleep.rs:2642-2689):
+ * with group_size G > 1, later sm_rl_generate / sm_rl_generate_ex /
+ * sm_rl_logprobs / sm_rl_prepare calls on this model take rollouts
+ * g*G .. g*G+G-1 to share one prompt and compute the prompt positions once
+ * per group (the prefill, and the recompute's prompt part), copying their
+ * K / V to the group's rollouts: the same values as per rollout, since a
+ * prompt position depends on the prompt alone. Each call checks on the device
+ * that S is whole groups and every prompt row equals its group's first (one
+ * host synchronisation; SM_ERR_INVALID otherwise). 1 (the default) computes
+ * every rollout's prompt. Set it before sm_rl_workspace_bytes /
+ * sm_model_bind_workspace, whose sizes depend on it. */
+int sm_model_set_prompt_groups(sm_model* model, int64_t group_size);
+
 /* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout
  * the semantics of TextGenerator::generate, generate.rs:68-124, with no EOS):
  * prompts [S, P] int32 -> tokens [S, N] int32 and behavior_lp [S, N] f32

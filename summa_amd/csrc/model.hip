@@ -161,6 +161,82 @@ __global__ void zero_i32_kernel(int32_t* p, int n) {
   if (i < n) p[i] = 0;
 }
 
+// ---- prompt groups: G consecutive rollouts share one prompt
+// flag[0] = 1 where a prompt row differs from its group's first row (every
+// writer stores the same value)
+__global__ void check_groups_kernel(const int32_t* __restrict__ prompts, int64_t S, int G, int P,
+                                    int32_t* __restrict__ flag) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S * P) return;
+  const int64_t s = i / P, t = i % P;
+  if (prompts[i] != prompts[(s / G) * G * P + t]) flag[0] = 1;
+}
+
+// out [groups, P] <- prompt row g * G
+__global__ void group_prompts_kernel(const int32_t* __restrict__ prompts, int64_t groups, int G,
+                                     int P, int32_t* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= groups * P) return;
+  const int64_t g = i / P, t = i % P;
+  out[i] = prompts[g * G * P + t];
+}
+
+// K or V cache rows of positions 0..P-1 for `nl` layers: sequence s of dst
+// ([S][KVH][cap][hd] per layer, layer stride dls bytes) <- group
+// (s0 + s) / G - g0 of src ([groups][KVH][P][hd], layer stride sls bytes);
+// rows of rb bytes, copied in 16-byte chunks
+__global__ void broadcast_prefix_kernel(const char* __restrict__ src, char* __restrict__ dst,
+                                        int nl, int64_t S, int64_t s0, int64_t g0, int G, int KVH,
+                                        int P, int cap, int rb, int64_t sls, int64_t dls) {
+  const int q16 = rb / 16;
+  const int64_t n = (int64_t)nl * S * KVH * P * q16;
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int q = i % q16;
+  int64_t r = i / q16;
+  const int pos = r % P;
+  r /= P;
+  const int kh = r % KVH;
+  r /= KVH;
+  const int64_t s = r % S;
+  const int l = (int)(r / S);
+  const int64_t g = (s0 + s) / G - g0;
+  const char* from = src + l * sls + ((g * KVH + kh) * P + pos) * (int64_t)rb + q * 16;
+  char* to = dst + l * dls + ((s * KVH + kh) * (int64_t)cap + pos) * rb + q * 16;
+  *reinterpret_cast<u32x4*>(to) = *reinterpret_cast<const u32x4*>(from);
+}
+
+// rows [S, d] <- x[((s / G) * L + off), :] (the group's hidden row)
+__global__ void gather_group_rows_kernel(const float* __restrict__ x, int64_t S, int G, int L,
+                                         int off, int d, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S * d) return;
+  const int64_t s = i / d;
+  const int c = i % d;
+  out[i] = x[((s / G) * L + off) * d + c];
+}
+
+// continuation ids [S, N-1] <- tokens[:, :N-1]
+__global__ void cont_ids_kernel(const int32_t* __restrict__ tokens, int64_t S, int N,
+                                int32_t* __restrict__ ids) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S * (N - 1)) return;
+  ids[i] = tokens[(i / (N - 1)) * N + i % (N - 1)];
+}
+
+// scored rows [S, N, d] of rollouts s0..s0+S-1: n = 0 from the group's last
+// prompt row prow[(s0 + s) / G], n >= 1 from the continuation pass xc[s, n-1]
+__global__ void gather_cont_rows_kernel(const float* __restrict__ prow,
+                                        const float* __restrict__ xc, int64_t S, int64_t s0,
+                                        int G, int N, int d, float* __restrict__ out) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= S * N * d) return;
+  const int c = i % d;
+  const int64_t sn = i / d, s = sn / N;
+  const int n = sn % N;
+  out[i] = n == 0 ? prow[((s0 + s) / G) * d + c] : xc[(s * (N - 1) + n - 1) * d + c];
+}
+
 unsigned blocks_for(int64_t n) { return (unsigned)ceil_div(n > 0 ? n : 1, 256); }
 
 }  // namespace
@@ -187,6 +263,11 @@ struct sm_model {
   // workspace
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
       lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws, seen, done;
+  // prompt groups (sm_model_set_prompt_groups): rollouts g*G .. g*G+G-1 share
+  // one prompt, whose positions are computed once per group: their K / V for
+  // every layer [layers][groups][KVH][P][hd] and last hidden rows [groups, d]
+  int64_t prompt_group = 1;
+  sm::DevBuf pkc, pvc, prow;
   int64_t gen_cap = 0, gen_S = 0;
   // caller-bound workspace (sm_model_bind_workspace): the buffers above are
   // fixed slices of it
@@ -298,12 +379,25 @@ size_t cache_layer_elems(const sm_model* m, int64_t S, int64_t cap) {
   return (size_t)S * m->cfg.kv_heads * cap * m->cfg.head_dim;
 }
 
+// The K / V of prompt positions 0..P-1 computed once per group of G rollouts
+// (src [layers][groups][KVH][P][hd], layer stride `layer_bytes`), for
+// run_layers over rollouts s0, s0 + 1, ... of a continuation.
+struct PrefixKV {
+  const void* k;
+  const void* v;
+  int64_t layer_bytes;
+  int G, P;
+  int64_t s0;
+};
+
 // All decoder layers over S sequences x L tokens (ids [S*L]) at positions
 // pos0[s] + i. K/V go to caches (per-layer stride `layer_elems`, 0 = one
 // buffer reused by every layer). decode: L == 1 and attention uses `lens`.
+// pre: before each layer, its prompt K / V go into cache positions 0..P-1 of
+// every sequence (the continuation of a group's prompt, pos0 = P).
 int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int32_t* pos0,
                const int32_t* lens, void* kc, void* vc, size_t layer_elems, int64_t cap,
-               bool decode, hipStream_t st) {
+               bool decode, hipStream_t st, const PrefixKV* pre = nullptr) {
   const auto& c = m->cfg;
   const int64_t rows = S * L;
   const int64_t d = c.d_model;
@@ -319,6 +413,14 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
     const Layer& Ly = m->layers[l];
     char* kl = (char*)kc + (size_t)l * layer_elems * m->kv_size;
     char* vl = (char*)vc + (size_t)l * layer_elems * m->kv_size;
+    if (pre) {
+      const int rb = c.head_dim * (int)m->kv_size;
+      const int64_t n = S * c.kv_heads * pre->P * (rb / 16);
+      for (int kv = 0; kv < 2; ++kv)
+        broadcast_prefix_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
+            (const char*)(kv ? pre->v : pre->k) + l * pre->layer_bytes, kv ? vl : kl, 1, S,
+            pre->s0, 0, pre->G, c.kv_heads, pre->P, (int)cap, rb, 0, 0);
+    }
     SM_TRY(sm_rmsnorm(x, Ly.attn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
     if (c.quantized) {  // qkv projection with RoPE + cache append in its epilogue
       SM_TRY(sm_q4_qkv_rope(Ly.qkv.codes, Ly.qkv.scales, c.heads, c.kv_heads, c.head_dim, d,
@@ -352,6 +454,66 @@ int head(sm_model* m, const float* xrows, int64_t M, float* logits, hipStream_t 
   SM_TRY(ensure(m->h, (size_t)M * std::max<int64_t>(m->cfg.d_model, m->qdim) * m->act_size));
   SM_TRY(sm_rmsnorm(xrows, m->final_norm, M, m->cfg.d_model, m->cfg.norm_eps, m->h.p, m->act, st));
   return linear_f32out(m, m->lm_head, m->h.p, M, logits, false, st);
+}
+
+// Prompt groups: S must be whole groups of G and every prompt row equal to
+// its group's first (checked on the device; one host synchronisation).
+int check_prompt_groups(sm_model* m, const int32_t* prompts, int64_t S, int64_t P,
+                        hipStream_t st) {
+  const int64_t G = m->prompt_group;
+  SM_REQUIRE(S % G == 0, "prompt groups of %lld: %lld rollouts are not whole groups",
+             (long long)G, (long long)S);
+  SM_TRY(ensure(m->flags, 4));
+  int32_t* f = (int32_t*)m->flags.p;
+  zero_i32_kernel<<<1, 64, 0, st>>>(f, 1);
+  check_groups_kernel<<<blocks_for(S * P), 256, 0, st>>>(prompts, S, (int)G, (int)P, f);
+  int32_t bad = 0;
+  SM_HIP(hipMemcpyAsync(&bad, f, 4, hipMemcpyDeviceToHost, st));
+  SM_HIP(hipStreamSynchronize(st));
+  SM_REQUIRE(bad == 0, "prompt groups of %lld: a rollout's prompt differs from its group's first",
+             (long long)G);
+  return SM_OK;
+}
+
+// The prompt prefill of a generation: cache positions 0..P-1 of every
+// rollout and its last prompt hidden row in m->rows [S, d]. With prompt
+// groups each group's prompt runs once and is copied to its rollouts (the
+// same values: a prompt position depends on the prompt alone).
+int prefill_prompts(sm_model* m, const int32_t* prompts, int64_t S, int64_t P, int64_t cap,
+                    size_t layer_elems, hipStream_t st) {
+  const auto& c = m->cfg;
+  int32_t* pos = (int32_t*)m->pos.p;
+  int32_t* lens = (int32_t*)m->lens.p;
+  const int64_t G = m->prompt_group;
+  if (G <= 1) {
+    set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, 0);
+    SM_TRY(run_layers(m, prompts, S, P, pos, nullptr, m->kc.p, m->vc.p, layer_elems, cap, false,
+                      st));
+    gather_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>(
+        (const float*)m->x.p, (int)S, (int)P, (int)P - 1, c.d_model, (float*)m->rows.p);
+    return SM_OK;
+  }
+  SM_TRY(check_prompt_groups(m, prompts, S, P, st));
+  const int64_t groups = S / G;
+  const size_t pl = (size_t)groups * c.kv_heads * P * c.head_dim;  // elements per layer
+  SM_TRY(ensure(m->pkc, pl * c.layers * m->kv_size));
+  SM_TRY(ensure(m->pvc, pl * c.layers * m->kv_size));
+  SM_TRY(ensure(m->ids, (size_t)groups * P * 4));
+  int32_t* ids = (int32_t*)m->ids.p;
+  group_prompts_kernel<<<blocks_for(groups * P), 256, 0, st>>>(prompts, groups, (int)G, (int)P,
+                                                                ids);
+  set_positions_kernel<<<blocks_for(groups), 256, 0, st>>>(pos, lens, (int)groups, 0);
+  SM_TRY(run_layers(m, ids, groups, P, pos, nullptr, m->pkc.p, m->pvc.p, pl, P, false, st));
+  const int rb = c.head_dim * (int)m->kv_size;
+  const int64_t n = (int64_t)c.layers * S * c.kv_heads * P * (rb / 16);
+  for (int kv = 0; kv < 2; ++kv)
+    broadcast_prefix_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
+        (const char*)(kv ? m->pvc.p : m->pkc.p), (char*)(kv ? m->vc.p : m->kc.p), c.layers, S, 0,
+        0, (int)G, c.kv_heads, (int)P, (int)cap, rb, (int64_t)(pl * m->kv_size),
+        (int64_t)(layer_elems * m->kv_size));
+  gather_group_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>(
+      (const float*)m->x.p, S, (int)G, (int)P, (int)P - 1, c.d_model, (float*)m->rows.p);
+  return SM_OK;
 }
 
 }  // namespace
@@ -437,7 +599,7 @@ std::vector<DevBuf*> model_bufs(sm_model* m) {
   return {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits, &m->rows,
           &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc, &m->rkc, &m->rvc,
           &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w, &m->moe_plan, &m->moe_u, &m->moe_y,
-          &m->moe_err, &m->mmws, &m->seen, &m->done};
+          &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow};
 }
 
 void release_bufs(sm_model* m) {
@@ -501,9 +663,13 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
     plan_max(at(m->h), (size_t)M * std::max<int64_t>(d, m->qdim) * m->act_size);
     mm(M, c.vocab, d, SM_EPI_STORE_F32);
   };
-  // generation: prefill S*P rows, decode steps S rows, head S rows
+  // generation: prefill S*P rows (groups*P with prompt groups), decode steps
+  // S rows, head S rows
   const int64_t cap = P + N - 1;
-  layers(S * P);
+  const int64_t G = m->prompt_group;
+  const bool grouped = G > 1 && S % G == 0;
+  const int64_t groups = grouped ? S / G : S;
+  layers(groups * P);
   layers(S);
   head(S);
   const size_t cache = (size_t)S * c.kv_heads * cap * c.head_dim * c.layers * m->kv_size;
@@ -531,6 +697,21 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
   const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 29) / c.vocab);
   head(std::min(rows, rchunk));
   plan_max(at(m->logits), (size_t)std::min(rows, rchunk) * c.vocab * 4);
+  if (grouped) {
+    // every group's prompt K / V for all layers, its last hidden rows; the
+    // recompute's prompt chunks of whole prompts
+    const size_t prefix = (size_t)groups * c.kv_heads * P * c.head_dim * c.layers * m->kv_size;
+    plan_max(at(m->pkc), prefix);
+    plan_max(at(m->pvc), prefix);
+    plan_max(at(m->prow), (size_t)groups * d * 4);
+    const int64_t gchunk = std::max<int64_t>(1, budget / P);
+    const int64_t prow_rows = std::min(groups, gchunk) * P;
+    layers(prow_rows);
+    plan_max(at(m->ids), (size_t)std::max(groups * P, prow_rows) * 4);
+    plan_max(at(m->pos), (size_t)groups * 4);
+    plan_max(at(m->lens), (size_t)groups * 4);
+    plan_max(at(m->flags), 4);
+  }
   return plan;
 }
 
@@ -590,6 +771,14 @@ extern "C" int sm_model_bind_workspace(sm_model* m, void* ws, int64_t bytes, int
 }
 
 extern "C" int64_t sm_model_weight_bytes(const sm_model* m) { return m ? (int64_t)m->weight_bytes : 0; }
+
+extern "C" int sm_model_set_prompt_groups(sm_model* m, int64_t group_size) {
+  SM_REQUIRE(m, "sm_model_set_prompt_groups: null model");
+  SM_REQUIRE(group_size >= 1 && group_size <= (1 << 20),
+             "sm_model_set_prompt_groups: group size must be in 1..2^20");
+  m->prompt_group = group_size;
+  return SM_OK;
+}
 
 extern "C" int sm_model_trace_routes(sm_model* m, int32_t* idx, float* logits, int64_t capacity) {
   SM_REQUIRE(m, "sm_model_trace_routes: null model");
@@ -823,11 +1012,7 @@ extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, in
   int32_t* pos = (int32_t*)m->pos.p;
   int32_t* lens = (int32_t*)m->lens.p;
   // prefill over the prompts at positions 0..P-1
-  set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, 0);
-  SM_TRY(run_layers(m, prompts, S, P, pos, nullptr, m->kc.p, m->vc.p, layer_elems, cap, false, st));
-  gather_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>((const float*)m->x.p, (int)S,
-                                                                (int)P, (int)P - 1, c.d_model,
-                                                                (float*)m->rows.p);
+  SM_TRY(prefill_prompts(m, prompts, S, P, cap, layer_elems, st));
   SM_TRY(head(m, (const float*)m->rows.p, S, (float*)m->logits.p, st));
   SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, 0, tokens, N,
                    behavior_lp, N, (int32_t*)m->next_ids.p, st));
@@ -902,11 +1087,7 @@ extern "C" int sm_rl_generate_ex(sm_model* m, const int32_t* prompts, int64_t S,
   int32_t* next = (int32_t*)m->next_ids.p;
   int32_t* pos = (int32_t*)m->pos.p;
   int32_t* lens = (int32_t*)m->lens.p;
-  set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, 0);
-  SM_TRY(run_layers(m, prompts, S, P, pos, nullptr, m->kc.p, m->vc.p, layer_elems, cap, false, st));
-  gather_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>((const float*)m->x.p, (int)S,
-                                                                (int)P, (int)P - 1, c.d_model,
-                                                                (float*)m->rows.p);
+  SM_TRY(prefill_prompts(m, prompts, S, P, cap, layer_elems, st));
   SM_TRY(head(m, (const float*)m->rows.p, S, (float*)m->logits.p, st));
   SM_TRY(sample_ex_launch((const float*)m->logits.p, S, c.vocab, c.vocab, sp, seed, 0, seen,
                           seen_ld, done, eos ? lengths : nullptr, eos ? done + S : nullptr, tokens,
@@ -936,6 +1117,93 @@ extern "C" int sm_rl_generate_ex(sm_model* m, const int32_t* prompts, int64_t S,
 
 // ---------------------------------------------------------------- logprobs ---
 
+namespace sm {
+namespace {
+
+// LM head + CE over scored rows [rows, d] (m->rows) in chunks bounding the
+// [rows, V] logits to ~2 GiB: lp of tokens (row-major as the rows).
+int score_rows(sm_model* m, int64_t rows, const int32_t* tokens, float* lp, hipStream_t st) {
+  const auto& c = m->cfg;
+  const int64_t rchunk = std::max<int64_t>(1, ((int64_t)1 << 29) / c.vocab);
+  SM_TRY(ensure(m->logits, (size_t)std::min(rows, rchunk) * c.vocab * 4));
+  for (int64_t r0 = 0; r0 < rows; r0 += rchunk) {
+    const int64_t rn = std::min(rchunk, rows - r0);
+    SM_TRY(head(m, (const float*)m->rows.p + r0 * c.d_model, rn, (float*)m->logits.p, st));
+    SM_TRY(sm_ce_rows(m->logits.p, SM_F32, tokens + r0, rn, c.vocab, c.vocab, lp + r0, nullptr,
+                      nullptr, 1.0f, nullptr, nullptr, st));
+  }
+  return SM_OK;
+}
+
+// The recompute with prompt groups: each group's prompt runs once (its K / V
+// for every layer and its last hidden row kept), then every rollout's
+// continuation tokens[:, :N-1] runs from position P over a cache whose
+// positions 0..P-1 receive the group's prompt K / V before each layer. The
+// scored row of token 0 is the group's last prompt row; those of tokens
+// 1..N-1 come from the continuation. A prompt position depends on the prompt
+// alone, so the values are those of the per-rollout forward.
+int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens, int64_t S,
+                     int64_t P, int64_t N, int64_t budget, int64_t chunk, float* lp_out,
+                     hipStream_t st) {
+  const auto& c = m->cfg;
+  const int64_t G = m->prompt_group, L = P + N - 1;
+  SM_TRY(check_prompt_groups(m, prompts, S, P, st));
+  const int64_t groups = S / G;
+  const size_t pl = (size_t)groups * c.kv_heads * P * c.head_dim;  // elements per layer
+  SM_TRY(ensure(m->pkc, pl * c.layers * m->kv_size));
+  SM_TRY(ensure(m->pvc, pl * c.layers * m->kv_size));
+  SM_TRY(ensure(m->prow, (size_t)groups * c.d_model * 4));
+  SM_TRY(ensure(m->pos, (size_t)std::max(groups, std::min(chunk, S)) * 4));
+  SM_TRY(ensure(m->lens, (size_t)std::max(groups, std::min(chunk, S)) * 4));
+  int32_t* pos = (int32_t*)m->pos.p;
+  int32_t* lens = (int32_t*)m->lens.p;
+  // prompts, once per group, in chunks of whole prompts within the budget
+  const int64_t gchunk = std::max<int64_t>(1, budget / P);
+  for (int64_t g0 = 0; g0 < groups; g0 += gchunk) {
+    const int64_t gc = std::min(gchunk, groups - g0);
+    SM_TRY(ensure(m->ids, (size_t)gc * P * 4));
+    int32_t* ids = (int32_t*)m->ids.p;
+    group_prompts_kernel<<<blocks_for(gc * P), 256, 0, st>>>(prompts + g0 * G * P, gc, (int)G,
+                                                              (int)P, ids);
+    set_positions_kernel<<<blocks_for(gc), 256, 0, st>>>(pos, lens, (int)gc, 0);
+    const size_t off = (size_t)g0 * c.kv_heads * P * c.head_dim * m->kv_size;
+    SM_TRY(run_layers(m, ids, gc, P, pos, nullptr, (char*)m->pkc.p + off, (char*)m->pvc.p + off,
+                      pl, P, false, st));
+    gather_rows_kernel<<<blocks_for(gc * c.d_model), 256, 0, st>>>(
+        (const float*)m->x.p, (int)gc, (int)P, (int)P - 1, c.d_model,
+        (float*)m->prow.p + g0 * c.d_model);
+  }
+  // continuations, in chunks of rollouts
+  const PrefixKV pre0{m->pkc.p, m->pvc.p, (int64_t)(pl * m->kv_size), (int)G, (int)P, 0};
+  for (int64_t s0 = 0; s0 < S; s0 += chunk) {
+    const int64_t cs = std::min(chunk, S - s0);
+    const int64_t rows = cs * N;
+    if (N > 1) {
+      const size_t layer_elems = cache_layer_elems(m, cs, L);
+      SM_TRY(ensure(m->rkc, layer_elems * m->kv_size));
+      SM_TRY(ensure(m->rvc, layer_elems * m->kv_size));
+      SM_TRY(ensure(m->ids, (size_t)cs * (N - 1) * 4));
+      int32_t* ids = (int32_t*)m->ids.p;
+      cont_ids_kernel<<<blocks_for(cs * (N - 1)), 256, 0, st>>>(tokens + s0 * N, cs, (int)N, ids);
+      set_positions_kernel<<<blocks_for(cs), 256, 0, st>>>(pos, lens, (int)cs, (int)P);
+      PrefixKV pre = pre0;
+      pre.s0 = s0;
+      SM_TRY(run_layers(m, ids, cs, N - 1, pos, nullptr, m->rkc.p, m->rvc.p, 0, L, false, st,
+                        &pre));
+    }
+    SM_TRY(ensure(m->rows, (size_t)rows * c.d_model * 4));
+    gather_cont_rows_kernel<<<blocks_for(rows * c.d_model), 256, 0, st>>>(
+        (const float*)m->prow.p, (const float*)m->x.p, cs, s0, (int)G, (int)N, c.d_model,
+        (float*)m->rows.p);
+    SM_TRY(score_rows(m, rows, tokens + s0 * N, lp_out + s0 * N, st));
+  }
+  return SM_OK;
+}
+
+}  // namespace
+}  // namespace sm
+
+
 extern "C" int sm_rl_logprobs(sm_model* m, const int32_t* prompts, const int32_t* tokens,
                               int64_t S, int64_t P, int64_t N, int64_t max_tokens_per_forward,
                               float* lp_out, void* stream) {
@@ -948,6 +1216,8 @@ extern "C" int sm_rl_logprobs(sm_model* m, const int32_t* prompts, const int32_t
   const auto& c = m->cfg;
   const int64_t budget = max_tokens_per_forward > 0 ? max_tokens_per_forward : 65536;
   const int64_t chunk = std::max<int64_t>(1, budget / L);
+  if (m->prompt_group > 1)
+    return logprobs_grouped(m, prompts, tokens, S, P, N, budget, chunk, lp_out, st);
   for (int64_t s0 = 0; s0 < S; s0 += chunk) {
     const int64_t cs = std::min(chunk, S - s0);
     const size_t layer_elems = cache_layer_elems(m, cs, L);

@@ -141,6 +141,13 @@ class Model:
         call("sm_model_trace_routes", self._h, None, None, 0)
         self._trace = None
 
+    def set_prompt_groups(self, group_size: int) -> None:
+        """sm_model_set_prompt_groups: rollouts g*G .. g*G+G-1 of later RL
+        calls share one prompt, computed once per group (1 = off). Set before
+        binding a workspace."""
+        call("sm_model_set_prompt_groups", self._h, int(group_size))
+        self.prompt_group = int(group_size)
+
     def workspace_bytes(self, S: int, P: int, N: int, max_tokens_per_forward: int = 0) -> int:
         """sm_rl_workspace_bytes: device bytes the RL calls need for these shapes."""
         n = int(_lib.lib().sm_rl_workspace_bytes(self._h, S, P, N, int(max_tokens_per_forward)))

@@ -176,3 +176,60 @@ def test_rl_prepare_matches_oracle(dev):
                                atol=1e-7)
     assert abs(res["mean_reward_sum"] - stats[:, 1].sum()) < 1e-5
     assert res["rollouts"] == groups * G
+
+
+@pytest.mark.parametrize("quantized,experts", [(True, 0), (False, 0), (True, 8)])
+def test_prompt_groups_equal_per_rollout(dev, quantized, experts):
+    """Prompt groups (sm_model_set_prompt_groups): generation (plain and with
+    EOS / top-k / repetition penalty), the recompute (one and several chunks)
+    and the GRPO prepare with each group's prompt computed once give the
+    tokens of computing every rollout's prompt and its log-probs up to the
+    order of f32 additions (the prompt GEMMs run at groups x P rows instead of
+    S x P, which can pick another tiling or K split; through the 16-bit K / V
+    cache that stays within 2e-4, 1e-5 for f32 models), P 40 not being a
+    multiple of the attention tiles. A prompt that differs inside a group, or
+    rollouts that are not whole groups, are rejected."""
+    from summa_amd.sampling import SamplingConfig
+    print(f"case prompt groups quantized={quantized} experts={experts}", flush=True)
+    kw = dict(experts=experts, expert_ffn=256) if experts else {}
+    cfg = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
+                      vocab=1024, max_seq=64, quantized=quantized, **kw)
+    plain, grouped = Model(cfg), Model(cfg)
+    for m in (plain, grouped):
+        m.init_random(17, std=0.05)
+    G, groups, P, N = 4, 3, 40, 12
+    grouped.set_prompt_groups(G)
+    gen = torch.Generator().manual_seed(3)
+    base = torch.randint(0, cfg.vocab, (groups, P), generator=gen, dtype=torch.int32)
+    prompts = base.repeat_interleave(G, 0).to(dev)
+    tol = 2e-4 if quantized else 1e-5
+
+    def close(a, b, what):
+        err = float((a - b).abs().max())
+        print(f"  {what}: max |grouped - per rollout| {err:.2e}", flush=True)
+        assert err <= tol, what
+
+    t1, l1 = plain.generate(prompts, N, temperature=1.0, seed=5)
+    t2, l2 = grouped.generate(prompts, N, temperature=1.0, seed=5)
+    assert torch.equal(t1, t2)
+    close(l1, l2, "generate")
+    sc = SamplingConfig(max_new_tokens=N, temperature=0.8, top_k=20, repetition_penalty=1.3,
+                        eos_token=int(t1[0, 3]), seed=9)
+    e1, e2 = plain.generate_ex(prompts, sc), grouped.generate_ex(prompts, sc)
+    assert torch.equal(e1[0], e2[0]) and torch.equal(e1[2], e2[2])
+    close(e1[1], e2[1], "generate_ex")
+    for budget in (0, 100):  # one chunk; one rollout and two prompts per forward
+        r1 = plain.logprobs(prompts, t1, max_tokens_per_forward=budget)
+        r2 = grouped.logprobs(prompts, t1, max_tokens_per_forward=budget)
+        close(r1, r2, f"logprobs (budget {budget})")
+    rewards = torch.rand(groups, G, generator=gen).to(dev)
+    o1 = rl_prepare(plain, plain, prompts, t1, l1, rewards)
+    o2 = rl_prepare(grouped, grouped, prompts, t1, l1, rewards)
+    close(o1["lp_cur"], o2["lp_cur"], "prepare lp_cur")
+    assert torch.equal(o2["lp_cur"], o2["lp_ref"])
+    bad = prompts.clone()
+    bad[5, 7] = (bad[5, 7] + 1) % cfg.vocab
+    with pytest.raises(Exception, match="differs from its group"):
+        grouped.generate(bad, N, temperature=1.0, seed=5)
+    with pytest.raises(Exception, match="whole groups"):
+        grouped.logprobs(prompts[:10], t1[:10])
