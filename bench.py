@@ -85,28 +85,36 @@ def q4_bytes(n: int, k: int) -> int:
 
 
 def recompute_flops(wl) -> float:
-    """Algorithmic flops of one model's log-prob recompute over S x (P + N - 1)
-    positions: 2 * tokens * per-layer linear params, the LM head over the S * N
-    scored rows, causal attention (Q.K^T and P.V over the lower triangle)."""
+    """Algorithmic flops of one model's log-prob recompute of S = prompts x
+    group rollouts of P + N - 1 positions, where a group's rollouts share one
+    prompt (GRPO), so its P prompt positions are computed once per group:
+    2 * tokens * per-layer linear params over prompts * P + S * (N - 1) token
+    rows, the LM head over the S * N scored rows, causal attention (Q.K^T and
+    P.V over the lower triangle: the prompt's triangle once per group, the
+    completion rows' keys per rollout)."""
     m = wl.model
-    L = wl.prompt_len + wl.new_tokens - 1
-    tokens = wl.rollouts * L
+    P, N, S = wl.prompt_len, wl.new_tokens, wl.rollouts
+    L = P + N - 1
+    tokens = wl.prompts * P + S * (N - 1)
     lin = sum(n * k for n, k in linear_shapes(m)) * m["layers"]
     head = m["vocab"] * m["d_model"]
-    attn = 4 * m["head_dim"] * (L * (L + 1) / 2) * m["heads"] * wl.rollouts * m["layers"]
-    return 2.0 * tokens * lin + 2.0 * wl.rollouts * wl.new_tokens * head + attn
+    keys = wl.prompts * P * (P + 1) / 2 + S * (L * (L + 1) / 2 - P * (P + 1) / 2)
+    attn = 4 * m["head_dim"] * keys * m["heads"] * m["layers"]
+    return 2.0 * tokens * lin + 2.0 * S * N * head + attn
 
 
-def decode_bytes(wl) -> float:
+def decode_bytes(wl, shared_prompt: bool = True) -> float:
     """Algorithmic HBM bytes of the N - 1 cached decode steps: every packed
-    weight once per step plus each sequence's K/V cache (f16) read once per
-    KV head per layer at its context length P + t."""
+    weight once per step plus the K/V cache (f16) each step's attention needs,
+    once per KV head per layer: a group's shared prompt keys once per group
+    (shared_prompt) or once per rollout, and each rollout's t generated keys."""
     m = wl.model
     S, P, N = wl.rollouts, wl.prompt_len, wl.new_tokens
     w = sum(q4_bytes(n, k) for n, k in linear_shapes(m)) * m["layers"]
     w += q4_bytes(m["vocab"], m["d_model"])
-    kv_tok = m["layers"] * S * m["kv_heads"] * m["head_dim"] * 2 * 2
-    ctx = sum(P + t for t in range(1, N))
+    kv_tok = m["layers"] * m["kv_heads"] * m["head_dim"] * 2 * 2
+    seqs_p = wl.prompts if shared_prompt else S
+    ctx = sum(seqs_p * P + S * t for t in range(1, N))
     return (N - 1) * w + kv_tok * ctx
 
 
@@ -114,16 +122,18 @@ def decode_bytes(wl) -> float:
 
 def recompute_gemm(wl, dev, reps: int = 10) -> dict:
     """The dominant kernel of the config[2] step: the FFN-in projection of the
-    log-prob recompute (SwiGLU f16-pair epilogue) at its chunk shape
-    M = 64 rollouts x 1023 positions, N = 2F = 11264, K = 2048, on the
-    wide-tile kernel. flops = 2 M N K per launch."""
+    log-prob recompute (SwiGLU f16-pair epilogue) at the shape of its
+    continuation chunks (prompt groups: a chunk is 65536 // (P + N - 1) = 64
+    rollouts of N - 1 = 511 continuation rows over the group's prompt K / V),
+    M = 32704, N = 2F = 11264, K = 2048, on the wide-tile kernel.
+    flops = 2 M N K per launch."""
     import torch
 
     from summa_amd import _lib, ops
 
     m = wl.model
     L = wl.prompt_len + wl.new_tokens - 1
-    M = max(1, 65536 // L) * L
+    M = max(1, 65536 // L) * (wl.new_tokens - 1)
     N, K = 2 * m["ffn"], m["d_model"]
     w = torch.empty(N, K, device=dev)
     ops.fill_normal(w, 0.0, 0.02, seed=5)
@@ -289,8 +299,10 @@ def ce_stress(dev, rows: int, reps: int = 5) -> dict:
 def rl_inputs(wl, mc, dev):
     import torch
     gen = torch.Generator().manual_seed(0)
-    prompts = torch.randint(0, mc.vocab, (wl.rollouts, wl.prompt_len), generator=gen,
-                            dtype=torch.int32).to(dev)
+    # GRPO: `prompts` prompts, each rolled out `group` times (rows g*group ..
+    # g*group + group - 1 carry prompt g)
+    prompts = torch.randint(0, mc.vocab, (wl.prompts, wl.prompt_len), generator=gen,
+                            dtype=torch.int32).repeat_interleave(wl.group, 0).to(dev)
     rewards = wl.sample_rewards(gen).to(dev)
     return prompts, rewards
 
@@ -348,6 +360,8 @@ def config0_leg(dev, steps: int = 5) -> dict:
     wl = RL_WORKLOADS[0]
     mc = wl.model_config()
     policy, reference = Model(mc), Model(mc)
+    for m in (policy, reference):  # each group's prompt computed once
+        m.set_prompt_groups(wl.group)
     w = draw_weights(wl, [policy, reference], dev, seed=1)
     prompts, rewards = rl_inputs(wl, mc, dev)
     roll, full, _, out = run_rl_step(wl, policy, reference, prompts, rewards, steps, 2)
@@ -512,6 +526,7 @@ def bench_rl_step(args) -> dict:
     policy, reference = Model(mc), Model(mc)
     dweights = draw_weights(wl, [policy, reference], dev)  # the frozen copy equals the policy
     for m in (policy, reference):  # hot calls carve their buffers from a bound workspace
+        m.set_prompt_groups(wl.group)  # each group's prompt computed once
         m.bind_workspace(wl.rollouts, wl.prompt_len, wl.new_tokens)
     prompts, rewards = rl_inputs(wl, mc, dev)
     S, N = wl.rollouts, wl.new_tokens
@@ -669,7 +684,8 @@ def bench_policy_update(args) -> dict:
     ref = Model(mc)
     pol.install(ref)
     G, P, N = wl.group, wl.prompt_len, wl.new_tokens
-    prompts = torch.randint(0, V, (G, P), dtype=torch.int32, device=dev)
+    # one GRPO group: G rollouts of one prompt
+    prompts = torch.randint(0, V, (1, P), dtype=torch.int32, device=dev).repeat(G, 1)
     tok, beh = ref.generate(prompts, N, temperature=wl.temperature, seed=1)
     rewards = torch.rand(1, G, device=dev)
     st = torch.cuda.current_stream()
