@@ -264,6 +264,24 @@ int sm_attn_decode(const void* q, const void* kcache, const void* vcache, const 
 int sm_attn_prefill(const void* q, const void* kcache, const void* vcache, const int32_t* pos0,
                     void* out, int dtype, int out_dtype, int64_t S, int64_t L, int64_t H,
                     int64_t KVH, int64_t cap, int64_t head_dim, void* stream);
+/* Decode attention for rollouts in groups of G that share a prompt of P
+ * tokens (GrpoGenerationBatchRequest: one example per group,
+ * posttrain.rs:1206-1216; per rollout the semantics of sm_attn_decode, i.e.
+ * forward_cached, attention.rs:216-265): rollout s attends keys 0..P-1 from
+ * prefix_k / prefix_v [S/G, KVH, P, hd] (its group's prompt, stored once) and
+ * keys P..lens[s]-1 from kcache / vcache [S, KVH, cap, hd] (its own
+ * continuation); every lens[s] must be >= P. The prompt keys are read once per
+ * (group, KV head) for all G * H/KVH query heads of the group. dtype SM_F16 or
+ * SM_BF16, out_dtype SM_F16X2; G * H / KVH <= 32. workspace: at least
+ * sm_attn_decode_prefix_workspace_bytes(S, G, P, H, KVH, head_dim) bytes,
+ * 16-byte aligned (per-(query head, key split) partials; no allocation). */
+int64_t sm_attn_decode_prefix_workspace_bytes(int64_t S, int64_t G, int64_t P, int64_t H,
+                                              int64_t KVH, int64_t head_dim);
+int sm_attn_decode_prefix(const void* q, const void* prefix_k, const void* prefix_v,
+                          const void* kcache, const void* vcache, const int32_t* lens, void* out,
+                          void* workspace, int64_t workspace_bytes, int dtype, int out_dtype,
+                          int64_t S, int64_t G, int64_t P, int64_t H, int64_t KVH, int64_t cap,
+                          int64_t head_dim, void* stream);
 /* Same, also writing the per-row log-sum-exp of the scaled, masked scores
  * (natural log) to lse [S*H, L] f32 (nullable): the convention of the flash
  * forward and attention_log_sum_exp (fused_attention.rs:166-172), which the

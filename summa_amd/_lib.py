@@ -51,6 +51,9 @@ SIGNATURES: dict[str, tuple] = {
     "sm_rmsnorm": (i32, [vp, vp, i64, i64, f32, vp, i32, vp]),
     "sm_rope_append": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i64, vp, i32, vp, vp, i32, vp]),
     "sm_attn_decode": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, vp]),
+    "sm_attn_decode_prefix_workspace_bytes": (i64, [i64, i64, i64, i64, i64, i64]),
+    "sm_attn_decode_prefix": (i32, [vp, vp, vp, vp, vp, vp, vp, vp, i64, i32, i32, i64, i64, i64,
+                                    i64, i64, i64, i64, vp]),
     "sm_attn_prefill": (i32, [vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_attn_prefill_lse": (i32, [vp, vp, vp, vp, vp, vp, i32, i32, i64, i64, i64, i64, i64, i64, vp]),
     "sm_attention": (i32, [vp, vp, vp, i32, i64, i64, i64, i64, i64, i32, vp, vp, vp]),

@@ -30,6 +30,7 @@
 // Prefill / recompute (many queries, causal) uses the flash-attention kernel
 // in prefill_attention.hip; fp32 models (config[0]) use the simple VALU
 // kernel below for both.
+#include <algorithm>
 #include <cmath>
 #include <type_traits>
 
@@ -43,11 +44,17 @@ constexpr int kMaxQpk = 16;  // query heads per KV head handled by one WG
 
 // QM: query heads per KV head the kernel is built for (>= H / KVH); EX: exactly
 // QM, so the per-head bounds are compile-time; DPL: V dims per lane in P.V.
-template <int HD, int QM, bool KF16, int OM, bool EX, int DPL>
+// PRE: keys 0..k0-1 were done by attn_prefix_kernel (a prompt shared by a
+// group of rollouts); this kernel takes keys k0..len-1 from the sequence's
+// cache and folds the prefix's nsplit partials (max, sum, unnormalised O per
+// query head) into its final merge.
+template <int HD, int QM, bool KF16, int OM, bool EX, int DPL, bool PRE = false>
 __global__ __launch_bounds__(256) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ lens,
-    void* __restrict__ out, int H, int KVH, int cap, float scale) {
+    void* __restrict__ out, int H, int KVH, int cap, float scale, int k0 = 0,
+    const float* __restrict__ pre_o = nullptr, const float* __restrict__ pre_ml = nullptr,
+    int nsplit = 0) {
   typedef typename Op8<KF16>::T op8;
   static_assert(DPL == 4 || DPL == 8, "DPL is 4 or 8");
   constexpr int LPK = HD / DPL;    // lanes per V row in the P.V pass (DPL dims each)
@@ -166,9 +173,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     __builtin_amdgcn_wave_barrier();
   };
 
-  // Wave w takes tiles w, w + 4, ...
+  // Wave w takes tiles w, w + 4, ... (of keys k0.. with a shared prefix)
   constexpr int STRIDE = 4 * TK;
-  for (int t0 = wave * TK; t0 < len; t0 += STRIDE) {
+  for (int t0 = (PRE ? k0 : 0) + wave * TK; t0 < len; t0 += STRIDE) {
     Tile ta;
     load(t0, ta);
     compute(t0, ta);
@@ -198,6 +205,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 4; ++w) m = fmaxf(m, mrg_m[w][i]);
+    const size_t slot = ((size_t)s * H + kvh * qpk + i) * nsplit;
+    if constexpr (PRE)
+      for (int p = 0; p < nsplit; ++p) m = fmaxf(m, pre_ml[(slot + p) * 2]);
     float l = 0.f, o = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -206,7 +216,179 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
       l += mrg_l[w][i] * c;
       o += mrg_o[w][i][d] * c;
     }
+    if constexpr (PRE)
+      for (int p = 0; p < nsplit; ++p) {
+        const float pm = pre_ml[(slot + p) * 2];
+        if (pm == -INFINITY) continue;
+        const float c = __expf(pm - m);
+        l += pre_ml[(slot + p) * 2 + 1] * c;
+        o += pre_o[(slot + p) * HD + d] * c;
+      }
     store_out<OM>(out, (size_t)s, H * HD, (kvh * qpk + i) * HD + d, o / l);
+  }
+}
+
+// Decode attention over a prompt shared by a group of G rollouts (prompt
+// groups): the prompt's K / V ([groups, KVH, P, hd], written once per group by
+// the prefill) is read once per (group, KV head) for all G x qpk query heads
+// of the group's rollouts at this decode step, instead of once per rollout.
+// One workgroup per (KV head, group, key split); its four waves take 32-key
+// tiles in turn. Per 16-key block:
+//   scores S^T = K . Q^T: v_mfma_f32_16x16x32_{f16,bf16}, A = 16 key rows (read
+//   straight from HBM, 16 bytes per lane), B = 16 queries (registers, loaded
+//   once); lane (g, j) gets keys 4g..4g+3 of the block for query j;
+//   online softmax per query = per lane column (max / sum over the block by
+//   two cross-row shuffles), so the rescale of O is lane-local;
+//   O^T += V^T . P^T: v_mfma_f32_16x16x4_f32 with P in f32 (the decode kernel's
+//   f32 probabilities), one MFMA per (key 4g + r, dim block db). A-row i of dim
+//   block db is dim i * (hd / 16) + db, so lane (g, j) loads dims
+//   j*hd/16 .. +hd/16 of its key row as one 16-byte (hd 128) or 8-byte load,
+//   and ends holding dims 4g*hd/16 .. +4*hd/16 of query j.
+// The four waves merge in LDS; each (query head, split) writes its partial
+// (max, sum, unnormalised O) for attn_decode_kernel<..., PRE>, which adds the
+// rollout's own keys P..len-1 and normalises. QB: 16-query blocks (G * qpk <=
+// 16 * QB).
+template <int HD, bool KF16, int QB>
+__global__ __launch_bounds__(256) void attn_prefix_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ pk,
+    const uint16_t* __restrict__ pv, float* __restrict__ part_o, float* __restrict__ part_ml,
+    int H, int KVH, int G, int P, int per, float scale) {
+  typedef typename Op8<KF16>::T op8;
+  constexpr int STEPS = HD / 32;  // score MFMA k-steps over head_dim
+  constexpr int DB = HD / 16;     // dim blocks of the P.V MFMA = V dims per lane
+  typedef typename std::conditional<DB == 8, u32x4, u32x2>::type vrow;
+  constexpr int TK = 32;          // keys per tile: two 16-key blocks
+  const int kvh = blockIdx.x, grp = blockIdx.y, sp = blockIdx.z, splits = gridDim.z;
+  const int qpk = H / KVH, nq = G * qpk;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  const int k_lo = sp * per, k_hi = min(P, k_lo + per);
+  const size_t base = ((size_t)grp * KVH + kvh) * P * HD;
+  __shared__ float mrg_m[4][QB * 16], mrg_l[4][QB * 16];
+  __shared__ float mrg_o[4][QB * 16][HD + 1];
+
+  // B operand of the scores: query column j of block qb is query qb*16 + j =
+  // (rollout grp*G + qi / qpk, head kvh*qpk + qi % qpk); zero past nq.
+  op8 qf[QB][STEPS];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = qb * 16 + j;
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) qf[qb][st] = op8{};
+    if (qi < nq) {
+      const int s = grp * G + qi / qpk, h = kvh * qpk + qi % qpk;
+      const uint16_t* qp = q + ((size_t)s * H + h) * HD + g * 8;
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) qf[qb][st] = *reinterpret_cast<const op8*>(qp + st * 32);
+    }
+  }
+  float m_i[QB], l_i[QB];
+  f4 o[QB][DB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_i[qb] = -INFINITY;
+    l_i[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[qb][db] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const int last = k_hi - 1;  // loads past the split's end re-read its last key (masked)
+  for (int t0 = k_lo + wave * TK; t0 < k_hi; t0 += 4 * TK) {
+    op8 kf[2][STEPS];
+    vrow vr[2][4];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const uint16_t* kp = pk + base + (size_t)min(t0 + kb * 16 + j, last) * HD + g * 8;
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) kf[kb][st] = *reinterpret_cast<const op8*>(kp + st * 32);
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        vr[kb][r] = *reinterpret_cast<const vrow*>(
+            pv + base + (size_t)min(t0 + kb * 16 + 4 * g + r, last) * HD + j * DB);
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      f4 sc[2];
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        sc[kb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) sc[kb] = Op8<KF16>::mfma(kf[kb][st], qf[qb][st], sc[kb]);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = (t0 + kb * 16 + 4 * g + r < k_hi) ? sc[kb][r] * scale : -INFINITY;
+          sc[kb][r] = v;
+          mx = fmaxf(mx, v);
+        }
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mnew = fmaxf(m_i[qb], mx);  // finite: key t0 is in range
+      const float alpha = (m_i[qb] == -INFINITY) ? 0.f : __expf(m_i[qb] - mnew);
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = (sc[kb][r] == -INFINITY) ? 0.f : __expf(sc[kb][r] - mnew);
+          sc[kb][r] = p;
+          ps += p;
+        }
+      ps += __shfl_xor(ps, 16, kWave);
+      ps += __shfl_xor(ps, 32, kWave);
+      l_i[qb] = l_i[qb] * alpha + ps;
+      m_i[qb] = mnew;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) o[qb][db] *= alpha;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          float v[DB];
+          if constexpr (DB == 8) unpack8<KF16>(vr[kb][r], v);
+          else unpack4<KF16>(vr[kb][r], v);
+#pragma unroll
+          for (int db = 0; db < DB; ++db)
+            o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x4f32(v[db], sc[kb][r], o[qb][db], 0, 0, 0);
+        }
+    }
+  }
+  // lane (g, j) holds dims (4g + r) * DB + db of query qb*16 + j
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) mrg_o[wave][qb * 16 + j][(4 * g + r) * DB + db] = o[qb][db][r];
+    if (g == 0) {
+      mrg_m[wave][qb * 16 + j] = m_i[qb];
+      mrg_l[wave][qb * 16 + j] = l_i[qb];
+    }
+  }
+  __syncthreads();
+  for (int e = threadIdx.x; e < nq * HD; e += 256) {
+    const int qi = e / HD, d = e % HD;
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) m = fmaxf(m, mrg_m[w][qi]);
+    float l = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (mrg_m[w][qi] == -INFINITY) continue;
+      const float c = __expf(mrg_m[w][qi] - m);
+      l += mrg_l[w][qi] * c;
+      acc += mrg_o[w][qi][d] * c;
+    }
+    const int s = grp * G + qi / qpk, h = kvh * qpk + qi % qpk;
+    const size_t slot = ((size_t)s * H + h) * splits + sp;
+    part_o[slot * HD + d] = acc;
+    if (d == 0) {
+      part_ml[slot * 2] = m;
+      part_ml[slot * 2 + 1] = l;
+    }
   }
 }
 
@@ -548,6 +730,103 @@ extern "C" int sm_attn_decode(const void* q, const void* kcache, const void* vca
 #undef SM_DEC
 #undef SM_DEC_X
 #undef SM_DEC_K
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+namespace sm {
+namespace {
+
+// Key splits of a shared prompt per (group, KV head): enough workgroups to
+// cover the CUs (>= 256) while each split keeps >= 256 keys (two 32-key tiles
+// per wave) and its partials stay small next to the keys it reads.
+int prefix_splits(int64_t groups, int64_t KVH, int64_t P) {
+  const int64_t pairs = groups * KVH;
+  int64_t sp = std::max<int64_t>(1, std::min<int64_t>((256 + pairs - 1) / pairs, P / 256));
+  const int64_t per = (P + sp - 1) / sp;
+  const int64_t per32 = (per + 31) / 32 * 32;
+  return (int)((P + per32 - 1) / per32);  // no empty split
+}
+
+}  // namespace
+}  // namespace sm
+
+extern "C" int64_t sm_attn_decode_prefix_workspace_bytes(int64_t S, int64_t G, int64_t P,
+                                                         int64_t H, int64_t KVH,
+                                                         int64_t head_dim) {
+  if (S <= 0 || G <= 0 || S % G || P <= 0 || H <= 0 || KVH <= 0 || H % KVH || head_dim <= 0)
+    return -1;
+  const int64_t sp = sm::prefix_splits(S / G, KVH, P);
+  return S * H * sp * (head_dim + 2) * 4;
+}
+
+extern "C" int sm_attn_decode_prefix(const void* q, const void* prefix_k, const void* prefix_v,
+                                     const void* kcache, const void* vcache, const int32_t* lens,
+                                     void* out, void* workspace, int64_t workspace_bytes,
+                                     int dtype, int out_dtype, int64_t S, int64_t G, int64_t P,
+                                     int64_t H, int64_t KVH, int64_t cap, int64_t head_dim,
+                                     void* stream) {
+  using namespace sm;
+  SM_REQUIRE(q && prefix_k && prefix_v && kcache && vcache && lens && out && workspace,
+             "sm_attn_decode_prefix: null buffer");
+  SM_REQUIRE(S > 0 && S <= 65535 && G > 0 && S % G == 0,
+             "sm_attn_decode_prefix: need 0 < S <= 65535 rollouts in whole groups of G");
+  SM_REQUIRE(H > 0 && KVH > 0 && H % KVH == 0, "sm_attn_decode_prefix: H must be a multiple of KVH");
+  const int64_t qpk = H / KVH;
+  SM_REQUIRE(qpk <= kMaxQpk && G * qpk <= 32,
+             "sm_attn_decode_prefix: at most %d query heads per KV head and 32 per group",
+             kMaxQpk);
+  SM_REQUIRE(P > 0 && P <= cap && cap <= (1 << 24), "sm_attn_decode_prefix: need 0 < P <= cap");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128,
+             "sm_attn_decode_prefix: head_dim must be 64 or 128");
+  SM_REQUIRE(dtype == SM_F16 || dtype == SM_BF16,
+             "sm_attn_decode_prefix: dtype must be SM_F16 or SM_BF16");
+  SM_REQUIRE(out_dtype == SM_F16X2, "sm_attn_decode_prefix: writes f16 pairs (SM_F16X2)");
+  const int64_t need = sm_attn_decode_prefix_workspace_bytes(S, G, P, H, KVH, head_dim);
+  SM_REQUIRE(workspace_bytes >= need, "sm_attn_decode_prefix: workspace of %lld bytes, %lld needed",
+             (long long)workspace_bytes, (long long)need);
+  SM_REQUIRE(reinterpret_cast<uintptr_t>(workspace) % 16 == 0,
+             "sm_attn_decode_prefix: workspace must be 16-byte aligned");
+  const int splits = prefix_splits(S / G, KVH, P);
+  const int per = (int)(((P + splits - 1) / splits + 31) / 32 * 32);
+  const float scale = 1.0f / sqrtf((float)head_dim);
+  hipStream_t st = as_stream(stream);
+  float* part_o = (float*)workspace;
+  float* part_ml = part_o + (size_t)S * H * splits * head_dim;
+  const uint16_t *qq = (const uint16_t*)q, *pk = (const uint16_t*)prefix_k,
+                 *pv = (const uint16_t*)prefix_v, *kk = (const uint16_t*)kcache,
+                 *vv = (const uint16_t*)vcache;
+  const dim3 ga((unsigned)KVH, (unsigned)(S / G), (unsigned)splits);
+  const bool f16 = dtype == SM_F16;
+  const bool two = G * qpk > 16;
+#define SM_PRE_A(HD, KF, QB)                                                              \
+  attn_prefix_kernel<HD, KF, QB><<<ga, 256, 0, st>>>(qq, pk, pv, part_o, part_ml, (int)H, \
+                                                      (int)KVH, (int)G, (int)P, per, scale)
+#define SM_PRE_AK(HD, KF) \
+  do { if (two) SM_PRE_A(HD, KF, 2); else SM_PRE_A(HD, KF, 1); } while (0)
+  if (head_dim == 64) {
+    if (f16) SM_PRE_AK(64, true); else SM_PRE_AK(64, false);
+  } else {
+    if (f16) SM_PRE_AK(128, true); else SM_PRE_AK(128, false);
+  }
+#undef SM_PRE_AK
+#undef SM_PRE_A
+  const dim3 gb((unsigned)KVH, (unsigned)S);
+#define SM_PRE_B(HD, QM, KF, EX)                                                              \
+  attn_decode_kernel<HD, QM, KF, 2, EX, (QM >= 4 ? 4 : 8), true><<<gb, 256, 0, st>>>(        \
+      qq, kk, vv, lens, out, (int)H, (int)KVH, (int)cap, scale, (int)P, part_o, part_ml, splits)
+#define SM_PRE_BX(HD, QM, EX) \
+  do { if (f16) SM_PRE_B(HD, QM, true, EX); else SM_PRE_B(HD, QM, false, EX); } while (0)
+#define SM_PRE_BQ(HD, QM) \
+  do { if (qpk == QM) SM_PRE_BX(HD, QM, true); else SM_PRE_BX(HD, QM, false); } while (0)
+  if (head_dim == 64) {
+    if (qpk == 1) SM_PRE_BQ(64, 1); else if (qpk <= 4) SM_PRE_BQ(64, 4); else SM_PRE_BQ(64, 16);
+  } else {
+    if (qpk == 1) SM_PRE_BQ(128, 1); else if (qpk <= 4) SM_PRE_BQ(128, 4); else SM_PRE_BQ(128, 16);
+  }
+#undef SM_PRE_BQ
+#undef SM_PRE_BX
+#undef SM_PRE_B
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

@@ -48,6 +48,11 @@ int sm_attn_decode(const void*, const void*, const void*, const int32_t*, void*,
                    int64_t, int64_t, int64_t, int64_t, int64_t, void*);
 int sm_attn_prefill(const void*, const void*, const void*, const int32_t*, void*, int, int,
                     int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void*);
+int64_t sm_attn_decode_prefix_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t,
+                                              int64_t);
+int sm_attn_decode_prefix(const void*, const void*, const void*, const void*, const void*,
+                          const int32_t*, void*, void*, int64_t, int, int, int64_t, int64_t,
+                          int64_t, int64_t, int64_t, int64_t, int64_t, void*);
 int sm_sample(const float*, int64_t, int64_t, int64_t, float, uint64_t, int64_t, int32_t*, int64_t,
               float*, int64_t, int32_t*, void*);
 int sm_ce_rows(const void*, int, const int32_t*, int64_t, int64_t, int64_t, float*, float*, void*,
@@ -268,6 +273,8 @@ struct sm_model {
   // every layer [layers][groups][KVH][P][hd] and last hidden rows [groups, d]
   int64_t prompt_group = 1;
   sm::DevBuf pkc, pvc, prow;
+  // partials of the shared-prompt decode attention (sm_attn_decode_prefix)
+  sm::DevBuf apart;
   int64_t gen_cap = 0, gen_S = 0;
   // caller-bound workspace (sm_model_bind_workspace): the buffers above are
   // fixed slices of it
@@ -381,7 +388,9 @@ size_t cache_layer_elems(const sm_model* m, int64_t S, int64_t cap) {
 
 // The K / V of prompt positions 0..P-1 computed once per group of G rollouts
 // (src [layers][groups][KVH][P][hd], layer stride `layer_bytes`), for
-// run_layers over rollouts s0, s0 + 1, ... of a continuation.
+// run_layers over rollouts s0, s0 + 1, ... of a continuation (copied into
+// cache positions 0..P-1 before each layer), or, at decode, read in place by
+// the shared-prompt attention (sm_attn_decode_prefix).
 struct PrefixKV {
   const void* k;
   const void* v;
@@ -389,6 +398,16 @@ struct PrefixKV {
   int G, P;
   int64_t s0;
 };
+
+// Whether decode attention reads a group's prompt K / V in place
+// (sm_attn_decode_prefix) instead of per-rollout copies: 16-bit caches with
+// f16-pair attention output (the quantized models), at most 32 query heads per
+// (group, KV head).
+bool prefix_attention(const sm_model* m, int64_t S) {
+  const auto& c = m->cfg;
+  const int64_t G = m->prompt_group;
+  return G > 1 && S % G == 0 && c.quantized && G * (c.heads / c.kv_heads) <= 32;
+}
 
 // All decoder layers over S sequences x L tokens (ids [S*L]) at positions
 // pos0[s] + i. K/V go to caches (per-layer stride `layer_elems`, 0 = one
@@ -413,7 +432,7 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
     const Layer& Ly = m->layers[l];
     char* kl = (char*)kc + (size_t)l * layer_elems * m->kv_size;
     char* vl = (char*)vc + (size_t)l * layer_elems * m->kv_size;
-    if (pre) {
+    if (pre && !decode) {
       const int rb = c.head_dim * (int)m->kv_size;
       const int64_t n = S * c.kv_heads * pre->P * (rb / 16);
       for (int kv = 0; kv < 2; ++kv)
@@ -431,7 +450,13 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
       SM_TRY(sm_rope_append((const float*)m->qkv.p, m->rope, pos0, S, L, c.heads, c.kv_heads,
                             c.head_dim, cap, m->qb.p, m->kvt, kl, vl, m->kvt, st));
     }
-    if (decode)
+    if (decode && pre)  // the group's prompt keys from the shared prefix, the rest per rollout
+      SM_TRY(sm_attn_decode_prefix(
+          m->qb.p, (const char*)pre->k + l * pre->layer_bytes,
+          (const char*)pre->v + l * pre->layer_bytes, kl, vl, lens, m->attn.p, m->apart.p,
+          (int64_t)m->apart.n, m->kvt, m->act, S, pre->G, pre->P, c.heads, c.kv_heads, cap,
+          c.head_dim, st));
+    else if (decode)
       SM_TRY(sm_attn_decode(m->qb.p, kl, vl, lens, m->attn.p, m->kvt, m->act, S, c.heads,
                             c.kv_heads, cap, c.head_dim, st));
     else
@@ -506,13 +531,28 @@ int prefill_prompts(sm_model* m, const int32_t* prompts, int64_t S, int64_t P, i
   SM_TRY(run_layers(m, ids, groups, P, pos, nullptr, m->pkc.p, m->pvc.p, pl, P, false, st));
   const int rb = c.head_dim * (int)m->kv_size;
   const int64_t n = (int64_t)c.layers * S * c.kv_heads * P * (rb / 16);
-  for (int kv = 0; kv < 2; ++kv)
+  // the shared-prompt decode attention reads the group's prompt K / V in place
+  for (int kv = 0; kv < (prefix_attention(m, S) ? 0 : 2); ++kv)
     broadcast_prefix_kernel<<<(unsigned)ceil_div(n, 256), 256, 0, st>>>(
         (const char*)(kv ? m->pvc.p : m->pkc.p), (char*)(kv ? m->vc.p : m->kc.p), c.layers, S, 0,
         0, (int)G, c.kv_heads, (int)P, (int)cap, rb, (int64_t)(pl * m->kv_size),
         (int64_t)(layer_elems * m->kv_size));
   gather_group_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>(
       (const float*)m->x.p, S, (int)G, (int)P, (int)P - 1, c.d_model, (float*)m->rows.p);
+  return SM_OK;
+}
+
+// After prefill_prompts: the group prompts' K / V that the decode steps'
+// attention reads in place (out.k == nullptr when it reads per-rollout caches).
+int decode_prefix(sm_model* m, int64_t S, int64_t P, PrefixKV& out) {
+  out = PrefixKV{};
+  if (!prefix_attention(m, S)) return SM_OK;
+  const auto& c = m->cfg;
+  const int64_t G = m->prompt_group;
+  SM_TRY(ensure(m->apart, (size_t)sm_attn_decode_prefix_workspace_bytes(
+                              S, G, P, c.heads, c.kv_heads, c.head_dim)));
+  const int64_t layer_bytes = (S / G) * c.kv_heads * P * c.head_dim * (int64_t)m->kv_size;
+  out = PrefixKV{m->pkc.p, m->pvc.p, layer_bytes, (int)G, (int)P, 0};
   return SM_OK;
 }
 
@@ -531,12 +571,12 @@ extern "C" int sm_model_create(const sm_model_config* cfg, sm_model** out) {
   SM_REQUIRE(c.head_dim == 64 || c.head_dim == 128, "sm_model_create: head_dim must be 64 or 128");
   if (c.quantized)
     SM_REQUIRE(c.d_model % 128 == 0 && c.ffn % 128 == 0 && (c.heads * c.head_dim) % 128 == 0,
-               "sm_model_create: quantized models need d_model, ffn and heads*head_dim % 128 == 0");
+               "sm_model_create: quantized models need d_model, ffn and heads*head_dim %% 128 == 0");
   SM_REQUIRE(c.experts >= 0 && c.experts <= 64, "sm_model_create: experts must be in 0..=64");
   if (c.experts > 0) {
     SM_REQUIRE(c.quantized, "sm_model_create: MoE layers are built for quantized models");
     SM_REQUIRE(c.experts >= 2 && c.expert_ffn > 0 && c.expert_ffn % 128 == 0,
-               "sm_model_create: MoE needs >= 2 experts and expert_ffn % 128 == 0");
+               "sm_model_create: MoE needs >= 2 experts and expert_ffn %% 128 == 0");
   }
   sm_model* m = new sm_model();
   m->cfg = c;
@@ -599,7 +639,7 @@ std::vector<DevBuf*> model_bufs(sm_model* m) {
   return {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits, &m->rows,
           &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc, &m->rkc, &m->rvc,
           &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w, &m->moe_plan, &m->moe_u, &m->moe_y,
-          &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow};
+          &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow, &m->apart};
 }
 
 void release_bufs(sm_model* m) {
@@ -704,6 +744,9 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
     plan_max(at(m->pkc), prefix);
     plan_max(at(m->pvc), prefix);
     plan_max(at(m->prow), (size_t)groups * d * 4);
+    if (prefix_attention(m, S))
+      plan_max(at(m->apart), (size_t)sm_attn_decode_prefix_workspace_bytes(
+                                 S, G, P, c.heads, c.kv_heads, c.head_dim));
     const int64_t gchunk = std::max<int64_t>(1, budget / P);
     const int64_t prow_rows = std::min(groups, gchunk) * P;
     layers(prow_rows);
@@ -1013,6 +1056,8 @@ extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, in
   int32_t* lens = (int32_t*)m->lens.p;
   // prefill over the prompts at positions 0..P-1
   SM_TRY(prefill_prompts(m, prompts, S, P, cap, layer_elems, st));
+  PrefixKV dpre{};
+  SM_TRY(decode_prefix(m, S, P, dpre));
   SM_TRY(head(m, (const float*)m->rows.p, S, (float*)m->logits.p, st));
   SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, 0, tokens, N,
                    behavior_lp, N, (int32_t*)m->next_ids.p, st));
@@ -1020,7 +1065,7 @@ extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, in
   for (int64_t t = 1; t < N; ++t) {
     set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, (int)(P + t - 1));
     SM_TRY(run_layers(m, (const int32_t*)m->next_ids.p, S, 1, pos, lens, m->kc.p, m->vc.p,
-                      layer_elems, cap, true, st));
+                      layer_elems, cap, true, st, dpre.k ? &dpre : nullptr));
     SM_TRY(head(m, (const float*)m->x.p, S, (float*)m->logits.p, st));
     SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, t,
                      tokens + t, N, behavior_lp ? behavior_lp + t : nullptr, N,
@@ -1088,6 +1133,8 @@ extern "C" int sm_rl_generate_ex(sm_model* m, const int32_t* prompts, int64_t S,
   int32_t* pos = (int32_t*)m->pos.p;
   int32_t* lens = (int32_t*)m->lens.p;
   SM_TRY(prefill_prompts(m, prompts, S, P, cap, layer_elems, st));
+  PrefixKV dpre{};
+  SM_TRY(decode_prefix(m, S, P, dpre));
   SM_TRY(head(m, (const float*)m->rows.p, S, (float*)m->logits.p, st));
   SM_TRY(sample_ex_launch((const float*)m->logits.p, S, c.vocab, c.vocab, sp, seed, 0, seen,
                           seen_ld, done, eos ? lengths : nullptr, eos ? done + S : nullptr, tokens,
@@ -1105,7 +1152,8 @@ extern "C" int sm_rl_generate_ex(sm_model* m, const int32_t* prompts, int64_t S,
       }
     }
     set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, (int)(P + t - 1));
-    SM_TRY(run_layers(m, next, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true, st));
+    SM_TRY(run_layers(m, next, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true, st,
+                      dpre.k ? &dpre : nullptr));
     SM_TRY(head(m, (const float*)m->x.p, S, (float*)m->logits.p, st));
     SM_TRY(sample_ex_launch((const float*)m->logits.p, S, c.vocab, c.vocab, sp, seed, t, seen,
                             seen_ld, done, eos ? lengths : nullptr, eos ? done + S : nullptr,

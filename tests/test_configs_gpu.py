@@ -42,11 +42,21 @@ SEED = 7
 ROUTER_TIE = 1e-3
 
 
-def _run_step(wl, dev):
+def _run_step(wl, dev, grouped):
+    """One GRPO step. grouped: the workload's `prompts` prompts rolled out
+    `group` times each, with prompt groups on (each group's prompt computed
+    once; at decode the quantized models read it in place through the
+    shared-prompt attention); else every rollout gets its own prompt."""
     mc, (policy, reference), host_w = build_models(wl, dev, seed=wl.index)
     gen = torch.Generator().manual_seed(wl.index)
     S, P, N = wl.rollouts, wl.prompt_len, wl.new_tokens
-    prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
+    if grouped:
+        for m in (policy, reference):
+            m.set_prompt_groups(wl.group)
+        prompts = torch.randint(0, mc.vocab, (wl.prompts, P), generator=gen,
+                                dtype=torch.int32).repeat_interleave(wl.group, 0).to(dev)
+    else:
+        prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
     rewards = wl.sample_rewards(gen).to(dev)
     tok, lp_beh = policy.generate(prompts, N, temperature=wl.temperature, seed=SEED)
     out = rl_prepare(policy, reference, prompts, tok, lp_beh, rewards, clip_epsilon=CLIP_EPSILON,
@@ -62,13 +72,13 @@ def _run_step(wl, dev):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("index", [0, 1, 2])
-def test_full_workload_rl_step(dev, index):
+@pytest.mark.parametrize("index,grouped", [(0, True), (1, True), (2, True), (2, False)])
+def test_full_workload_rl_step(dev, index, grouped):
     wl = RL_WORKLOADS[index]
     S, P, N, G = wl.rollouts, wl.prompt_len, wl.new_tokens, wl.group
-    print(f"case config[{index}] full workload: S={S} P={P} N={N} layers={wl.model['layers']}",
-          flush=True)
-    mc, host_w, a, res = _run_step(wl, dev)
+    print(f"case config[{index}] full workload: S={S} P={P} N={N} layers={wl.model['layers']} "
+          f"prompt groups={grouped}", flush=True)
+    mc, host_w, a, res = _run_step(wl, dev, grouped)
     V = mc.vocab
     tok, lp_beh, lp_cur, lp_ref = a["tokens"], a["lp_beh"], a["lp_cur"], a["lp_ref"]
     lp_tol = 2e-3 if wl.quantized else 1e-5

@@ -111,6 +111,74 @@ def test_attn_decode_tile_edges(dev, H, KVH, hd):
     np.testing.assert_allclose(_unpair(out, H * hd).reshape(S, H, hd), ref, rtol=2e-5, atol=2e-6)
 
 
+@pytest.mark.parametrize("G,S,H,KVH,hd,P,cap,kf16",
+                         [(8, 16, 16, 4, 128, 512, 700, True), (8, 16, 12, 12, 64, 128, 300, True),
+                          (4, 8, 8, 2, 128, 40, 100, True), (2, 6, 16, 1, 64, 600, 700, True),
+                          (8, 16, 16, 4, 128, 300, 400, False), (1, 3, 4, 4, 64, 33, 90, True)])
+def test_attn_decode_prefix(dev, G, S, H, KVH, hd, P, cap, kf16):
+    """Shared-prompt decode attention (sm_attn_decode_prefix): rollout s attends
+    its group's prompt keys 0..P-1 (stored once per group) and its own keys
+    P..lens[s]-1, against f64 attention over the concatenation, and against
+    sm_attn_decode over per-rollout copies of the prompt (same keys, other
+    f32 order). Prompt lengths off the 32-key tiles, empty continuations
+    (lens = P), one and two 16-query blocks, one and two key splits. The
+    per-rollout cache rows below P and past each length are poisoned."""
+    print(f"case prefix G={G} S={S} H={H} KVH={KVH} hd={hd} P={P} cap={cap} f16={kf16}",
+          flush=True)
+    rng = np.random.default_rng(G * 1000 + P + hd)
+    groups = S // G
+    q = rng.normal(0, 1, (S, H, hd)).astype(np.float32)
+    pk = rng.normal(0, 1, (groups, KVH, P, hd)).astype(np.float32)
+    pv = rng.normal(0, 1, (groups, KVH, P, hd)).astype(np.float32)
+    k = rng.normal(0, 1, (S, KVH, cap, hd)).astype(np.float32)
+    v = rng.normal(0, 1, (S, KVH, cap, hd)).astype(np.float32)
+    rnd = (lambda a: a.astype(np.float16).astype(np.float32)) if kf16 else oracle.round_bf16
+    q, pk, pv, k, v = (rnd(a) for a in (q, pk, pv, k, v))
+    lens = rng.integers(P, cap + 1, S).astype(np.int32)
+    lens[0], lens[-1] = P, P + 1
+    full_k, full_v = k.copy(), v.copy()  # the per-rollout cache with the prompt copied in
+    for s_ in range(S):
+        full_k[s_, :, :P], full_v[s_, :, :P] = pk[s_ // G], pv[s_ // G]
+        k[s_, :, :P], v[s_, :, :P] = 60.0, 1000.0  # never read: the prompt comes from pk / pv
+        k[s_, :, lens[s_]:], v[s_, :, lens[s_]:] = 60.0, 1000.0
+        full_k[s_, :, lens[s_]:], full_v[s_, :, lens[s_]:] = 60.0, 1000.0
+    to = (lambda a: _f16(a, dev)) if kf16 else (lambda a: _bf16(a, dev))
+    dt = SM_F16 if kf16 else SM_BF16
+    qd, pkd, pvd, kd, vd = (to(a) for a in (q, pk, pv, k, v))
+    L = torch.from_numpy(lens).to(dev)
+    nws = int(_lib.lib().sm_attn_decode_prefix_workspace_bytes(S, G, P, H, KVH, hd))
+    assert nws > 0
+    ws = torch.empty(nws // 4, dtype=torch.float32, device=dev)
+    out = torch.empty(S, 2 * H * hd, dtype=torch.float16, device=dev)
+    call("sm_attn_decode_prefix", qd.data_ptr(), pkd.data_ptr(), pvd.data_ptr(), kd.data_ptr(),
+         vd.data_ptr(), L.data_ptr(), out.data_ptr(), ws.data_ptr(), nws, dt, SM_F16X2, S, G, P,
+         H, KVH, cap, hd, _s())
+    got = _unpair(out, H * hd).reshape(S, H, hd)
+    ref = _attn_ref(q, full_k, full_v, lens)
+    np.testing.assert_allclose(got, ref, rtol=2e-5, atol=2e-6)
+    fk, fv = to(full_k), to(full_v)
+    out2 = torch.empty_like(out)
+    call("sm_attn_decode", qd.data_ptr(), fk.data_ptr(), fv.data_ptr(), L.data_ptr(),
+         out2.data_ptr(), dt, SM_F16X2, S, H, KVH, cap, hd, _s())
+    np.testing.assert_allclose(got, _unpair(out2, H * hd).reshape(S, H, hd), rtol=2e-5, atol=2e-6)
+
+
+def test_attn_decode_prefix_rejects(dev):
+    """Bad shapes and a short workspace are refused before any launch."""
+    ws = torch.empty(16, dtype=torch.float32, device=dev)
+    x = torch.empty(16, dtype=torch.float16, device=dev)
+    L = torch.full((4,), 8, dtype=torch.int32, device=dev)
+    p = [x.data_ptr()] * 5 + [L.data_ptr(), x.data_ptr(), ws.data_ptr()]
+    with pytest.raises(RuntimeError, match="workspace"):
+        call("sm_attn_decode_prefix", *p, 64, SM_F16, SM_F16X2, 4, 2, 8, 4, 4, 16, 64, _s())
+    with pytest.raises(RuntimeError, match="whole groups"):
+        call("sm_attn_decode_prefix", *p, 1 << 20, SM_F16, SM_F16X2, 5, 2, 8, 4, 4, 16, 64, _s())
+    with pytest.raises(RuntimeError, match="32 per group"):
+        call("sm_attn_decode_prefix", *p, 1 << 20, SM_F16, SM_F16X2, 4, 4, 8, 16, 1, 16, 64, _s())
+    with pytest.raises(RuntimeError, match="P <= cap"):
+        call("sm_attn_decode_prefix", *p, 1 << 20, SM_F16, SM_F16X2, 4, 2, 20, 4, 4, 16, 64, _s())
+
+
 @pytest.mark.parametrize("S,L,p0,H,KVH,hd", [(2, 100, 0, 4, 4, 64), (2, 64, 0, 16, 4, 128),
                                              (1, 130, 3, 8, 2, 128)])
 def test_attn_prefill_f16_cache_pair_out(dev, S, L, p0, H, KVH, hd):
