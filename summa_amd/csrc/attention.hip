@@ -41,6 +41,7 @@ namespace sm {
 namespace {
 
 constexpr int kMaxQpk = 16;  // query heads per KV head handled by one WG
+constexpr int kMaxPrefixSplits = 4;  // key splits of a shared prompt (attn_prefix_*)
 
 // QM: query heads per KV head the kernel is built for (>= H / KVH); EX: exactly
 // QM, so the per-head bounds are compile-time; DPL: V dims per lane in P.V.
@@ -74,6 +75,15 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
   __shared__ float pbuf[4][QM][TK];
   __shared__ float mrg_m[4][QM], mrg_l[4][QM];
   __shared__ float mrg_o[4][QM][HD];
+  // PRE: the prefix partials of this (sequence, KV head), staged at the start
+  // so their loads overlap the key loop: [head][split][HD] O, [head][split][2]
+  __shared__ float pre_os[PRE ? QM * kMaxPrefixSplits * HD : 1];
+  __shared__ float pre_mls[PRE ? QM * kMaxPrefixSplits * 2 : 1];
+  if constexpr (PRE) {
+    const size_t first = ((size_t)s * H + kvh * qpk) * nsplit;  // this WG's first slot
+    for (int e = threadIdx.x; e < qpk * nsplit * HD; e += 256) pre_os[e] = pre_o[first * HD + e];
+    for (int e = threadIdx.x; e < qpk * nsplit * 2; e += 256) pre_mls[e] = pre_ml[first * 2 + e];
+  }
 
   // A operand: query head (kvh*qpk + j) if j < qpk.
   op8 qa[STEPS];
@@ -205,9 +215,9 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     float m = -INFINITY;
 #pragma unroll
     for (int w = 0; w < 4; ++w) m = fmaxf(m, mrg_m[w][i]);
-    const size_t slot = ((size_t)s * H + kvh * qpk + i) * nsplit;
+    const int slot = i * nsplit;  // in the staged partials
     if constexpr (PRE)
-      for (int p = 0; p < nsplit; ++p) m = fmaxf(m, pre_ml[(slot + p) * 2]);
+      for (int p = 0; p < nsplit; ++p) m = fmaxf(m, pre_mls[(slot + p) * 2]);
     float l = 0.f, o = 0.f;
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
@@ -218,11 +228,11 @@ __global__ __launch_bounds__(256) void attn_decode_kernel(
     }
     if constexpr (PRE)
       for (int p = 0; p < nsplit; ++p) {
-        const float pm = pre_ml[(slot + p) * 2];
+        const float pm = pre_mls[(slot + p) * 2];
         if (pm == -INFINITY) continue;
         const float c = __expf(pm - m);
-        l += pre_ml[(slot + p) * 2 + 1] * c;
-        o += pre_o[(slot + p) * HD + d] * c;
+        l += pre_mls[(slot + p) * 2 + 1] * c;
+        o += pre_os[(slot + p) * HD + d] * c;
       }
     store_out<OM>(out, (size_t)s, H * HD, (kvh * qpk + i) * HD + d, o / l);
   }
@@ -381,6 +391,184 @@ __global__ __launch_bounds__(256) void attn_prefix_kernel(
       const float c = __expf(mrg_m[w][qi] - m);
       l += mrg_l[w][qi] * c;
       acc += mrg_o[w][qi][d] * c;
+    }
+    const int s = grp * G + qi / qpk, h = kvh * qpk + qi % qpk;
+    const size_t slot = ((size_t)s * H + h) * splits + sp;
+    part_o[slot * HD + d] = acc;
+    if (d == 0) {
+      part_ml[slot * 2] = m;
+      part_ml[slot * 2 + 1] = l;
+    }
+  }
+}
+
+// The f16-cache form of attn_prefix_kernel (the quantized models' cache):
+// P.V on the f16 matrix cores instead of f32 ones. Per 16-key tile,
+// O^T += V^T . P^T with v_mfma_f32_16x16x16_f16: B = P^T, lane (g, j) holding
+// p of keys 4g..4g+3 for query j, which is exactly the score MFMA's output
+// layout; A = V^T for dim block db, lane (g, j) holding dim j*hd/16 + db of
+// keys 4g..4g+3, gathered from the same 16-byte V loads as before (a 4 x 8
+// transpose of 16-bit values per lane and tile). P enters as an f16 hi + lo
+// pair (about 22 significant bits, so the f32 probabilities of the decode
+// kernel), scaled by 2^14 first so that probabilities far below the row's
+// maximum stay normal f16 numbers; O is scaled back before the merge. Two
+// MFMAs per (dim block, query block) replace the f32 form's four and run
+// 4x faster each. The next tile's K / V loads are issued before the current
+// tile's math (a 16-key tile, so both fit the registers).
+template <int HD, int QB>
+__global__ __launch_bounds__(256) void attn_prefix_f16_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ pk,
+    const uint16_t* __restrict__ pv, float* __restrict__ part_o, float* __restrict__ part_ml,
+    int H, int KVH, int G, int P, int per, float scale) {
+  constexpr int STEPS = HD / 32;  // score MFMA k-steps over head_dim
+  constexpr int DB = HD / 16;     // dim blocks of the P.V MFMA = V dims per lane
+  typedef typename std::conditional<DB == 8, u32x4, u32x2>::type vrow;
+  constexpr int TK = 16;          // keys per tile
+  constexpr float kPS = 16384.f;  // P scale before the f16 split
+  const int qpk = H / KVH, nq = G * qpk;
+  // blockIdx.z = split * nqg + query group: each workgroup takes QB 16-query
+  // blocks, so a group's query blocks run in several workgroups (fewer
+  // registers, more of them resident); their K / V reads after the first hit
+  // L2 (the workgroups of one split are KVH * groups apart in launch order, a
+  // multiple of the 8 XCDs at the configs' shapes, so on one XCD).
+  const int nqg = (nq + QB * 16 - 1) / (QB * 16);
+  const int kvh = blockIdx.x, grp = blockIdx.y, sp = blockIdx.z / nqg;
+  const int splits = gridDim.z / nqg, qbase = (blockIdx.z % nqg) * QB * 16;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  const int k_lo = sp * per, k_hi = min(P, k_lo + per);
+  const size_t base = ((size_t)grp * KVH + kvh) * P * HD;
+  __shared__ float mrg_m[4][QB * 16], mrg_l[4][QB * 16];
+  __shared__ float mrg_o[4][QB * 16][HD + 1];
+
+  h8 qf[QB][STEPS];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = qbase + qb * 16 + j;
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) qf[qb][st] = h8{};
+    if (qi < nq) {
+      const int s = grp * G + qi / qpk, h = kvh * qpk + qi % qpk;
+      const uint16_t* qp = q + ((size_t)s * H + h) * HD + g * 8;
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st) qf[qb][st] = *reinterpret_cast<const h8*>(qp + st * 32);
+    }
+  }
+  float m_i[QB], l_i[QB];
+  f4 o[QB][DB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_i[qb] = -INFINITY;
+    l_i[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < DB; ++db) o[qb][db] = f4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  struct Tile {
+    h8 kf[STEPS];
+    vrow vr[4];
+  };
+  const int last = k_hi - 1;  // loads past the split's end re-read its last key (masked)
+  auto load = [&](int t0, Tile& T) {
+    const uint16_t* kp = pk + base + (size_t)min(t0 + j, last) * HD + g * 8;
+#pragma unroll
+    for (int st = 0; st < STEPS; ++st) T.kf[st] = *reinterpret_cast<const h8*>(kp + st * 32);
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      T.vr[r] = *reinterpret_cast<const vrow*>(pv + base + (size_t)min(t0 + 4 * g + r, last) * HD +
+                                               j * DB);
+  };
+  auto half_of = [](const vrow& v, int e) -> uint32_t {
+    const uint32_t w = (e >> 1) == 0 ? v[0] : (e >> 1) == 1 ? v[1] : (e >> 1) == 2 ? v[2] : v[3];
+    return (e & 1) ? (w >> 16) : (w & 0xffffu);
+  };
+  auto compute = [&](int t0, const Tile& T) {
+    h4 a[DB];  // V^T: dim j*DB + db of keys t0 + 4g + r, r = 0..3
+#pragma unroll
+    for (int db = 0; db < DB; ++db) {
+      u32x2 w;
+      w[0] = half_of(T.vr[0], db) | (half_of(T.vr[1], db) << 16);
+      w[1] = half_of(T.vr[2], db) | (half_of(T.vr[3], db) << 16);
+      a[db] = __builtin_bit_cast(h4, w);
+    }
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+      f4 sc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int st = 0; st < STEPS; ++st)
+        sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(T.kf[st], qf[qb][st], sc, 0, 0, 0);
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = (t0 + 4 * g + r < k_hi) ? sc[r] * scale : -INFINITY;
+        sc[r] = v;
+        mx = fmaxf(mx, v);
+      }
+      mx = fmaxf(mx, __shfl_xor(mx, 16, kWave));
+      mx = fmaxf(mx, __shfl_xor(mx, 32, kWave));
+      const float mnew = fmaxf(m_i[qb], mx);  // finite: key t0 is in range
+      const float alpha = (m_i[qb] == -INFINITY) ? 0.f : __expf(m_i[qb] - mnew);
+      float ps = 0.f;
+      h4 bh, bl;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = (sc[r] == -INFINITY) ? 0.f : __expf(sc[r] - mnew);
+        ps += p;
+        _Float16 hi, lo;
+        split_f16(p * kPS, hi, lo);
+        bh[r] = hi;
+        bl[r] = lo;
+      }
+      ps += __shfl_xor(ps, 16, kWave);
+      ps += __shfl_xor(ps, 32, kWave);
+      l_i[qb] = l_i[qb] * alpha + ps;
+      m_i[qb] = mnew;
+#pragma unroll
+      for (int db = 0; db < DB; ++db) {
+        o[qb][db] *= alpha;
+        o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[db], bh, o[qb][db], 0, 0, 0);
+        o[qb][db] = __builtin_amdgcn_mfma_f32_16x16x16f16(a[db], bl, o[qb][db], 0, 0, 0);
+      }
+    }
+  };
+  int t0 = k_lo + wave * TK;
+  if (t0 < k_hi) {
+    Tile cur;
+    load(t0, cur);
+    for (; t0 < k_hi; t0 += 4 * TK) {
+      Tile nxt;
+      load(t0 + 4 * TK, nxt);  // clamped into the split: in bounds past its end too
+      compute(t0, cur);
+      cur = nxt;
+    }
+  }
+  // lane (g, j) holds dims (4g + r) * DB + db of query qb*16 + j (times kPS)
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+    for (int db = 0; db < DB; ++db)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        mrg_o[wave][qb * 16 + j][(4 * g + r) * DB + db] = o[qb][db][r] * (1.f / kPS);
+    if (g == 0) {
+      mrg_m[wave][qb * 16 + j] = m_i[qb];
+      mrg_l[wave][qb * 16 + j] = l_i[qb];
+    }
+  }
+  __syncthreads();
+  const int nql = min(nq - qbase, QB * 16);  // this workgroup's queries
+  for (int e = threadIdx.x; e < nql * HD; e += 256) {
+    const int ql = e / HD, d = e % HD, qi = qbase + ql;
+    float m = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) m = fmaxf(m, mrg_m[w][ql]);
+    float l = 0.f, acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (mrg_m[w][ql] == -INFINITY) continue;
+      const float c = __expf(mrg_m[w][ql] - m);
+      l += mrg_l[w][ql] * c;
+      acc += mrg_o[w][ql][d] * c;
     }
     const int s = grp * G + qi / qpk, h = kvh * qpk + qi % qpk;
     const size_t slot = ((size_t)s * H + h) * splits + sp;
@@ -743,6 +931,7 @@ namespace {
 int prefix_splits(int64_t groups, int64_t KVH, int64_t P) {
   const int64_t pairs = groups * KVH;
   int64_t sp = std::max<int64_t>(1, std::min<int64_t>((256 + pairs - 1) / pairs, P / 256));
+  sp = std::min<int64_t>(sp, kMaxPrefixSplits);
   const int64_t per = (P + sp - 1) / sp;
   const int64_t per32 = (per + 31) / 32 * 32;
   return (int)((P + per32 - 1) / per32);  // no empty split
@@ -804,11 +993,19 @@ extern "C" int sm_attn_decode_prefix(const void* q, const void* prefix_k, const 
                                                       (int)KVH, (int)G, (int)P, per, scale)
 #define SM_PRE_AK(HD, KF) \
   do { if (two) SM_PRE_A(HD, KF, 2); else SM_PRE_A(HD, KF, 1); } while (0)
-  if (head_dim == 64) {
-    if (f16) SM_PRE_AK(64, true); else SM_PRE_AK(64, false);
+  const dim3 ga16((unsigned)KVH, (unsigned)(S / G), (unsigned)(splits * (two ? 2 : 1)));
+#define SM_PRE_A16(HD)                                                                   \
+  attn_prefix_f16_kernel<HD, 1><<<ga16, 256, 0, st>>>(qq, pk, pv, part_o, part_ml, (int)H, \
+                                                       (int)KVH, (int)G, (int)P, per, scale)
+  if (f16) {  // P.V on the f16 matrix cores, one 16-query block per workgroup
+    if (head_dim == 64) SM_PRE_A16(64);
+    else SM_PRE_A16(128);
+  } else if (head_dim == 64) {
+    SM_PRE_AK(64, false);
   } else {
-    if (f16) SM_PRE_AK(128, true); else SM_PRE_AK(128, false);
+    SM_PRE_AK(128, false);
   }
+#undef SM_PRE_A16
 #undef SM_PRE_AK
 #undef SM_PRE_A
   const dim3 gb((unsigned)KVH, (unsigned)S);
