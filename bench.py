@@ -534,7 +534,9 @@ def bench_rl_step(args) -> dict:
     roll, full, wall, out = run_rl_step(wl, policy, reference, prompts, rewards, args.steps,
                                         args.warmup, tag=f"config[{wl.index}]")
     res = batch_result(out)
-    lp_gap = float((out["lp_beh"] - out["lp_cur"]).abs().max())
+    gap = (out["lp_beh"] - out["lp_cur"]).abs()
+    lp_gap = float(gap.max())
+    within = float((gap <= 2e-3).float().mean())
     r_ms, f_ms = sum(roll) / len(roll), sum(full) / len(full)
     pre_ms = prefill_ms(wl, policy, prompts)
     dec_ms = r_ms - pre_ms
@@ -554,7 +556,12 @@ def bench_rl_step(args) -> dict:
         "rl_step_ms": round(f_ms, 3), "rollout_ms": round(r_ms, 3), "prepare_ms": round(prep_ms, 3),
         "wall_s": round(wall, 3),
         "grpo": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()},
-        "check": {"max_abs_lp_behaviour_minus_recompute": lp_gap},
+        # cached decode vs the recompute over the whole batch (2e-3 bar); for
+        # MoE models a router near-tie can pick another expert pair in one
+        # path, after which that rollout's tokens differ (tests resolve those
+        # through traced router decisions)
+        "check": {"max_abs_lp_behaviour_minus_recompute": lp_gap,
+                  "fraction_of_tokens_within_2e-3": within},
         "phases": {
             "prefill_ms": round(pre_ms, 3),
             "decode": {"ms": round(dec_ms, 3), "steps": N - 1,

@@ -140,7 +140,8 @@ def _margins(logits):
 
 
 @pytest.mark.timeout(600)
-def test_moe_full_workload_rl_step(dev):
+@pytest.mark.parametrize("grouped", [False, True])
+def test_moe_full_workload_rl_step(dev, grouped):
     """Config[4] (16-layer top-2 MoE, 32 experts) at its full workload.
 
     The decode path, the recompute path and the oracle can each resolve a
@@ -154,35 +155,61 @@ def test_moe_full_workload_rl_step(dev):
     * the oracle takes the recompute path's pair wherever its own margin is
       below ROUTER_TIE and must agree everywhere else; with that, rollouts 0
       and S-1 must match it within 2e-3 over their whole length (recompute)
-      and up to the first flip (behaviour, sampled tokens)."""
+      and up to the first flip (behaviour, sampled tokens).
+    grouped: the workload's prompts rolled out `group` times each with prompt
+    groups on, so each group's prompt positions (and their router decisions)
+    are computed once; their traces are expanded to the group's rollouts."""
     wl = RL_WORKLOADS[4]
     S, P, N, G = wl.rollouts, wl.prompt_len, wl.new_tokens, wl.group
     L = P + N - 1
-    print(f"case config[4] full workload: S={S} P={P} N={N} layers={wl.model['layers']}",
-          flush=True)
+    print(f"case config[4] full workload: S={S} P={P} N={N} layers={wl.model['layers']} "
+          f"prompt groups={grouped}", flush=True)
     mc, (policy, reference), host_w = build_models(wl, dev, seed=wl.index)
     Lr, E = mc.layers, mc.experts
     gen = torch.Generator().manual_seed(wl.index)
-    prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
+    # prompt rows computed per call: groups of G share theirs when grouped
+    PS = wl.prompts if grouped else S
+    if grouped:
+        for m in (policy, reference):
+            m.set_prompt_groups(G)
+        prompts = torch.randint(0, mc.vocab, (wl.prompts, P), generator=gen,
+                                dtype=torch.int32).repeat_interleave(G, 0).to(dev)
+    else:
+        prompts = torch.randint(0, mc.vocab, (S, P), generator=gen, dtype=torch.int32).to(dev)
     rewards = wl.sample_rewards(gen).to(dev)
-    cap = Lr * (S * P + (N - 1) * S)
+    cap = Lr * (PS * P + (N - 1) * S)
     gi, gl = policy.trace_routes(cap)
     tok, lp_beh = policy.generate(prompts, N, temperature=wl.temperature, seed=SEED)
     assert policy.route_trace_count() == (cap, 0)
     gi, gl = gi.cpu().numpy(), gl.cpu().numpy()
-    assert S * L <= 65536  # the recompute runs as one chunk: one trace block per layer
-    ri, rl = policy.trace_routes(Lr * S * L)
+    # the recompute runs as one chunk (grouped: one prompt chunk, then one
+    # continuation chunk): one trace block per layer and chunk
+    assert S * L <= 65536
+    rcap = Lr * (PS * P + S * (N - 1)) if grouped else Lr * S * L
+    ri, rl = policy.trace_routes(rcap)
     out = rl_prepare(policy, reference, prompts, tok, lp_beh, rewards, clip_epsilon=CLIP_EPSILON,
                      advantage_epsilon=ADVANTAGE_EPSILON, kl_coefficient=KL_COEFFICIENT)
     res = batch_result(out)
-    assert policy.route_trace_count() == (Lr * S * L, 0)
+    assert policy.route_trace_count() == (rcap, 0)
     policy.stop_trace()
-    ri, rl = ri.cpu().numpy().reshape(Lr, S, L, 2), rl.cpu().numpy().reshape(Lr, S, L, E)
-    # generate trace: prefill [Lr, S, P], then per decode step [Lr, S] (position P + t - 1)
-    pre = Lr * S * P
-    g_ids = np.concatenate([gi[:pre].reshape(Lr, S, P, 2),
+    ri, rl = ri.cpu().numpy(), rl.cpu().numpy()
+
+    def per_rollout(a, k):  # prompt trace [Lr, PS, P, k] -> [Lr, S, P, k]
+        return np.repeat(a, G, axis=1) if grouped else a
+
+    if grouped:  # prompt chunk [Lr, groups, P], then continuation chunk [Lr, S, N - 1]
+        pr = Lr * PS * P
+        ri = np.concatenate([per_rollout(ri[:pr].reshape(Lr, PS, P, 2), 2),
+                             ri[pr:].reshape(Lr, S, N - 1, 2)], 2)
+        rl = np.concatenate([per_rollout(rl[:pr].reshape(Lr, PS, P, E), E),
+                             rl[pr:].reshape(Lr, S, N - 1, E)], 2)
+    else:
+        ri, rl = ri.reshape(Lr, S, L, 2), rl.reshape(Lr, S, L, E)
+    # generate trace: prefill [Lr, PS, P], then per decode step [Lr, S] (position P + t - 1)
+    pre = Lr * PS * P
+    g_ids = np.concatenate([per_rollout(gi[:pre].reshape(Lr, PS, P, 2), 2),
                             gi[pre:].reshape(N - 1, Lr, S, 2).transpose(1, 2, 0, 3)], 2)
-    g_lg = np.concatenate([gl[:pre].reshape(Lr, S, P, E),
+    g_lg = np.concatenate([per_rollout(gl[:pre].reshape(Lr, PS, P, E), E),
                            gl[pre:].reshape(N - 1, Lr, S, E).transpose(1, 2, 0, 3)], 2)
     del gi, gl
     tok, lp_beh = tok.cpu().numpy(), lp_beh.cpu().numpy()
