@@ -50,7 +50,7 @@ constexpr int kMaxPrefixSplits = 4;  // key splits of a shared prompt (attn_pref
 // cache and folds the prefix's nsplit partials (max, sum, unnormalised O per
 // query head) into its final merge.
 template <int HD, int QM, bool KF16, int OM, bool EX, int DPL, bool PRE = false>
-__global__ __launch_bounds__(256) void attn_decode_kernel(
+__global__ __launch_bounds__(256, PRE ? 4 : 1) void attn_decode_kernel(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc,
     const uint16_t* __restrict__ vc, const int32_t* __restrict__ lens,
     void* __restrict__ out, int H, int KVH, int cap, float scale, int k0 = 0,
