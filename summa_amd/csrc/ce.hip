@@ -25,7 +25,10 @@
 //     threads x 4 vectors: 7.3-7.4 ms. Keeping each row in VGPRs
 //     (read once, write once) was 9.9 ms: a 1024-thread workgroup holding
 //     256 KB in registers fits once per CU, so its read, reduce and write
-//     phases never overlap with another row's.
+//     phases never overlap with another row's. Keeping only the row's last
+//     1/8 to 1/2 in registers (those gradients written without a second
+//     read, the rest re-read newest first) was 7.3-8.6 ms: the registers
+//     cost rows in flight per CU, and with them more than the re-reads.
 #include <cfloat>
 #include <cmath>
 
