@@ -163,6 +163,21 @@ int64_t sm_q4_matmul_workspace_bytes(int64_t M, int64_t N, int64_t K, int epilog
 int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
                     const void* x, int x_dtype, int64_t M, int64_t ldx, void* y, int64_t ldy,
                     int epilogue, void* workspace, int64_t workspace_bytes, void* stream);
+/* A residual projection and the RMSNorm that follows it (the pre-norm
+ * decoder's x = x + Linear(h); h = RMSNorm(x) * gamma, block.rs / norm.rs:36-50,
+ * with the Linear over a quantized weight, matmul.rs:57-66): resid [M, N] f32
+ * += x . W^T (as sm_q4_matmul_ws with SM_EPI_ADD_F32, ldy = N), then h_out
+ * [M, 2N] f16 pairs (SM_F16X2 rows) = RMSNorm(resid) * gamma (as sm_rmsnorm).
+ * At decode batch sizes (the LDS-staged decode kernel's shapes, N a multiple
+ * of 256 up to 4096, a workspace of sm_q4_matmul_workspace_bytes(M, N, K,
+ * SM_EPI_ADD_F32) bytes) K is split and one kernel sums the partials in split
+ * order into resid and normalises the rows; elsewhere the two steps run. The
+ * results are those of the two calls wherever the matmul would split K
+ * itself, and within f32 summation order otherwise. */
+int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                             const void* x, int x_dtype, int64_t M, int64_t ldx, float* resid,
+                             const float* gamma, float eps, void* h_out, void* workspace,
+                             int64_t workspace_bytes, void* stream);
 /* sm_q4_matmul_ws without a caller workspace and without any allocation, for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the

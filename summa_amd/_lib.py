@@ -41,6 +41,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_q4_qkv_rope": (i32, [vp, vp, i64, i64, i64, i64, vp, i32, i64, i64, i64, vp, vp, i64, vp,
                              vp, vp, i32, vp]),
     "sm_q4_matmul_ws": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp, i64, vp]),
+    "sm_q4_matmul_add_rmsnorm": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, vp, f32, vp, vp,
+                                       i64, vp]),
     "sm_q4_noalloc_scratch_bytes": (i64, []),
     "sm_q4_matmul_noalloc": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
     "sm_q4_gemv_multi_plan": (i64, [vp, i64, vp]),

@@ -48,6 +48,9 @@ int sm_attn_decode(const void*, const void*, const void*, const int32_t*, void*,
                    int64_t, int64_t, int64_t, int64_t, int64_t, void*);
 int sm_attn_prefill(const void*, const void*, const void*, const int32_t*, void*, int, int,
                     int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void*);
+int sm_q4_matmul_add_rmsnorm(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int,
+                             int64_t, int64_t, float*, const float*, float, void*, void*, int64_t,
+                             void*);
 int64_t sm_attn_decode_prefix_workspace_bytes(int64_t, int64_t, int64_t, int64_t, int64_t,
                                               int64_t);
 int sm_attn_decode_prefix(const void*, const void*, const void*, const void*, const void*,
@@ -330,6 +333,25 @@ int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float*
   return sm_gemm_f32(L.w, L.N, L.K, (const float*)x, M, L.K, y, L.N, epi, st);
 }
 
+// x += xin . W^T, then m->h = RMSNorm(x) * gamma in the activation dtype (a
+// residual projection and the norm that follows it). Quantized models make it
+// one call, which at decode batch sizes sums the projection's split-K partials
+// into x and normalises the rows in one launch; elsewhere the two steps.
+int linear_add_norm(sm_model* m, const Linear& L, const void* xin, int64_t M, float* x,
+                    const float* gamma, hipStream_t st) {
+  const auto& c = m->cfg;
+  if (c.quantized && m->act == SM_F16X2) {
+    const int64_t want =
+        std::min(kMatmulWs, sm_q4_matmul_workspace_bytes(M, L.N, L.K, SM_EPI_ADD_F32));
+    if (want > 0) SM_TRY(ensure(m->mmws, (size_t)want));
+    return sm_q4_matmul_add_rmsnorm(L.codes, L.scales, L.N, L.K, xin, m->act, M, m->act_ld(L.K),
+                                    x, gamma, c.norm_eps, m->h.p, want > 0 ? m->mmws.p : nullptr,
+                                    want, st);
+  }
+  SM_TRY(linear_f32out(m, L, xin, M, x, true, st));
+  return sm_rmsnorm(x, gamma, M, c.d_model, c.norm_eps, m->h.p, m->act, st);
+}
+
 // u = silu(x W_gate^T) * (x W_value^T) in the activation dtype.
 int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* u,
                   hipStream_t st) {
@@ -428,6 +450,7 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
   SM_TRY(ensure(m->u, (size_t)rows * c.ffn * m->act_size));
   float* x = (float*)m->x.p;
   SM_TRY(sm_embed(m->embed, m->embt, ids, rows, d, c.vocab, 1.0f, x, st));
+  bool normed = false;  // m->h already holds this layer's attention-norm output
   for (int l = 0; l < c.layers; ++l) {
     const Layer& Ly = m->layers[l];
     char* kl = (char*)kc + (size_t)l * layer_elems * m->kv_size;
@@ -440,7 +463,8 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
             (const char*)(kv ? pre->v : pre->k) + l * pre->layer_bytes, kv ? vl : kl, 1, S,
             pre->s0, 0, pre->G, c.kv_heads, pre->P, (int)cap, rb, 0, 0);
     }
-    SM_TRY(sm_rmsnorm(x, Ly.attn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
+    if (!normed) SM_TRY(sm_rmsnorm(x, Ly.attn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
+    normed = false;
     if (c.quantized) {  // qkv projection with RoPE + cache append in its epilogue
       SM_TRY(sm_q4_qkv_rope(Ly.qkv.codes, Ly.qkv.scales, c.heads, c.kv_heads, c.head_dim, d,
                             m->h.p, m->act, S, L, m->act_ld(d), m->rope, pos0, cap, m->qb.p, kl,
@@ -462,13 +486,17 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
     else
       SM_TRY(sm_attn_prefill(m->qb.p, kl, vl, pos0, m->attn.p, m->kvt, m->act, S, L, c.heads,
                              c.kv_heads, cap, c.head_dim, st));
-    SM_TRY(linear_f32out(m, Ly.o, m->attn.p, rows, x, true, st));
-    SM_TRY(sm_rmsnorm(x, Ly.ffn_norm, rows, d, c.norm_eps, m->h.p, m->act, st));
+    SM_TRY(linear_add_norm(m, Ly.o, m->attn.p, rows, x, Ly.ffn_norm, st));
     if (c.experts > 0) {
       SM_TRY(moe_ffn(m, Ly, rows, st));
     } else {
       SM_TRY(linear_swiglu(m, Ly.in, m->h.p, rows, m->u.p, st));
-      SM_TRY(linear_f32out(m, Ly.down, m->u.p, rows, x, true, st));
+      if (l + 1 < c.layers) {  // the down projection with the next layer's attention norm
+        SM_TRY(linear_add_norm(m, Ly.down, m->u.p, rows, x, m->layers[l + 1].attn_norm, st));
+        normed = true;
+      } else {
+        SM_TRY(linear_f32out(m, Ly.down, m->u.p, rows, x, true, st));
+      }
     }
   }
   return SM_OK;

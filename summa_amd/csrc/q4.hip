@@ -556,7 +556,8 @@ void launch_gl(dim3 grid, hipStream_t st, const Q4Args& a) {
 }
 
 template <int XT, int NB>
-int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks) {
+int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks,
+                          bool reduce = true) {
   const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
   const dim3 grid((unsigned)ceil_div(logical_cols, 8 * 16 * NB), (unsigned)row_tiles, (unsigned)ks);
   switch (epi) {
@@ -573,7 +574,7 @@ int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_
     default: set_error("sm_q4_grouped_matmul: unknown epilogue %d", epi); return SM_ERR_INVALID;
   }
   SM_LAUNCH_CHECK();
-  if (ks > 1) return splitk_reduce(a.part, ks, a.M, a.N, a.ncols, a.y, a.ldy, epi, st);
+  if (ks > 1 && reduce) return splitk_reduce(a.part, ks, a.M, a.N, a.ncols, a.y, a.ldy, epi, st);
   return SM_OK;
 }
 
@@ -584,10 +585,11 @@ int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_
 // bits): config[1] rollout 213.4 -> 206.8 ms, config[4] 844 -> 837 ms, while
 // config[2]'s 256-row decode is 0.8 % slower that way and keeps 256.
 template <int XT>
-int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1) {
+int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1,
+                       bool reduce = true) {
   if (!a.tiles && !is_swiglu(epi) && a.M <= 128)
-    return launch_grouped_lds_nb<XT, 1>(a, epi, st, row_tiles, ks);
-  return launch_grouped_lds_nb<XT, 2>(a, epi, st, row_tiles, ks);
+    return launch_grouped_lds_nb<XT, 1>(a, epi, st, row_tiles, ks, reduce);
+  return launch_grouped_lds_nb<XT, 2>(a, epi, st, row_tiles, ks, reduce);
 }
 
 // M = 1 (one sequence's decode step; the LM head at batch 1). One wave owns a
@@ -858,6 +860,94 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
                     st, nullptr, nullptr, 0, nullptr, nullptr, 0, 0, ws, ws_bytes, nullptr);
 }
 
+// Split-K partials of a residual projection, summed in split order and added
+// to the residual (splitk_reduce_kernel's EPI_ADD_F32 arithmetic), then the
+// next RMSNorm of the updated rows written as f16 pairs, with
+// rmsnorm_wave_kernel's arithmetic: lane l's sum of squares runs over float4s
+// l, 64 + l, ... of the row in that order, then one wave reduction, and
+// x / rms * gamma. One workgroup per row, wave i owning float4s i*64 + l; KS
+// (the split count, 0 = given at run time) is a template parameter so every
+// lane issues all its partial, residual and gamma loads at once. The squares
+// meet in LDS so that wave 0 sums them in the one-wave order. Replaces the
+// reduce launch and the norm launch with one.
+template <int V, int KS>
+__global__ __launch_bounds__(64 * V) void splitk_add_rmsnorm_kernel(
+    const float* __restrict__ part, int ks, int64_t rows, float* __restrict__ resid,
+    const float* __restrict__ gamma, float eps, _Float16* __restrict__ h) {
+  constexpr int D = 256 * V;
+  __shared__ float4 sq[V][kWave];
+  __shared__ float rms_s;
+  const int64_t r = blockIdx.x;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int c4 = wave * kWave + lane;
+  const size_t split4 = (size_t)rows * (D / 4);
+  const float4* pr = reinterpret_cast<const float4*>(part) + r * (D / 4) + c4;
+  float4* xr = reinterpret_cast<float4*>(resid + r * D) + c4;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+  if constexpr (KS > 0) {
+    float4 p[KS];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) p[k] = pr[k * split4];
+#pragma unroll
+    for (int k = 0; k < KS; ++k) {
+      acc.x += p[k].x; acc.y += p[k].y; acc.z += p[k].z; acc.w += p[k].w;
+    }
+  } else {
+    for (int k = 0; k < ks; ++k) {
+      const float4 p = pr[k * split4];
+      acc.x += p.x; acc.y += p.y; acc.z += p.z; acc.w += p.w;
+    }
+  }
+  const float4 x = *xr;
+  const float4 gm = reinterpret_cast<const float4*>(gamma)[c4];
+  const float4 v = make_float4(x.x + acc.x, x.y + acc.y, x.z + acc.z, x.w + acc.w);
+  *xr = v;
+  sq[wave][lane] = v;
+  __syncthreads();
+  if (wave == 0) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float4 t = sq[i][lane];
+      ss = fmaf(t.w, t.w, fmaf(t.z, t.z, fmaf(t.y, t.y, fmaf(t.x, t.x, ss))));
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) rms_s = sqrtf(ss / (float)D + eps);
+  }
+  __syncthreads();
+  const float rms = rms_s;
+  const float o[4] = {v.x / rms * gm.x, v.y / rms * gm.y, v.z / rms * gm.z, v.w / rms * gm.w};
+  _Float16 hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) split_f16(o[e], hi[e], lo[e]);
+  _Float16* yr = h + r * 2 * D;
+  *reinterpret_cast<h4*>(yr + 4 * c4) = h4{hi[0], hi[1], hi[2], hi[3]};
+  *reinterpret_cast<h4*>(yr + D + 4 * c4) = h4{lo[0], lo[1], lo[2], lo[3]};
+}
+
+// K splits of the fused residual projection + RMSNorm, or 0 when the fused
+// form does not apply (dispatch_q4 would not pick the LDS-staged decode kernel
+// for this shape, the width is not one the row-in-registers norm handles, or
+// the workspace cannot hold two splits). The split count follows dispatch_q4's
+// rule for the LDS-staged kernel over K ranges (>= 3 groups per split, up to
+// ~512 workgroups), so a projection it already splits keeps its partials.
+int add_rmsnorm_splits(int64_t M, int64_t N, int64_t K, int xt, int64_t ws_bytes) {
+  if (xt != X_F16X2 && xt != X_F16) return 0;
+  if (N % 256 != 0) return 0;
+  const int64_t v = N / 256;
+  if (v != 3 && v != 4 && v != 8 && v != 12 && v != 16) return 0;
+  const int64_t bl_wgs = ceil_div(M, 64) * ceil_div(N, 64);
+  if (M <= 32 || M > 256 || bl_wgs < 64) return 0;
+  if (!use_dense_lds(M, K, N, xt) && !use_dense_lds_split(M, K, N, xt)) return 0;
+  const int ng = (int)(K / 128);
+  const int64_t base = ceil_div(N, 256) * ceil_div(M, 16);
+  int ks = (int)std::min<int64_t>(ng / 3, std::max<int64_t>(1, 512 / base));
+  while (ks > 1 && (int64_t)ks * M * N * 4 > ws_bytes) --ks;
+  if (ks < 2) return 0;
+  const int gper = (int)ceil_div(ng, ks);
+  return (int)ceil_div(ng, gper);  // every split non-empty
+}
+
 // ----------------------------------------------------------- quantizer ---
 // One wave per 128-element group; lane l owns elements 2l, 2l+1 (one byte).
 __device__ inline float round_half_away(float v) {
@@ -1005,6 +1095,66 @@ extern "C" int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int
   if (M == 0) return SM_OK;
   Q4Args a{codes, scales, x, y, (int)M, (int)N, (int)K, (int)ldx, (int)ldy, (int)ncols};
   return dispatch_q4(a, epilogue, xt, as_stream(stream), workspace, workspace_bytes);
+}
+
+extern "C" int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int64_t d, float eps,
+                          void* y, int out_dtype, void* stream);
+
+extern "C" int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N,
+                                        int64_t K, const void* x, int x_dtype, int64_t M,
+                                        int64_t ldx, float* resid, const float* gamma, float eps,
+                                        void* h_out, void* workspace, int64_t workspace_bytes,
+                                        void* stream) {
+  using namespace sm;
+  SM_REQUIRE(resid && gamma && h_out, "sm_q4_matmul_add_rmsnorm: null buffer");
+  const int xt = xmode_of(x_dtype);
+  const int ks = (xt >= 0 && workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(h_out) % 8 == 0 && M <= 0x7fffffff &&
+                  N <= 0x7fffffff && K > 0 && K % 128 == 0)
+                     ? add_rmsnorm_splits(M, N, K, xt, workspace_bytes) : 0;
+  hipStream_t st = as_stream(stream);
+  if (ks == 0) {  // the two-step form: residual projection, then the norm
+    SM_TRY(sm_q4_matmul_ws(codes, scales, N, K, x, x_dtype, M, ldx, resid, N, EPI_ADD_F32,
+                           workspace, workspace_bytes, stream));
+    return sm_rmsnorm(resid, gamma, M, N, eps, h_out, SM_F16X2, stream);
+  }
+  SM_REQUIRE(codes && scales && x && ldx >= (xt == X_F16X2 ? 2 * K : K) && ldx % 8 == 0 &&
+                 reinterpret_cast<uintptr_t>(codes) % 16 == 0 &&
+                 reinterpret_cast<uintptr_t>(x) % 16 == 0,
+             "sm_q4_matmul_add_rmsnorm: bad matmul operands");
+  Q4Args a{codes, scales, x, resid, (int)M, (int)N, (int)K, (int)ldx, (int)N, (int)N};
+  const int ng = (int)(K / 128);
+  a.gper = (int)ceil_div(ng, ks);
+  a.part = static_cast<float*>(workspace);
+  const int64_t rt = ceil_div(M, 16);
+  if (xt == X_F16X2) SM_TRY(launch_grouped_lds<X_F16X2>(a, EPI_ADD_F32, st, rt, ks, false));
+  else SM_TRY(launch_grouped_lds<X_F16>(a, EPI_ADD_F32, st, rt, ks, false));
+  const unsigned blocks = (unsigned)M;
+  _Float16* h = static_cast<_Float16*>(h_out);
+#define SM_ARK(V, KS)                                                                   \
+  splitk_add_rmsnorm_kernel<V, KS><<<blocks, 64 * V, 0, st>>>(a.part, ks, M, resid, gamma, \
+                                                              eps, h)
+#define SM_ARN(V)                                                \
+    case V:                                                      \
+      if (ks == 2) SM_ARK(V, 2);                                 \
+      else if (ks == 3) SM_ARK(V, 3);                            \
+      else if (ks == 4) SM_ARK(V, 4);                            \
+      else SM_ARK(V, 0);                                         \
+      break;
+  switch (N / 256) {
+    SM_ARN(3)
+    SM_ARN(4)
+    SM_ARN(8)
+    SM_ARN(12)
+    SM_ARN(16)
+    default: set_error("sm_q4_matmul_add_rmsnorm: width %lld", (long long)N); return SM_ERR_INVALID;
+  }
+#undef SM_ARN
+#undef SM_ARK
+  SM_LAUNCH_CHECK();
+  return SM_OK;
 }
 
 extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts,

@@ -556,3 +556,60 @@ def test_gemv_multi_equals_single_launches(dev, pair):
     batch.launch()
     for (qw, xd, y, epi), (base, ref) in zip(jobs, refs):
         assert torch.equal(y.float(), ref.float()), qw.n
+
+
+@pytest.mark.parametrize("m,n,k,exact", [(256, 2048, 2048, False), (256, 2048, 5632, True),
+                                         (128, 2048, 2048, False), (200, 1024, 2048, True),
+                                         (256, 768, 3072, True), (1024, 2048, 2048, True)])
+def test_matmul_add_rmsnorm(dev, m, n, k, exact):
+    """sm_q4_matmul_add_rmsnorm (a residual projection and the RMSNorm after
+    it in one call) against the two-step form (sm_q4_matmul_ws + sm_rmsnorm):
+    the normalised rows are always sm_rmsnorm's bits of the returned residual;
+    the residual equals the two-step one bit for bit where the matmul splits K
+    itself or the fused form does not apply (exact), and is within the split
+    tolerance of base + x.W^T in f64 everywhere. Shapes: config[2]'s decode o
+    (forced split) and down projections, config[4]'s o at 128 rows, a narrow
+    N, and two shapes that fall back (narrow 768-column decode, prefill)."""
+    print(f"case add+rmsnorm m={m} n={n} k={k}", flush=True)
+    st = torch.cuda.current_stream().cuda_stream
+    w = _weights(n, k, m + n + k)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(m + 11).normal(0, 1, (m, k)).astype(np.float32)
+    xp, xr = _pair_host(x)
+    xd = torch.from_numpy(xp).to(dev)
+    rng = np.random.default_rng(n)
+    base = rng.normal(0, 1, (m, n)).astype(np.float32)
+    gamma = torch.from_numpy(rng.uniform(0.5, 1.5, n).astype(np.float32)).to(dev)
+    eps = 1e-5
+    ws = ops.q4_workspace(m, n, k, _lib.SM_EPI_ADD_F32, dev)
+
+    def fused():
+        r = torch.from_numpy(base.copy()).to(dev)
+        h = torch.empty((m, 2 * n), dtype=torch.float16, device=dev)
+        _lib.call("sm_q4_matmul_add_rmsnorm", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), n, k,
+                  xd.data_ptr(), _lib.SM_F16X2, m, 2 * k, r.data_ptr(), gamma.data_ptr(), eps,
+                  h.data_ptr(), ws.data_ptr(), ws.numel(), st)
+        return r, h
+
+    def norm(r):
+        h = torch.empty((m, 2 * n), dtype=torch.float16, device=dev)
+        _lib.call("sm_rmsnorm", r.data_ptr(), gamma.data_ptr(), m, n, eps, h.data_ptr(),
+                  _lib.SM_F16X2, st)
+        return h
+
+    r1, h1 = fused()
+    r1b, h1b = fused()
+    torch.testing.assert_close(r1, r1b, rtol=0, atol=0)  # run to run
+    torch.testing.assert_close(h1, h1b, rtol=0, atol=0)
+    torch.testing.assert_close(h1, norm(r1), rtol=0, atol=0)
+    r2 = torch.from_numpy(base.copy()).to(dev)
+    ops.q4_matmul(qw, xd, out=r2, epilogue=_lib.SM_EPI_ADD_F32, pair=True, workspace=ws)
+    if exact:
+        torch.testing.assert_close(r1, r2, rtol=0, atol=0)
+        torch.testing.assert_close(h1, norm(r2), rtol=0, atol=0)
+    dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+    expect = base + xr.astype(np.float64) @ dense.T
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-6
+    got = r1.cpu().numpy()
+    assert np.all(np.abs(got - expect) <= tol), float(np.abs(got - expect).max())
