@@ -643,7 +643,7 @@ int sm_model_set_prompt_groups(sm_model* model, int64_t group_size);
 
 /* Decode-step graphs (no counterpart in the reference; its decode loop is
  * generate.rs:101-121): with enable = 1 (the default), sm_rl_generate /
- * sm_rl_generate_ex (calls that trace MoE router decisions aside) run the
+ * sm_rl_generate_ex on a dense model (no MoE layers, no route trace) run the
  * first decode step eagerly, then capture one step's layer stack as a HIP
  * graph on a private stream and replay it on the caller's stream for every
  * later step, and for later calls of the same shape (re-captured when the

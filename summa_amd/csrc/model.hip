@@ -710,17 +710,16 @@ void release_bufs(sm_model* m) {
 // private stream as a HIP graph and each later step replays it on the
 // caller's stream: one launch instead of ~10 per layer, without the gaps
 // between dependent launches. The graph is kept across calls of the same
-// shape and re-captured when a buffer, the shape or the prefix moves. MoE
-// layers capture too (router, route plan, grouped matmuls and combine are
-// kernels over device-side plans); calls that trace router decisions run
-// eagerly, and so does everything if the capture fails.
+// shape and re-captured when a buffer, the shape or the prefix moves. Models
+// with MoE layers (route plans, traces) and traced calls run eagerly; so does
+// everything if the capture fails.
 int decode_step(sm_model* m, int64_t t, const int32_t* ids, int64_t S, const int32_t* pos,
                 const int32_t* lens, size_t layer_elems, int64_t cap, const PrefixKV* pre,
                 hipStream_t st) {
   auto eager = [&] {
     return run_layers(m, ids, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true, st, pre);
   };
-  if (!m->decode_graphs || m->trace_idx || t < 2) return eager();
+  if (!m->decode_graphs || m->cfg.experts > 0 || m->trace_idx || t < 2) return eager();
   const std::vector<uint64_t> key = {
       g_buf_epoch, (uint64_t)S, (uint64_t)layer_elems, (uint64_t)cap,
       (uint64_t)(uintptr_t)ids, (uint64_t)(uintptr_t)pos, (uint64_t)(uintptr_t)lens,
