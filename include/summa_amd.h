@@ -641,19 +641,6 @@ int sm_model_bind_workspace(sm_model* model, void* ws, int64_t bytes, int64_t S,
  * sm_model_bind_workspace, whose sizes depend on it. */
 int sm_model_set_prompt_groups(sm_model* model, int64_t group_size);
 
-/* Decode-step graphs (no counterpart in the reference; its decode loop is
- * generate.rs:101-121): with enable = 1 (the default), sm_rl_generate /
- * sm_rl_generate_ex on a dense model (no MoE layers, no route trace) run the
- * first decode step eagerly, then capture one step's layer stack as a HIP
- * graph on a private stream and replay it on the caller's stream for every
- * later step, and for later calls of the same shape (re-captured when the
- * shape, a workspace buffer or the prompt groups change; a failed capture
- * falls back to eager launches). Same kernels in the same order: the results
- * equal the eager ones bit for bit. enable = 0 launches every kernel. Both
- * synchronise the device. sm_model_decode_graph_launches: replays so far. */
-int sm_model_set_decode_graphs(sm_model* model, int enable);
-int64_t sm_model_decode_graph_launches(const sm_model* model);
-
 /* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout
  * the semantics of TextGenerator::generate, generate.rs:68-124, with no EOS):
  * prompts [S, P] int32 -> tokens [S, N] int32 and behavior_lp [S, N] f32

@@ -103,8 +103,6 @@ SIGNATURES: dict[str, tuple] = {
     "sm_rl_workspace_bytes": (i64, [vp, i64, i64, i64, i64]),
     "sm_model_bind_workspace": (i32, [vp, vp, i64, i64, i64, i64, i64]),
     "sm_model_set_prompt_groups": (i32, [vp, i64]),
-    "sm_model_set_decode_graphs": (i32, [vp, i32]),
-    "sm_model_decode_graph_launches": (i64, [vp]),
     "sm_rl_generate": (i32, [vp, vp, i64, i64, i64, f32, u64, vp, vp, vp]),
     "sm_rl_generate_ex": (i32, [vp, vp, i64, i64, i64, vp, u64, vp, vp, vp, vp]),
     "sm_completion_mask": (i32, [vp, i64, i64, vp, vp]),

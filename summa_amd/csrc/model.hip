@@ -86,13 +86,8 @@ struct DevBuf {
   bool fixed = false;
 };
 
-// Bumped whenever a workspace buffer moves (growth, release): cached decode
-// graphs hold the old addresses and are re-captured.
-uint64_t g_buf_epoch = 1;
-
 int ensure(DevBuf& b, size_t bytes) {
   if (b.n >= bytes) return SM_OK;
-  ++g_buf_epoch;
   SM_REQUIRE(!b.fixed,
              "the bound workspace holds %zu bytes for a buffer this call needs %zu of: query "
              "sm_rl_workspace_bytes for the larger shape and bind again",
@@ -292,15 +287,6 @@ struct sm_model {
   int32_t* trace_idx = nullptr;
   float* trace_logits = nullptr;
   int64_t trace_cap = 0, trace_used = 0, trace_dropped = 0;
-  // decode-step graphs (sm_model_set_decode_graphs): the layer stack of one
-  // decode step captured once and replayed; the key is everything the
-  // captured launches read from the host side
-  int decode_graphs = 1;
-  hipStream_t cap_stream = nullptr;
-  hipGraph_t dgraph = nullptr;
-  hipGraphExec_t dexec = nullptr;
-  std::vector<uint64_t> dkey;
-  int64_t dlaunches = 0;
 };
 
 namespace sm {
@@ -684,79 +670,13 @@ std::vector<DevBuf*> model_bufs(sm_model* m) {
           &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow, &m->apart};
 }
 
-void drop_decode_graph(sm_model* m) {  // callers have synchronised the device
-  if (m->dexec) hipGraphExecDestroy(m->dexec);
-  if (m->dgraph) hipGraphDestroy(m->dgraph);
-  m->dexec = nullptr;
-  m->dgraph = nullptr;
-  m->dkey.clear();
-}
-
 void release_bufs(sm_model* m) {
-  ++g_buf_epoch;
-  drop_decode_graph(m);
   for (DevBuf* b : model_bufs(m)) {
     if (b->p && !b->fixed) hipFree(b->p);
     *b = DevBuf{};
   }
   m->ws_base = nullptr;
   m->ws_bytes = 0;
-}
-
-// One cached decode step (the layer stack over S rows at decode step t). The
-// step's launches are the same every step of a generation: the positions and
-// lengths they read live in device memory (set before each step), so after a
-// first eager step (which sizes every buffer) the stack is captured once on a
-// private stream as a HIP graph and each later step replays it on the
-// caller's stream: one launch instead of ~10 per layer, without the gaps
-// between dependent launches. The graph is kept across calls of the same
-// shape and re-captured when a buffer, the shape or the prefix moves. Models
-// with MoE layers (route plans, traces) and traced calls run eagerly; so does
-// everything if the capture fails.
-int decode_step(sm_model* m, int64_t t, const int32_t* ids, int64_t S, const int32_t* pos,
-                const int32_t* lens, size_t layer_elems, int64_t cap, const PrefixKV* pre,
-                hipStream_t st) {
-  auto eager = [&] {
-    return run_layers(m, ids, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true, st, pre);
-  };
-  if (!m->decode_graphs || m->cfg.experts > 0 || m->trace_idx || t < 2) return eager();
-  const std::vector<uint64_t> key = {
-      g_buf_epoch, (uint64_t)S, (uint64_t)layer_elems, (uint64_t)cap,
-      (uint64_t)(uintptr_t)ids, (uint64_t)(uintptr_t)pos, (uint64_t)(uintptr_t)lens,
-      (uint64_t)(uintptr_t)m->kc.p, (uint64_t)(uintptr_t)m->vc.p,
-      (uint64_t)(uintptr_t)(pre ? pre->k : nullptr), (uint64_t)(uintptr_t)(pre ? pre->v : nullptr),
-      (uint64_t)(pre ? pre->layer_bytes : 0), (uint64_t)(pre ? pre->G : 0),
-      (uint64_t)(pre ? pre->P : 0)};
-  if (!m->dexec || m->dkey != key) {
-    if (m->dexec) {  // an earlier graph may still be in flight on some stream
-      SM_HIP(hipDeviceSynchronize());
-      drop_decode_graph(m);
-    }
-    if (!m->cap_stream) SM_HIP(hipStreamCreateWithFlags(&m->cap_stream, hipStreamNonBlocking));
-    if (hipStreamBeginCapture(m->cap_stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
-      (void)hipGetLastError();
-      m->decode_graphs = 0;
-      return eager();
-    }
-    const int s = run_layers(m, ids, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true,
-                             m->cap_stream, pre);
-    hipGraph_t g = nullptr;
-    const hipError_t ec = hipStreamEndCapture(m->cap_stream, &g);
-    hipGraphExec_t e = nullptr;
-    if (s != SM_OK || ec != hipSuccess || !g ||
-        hipGraphInstantiate(&e, g, nullptr, nullptr, 0) != hipSuccess) {
-      if (g) (void)hipGraphDestroy(g);
-      (void)hipGetLastError();
-      m->decode_graphs = 0;  // run this model eagerly from now on
-      return eager();
-    }
-    m->dgraph = g;
-    m->dexec = e;
-    m->dkey = key;
-  }
-  SM_HIP(hipGraphLaunch(m->dexec, st));
-  ++m->dlaunches;
-  return SM_OK;
 }
 
 // Largest size each buffer reaches in sm_rl_generate(_ex) of S rollouts with
@@ -883,7 +803,6 @@ extern "C" int sm_model_destroy(sm_model* m) {
   hipDeviceSynchronize();
   for (void* p : m->owned) hipFree(p);
   release_bufs(m);
-  if (m->cap_stream) hipStreamDestroy(m->cap_stream);
   delete m;
   return SM_OK;
 }
@@ -923,18 +842,6 @@ extern "C" int sm_model_bind_workspace(sm_model* m, void* ws, int64_t bytes, int
 }
 
 extern "C" int64_t sm_model_weight_bytes(const sm_model* m) { return m ? (int64_t)m->weight_bytes : 0; }
-
-extern "C" int sm_model_set_decode_graphs(sm_model* m, int enable) {
-  SM_REQUIRE(m, "sm_model_set_decode_graphs: null model");
-  SM_HIP(hipDeviceSynchronize());
-  drop_decode_graph(m);
-  m->decode_graphs = enable ? 1 : 0;
-  return SM_OK;
-}
-
-extern "C" int64_t sm_model_decode_graph_launches(const sm_model* m) {
-  return m ? m->dlaunches : -1;
-}
 
 extern "C" int sm_model_set_prompt_groups(sm_model* m, int64_t group_size) {
   SM_REQUIRE(m, "sm_model_set_prompt_groups: null model");
@@ -1185,8 +1092,8 @@ extern "C" int sm_rl_generate(sm_model* m, const int32_t* prompts, int64_t S, in
   // cached single-token steps
   for (int64_t t = 1; t < N; ++t) {
     set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, (int)(P + t - 1));
-    SM_TRY(decode_step(m, t, (const int32_t*)m->next_ids.p, S, pos, lens, layer_elems, cap,
-                       dpre.k ? &dpre : nullptr, st));
+    SM_TRY(run_layers(m, (const int32_t*)m->next_ids.p, S, 1, pos, lens, m->kc.p, m->vc.p,
+                      layer_elems, cap, true, st, dpre.k ? &dpre : nullptr));
     SM_TRY(head(m, (const float*)m->x.p, S, (float*)m->logits.p, st));
     SM_TRY(sm_sample((const float*)m->logits.p, S, c.vocab, c.vocab, temperature, seed, t,
                      tokens + t, N, behavior_lp ? behavior_lp + t : nullptr, N,
@@ -1273,7 +1180,8 @@ extern "C" int sm_rl_generate_ex(sm_model* m, const int32_t* prompts, int64_t S,
       }
     }
     set_positions_kernel<<<blocks_for(S), 256, 0, st>>>(pos, lens, (int)S, (int)(P + t - 1));
-    SM_TRY(decode_step(m, t, next, S, pos, lens, layer_elems, cap, dpre.k ? &dpre : nullptr, st));
+    SM_TRY(run_layers(m, next, S, 1, pos, lens, m->kc.p, m->vc.p, layer_elems, cap, true, st,
+                      dpre.k ? &dpre : nullptr));
     SM_TRY(head(m, (const float*)m->x.p, S, (float*)m->logits.p, st));
     SM_TRY(sample_ex_launch((const float*)m->logits.p, S, c.vocab, c.vocab, sp, seed, t, seen,
                             seen_ld, done, eos ? lengths : nullptr, eos ? done + S : nullptr,

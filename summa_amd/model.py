@@ -148,15 +148,6 @@ class Model:
         call("sm_model_set_prompt_groups", self._h, int(group_size))
         self.prompt_group = int(group_size)
 
-    def set_decode_graphs(self, enable: bool) -> None:
-        """sm_model_set_decode_graphs: replay each generation's decode steps
-        from a captured HIP graph (default on; same bits as eager launches)."""
-        call("sm_model_set_decode_graphs", self._h, int(bool(enable)))
-
-    def decode_graph_launches(self) -> int:
-        """sm_model_decode_graph_launches: decode steps replayed from a graph."""
-        return int(_lib.lib().sm_model_decode_graph_launches(self._h))
-
     def workspace_bytes(self, S: int, P: int, N: int, max_tokens_per_forward: int = 0) -> int:
         """sm_rl_workspace_bytes: device bytes the RL calls need for these shapes."""
         n = int(_lib.lib().sm_rl_workspace_bytes(self._h, S, P, N, int(max_tokens_per_forward)))

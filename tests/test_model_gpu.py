@@ -233,46 +233,3 @@ def test_prompt_groups_equal_per_rollout(dev, quantized, experts):
         grouped.generate(bad, N, temperature=1.0, seed=5)
     with pytest.raises(Exception, match="whole groups"):
         grouped.logprobs(prompts[:10], t1[:10])
-
-
-@pytest.mark.parametrize("quantized,groups", [(True, 4), (True, 1), (False, 1)])
-def test_decode_graphs_equal_eager(dev, quantized, groups):
-    """Decode-step graphs (sm_model_set_decode_graphs): generation replaying a
-    captured layer stack gives the eager launches' tokens and log-probs bit
-    for bit, over several calls that reuse the graph (same shape, with other
-    device work and host synchronisations between them) and re-capture it (a
-    new N, generate_ex, a new batch size); the eager model replays nothing."""
-    from summa_amd.sampling import SamplingConfig
-    print(f"case decode graphs quantized={quantized} groups={groups}", flush=True)
-    cfg = ModelConfig(layers=3, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
-                      vocab=1024, max_seq=96, quantized=quantized)
-    graph, eager = Model(cfg), Model(cfg)
-    for m in (graph, eager):
-        m.init_random(23, std=0.05)
-        m.set_prompt_groups(groups)
-    eager.set_decode_graphs(False)
-    gen = torch.Generator().manual_seed(5)
-    P = 24
-
-    def prompts(S):
-        base = torch.randint(0, cfg.vocab, (S // groups, P), generator=gen, dtype=torch.int32)
-        return base.repeat_interleave(groups, 0).to(dev)
-
-    calls = [(8, 20, 1), (8, 20, 2), (8, 33, 3), (12, 20, 4)]  # (S, N, seed)
-    for S, N, seed in calls:
-        pr = prompts(S)
-        t1, l1 = graph.generate(pr, N, temperature=1.0, seed=seed)
-        t2, l2 = eager.generate(pr, N, temperature=1.0, seed=seed)
-        assert torch.equal(t1, t2), (S, N)
-        assert torch.equal(l1, l2), (S, N)
-        lp = graph.logprobs(pr, t1)  # other device work between the replays
-        torch.cuda.synchronize()
-        assert torch.isfinite(lp).all()
-    sc = SamplingConfig(max_new_tokens=20, temperature=0.7, top_k=40, repetition_penalty=1.2,
-                        seed=3)
-    pr = prompts(8)
-    e1, e2 = graph.generate_ex(pr, sc), eager.generate_ex(pr, sc)
-    for a, b in zip(e1, e2):
-        assert torch.equal(a, b)
-    assert graph.decode_graph_launches() > 0
-    assert eager.decode_graph_launches() == 0
