@@ -123,17 +123,16 @@ def decode_bytes(wl, shared_prompt: bool = True) -> float:
 def recompute_gemm(wl, dev, reps: int = 10) -> dict:
     """The dominant kernel of the config[2] step: the FFN-in projection of the
     log-prob recompute (SwiGLU f16-pair epilogue) at the shape of its
-    continuation chunks (prompt groups: a chunk is 65536 // (P + N - 1) = 64
+    continuation chunks (prompt groups: a chunk is 65536 // (N - 1) = 128
     rollouts of N - 1 = 511 continuation rows over the group's prompt K / V),
-    M = 32704, N = 2F = 11264, K = 2048, on the wide-tile kernel.
+    M = 65408, N = 2F = 11264, K = 2048, on the wide-tile kernel.
     flops = 2 M N K per launch."""
     import torch
 
     from summa_amd import _lib, ops
 
     m = wl.model
-    L = wl.prompt_len + wl.new_tokens - 1
-    M = max(1, 65536 // L) * (wl.new_tokens - 1)
+    M = max(1, 65536 // (wl.new_tokens - 1)) * (wl.new_tokens - 1)
     N, K = 2 * m["ffn"], m["d_model"]
     w = torch.empty(N, K, device=dev)
     ops.fill_normal(w, 0.0, 0.02, seed=5)

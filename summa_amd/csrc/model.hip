@@ -421,6 +421,12 @@ struct PrefixKV {
   int64_t s0;
 };
 
+// Rollouts per continuation chunk of the grouped recompute: as many whole
+// rollouts as keep their N - 1 new rows within the token budget.
+int64_t grouped_chunk(int64_t budget, int64_t N) {
+  return std::max<int64_t>(1, budget / std::max<int64_t>(N - 1, 1));
+}
+
 // Whether decode attention reads a group's prompt K / V in place
 // (sm_attn_decode_prefix) instead of per-rollout copies: 16-bit caches with
 // f16-pair attention output (the quantized models), at most 32 query heads per
@@ -772,6 +778,15 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
     plan_max(at(m->pkc), prefix);
     plan_max(at(m->pvc), prefix);
     plan_max(at(m->prow), (size_t)groups * d * 4);
+    // continuation chunks: cc rollouts x (N - 1) rows (within the budget, so
+    // covered by layers(rows) above) over a K / V buffer of cc x L positions
+    const int64_t cc = std::min(S, grouped_chunk(budget, N));
+    plan_max(at(m->rkc), (size_t)cc * c.kv_heads * L * c.head_dim * m->kv_size);
+    plan_max(at(m->rvc), (size_t)cc * c.kv_heads * L * c.head_dim * m->kv_size);
+    plan_max(at(m->ids), (size_t)cc * (N - 1) * 4);
+    plan_max(at(m->rows), (size_t)cc * N * d * 4);
+    plan_max(at(m->pos), (size_t)cc * 4);
+    plan_max(at(m->lens), (size_t)cc * 4);
     if (prefix_attention(m, S))
       plan_max(at(m->apart), (size_t)sm_attn_decode_prefix_workspace_bytes(
                                  S, G, P, c.heads, c.kv_heads, c.head_dim));
@@ -1225,6 +1240,9 @@ int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens,
   const int64_t G = m->prompt_group, L = P + N - 1;
   SM_TRY(check_prompt_groups(m, prompts, S, P, st));
   const int64_t groups = S / G;
+  // continuations in chunks of whole rollouts whose N - 1 new rows fit the
+  // token budget (the prompt rows come from the group's prompt K / V)
+  chunk = grouped_chunk(budget, N);
   const size_t pl = (size_t)groups * c.kv_heads * P * c.head_dim;  // elements per layer
   SM_TRY(ensure(m->pkc, pl * c.layers * m->kv_size));
   SM_TRY(ensure(m->pvc, pl * c.layers * m->kv_size));
