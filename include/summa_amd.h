@@ -636,9 +636,12 @@ int sm_model_bind_workspace(sm_model* model, void* ws, int64_t bytes, int64_t S,
  * K / V to the group's rollouts: the same values as per rollout, since a
  * prompt position depends on the prompt alone. Each call checks on the device
  * that S is whole groups and every prompt row equals its group's first (one
- * host synchronisation; SM_ERR_INVALID otherwise). 1 (the default) computes
- * every rollout's prompt. Set it before sm_rl_workspace_bytes /
- * sm_model_bind_workspace, whose sizes depend on it. */
+ * host synchronisation; SM_ERR_INVALID otherwise). A grouped recompute whose
+ * prompts, weights and buffers equal those of the model's last grouped prompt
+ * pass (a generation's prefill, or a recompute) reuses that pass's K / V and
+ * last rows instead of computing them again (the same values). 1 (the
+ * default) computes every rollout's prompt. Set it before sm_rl_workspace_bytes
+ * / sm_model_bind_workspace, whose sizes depend on it. */
 int sm_model_set_prompt_groups(sm_model* model, int64_t group_size);
 
 /* Batched rollouts (generate_device_batch, posttrain.rs:1191-1216; per rollout

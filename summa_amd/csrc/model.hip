@@ -86,8 +86,13 @@ struct DevBuf {
   bool fixed = false;
 };
 
+// Bumped whenever a workspace buffer moves (growth, release): a cached
+// prompt state whose buffers may have moved is then recomputed.
+uint64_t g_buf_epoch = 1;
+
 int ensure(DevBuf& b, size_t bytes) {
   if (b.n >= bytes) return SM_OK;
+  ++g_buf_epoch;
   SM_REQUIRE(!b.fixed,
              "the bound workspace holds %zu bytes for a buffer this call needs %zu of: query "
              "sm_rl_workspace_bytes for the larger shape and bind again",
@@ -172,12 +177,17 @@ __global__ void zero_i32_kernel(int32_t* p, int n) {
 // ---- prompt groups: G consecutive rollouts share one prompt
 // flag[0] = 1 where a prompt row differs from its group's first row (every
 // writer stores the same value)
+// flag[0] = 1 if a prompt row differs from its group's first; with cached
+// ([groups, P] ids of the prompt state), flag[1] = 1 if a group's prompt
+// differs from the cached one.
 __global__ void check_groups_kernel(const int32_t* __restrict__ prompts, int64_t S, int G, int P,
+                                    const int32_t* __restrict__ cached,
                                     int32_t* __restrict__ flag) {
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (i >= S * P) return;
   const int64_t s = i / P, t = i % P;
   if (prompts[i] != prompts[(s / G) * G * P + t]) flag[0] = 1;
+  if (cached && prompts[i] != cached[(s / G) * P + t]) flag[1] = 1;
 }
 
 // out [groups, P] <- prompt row g * G
@@ -276,6 +286,15 @@ struct sm_model {
   // every layer [layers][groups][KVH][P][hd] and last hidden rows [groups, d]
   int64_t prompt_group = 1;
   sm::DevBuf pkc, pvc, prow;
+  // the grouped prompt pass last computed (by a generation's prefill or a
+  // recompute): its group prompt ids [groups, P] (pids), K / V (pkc, pvc) and
+  // last hidden rows (prow) serve a later grouped recompute of the same
+  // prompts with the same weights and buffers, which then skips its prompt pass
+  sm::DevBuf pids;
+  bool pstate_valid = false;
+  uint64_t pstate_weights = 0, pstate_epoch = 0;
+  int64_t pstate_groups = 0, pstate_G = 0, pstate_P = 0;
+  uint64_t weights_version = 1;  // bumped by every weight write
   // partials of the shared-prompt decode attention (sm_attn_decode_prefix)
   sm::DevBuf apart;
   int64_t gen_cap = 0, gen_S = 0;
@@ -517,20 +536,49 @@ int head(sm_model* m, const float* xrows, int64_t M, float* logits, hipStream_t 
 
 // Prompt groups: S must be whole groups of G and every prompt row equal to
 // its group's first (checked on the device; one host synchronisation).
+// Whether the model's prompt state was computed for groups of G x P with the
+// current weights and buffers (its prompts still to be compared).
+bool pstate_matches(const sm_model* m, int64_t groups, int64_t P) {
+  return m->pstate_valid && m->pstate_weights == m->weights_version &&
+         m->pstate_epoch == g_buf_epoch && m->pstate_groups == groups &&
+         m->pstate_G == m->prompt_group && m->pstate_P == P;
+}
+
+// Prompt groups: S must be whole groups of G and every prompt row equal to
+// its group's first (checked on the device; one host synchronisation). With
+// cached_out, also whether the prompts are those of the model's prompt state.
 int check_prompt_groups(sm_model* m, const int32_t* prompts, int64_t S, int64_t P,
-                        hipStream_t st) {
+                        hipStream_t st, bool* cached_out = nullptr) {
   const int64_t G = m->prompt_group;
   SM_REQUIRE(S % G == 0, "prompt groups of %lld: %lld rollouts are not whole groups",
              (long long)G, (long long)S);
-  SM_TRY(ensure(m->flags, 4));
+  const bool cmp = cached_out && pstate_matches(m, S / G, P);
+  SM_TRY(ensure(m->flags, 8));
   int32_t* f = (int32_t*)m->flags.p;
-  zero_i32_kernel<<<1, 64, 0, st>>>(f, 1);
-  check_groups_kernel<<<blocks_for(S * P), 256, 0, st>>>(prompts, S, (int)G, (int)P, f);
-  int32_t bad = 0;
-  SM_HIP(hipMemcpyAsync(&bad, f, 4, hipMemcpyDeviceToHost, st));
+  zero_i32_kernel<<<1, 64, 0, st>>>(f, 2);
+  check_groups_kernel<<<blocks_for(S * P), 256, 0, st>>>(
+      prompts, S, (int)G, (int)P, cmp ? (const int32_t*)m->pids.p : nullptr, f);
+  int32_t bad[2] = {0, 0};
+  SM_HIP(hipMemcpyAsync(bad, f, 8, hipMemcpyDeviceToHost, st));
   SM_HIP(hipStreamSynchronize(st));
-  SM_REQUIRE(bad == 0, "prompt groups of %lld: a rollout's prompt differs from its group's first",
+  SM_REQUIRE(bad[0] == 0, "prompt groups of %lld: a rollout's prompt differs from its group's first",
              (long long)G);
+  if (cached_out) *cached_out = cmp && bad[1] == 0;
+  return SM_OK;
+}
+
+// Record the grouped prompt pass just computed (group prompt ids in ids
+// [groups, P], K / V in pkc / pvc, last rows in prow) as the prompt state.
+int record_pstate(sm_model* m, const int32_t* ids, int64_t groups, int64_t P, hipStream_t st) {
+  m->pstate_valid = false;
+  SM_TRY(ensure(m->pids, (size_t)groups * P * 4));
+  SM_HIP(hipMemcpyAsync(m->pids.p, ids, (size_t)groups * P * 4, hipMemcpyDeviceToDevice, st));
+  m->pstate_valid = true;
+  m->pstate_weights = m->weights_version;
+  m->pstate_epoch = g_buf_epoch;
+  m->pstate_groups = groups;
+  m->pstate_G = m->prompt_group;
+  m->pstate_P = P;
   return SM_OK;
 }
 
@@ -557,6 +605,7 @@ int prefill_prompts(sm_model* m, const int32_t* prompts, int64_t S, int64_t P, i
   const size_t pl = (size_t)groups * c.kv_heads * P * c.head_dim;  // elements per layer
   SM_TRY(ensure(m->pkc, pl * c.layers * m->kv_size));
   SM_TRY(ensure(m->pvc, pl * c.layers * m->kv_size));
+  SM_TRY(ensure(m->prow, (size_t)groups * c.d_model * 4));
   SM_TRY(ensure(m->ids, (size_t)groups * P * 4));
   int32_t* ids = (int32_t*)m->ids.p;
   group_prompts_kernel<<<blocks_for(groups * P), 256, 0, st>>>(prompts, groups, (int)G, (int)P,
@@ -573,6 +622,10 @@ int prefill_prompts(sm_model* m, const int32_t* prompts, int64_t S, int64_t P, i
         (int64_t)(layer_elems * m->kv_size));
   gather_group_rows_kernel<<<blocks_for(S * c.d_model), 256, 0, st>>>(
       (const float*)m->x.p, S, (int)G, (int)P, (int)P - 1, c.d_model, (float*)m->rows.p);
+  // the same prompt pass as a recompute's (one chunk of all groups): kept for it
+  gather_rows_kernel<<<blocks_for(groups * c.d_model), 256, 0, st>>>(
+      (const float*)m->x.p, (int)groups, (int)P, (int)P - 1, c.d_model, (float*)m->prow.p);
+  if (!m->trace_idx) SM_TRY(record_pstate(m, ids, groups, P, st));
   return SM_OK;
 }
 
@@ -673,10 +726,13 @@ std::vector<DevBuf*> model_bufs(sm_model* m) {
   return {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits, &m->rows,
           &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc, &m->rkc, &m->rvc,
           &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w, &m->moe_plan, &m->moe_u, &m->moe_y,
-          &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow, &m->apart};
+          &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow, &m->apart,
+          &m->pids};
 }
 
 void release_bufs(sm_model* m) {
+  ++g_buf_epoch;
+  m->pstate_valid = false;
   for (DevBuf* b : model_bufs(m)) {
     if (b->p && !b->fixed) hipFree(b->p);
     *b = DevBuf{};
@@ -778,6 +834,7 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
     plan_max(at(m->pkc), prefix);
     plan_max(at(m->pvc), prefix);
     plan_max(at(m->prow), (size_t)groups * d * 4);
+    plan_max(at(m->pids), (size_t)groups * P * 4);
     // continuation chunks: cc rollouts x (N - 1) rows (within the budget, so
     // covered by layers(rows) above) over a K / V buffer of cc x L positions
     const int64_t cc = std::min(S, grouped_chunk(budget, N));
@@ -796,7 +853,7 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
     plan_max(at(m->ids), (size_t)std::max(groups * P, prow_rows) * 4);
     plan_max(at(m->pos), (size_t)groups * 4);
     plan_max(at(m->lens), (size_t)groups * 4);
-    plan_max(at(m->flags), 4);
+    plan_max(at(m->flags), 8);
   }
   return plan;
 }
@@ -930,6 +987,7 @@ __global__ void f32_to_bf16_kernel(const float* __restrict__ a, int64_t n, uint1
 extern "C" int sm_model_set_tensor(sm_model* m, int kind, int layer, const float* src,
                                    void* stream) {
   SM_REQUIRE(m && src, "sm_model_set_tensor: null argument");
+  ++m->weights_version;  // a cached prompt pass is stale from here
   Linear* lin;
   void* dense;
   int64_t n, count;
@@ -984,6 +1042,7 @@ int hquant_decode_device(const sm_hquant* t, float* out, int transpose, hipStrea
 extern "C" int sm_model_load_packed(sm_model* m, int kind, int layer, const sm_hquant* t,
                                     int layout, void* stream) {
   SM_REQUIRE(m && t && t->scales && t->codes, "sm_model_load_packed: null argument");
+  ++m->weights_version;  // a cached prompt pass is stale from here
   SM_REQUIRE(layout == 0 || layout == 1,
              "sm_model_load_packed: layout must be 0 ([out, in]) or 1 ([in, out])");
   Linear* lin;
@@ -1025,6 +1084,7 @@ extern "C" int sm_model_load_packed(sm_model* m, int kind, int layer, const sm_h
 
 extern "C" int sm_model_init_random(sm_model* m, uint64_t seed, float std, void* stream) {
   SM_REQUIRE(m, "sm_model_init_random: null model");
+  ++m->weights_version;  // a cached prompt pass is stale from here
   hipStream_t st = as_stream(stream);
   const auto& c = m->cfg;
   int64_t maxn = (int64_t)c.vocab * c.d_model;
@@ -1238,7 +1298,8 @@ int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens,
                      hipStream_t st) {
   const auto& c = m->cfg;
   const int64_t G = m->prompt_group, L = P + N - 1;
-  SM_TRY(check_prompt_groups(m, prompts, S, P, st));
+  bool cached = false;
+  SM_TRY(check_prompt_groups(m, prompts, S, P, st, &cached));
   const int64_t groups = S / G;
   // continuations in chunks of whole rollouts whose N - 1 new rows fit the
   // token budget (the prompt rows come from the group's prompt K / V)
@@ -1249,11 +1310,16 @@ int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens,
   SM_TRY(ensure(m->prow, (size_t)groups * c.d_model * 4));
   SM_TRY(ensure(m->pos, (size_t)std::max(groups, std::min(chunk, S)) * 4));
   SM_TRY(ensure(m->lens, (size_t)std::max(groups, std::min(chunk, S)) * 4));
+  cached = cached && m->pstate_epoch == g_buf_epoch;  // no buffer moved since the check
   int32_t* pos = (int32_t*)m->pos.p;
   int32_t* lens = (int32_t*)m->lens.p;
-  // prompts, once per group, in chunks of whole prompts within the budget
+  // prompts, once per group, in chunks of whole prompts within the budget;
+  // skipped when the model's prompt state holds these prompts' pass (the same
+  // single-chunk pass, so the same values), e.g. from the generation that
+  // produced the tokens
   const int64_t gchunk = std::max<int64_t>(1, budget / P);
-  for (int64_t g0 = 0; g0 < groups; g0 += gchunk) {
+  const bool one_chunk = gchunk >= groups && !m->trace_idx;
+  for (int64_t g0 = 0; g0 < groups && !(cached && one_chunk); g0 += gchunk) {
     const int64_t gc = std::min(gchunk, groups - g0);
     SM_TRY(ensure(m->ids, (size_t)gc * P * 4));
     int32_t* ids = (int32_t*)m->ids.p;
@@ -1266,6 +1332,7 @@ int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens,
     gather_rows_kernel<<<blocks_for(gc * c.d_model), 256, 0, st>>>(
         (const float*)m->x.p, (int)gc, (int)P, (int)P - 1, c.d_model,
         (float*)m->prow.p + g0 * c.d_model);
+    if (one_chunk) SM_TRY(record_pstate(m, ids, groups, P, st));
   }
   // continuations, in chunks of rollouts
   const PrefixKV pre0{m->pkc.p, m->pvc.p, (int64_t)(pl * m->kv_size), (int)G, (int)P, 0};

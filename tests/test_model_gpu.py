@@ -233,3 +233,45 @@ def test_prompt_groups_equal_per_rollout(dev, quantized, experts):
         grouped.generate(bad, N, temperature=1.0, seed=5)
     with pytest.raises(Exception, match="whole groups"):
         grouped.logprobs(prompts[:10], t1[:10])
+
+
+@pytest.mark.parametrize("quantized,experts", [(True, 0), (False, 0), (True, 8)])
+def test_prompt_state_reuse(dev, quantized, experts):
+    """A grouped recompute reuses the prompt pass of the generation (or
+    recompute) before it when the prompts, the weights and the buffers are
+    the same, and recomputes it otherwise: every result equals a fresh
+    model's recompute bit for bit: after generating, for other prompts, for
+    the first prompts again, after a weight change, with a budget that splits
+    the prompt pass."""
+    print(f"case prompt state reuse quantized={quantized} experts={experts}", flush=True)
+    kw = dict(experts=experts, expert_ffn=256) if experts else {}
+    cfg = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
+                      vocab=1024, max_seq=64, quantized=quantized, **kw)
+    a, b = Model(cfg), Model(cfg)
+    for m in (a, b):
+        m.init_random(29, std=0.05)
+        m.set_prompt_groups(4)
+    gen = torch.Generator().manual_seed(8)
+    P, N = 24, 10
+
+    def prompts():
+        base = torch.randint(0, cfg.vocab, (3, P), generator=gen, dtype=torch.int32)
+        return base.repeat_interleave(4, 0).to(dev)
+
+    p1, p2 = prompts(), prompts()
+    tok, _ = a.generate(p1, N, temperature=1.0, seed=2)
+
+    def same(prm, what, budget=0):
+        la = a.logprobs(prm, tok, max_tokens_per_forward=budget)
+        lb = b.logprobs(prm, tok, max_tokens_per_forward=budget)
+        assert torch.equal(la, lb), what
+
+    same(p1, "after the generation")
+    same(p1, "again")
+    same(p2, "other prompts")
+    same(p1, "the first prompts again")
+    a.generate(p1, N, temperature=1.0, seed=3)
+    for m in (a, b):
+        m.init_random(31, std=0.05)  # new weights: the generation's prompt pass is stale
+    same(p1, "after a weight change")
+    same(p1, "prompt pass in chunks", budget=30)
