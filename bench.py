@@ -84,21 +84,24 @@ def q4_bytes(n: int, k: int) -> int:
     return n * k // 2 + n * k // 128 * 2  # 4-bit codes + one bf16 scale per 128
 
 
-def recompute_flops(wl) -> float:
+def recompute_flops(wl, prompt_pass: bool = True) -> float:
     """Algorithmic flops of one model's log-prob recompute of S = prompts x
     group rollouts of P + N - 1 positions, where a group's rollouts share one
     prompt (GRPO), so its P prompt positions are computed once per group:
     2 * tokens * per-layer linear params over prompts * P + S * (N - 1) token
     rows, the LM head over the S * N scored rows, causal attention (Q.K^T and
     P.V over the lower triangle: the prompt's triangle once per group, the
-    completion rows' keys per rollout)."""
+    completion rows' keys per rollout). prompt_pass=False leaves out the prompt
+    rows and their triangle: the policy's recompute reuses the prompt pass of
+    the generation that produced the tokens."""
     m = wl.model
     P, N, S = wl.prompt_len, wl.new_tokens, wl.rollouts
     L = P + N - 1
-    tokens = wl.prompts * P + S * (N - 1)
+    pp = 1 if prompt_pass else 0
+    tokens = pp * wl.prompts * P + S * (N - 1)
     lin = sum(n * k for n, k in linear_shapes(m)) * m["layers"]
     head = m["vocab"] * m["d_model"]
-    keys = wl.prompts * P * (P + 1) / 2 + S * (L * (L + 1) / 2 - P * (P + 1) / 2)
+    keys = pp * wl.prompts * P * (P + 1) / 2 + S * (L * (L + 1) / 2 - P * (P + 1) / 2)
     attn = 4 * m["head_dim"] * keys * m["heads"] * m["layers"]
     return 2.0 * tokens * lin + 2.0 * S * N * head + attn
 
@@ -540,7 +543,9 @@ def bench_rl_step(args) -> dict:
     pre_ms = prefill_ms(wl, policy, prompts)
     dec_ms = r_ms - pre_ms
     dec_bytes = decode_bytes(wl)
-    rec_flops = 2 * recompute_flops(wl)  # policy + frozen reference
+    # the frozen reference's full recompute + the policy's without its prompt
+    # pass (reused from the generation, sm_model_set_prompt_groups)
+    rec_flops = recompute_flops(wl) + recompute_flops(wl, prompt_pass=False)
     prep_ms = f_ms - r_ms
     line = {
         "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
