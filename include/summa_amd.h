@@ -416,6 +416,14 @@ int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t e
                          int epilogue, void* stream);
 int sm_moe_combine(const float* routed, const float* top_w, const int32_t* plan, int64_t tokens,
                    int64_t top_k, int64_t experts, int64_t d, float* x, void* stream);
+/* The combine and the next RMSNorm (block.rs: x = x + MoE(h); h = RMSNorm(x) *
+ * gamma, norm.rs:36-50): x as sm_moe_combine, then h_out [tokens, 2d] f16
+ * pairs (SM_F16X2 rows) = RMSNorm(x) * gamma as sm_rmsnorm, in one launch for
+ * d a multiple of 256 up to 4096 (the two steps otherwise); the same results
+ * as the two calls. */
+int sm_moe_combine_rmsnorm(const float* routed, const float* top_w, const int32_t* plan,
+                           int64_t tokens, int64_t top_k, int64_t experts, int64_t d, float* x,
+                           const float* gamma, float eps, void* h_out, void* stream);
 
 /* MoE training kernels (route_gather_* / route_combine_*,
  * summa-llm/src/model/moe_dispatch.rs:244-384; swiglu_forward / _backward,

@@ -71,6 +71,7 @@ SIGNATURES: dict[str, tuple] = {
     "sm_q4_grouped_matmul": (i32, [vp, vp, i64, i64, i64, vp, i32, i64, i32, vp, i64, i64, vp, i64,
                                    i32, vp]),
     "sm_moe_combine": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
+    "sm_moe_combine_rmsnorm": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp, f32, vp, vp]),
     "sm_moe_gather": (i32, [vp, i32, vp, i64, i64, i64, i64, vp, vp]),
     "sm_moe_gather_backward": (i32, [vp, i32, vp, i64, i64, i64, i64, vp, vp]),
     "sm_moe_combine_backward": (i32, [vp, vp, i32, vp, vp, i64, i64, i64, i64, vp, vp, vp]),

@@ -219,6 +219,39 @@ __device__ inline void split_f16(float x, _Float16& hi, _Float16& lo) {
   lo = (_Float16)(x - (float)hi);
 }
 
+// The RMSNorm of one row of D = 256 * V columns written as f16 pairs, with
+// one workgroup per row: wave i holds float4 i * 64 + lane (v) and gamma (g).
+// The squares meet in LDS (sq [V][64]) so that wave 0 sums them in the order
+// of a one-wave-per-row norm (lane l over float4s l, 64 + l, ... then one wave
+// reduction); then x / rms * gamma, split into hi | lo halves of the row.
+template <int V>
+__device__ inline void row_rmsnorm_pair(const float4& v, const float4& g, float eps,
+                                        float4 (&sq)[V][64], float& rms_s, _Float16* row) {
+  constexpr int D = 256 * V;
+  const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
+  const int c4 = wave * 64 + lane;
+  sq[wave][lane] = v;
+  __syncthreads();
+  if (wave == 0) {
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < V; ++i) {
+      const float4 t = sq[i][lane];
+      ss = fmaf(t.w, t.w, fmaf(t.z, t.z, fmaf(t.y, t.y, fmaf(t.x, t.x, ss))));
+    }
+    ss = wave_sum(ss);
+    if (lane == 0) rms_s = sqrtf(ss / (float)D + eps);
+  }
+  __syncthreads();
+  const float rms = rms_s;
+  const float o[4] = {v.x / rms * g.x, v.y / rms * g.y, v.z / rms * g.z, v.w / rms * g.w};
+  _Float16 hi[4], lo[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) split_f16(o[e], hi[e], lo[e]);
+  *reinterpret_cast<h4*>(row + 4 * c4) = h4{hi[0], hi[1], hi[2], hi[3]};
+  *reinterpret_cast<h4*>(row + D + 4 * c4) = h4{lo[0], lo[1], lo[2], lo[3]};
+}
+
 // One prepared word -> its 8 codes q in natural k order as f16. Each 16-bit
 // half becomes 1024 + u (or 1024 + 16u) by OR-ing the nibble into the
 // mantissa of 0x6400; one packed add / fma removes the bias. 9 VALU ops: each

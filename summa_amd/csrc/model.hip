@@ -48,6 +48,8 @@ int sm_attn_decode(const void*, const void*, const void*, const int32_t*, void*,
                    int64_t, int64_t, int64_t, int64_t, int64_t, void*);
 int sm_attn_prefill(const void*, const void*, const void*, const int32_t*, void*, int, int,
                     int64_t, int64_t, int64_t, int64_t, int64_t, int64_t, void*);
+int sm_moe_combine_rmsnorm(const float*, const float*, const int32_t*, int64_t, int64_t, int64_t,
+                           int64_t, float*, const float*, float, void*, void*);
 int sm_q4_matmul_add_rmsnorm(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*, int,
                              int64_t, int64_t, float*, const float*, float, void*, void*, int64_t,
                              void*);
@@ -383,8 +385,11 @@ int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* 
 }
 
 // x += MoE(h) for `rows` tokens: router + top-2, route plan, two grouped Q4
-// matmuls (gathered SwiGLU in, down), combine. All device side.
-int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st) {
+// matmuls (gathered SwiGLU in, down), combine. All device side. With
+// next_norm, the combine also leaves RMSNorm(x) * next_norm in m->h (the next
+// layer's attention norm, one launch).
+int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st,
+            const float* next_norm = nullptr) {
   const auto& c = m->cfg;
   const int64_t E = c.experts, Fe = c.expert_ffn, d = c.d_model, k = 2;
   const int64_t routes = rows * k;
@@ -419,8 +424,14 @@ int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st) {
   SM_TRY(sm_q4_grouped_matmul(Ly.exp_down.codes, Ly.exp_down.scales, E, d, Fe, m->moe_u.p,
                               m->act, m->act_ld(Fe), 0, plan, rows, k, m->moe_y.p, d,
                               SM_EPI_STORE_F32, st));
-  return sm_moe_combine((const float*)m->moe_y.p, (const float*)m->moe_w.p, plan, rows, k, E, d,
-                        (float*)m->x.p, st);
+  if (next_norm && m->act == SM_F16X2)
+    return sm_moe_combine_rmsnorm((const float*)m->moe_y.p, (const float*)m->moe_w.p, plan, rows,
+                                  k, E, d, (float*)m->x.p, next_norm, c.norm_eps, m->h.p, st);
+  SM_TRY(sm_moe_combine((const float*)m->moe_y.p, (const float*)m->moe_w.p, plan, rows, k, E, d,
+                        (float*)m->x.p, st));
+  return next_norm ? sm_rmsnorm((const float*)m->x.p, next_norm, rows, d, c.norm_eps, m->h.p,
+                                m->act, st)
+                   : SM_OK;
 }
 
 size_t cache_layer_elems(const sm_model* m, int64_t S, int64_t cap) {
@@ -512,8 +523,13 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
       SM_TRY(sm_attn_prefill(m->qb.p, kl, vl, pos0, m->attn.p, m->kvt, m->act, S, L, c.heads,
                              c.kv_heads, cap, c.head_dim, st));
     SM_TRY(linear_add_norm(m, Ly.o, m->attn.p, rows, x, Ly.ffn_norm, st));
-    if (c.experts > 0) {
-      SM_TRY(moe_ffn(m, Ly, rows, st));
+    if (c.experts > 0) {  // the combine with the next layer's attention norm
+      if (l + 1 < c.layers) {
+        SM_TRY(moe_ffn(m, Ly, rows, st, m->layers[l + 1].attn_norm));
+        normed = true;
+      } else {
+        SM_TRY(moe_ffn(m, Ly, rows, st));
+      }
     } else {
       SM_TRY(linear_swiglu(m, Ly.in, m->h.p, rows, m->u.p, st));
       if (l + 1 < c.layers) {  // the down projection with the next layer's attention norm

@@ -369,10 +369,90 @@ __global__ void combine_kernel(const float* __restrict__ routed, const float* __
   x[i] += sum;
 }
 
+// combine_kernel's sum for one token row (its routes in order, x += sum),
+// then the next RMSNorm of the row as f16 pairs (row_rmsnorm_pair): one
+// workgroup per token, wave i owning float4s i * 64 + lane of the row.
+template <int V>
+__global__ __launch_bounds__(64 * V) void combine_rmsnorm_kernel(
+    const float* __restrict__ routed, const float* __restrict__ w,
+    const int32_t* __restrict__ inverse, int64_t tokens, int k, float* __restrict__ x,
+    const float* __restrict__ gamma, float eps, _Float16* __restrict__ h) {
+  constexpr int D = 256 * V;
+  __shared__ float4 sq[V][64];
+  __shared__ float rms_s;
+  const int64_t t = blockIdx.x;
+  const int c4 = threadIdx.x;
+  const int64_t routes = tokens * k;
+  float4 sum = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int j = 0; j < k; ++j) {
+    const int64_t route = t * k + j;
+    const int p = inverse[route];
+    if (p >= 0 && p < routes) {
+      const float4 r4 = reinterpret_cast<const float4*>(routed + (int64_t)p * D)[c4];
+      const float wj = w[route];
+      sum.x += r4.x * wj;
+      sum.y += r4.y * wj;
+      sum.z += r4.z * wj;
+      sum.w += r4.w * wj;
+    }
+  }
+  float4* xr = reinterpret_cast<float4*>(x + t * D) + c4;
+  const float4 x4 = *xr;
+  const float4 v = make_float4(x4.x + sum.x, x4.y + sum.y, x4.z + sum.z, x4.w + sum.w);
+  *xr = v;
+  row_rmsnorm_pair<V>(v, reinterpret_cast<const float4*>(gamma)[c4], eps, sq, rms_s,
+                      h + t * 2 * D);
+}
+
 }  // namespace
 }  // namespace sm
 
 using namespace sm;
+
+extern "C" int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int64_t d, float eps,
+                          void* y, int out_dtype, void* stream);
+extern "C" int sm_moe_combine(const float* routed, const float* top_w, const int32_t* plan,
+                              int64_t tokens, int64_t top_k, int64_t experts, int64_t d, float* x,
+                              void* stream);
+
+extern "C" int sm_moe_combine_rmsnorm(const float* routed, const float* top_w,
+                                      const int32_t* plan, int64_t tokens, int64_t top_k,
+                                      int64_t experts, int64_t d, float* x, const float* gamma,
+                                      float eps, void* h_out, void* stream) {
+  SM_REQUIRE(routed && top_w && plan && x && gamma && h_out,
+             "sm_moe_combine_rmsnorm: null buffer");
+  SM_REQUIRE(tokens >= 0 && top_k >= 1 && d > 0, "sm_moe_combine_rmsnorm: bad shape");
+  if (tokens == 0) return SM_OK;
+  const int64_t v = d / 256;
+  const bool fused = d % 256 == 0 && (v == 3 || v == 4 || v == 8 || v == 12 || v == 16) &&
+                     tokens <= 0x7fffffff && reinterpret_cast<uintptr_t>(routed) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
+                     reinterpret_cast<uintptr_t>(h_out) % 8 == 0;
+  if (!fused) {  // the two steps
+    SM_TRY(sm_moe_combine(routed, top_w, plan, tokens, top_k, experts, d, x, stream));
+    return sm_rmsnorm(x, gamma, tokens, d, eps, h_out, SM_F16X2, stream);
+  }
+  PlanView pv = plan_view(const_cast<int32_t*>(plan), tokens * top_k, experts);
+  hipStream_t st = as_stream(stream);
+  _Float16* h = static_cast<_Float16*>(h_out);
+#define SM_CRN(V)                                                                        \
+  case V:                                                                                \
+    combine_rmsnorm_kernel<V><<<(unsigned)tokens, 64 * V, 0, st>>>(                      \
+        routed, top_w, pv.inverse, tokens, (int)top_k, x, gamma, eps, h);                \
+    break;
+  switch (v) {
+    SM_CRN(3)
+    SM_CRN(4)
+    SM_CRN(8)
+    SM_CRN(12)
+    SM_CRN(16)
+    default: break;
+  }
+#undef SM_CRN
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
 
 extern "C" int64_t sm_moe_plan_words(int64_t tokens, int64_t top_k, int64_t experts) {
   const int64_t routes = tokens * top_k;

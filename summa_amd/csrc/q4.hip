@@ -875,7 +875,7 @@ __global__ __launch_bounds__(64 * V) void splitk_add_rmsnorm_kernel(
     const float* __restrict__ part, int ks, int64_t rows, float* __restrict__ resid,
     const float* __restrict__ gamma, float eps, _Float16* __restrict__ h) {
   constexpr int D = 256 * V;
-  __shared__ float4 sq[V][kWave];
+  __shared__ float4 sq[V][64];
   __shared__ float rms_s;
   const int64_t r = blockIdx.x;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
@@ -902,27 +902,7 @@ __global__ __launch_bounds__(64 * V) void splitk_add_rmsnorm_kernel(
   const float4 gm = reinterpret_cast<const float4*>(gamma)[c4];
   const float4 v = make_float4(x.x + acc.x, x.y + acc.y, x.z + acc.z, x.w + acc.w);
   *xr = v;
-  sq[wave][lane] = v;
-  __syncthreads();
-  if (wave == 0) {
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < V; ++i) {
-      const float4 t = sq[i][lane];
-      ss = fmaf(t.w, t.w, fmaf(t.z, t.z, fmaf(t.y, t.y, fmaf(t.x, t.x, ss))));
-    }
-    ss = wave_sum(ss);
-    if (lane == 0) rms_s = sqrtf(ss / (float)D + eps);
-  }
-  __syncthreads();
-  const float rms = rms_s;
-  const float o[4] = {v.x / rms * gm.x, v.y / rms * gm.y, v.z / rms * gm.z, v.w / rms * gm.w};
-  _Float16 hi[4], lo[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) split_f16(o[e], hi[e], lo[e]);
-  _Float16* yr = h + r * 2 * D;
-  *reinterpret_cast<h4*>(yr + 4 * c4) = h4{hi[0], hi[1], hi[2], hi[3]};
-  *reinterpret_cast<h4*>(yr + D + 4 * c4) = h4{lo[0], lo[1], lo[2], lo[3]};
+  row_rmsnorm_pair<V>(v, gm, eps, sq, rms_s, h + r * 2 * D);
 }
 
 // K splits of the fused residual projection + RMSNorm, or 0 when the fused

@@ -215,6 +215,32 @@ def test_combine_matches_tensor_expression(dev, T, E, d):
     np.testing.assert_allclose(x, ref, rtol=1e-6, atol=1e-6)
 
 
+@pytest.mark.parametrize("T,E,d", [(128, 32, 2048), (33, 8, 768), (5, 4, 4096), (7, 4, 320)])
+def test_combine_rmsnorm_equals_two_steps(dev, T, E, d):
+    """sm_moe_combine_rmsnorm (the combine and the next RMSNorm in one launch)
+    gives sm_moe_combine + sm_rmsnorm's bits for x and for the f16-pair rows,
+    for the widths it fuses and for one it hands to the two steps (320)."""
+    from summa_amd._lib import SM_F16X2, call
+    print(f"case combine+rmsnorm T={T} E={E} d={d}", flush=True)
+    st = torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(T * d + E)
+    idx = torch.from_numpy(rng.integers(0, E, (T, 2)).astype(np.int32)).to(dev)
+    plan = ops.moe_route_plan(idx, E)
+    routed = torch.from_numpy(rng.normal(0, 1, (2 * T, d)).astype(np.float32)).to(dev)
+    w = torch.from_numpy(rng.uniform(0, 1, (T, 2)).astype(np.float32)).to(dev)
+    x0 = rng.normal(0, 1, (T, d)).astype(np.float32)
+    gamma = torch.from_numpy(rng.uniform(0.5, 1.5, d).astype(np.float32)).to(dev)
+    x1, x2 = torch.from_numpy(x0.copy()).to(dev), torch.from_numpy(x0.copy()).to(dev)
+    h1 = torch.empty((T, 2 * d), dtype=torch.float16, device=dev)
+    h2 = torch.empty_like(h1)
+    call("sm_moe_combine_rmsnorm", routed.data_ptr(), w.data_ptr(), plan.words.data_ptr(), T, 2,
+         E, d, x1.data_ptr(), gamma.data_ptr(), 1e-5, h1.data_ptr(), st)
+    ops.moe_route_combine(routed, w, plan, x2)
+    call("sm_rmsnorm", x2.data_ptr(), gamma.data_ptr(), T, d, 1e-5, h2.data_ptr(), SM_F16X2, st)
+    torch.testing.assert_close(x1, x2, rtol=0, atol=0)
+    torch.testing.assert_close(h1, h2, rtol=0, atol=0)
+
+
 # ------------------------------------------------------------ end to end ---
 
 def _first_bad(lp, lp_ref, tol):
