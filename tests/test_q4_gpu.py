@@ -560,7 +560,8 @@ def test_gemv_multi_equals_single_launches(dev, pair):
 
 @pytest.mark.parametrize("m,n,k,exact", [(256, 2048, 2048, False), (256, 2048, 5632, True),
                                          (128, 2048, 2048, False), (200, 1024, 2048, True),
-                                         (256, 768, 3072, True), (1024, 2048, 2048, True)])
+                                         (128, 768, 768, False), (128, 768, 3072, False),
+                                         (1024, 2048, 2048, True)])
 def test_matmul_add_rmsnorm(dev, m, n, k, exact):
     """sm_q4_matmul_add_rmsnorm (a residual projection and the RMSNorm after
     it in one call) against the two-step form (sm_q4_matmul_ws + sm_rmsnorm):
@@ -569,7 +570,9 @@ def test_matmul_add_rmsnorm(dev, m, n, k, exact):
     itself or the fused form does not apply (exact), and is within the split
     tolerance of base + x.W^T in f64 everywhere. Shapes: config[2]'s decode o
     (forced split) and down projections, config[4]'s o at 128 rows, a narrow
-    N, and two shapes that fall back (narrow 768-column decode, prefill)."""
+    N, config[1]'s decode o and down (768 columns, where the plain matmul
+    takes the in-workgroup K-split kernel), and a prefill shape that falls
+    back to the two steps."""
     print(f"case add+rmsnorm m={m} n={n} k={k}", flush=True)
     st = torch.cuda.current_stream().cuda_stream
     w = _weights(n, k, m + n + k)
