@@ -16,6 +16,8 @@ Prints ONE JSON line (the driver's contract). Workloads:
   q4_gemv         the whole-model M = 1 Q4 GEMV sweep (config[2] weights).
   recompute_gemm  the dominant kernel alone: the config[2] recompute FFN-in
                   GEMM (wide-tile kernel), for counter runs.
+  decode_attention  config[2]'s decode attention, per-rollout vs shared
+                  prompt, at t = 1, 256, 511 (value = speedup at t = 511).
 Timing: W warmup steps, then K timed steps bracketed by synchronisation; GPU
 durations come from HIP events recorded on the stream the work runs on.
 """
@@ -668,6 +670,67 @@ def bench_recompute_gemm(args) -> dict:
                                                    "traffic_bytes_per_launch")}}
 
 
+def bench_decode_attention(args) -> dict:
+    """Decode attention at the config[2] decode shape (256 rollouts in 32
+    prompt groups of 8, 512-token prompt, 16 query / 4 KV heads, head dim
+    128, f16 K/V cache of capacity 1023, f16-pair queries and output) at
+    positions t = 1, 256, 511 after the prompt: the per-rollout kernel
+    (sm_attn_decode, every rollout reads its own prompt K/V) against the
+    shared-prompt path (sm_attn_decode_prefix: the prompt K/V once per
+    group, then each rollout's t continuation keys). Algorithmic bytes:
+    per-rollout 256 x 4 x (512 + t) x 128 x 2 B x 2 + queries + output;
+    shared prompt 32 x 4 x 512 x 128 x 2 B x 2 + 256 x 4 x t x 128 x 2 B x 2
+    + queries + output + the prompt partials written and read once."""
+    import torch
+
+    from summa_amd import _lib
+    from summa_amd._lib import SM_F16, SM_F16X2, call
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    S, G, P, H, KVH, hd, cap = 256, 8, 512, 16, 4, 128, 1023
+    gen = torch.Generator(device=dev).manual_seed(0)
+    rnd = lambda *sh: torch.randn(*sh, generator=gen, device=dev).half()  # noqa: E731
+    q, kc, vc = rnd(S, H, hd), rnd(S, KVH, cap, hd), rnd(S, KVH, cap, hd)
+    pk, pv = rnd(S // G, KVH, P, hd), rnd(S // G, KVH, P, hd)
+    out = torch.empty(S, 2 * H * hd, dtype=torch.float16, device=dev)
+    nws = int(_lib.lib().sm_attn_decode_prefix_workspace_bytes(S, G, P, H, KVH, hd))
+    ws = torch.empty(nws // 4, device=dev)
+    qo = S * H * hd * 4 + S * 2 * H * hd * 2           # f16-pair queries + output
+    res = {}
+    for t in (1, 256, 511):
+        lens = torch.full((S,), P + t, dtype=torch.int32, device=dev)
+        full = _time_launches(lambda: call(
+            "sm_attn_decode", q.data_ptr(), kc.data_ptr(), vc.data_ptr(), lens.data_ptr(),
+            out.data_ptr(), SM_F16, SM_F16X2, S, H, KVH, cap, hd, st.cuda_stream),
+            max(args.steps, 1))
+        pre = _time_launches(lambda: call(
+            "sm_attn_decode_prefix", q.data_ptr(), pk.data_ptr(), pv.data_ptr(), kc.data_ptr(),
+            vc.data_ptr(), lens.data_ptr(), out.data_ptr(), ws.data_ptr(), nws, SM_F16,
+            SM_F16X2, S, G, P, H, KVH, cap, hd, st.cuda_stream), max(args.steps, 1))
+        b_full = S * KVH * (P + t) * hd * 4 + qo
+        b_pre = (S // G) * KVH * P * hd * 4 + S * KVH * t * hd * 4 + qo + 2 * nws
+        res[str(t)] = {"per_rollout_us": round(full * 1e3, 2), "shared_prompt_us": round(pre * 1e3, 2),
+                       "per_rollout_GBs": round(b_full / full / 1e6, 1),
+                       "shared_prompt_GBs": round(b_pre / pre / 1e6, 1),
+                       "speedup": round(full / pre, 3)}
+    # calibration copy for the counter runs (256 MiB read + 256 MiB written)
+    src = torch.empty(64 << 20, dtype=torch.float32, device=dev)
+    torch.empty_like(src).copy_(src)
+    torch.cuda.synchronize()
+    top = res["511"]
+    return {"metric": "decode attention speedup of the shared prompt (config[2] shape, t=511)",
+            "value": top["speedup"], "unit": "x", "ms_per_step": top["shared_prompt_us"] / 1e3,
+            "dtype": "f16 K/V, f16-pair q/out, f32 softmax",
+            "config": {"workload": "decode_attention config[2]", "rollouts": S, "group": G,
+                       "prompt_len": P, "heads": H, "kv_heads": KVH, "head_dim": hd},
+            "roofline": {"bound": "hbm", "kernel": "sm_attn_decode_prefix at t=511",
+                         "achieved": top["shared_prompt_GBs"], "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(top["shared_prompt_GBs"] / HBM_PEAK_GBS, 4),
+                         "traffic": profile_figure("decode_attention_shared_prompt_traffic.md",
+                                                   "traffic_bytes_per_launch")},
+            "by_t": res}
+
+
 def bench_policy_update(args) -> dict:
     """The GRPO policy update at config[2] scale (sm_policy_prepare +
     sm_policy_optimizer_step): one group of 8 rollouts x (512 + 512) per call,
@@ -730,7 +793,8 @@ def bench_policy_update(args) -> dict:
 
 
 WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress, "q4_gemv": bench_q4_gemv,
-             "recompute_gemm": bench_recompute_gemm, "policy_update": bench_policy_update}
+             "recompute_gemm": bench_recompute_gemm, "policy_update": bench_policy_update,
+             "decode_attention": bench_decode_attention}
 
 
 def main() -> int:
