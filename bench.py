@@ -268,11 +268,13 @@ def q4_gemv_sweep(model_cfg: dict, dev, ms=(1, 2, 4, 8, 16), reps: int = 10) -> 
     return res
 
 
-def ce_stress(dev, rows: int, reps: int = 5) -> dict:
+def ce_stress(dev, rows: int, reps: int = 5, host_sample: int = 0) -> dict:
     """config[3]: fused log-softmax / CE / token log-prob over bf16
     [rows, 131072] logits ~ N(0, 3) with a +8 spike at the target. lp + loss
     read the logits once (algorithmic bytes rows * V * 2); grad in place reads
-    and writes them once (2 * rows * V * 2)."""
+    and writes them once (2 * rows * V * 2). host_sample > 0: also returns
+    (``_sample``) that many rows spread over the batch (bf16 bits, targets)
+    copied to the host before any timing, for the CPU baseline."""
     import torch
 
     from summa_amd import ops
@@ -283,13 +285,20 @@ def ce_stress(dev, rows: int, reps: int = 5) -> dict:
     t = torch.empty(rows, dtype=torch.int32, device=dev)
     ops.fill_ce_stress(x, t, CE_STRESS["std"], CE_STRESS["spike"], seed=0)
     torch.cuda.synchronize()
+    sample = None
+    if host_sample:
+        idx = torch.linspace(0, rows - 1, host_sample, device=dev).long()
+        lp_gpu = ops.ce_rows(x, t)[0][idx]
+        sample = (x[idx].view(torch.int16).cpu().numpy().view("uint16"),
+                  t[idx].cpu().numpy(), lp_gpu.cpu().numpy().astype("float64"))
     lp_ms = _time_launches(lambda: ops.ce_rows(x, t), reps)
     g_ms = _time_launches(lambda: ops.ce_rows(x, t, grad_in_place=True, grad_scale=1.0 / rows),
                           reps)
     rb = rows * vocab * 2
     del x, t
     torch.cuda.empty_cache()
-    return {"shape": [rows, vocab], "dtype": "bf16",
+    out = {"_sample": sample} if host_sample else {}
+    return {**out, "shape": [rows, vocab], "dtype": "bf16",
             "lp_loss": {"ms": round(lp_ms, 4), "bytes": rb,
                         "GBs": round(rb / lp_ms / 1e6, 1),
                         "frac": round(rb / lp_ms / 1e6 / HBM_PEAK_GBS, 4)},
@@ -300,29 +309,39 @@ def ce_stress(dev, rows: int, reps: int = 5) -> dict:
 
 # ---------------------------------------------------------------- RL step ---
 
-def rl_inputs(wl, mc, dev):
+def rl_inputs(wl, mc, dev, count: int = 1, seed: int = 0):
+    """``count`` distinct GRPO batches (prompts, rewards), drawn before any
+    timing: `prompts` prompts each rolled out `group` times (rows g*group ..
+    g*group + group - 1 carry prompt g). Every step of a run takes its own
+    batch, as every update of the reference's post-training loop generates on
+    new examples (posttrain.rs:4339-4440), so no step can reuse the prompt
+    pass of a step before it."""
     import torch
-    gen = torch.Generator().manual_seed(0)
-    # GRPO: `prompts` prompts, each rolled out `group` times (rows g*group ..
-    # g*group + group - 1 carry prompt g)
-    prompts = torch.randint(0, mc.vocab, (wl.prompts, wl.prompt_len), generator=gen,
-                            dtype=torch.int32).repeat_interleave(wl.group, 0).to(dev)
-    rewards = wl.sample_rewards(gen).to(dev)
-    return prompts, rewards
+    gen = torch.Generator().manual_seed(seed)
+    out = []
+    for _ in range(count):
+        prompts = torch.randint(0, mc.vocab, (wl.prompts, wl.prompt_len), generator=gen,
+                                dtype=torch.int32).repeat_interleave(wl.group, 0).to(dev)
+        rewards = wl.sample_rewards(gen).to(dev)
+        out.append((prompts, rewards))
+    return out
 
 
-def run_rl_step(wl, policy, reference, prompts, rewards, steps, warmup, tag=""):
-    """W + K GRPO steps; returns per-step rollout / prepare / step ms (events)
-    and the last step's outputs."""
+def run_rl_step(wl, policy, reference, batches, steps, warmup, tag=""):
+    """W + K GRPO steps, step i on batches[i] (W + K distinct batches);
+    returns per-step rollout / prepare / step ms (events) and the last step's
+    outputs and batch."""
     import torch
 
     from summa_amd.configs import ADVANTAGE_EPSILON, CLIP_EPSILON, KL_COEFFICIENT
     from summa_amd.model import rl_prepare
 
+    assert len(batches) >= warmup + steps
     st = torch.cuda.current_stream()
     e0, e_mid, e1 = _events(3)
 
-    def step(seed):
+    def step(seed, batch):
+        prompts, rewards = batch
         tok, lp_beh = policy.generate(prompts, wl.new_tokens, temperature=wl.temperature,
                                       seed=seed)
         e_mid.record(st)
@@ -333,13 +352,13 @@ def run_rl_step(wl, policy, reference, prompts, rewards, steps, warmup, tag=""):
         return out
 
     for i in range(warmup):
-        step(1000 + i)
+        step(1000 + i, batches[i])
     torch.cuda.synchronize()
     roll, full = [], []
     t0 = time.perf_counter()
     for i in range(steps):
         e0.record(st)
-        out = step(i)
+        out = step(i, batches[warmup + i])
         e1.record(st)
         torch.cuda.synchronize()
         roll.append(e0.elapsed_time(e_mid))
@@ -347,7 +366,7 @@ def run_rl_step(wl, policy, reference, prompts, rewards, steps, warmup, tag=""):
         if tag:
             log(f"bench: {tag} step {i} rollout {roll[-1]:.1f} ms, RL step {full[-1]:.1f} ms")
     wall = time.perf_counter() - t0
-    return roll, full, wall, out
+    return roll, full, wall, out, batches[warmup + steps - 1]
 
 
 def prefill_ms(wl, policy, prompts, reps: int = 3) -> float:
@@ -367,8 +386,8 @@ def config0_leg(dev, steps: int = 5) -> dict:
     for m in (policy, reference):  # each group's prompt computed once
         m.set_prompt_groups(wl.group)
     w = draw_weights(wl, [policy, reference], dev, seed=1)
-    prompts, rewards = rl_inputs(wl, mc, dev)
-    roll, full, _, out = run_rl_step(wl, policy, reference, prompts, rewards, steps, 2)
+    batches = rl_inputs(wl, mc, dev, count=steps + 2)
+    roll, full, _, out, (prompts, _) = run_rl_step(wl, policy, reference, batches, steps, 2)
     r, f = statistics.median(roll), statistics.median(full)
     return {"rl_step_ms": round(f, 3), "rollout_ms": round(r, 3),
             "rollout_tok_s": round(wl.rollouts * wl.new_tokens / (r * 1e-3), 1),
@@ -388,14 +407,112 @@ def _cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
-def cpu_baseline_rl(wl, host_weights, c0=None) -> dict:
+CPU_CE_ROWS = 512        # config[3] rows the CPU CE leg runs (spread over the batch)
+CPU_RECOMPUTE_ROWS = 32  # continuation rows of the CPU recompute sample
+
+
+def cpu_ce_leg(sample, gpu_ce) -> dict:
+    """config[3] on the oracle (``or_ce_rows``: f64 two-pass log-softmax, the
+    reference's CE restated) over CPU_CE_ROWS of the GPU's own logits rows
+    (bf16, spread over the 65536-row batch): lp + loss at 1 thread and at
+    every core, lp + loss + gradient at every core (the oracle writes an f32
+    gradient array rather than bf16 in place), each the median of 3; ms and
+    GB/s scaled to the full 65536 x 131072 batch by rows (the algorithmic
+    bytes of the GPU leg); and the GPU's lp on those rows against the
+    oracle's (1e-5)."""
+    import numpy as np
+
+    import oracle
+    from summa_amd.configs import CE_STRESS
+
+    logits, tgt, lp_gpu = sample
+    R, V = logits.shape
+    scale = CE_STRESS["rows"] / R
+    out = {"sample_rows": R, "vocab": V}
+
+    def med(fn):
+        ts = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return statistics.median(ts)
+
+    for label, threads in (("1_thread", 1), ("all_threads", 0)):
+        n = oracle.set_threads(threads)
+        t = med(lambda: oracle.ce_rows(logits, tgt))
+        full_ms = t * scale * 1e3
+        out[f"lp_loss_{label}"] = {"threads": n, "sample_ms": round(t * 1e3, 2),
+                                   "full_batch_ms": round(full_ms, 1),
+                                   "GBs": round(gpu_ce["lp_loss"]["bytes"] / full_ms / 1e6, 2)}
+    t = med(lambda: oracle.ce_rows(logits, tgt, grad=True, grad_scale=1.0 / CE_STRESS["rows"]))
+    full_ms = t * scale * 1e3
+    out["grad_all_threads"] = {"threads": oracle.set_threads(0), "sample_ms": round(t * 1e3, 2),
+                               "full_batch_ms": round(full_ms, 1),
+                               "GBs": round(gpu_ce["grad_in_place"]["bytes"] / full_ms / 1e6, 2)}
+    lp_or, _, _ = oracle.ce_rows(logits, tgt)
+    err = float(np.abs(lp_or - lp_gpu).max())
+    out["parity"] = {"max_abs_lp_gpu_minus_oracle": err, "tolerance": 1e-5,
+                     "verdict": "pass" if err <= 1e-5 else "fail"}
+    out["gpu_speedup_lp_loss"] = round(out["lp_loss_all_threads"]["full_batch_ms"]
+                                       / gpu_ce["lp_loss"]["ms"], 1)
+    return out
+
+
+def cpu_recompute_leg(wl, host) -> dict:
+    """The log-prob recompute on the oracle at the config's real context: one
+    rollout's last CPU_RECOMPUTE_ROWS continuation positions (pos P + N - 1 -
+    rows .. P + N - 2, attending over a full cache of P + N - 1 positions
+    filled with synthetic K / V, the same work as the recompute's last rows),
+    then the LM head and the log-softmax over those rows; at every core,
+    median of 3. Scaled to one RL step's recompute of the policy (continuation
+    rows) and of the frozen copy (prompt rows once per group + continuation
+    rows) by token rows, the attention at the end-of-context cost (an upper
+    bound for the earlier rows)."""
+    import numpy as np
+
+    import oracle
+
+    c = host.cfg
+    P, N, S = wl.prompt_len, wl.new_tokens, wl.rollouts
+    cap = P + N - 1
+    R = CPU_RECOMPUTE_ROWS
+    pos0 = cap - R
+    rng = np.random.default_rng(3)
+    kc = (rng.standard_normal(c["layers"] * c["KVH"] * cap * c["hd"], dtype=np.float32)
+          * np.float32(0.5))
+    vc = (rng.standard_normal(kc.size, dtype=np.float32) * np.float32(0.5))
+    ids = rng.integers(0, c["V"], R).astype(np.int32)
+    n = oracle.set_threads(0)
+    t_fwd, t_head = [], []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        x = host.forward_at(ids, pos0, kc, vc, cap)
+        t1 = time.perf_counter()
+        oracle.ce_rows(host.logits(x), ids)
+        t2 = time.perf_counter()
+        t_fwd.append(t1 - t0)
+        t_head.append(t2 - t1)
+    f_row, h_row = statistics.median(t_fwd) / R, statistics.median(t_head) / R
+    layer_rows = wl.prompts * P + 2 * S * (N - 1)  # frozen copy's prompt pass + 2 continuations
+    head_rows = 2 * S * N
+    return {"threads": n, "sample": (f"1 rollout, positions {pos0}..{cap - 1} of {cap} "
+                                     f"(full synthetic cache), {R} rows"),
+            "forward_ms_per_row": round(f_row * 1e3, 2), "head_ce_ms_per_row": round(h_row * 1e3, 2),
+            "rl_step_recompute_s_extrapolated": round(f_row * layer_rows + h_row * head_rows, 1),
+            "rows_extrapolated": {"layer_rows": layer_rows, "head_rows": head_rows}}
+
+
+def cpu_baseline_rl(wl, host_weights, c0=None, ce=None) -> dict:
     """The C oracle (the reference CPU path restated: fp32, batch 1 per
     rollout, generate.rs:68-124) on the GPU box's host cores, on a bounded
     sample of the workload: one rollout, a 64-token prompt prefilled untimed,
     then cached decode steps (rollout tok/s = 1 / time per step, the rate of
     the reference's per-rollout loop); warm-up, then the median of 5 reps, at
-    1 thread and at every core. Plus the GRPO loss over the full [S, N]
-    arrays, and config[0]'s full RL step with its oracle parity verdict."""
+    1 thread and at every core. Plus the log-prob recompute at the config's
+    real context (cpu_recompute_leg), the GRPO loss over the full [S, N]
+    arrays, config[3]'s CE on a row sample (cpu_ce_leg) and config[0]'s full
+    RL step with its oracle parity verdict."""
     import numpy as np
 
     import oracle
@@ -419,6 +536,9 @@ def cpu_baseline_rl(wl, host_weights, c0=None) -> dict:
         out[label] = {"threads": n, "s_per_token": round(med, 4),
                       "rollout_tok_s": round(1.0 / med, 4)}
     oracle.set_threads(0)
+    log("bench: cpu recompute sample")
+    out["recompute"] = cpu_recompute_leg(wl, host)
+    del host
     # GRPO loss over the whole batch's [S, N] arrays (f64 oracle)
     rng = np.random.default_rng(1)
     sh = (wl.prompts, wl.group, wl.new_tokens)
@@ -433,9 +553,14 @@ def cpu_baseline_rl(wl, host_weights, c0=None) -> dict:
            "cores": out["all_threads"]["threads"], "kind": "port",
            "sample": (f"config[{wl.index}] Q4 model, 1 rollout: 64-token prompt prefilled "
                       f"untimed, then median of 5 reps of cached decode steps (1 thread: 1 "
-                      f"step per rep, all threads: 2); GRPO loss over the full "
-                      f"{list(sh)} arrays"),
+                      f"step per rep, all threads: 2); recompute: {CPU_RECOMPUTE_ROWS} rows at "
+                      f"the end of a {wl.prompt_len + wl.new_tokens - 1}-position context; "
+                      f"GRPO loss over the full {list(sh)} arrays; config[3] CE over "
+                      f"{CPU_CE_ROWS} of its rows"),
            "cpu_model": _cpu_model(), "nproc": os.cpu_count(), **out}
+    if ce is not None:
+        log("bench: cpu CE sample (config[3])")
+        res["ce_config3"] = cpu_ce_leg(*ce)
     if c0 is not None:
         res["config0"] = c0
     return res
@@ -518,25 +643,28 @@ def draw_weights(wl, models, dev, seed: int = 0) -> dict:
 
 # ------------------------------------------------------------- workloads ---
 
-def bench_rl_step(args) -> dict:
+def rl_step_leg(wl, dev, steps: int, warmup: int, seed: int = 0) -> dict:
+    """One BASELINE RL config on the GPU: the policy and its frozen copy (same
+    weights) with prompt groups and bound workspaces, W warm-up and K timed
+    GRPO steps, each on its own prompts (so the frozen copy always runs its
+    prompt pass, and the policy reuses only the prompt pass of the generation
+    of the same step). Returns the step's figures, the phase split and the
+    decode-vs-recompute check, plus private keys for the CPU baseline."""
     import torch
 
-    from summa_amd.configs import CE_STRESS, RL_WORKLOADS
     from summa_amd.model import Model, batch_result
 
-    wl = RL_WORKLOADS[args.config]
-    dev = torch.device("cuda:0")
     mc = wl.model_config()
     policy, reference = Model(mc), Model(mc)
-    dweights = draw_weights(wl, [policy, reference], dev)  # the frozen copy equals the policy
+    dweights = draw_weights(wl, [policy, reference], dev, seed=seed)
     for m in (policy, reference):  # hot calls carve their buffers from a bound workspace
         m.set_prompt_groups(wl.group)  # each group's prompt computed once
         m.bind_workspace(wl.rollouts, wl.prompt_len, wl.new_tokens)
-    prompts, rewards = rl_inputs(wl, mc, dev)
+    batches = rl_inputs(wl, mc, dev, count=warmup + steps, seed=seed)
     S, N = wl.rollouts, wl.new_tokens
-    log("bench: warmup")
-    roll, full, wall, out = run_rl_step(wl, policy, reference, prompts, rewards, args.steps,
-                                        args.warmup, tag=f"config[{wl.index}]")
+    log(f"bench: config[{wl.index}] warmup")
+    roll, full, wall, out, (prompts, _) = run_rl_step(wl, policy, reference, batches, steps,
+                                                      warmup, tag=f"config[{wl.index}]")
     res = batch_result(out)
     gap = (out["lp_beh"] - out["lp_cur"]).abs()
     lp_gap = float(gap.max())
@@ -545,22 +673,16 @@ def bench_rl_step(args) -> dict:
     pre_ms = prefill_ms(wl, policy, prompts)
     dec_ms = r_ms - pre_ms
     dec_bytes = decode_bytes(wl)
-    # the frozen reference's full recompute + the policy's without its prompt
-    # pass (reused from the generation, sm_model_set_prompt_groups)
+    # the frozen reference's full recompute (its prompt pass included: every
+    # step brings new prompts) + the policy's without its prompt pass (the
+    # generation of the same step computed it, sm_model_set_prompt_groups)
     rec_flops = recompute_flops(wl) + recompute_flops(wl, prompt_pass=False)
     prep_ms = f_ms - r_ms
-    line = {
-        "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
-        "value": S * N / (r_ms * 1e-3), "unit": "rollout tok/s", "ms_per_step": f_ms,
-        "dtype": ("q4g128 weights, f16-pair (fp32-grade) matmul inputs, f16 KV, f32 accumulate"
-                  if wl.quantized else "f32"),
-        "config": {"workload": f"rl_step config[{wl.index}]", **wl.model, "prompts": wl.prompts,
-                   "group": wl.group, "prompt_len": wl.prompt_len, "new_tokens": N,
-                   "temperature": wl.temperature,
-                   "weights": "Q4G128 (bf16 scales)" if wl.quantized else "f32",
-                   "rewards": wl.reward_label()},
+    leg = {
+        "rollout_tok_s": round(S * N / (r_ms * 1e-3), 1),
         "rl_step_ms": round(f_ms, 3), "rollout_ms": round(r_ms, 3), "prepare_ms": round(prep_ms, 3),
-        "wall_s": round(wall, 3),
+        "steps": steps, "warmup": warmup, "wall_s": round(wall, 3),
+        "prompts_per_step": "distinct (new prompts every warm-up and timed step)",
         "grpo": {k: (round(v, 6) if isinstance(v, float) else v) for k, v in res.items()},
         # cached decode vs the recompute over the whole batch (2e-3 bar); for
         # MoE models a router near-tie can pick another expert pair in one
@@ -579,9 +701,52 @@ def bench_rl_step(args) -> dict:
                                    "TFLOPs": round(rec_flops / (prep_ms * 1e-3) / 1e12, 1),
                                    "mfma_frac": round(rec_flops / (prep_ms * 1e-3) / 1e12
                                                       / MFMA_F16_PEAK_TFS, 4)}},
+        "_value": S * N / (r_ms * 1e-3), "_f_ms": f_ms, "_weights": dweights,
     }
+    if wl.model.get("experts"):
+        leg["check"]["note"] = ("MoE: a router near-tie can flip a token's expert pair between "
+                                "the decode and recompute paths; the GPU tests resolve each flip "
+                                "through the traced router decisions")
+    policy.close()
+    reference.close()
     del policy, reference
     torch.cuda.empty_cache()
+    return leg
+
+
+def bench_rl_step(args) -> dict:
+    import torch
+
+    from summa_amd.configs import CE_STRESS, RL_WORKLOADS
+
+    wl = RL_WORKLOADS[args.config]
+    dev = torch.device("cuda:0")
+    leg = rl_step_leg(wl, dev, args.steps, args.warmup)
+    dweights = leg.pop("_weights")
+    line = {
+        "metric": "rollout tok/s + RL step ms on 1 MI355X; % HBM roofline of 4-bit GEMV",
+        "value": leg.pop("_value"), "unit": "rollout tok/s", "ms_per_step": leg.pop("_f_ms"),
+        "dtype": ("q4g128 weights, f16-pair (fp32-grade) matmul inputs, f16 KV, f32 accumulate"
+                  if wl.quantized else "f32"),
+        "config": {"workload": f"rl_step config[{wl.index}]", **wl.model, "prompts": wl.prompts,
+                   "group": wl.group, "prompt_len": wl.prompt_len, "new_tokens": wl.new_tokens,
+                   "temperature": wl.temperature,
+                   "weights": "Q4G128 (bf16 scales)" if wl.quantized else "f32",
+                   "rewards": wl.reward_label()},
+    }
+    for k in ("steps", "warmup", "rollout_tok_s"):
+        leg.pop(k)
+    line.update(leg)
+    # the other quantized configs' RL steps (a few steps each: they run the
+    # same kernels at other shapes)
+    for idx in (1, 2, 4):
+        if idx == args.config or args.config == 0:
+            continue
+        log(f"bench: config[{idx}]")
+        sub = rl_step_leg(RL_WORKLOADS[idx], dev, steps=3, warmup=1, seed=idx)
+        for k in ("_value", "_f_ms", "_weights"):
+            sub.pop(k)
+        line[f"config{idx}"] = sub
     log("bench: dominant kernel (recompute FFN-in GEMM)")
     k = recompute_gemm(RL_WORKLOADS[2], dev)
     line["roofline"] = {"bound": "mfma", "kernel": k["kernel"], "shape": k["shape"],
@@ -595,11 +760,13 @@ def bench_rl_step(args) -> dict:
                                               "traffic_bytes_per_launch")
     line["q4_gemv"] = sweep
     log("bench: fused CE (config[3])")
-    line["ce_config3"] = ce_stress(dev, CE_STRESS["rows"])
+    ce = ce_stress(dev, CE_STRESS["rows"], host_sample=CPU_CE_ROWS)
+    ce_sample = ce.pop("_sample")
+    line["ce_config3"] = ce
     log("bench: config[0]")
     c0 = config0_leg(dev)
     line["config0"] = {k: v for k, v in c0.items() if not k.startswith("_")}
-    line["_cpu"] = (dweights, c0)
+    line["_cpu"] = (dweights, c0, ce_sample, ce)
     return line
 
 
@@ -825,10 +992,11 @@ def main() -> int:
     if not args.no_cpu_baseline and cpu is not None:
         log("bench: cpu baseline (oracle on the host cores)")
         from summa_amd.configs import RL_WORKLOADS
-        dweights, c0 = cpu
+        dweights, c0, ce_sample, ce = cpu
         host_w = _model_host_weights(dweights)
         del dweights
-        out["cpu_baseline"] = cpu_baseline_rl(RL_WORKLOADS[args.config], host_w, cpu_config0(c0))
+        out["cpu_baseline"] = cpu_baseline_rl(RL_WORKLOADS[args.config], host_w, cpu_config0(c0),
+                                              (ce_sample, ce))
     print(json.dumps(out), flush=True)
     return 0
 

@@ -65,6 +65,48 @@ int sm_ce_rows(const void* logits, int dtype, const int32_t* targets, int64_t ro
                float* loss, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Fused linear head + cross-entropy: the LinearCrossEntropyBackend seam
+ * (summa-llm/src/model/linear_cross_entropy/mod.rs:33-57) that
+ * Dispatch::linear_cross_entropy_inner calls (mod.rs:73), with the chunked
+ * semantics of chunked_loss / chunked_backward (reference.rs:42-159) and
+ * fused_loss / fused_backward (gpu.rs:264-426). f32 operands, f32-grade
+ * GEMMs (sm_gemm_ex), so [chunk, stored_vocab] f32 logits exist only in the
+ * workspace.
+ *
+ * hidden [tokens, d] f32, weight [stored_vocab, d] f32 (Burn's [vocab,
+ *   hidden] head weight), bias [stored_vocab] f32 (read only when use_bias),
+ *   targets [tokens] int32 in [0, logical_vocab) (the reference's Int tensor,
+ *   narrowed), chunk > 0 rows per logits slab.
+ * sm_linear_cross_entropy: loss [1] = mean over tokens of
+ *   -log_softmax(hidden . W^T + b)[target] over the logical vocabulary
+ *   (padded columns masked, mask_padded_logits reference.rs:21-40);
+ *   token_logprob (nullable) [tokens] receives each row's log-prob.
+ * sm_linear_cross_entropy_backward: grad_output [1] f32 on the device (the
+ *   loss's upstream gradient); grad_hidden [tokens, d] =, grad_weight
+ *   [stored_vocab, d] =, grad_bias [stored_vocab] = (when use_bias) the
+ *   three gradients of linear_cross_entropy_backward; rows >= logical_vocab
+ *   of grad_weight / grad_bias are exactly 0.
+ * workspace: sm_linear_cross_entropy_workspace_bytes(...) bytes, 256-byte
+ *   aligned (-1 for a bad shape); no call allocates.
+ * Errors (no panic across the ABI): chunk <= 0 ("linear cross-entropy chunk
+ *   size must be positive"), tokens == 0 ("linear cross-entropy requires at
+ *   least one token"), logical_vocab outside 1..=stored_vocab.
+ */
+int64_t sm_linear_cross_entropy_workspace_bytes(int64_t tokens, int64_t d, int64_t stored_vocab,
+                                                int64_t chunk, int use_bias);
+int sm_linear_cross_entropy(const float* hidden, const float* weight, const float* bias,
+                            const int32_t* targets, int64_t tokens, int64_t d,
+                            int64_t stored_vocab, int64_t logical_vocab, int64_t chunk,
+                            int use_bias, float* loss, float* token_logprob, void* workspace,
+                            int64_t workspace_bytes, void* stream);
+int sm_linear_cross_entropy_backward(const float* hidden, const float* weight, const float* bias,
+                                     const int32_t* targets, const float* grad_output,
+                                     int64_t tokens, int64_t d, int64_t stored_vocab,
+                                     int64_t logical_vocab, int64_t chunk, int use_bias,
+                                     float* grad_hidden, float* grad_weight, float* grad_bias,
+                                     void* workspace, int64_t workspace_bytes, void* stream);
+
+/* ------------------------------------------------------------------------
  * GRPO clipped policy-gradient + k3-KL loss, batched over prompt groups.
  * Replaces grpo_loss_tensor (summa-train/src/posttrain.rs:874-1028) and
  * follows the scalar oracle grpo_loss (posttrain.rs:720-868) for the

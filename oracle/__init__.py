@@ -366,6 +366,28 @@ class HostModel:
                             toks[t:].ctypes.data, 1, lp.ctypes.data, 1)
         return toks
 
+    def forward_at(self, ids, pos0, kc, vc, cap):
+        """One sequence's forward of ids [R] at positions pos0 .. pos0 + R - 1
+        over caller caches kc / vc (float32, [layers, KVH, cap, hd] each; the
+        positions before pos0 are read as they are): ``or_model_forward`` with
+        S = 1. Returns the hidden rows [R, d]."""
+        ids = np.ascontiguousarray(ids, dtype=np.int32)
+        R = ids.shape[0]
+        c = self.cfg
+        assert kc.dtype == np.float32 and kc.size == c["layers"] * c["KVH"] * cap * c["hd"]
+        assert vc.dtype == np.float32 and vc.size == kc.size and pos0 + R <= cap
+        x = np.empty((R, c["d"]), np.float32)
+        lib().or_model_forward(C.byref(self.m), ids.ctypes.data, 1, R, int(pos0), kc.ctypes.data,
+                               vc.ctypes.data, int(cap), x.ctypes.data)
+        return x
+
+    def logits(self, x):
+        """Final norm + LM head of hidden rows x [R, d]: logits [R, V] f32."""
+        x = np.ascontiguousarray(x, dtype=np.float32)
+        out = np.empty((x.shape[0], self.cfg["V"]), np.float32)
+        lib().or_model_logits(C.byref(self.m), x.ctypes.data, x.shape[0], out.ctypes.data)
+        return out
+
     def forward_logits(self, ids):
         """Full causal forward over ids [S, L]; returns logits [S, L, V] (float32)."""
         ids = np.ascontiguousarray(ids, dtype=np.int32)

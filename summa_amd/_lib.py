@@ -32,6 +32,11 @@ SIGNATURES: dict[str, tuple] = {
     "sm_version": (i32, []),
     "sm_last_error": (C.c_char_p, []),
     "sm_ce_rows": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, f32, vp, vp, vp]),
+    "sm_linear_cross_entropy_workspace_bytes": (i64, [i64, i64, i64, i64, i32]),
+    "sm_linear_cross_entropy": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, i32, vp, vp, vp,
+                                      i64, vp]),
+    "sm_linear_cross_entropy_backward": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i32,
+                                               vp, vp, vp, vp, i64, vp]),
     "sm_grpo_loss": (i32, [vp, vp, vp, vp, vp, i64, i64, i64, f64, f64, f64, vp, vp, vp, vp, vp]),
     "sm_grpo_flags_message": (C.c_char_p, [C.c_int32]),
     "sm_q4_quantize": (i32, [vp, i32, i64, vp, vp, vp, vp]),

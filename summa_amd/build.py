@@ -2,7 +2,11 @@
 
 Compiles every ``csrc/*.hip`` translation unit with hipcc for ``gfx950`` and
 links them into ``summa_amd/libsumma_amd.so`` (in-tree, so the built library
-travels with the source tree to the GPU host). Run ``python -m summa_amd.build``.
+travels with the source tree to the GPU host), and archives the same objects
+as ``summa_amd/libsumma_amd.a``: the static library a Rust ``build.rs`` links
+(each object carries its own gfx950 code object and registers it at load, so
+the archive links with the host linker plus ``-lamdhip64 -lstdc++``). Run
+``python -m summa_amd.build``.
 """
 from __future__ import annotations
 
@@ -17,6 +21,7 @@ PKG = Path(__file__).resolve().parent
 CSRC = PKG / "csrc"
 OBJ = PKG / "_build"
 LIB = PKG / "libsumma_amd.so"
+ARCHIVE = PKG / "libsumma_amd.a"
 ARCH = "gfx950"
 
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
@@ -58,8 +63,16 @@ def build(verbose: bool = True) -> Path:
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{proc.stderr}")
     os.replace(tmp, LIB)
+    tmp_a = ARCHIVE.with_suffix(".a.tmp")
+    if tmp_a.exists():
+        tmp_a.unlink()
+    proc = subprocess.run([shutil.which("ar") or "ar", "rcs", str(tmp_a), *map(str, objs)],
+                          capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"ar failed:\n{proc.stderr}")
+    os.replace(tmp_a, ARCHIVE)
     if verbose:
-        print(f"built {LIB} from {len(sources)} sources", flush=True)
+        print(f"built {LIB} and {ARCHIVE.name} from {len(sources)} sources", flush=True)
     return LIB
 
 

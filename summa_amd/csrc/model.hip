@@ -86,15 +86,14 @@ struct DevBuf {
   void* p = nullptr;
   size_t n = 0;
   bool fixed = false;
+  // bumped whenever p changes (growth, release, binding): a prompt state
+  // recorded in this buffer is stale once its generation moved
+  uint64_t gen = 0;
 };
-
-// Bumped whenever a workspace buffer moves (growth, release): a cached
-// prompt state whose buffers may have moved is then recomputed.
-uint64_t g_buf_epoch = 1;
 
 int ensure(DevBuf& b, size_t bytes) {
   if (b.n >= bytes) return SM_OK;
-  ++g_buf_epoch;
+  ++b.gen;
   SM_REQUIRE(!b.fixed,
              "the bound workspace holds %zu bytes for a buffer this call needs %zu of: query "
              "sm_rl_workspace_bytes for the larger shape and bind again",
@@ -294,7 +293,8 @@ struct sm_model {
   // prompts with the same weights and buffers, which then skips its prompt pass
   sm::DevBuf pids;
   bool pstate_valid = false;
-  uint64_t pstate_weights = 0, pstate_epoch = 0;
+  uint64_t pstate_weights = 0;
+  uint64_t pstate_gens[4] = {0, 0, 0, 0};  // pkc, pvc, prow, pids generations
   int64_t pstate_groups = 0, pstate_G = 0, pstate_P = 0;
   uint64_t weights_version = 1;  // bumped by every weight write
   // partials of the shared-prompt decode attention (sm_attn_decode_prefix)
@@ -554,10 +554,15 @@ int head(sm_model* m, const float* xrows, int64_t M, float* logits, hipStream_t 
 // its group's first (checked on the device; one host synchronisation).
 // Whether the model's prompt state was computed for groups of G x P with the
 // current weights and buffers (its prompts still to be compared).
+// Whether the buffers holding the prompt state are those it was recorded in.
+bool pstate_bufs_same(const sm_model* m) {
+  return m->pstate_gens[0] == m->pkc.gen && m->pstate_gens[1] == m->pvc.gen &&
+         m->pstate_gens[2] == m->prow.gen && m->pstate_gens[3] == m->pids.gen;
+}
+
 bool pstate_matches(const sm_model* m, int64_t groups, int64_t P) {
-  return m->pstate_valid && m->pstate_weights == m->weights_version &&
-         m->pstate_epoch == g_buf_epoch && m->pstate_groups == groups &&
-         m->pstate_G == m->prompt_group && m->pstate_P == P;
+  return m->pstate_valid && m->pstate_weights == m->weights_version && pstate_bufs_same(m) &&
+         m->pstate_groups == groups && m->pstate_G == m->prompt_group && m->pstate_P == P;
 }
 
 // Prompt groups: S must be whole groups of G and every prompt row equal to
@@ -591,7 +596,10 @@ int record_pstate(sm_model* m, const int32_t* ids, int64_t groups, int64_t P, hi
   SM_HIP(hipMemcpyAsync(m->pids.p, ids, (size_t)groups * P * 4, hipMemcpyDeviceToDevice, st));
   m->pstate_valid = true;
   m->pstate_weights = m->weights_version;
-  m->pstate_epoch = g_buf_epoch;
+  m->pstate_gens[0] = m->pkc.gen;
+  m->pstate_gens[1] = m->pvc.gen;
+  m->pstate_gens[2] = m->prow.gen;
+  m->pstate_gens[3] = m->pids.gen;
   m->pstate_groups = groups;
   m->pstate_G = m->prompt_group;
   m->pstate_P = P;
@@ -627,6 +635,9 @@ int prefill_prompts(sm_model* m, const int32_t* prompts, int64_t S, int64_t P, i
   group_prompts_kernel<<<blocks_for(groups * P), 256, 0, st>>>(prompts, groups, (int)G, (int)P,
                                                                 ids);
   set_positions_kernel<<<blocks_for(groups), 256, 0, st>>>(pos, lens, (int)groups, 0);
+  // this pass overwrites the prompt state's K / V and rows: it holds again
+  // only if the pass is recorded below
+  m->pstate_valid = false;
   SM_TRY(run_layers(m, ids, groups, P, pos, nullptr, m->pkc.p, m->pvc.p, pl, P, false, st));
   const int rb = c.head_dim * (int)m->kv_size;
   const int64_t n = (int64_t)c.layers * S * c.kv_heads * P * (rb / 16);
@@ -747,11 +758,12 @@ std::vector<DevBuf*> model_bufs(sm_model* m) {
 }
 
 void release_bufs(sm_model* m) {
-  ++g_buf_epoch;
   m->pstate_valid = false;
   for (DevBuf* b : model_bufs(m)) {
     if (b->p && !b->fixed) hipFree(b->p);
+    const uint64_t gen = b->gen + 1;
     *b = DevBuf{};
+    b->gen = gen;
   }
   m->ws_base = nullptr;
   m->ws_bytes = 0;
@@ -860,6 +872,10 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
     plan_max(at(m->rows), (size_t)cc * N * d * 4);
     plan_max(at(m->pos), (size_t)cc * 4);
     plan_max(at(m->lens), (size_t)cc * 4);
+    // a continuation chunk scores cc * N rows (its N - 1 new rows plus the
+    // group's last prompt row per rollout), which can exceed the budget
+    head(std::min(cc * N, rchunk));
+    plan_max(at(m->logits), (size_t)std::min(cc * N, rchunk) * c.vocab * 4);
     if (prefix_attention(m, S))
       plan_max(at(m->apart), (size_t)sm_attn_decode_prefix_workspace_bytes(
                                  S, G, P, c.heads, c.kv_heads, c.head_dim));
@@ -920,6 +936,7 @@ extern "C" int sm_model_bind_workspace(sm_model* m, void* ws, int64_t bytes, int
   size_t off = 0;
   for (size_t i = 0; i < bufs.size(); ++i) {
     bufs[i]->fixed = true;
+    ++bufs[i]->gen;
     bufs[i]->n = plan.bytes[i];
     bufs[i]->p = plan.bytes[i] ? static_cast<char*>(ws) + off : nullptr;
     off += align_up(plan.bytes[i]);
@@ -1326,7 +1343,7 @@ int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens,
   SM_TRY(ensure(m->prow, (size_t)groups * c.d_model * 4));
   SM_TRY(ensure(m->pos, (size_t)std::max(groups, std::min(chunk, S)) * 4));
   SM_TRY(ensure(m->lens, (size_t)std::max(groups, std::min(chunk, S)) * 4));
-  cached = cached && m->pstate_epoch == g_buf_epoch;  // no buffer moved since the check
+  cached = cached && pstate_bufs_same(m);  // no prompt-state buffer moved since the check
   int32_t* pos = (int32_t*)m->pos.p;
   int32_t* lens = (int32_t*)m->lens.p;
   // prompts, once per group, in chunks of whole prompts within the budget;
@@ -1337,6 +1354,9 @@ int logprobs_grouped(sm_model* m, const int32_t* prompts, const int32_t* tokens,
   const bool one_chunk = gchunk >= groups && !m->trace_idx;
   for (int64_t g0 = 0; g0 < groups && !(cached && one_chunk); g0 += gchunk) {
     const int64_t gc = std::min(gchunk, groups - g0);
+    // the pass overwrites the prompt state: valid again only once a whole
+    // single-chunk untraced pass is recorded
+    m->pstate_valid = false;
     SM_TRY(ensure(m->ids, (size_t)gc * P * 4));
     int32_t* ids = (int32_t*)m->ids.p;
     group_prompts_kernel<<<blocks_for(gc * P), 256, 0, st>>>(prompts + g0 * G * P, gc, (int)G,

@@ -70,6 +70,68 @@ def ce_rows(logits: torch.Tensor, targets: torch.Tensor, logical_vocab: int | No
     return lp, loss, lse
 
 
+def _lce_args(hidden, weight, bias, targets, logical_vocab, chunk_size):
+    for t, name in ((hidden, "hidden"), (weight, "weight"), (targets, "targets")):
+        _dev(t, name)
+    if hidden.dtype != torch.float32 or weight.dtype != torch.float32:
+        raise TypeError("hidden and weight must be float32")
+    if targets.dtype != torch.int32:
+        raise TypeError("targets must be int32")
+    tokens, d = hidden.shape
+    stored, dw = weight.shape
+    if dw != d or targets.shape != (tokens,):
+        raise ValueError("linear cross-entropy: hidden [T, d], weight [V, d], targets [T]")
+    if bias is not None:
+        _dev(bias, "bias")
+        if bias.dtype != torch.float32 or bias.shape != (stored,):
+            raise ValueError("bias must be float32 [V]")
+    lv = stored if logical_vocab is None else int(logical_vocab)
+    nbytes = int(_lib.lib().sm_linear_cross_entropy_workspace_bytes(
+        tokens, d, stored, int(chunk_size), int(bias is not None)))
+    ws = torch.empty(max(nbytes, 0) + 256, dtype=torch.uint8, device=hidden.device)
+    base = (ws.data_ptr() + 255) // 256 * 256
+    return tokens, d, stored, lv, ws, base, nbytes
+
+
+def linear_cross_entropy(hidden: torch.Tensor, weight: torch.Tensor, bias, targets: torch.Tensor,
+                         logical_vocab: int | None = None, chunk_size: int = 1024,
+                         want_logprob: bool = False):
+    """Fused linear head + cross-entropy (``sm_linear_cross_entropy``): the
+    mean over tokens of -log_softmax(hidden W^T + b)[target] over the logical
+    vocabulary, computed in chunks of ``chunk_size`` rows
+    (linear_cross_entropy_inner, summa-llm/src/model/linear_cross_entropy/mod.rs:33-43,
+    reference.rs:42-92). Returns ``loss [1]`` (and the per-token log-probs with
+    ``want_logprob``)."""
+    tokens, d, stored, lv, ws, base, nbytes = _lce_args(hidden, weight, bias, targets,
+                                                        logical_vocab, chunk_size)
+    loss = torch.empty(1, dtype=torch.float32, device=hidden.device)
+    lp = torch.empty(tokens, dtype=torch.float32, device=hidden.device) if want_logprob else None
+    call("sm_linear_cross_entropy", hidden.data_ptr(), weight.data_ptr(), _p(bias),
+         targets.data_ptr(), tokens, d, stored, lv, int(chunk_size), int(bias is not None),
+         loss.data_ptr(), _p(lp), base, nbytes, _stream())
+    return (loss, lp) if want_logprob else loss
+
+
+def linear_cross_entropy_backward(hidden: torch.Tensor, weight: torch.Tensor, bias,
+                                  targets: torch.Tensor, grad_output: torch.Tensor,
+                                  logical_vocab: int | None = None, chunk_size: int = 1024):
+    """The three gradients (hidden [T, d], weight [V, d], bias [V] or None) of
+    ``linear_cross_entropy`` for the upstream gradient ``grad_output`` [1]
+    (``sm_linear_cross_entropy_backward``; linear_cross_entropy_backward,
+    mod.rs:45-57, reference.rs:94-159, gpu.rs:313-426)."""
+    tokens, d, stored, lv, ws, base, nbytes = _lce_args(hidden, weight, bias, targets,
+                                                        logical_vocab, chunk_size)
+    _dev(grad_output, "grad_output")
+    go = grad_output.reshape(1).to(torch.float32).contiguous()
+    gh = torch.empty_like(hidden)
+    gw = torch.empty_like(weight)
+    gb = torch.empty_like(bias) if bias is not None else None
+    call("sm_linear_cross_entropy_backward", hidden.data_ptr(), weight.data_ptr(), _p(bias),
+         targets.data_ptr(), go.data_ptr(), tokens, d, stored, lv, int(chunk_size),
+         int(bias is not None), gh.data_ptr(), gw.data_ptr(), _p(gb), base, nbytes, _stream())
+    return gh, gw, gb
+
+
 # ----------------------------------------------------------------- GRPO ---
 
 class GrpoValidationError(ValueError):

@@ -108,3 +108,26 @@ def test_gemv_multi_plan_host_checks():
     jobs[2].epilogue = _lib.SM_EPI_SWIGLU_F16
     assert L.sm_q4_gemv_multi_plan(ctypes.byref(jobs), 3, None) == -1
     assert b"job 2" in L.sm_last_error()
+
+
+def test_linear_cross_entropy_host_checks():
+    """sm_linear_cross_entropy rejects bad arguments with the reference's
+    messages (linear_cross_entropy/mod.rs:66-69, reference.rs:21-30) before
+    any device work; the workspace query refuses bad shapes."""
+    L = _lib.lib()
+    assert L.sm_linear_cross_entropy_workspace_bytes(0, 8, 16, 4, 0) == -1
+    assert L.sm_linear_cross_entropy_workspace_bytes(4, 8, 16, 4, 1) > 4 * 16 * 4
+    ws = 1 << 20
+    st = L.sm_linear_cross_entropy(16, 16, None, 16, 4, 8, 16, 16, 0, 0, 16, None, ws, 1 << 20,
+                                   None)
+    assert st == -1 and L.sm_last_error().decode() == \
+        "linear cross-entropy chunk size must be positive"
+    st = L.sm_linear_cross_entropy(16, 16, None, 16, 0, 8, 16, 16, 2, 0, 16, None, ws, 1 << 20,
+                                   None)
+    assert st == -1 and L.sm_last_error().decode() == \
+        "linear cross-entropy requires at least one token"
+    st = L.sm_linear_cross_entropy_backward(16, 16, None, 16, 16, 4, 8, 16, 20, 2, 0, 16, 16,
+                                            None, ws, 1 << 20, None)
+    assert st == -1 and L.sm_last_error().decode() == "logical vocabulary 20 must be in 1..=16"
+    st = L.sm_linear_cross_entropy(16, 16, None, 16, 4, 8, 16, 16, 2, 0, 16, None, ws, 100, None)
+    assert st == -1 and b"workspace holds 100 bytes" in L.sm_last_error()

@@ -84,3 +84,59 @@ def test_ce_bad_targets_give_nan_not_fault(dev):
     lp, _, _ = ops.ce_rows(x, t, want_loss=False)
     v = lp.cpu().numpy()
     assert abs(v[0] + np.log(64)) < 1e-6 and np.isnan(v[1]) and np.isnan(v[2])
+
+
+@pytest.mark.timeout(300)
+def test_ce_config3_full_size(dev):
+    """Config[3] at its full size: bf16 logits [65536, 131072] (2^33
+    elements, so row offsets need 64 bits, on a 65536-row grid), N(0, 3) plus
+    a +8 spike at each row's target, lp + loss, then grad in place over a
+    logical vocab 64 columns short of the stored one (the padded-vocab
+    contract of linear_cross_entropy/tests.rs:132-216). Checked over the
+    whole batch through size-independent properties (every lp finite and
+    <= 0, loss == mean(-lp), every gradient row summing to 0, every padded
+    column exactly 0) and, on 64 rows spread over the batch including the
+    last, against the f64 oracle."""
+    from summa_amd.configs import CE_STRESS
+    R, V = CE_STRESS["rows"], CE_STRESS["vocab"]
+    print(f"case config[3] full size rows={R} vocab={V}", flush=True)
+    x = torch.empty(R, V, dtype=torch.bfloat16, device=dev)
+    t = torch.empty(R, dtype=torch.int32, device=dev)
+    ops.fill_ce_stress(x, t, CE_STRESS["std"], CE_STRESS["spike"], seed=11)
+    idx = np.unique(np.linspace(0, R - 1, 64).astype(np.int64))  # includes the last row
+    assert idx[-1] == R - 1 and len(idx) == 64
+    sel = torch.from_numpy(idx).to(dev)
+    xs = x[sel].view(torch.int16).cpu().numpy().view(np.uint16)
+    ts = t[sel].cpu().numpy()
+
+    lp, loss, _ = ops.ce_rows(x, t)
+    lpn = lp.cpu().numpy()
+    assert np.isfinite(lpn).all() and (lpn <= 0).all()
+    mean = float(-lpn.astype(np.float64).mean())
+    assert abs(float(loss.cpu()[0]) - mean) <= 1e-5 * max(1.0, abs(mean))
+    lp_ref, _, _ = oracle.ce_rows(xs, ts)
+    np.testing.assert_allclose(lpn[idx], lp_ref, atol=1e-5, rtol=0)
+
+    lv, scale = V - 64, 1.0 / R
+    t2 = torch.where(t >= lv, t - 64, t)
+    ts2 = t2[sel].cpu().numpy()
+    lp2, _, _ = ops.ce_rows(x, t2, lv, grad_in_place=True, grad_scale=scale)
+    lp2n = lp2.cpu().numpy()
+    assert np.isfinite(lp2n).all() and (lp2n <= 0).all()
+    lp2_ref, _, g_ref = oracle.ce_rows(xs, ts2, lv, grad=True, grad_scale=scale)
+    np.testing.assert_allclose(lp2n[idx], lp2_ref, atol=1e-5, rtol=0)
+    g = x[sel].float().cpu().numpy()
+    assert np.all(g[:, lv:] == 0)
+    np.testing.assert_allclose(g, g_ref, rtol=2 ** -8, atol=1e-30)
+    # whole batch: padded columns exactly 0, every row's gradient sums to 0
+    # (softmax sums to 1, minus the one-hot) up to the bf16 rounding of each
+    # element (relative 2^-9 of sum |g| <= 2 * scale)
+    assert not bool((x[:, lv:] != 0).any())
+    worst = 0.0
+    for r0 in range(0, R, 4096):
+        rs = x[r0:r0 + 4096, :lv].float().sum(1, dtype=torch.float64)
+        worst = max(worst, float(rs.abs().max()))
+    print(f"max |row sum of the gradient| {worst:.3e} (scale {scale:.3e})", flush=True)
+    assert worst <= 2 ** -8 * scale
+    del x
+    torch.cuda.empty_cache()

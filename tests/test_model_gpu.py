@@ -239,18 +239,19 @@ def test_prompt_groups_equal_per_rollout(dev, quantized, experts):
 def test_prompt_state_reuse(dev, quantized, experts):
     """A grouped recompute reuses the prompt pass of the generation (or
     recompute) before it when the prompts, the weights and the buffers are
-    the same, and recomputes it otherwise: every result equals a fresh
-    model's recompute bit for bit: after generating, for other prompts, for
-    the first prompts again, after a weight change, with a budget that splits
-    the prompt pass."""
+    the same, and recomputes it otherwise: every result equals the recompute
+    of a model created for that one call, bit for bit: after generating, for
+    other prompts, for the first prompts again, after a weight change, with a
+    budget that splits the prompt pass, after a split pass of other prompts,
+    and (MoE) after a router-traced generation of other prompts."""
     print(f"case prompt state reuse quantized={quantized} experts={experts}", flush=True)
     kw = dict(experts=experts, expert_ffn=256) if experts else {}
     cfg = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
                       vocab=1024, max_seq=64, quantized=quantized, **kw)
-    a, b = Model(cfg), Model(cfg)
-    for m in (a, b):
-        m.init_random(29, std=0.05)
-        m.set_prompt_groups(4)
+    a = Model(cfg)
+    seed = [29]
+    a.init_random(seed[0], std=0.05)
+    a.set_prompt_groups(4)
     gen = torch.Generator().manual_seed(8)
     P, N = 24, 10
 
@@ -261,17 +262,38 @@ def test_prompt_state_reuse(dev, quantized, experts):
     p1, p2 = prompts(), prompts()
     tok, _ = a.generate(p1, N, temperature=1.0, seed=2)
 
+    def fresh(prm, budget):
+        b = Model(cfg)
+        b.init_random(seed[0], std=0.05)
+        b.set_prompt_groups(4)
+        out = b.logprobs(prm, tok, max_tokens_per_forward=budget)
+        torch.cuda.synchronize()
+        b.close()
+        return out
+
     def same(prm, what, budget=0):
         la = a.logprobs(prm, tok, max_tokens_per_forward=budget)
-        lb = b.logprobs(prm, tok, max_tokens_per_forward=budget)
-        assert torch.equal(la, lb), what
+        assert torch.equal(la, fresh(prm, budget)), what
 
     same(p1, "after the generation")
     same(p1, "again")
     same(p2, "other prompts")
     same(p1, "the first prompts again")
+    # a prompt pass split by the budget overwrites the kept prompt K / V
+    # without recording them: the next default-budget recompute of the old
+    # prompts must not reuse them
+    same(p1, "recorded p1")
+    same(p2, "p2 in chunks", budget=30)
+    same(p1, "p1 after a split pass of p2")
+    if experts:
+        # a traced generation runs a prompt pass it does not record
+        a.generate(p1, N, temperature=1.0, seed=2)
+        a.trace_routes(4096, logits=False)
+        a.generate(p2, N, temperature=1.0, seed=2)
+        a.stop_trace()
+        same(p1, "p1 after a traced generation of p2")
     a.generate(p1, N, temperature=1.0, seed=3)
-    for m in (a, b):
-        m.init_random(31, std=0.05)  # new weights: the generation's prompt pass is stale
+    seed[0] = 31
+    a.init_random(seed[0], std=0.05)  # new weights: the generation's prompt pass is stale
     same(p1, "after a weight change")
     same(p1, "prompt pass in chunks", budget=30)

@@ -74,6 +74,31 @@ def test_bound_workspace_equals_own_buffers(dev, geom):
     assert torch.equal(t4, t5) and torch.equal(l4, l5)
 
 
+def test_bound_workspace_prompt_groups(dev):
+    """Shared prompts (sm_model_set_prompt_groups) with a bound workspace and a
+    budget whose continuation chunks score more rows than the budget (cc = 600
+    // 11 = 54 rollouts of N = 12 scored rows: 648 > 600): the bound model's
+    rollout and recompute equal the own-buffer model's bit for bit."""
+    mc = GEOMS["q4"]
+    groups, G, P, N, mtpf = 8, 8, 40, 12, 600
+    S = groups * G
+    g = torch.Generator().manual_seed(7)
+    prompts = torch.randint(0, mc.vocab, (groups, P), generator=g,
+                            dtype=torch.int32).repeat_interleave(G, 0).to(dev)
+    rewards = torch.rand(groups, G, generator=g).to(dev)
+    a_pol, a_ref = _pair(mc, 5, dev)
+    b_pol, b_ref = _pair(mc, 5, dev)
+    for m in (a_pol, a_ref, b_pol, b_ref):
+        m.set_prompt_groups(G)
+    for m in (b_pol, b_ref):
+        m.bind_workspace(S, P, N, mtpf)
+    ta, la, oa = _step(a_pol, a_ref, prompts, N, rewards, mtpf)
+    tb, lb, ob = _step(b_pol, b_ref, prompts, N, rewards, mtpf)
+    assert torch.equal(ta, tb) and torch.equal(la, lb)
+    for k in ("lp_cur", "lp_ref", "stats", "dlp", "flags"):
+        assert torch.equal(oa[k], ob[k]), k
+
+
 def test_bound_calls_allocate_nothing(dev):
     """A bound model's first rollout and recompute leave the device's free
     memory unchanged; the same calls on an unbound model take hundreds of MB
