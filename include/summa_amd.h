@@ -220,6 +220,20 @@ int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64
                              const void* x, int x_dtype, int64_t M, int64_t ldx, float* resid,
                              const float* gamma, float eps, void* h_out, void* workspace,
                              int64_t workspace_bytes, void* stream);
+/* sm_q4_matmul_add_rmsnorm for an MoE layer's FFN norm, with the router of
+ * the normed rows (SparseMoe::forward's fp32 router and top-2, ffn.rs:489-514,
+ * moe_topk.rs:74-104, over h as its f16 pairs hold it): top_idx / top_w
+ * [M, 2] as sm_moe_router_top2 gives them, router_logits [M, experts] f32
+ * (nullable) = h . w_router^T, w_router [experts, N] f32, 2 <= experts <= 64.
+ * Where the fused form applies, the router runs in the same launch as the
+ * norm (the row sums in a different order than sm_moe_router_top2's, within
+ * f32 rounding of it); otherwise the two steps plus sm_moe_router_top2. */
+int sm_q4_matmul_add_rmsnorm_router(const uint8_t* codes, const uint16_t* scales, int64_t N,
+                                    int64_t K, const void* x, int x_dtype, int64_t M, int64_t ldx,
+                                    float* resid, const float* gamma, float eps, void* h_out,
+                                    const float* w_router, int64_t experts, float* router_logits,
+                                    int32_t* top_idx, float* top_w, void* workspace,
+                                    int64_t workspace_bytes, void* stream);
 /* sm_q4_matmul_ws without a caller workspace and without any allocation, for
  * callers that cannot allocate device memory (code under HIP graph capture,
  * tight serving loops, harnesses that forbid hipMalloc). No counterpart in the
@@ -426,8 +440,13 @@ int sm_seen_tokens(const int32_t* ids, int64_t rows, int64_t n, int64_t ids_ld, 
  * 478-711), all on the device with no host round trip.
  * sm_moe_router_top2: logits = f32 h . W_r^T (W_r [E, d] f32), top-2 with a
  *   strict '>' scan (top2_indices_kernel, moe_topk.rs:74-104), weights =
- *   softmax over the pair. top_idx/top_w [tokens, 2]; logits_out nullable.
+ *   softmax over the pair. top_idx/top_w [tokens, 2]; logits_out nullable
+ *   (or logits only: top_idx and top_w both NULL, logits_out required).
  *   h f32, f16 or f16 pairs [tokens, d], d <= 8192, 2 <= E <= 64.
+ * sm_moe_route_plan_logits: top-2 routing from router logits [tokens, E]
+ *   (as sm_moe_router_top2 takes it: top_idx / top_w [tokens, 2]) and the
+ *   route plan of those routes (as sm_moe_route_plan with top_k = 2), in one
+ *   launch for up to 512 tokens (moe_topk.rs:36-104 + moe_route.rs:22-142).
  * sm_moe_route_plan: stable sort of routes r = t*k + j by expert
  *   (host_route_plan ffn.rs:888-929 / route_plan moe_route.rs:22-142) into the
  *   int32 `plan` buffer of sm_moe_plan_words() words: counts[E],
@@ -452,6 +471,9 @@ int sm_moe_router_top2(const void* h, int h_dtype, const float* w_router, int64_
                        float* top_w, void* stream);
 int sm_moe_route_plan(const int32_t* top_idx, int64_t tokens, int64_t top_k, int64_t experts,
                       int32_t* plan, int32_t* error, void* stream);
+int sm_moe_route_plan_logits(const float* logits, int64_t tokens, int64_t experts,
+                             int32_t* top_idx, float* top_w, int32_t* plan, int32_t* error,
+                             void* stream);
 int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts, int64_t N,
                          int64_t K, const void* x, int x_dtype, int64_t ldx, int gather,
                          const int32_t* plan, int64_t tokens, int64_t top_k, void* y, int64_t ldy,

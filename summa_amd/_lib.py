@@ -48,6 +48,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_q4_matmul_ws": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp, i64, vp]),
     "sm_q4_matmul_add_rmsnorm": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, vp, f32, vp, vp,
                                        i64, vp]),
+    "sm_q4_matmul_add_rmsnorm_router": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, vp, f32,
+                                              vp, vp, i64, vp, vp, vp, vp, i64, vp]),
     "sm_q4_noalloc_scratch_bytes": (i64, []),
     "sm_q4_matmul_noalloc": (i32, [vp, vp, i64, i64, vp, i32, i64, i64, vp, i64, i32, vp]),
     "sm_q4_gemv_multi_plan": (i64, [vp, i64, vp]),
@@ -73,6 +75,7 @@ SIGNATURES: dict[str, tuple] = {
     "sm_moe_plan_words": (i64, [i64, i64, i64]),
     "sm_moe_router_top2": (i32, [vp, i32, vp, i64, i64, i64, vp, vp, vp, vp]),
     "sm_moe_route_plan": (i32, [vp, i64, i64, i64, vp, vp, vp]),
+    "sm_moe_route_plan_logits": (i32, [vp, i64, i64, vp, vp, vp, vp, vp]),
     "sm_q4_grouped_matmul": (i32, [vp, vp, i64, i64, i64, vp, i32, i64, i32, vp, i64, i64, vp, i64,
                                    i32, vp]),
     "sm_moe_combine": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),

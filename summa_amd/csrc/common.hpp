@@ -224,9 +224,12 @@ __device__ inline void split_f16(float x, _Float16& hi, _Float16& lo) {
 // The squares meet in LDS (sq [V][64]) so that wave 0 sums them in the order
 // of a one-wave-per-row norm (lane l over float4s l, 64 + l, ... then one wave
 // reduction); then x / rms * gamma, split into hi | lo halves of the row.
+// pair_out (optional): the four values as the pair holds them, hi + lo in f32
+// (what a consumer of the pair row reads back).
 template <int V>
 __device__ inline void row_rmsnorm_pair(const float4& v, const float4& g, float eps,
-                                        float4 (&sq)[V][64], float& rms_s, _Float16* row) {
+                                        float4 (&sq)[V][64], float& rms_s, _Float16* row,
+                                        float* pair_out = nullptr) {
   constexpr int D = 256 * V;
   const int wave = threadIdx.x / 64, lane = threadIdx.x % 64;
   const int c4 = wave * 64 + lane;
@@ -250,6 +253,10 @@ __device__ inline void row_rmsnorm_pair(const float4& v, const float4& g, float 
   for (int e = 0; e < 4; ++e) split_f16(o[e], hi[e], lo[e]);
   *reinterpret_cast<h4*>(row + 4 * c4) = h4{hi[0], hi[1], hi[2], hi[3]};
   *reinterpret_cast<h4*>(row + D + 4 * c4) = h4{lo[0], lo[1], lo[2], lo[3]};
+  if (pair_out) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pair_out[e] = (float)hi[e] + (float)lo[e];
+  }
 }
 
 // One prepared word -> its 8 codes q in natural k order as f16. Each 16-bit

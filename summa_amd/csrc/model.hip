@@ -69,6 +69,10 @@ int64_t sm_moe_plan_words(int64_t, int64_t, int64_t);
 int sm_moe_router_top2(const void*, int, const float*, int64_t, int64_t, int64_t, float*, int32_t*,
                        float*, void*);
 int sm_moe_route_plan(const int32_t*, int64_t, int64_t, int64_t, int32_t*, int32_t*, void*);
+int sm_q4_matmul_add_rmsnorm_router(const uint8_t*, const uint16_t*, int64_t, int64_t, const void*,
+                                    int, int64_t, int64_t, float*, const float*, float, void*,
+                                    const float*, int64_t, float*, int32_t*, float*, void*,
+                                    int64_t, void*);
 int sm_q4_grouped_matmul(const uint8_t*, const uint16_t*, int64_t, int64_t, int64_t, const void*,
                          int, int64_t, int, const int32_t*, int64_t, int64_t, void*, int64_t, int,
                          void*);
@@ -281,7 +285,7 @@ struct sm_model {
   size_t weight_bytes = 0;
   // workspace
   sm::DevBuf x, h, qkv, qb, attn, u, gv, logits, rows, ids, pos, lens, next_ids, kc, vc, rkc, rvc,
-      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, mmws, seen, done;
+      lp_tmp, flags, moe_idx, moe_w, moe_plan, moe_u, moe_y, moe_err, moe_lg, mmws, seen, done;
   // prompt groups (sm_model_set_prompt_groups): rollouts g*G .. g*G+G-1 share
   // one prompt, whose positions are computed once per group: their K / V for
   // every layer [layers][groups][KVH][P][hd] and last hidden rows [groups, d]
@@ -358,13 +362,25 @@ int linear_f32out(sm_model* m, const Linear& L, const void* x, int64_t M, float*
 // residual projection and the norm that follows it). Quantized models make it
 // one call, which at decode batch sizes sums the projection's split-K partials
 // into x and normalises the rows in one launch; elsewhere the two steps.
+// router (MoE layers, quantized models): also the router's top-2 of the normed
+// rows into m->moe_idx / m->moe_w (and, under a router trace, the logits into
+// m->moe_lg; sm_q4_matmul_add_rmsnorm_router).
 int linear_add_norm(sm_model* m, const Linear& L, const void* xin, int64_t M, float* x,
-                    const float* gamma, hipStream_t st) {
+                    const float* gamma, hipStream_t st, const float* router = nullptr) {
   const auto& c = m->cfg;
   if (c.quantized && m->act == SM_F16X2) {
     const int64_t want =
         std::min(kMatmulWs, sm_q4_matmul_workspace_bytes(M, L.N, L.K, SM_EPI_ADD_F32));
     if (want > 0) SM_TRY(ensure(m->mmws, (size_t)want));
+    if (router) {  // top-2 into moe_idx / moe_w; the logits only for a router trace
+      SM_TRY(ensure(m->moe_idx, (size_t)M * 2 * 4));
+      SM_TRY(ensure(m->moe_w, (size_t)M * 2 * 4));
+      if (m->trace_logits) SM_TRY(ensure(m->moe_lg, (size_t)M * c.experts * 4));
+      return sm_q4_matmul_add_rmsnorm_router(
+          L.codes, L.scales, L.N, L.K, xin, m->act, M, m->act_ld(L.K), x, gamma, c.norm_eps,
+          m->h.p, router, c.experts, m->trace_logits ? (float*)m->moe_lg.p : nullptr,
+          (int32_t*)m->moe_idx.p, (float*)m->moe_w.p, want > 0 ? m->mmws.p : nullptr, want, st);
+    }
     return sm_q4_matmul_add_rmsnorm(L.codes, L.scales, L.N, L.K, xin, m->act, M, m->act_ld(L.K),
                                     x, gamma, c.norm_eps, m->h.p, want > 0 ? m->mmws.p : nullptr,
                                     want, st);
@@ -387,9 +403,11 @@ int linear_swiglu(sm_model* m, const Linear& L, const void* x, int64_t M, void* 
 // x += MoE(h) for `rows` tokens: router + top-2, route plan, two grouped Q4
 // matmuls (gathered SwiGLU in, down), combine. All device side. With
 // next_norm, the combine also leaves RMSNorm(x) * next_norm in m->h (the next
-// layer's attention norm, one launch).
+// layer's attention norm, one launch). routed: the FFN norm already ran the
+// router (linear_add_norm with the router: top-2 in m->moe_idx / m->moe_w,
+// logits in m->moe_lg under a trace).
 int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st,
-            const float* next_norm = nullptr) {
+            const float* next_norm = nullptr, bool routed = false) {
   const auto& c = m->cfg;
   const int64_t E = c.experts, Fe = c.expert_ffn, d = c.d_model, k = 2;
   const int64_t routes = rows * k;
@@ -411,13 +429,17 @@ int moe_ffn(sm_model* m, const Layer& Ly, int64_t rows, hipStream_t st,
       m->trace_dropped += rows;
     }
   }
-  SM_TRY(sm_moe_router_top2(m->h.p, m->act, Ly.router, rows, d, E, trace_lg,
-                            (int32_t*)m->moe_idx.p, (float*)m->moe_w.p, st));
-  if (trace_idx)
-    SM_HIP(hipMemcpyAsync(trace_idx, m->moe_idx.p, (size_t)routes * 4, hipMemcpyDeviceToDevice,
+  if (!routed)
+    SM_TRY(sm_moe_router_top2(m->h.p, m->act, Ly.router, rows, d, E, trace_lg,
+                              (int32_t*)m->moe_idx.p, (float*)m->moe_w.p, st));
+  else if (trace_lg)
+    SM_HIP(hipMemcpyAsync(trace_lg, m->moe_lg.p, (size_t)rows * E * 4, hipMemcpyDeviceToDevice,
                           st));
   SM_TRY(sm_moe_route_plan((const int32_t*)m->moe_idx.p, rows, k, E, plan,
                            (int32_t*)m->moe_err.p, st));
+  if (trace_idx)
+    SM_HIP(hipMemcpyAsync(trace_idx, m->moe_idx.p, (size_t)routes * 4, hipMemcpyDeviceToDevice,
+                          st));
   SM_TRY(sm_q4_grouped_matmul(Ly.exp_in.codes, Ly.exp_in.scales, E, 2 * Fe, d, m->h.p, m->act,
                               m->act_ld(d), 1, plan, rows, k, m->moe_u.p, m->act_ld(Fe),
                               SM_EPI_SWIGLU_F16X2, st));
@@ -522,13 +544,16 @@ int run_layers(sm_model* m, const int32_t* ids, int64_t S, int64_t L, const int3
     else
       SM_TRY(sm_attn_prefill(m->qb.p, kl, vl, pos0, m->attn.p, m->kvt, m->act, S, L, c.heads,
                              c.kv_heads, cap, c.head_dim, st));
-    SM_TRY(linear_add_norm(m, Ly.o, m->attn.p, rows, x, Ly.ffn_norm, st));
+    // MoE layers: the FFN norm also computes the router logits
+    const bool fused_router = c.experts > 0 && c.quantized && m->act == SM_F16X2;
+    SM_TRY(linear_add_norm(m, Ly.o, m->attn.p, rows, x, Ly.ffn_norm, st,
+                           fused_router ? Ly.router : nullptr));
     if (c.experts > 0) {  // the combine with the next layer's attention norm
       if (l + 1 < c.layers) {
-        SM_TRY(moe_ffn(m, Ly, rows, st, m->layers[l + 1].attn_norm));
+        SM_TRY(moe_ffn(m, Ly, rows, st, m->layers[l + 1].attn_norm, fused_router));
         normed = true;
       } else {
-        SM_TRY(moe_ffn(m, Ly, rows, st));
+        SM_TRY(moe_ffn(m, Ly, rows, st, nullptr, fused_router));
       }
     } else {
       SM_TRY(linear_swiglu(m, Ly.in, m->h.p, rows, m->u.p, st));
@@ -753,7 +778,8 @@ std::vector<DevBuf*> model_bufs(sm_model* m) {
   return {&m->x, &m->h, &m->qkv, &m->qb, &m->attn, &m->u, &m->gv, &m->logits, &m->rows,
           &m->ids, &m->pos, &m->lens, &m->next_ids, &m->kc, &m->vc, &m->rkc, &m->rvc,
           &m->lp_tmp, &m->flags, &m->moe_idx, &m->moe_w, &m->moe_plan, &m->moe_u, &m->moe_y,
-          &m->moe_err, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow, &m->apart,
+          &m->moe_err, &m->moe_lg, &m->mmws, &m->seen, &m->done, &m->pkc, &m->pvc, &m->prow,
+          &m->apart,
           &m->pids};
 }
 
@@ -812,6 +838,7 @@ WsPlan plan_workspace(sm_model* m, int64_t S, int64_t P, int64_t N, int64_t mtpf
       plan_max(at(m->moe_u), (size_t)routes * c.expert_ffn * m->act_size);
       plan_max(at(m->moe_y), (size_t)routes * d * 4);
       plan_max(at(m->moe_err), 4);
+      plan_max(at(m->moe_lg), (size_t)rows * c.experts * 4);
     } else {
       mm(rows, 2 * (int64_t)c.ffn, d, SM_EPI_SWIGLU_F16X2);
       mm(rows, d, c.ffn, SM_EPI_ADD_F32);

@@ -62,6 +62,23 @@ constexpr int kRouterLds = 64 * 1024;  // dynamic LDS budget (h rows + logits)
 // pair. Rows past the last token repeat the last token (their results are
 // not stored), so the inner loops carry no per-token branches.
 // TH: f32, f16, or f16 pair (PAIR: row t is hi[d] | lo[d]); VEC: d % 64 == 0.
+// Top-2 of one token's E router logits, strict '>' so the first index wins
+// ties (top2_indices_kernel, moe_topk.rs:74-104), and the softmax over the
+// selected pair (ffn.rs:514).
+__device__ inline void top2_of(const float* l, int E, int& i0, int& i1, float& w0, float& w1) {
+  float v0 = -INFINITY, v1 = -INFINITY;
+  i0 = 0;
+  i1 = 0;
+  for (int e = 0; e < E; ++e) {
+    const float v = l[e];
+    if (v > v0) { v1 = v0; i1 = i0; v0 = v; i0 = e; }
+    else if (v > v1) { v1 = v; i1 = e; }
+  }
+  const float e1 = expf(v1 - v0);  // softmax over [v0, v1] (v0 >= v1)
+  w0 = 1.f / (1.f + e1);
+  w1 = e1 / (1.f + e1);
+}
+
 template <typename TH, bool PAIR, int TT, bool VEC, int CH = 0>
 __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
     const TH* __restrict__ h, const float* __restrict__ wr, int64_t tokens, int d, int E,
@@ -143,19 +160,15 @@ __global__ __launch_bounds__(kRouterThreads) void router_top2_kernel(
     const int t = threadIdx.x;
     const int64_t r = t0 + t;
     const float* l = lg + t * E;
-    float v0 = -INFINITY, v1 = -INFINITY;
-    int i0 = 0, i1 = 0;
-    for (int e = 0; e < E; ++e) {
-      const float v = l[e];
-      if (v > v0) { v1 = v0; i1 = i0; v0 = v; i0 = e; }
-      else if (v > v1) { v1 = v; i1 = e; }
+    if (top_idx) {  // (logits only when top_idx is null)
+      int i0, i1;
+      float w0, w1;
+      top2_of(l, E, i0, i1, w0, w1);
+      top_idx[r * 2] = i0;
+      top_idx[r * 2 + 1] = i1;
+      top_w[r * 2] = w0;
+      top_w[r * 2 + 1] = w1;
     }
-    // softmax over [v0, v1] (v0 >= v1)
-    const float e1 = expf(v1 - v0);
-    top_idx[r * 2] = i0;
-    top_idx[r * 2 + 1] = i1;
-    top_w[r * 2] = 1.f / (1.f + e1);
-    top_w[r * 2 + 1] = e1 / (1.f + e1);
     if (logits_out)
       for (int e = 0; e < E; ++e) logits_out[r * E + e] = l[e];
   }
@@ -281,16 +294,33 @@ __global__ __launch_bounds__(kPlanThreads) void route_plan_kernel(const int32_t*
 // expert totals and tile counts with shuffles. Output identical to
 // route_plan_kernel.
 constexpr int kPlanSmall = 1024;
+constexpr size_t kPlanLogitsLds = 64 * 1024;  // logits route_plan_small_kernel stages
 
+// With logits (top-2 routing, k = 2): route r first takes the top-2 of its
+// token's router logits [tokens, E] itself (top2_of, as router_top2_kernel),
+// writing top_idx / top_w, so a decode step needs no router launch.
 __global__ __launch_bounds__(kPlanSmall) void route_plan_small_kernel(
     const int32_t* __restrict__ idx, int routes, int k, int E, PlanView pv, int max16,
-    int max128, int32_t* __restrict__ error) {
+    int max128, int32_t* __restrict__ error, const float* __restrict__ logits = nullptr,
+    int32_t* __restrict__ top_idx = nullptr, float* __restrict__ top_w = nullptr) {
   constexpr int NW = kPlanSmall / kWave;
   __shared__ int32_t wc[NW][kMaxExperts];  // wave counts, then wave bases
   __shared__ int32_t offs[kMaxExperts];
   const int r = threadIdx.x, wave = r / kWave, lane = r % kWave;
   int e = -1;
-  if (r < routes) {
+  if (logits) {  // the logits [routes / 2, E] staged in LDS (coalesced), then scanned there
+    extern __shared__ float lgs[];
+    for (int i = r; i < (routes / 2) * E; i += kPlanSmall) lgs[i] = logits[i];
+    __syncthreads();
+    if (r < routes) {
+      int i0, i1;
+      float w0, w1;
+      top2_of(lgs + (r / 2) * E, E, i0, i1, w0, w1);
+      e = (r & 1) ? i1 : i0;
+      top_idx[r] = e;
+      top_w[r] = (r & 1) ? w1 : w0;
+    }
+  } else if (r < routes) {
     e = idx[r];
     if (e < 0 || e >= E) {
       atomicOr(error, 1);
@@ -348,6 +378,21 @@ __global__ __launch_bounds__(kPlanSmall) void route_plan_small_kernel(
     pv.inverse[r] = pos;
     pv.src_rows[pos] = r / k;
   }
+}
+
+// top_idx / top_w [tokens, 2] from router logits [tokens, E], one thread per
+// token (the batches too large for route_plan_small_kernel's fused form).
+__global__ void top2_from_logits_kernel(const float* __restrict__ logits, int64_t tokens, int E,
+                                        int32_t* __restrict__ top_idx, float* __restrict__ top_w) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (t >= tokens) return;
+  int i0, i1;
+  float w0, w1;
+  top2_of(logits + t * E, E, i0, i1, w0, w1);
+  top_idx[t * 2] = i0;
+  top_idx[t * 2 + 1] = i1;
+  top_w[t * 2] = w0;
+  top_w[t * 2 + 1] = w1;
 }
 
 // x[t, c] += sum_j w[t, j] * routed[inverse[t*k + j], c]   (f32); routes the
@@ -463,7 +508,8 @@ extern "C" int64_t sm_moe_plan_words(int64_t tokens, int64_t top_k, int64_t expe
 extern "C" int sm_moe_router_top2(const void* h, int h_dtype, const float* w_router,
                                   int64_t tokens, int64_t d, int64_t experts, float* logits_out,
                                   int32_t* top_idx, float* top_w, void* stream) {
-  SM_REQUIRE(h && w_router && top_idx && top_w, "sm_moe_router_top2: null buffer");
+  SM_REQUIRE(h && w_router && ((top_idx && top_w) || (logits_out && !top_idx && !top_w)),
+             "sm_moe_router_top2: null buffer");
   SM_REQUIRE(experts >= 2, "top-2 routing needs at least two experts");
   SM_REQUIRE(tokens >= 0 && tokens <= 0x7fffffff && d > 0 && d <= 8192 && experts <= kMaxExperts,
              "sm_moe_router_top2: bad shape (d <= 8192, experts <= %d)", kMaxExperts);
@@ -501,6 +547,34 @@ extern "C" int sm_moe_route_plan(const int32_t* top_idx, int64_t tokens, int64_t
   else
     route_plan_kernel<<<1, kPlanThreads, 0, as_stream(stream)>>>(
         top_idx, (int)routes, (int)top_k, (int)experts, pv, max16, max128, error);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+extern "C" int sm_moe_route_plan_logits(const float* logits, int64_t tokens, int64_t experts,
+                                        int32_t* top_idx, float* top_w, int32_t* plan,
+                                        int32_t* error, void* stream) {
+  SM_REQUIRE((logits || tokens == 0) && top_idx && top_w && plan && error,
+             "sm_moe_route_plan_logits: null buffer");
+  SM_REQUIRE(experts >= 2 && experts <= kMaxExperts,
+             "sm_moe_route_plan_logits: experts must be in 2..=%d", kMaxExperts);
+  SM_REQUIRE(tokens >= 0 && tokens * 2 <= 0x7fffffff, "sm_moe_route_plan_logits: bad shape");
+  const int64_t routes = tokens * 2;
+  PlanView pv = plan_view(plan, routes, experts);
+  const int max16 = (int)moe_max_tiles(routes, experts, 16);
+  const int max128 = (int)moe_max_tiles(routes, experts, 128);
+  hipStream_t st = as_stream(stream);
+  const size_t lds = (size_t)tokens * experts * sizeof(float);  // the staged logits
+  if (routes <= kPlanSmall && lds <= kPlanLogitsLds) {
+    route_plan_small_kernel<<<1, kPlanSmall, lds, st>>>(nullptr, (int)routes, 2, (int)experts, pv,
+                                                       max16, max128, error, logits, top_idx,
+                                                       top_w);
+  } else {
+    top2_from_logits_kernel<<<(unsigned)ceil_div(tokens, 256), 256, 0, st>>>(
+        logits, tokens, (int)experts, top_idx, top_w);
+    route_plan_kernel<<<1, kPlanThreads, 0, st>>>(top_idx, (int)routes, 2, (int)experts, pv,
+                                                  max16, max128, error);
+  }
   SM_LAUNCH_CHECK();
   return SM_OK;
 }

@@ -870,13 +870,30 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
 // lane issues all its partial, residual and gamma loads at once. The squares
 // meet in LDS so that wave 0 sums them in the one-wave order. Replaces the
 // reduce launch and the norm launch with one.
-template <int V, int KS>
+//
+// With a router (ROUTER, the MoE layers' FFN norm): the row's router logits
+// sum_c h[c] * wr[e, c] (SparseMoe::forward's fp32 router, ffn.rs:489-490)
+// over h as its f16 pair holds it (hi + lo, what the router kernel reads):
+// each lane multiplies its four columns by every expert's weights (all of
+// them requested at once), a wave sums the lanes, and the V wave sums are
+// added in wave order. Wave 0 then takes the row's top-2 as the sequential
+// strict '>' scan would (top2_indices_kernel, moe_topk.rs:74-104: the
+// lowest index among equal maxima; NaN never wins; an all -inf / NaN row
+// keeps the scan's initial index 0) and the softmax over the pair (ffn.rs:514),
+// into top_idx / top_w [rows, 2]; logits [rows, E] optional. This replaces
+// the router launch of a decode step.
+constexpr int kRouterMaxExperts = 64;
+
+template <int V, int KS, bool ROUTER = false>
 __global__ __launch_bounds__(64 * V) void splitk_add_rmsnorm_kernel(
     const float* __restrict__ part, int ks, int64_t rows, float* __restrict__ resid,
-    const float* __restrict__ gamma, float eps, _Float16* __restrict__ h) {
+    const float* __restrict__ gamma, float eps, _Float16* __restrict__ h,
+    const float* __restrict__ wr = nullptr, int E = 0, float* __restrict__ logits = nullptr,
+    int32_t* __restrict__ top_idx = nullptr, float* __restrict__ top_w = nullptr) {
   constexpr int D = 256 * V;
   __shared__ float4 sq[V][64];
   __shared__ float rms_s;
+  __shared__ float red[V][kRouterMaxExperts];
   const int64_t r = blockIdx.x;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int c4 = wave * kWave + lane;
@@ -902,7 +919,52 @@ __global__ __launch_bounds__(64 * V) void splitk_add_rmsnorm_kernel(
   const float4 gm = reinterpret_cast<const float4*>(gamma)[c4];
   const float4 v = make_float4(x.x + acc.x, x.y + acc.y, x.z + acc.z, x.w + acc.w);
   *xr = v;
-  row_rmsnorm_pair<V>(v, gm, eps, sq, rms_s, h + r * 2 * D);
+  float hv[4];
+  row_rmsnorm_pair<V>(v, gm, eps, sq, rms_s, h + r * 2 * D, hv);
+  if constexpr (!ROUTER) return;
+  // every expert's weights for this lane's columns requested at once (32
+  // experts per round; rows past E re-read the last expert, unused), so the
+  // router costs one L2 round trip per 32 experts
+  constexpr int EB = 32;
+  for (int e0 = 0; e0 < E; e0 += EB) {
+    float4 w[EB];
+#pragma unroll
+    for (int u = 0; u < EB; ++u)
+      w[u] = reinterpret_cast<const float4*>(wr + (size_t)min(e0 + u, E - 1) * D)[c4];
+#pragma unroll
+    for (int u = 0; u < EB; ++u) {
+      float p = hv[0] * w[u].x;
+      p = fmaf(hv[1], w[u].y, p);
+      p = fmaf(hv[2], w[u].z, p);
+      p = fmaf(hv[3], w[u].w, p);
+      p = wave_sum(p);
+      if (lane == 0 && e0 + u < E) red[wave][e0 + u] = p;
+    }
+  }
+  __syncthreads();
+  if (wave != 0) return;
+  float lv = -INFINITY;
+  if (lane < E) {
+    lv = 0.f;
+#pragma unroll
+    for (int w = 0; w < V; ++w) lv += red[w][lane];
+    if (logits) logits[r * E + lane] = lv;
+  }
+  const float key = (lv == lv) ? lv : -INFINITY;  // NaN never wins a '>'
+  const float v0 = wave_max(key);
+  int i0 = __ffsll((unsigned long long)__ballot(lane < E && key == v0)) - 1;
+  if (v0 == -INFINITY) i0 = 0;
+  const float key1 = (lane == i0) ? -INFINITY : key;
+  const float v1 = wave_max(key1);
+  int i1 = __ffsll((unsigned long long)__ballot(lane < E && lane != i0 && key1 == v1)) - 1;
+  if (v1 == -INFINITY) i1 = 0;
+  if (lane == 0) {
+    const float e1 = expf(v1 - v0);  // softmax over [v0, v1] (v0 >= v1)
+    top_idx[r * 2] = i0;
+    top_idx[r * 2 + 1] = i1;
+    top_w[r * 2] = 1.f / (1.f + e1);
+    top_w[r * 2 + 1] = e1 / (1.f + e1);
+  }
 }
 
 // K splits of the fused residual projection + RMSNorm, or 0 when the fused
@@ -1083,25 +1145,35 @@ extern "C" int sm_q4_matmul_ws(const uint8_t* codes, const uint16_t* scales, int
 extern "C" int sm_rmsnorm(const float* x, const float* gamma, int64_t rows, int64_t d, float eps,
                           void* y, int out_dtype, void* stream);
 
-extern "C" int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N,
-                                        int64_t K, const void* x, int x_dtype, int64_t M,
-                                        int64_t ldx, float* resid, const float* gamma, float eps,
-                                        void* h_out, void* workspace, int64_t workspace_bytes,
-                                        void* stream) {
-  using namespace sm;
-  SM_REQUIRE(resid && gamma && h_out, "sm_q4_matmul_add_rmsnorm: null buffer");
+extern "C" int sm_moe_router_top2(const void* h, int h_dtype, const float* w_router,
+                                  int64_t tokens, int64_t d, int64_t experts, float* logits_out,
+                                  int32_t* top_idx, float* top_w, void* stream);
+
+namespace sm {
+namespace {
+
+// sm_q4_matmul_add_rmsnorm, and with wr the router logits of the normed rows
+// (sm_q4_matmul_add_rmsnorm_router).
+int matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K,
+                       const void* x, int x_dtype, int64_t M, int64_t ldx, float* resid,
+                       const float* gamma, float eps, void* h_out, void* workspace,
+                       int64_t workspace_bytes, const float* wr, int64_t E, float* logits,
+                       int32_t* top_idx, float* top_w, void* stream) {
   const int xt = xmode_of(x_dtype);
   const int ks = (xt >= 0 && workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
-                  reinterpret_cast<uintptr_t>(h_out) % 8 == 0 && M <= 0x7fffffff &&
+                  reinterpret_cast<uintptr_t>(h_out) % 8 == 0 &&
+                  (!wr || reinterpret_cast<uintptr_t>(wr) % 16 == 0) && M <= 0x7fffffff &&
                   N <= 0x7fffffff && K > 0 && K % 128 == 0)
                      ? add_rmsnorm_splits(M, N, K, xt, workspace_bytes) : 0;
   hipStream_t st = as_stream(stream);
-  if (ks == 0) {  // the two-step form: residual projection, then the norm
+  if (ks == 0) {  // the two-step form: residual projection, then the norm (and router)
     SM_TRY(sm_q4_matmul_ws(codes, scales, N, K, x, x_dtype, M, ldx, resid, N, EPI_ADD_F32,
                            workspace, workspace_bytes, stream));
-    return sm_rmsnorm(resid, gamma, M, N, eps, h_out, SM_F16X2, stream);
+    SM_TRY(sm_rmsnorm(resid, gamma, M, N, eps, h_out, SM_F16X2, stream));
+    return wr ? sm_moe_router_top2(h_out, SM_F16X2, wr, M, N, E, logits, top_idx, top_w, stream)
+              : SM_OK;
   }
   SM_REQUIRE(codes && scales && x && ldx >= (xt == X_F16X2 ? 2 * K : K) && ldx % 8 == 0 &&
                  reinterpret_cast<uintptr_t>(codes) % 16 == 0 &&
@@ -1116,9 +1188,15 @@ extern "C" int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* sc
   else SM_TRY(launch_grouped_lds<X_F16>(a, EPI_ADD_F32, st, rt, ks, false));
   const unsigned blocks = (unsigned)M;
   _Float16* h = static_cast<_Float16*>(h_out);
-#define SM_ARK(V, KS)                                                                   \
-  splitk_add_rmsnorm_kernel<V, KS><<<blocks, 64 * V, 0, st>>>(a.part, ks, M, resid, gamma, \
-                                                              eps, h)
+#define SM_ARK(V, KS)                                                                       \
+  do {                                                                                      \
+    if (wr)                                                                                 \
+      splitk_add_rmsnorm_kernel<V, KS, true><<<blocks, 64 * V, 0, st>>>(                    \
+          a.part, ks, M, resid, gamma, eps, h, wr, (int)E, logits, top_idx, top_w);         \
+    else                                                                                    \
+      splitk_add_rmsnorm_kernel<V, KS><<<blocks, 64 * V, 0, st>>>(a.part, ks, M, resid,     \
+                                                                  gamma, eps, h);           \
+  } while (0)
 #define SM_ARN(V)                                                \
     case V:                                                      \
       if (ks == 2) SM_ARK(V, 2);                                 \
@@ -1140,6 +1218,36 @@ extern "C" int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* sc
 #undef SM_ARK
   SM_LAUNCH_CHECK();
   return SM_OK;
+}
+
+}  // namespace
+}  // namespace sm
+
+extern "C" int sm_q4_matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N,
+                                        int64_t K, const void* x, int x_dtype, int64_t M,
+                                        int64_t ldx, float* resid, const float* gamma, float eps,
+                                        void* h_out, void* workspace, int64_t workspace_bytes,
+                                        void* stream) {
+  using namespace sm;
+  SM_REQUIRE(resid && gamma && h_out, "sm_q4_matmul_add_rmsnorm: null buffer");
+  return matmul_add_rmsnorm(codes, scales, N, K, x, x_dtype, M, ldx, resid, gamma, eps, h_out,
+                            workspace, workspace_bytes, nullptr, 0, nullptr, nullptr, nullptr,
+                            stream);
+}
+
+extern "C" int sm_q4_matmul_add_rmsnorm_router(
+    const uint8_t* codes, const uint16_t* scales, int64_t N, int64_t K, const void* x,
+    int x_dtype, int64_t M, int64_t ldx, float* resid, const float* gamma, float eps, void* h_out,
+    const float* w_router, int64_t experts, float* router_logits, int32_t* top_idx,
+    float* top_w, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace sm;
+  SM_REQUIRE(resid && gamma && h_out && w_router && top_idx && top_w,
+             "sm_q4_matmul_add_rmsnorm_router: null buffer");
+  SM_REQUIRE(experts >= 2 && experts <= kRouterMaxExperts,
+             "sm_q4_matmul_add_rmsnorm_router: experts must be in 2..=%d", kRouterMaxExperts);
+  return matmul_add_rmsnorm(codes, scales, N, K, x, x_dtype, M, ldx, resid, gamma, eps, h_out,
+                            workspace, workspace_bytes, w_router, experts, router_logits, top_idx,
+                            top_w, stream);
 }
 
 extern "C" int sm_q4_grouped_matmul(const uint8_t* codes, const uint16_t* scales, int64_t experts,

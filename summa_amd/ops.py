@@ -466,6 +466,24 @@ def moe_route_plan(top_idx: torch.Tensor, experts: int) -> RoutePlan:
     return RoutePlan(words, T, k, experts, error)
 
 
+def moe_route_plan_logits(logits: torch.Tensor) -> tuple:
+    """Top-2 routing from router logits [T, E] and its stable route plan in one
+    launch (``sm_moe_route_plan_logits``; moe_topk.rs:36-104 + moe_route.rs:22).
+    Returns (top_idx [T, 2] int32, top_w [T, 2] f32, RoutePlan)."""
+    _dev(logits, "logits")
+    if logits.dtype != torch.float32:
+        raise TypeError("logits must be float32")
+    T, E = logits.shape
+    idx = torch.empty((T, 2), dtype=torch.int32, device=logits.device)
+    wts = torch.empty((T, 2), dtype=torch.float32, device=logits.device)
+    words = torch.empty(int(_lib.lib().sm_moe_plan_words(T, 2, E)), dtype=torch.int32,
+                        device=logits.device)
+    error = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    call("sm_moe_route_plan_logits", logits.data_ptr(), T, E, idx.data_ptr(), wts.data_ptr(),
+         words.data_ptr(), error.data_ptr(), _stream())
+    return idx, wts, RoutePlan(words, T, 2, E, error)
+
+
 def grouped_q4_matmul(bank: ExpertBank, x: torch.Tensor, plan: RoutePlan, *, gather: bool,
                       epilogue: int = _lib.SM_EPI_STORE_F32, pair: bool = False) -> torch.Tensor:
     """Per-expert y[p] = x[row(p)] . W_e^T over the plan's sorted positions p

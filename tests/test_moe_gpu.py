@@ -291,3 +291,119 @@ def test_moe_decoder_matches_oracle(dev):
     print(f"sequences excused by a router near-tie: {len(excused)}, min gap {gaps.min():.2e}",
           flush=True)
     assert len(excused) <= S // 2
+
+
+# --------------------------------------------- fused decode-step routing ---
+
+@pytest.mark.parametrize("T,E", [(1, 2), (128, 32), (512, 64), (700, 32), (4096, 8)])
+def test_route_plan_from_logits_equals_two_steps(dev, T, E):
+    """sm_moe_route_plan_logits (the top-2 of router logits and the route plan
+    in one launch for up to 512 tokens, a top-2 kernel then the plan kernel
+    above) equals sm_moe_router_top2's top-2 of the same logits and
+    sm_moe_route_plan of those indices, bit for bit."""
+    print(f"case plan from logits T={T} E={E}", flush=True)
+    rng = np.random.default_rng(T * 3 + E)
+    d = 256
+    h = torch.from_numpy(rng.normal(0, 1, (T, d)).astype(np.float32)).to(dev)
+    wr = torch.from_numpy(rng.normal(0, 1 / np.sqrt(d), (E, d)).astype(np.float32)).to(dev)
+    if T >= 4:  # exact ties: identical router rows
+        wr[E // 2] = wr[0]
+    idx0, w0, logits = ops.moe_top2_indices(h, wr, want_logits=True)
+    plan0 = ops.moe_route_plan(idx0, E)
+    idx1, w1, plan1 = ops.moe_route_plan_logits(logits)
+    torch.cuda.synchronize()
+    assert torch.equal(idx0, idx1)
+    assert torch.equal(w0, w1)
+    assert _plan_content(plan0) == _plan_content(plan1)
+    assert int(plan1.error.cpu()[0]) == 0
+
+
+def _plan_content(plan):
+    """The defined words of a route plan: counts, offsets, order, inverse,
+    src_rows and both tile lists up to their lengths (the unused tail of a
+    tile list is never written)."""
+    R, E = plan.tokens * plan.top_k, plan.experts
+    w = plan.words.cpu().numpy()
+    at = 2 * E + 1 + 3 * R
+    out = [w[:at].tolist()]
+    for rows in (16, 128):
+        cap = -(-R // rows) + E
+        n = int(w[at])
+        out.append(w[at + 1:at + 1 + 2 * n].tolist())
+        at += 1 + 2 * cap
+    return out
+
+
+@pytest.mark.parametrize("m,n,k,E", [(128, 2048, 2048, 32), (64, 1024, 2048, 8),
+                                     (200, 2048, 5632, 64), (600, 2048, 2048, 32)])
+def test_add_rmsnorm_router_equals_separate_router(dev, m, n, k, E):
+    """sm_q4_matmul_add_rmsnorm_router (config[4]'s decode FFN norm with the
+    router and its top-2 in the same launch) against sm_q4_matmul_add_rmsnorm
+    followed by sm_moe_router_top2 on its output: residual and normed rows
+    bit-identical; logits within f32 summation order of each other and of f64
+    over the pair values; the top-2 equal to the strict first-index scan of the
+    fused logits (the same scan over the separate router's logits wherever the
+    top-2 set is not a near-tie); a prefill-size M (600) falls back to the
+    separate router kernel and matches it exactly. Exact ties (two identical
+    router rows) keep the lower index."""
+    print(f"case add+rmsnorm+router m={m} n={n} k={k} E={E}", flush=True)
+    st = torch.cuda.current_stream().cuda_stream
+    rng = np.random.default_rng(m + n + E)
+    w = rng.normal(0, 0.02, (n, k)).astype(np.float32)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    xd = ops.f16_pair(torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float32)).to(dev))
+    base = rng.normal(0, 1, (m, n)).astype(np.float32)
+    gamma = torch.from_numpy(rng.uniform(0.5, 1.5, n).astype(np.float32)).to(dev)
+    wr_h = rng.normal(0, 1 / np.sqrt(n), (E, n)).astype(np.float32)
+    wr_h[E - 1] = wr_h[1]  # an exact tie between experts 1 and E - 1
+    wr = torch.from_numpy(wr_h).to(dev)
+    ws = ops.q4_workspace(m, n, k, _lib.SM_EPI_ADD_F32, dev)
+    eps = 1e-5
+
+    def run(router):
+        r = torch.from_numpy(base.copy()).to(dev)
+        h = torch.empty((m, 2 * n), dtype=torch.float16, device=dev)
+        if router:
+            lg = torch.full((m, E), float("nan"), dtype=torch.float32, device=dev)
+            idx = torch.full((m, 2), -7, dtype=torch.int32, device=dev)
+            wts = torch.full((m, 2), float("nan"), dtype=torch.float32, device=dev)
+            _lib.call("sm_q4_matmul_add_rmsnorm_router", qw.tcodes.data_ptr(),
+                      qw.tscales.data_ptr(), n, k, xd.data_ptr(), _lib.SM_F16X2, m, 2 * k,
+                      r.data_ptr(), gamma.data_ptr(), eps, h.data_ptr(), wr.data_ptr(), E,
+                      lg.data_ptr(), idx.data_ptr(), wts.data_ptr(), ws.data_ptr(), ws.numel(),
+                      st)
+        else:
+            _lib.call("sm_q4_matmul_add_rmsnorm", qw.tcodes.data_ptr(), qw.tscales.data_ptr(), n,
+                      k, xd.data_ptr(), _lib.SM_F16X2, m, 2 * k, r.data_ptr(), gamma.data_ptr(),
+                      eps, h.data_ptr(), ws.data_ptr(), ws.numel(), st)
+            idx, wts, lg = ops.moe_top2_indices(h, wr, want_logits=True, pair=True)
+        torch.cuda.synchronize()
+        return r, h, lg, idx, wts
+
+    r1, h1, l1, i1, w1 = run(True)
+    r0, h0, l0, i0, w0 = run(False)
+    assert torch.equal(r1, r0) and torch.equal(h1, h0)
+    assert torch.isfinite(l1).all()
+    hv = ops.unpair(h1).double().cpu().numpy()
+    ref = hv @ wr.double().cpu().numpy().T
+    bound = np.abs(hv) @ np.abs(wr.double().cpu().numpy().T)
+    for got in (l1, l0):
+        assert np.all(np.abs(got.cpu().numpy() - ref) <= 2e-6 * bound + 1e-7)
+    lg = l1.cpu().numpy()
+    top = np.argsort(-lg, axis=1, kind="stable")[:, :2]  # == the strict '>' first-index scan
+    np.testing.assert_array_equal(i1.cpu().numpy(), top)
+    v0 = np.take_along_axis(lg, top[:, :1], 1)[:, 0].astype(np.float64)
+    v1 = np.take_along_axis(lg, top[:, 1:], 1)[:, 0].astype(np.float64)
+    e1 = np.exp(v1 - v0)
+    np.testing.assert_allclose(w1.cpu().numpy()[:, 1], e1 / (1 + e1), rtol=1e-6, atol=1e-7)
+    np.testing.assert_allclose(w1.cpu().numpy()[:, 0], 1 / (1 + e1), rtol=1e-6, atol=1e-7)
+    # expert E - 1 ties with expert 1: it can only be the second choice, after 1
+    ii = i1.cpu().numpy()
+    has = (ii == E - 1).any(1)
+    assert np.all(ii[has, 0] == 1) and np.all(ii[has, 1] == E - 1)
+    srt = np.sort(ref, 1)[:, ::-1]
+    clear = (srt[:, 1] - srt[:, 2] > 1e-4) & (srt[:, 0] - srt[:, 1] > 1e-4)
+    np.testing.assert_array_equal(i1.cpu().numpy()[clear], i0.cpu().numpy()[clear])
+    if m > 512:  # the two-step fallback runs the router kernel itself
+        assert torch.equal(l1, l0) and torch.equal(i1, i0) and torch.equal(w1, w0)
