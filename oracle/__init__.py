@@ -8,13 +8,16 @@ checker. The product library ``summa_amd`` never imports it.
 from __future__ import annotations
 
 import ctypes as C
+import os
 import subprocess
 from pathlib import Path
 
 import numpy as np
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "liboracle.so"
+# SUMMA_ORACLE_LIB selects another build of the checker (the AddressSanitizer
+# one, `make -C oracle asan`)
+LIB_PATH = Path(os.environ.get("SUMMA_ORACLE_LIB", HERE / "liboracle.so"))
 
 _lib = None
 

@@ -7,9 +7,13 @@ every op raises.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libsumma_amd.so"
+# SUMMA_AMD_LIB selects another build of the library (the AddressSanitizer
+# build of the host code, python -m summa_amd.build --asan)
+LIB_PATH = Path(os.environ.get("SUMMA_AMD_LIB",
+                               Path(__file__).resolve().parent / "libsumma_amd.so"))
 
 SM_OK = 0
 SM_F32, SM_BF16, SM_F16, SM_F16X2 = 0, 1, 2, 3

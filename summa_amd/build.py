@@ -40,9 +40,15 @@ COMMON_FLAGS = [
 ]
 
 
-def _compile(src: Path) -> Path:
-    obj = OBJ / (src.stem + ".o")
-    cmd = [HIPCC, *COMMON_FLAGS, "-c", str(src), "-o", str(obj)]
+# AddressSanitizer on the host side only (the argument checks, plans and
+# HQUANT parsing that run on the CPU); device code is built as usual.
+ASAN_FLAGS = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fno-omit-frame-pointer",
+              "-Xarch_host", "-g"]
+
+
+def _compile(src: Path, obj_dir: Path = OBJ, extra=()) -> Path:
+    obj = obj_dir / (src.stem + ".o")
+    cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stderr}")
@@ -76,6 +82,30 @@ def build(verbose: bool = True) -> Path:
     return LIB
 
 
+def build_asan(verbose: bool = True) -> Path:
+    """The library with AddressSanitizer on its host code, in summa_amd/_asan/
+    (for the CPU test suite: SUMMA_AMD_LIB=summa_amd/_asan/libsumma_amd.so
+    with clang's ASan runtime preloaded)."""
+    out_dir = PKG / "_asan"
+    out_dir.mkdir(exist_ok=True)
+    sources = sorted(CSRC.glob("*.hip"))
+    jobs = min(len(sources), int(os.environ.get("MAX_JOBS", "8")))
+    with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
+        objs = list(pool.map(lambda src: _compile(src, out_dir, ASAN_FLAGS), sources))
+    lib = out_dir / "libsumma_amd.so"
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-fsanitize=address",
+           *map(str, objs), "-o", str(lib)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    if verbose:
+        print(f"built {lib} (host AddressSanitizer)", flush=True)
+    return lib
+
+
 if __name__ == "__main__":
-    build()
+    if "--asan" in sys.argv[1:]:
+        build_asan()
+    else:
+        build()
     sys.exit(0)
