@@ -932,29 +932,38 @@ def bench_policy_update(args) -> dict:
     rewards = torch.rand(1, G, device=dev)
     st = torch.cuda.current_stream()
     e0, e1, e2 = _events(3)
-    prep, step = [], []
-    for i in range(args.warmup + args.steps):
-        e0.record(st)
-        out = pol.prepare(ref, prompts, tok, beh, rewards)
-        e1.record(st)
-        pol.optimizer_step(1.0)
-        e2.record(st)
-        torch.cuda.synchronize()
-        if i == 0:  # the policy still equals the model that rolled out
-            lp_gap = float((out["lp_cur"] - beh).abs().max())
-        if i >= args.warmup:
-            prep.append(e0.elapsed_time(e1))
-            step.append(e1.elapsed_time(e2))
-        log(f"bench: policy update {i}: prepare {e0.elapsed_time(e1):.1f} ms, "
-            f"optimizer step {e1.elapsed_time(e2):.1f} ms")
-    p_ms, s_ms = sum(prep) / len(prep), sum(step) / len(step)
+    by_planes, lp_gap = {}, None
+    # the f32-grade three-plane GEMMs (the headline), then 16-bit and bf16
+    # operands (the reference's CUDA-path matmul precision)
+    for planes in (3, 2, 1):
+        pol.set_matmul_planes(planes)
+        prep, step = [], []
+        for i in range(args.warmup + args.steps):
+            e0.record(st)
+            out = pol.prepare(ref, prompts, tok, beh, rewards)
+            e1.record(st)
+            pol.optimizer_step(1.0)
+            e2.record(st)
+            torch.cuda.synchronize()
+            if lp_gap is None:  # the policy still equals the model that rolled out
+                lp_gap = float((out["lp_cur"] - beh).abs().max())
+            if i >= args.warmup:
+                prep.append(e0.elapsed_time(e1))
+                step.append(e1.elapsed_time(e2))
+            log(f"bench: policy update planes={planes} {i}: prepare {e0.elapsed_time(e1):.1f} ms, "
+                f"optimizer step {e1.elapsed_time(e2):.1f} ms")
+        by_planes[str(planes)] = {"prepare_ms": round(sum(prep) / len(prep), 2),
+                                  "optimizer_step_ms": round(sum(step) / len(step), 2)}
+    p_ms, s_ms = by_planes["3"]["prepare_ms"], by_planes["3"]["optimizer_step_ms"]
     positions = G * (P + N - 1)
     return {"metric": "GRPO policy update positions/s (config[2], one group per call)",
             "value": positions / ((p_ms + s_ms) / 1e3), "unit": "positions/s",
-            "ms_per_step": p_ms + s_ms, "dtype": "f32 masters, Q4G128 fake-quantized forward",
+            "ms_per_step": p_ms + s_ms,
+            "dtype": "f32 masters, Q4G128 fake-quantized forward, three-plane bf16 GEMMs",
             "config": {"workload": "policy_update config[2]", "rollouts": G, "prompt_len": P,
                        "new_tokens": N},
             "prepare_ms": round(p_ms, 2), "optimizer_step_ms": round(s_ms, 2),
+            "by_matmul_planes": by_planes,
             "parameters": int(Ly * (qn * d + d * mc.heads * mc.head_dim + 3 * F * d + 2 * d)
                               + 2 * V * d + d),
             "first_prepare_lp_vs_rollout_max_abs": lp_gap}

@@ -529,6 +529,11 @@ int sm_swiglu_backward(const void* gate_value, const void* grad, int dtype, int6
  *   products of weight >= 2^-16 are accumulated in f32, an f32 GEMM up to the
  *   order of its additions (the bf16 operands of matmul_2 / linear on the
  *   reference's CUDA path, matmul.rs:73-82, 132-143, with f32 results).
+ * sm_gemm_planes: sm_gemm_mfma with `planes` bf16 planes per operand: 3 as
+ *   sm_gemm_mfma; 2: hi + lo planes, three products (16-bit operands, each
+ *   product within about 2^-15 relative); 1: the bf16-rounded operands' product
+ *   accumulated in f32, which is the reference's CUDA-path matmul
+ *   (matmul.rs:73-82, 132-143: bf16 operands). Other values fail.
  * sm_rmsnorm_backward: dx (= or += with accumulate) and dgamma (nullable; =
  *   or += ; summed over rows in order) of y = x / sqrt(mean x^2 + eps) * gamma
  *   (norm.rs:36-50); rinv_scratch [rows].
@@ -552,6 +557,9 @@ int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float 
 int sm_gemm_mfma(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                  const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
                  int64_t ldc, void* stream);
+int sm_gemm_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                   float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
+                   float beta, float* C, int64_t ldc, void* stream);
 int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy, int64_t rows,
                         int64_t d, float eps, int accumulate, float* dx, float* dgamma,
                         float* rinv_scratch, void* stream);
@@ -779,7 +787,11 @@ int sm_rl_prepare(sm_model* policy, sm_model* reference, const int32_t* prompts,
  * sm_policy_install: the master weights into an inference model
  *   (sm_model_set_tensor per tensor: quantized models re-quantize).
  * sm_policy_get_tensor: a master weight (gradient = 0) or its staged
- *   gradient (gradient = 1) into dst. */
+ *   gradient (gradient = 1) into dst.
+ * sm_policy_set_matmul_planes: the bf16 planes per operand of the prepare's
+ *   GEMMs (sm_gemm_planes): 3 (the default, f32-grade), 2 (16-bit operands) or
+ *   1 (bf16 operands with f32 accumulation: the precision of the reference's
+ *   CUDA-path training matmul, matmul.rs:73-82, 132-143). */
 typedef struct sm_policy sm_policy;
 typedef struct sm_optimizer_config {
   float lr, beta1, beta2, eps, weight_decay;
@@ -789,6 +801,7 @@ typedef struct sm_optimizer_config {
 int sm_policy_create(const sm_model_config* cfg, const sm_optimizer_config* opt,
                      sm_policy** out);
 int sm_policy_destroy(sm_policy* policy);
+int sm_policy_set_matmul_planes(sm_policy* policy, int planes);
 int sm_policy_set_tensor(sm_policy* policy, int kind, int layer, const float* src, void* stream);
 int sm_policy_get_tensor(const sm_policy* policy, int kind, int layer, float* dst, int gradient,
                          void* stream);

@@ -91,6 +91,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_swiglu_backward": (i32, [vp, vp, i32, i64, i64, vp, vp]),
     "sm_gemm_ex": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp]),
     "sm_gemm_mfma": (i32, [i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64, vp]),
+    "sm_gemm_planes": (i32, [i32, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64,
+                             vp]),
     "sm_rmsnorm_backward": (i32, [vp, vp, vp, i64, i64, f32, i32, vp, vp, vp, vp]),
     "sm_rope_qk": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp]),
     "sm_attn_backward_f32": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, vp,
@@ -124,6 +126,7 @@ SIGNATURES: dict[str, tuple] = {
                             vp, vp, vp, vp, vp, vp]),
     "sm_policy_create": (i32, [vp, vp, vp]),
     "sm_policy_destroy": (i32, [vp]),
+    "sm_policy_set_matmul_planes": (i32, [vp, i32]),
     "sm_policy_set_tensor": (i32, [vp, i32, i32, vp, vp]),
     "sm_policy_get_tensor": (i32, [vp, i32, i32, vp, i32, vp]),
     "sm_policy_install": (i32, [vp, vp, vp]),

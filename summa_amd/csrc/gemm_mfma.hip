@@ -3,28 +3,38 @@
 // Newton-Schulz): C = alpha op(A) op(B) + beta C with op = identity or
 // transpose, f32 in and out, any shape and leading dimensions. The reference
 // trains through Burn's matmul (summa-llm/src/model/matmul.rs:132-143; bf16
-// operands on its CUDA path, f32 on its CPU path); this keeps f32 results.
+// operands on its CUDA path, f32 on its CPU path).
 //
-// Each f32 operand value is split exactly into three bf16 planes,
-// x = x0 + x1 + x2 (round to nearest even at each step: 24 significant bits,
-// f32's own precision; bf16 has f32's exponent range, so no scaling is
-// needed), and a product x y is the sum of the six plane products of weight
-// >= 2^-16 relative (x2 y0, x1 y1, x0 y2, x1 y0, x0 y1, x0 y0, smallest
-// first), accumulated in f32 by v_mfma_f32_32x32x16_bf16. The dropped terms
-// (x1 y2, x2 y1, x2 y2) are below 2^-23 relative, so the result is an f32
-// GEMM's up to the order of its f32 additions.
+// Each f32 operand value is split into P bf16 planes, round to nearest even
+// at each step (bf16 has f32's exponent range, so no scaling is needed):
+// - P = 3 (the default): x = x0 + x1 + x2 exactly (24 significant bits, f32's
+//   own precision), and a product x y is the sum of the six plane products of
+//   weight >= 2^-16 relative (x2 y0, x1 y1, x0 y2, x1 y0, x0 y1, x0 y0,
+//   smallest first). The dropped terms (x1 y2, x2 y1, x2 y2) are below 2^-23
+//   relative, so the result is an f32 GEMM's up to the order of its f32
+//   additions.
+// - P = 2: x = x0 + x1 + r with |r| <= 2^-17 |x|, products x1 y0, x0 y1,
+//   x0 y0: each product within about 2^-15 relative (16-bit operands).
+// - P = 1: x0 y0, the product of the bf16-rounded operands (each within 2^-9
+//   relative): the reference's CUDA-path matmul, bf16 operands with f32
+//   accumulation.
+// Products are accumulated in f32 by v_mfma_f32_32x32x16_bf16.
 //
 // Workgroup = 128 x 128 output tile, 4 waves of 64 x 64 (2 x 2 blocks of
-// 32 x 32); K in steps of 32. Each thread holds 16 consecutive k of one row
-// of each operand tile (16-byte loads when k is the contiguous dimension,
-// else scalar loads that are coalesced along the rows), splits them once into
-// the three planes and stores them to LDS as [plane][row][k] bf16, rows
-// padded to 40 elements so that the 16-byte writes and fragment reads of
-// consecutive rows spread over the banks; the next step's loads are in
-// flight while the current step's MFMAs run. One LDS buffer (60 KB), two
-// workgroups per CU. Per 16-k slice a wave reads its 2 + 2 fragments of each
-// plane and issues the 24 MFMAs product by product across its four blocks,
-// so four independent accumulations separate two dependent ones.
+// 32 x 32); K in steps of 32. Each thread loads 16 values of each operand
+// tile per step, splits them once into the planes and stores them to LDS as
+// [plane][row][k] bf16, rows padded to 40 elements so that the 16-byte writes
+// and fragment reads of consecutive rows spread over the banks; the next
+// step's loads are in flight while the current step's MFMAs run. A thread
+// holds 16 consecutive k of one row: four 16-byte loads when k is the
+// operand's contiguous dimension, else 16 scalar loads, each instruction 64
+// consecutive rows. (16-byte loads along the rows of a transposed operand, a
+// thread holding 4 rows x 4 k, measured 1.1-1.6x slower at the policy
+// update's shapes: their 8-byte LDS stores conflict.) One LDS buffer (20 KB
+// per plane), two workgroups per CU. Per 16-k slice a
+// wave reads its 2 + 2 fragments of each plane and issues the MFMAs product
+// by product across its four blocks, so four independent accumulations
+// separate two dependent ones.
 #include "common.hpp"
 
 namespace sm {
@@ -37,41 +47,45 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int kBM = 128, kBK = 32, kRS = kBK + 8;  // tile rows, k per step, LDS row stride
 constexpr int kPlane = kBM * kRS;                   // bf16 per plane of one operand tile
 
-// (a, b) -> bf16 planes with v = p0 + p1 + p2 exactly (finite v), as packed
-// words (a in the low half).
-__device__ inline void split3x2(float a, float b, uint32_t& p0, uint32_t& p1, uint32_t& p2) {
-  p0 = pack_bf16x2(a, b);
-  const float ra = a - bf16lo(p0), rb = b - bf16hi(p0);
-  p1 = pack_bf16x2(ra, rb);
-  p2 = pack_bf16x2(ra - bf16lo(p1), rb - bf16hi(p1));
+// (a, b) -> P bf16 planes as packed words (a in the low half); for P = 3,
+// v = p0 + p1 + p2 exactly (finite v)
+template <int P>
+__device__ inline void split_pair(float a, float b, uint32_t (&w)[P]) {
+  w[0] = pack_bf16x2(a, b);
+  if constexpr (P > 1) {
+    const float ra = a - bf16lo(w[0]), rb = b - bf16hi(w[0]);
+    w[1] = pack_bf16x2(ra, rb);
+    if constexpr (P > 2) w[2] = pack_bf16x2(ra - bf16lo(w[1]), rb - bf16hi(w[1]));
+  }
 }
 
-// 8 consecutive k of one row -> the three planes at LDS offset o (16 bytes each)
+// 8 consecutive k of one row -> the P planes at LDS offset o (16 bytes each)
+template <int P>
 __device__ inline void store8(const float* v, __bf16* lds, int o) {
-  u32x4 w0, w1, w2;
+  u32x4 w[P];
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    uint32_t x0, x1, x2;
-    split3x2(v[2 * i], v[2 * i + 1], x0, x1, x2);
-    w0[i] = x0; w1[i] = x1; w2[i] = x2;
+    uint32_t x[P];
+    split_pair<P>(v[2 * i], v[2 * i + 1], x);
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[p][i] = x[p];
   }
-  *reinterpret_cast<u32x4*>(lds + o) = w0;
-  *reinterpret_cast<u32x4*>(lds + kPlane + o) = w1;
-  *reinterpret_cast<u32x4*>(lds + 2 * kPlane + o) = w2;
+#pragma unroll
+  for (int p = 0; p < P; ++p) *reinterpret_cast<u32x4*>(lds + p * kPlane + o) = w[p];
 }
 
 // One operand tile (128 rows x 32 k) of X, element (r, k) at X[r * ld + k]
 // when KC (k contiguous), else at X[k * ld + r]; 16 values per thread.
 // Thread t: 16 consecutive k of one row, v[i] = (row, k + i): KC: row t / 2,
-// k 16 (t % 2) (four 16-byte loads); otherwise row t % 128, k 16 (t / 128)
-// (one scalar load per k, each instruction 64 consecutive rows). Out-of-range
-// elements are 0.
+// k 16 (t % 2) (four 16-byte loads when `vec`); otherwise row t % 128,
+// k 16 (t / 128) (one scalar load per k, each instruction 64 consecutive
+// rows). Out-of-range elements are 0.
 template <bool KC>
 struct TileLoader {
   const float* X;
   int64_t ld;
   int r0, R, K;
-  bool vec;  // aligned vectors along the contiguous dimension (uniform)
+  bool vec;  // 16-byte aligned rows along k (uniform; KC only)
   int ra, ka;
   __device__ inline void init(int t) {
     ra = KC ? t / 2 : t % kBM;
@@ -99,20 +113,36 @@ struct TileLoader {
         v[i] = (gr < R && gk + i < K) ? X[(int64_t)min(gk + i, K - 1) * ld + c] : 0.f;
     }
   }
-  // this thread's values as three planes into the LDS tile [plane][row][k]
+  // this thread's values as P planes into the LDS tile [plane][row][k]
+  template <int P>
   __device__ inline void store(const float (&v)[16], __bf16* lds) const {
-    store8(v, lds, ra * kRS + ka);
-    store8(v + 8, lds, ra * kRS + ka + 8);
+    store8<P>(v, lds, ra * kRS + ka);
+    store8<P>(v + 8, lds, ra * kRS + ka + 8);
   }
 };
 
-template <bool TA, bool TB>
-__global__ __launch_bounds__(256, 2) void gemm_bf16x3_kernel(
+// plane pairs (pa, pb) of each product, smallest weight first
+template <int P> struct Products;
+template <> struct Products<3> {
+  static constexpr int n = 6;
+  static constexpr int a[6] = {2, 1, 0, 1, 0, 0}, b[6] = {0, 1, 2, 0, 1, 0};
+};
+template <> struct Products<2> {
+  static constexpr int n = 3;
+  static constexpr int a[3] = {1, 0, 0}, b[3] = {0, 1, 0};
+};
+template <> struct Products<1> {
+  static constexpr int n = 1;
+  static constexpr int a[1] = {0}, b[1] = {0};
+};
+
+template <bool TA, bool TB, int P>
+__global__ __launch_bounds__(256, 2) void gemm_planes_kernel(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, int M, int N, int K, float alpha, float beta, int vec_a,
     int vec_b) {
-  __shared__ __attribute__((aligned(16))) __bf16 As[3 * kPlane];
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[3 * kPlane];
+  __shared__ __attribute__((aligned(16))) __bf16 As[P * kPlane];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[P * kPlane];
   const int t = threadIdx.x, wave = t / kWave, lane = t % kWave;
   const int wm = wave / 2, wn = wave % 2;
   const int m0 = (int)blockIdx.y * kBM, n0 = (int)blockIdx.x * kBM;
@@ -125,8 +155,8 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16x3_kernel(
   float va[16], vb[16];
   la.load(0, va);
   lb.load(0, vb);
-  la.store(va, As);
-  lb.store(vb, Bs);
+  la.template store<P>(va, As);
+  lb.template store<P>(vb, Bs);
   __syncthreads();
 
   f32x16 acc[2][2];
@@ -146,9 +176,9 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16x3_kernel(
     }
 #pragma unroll
     for (int ks = 0; ks < kBK; ks += 16) {
-      bf16x8 a[3][2], b[3][2];
+      bf16x8 a[P][2], b[P][2];
 #pragma unroll
-      for (int p = 0; p < 3; ++p)
+      for (int p = 0; p < P; ++p)
 #pragma unroll
         for (int i = 0; i < 2; ++i) {
           a[p][i] = *reinterpret_cast<const bf16x8*>(As + p * kPlane + (wm * 64 + i * 32) * kRS +
@@ -156,21 +186,19 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16x3_kernel(
           b[p][i] = *reinterpret_cast<const bf16x8*>(Bs + p * kPlane + (wn * 64 + i * 32) * kRS +
                                                      fo + ks);
         }
-      // plane pairs (pa, pb), smallest weight first
-      constexpr int PA[6] = {2, 1, 0, 1, 0, 0}, PB[6] = {0, 1, 2, 0, 1, 0};
 #pragma unroll
-      for (int q = 0; q < 6; ++q)
+      for (int q = 0; q < Products<P>::n; ++q)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[PA[q]][i], b[PB[q]][j],
-                                                                 acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                a[Products<P>::a[q]][i], b[Products<P>::b[q]][j], acc[i][j], 0, 0, 0);
     }
     if (more) {
       __syncthreads();  // every wave is done with this step's tiles
-      la.store(va, As);
-      lb.store(vb, Bs);
+      la.template store<P>(va, As);
+      lb.template store<P>(vb, Bs);
       __syncthreads();
     }
   }
@@ -191,11 +219,25 @@ __global__ __launch_bounds__(256, 2) void gemm_bf16x3_kernel(
     }
 }
 
+template <int P>
+void launch_planes(bool ta, bool tb, dim3 grid, hipStream_t st, const float* A, int64_t lda,
+                   const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
+                   float alpha, float beta, int vec_a, int vec_b) {
+#define SM_GB(TA, TB)                                                                      \
+  gemm_planes_kernel<TA, TB, P><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K,    \
+                                                       alpha, beta, vec_a, vec_b)
+  if (ta && tb) SM_GB(true, true);
+  else if (ta) SM_GB(true, false);
+  else if (tb) SM_GB(false, true);
+  else SM_GB(false, false);
+#undef SM_GB
+}
+
 }  // namespace
 
-int gemm_bf16x3(bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
-                int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
-                hipStream_t st) {
+int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
+                const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+                int64_t ldc, hipStream_t st) {
   // 16-byte loads along k need aligned rows (op(A) rows of an untransposed
   // A, op(B) columns of a transposed B)
   auto aligned = [](const float* p, int64_t ld) {
@@ -203,32 +245,56 @@ int gemm_bf16x3(bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha, 
   };
   const int vec_a = !ta && aligned(A, lda), vec_b = tb && aligned(B, ldb);
   const dim3 grid((unsigned)ceil_div(N, kBM), (unsigned)ceil_div(M, kBM));
-#define SM_GB(TA, TB)                                                                          \
-  gemm_bf16x3_kernel<TA, TB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, (int)M, (int)N,     \
-                                                   (int)K, alpha, beta, vec_a, vec_b)
-  if (ta && tb) SM_GB(true, true);
-  else if (ta) SM_GB(true, false);
-  else if (tb) SM_GB(false, true);
-  else SM_GB(false, false);
-#undef SM_GB
+  if (planes == 1)
+    launch_planes<1>(ta, tb, grid, st, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, alpha,
+                     beta, vec_a, vec_b);
+  else if (planes == 2)
+    launch_planes<2>(ta, tb, grid, st, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, alpha,
+                     beta, vec_a, vec_b);
+  else
+    launch_planes<3>(ta, tb, grid, st, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, alpha,
+                     beta, vec_a, vec_b);
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
 
 }  // namespace sm
 
+namespace {
+int check_gemm(const char* fn, int64_t M, int64_t N, int64_t K, const float* A, int64_t lda,
+               const float* B, int64_t ldb, const float* C, int64_t ldc, int trans_a,
+               int trans_b) {
+  using namespace sm;
+  SM_REQUIRE(A && B && C, "%s: null buffer", fn);
+  SM_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1 << 30) && N < (1 << 30) && K < (1 << 30),
+             "%s: bad shape", fn);
+  SM_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N,
+             "%s: leading dimension too small", fn);
+  if (M == 0 || N == 0) return SM_OK;
+  SM_REQUIRE(K > 0, "%s: K must be positive", fn);
+  SM_REQUIRE(ceil_div(M, 128) <= 65535, "%s: M above 65535 x 128 rows", fn);
+  return SM_OK;
+}
+}  // namespace
+
 extern "C" int sm_gemm_mfma(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                             float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
                             float beta, float* C, int64_t ldc, void* stream) {
   using namespace sm;
-  SM_REQUIRE(A && B && C, "sm_gemm_mfma: null buffer");
-  SM_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1 << 30) && N < (1 << 30) && K < (1 << 30),
-             "sm_gemm_mfma: bad shape");
-  SM_REQUIRE(lda >= (trans_a ? M : K) && ldb >= (trans_b ? K : N) && ldc >= N,
-             "sm_gemm_mfma: leading dimension too small");
+  SM_TRY(check_gemm("sm_gemm_mfma", M, N, K, A, lda, B, ldb, C, ldc, trans_a, trans_b));
   if (M == 0 || N == 0) return SM_OK;
-  SM_REQUIRE(K > 0, "sm_gemm_mfma: K must be positive");
-  SM_REQUIRE(ceil_div(M, 128) <= 65535, "sm_gemm_mfma: M above 65535 x 128 rows");
-  return gemm_bf16x3(trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
+  return gemm_planes(3, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
                      as_stream(stream));
+}
+
+extern "C" int sm_gemm_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N,
+                              int64_t K, float alpha, const float* A, int64_t lda, const float* B,
+                              int64_t ldb, float beta, float* C, int64_t ldc, void* stream) {
+  using namespace sm;
+  SM_REQUIRE(planes >= 1 && planes <= 3, "sm_gemm_planes: planes must be 1, 2 or 3 (got %d)",
+             planes);
+  SM_TRY(check_gemm("sm_gemm_planes", M, N, K, A, lda, B, ldb, C, ldc, trans_a, trans_b));
+  if (M == 0 || N == 0) return SM_OK;
+  return gemm_planes(planes, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C,
+                     ldc, as_stream(stream));
 }

@@ -57,6 +57,13 @@ int sm_q4_quantize(const void*, int, int64_t, uint8_t*, uint16_t*, int32_t*, voi
 }
 
 namespace sm {
+int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                   float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
+                   float beta, float* C, int64_t ldc, void* stream);  // train.hip
+int64_t rmsnorm_dgamma_chunks(int64_t rows);                          // train.hip
+int rmsnorm_backward_parts(const float* x, const float* gamma, const float* dy, int64_t rows,
+                           int64_t d, float eps, int accumulate, float* dx, float* dgamma,
+                           float* rinv_scratch, float* parts, hipStream_t st);
 namespace {
 
 constexpr int kKinds = 9;  // SM_W_EMBED .. SM_W_LM_HEAD
@@ -219,6 +226,7 @@ struct sm_policy {
   float* m1[sm::kKinds] = {};   // AdamW moments / Muon velocity in m1
   float* m2[sm::kKinds] = {};
   int64_t adam_step = 0, muon_step = 0;
+  int planes = 3;  // bf16 planes per GEMM operand in sm_policy_prepare
   float* rope = nullptr;
   std::vector<void*> owned;
   // forward activations and scratch (grow-only)
@@ -379,6 +387,13 @@ extern "C" int sm_policy_destroy(sm_policy* p) {
   return SM_OK;
 }
 
+extern "C" int sm_policy_set_matmul_planes(sm_policy* p, int planes) {
+  SM_REQUIRE(p, "sm_policy_set_matmul_planes: null policy");
+  SM_REQUIRE(planes >= 1 && planes <= 3, "matmul planes must be 1, 2 or 3 (got %d)", planes);
+  p->planes = planes;
+  return SM_OK;
+}
+
 extern "C" int sm_policy_set_tensor(sm_policy* p, int kind, int layer, const float* src,
                                     void* stream) {
   SM_REQUIRE(p && src, "sm_policy_set_tensor: null argument");
@@ -436,6 +451,12 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   SM_REQUIRE(L <= c.max_seq, "sequence length %lld exceeds max_seq_len %d", (long long)L,
              c.max_seq);
   hipStream_t st = as_stream(stream);
+  // the prepare's GEMMs on the policy's plane count
+  auto pgemm = [&](int ta, int tb, int64_t m, int64_t n, int64_t k, float alpha, const float* A,
+                   int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                   void* sp) {
+    return gemm_ex_planes(p->planes, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, sp);
+  };
   const int64_t d = c.d_model, H = c.heads, KVH = c.kv_heads, hd = c.head_dim, F = c.ffn;
   const int64_t V = c.vocab, qn = p->qn, qdim = p->qdim;
   if (c.quantized) SM_TRY(fake_quantize(p, st));
@@ -445,7 +466,8 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
                         M * d /*dx*/ + M * d /*dhf*/ + R * d /*dhr*/ + M * 2 * F /*du*/ +
                         M * F /*da*/ + M * d /*dh*/ + M * qdim /*do*/ + M * qdim /*dq*/ +
                         2 * S * KVH * L * hd /*dk dv*/ + M * qn /*dqkv*/ + M /*rinv*/ +
-                        S * H * L /*delta*/ + R /*row scale*/ + d /*dgamma final*/ + S /*pos0*/;
+                        S * H * L /*delta*/ + R /*row scale*/ + d /*dgamma final*/ + S /*pos0*/ +
+                        rmsnorm_dgamma_chunks(M) * d /*dgamma parts*/;
   const size_t bytes = (size_t)(per_layer * c.layers + fixed) * 4 + (size_t)M * 4 /*ids*/ +
                        (size_t)R * 8 /*rows*/ + (size_t)(12 * c.layers + 32) * 256;
   SM_TRY(grow(p->act, bytes));
@@ -483,6 +505,7 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   float* delta = (float*)take(S * H * L);
   float* rscale = (float*)take(R);
   float* dgf = (float*)take(d);
+  float* dgparts = (float*)take(rmsnorm_dgamma_chunks(M) * d);
   int32_t* pos0 = (int32_t*)take(S);
   int32_t* ids = (int32_t*)take(M);
   int64_t* rows = (int64_t*)take(R, 8);
@@ -495,25 +518,25 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
     Saved& s = sv[l];
     SM_HIP(hipMemcpyAsync(s.x0, x, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
     SM_TRY(sm_rmsnorm(s.x0, fwl(p, SM_W_ATTN_NORM, l), M, d, c.norm_eps, s.h, SM_F32, stream));
-    SM_TRY(sm_gemm_ex(0, 1, M, qn, d, 1.f, s.h, d, fwl(p, SM_W_QKV, l), d, 0.f, s.qkv, qn, stream));
+    SM_TRY(pgemm(0, 1, M, qn, d, 1.f, s.h, d, fwl(p, SM_W_QKV, l), d, 0.f, s.qkv, qn, stream));
     SM_TRY(sm_rope_qk(s.qkv, p->rope, pos0, S, L, H, KVH, hd, 0, stream));
     split_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(s.qkv, (int)S, (int)L, (int)H, (int)KVH,
                                                      (int)hd, s.q, s.k, s.v);
     SM_TRY(sm_attn_prefill_lse(s.q, s.k, s.v, pos0, s.o, s.lse, SM_F32, SM_F32, S, L, H, KVH, L,
                                hd, stream));
     SM_HIP(hipMemcpyAsync(s.x1, s.x0, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
-    SM_TRY(sm_gemm_ex(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
+    SM_TRY(pgemm(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
                       stream));
     SM_TRY(sm_rmsnorm(s.x1, fwl(p, SM_W_FFN_NORM, l), M, d, c.norm_eps, s.h2, SM_F32, stream));
-    SM_TRY(sm_gemm_ex(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
+    SM_TRY(pgemm(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
                       stream));
     SM_TRY(sm_swiglu(s.u, SM_F32, M, F, s.a, stream));
     SM_HIP(hipMemcpyAsync(x, s.x1, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
-    SM_TRY(sm_gemm_ex(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
+    SM_TRY(pgemm(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
   }
   SM_TRY(sm_rmsnorm(x, fw(p, SM_W_FINAL_NORM), M, d, c.norm_eps, hf, SM_F32, stream));
   gather_rows_f32<<<blocks256(R * d), 256, 0, st>>>(hf, rows, R, (int)d, hr);
-  SM_TRY(sm_gemm_ex(0, 1, R, V, d, 1.f, hr, d, fw(p, SM_W_LM_HEAD), d, 0.f, logits, V, stream));
+  SM_TRY(pgemm(0, 1, R, V, d, 1.f, hr, d, fw(p, SM_W_LM_HEAD), d, 0.f, logits, V, stream));
   SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, lp_cur, nullptr, nullptr, 1.f, nullptr,
                     nullptr, stream));
   // ---- the frozen reference and the loss
@@ -527,39 +550,39 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   neg_f32<<<blocks256(R), 256, 0, st>>>(dlp, R, rscale);
   SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, nullptr, nullptr, logits, 1.f, rscale,
                     nullptr, stream));
-  SM_TRY(sm_gemm_ex(1, 0, V, d, R, 1.f, logits, V, hr, d, 1.f, p->g[SM_W_LM_HEAD], d, stream));
-  SM_TRY(sm_gemm_ex(0, 0, R, d, V, 1.f, logits, V, fw(p, SM_W_LM_HEAD), d, 0.f, dhr, d, stream));
+  SM_TRY(pgemm(1, 0, V, d, R, 1.f, logits, V, hr, d, 1.f, p->g[SM_W_LM_HEAD], d, stream));
+  SM_TRY(pgemm(0, 0, R, d, V, 1.f, logits, V, fw(p, SM_W_LM_HEAD), d, 0.f, dhr, d, stream));
   SM_HIP(hipMemsetAsync(dhf, 0, (size_t)M * d * 4, st));
   scatter_rows_f32<<<blocks256(R * d), 256, 0, st>>>(dhr, rows, R, (int)d, dhf);
-  SM_TRY(sm_rmsnorm_backward(x, fw(p, SM_W_FINAL_NORM), dhf, M, d, c.norm_eps, 0, dx, dgf, rinv,
-                             stream));
+  SM_TRY(rmsnorm_backward_parts(x, fw(p, SM_W_FINAL_NORM), dhf, M, d, c.norm_eps, 0, dx, dgf,
+                                rinv, dgparts, st));
   SM_TRY(sm_axpby(dgf, p->g[SM_W_FINAL_NORM], d, 1.f, 1.f, stream));
   for (int l = c.layers - 1; l >= 0; --l) {
     Saved& s = sv[l];
     // FFN: x = x1 + swiglu(h2 W_in^T) W_down^T
-    SM_TRY(sm_gemm_ex(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
-    SM_TRY(sm_gemm_ex(1, 0, d, F, M, 1.f, dx, d, s.a, F, 1.f, gl(p, SM_W_DOWN, l), F, stream));
+    SM_TRY(pgemm(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
+    SM_TRY(pgemm(1, 0, d, F, M, 1.f, dx, d, s.a, F, 1.f, gl(p, SM_W_DOWN, l), F, stream));
     SM_TRY(sm_swiglu_backward(s.u, da, SM_F32, M, F, du, stream));
-    SM_TRY(sm_gemm_ex(1, 0, 2 * F, d, M, 1.f, du, 2 * F, s.h2, d, 1.f, gl(p, SM_W_IN, l), d,
+    SM_TRY(pgemm(1, 0, 2 * F, d, M, 1.f, du, 2 * F, s.h2, d, 1.f, gl(p, SM_W_IN, l), d,
                       stream));
-    SM_TRY(sm_gemm_ex(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
+    SM_TRY(pgemm(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
                       stream));
-    SM_TRY(sm_rmsnorm_backward(s.x1, fwl(p, SM_W_FFN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
-                               gl(p, SM_W_FFN_NORM, l), rinv, stream));
+    SM_TRY(rmsnorm_backward_parts(s.x1, fwl(p, SM_W_FFN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
+                                  gl(p, SM_W_FFN_NORM, l), rinv, dgparts, st));
     // attention: x1 = x0 + attn(rope(h W_qkv^T)) W_o^T
-    SM_TRY(sm_gemm_ex(0, 0, M, qdim, d, 1.f, dx, d, fwl(p, SM_W_O, l), qdim, 0.f, dO, qdim,
+    SM_TRY(pgemm(0, 0, M, qdim, d, 1.f, dx, d, fwl(p, SM_W_O, l), qdim, 0.f, dO, qdim,
                       stream));
-    SM_TRY(sm_gemm_ex(1, 0, d, qdim, M, 1.f, dx, d, s.o, qdim, 1.f, gl(p, SM_W_O, l), qdim,
+    SM_TRY(pgemm(1, 0, d, qdim, M, 1.f, dx, d, s.o, qdim, 1.f, gl(p, SM_W_O, l), qdim,
                       stream));
     SM_TRY(sm_attn_backward_f32(s.q, s.k, s.v, s.o, dO, s.lse, S, L, H, KVH, hd, dq, dk, dv,
                                 delta, stream));
     merge_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(dq, dk, dv, (int)S, (int)L, (int)H,
                                                      (int)KVH, (int)hd, dqkv);
     SM_TRY(sm_rope_qk(dqkv, p->rope, pos0, S, L, H, KVH, hd, 1, stream));
-    SM_TRY(sm_gemm_ex(1, 0, qn, d, M, 1.f, dqkv, qn, s.h, d, 1.f, gl(p, SM_W_QKV, l), d, stream));
-    SM_TRY(sm_gemm_ex(0, 0, M, d, qn, 1.f, dqkv, qn, fwl(p, SM_W_QKV, l), d, 0.f, dh, d, stream));
-    SM_TRY(sm_rmsnorm_backward(s.x0, fwl(p, SM_W_ATTN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
-                               gl(p, SM_W_ATTN_NORM, l), rinv, stream));
+    SM_TRY(pgemm(1, 0, qn, d, M, 1.f, dqkv, qn, s.h, d, 1.f, gl(p, SM_W_QKV, l), d, stream));
+    SM_TRY(pgemm(0, 0, M, d, qn, 1.f, dqkv, qn, fwl(p, SM_W_QKV, l), d, 0.f, dh, d, stream));
+    SM_TRY(rmsnorm_backward_parts(s.x0, fwl(p, SM_W_ATTN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
+                                  gl(p, SM_W_ATTN_NORM, l), rinv, dgparts, st));
   }
   SM_TRY(sm_embed_backward(ids, dx, M, d, V, p->g[SM_W_EMBED], stream));
   SM_LAUNCH_CHECK();

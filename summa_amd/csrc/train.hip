@@ -13,6 +13,7 @@
 //   * AdamW and Muon's momentum step (burn_optim AdamW; BatchedMuon,
 //     summa-train/src/muon.rs:196-215).
 // All f32 with f32 accumulation: the precision of the reference CPU path.
+#include <algorithm>
 #include <cmath>
 
 #include "attn_common.hpp"
@@ -143,6 +144,53 @@ __global__ __launch_bounds__(256) void rmsnorm_dgamma_kernel(const float* __rest
   float tot = 0.f;
 #pragma unroll
   for (int i = 0; i < 16; ++i) tot += part[i][threadIdx.x];
+  dgamma[c] = accumulate ? dgamma[c] + tot : tot;
+}
+
+// dgamma over row chunks: block (x, y) sums rows [y * rpc, (y + 1) * rpc) of
+// columns 64x .. 64x + 63 (as rmsnorm_dgamma_kernel does over all rows) into
+// parts[y][col]; dgamma_finish_kernel then adds the chunks in order. For the
+// policy update's 8k-row norms, where 32 column blocks cannot fill the GPU.
+__global__ __launch_bounds__(256) void rmsnorm_dgamma_parts_kernel(
+    const float* __restrict__ x, const float* __restrict__ dy, const float* __restrict__ rinv,
+    int64_t rows, int d, int64_t rpc, float* __restrict__ parts) {
+  __shared__ float part[16][64];
+  const int cg = threadIdx.x % 16, rl = threadIdx.x / 16;
+  const int c0 = blockIdx.x * 64 + 4 * cg;
+  const int64_t r0 = (int64_t)blockIdx.y * rpc, r1 = min(rows, r0 + rpc);
+  float s[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int64_t r = r0 + rl; r < r1; r += 16) {
+    const float ri = rinv[r];
+    if (c0 + 4 <= d && d % 4 == 0) {
+      const float4 a = *reinterpret_cast<const float4*>(dy + r * d + c0);
+      const float4 b = *reinterpret_cast<const float4*>(x + r * d + c0);
+      s[0] = fmaf(a.x * b.x, ri, s[0]);
+      s[1] = fmaf(a.y * b.y, ri, s[1]);
+      s[2] = fmaf(a.z * b.z, ri, s[2]);
+      s[3] = fmaf(a.w * b.w, ri, s[3]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        if (c0 + j < d) s[j] = fmaf(dy[r * d + c0 + j] * x[r * d + c0 + j], ri, s[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; ++j) part[rl][4 * cg + j] = s[j];
+  __syncthreads();
+  const int c = blockIdx.x * 64 + (int)threadIdx.x;
+  if (threadIdx.x >= 64 || c >= d) return;
+  float tot = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tot += part[i][threadIdx.x];
+  parts[(int64_t)blockIdx.y * d + c] = tot;
+}
+
+__global__ void dgamma_finish_kernel(const float* __restrict__ parts, int chunks, int d,
+                                     int accumulate, float* __restrict__ dgamma) {
+  const int c = blockIdx.x * blockDim.x + threadIdx.x;
+  if (c >= d) return;
+  float tot = 0.f;
+  for (int i = 0; i < chunks; ++i) tot += parts[(int64_t)i * d + c];
   dgamma[c] = accumulate ? dgamma[c] + tot : tot;
 }
 
@@ -483,16 +531,16 @@ inline unsigned g256(int64_t n) { return (unsigned)ceil_div(n, 256); }
 
 }  // namespace
 
-int gemm_bf16x3(bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha, const float* A,
-                int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
-                hipStream_t st);  // gemm_mfma.hip
-}  // namespace sm
+int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
+                const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
+                int64_t ldc, hipStream_t st);  // gemm_mfma.hip
 
-using namespace sm;
-
-extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
-                          const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
-                          float* C, int64_t ldc, void* stream) {
+// sm_gemm_ex with the matrix-core launches on `planes` bf16 planes per operand
+// (3: f32-grade; 2: 16-bit operands; 1: bf16 operands); the small problems
+// stay on the f32 FMA kernel.
+int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
+                   float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
+                   float beta, float* C, int64_t ldc, void* stream) {
   SM_REQUIRE(A && B && C, "sm_gemm_ex: null buffer");
   SM_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1 << 30) && N < (1 << 30) && K < (1 << 30),
              "sm_gemm_ex: bad shape");
@@ -501,11 +549,11 @@ extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_
   if (M == 0 || N == 0) return SM_OK;
   SM_REQUIRE(ceil_div(M, 64) <= 65535, "sm_gemm_ex: M above 65535 x 64 rows");
   hipStream_t st = as_stream(stream);
-  // large problems on the matrix cores (f32-grade three-plane bf16 products,
-  // gemm_mfma.hip); small ones, where a launch has few 128 x 128 tiles, here
+  // large problems on the matrix cores (bf16 plane products, gemm_mfma.hip);
+  // small ones, where a launch has few 128 x 128 tiles, here
   if (K >= 32 && M * N >= (int64_t)128 * 128 * 16 && M * N * K >= ((int64_t)1 << 27))
-    return gemm_bf16x3(trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
-                       st);
+    return gemm_planes(planes, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta,
+                       C, ldc, st);
   const dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
 #define SM_GX(TA, TB)                                                                        \
   gemm_ex_kernel<TA, TB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, \
@@ -517,6 +565,15 @@ extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_
 #undef SM_GX
   SM_LAUNCH_CHECK();
   return SM_OK;
+}
+}  // namespace sm
+
+using namespace sm;
+
+extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
+                          const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
+                          float* C, int64_t ldc, void* stream) {
+  return gemm_ex_planes(3, trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
 }
 
 extern "C" int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy,
@@ -534,6 +591,34 @@ extern "C" int sm_rmsnorm_backward(const float* x, const float* gamma, const flo
   SM_LAUNCH_CHECK();
   return SM_OK;
 }
+
+namespace sm {
+// Row chunks of rmsnorm_backward_parts: up to kDgammaChunks chunks of at least
+// 128 rows; parts needs chunks x d floats.
+constexpr int kDgammaChunks = 64;
+int64_t rmsnorm_dgamma_chunks(int64_t rows) {
+  return std::max<int64_t>(1, std::min<int64_t>(kDgammaChunks, rows / 128));
+}
+// sm_rmsnorm_backward with dgamma summed over row chunks (parts: at least
+// rmsnorm_dgamma_chunks(rows) * d floats of scratch).
+int rmsnorm_backward_parts(const float* x, const float* gamma, const float* dy, int64_t rows,
+                           int64_t d, float eps, int accumulate, float* dx, float* dgamma,
+                           float* rinv_scratch, float* parts, hipStream_t st) {
+  SM_REQUIRE(x && gamma && dy && dx && rinv_scratch && dgamma && parts,
+             "sm_rmsnorm_backward: null buffer");
+  SM_REQUIRE(rows >= 0 && d > 0, "sm_rmsnorm_backward: bad shape");
+  if (rows == 0) return SM_OK;
+  rmsnorm_bwd_kernel<<<(unsigned)rows, 256, 0, st>>>(x, gamma, dy, (int)d, eps, accumulate, dx,
+                                                     rinv_scratch);
+  const int64_t chunks = rmsnorm_dgamma_chunks(rows), rpc = ceil_div(rows, chunks);
+  rmsnorm_dgamma_parts_kernel<<<dim3((unsigned)ceil_div(d, 64), (unsigned)chunks), 256, 0, st>>>(
+      x, dy, rinv_scratch, rows, (int)d, rpc, parts);
+  dgamma_finish_kernel<<<(unsigned)ceil_div(d, 256), 256, 0, st>>>(parts, (int)chunks, (int)d,
+                                                                   accumulate, dgamma);
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+}  // namespace sm
 
 extern "C" int sm_rope_qk(float* qkv, const float* rope_table, const int32_t* pos0, int64_t S,
                           int64_t L, int64_t H, int64_t KVH, int64_t head_dim, int backward,

@@ -270,16 +270,21 @@ class Policy:
     another (posttrain.rs:1288-1305), with the trainer's optimizer settings as
     defaults (AdamW 3e-4 / 0.9 / 0.95 / 1e-8 / wd 0.1, global-norm clip 1.0: the
     CLI defaults of summa-train/src/main.rs:171-176 and trainer.rs:1124-1129;
-    ``muon_lr > 0`` adds Muon for the per-layer projections)."""
+    ``muon_lr > 0`` adds Muon for the per-layer projections).
+    ``matmul_planes``: bf16 planes per GEMM operand in ``prepare``
+    (sm_policy_set_matmul_planes): 3 f32-grade, 2 16-bit operands, 1 bf16
+    operands with f32 accumulation (the reference's CUDA-path matmul)."""
 
     def __init__(self, cfg: ModelConfig, weights: dict, device, lr=3e-4, betas=(0.9, 0.95),
-                 eps=1e-8, weight_decay=0.1, muon_lr=0.0, grad_clip=1.0):
+                 eps=1e-8, weight_decay=0.1, muon_lr=0.0, grad_clip=1.0, matmul_planes=3):
         from . import _lib
         self.cfg, self.dev = cfg, device
         self._h = C.c_void_p()
         oc = OptimizerConfigC(lr, betas[0], betas[1], eps, weight_decay, muon_lr, grad_clip)
         cc = cfg.c()
         _lib.check(_lib.lib().sm_policy_create(C.byref(cc), C.byref(oc), C.byref(self._h)))
+        if matmul_planes != 3:
+            self.set_matmul_planes(matmul_planes)
         for name, arr in weights.items():
             if isinstance(arr, torch.Tensor):  # host or device tensors
                 t = arr.to(device=device, dtype=torch.float32).contiguous()
@@ -293,6 +298,10 @@ class Policy:
                 call("sm_policy_set_tensor", self._h, _POLICY_KINDS[name], -1, t.data_ptr(),
                      _st())
         torch.cuda.synchronize()
+
+    def set_matmul_planes(self, planes: int) -> None:
+        """bf16 planes per operand of the prepare's GEMMs (1, 2 or 3)."""
+        call("sm_policy_set_matmul_planes", self._h, int(planes))
 
     def close(self):
         if self._h.value:

@@ -62,16 +62,28 @@ def test_native_policy_gradient_matches_autograd(dev):
     torch.testing.assert_close(pol.tensor("qkv", 1, gradient=True), 2 * g1, rtol=1e-5, atol=1e-7)
 
 
-def test_native_policy_gradient_on_matrix_cores(dev):
+# (max |lp - f64|, max relative gradient error) per GEMM plane count: f32-grade
+# for three planes (measured 1.0e-5, 2.2e-6); 16-bit operands for two
+# (5.8e-5, 2.1e-5); bf16 operands, the reference's CUDA-path matmul precision,
+# for one (2.9e-2, 1.2e-2: this policy's weights are N(0, 0.05), its logits a
+# few units). Every gradient also keeps its direction (cosine >= 0.9999).
+PLANE_BOUNDS = {3: (2e-5, 2e-4), 2: (2e-4, 1e-4), 1: (6e-2, 3e-2)}
+
+
+@pytest.mark.parametrize("planes", [3, 2, 1])
+def test_native_policy_gradient_on_matrix_cores(dev, planes):
     """A policy large enough that every linear's forward, data-gradient and
     weight-gradient GEMM crosses sm_gemm_ex's matrix-core threshold (2^27
     multiply-adds, 128 x 128 x 16 outputs) and attention spans several 32 x 32
     backward tiles (127 positions): the staged gradient against float64
-    autograd, as for the small policy."""
+    autograd, as for the small policy, with the GEMMs on 3, 2 or 1 bf16 planes
+    (PLANE_BOUNDS)."""
+    print(f"case matrix-core policy planes={planes}", flush=True)
     cfg = ModelConfig(layers=1, d_model=512, heads=4, kv_heads=2, head_dim=128, ffn=1024,
                       vocab=2048, max_seq=160, quantized=False)
     w = oracle.random_weights(cfg.oracle_cfg(), seed=21, std=0.05)
-    pol = train.Policy(cfg, w, dev)
+    pol = train.Policy(cfg, w, dev, matmul_planes=planes)
+    lp_bound, grad_bound = PLANE_BOUNDS[planes]
     prompts, tokens, rewards = _batch(cfg, 5, dev, P=64, N=64)
     beh = torch.full(tokens.shape, -9.0, device=dev)
     out = pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
@@ -81,7 +93,7 @@ def test_native_policy_gradient_on_matrix_cores(dev):
     lp_t = _torch_lp(wt, cfg, prompts.cpu(), tokens.cpu())
     lp_err = float((out["lp_cur"].cpu().double() - lp_t.detach()).abs().max())
     print(f"matrix-core policy: max |lp - f64| {lp_err:.2e}", flush=True)
-    assert lp_err < 2e-5
+    assert lp_err < lp_bound
     (out["dlp"].cpu().double() * lp_t).sum().backward()
     for k, t in wt.items():
         layers = range(cfg.layers) if k in train.LAYER_KEYS else [-1]
@@ -89,8 +101,11 @@ def test_native_policy_gradient_on_matrix_cores(dev):
             got = pol.tensor(k, layer, gradient=True).cpu().double()
             want = t.grad[layer] if layer >= 0 else t.grad
             err = (got - want).abs().max().item() / (want.abs().max().item() + 1e-12)
-            print(f"  {k}[{layer}] relative gradient error {err:.2e}", flush=True)
-            assert err < 2e-4, (k, layer)
+            cos = float((got * want).sum() / (got.norm() * want.norm() + 1e-300))
+            print(f"  {k}[{layer}] relative gradient error {err:.2e}, cosine {cos:.6f}",
+                  flush=True)
+            assert err < grad_bound, (k, layer)
+            assert cos >= 0.9999, (k, layer)
 
 
 @pytest.mark.timeout(600)

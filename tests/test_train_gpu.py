@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from summa_amd import ops, train
+from summa_amd import _lib, ops, train
 from summa_amd._lib import call
 from summa_amd.model import Model, ModelConfig
 
@@ -76,6 +76,57 @@ def test_gemm_mfma_f32_grade(dev, ta, tb, M, N, K, pad):
     train.gemm(a, b, ta=bool(ta), tb=bool(tb), out=out2, alpha=0.5, beta=2.0, entry="sm_gemm_mfma")
     np.testing.assert_allclose(out2.cpu().numpy(), 0.5 * ref + 2.0 * C.astype(np.float32),
                                rtol=1e-5, atol=1e-4)
+
+
+def _bf16_rne(x):
+    """f32 -> the nearest bf16 (ties to even), as f64 (finite inputs)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000
+    return u.astype(np.uint32).view(np.float32).astype(np.float64)
+
+
+@pytest.mark.parametrize("planes", [1, 2])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K,pad", [(300, 260, 333, 0), (129, 257, 100, 1)])
+def test_gemm_planes_reduced(dev, planes, ta, tb, M, N, K, pad):
+    """sm_gemm_planes with one or two bf16 planes against the same plane
+    arithmetic done in f64 on the host: planes 1 = bf16(a) bf16(b) (round to
+    nearest even), planes 2 = a0 b0 + a0 b1 + a1 b0 with a1 = bf16(a - a0).
+    The kernel's only other error is its f32 accumulation, so it stays within
+    4x torch's f32 matmul error of that f64 value; a truncating rounding, a
+    dropped or extra cross term, or the third plane would be off by ~2^-9 or
+    ~2^-17 relative per product, far outside."""
+    print(f"case gemm_planes planes={planes} ta={ta} tb={tb} M={M} N={N} K={K} pad={pad}",
+          flush=True)
+    rng = np.random.default_rng(2000 + 8 * planes + 4 * ta + 2 * tb + M)
+    a, b, ref, A32, B32 = _gemm_case(rng, ta, tb, M, N, K, pad)
+    A0, B0 = _bf16_rne(A32), _bf16_rne(B32)
+    opA = lambda x: x.T if ta else x  # noqa: E731
+    opB = lambda x: x.T if tb else x  # noqa: E731
+    if planes == 1:
+        want = opA(A0) @ opB(B0)
+    else:
+        A1, B1 = _bf16_rne(A32 - A0), _bf16_rne(B32 - B0)
+        want = opA(A0) @ opB(B0) + opA(A0) @ opB(B1) + opA(A1) @ opB(B0)
+    out = torch.full((M, N), float("nan"), device=dev)
+    call("sm_gemm_planes", planes, ta, tb, M, N, K, 1.0, a.data_ptr(), a.stride(0), b.data_ptr(),
+         b.stride(0), 0.0, out.data_ptr(), out.stride(0), torch.cuda.current_stream().cuda_stream)
+    t32 = (torch.from_numpy(opA(A32)).float() @ torch.from_numpy(opB(B32)).float())
+    err = float(np.abs(out.cpu().double().numpy() - want).max())
+    err32 = float(np.abs(t32.double().numpy() - ref).max())
+    dist = float(np.abs(want - ref).max())
+    print(f"  max |err| vs plane model {err:.3g} (torch f32 {err32:.3g}; plane model vs exact "
+          f"{dist:.3g})", flush=True)
+    assert err <= 4 * err32 + 1e-6
+    assert dist > 3 * err  # the kernel follows the plane model, not the exact product
+
+
+def test_gemm_planes_rejects_bad_count(dev):
+    x = torch.zeros(4, 4, device=dev)
+    for planes in (0, 4):
+        with pytest.raises(_lib.SummaError, match="planes must be 1, 2 or 3"):
+            call("sm_gemm_planes", planes, 0, 0, 4, 4, 4, 1.0, x.data_ptr(), 4, x.data_ptr(), 4,
+                 0.0, x.data_ptr(), 4, 0)
 
 
 def test_gemm_ex_large_runs_on_matrix_cores(dev):
