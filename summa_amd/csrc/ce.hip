@@ -13,22 +13,20 @@
 //   * lp / loss only: one 256-thread workgroup per row, 4 x 16 B loads in
 //     flight per lane, online max/sum in registers, wave shuffles + LDS merge.
 //     Traffic = one read of the logits.
-//   * lp + grad in place: one 512-thread workgroup per row streams the row
-//     twice: a statistics pass with ordinary (cached) loads, then a gradient
-//     pass whose loads and stores are nontemporal (last use), 8 vectors per
-//     lane in flight. The second read of a row (256 KB at config[3]) misses
-//     L2: the L2-miss read counter shows 1.76x the algorithmic read, served by
-//     the 256 MB MALL or by HBM. Config[3] (bf16 65536 x 131072): 7.2 ms for
-//     34 GB of algorithmic traffic; a plain elementwise in-place pass over the
-//     same bytes (one read, one write, no statistics pass) runs at 5.9 TB/s.
-//     Plain or mixed load / store kinds in the second pass: 7.4-7.6 ms; 1024
-//     threads x 4 vectors: 7.3-7.4 ms. Keeping each row in VGPRs
-//     (read once, write once) was 9.9 ms: a 1024-thread workgroup holding
-//     256 KB in registers fits once per CU, so its read, reduce and write
-//     phases never overlap with another row's. Keeping only the row's last
-//     1/8 to 1/2 in registers (those gradients written without a second
-//     read, the rest re-read newest first) was 7.3-8.6 ms: the registers
-//     cost rows in flight per CU, and with them more than the re-reads.
+//   * lp + grad in place, bf16 rows of 64k-128k columns (config[3]'s
+//     131072): ce_grad_resident_kernel holds the row on chip (VGPRs + an LDS
+//     stash), so it is read once and written once: 6.13 ms for 34.4 GB at
+//     config[3], 0.70 of HBM, counters 1.00x the algorithmic bytes.
+//   * lp + grad in place, other rows: one 512-thread workgroup per row
+//     streams the row twice: a statistics pass with ordinary (cached) loads,
+//     then a gradient pass whose loads and stores are nontemporal (last use),
+//     8 vectors per lane in flight. The second read of a row misses L2 when
+//     the row is long (256 KB at config[3]: 1.5x the algorithmic bytes beyond
+//     L2, 7.2 ms). Measured there and not kept: plain or mixed load / store
+//     kinds in the second pass (7.4-7.6 ms); 1024 threads x 4 vectors
+//     (7.3-7.4 ms); the row in VGPRs of one 1024-thread workgroup, once per CU,
+//     so its read, reduce and write phases never overlap another row's
+//     (8.2-9.9 ms); only the row's last 1/8 to 1/2 in registers (7.3-8.6 ms).
 #include <cfloat>
 #include <cmath>
 
@@ -255,6 +253,176 @@ __global__ __launch_bounds__(THREADS) void ce_grad_stream_kernel(
   }
 }
 
+// Gradient in place with the row held on chip: bf16 rows of at most
+// 8 * 512 * (VR + VL) stored columns, 16-byte aligned. Each of the 512
+// threads keeps VR 16-byte vectors of its row in VGPRs (vector u*512 + tid)
+// and VL more in an LDS stash (vector (VR + w)*512 + tid, copied there by
+// global_load_lds_dwordx4 without passing through registers), so the row is
+// read from HBM once and written once. With the row resident the statistics
+// need no online rescaling: the row max first (one workgroup reduction), then
+// sum exp(x - max) (another), in a fixed order, so lse is deterministic (it
+// differs from the streaming kernels' online order in the last bits; measured
+// 1 % faster than one online pass here).
+// 96 + 64 KB at VR = 24, VL = 8 (config[3]'s 131072 columns), 128 VGPRs:
+// two workgroups per CU, so one row's reads overlap another row's writes.
+// Loads and stores are nontemporal (each element is read once and written
+// once): 6.24 against 6.28-6.57 ms with plain loads or stores. A persistent
+// grid (two workgroups per CU walking the rows) measured 6.52 ms.
+// The gradient away from the target column and the padding is
+// 2^(x log2e - lse log2e + log2 |scale|) with the sign set on the bf16 bits
+// (one exp, no multiply; within a few f32 ulps of softmax * scale before the
+// bf16 rounding); elsewhere it is ce_grad_stream_kernel's arithmetic.
+template <int VR, int VL, bool FULL>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(4, 4))) void
+ce_grad_resident_kernel(void* __restrict__ logits, const int32_t* __restrict__ targets,
+                        int64_t ld, int64_t vl, float* __restrict__ lp,
+                        float* __restrict__ lse_out, float grad_scale,
+                        const float* __restrict__ row_scale) {
+  constexpr int T = 512, kV = 8, NW = T / kWave;
+  __shared__ u32x4 stash[VL > 0 ? VL * T : 1];
+  __shared__ float red_m[NW], red_s[NW];
+  __shared__ float target_logit;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  // FULL: ld == vl == 512 * 8 * (VR + VL), every vector present, no masks
+  const int nvec = FULL ? (VR + VL) * T : (int)(vl / kV);
+  const int nvec_st = FULL ? (VR + VL) * T : (int)(ld / kV), vli = FULL ? nvec * kV : (int)vl;
+  const int tl = tid;
+  const int64_t row = blockIdx.x;
+  const uint32_t lo16 = (uint32_t)tl * 16u;  // lane offset inside each 8 KB slice
+  auto present = [&](int i, int n) { return FULL || i * T + tl < n; };
+  char* row_ptr = static_cast<char*>(logits) + row * ld * 2;
+  // vector i*512 + tid sits at slice(i) + lo16
+  auto slice = [&](int i) { return row_ptr + (size_t)i * (T * 16); };
+  const int32_t t = targets[row];
+  if (tid == 0)
+    target_logit =
+        (t >= 0 && t < vl) ? bf16_to_f32(reinterpret_cast<const uint16_t*>(row_ptr)[t]) : NAN;
+  // the stash copies first, then the register vectors: loads complete in
+  // order, so the max pass can start on r[0] while the rest arrive
+#if defined(__HIP_DEVICE_COMPILE__)  // (the host pass does not emit the launch stub otherwise)
+#pragma unroll
+  for (int w = 0; w < VL; ++w) {
+    if (present(VR + w, nvec_st))  // aux 2: nontemporal, the row's only read
+      __builtin_amdgcn_global_load_lds(
+          slice(VR + w) + lo16,
+          (__attribute__((address_space(3))) void*)&stash[w * T + wave * kWave], 16, 0, 2);
+  }
+#endif
+  u32x4 r[VR];
+#pragma unroll
+  for (int u = 0; u < VR; ++u) {
+    r[u] = present(u, nvec_st)
+               ? __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(slice(u) + lo16))
+               : u32x4{0u, 0u, 0u, 0u};
+  }
+  // ---- row max
+  float mx = -INFINITY;
+#pragma unroll
+  for (int u = 0; u < VR; ++u) {
+    if (present(u, nvec)) {
+      float x[kV];
+      unpack<true>(r[u], x);
+#pragma unroll
+      for (int e = 0; e < kV; ++e) mx = fmaxf(mx, x[e]);
+    }
+  }
+  // the stash copies are done (each wave reads back only the slots it copied)
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int w = 0; w < VL; ++w) {
+    if (present(VR + w, nvec)) {
+      float x[kV];
+      unpack<true>(stash[w * T + tid], x);
+#pragma unroll
+      for (int e = 0; e < kV; ++e) mx = fmaxf(mx, x[e]);
+    }
+  }
+  if (!FULL)
+    for (int c = nvec * kV + tl; c < vli; c += T) mx = fmaxf(mx, load_scalar<true>(row_ptr, c));
+  mx = wave_max(mx);
+  if (lane == 0) red_m[wave] = mx;
+  __syncthreads();
+  float m = red_m[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m = fmaxf(m, red_m[w]);
+  // ---- sum of exp(x - max), in the log2 domain as online_update
+  const float nm = -m * kLog2e;
+  float sum = 0.f;
+#pragma unroll
+  for (int u = 0; u < VR; ++u) {
+    asm volatile("" : "+v"(r[u]));  // unpack again: no unpacked row kept across passes
+    if (present(u, nvec)) {
+      float x[kV];
+      unpack<true>(r[u], x);
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < kV; ++e) acc += __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, nm));
+      sum += acc;
+    }
+  }
+#pragma unroll
+  for (int w = 0; w < VL; ++w) {
+    if (present(VR + w, nvec)) {
+      float x[kV];
+      unpack<true>(stash[w * T + tid], x);
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < kV; ++e) acc += __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, nm));
+      sum += acc;
+    }
+  }
+  if (!FULL)
+    for (int c = nvec * kV + tl; c < vli; c += T)
+      sum += __builtin_amdgcn_exp2f(fmaf(load_scalar<true>(row_ptr, c), kLog2e, nm));
+  sum = wave_sum(sum);
+  if (lane == 0) red_s[wave] = sum;
+  __syncthreads();
+  float s = red_s[0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) s += red_s[w];
+  const float lse = m + __logf(s);
+  if (tid == 0) {
+    if (lse_out) lse_out[row] = lse;
+    if (lp) lp[row] = target_logit - lse;
+  }
+  // ---- gradient: (softmax - onehot(t)) * scale, zeros past the logical vocab
+  const float scale = grad_scale * (row_scale ? row_scale[row] : 1.f);
+  const float nl = -lse * kLog2e;
+  // away from the target and the padding: |scale| p = 2^(x log2e - lse log2e +
+  // log2 |scale|), the sign of scale set on the packed bf16 words (no multiply)
+  const float nls = nl + __log2f(fabsf(scale));
+  const uint32_t sgn = scale < 0.f ? 0x80008000u : 0u;
+  auto grad = [&](const u32x4& v, int c0) -> u32x4 {
+    if (c0 + kV <= vli && (unsigned)(t - c0) >= (unsigned)kV) {  // no target, no padding
+      float x[kV];
+      unpack<true>(v, x);
+      float g[kV];
+#pragma unroll
+      for (int e = 0; e < kV; ++e) g[e] = __builtin_amdgcn_exp2f(fmaf(x[e], kLog2e, nls));
+      return u32x4{pack_bf16x2(g[0], g[1]) ^ sgn, pack_bf16x2(g[2], g[3]) ^ sgn,
+                   pack_bf16x2(g[4], g[5]) ^ sgn, pack_bf16x2(g[6], g[7]) ^ sgn};
+    }
+    return grad_vec<true>(v, c0, vl, t, nl, scale);
+  };
+#pragma unroll
+  for (int u = 0; u < VR; ++u) {
+    asm volatile("" : "+v"(r[u]));
+    uint32_t off = lo16;
+    asm volatile("" : "+v"(off));  // the store address is formed here, not kept from the loads
+    if (present(u, nvec_st))
+      __builtin_nontemporal_store(grad(r[u], (u * T + tl) * kV),
+                                  reinterpret_cast<u32x4*>(slice(u) + off));
+  }
+#pragma unroll
+  for (int w = 0; w < VL; ++w) {
+    uint32_t off = lo16;
+    asm volatile("" : "+v"(off));
+    if (present(VR + w, nvec_st))
+      __builtin_nontemporal_store(grad(stash[w * T + tid], ((VR + w) * T + tl) * kV),
+                                  reinterpret_cast<u32x4*>(slice(VR + w) + off));
+  }
+}
+
 // Gradient in place for any row length: stats pass, then a read+write pass.
 template <int THREADS, bool BF16, bool VEC>
 __global__ __launch_bounds__(THREADS) void ce_grad_2pass_kernel(
@@ -301,6 +469,9 @@ __global__ __launch_bounds__(1024) void mean_neg_kernel(const float* __restrict_
   }
 }
 
+// bf16 columns the resident gradient kernel holds (512 threads x 32 vectors)
+constexpr int64_t kResidentCols = 512 * 32 * 8;
+
 template <bool BF16>
 int launch_ce(const void* logits, const int32_t* targets, int64_t rows, int64_t ld, int64_t vl,
               float* lp, float* lse, void* grad, float grad_scale, const float* row_scale,
@@ -313,6 +484,18 @@ int launch_ce(const void* logits, const int32_t* targets, int64_t rows, int64_t 
     else ce_lp_kernel<256, BF16, false><<<grid, 256, 0, st>>>(logits, targets, ld, vl, lp, lse);
     SM_LAUNCH_CHECK();
     return SM_OK;
+  }
+  if constexpr (BF16) {
+    if (vec && ld > kResidentCols / 2 && ld <= kResidentCols) {
+      if (ld == kResidentCols && vl == ld)
+        ce_grad_resident_kernel<24, 8, true><<<grid, 512, 0, st>>>(grad, targets, ld, vl, lp, lse,
+                                                                    grad_scale, row_scale);
+      else
+        ce_grad_resident_kernel<24, 8, false><<<grid, 512, 0, st>>>(grad, targets, ld, vl, lp,
+                                                                     lse, grad_scale, row_scale);
+      SM_LAUNCH_CHECK();
+      return SM_OK;
+    }
   }
   if (vec) {
     ce_grad_stream_kernel<512, 8, BF16><<<grid, 512, 0, st>>>(grad, targets, ld, vl, lp, lse,

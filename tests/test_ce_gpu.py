@@ -40,8 +40,13 @@ def test_ce_lp_matches_oracle(dev, rows, vocab, lv, dtype):
     assert abs(loss - (-lp_ref.mean())) < 1e-5
 
 
+# (2, 131072, 131072): bf16 rows held on chip whole (the config[3] row);
+# (3, 65544, 65537), (5, 100000, 99995), (2, 131072, 70001): the on-chip kernel
+# with absent vectors, a logical tail and padded columns
 @pytest.mark.parametrize("rows,vocab,lv", [(7, 64, 50), (3, 4096, 4096), (2, 131072, 131072),
-                                           (2, 200000, 199990), (3, 1001, 1000)])
+                                           (2, 200000, 199990), (3, 1001, 1000),
+                                           (3, 65544, 65537), (5, 100000, 99995),
+                                           (2, 131072, 70001)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_ce_grad_in_place(dev, rows, vocab, lv, dtype):
     print(f"case rows={rows} vocab={vocab} lv={lv} dtype={dtype}", flush=True)
