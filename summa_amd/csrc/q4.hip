@@ -536,6 +536,281 @@ __global__ __launch_bounds__(512) void q4_grouped_lds_kernel(Q4Args a) {
   }
 }
 
+// Dense decode batches with thick waves: q4_grouped_lds_kernel's scheme (each
+// K group's activation tile staged once per workgroup into LDS; weight codes
+// register-direct per wave, dequantised in the wave; per group and 16 x 16
+// block the four k-steps accumulated unscaled, then one scale FMA, so the
+// results are that kernel's bits) with MT 16-row blocks per wave and W waves
+// of NB 16-column blocks per workgroup. Every dequantised B fragment feeds
+// MT x (1 or 2) MFMAs and every A fragment read from LDS NB of them, where
+// the 16-row form pays one LDS read and one dequantisation per two MFMAs.
+template <int W, int MT, int NB, int EPI, int XT>
+__global__ __launch_bounds__(W * 64) void q4_thick_kernel(Q4Args a) {
+  constexpr int NA = (XT == X_F16X2) ? 2 : 1;
+  constexpr int T = W * 64, TM = 16 * MT;
+  constexpr int AP = NA * 128 + 8;            // LDS row (f16): hi | lo | pad
+  constexpr int STG = TM * NA * 16;           // 16-byte chunks per group tile
+  constexpr int SPT = (STG + T - 1) / T;      // chunks per thread
+  __shared__ __attribute__((aligned(16))) _Float16 As[2][TM * AP];
+  const int m0 = (int)blockIdx.y * TM, mlim = a.M;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int j = lane % 16, g = lane / 16;
+  const int c0 = (int)blockIdx.x * W * 16 * NB + wave * 16 * NB;
+  const int ngroups = a.K / 128;
+  const int g0 = a.part ? (int)blockIdx.z * a.gper : 0;  // host: g0 < g1
+  const int g1 = a.part ? min(ngroups, g0 + a.gper) : ngroups;
+  int brow[NB], brow_c[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if constexpr (is_swiglu(EPI)) {
+      const int col = c0 / 2 + (b % (NB / 2)) * 16 + j;
+      brow[b] = (col < a.ncols) ? ((b < NB / 2) ? col : a.ncols + col) : -1;
+    } else {
+      const int col = c0 + b * 16 + j;
+      brow[b] = (col < a.N) ? col : -1;
+    }
+    brow_c[b] = brow[b] >= 0 ? brow[b] : 0;
+  }
+  // staging: chunk c = t + i*T copies 16 bytes of half (c / 16) % NA of tile
+  // row c / (16 NA); rows past M repeat a valid row
+  const int t = threadIdx.x;
+  size_t sxo[SPT];
+  int sdst[SPT];
+#pragma unroll
+  for (int i = 0; i < SPT; ++i) {
+    const int c = min(t + i * T, STG - 1);
+    const int srow = c / (NA * 16), sh = (c / 16) % NA, sc16 = c % 16;
+    const int sprow = min(m0 + srow, mlim - 1);
+    sxo[i] = (size_t)sprow * a.ldx + (size_t)sh * a.K + sc16 * 8;
+    sdst[i] = srow * AP + sh * 128 + sc16 * 8;
+  }
+  auto aload = [&](int kg, u32x4 (&v)[SPT]) {
+    const size_t ko = (size_t)min(kg, g1 - 1) * 128;
+#pragma unroll
+    for (int i = 0; i < SPT; ++i) {
+      if (STG % T == 0 || t + i * T < STG) {
+        if constexpr (XT == X_BF16) {
+          const h8 f = act_frag(
+              *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.x) + sxo[i] + ko));
+          v[i] = __builtin_bit_cast(u32x4, f);
+        } else {
+          v[i] = *reinterpret_cast<const u32x4*>(static_cast<const _Float16*>(a.x) + sxo[i] + ko);
+        }
+      }
+    }
+  };
+  auto astore = [&](int buf, const u32x4 (&v)[SPT]) {
+#pragma unroll
+    for (int i = 0; i < SPT; ++i)
+      if (STG % T == 0 || t + i * T < STG) *reinterpret_cast<u32x4*>(&As[buf][sdst[i]]) = v[i];
+  };
+  auto wload = [&](int kg, u32x4 (&w)[NB], uint16_t (&sr)[NB]) {
+    const int kc = min(kg, g1 - 1);
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      w[b] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(
+          a.codes + q4t_code_offset(brow_c[b], kc, ngroups) + g * 16));
+      sr[b] = a.scales[q4t_scale_index(brow_c[b], kc, ngroups)];
+    }
+  };
+  f4 acc[MT][NB];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int b = 0; b < NB; ++b) acc[mt][b] = f4{0.f, 0.f, 0.f, 0.f};
+  auto group = [&](int kg, const u32x4 (&w)[NB], const uint16_t (&sr)[NB]) {
+    const _Float16* ab = &As[(kg - g0) & 1][j * AP + g * 32];
+    f4 tt[MT][NB];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) tt[mt][b] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s4 = 0; s4 < 4; ++s4) {
+      h8 af[MT][NA];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int h = 0; h < NA; ++h)
+          af[mt][h] = *reinterpret_cast<const h8*>(ab + mt * 16 * AP + h * 128 + s4 * 8);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const h8 bq = q4_unpack(w[b][s4]);
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          tt[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt][0], bq, tt[mt][b], 0, 0, 0);
+          if constexpr (NA == 2)
+            tt[mt][b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af[mt][1], bq, tt[mt][b], 0, 0, 0);
+        }
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const float scl = brow[b] >= 0 ? bf16_to_f32(sr[b]) : 0.f;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[mt][b][r] = fmaf(tt[mt][b][r], scl, acc[mt][b][r]);
+    }
+  };
+  // the two-stage loop of q4_grouped_lds_kernel
+  u32x4 w0[NB], w1[NB];
+  uint16_t s0[NB], s1[NB];
+  u32x4 av[SPT];
+  aload(g0, av);
+  wload(g0, w0, s0);
+  astore(0, av);
+  for (int kg = g0; kg < g1; kg += 2) {
+    aload(kg + 1, av);
+    wload(kg + 1, w1, s1);
+    __syncthreads();
+    group(kg, w0, s0);
+    astore((kg + 1 - g0) & 1, av);
+    if (kg + 1 >= g1) break;
+    aload(kg + 2, av);
+    wload(kg + 2, w0, s0);
+    __syncthreads();
+    group(kg + 1, w1, s1);
+    astore((kg - g0) & 1, av);
+  }
+  // ---- epilogue: lane holds rows m0 + 16 mt + 4g + r of column j of each block
+  if (a.part) {  // split-K partial tile, logical columns (uniform branch)
+    const int lc_total = is_swiglu(EPI) ? 2 * a.ncols : a.N;
+    float* pp = a.part + (size_t)blockIdx.z * a.M * lc_total;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + mt * 16 + 4 * g + r;
+        if (row >= mlim) continue;
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          int lc;
+          if constexpr (is_swiglu(EPI)) {
+            const int hcol = c0 / 2 + (b % (NB / 2)) * 16 + j;
+            if (hcol >= a.ncols) continue;
+            lc = (b < NB / 2) ? hcol : a.ncols + hcol;
+          } else {
+            lc = c0 + b * 16 + j;
+            if (lc >= a.N) continue;
+          }
+          pp[(size_t)row * lc_total + lc] = acc[mt][b][r];
+        }
+      }
+    return;
+  }
+  if constexpr (EPI == 6) {
+    // RoPE pairs (2p, 2p+1) are adjacent columns, i.e. lanes j and j^1 of the
+    // same rows: swap partners before any lane-dependent branch
+    f4 partner[MT][NB];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) partner[mt][b][r] = __shfl_xor(acc[mt][b][r], 1, kWave);
+    if ((j & 1) != 0) return;
+    const int hd_shift = __builtin_ctz(a.hd);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = m0 + mt * 16 + 4 * g + r;
+        const int rc = min(row, mlim - 1);
+        const int sq = (a.rope_L == 1) ? rc : rc / a.rope_L;
+        const int pos = a.pos0[sq] + (rc - sq * a.rope_L);
+        if (row >= mlim || pos < 0 || pos >= a.cap) continue;
+        const float2* rrow = a.rope + (size_t)pos * (a.hd / 2);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int col = c0 + b * 16 + j;
+          if (col >= a.N) continue;
+          const int slot = col >> hd_shift, e = col & (a.hd - 1);
+          const float va = acc[mt][b][r], vb = partner[mt][b][r];  // columns e, e+1
+          h2 out;
+          _Float16* dst;
+          if (slot >= a.H + a.KVH) {  // value: no rotation
+            out = h2{(_Float16)va, (_Float16)vb};
+            dst = a.vc + (((size_t)sq * a.KVH + (slot - a.H - a.KVH)) * a.cap + pos) * a.hd + e;
+          } else {
+            const float2 cs = rrow[e >> 1];
+            out = h2{(_Float16)(va * cs.x - vb * cs.y), (_Float16)(vb * cs.x + va * cs.y)};
+            dst = (slot < a.H) ? a.q_out + ((size_t)row * a.H + slot) * a.hd + e
+                               : a.kc + (((size_t)sq * a.KVH + (slot - a.H)) * a.cap + pos) * a.hd + e;
+          }
+          *reinterpret_cast<h2*>(dst) = out;
+        }
+      }
+    return;
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = m0 + mt * 16 + 4 * g + r;
+      if (row >= mlim) continue;
+      if constexpr (is_swiglu(EPI)) {
+#pragma unroll
+        for (int b = 0; b < NB / 2; ++b) {
+          const int col = c0 / 2 + b * 16 + j;
+          if (col < a.ncols) {
+            const float hv = silu(acc[mt][b][r]) * acc[mt][b + NB / 2][r];
+            if constexpr (EPI == EPI_SWIGLU_F16X2) {
+              _Float16 hi, lo;
+              split_f16(hv, hi, lo);
+              static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = hi;
+              static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + a.ncols + col] = lo;
+            } else if constexpr (EPI == EPI_SWIGLU_F16) {
+              static_cast<_Float16*>(a.y)[(size_t)row * a.ldy + col] = (_Float16)hv;
+            } else {
+              static_cast<uint16_t*>(a.y)[(size_t)row * a.ldy + col] = f32_to_bf16(hv);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int col = c0 + b * 16 + j;
+          if (col >= a.N) continue;
+          const size_t o = (size_t)row * a.ldy + col;
+          if constexpr (EPI == EPI_STORE_F32) static_cast<float*>(a.y)[o] = acc[mt][b][r];
+          else if constexpr (EPI == EPI_ADD_F32) static_cast<float*>(a.y)[o] += acc[mt][b][r];
+          else static_cast<uint16_t*>(a.y)[o] = f32_to_bf16(acc[mt][b][r]);
+        }
+      }
+    }
+}
+
+template <int W, int MT, int NB, int XT>
+int launch_thick(const Q4Args& a, int epi, hipStream_t st, int ks) {
+  const int logical_cols = is_swiglu(epi) ? 2 * a.ncols : a.N;
+  const dim3 grid((unsigned)ceil_div(logical_cols, W * 16 * NB), (unsigned)ceil_div(a.M, 16 * MT),
+                  (unsigned)ks);
+  switch (epi) {  // the SwiGLU FFN-in is the shape it is used for (use_thick)
+#define SM_TK(E) \
+    case E: q4_thick_kernel<W, MT, NB, E, XT><<<grid, W * 64, 0, st>>>(a); break;
+    SM_TK(EPI_SWIGLU_BF16)
+    SM_TK(EPI_SWIGLU_F16)
+    SM_TK(EPI_SWIGLU_F16X2)
+#undef SM_TK
+    default: set_error("sm_q4_matmul: thick kernel for epilogue %d", epi); return SM_ERR_INVALID;
+  }
+  SM_LAUNCH_CHECK();
+  return SM_OK;
+}
+
+// The decode FFN-in at 128 < M <= 256 with more than 8192 gate + value columns
+// (config[2]: M 256, 2 x 5632): 4 waves of 2 x 2 blocks (32 x 128 tiles).
+// Measured against the batch kernel (42.3 us) on that shape, 16-column wave
+// tiles: 33.7 us; 8 waves 34.5; 64-row tiles 40.3; 4 column blocks 38.5; the
+// 16-row form 38.8. Other decode projections measured no faster in this form
+// (qkv 15.6 -> 16-25 us, o 14.6 -> 11.7 us unsplit but the split fused-norm
+// path is faster, down 22.8 -> 30-68 us), so they keep their kernels.
+inline bool use_thick(int64_t M, int64_t logical_cols, int epi, int xt) {
+  return is_swiglu(epi) && (xt == X_F16X2 || xt == X_F16) && M > 128 && M <= 256 &&
+         logical_cols > 8192;
+}
+
 // Dense decode shapes that the LDS-shared kernel serves faster (measured).
 inline bool use_dense_lds(int64_t M, int64_t K, int64_t logical_cols, int xt) {
   return (xt == X_F16X2 || xt == X_F16) && M > 32 && M <= 256 && K <= 2048 &&
@@ -587,6 +862,7 @@ int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_
 template <int XT>
 int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1,
                        bool reduce = true) {
+
   if (!a.tiles && !is_swiglu(epi) && a.M <= 128)
     return launch_grouped_lds_nb<XT, 1>(a, epi, st, row_tiles, ks, reduce);
   return launch_grouped_lds_nb<XT, 2>(a, epi, st, row_tiles, ks, reduce);
@@ -835,6 +1111,10 @@ int dispatch_q4(const Q4Args& a, int epi, int xt, hipStream_t st, void* ws, int6
     }
     if (wgs < 512 && ksplit_ok) return launch_q4<2, 4>(a, epi, xt, st, rt);
     return launch_q4<2, 1>(a, epi, xt, st, rt);
+  }
+  if (!a.tiles && !a.rowidx && use_thick(a.M, logical_cols, epi, xt)) {
+    if (xt == X_F16X2) return launch_thick<4, 2, 2, X_F16X2>(a, epi, st, 1);
+    return launch_thick<4, 2, 2, X_F16>(a, epi, st, 1);
   }
   if (!a.tiles && !a.rowidx && use_dense_lds(a.M, a.K, logical_cols, xt)) {
     if (xt == X_F16X2) return launch_grouped_lds<X_F16X2>(a, epi, st, ceil_div(a.M, 16));

@@ -418,6 +418,40 @@ def test_dense_decode_lds_kernel(dev, m, n, k, pair):
     assert np.all(np.abs(h - ref_h) <= hb + rel * np.abs(ref_h) + 1e-7)
 
 
+@pytest.mark.parametrize("m,n,k", [(256, 11264, 2048), (200, 8320, 512), (129, 8448, 256)])
+@pytest.mark.parametrize("pair", [True, False])
+def test_decode_ffn_in_thick_kernel(dev, m, n, k, pair):
+    """The decode FFN-in shapes (128 < M <= 256, more than 8192 gate + value
+    columns: config[2]'s 256 x 2 x 5632) run the 32 x 128-tile thick-wave
+    kernel: its SwiGLU epilogues (f16 pair, f16, bf16) against float64 on the
+    decoded weights, ragged row tiles included."""
+    print(f"case thick ffn-in m={m} n={n} k={k} pair={pair}", flush=True)
+    w = _weights(n, k, m + 3 * n)
+    codes, scales = oracle.q4_quantize(w)
+    qw = ops.Q4Weight.from_host(codes, scales, n, k, dev)
+    x = np.random.default_rng(m + 5).normal(0, 1, (m, k)).astype(np.float32)
+    if pair:
+        xp, xr = _pair_host(x)
+        xd = torch.from_numpy(xp).to(dev)
+    else:
+        xd = torch.from_numpy(x).to(dev).to(torch.float16)
+        xr = xd.float().cpu().numpy()
+    dense = oracle.q4_decode(codes, scales, n * k).reshape(n, k).astype(np.float64)
+    y_ref = xr.astype(np.float64) @ dense.T
+    tol = 2e-6 * _bound(codes, scales, n, k, xr) + 1e-7
+    F = n // 2
+    g, v = y_ref[:, :F], y_ref[:, F:]
+    ref_h = g / (1 + np.exp(-g)) * v
+    hb = (np.abs(g) + 1) * (tol[:, F:] + tol[:, :F]) * (np.abs(v) + 1)
+    epis = ([(_lib.SM_EPI_SWIGLU_F16X2, ops.unpair, 1e-6)] if pair else
+            [(_lib.SM_EPI_SWIGLU_F16, lambda t: t.float(), 2.0 ** -11),
+             (_lib.SM_EPI_SWIGLU_BF16, lambda t: t.float(), 2.0 ** -8)])
+    for e, conv, rel in epis:
+        h = conv(ops.q4_matmul(qw, xd, pair=pair, epilogue=e)).cpu().numpy()
+        assert h.shape == (m, F)
+        assert np.all(np.abs(h - ref_h) <= hb + rel * np.abs(ref_h) + 1e-7), e
+
+
 @pytest.mark.parametrize("S,H,KVH,hd,K", [(128, 12, 12, 64, 768), (256, 16, 4, 128, 2048),
                                           (40, 16, 16, 128, 2048)])
 def test_dense_decode_lds_qkv_rope(dev, S, H, KVH, hd, K):
