@@ -900,27 +900,36 @@ def bench_decode_attention(args) -> dict:
 
 
 def bench_policy_update(args) -> dict:
-    """The GRPO policy update at config[2] scale (sm_policy_prepare +
-    sm_policy_optimizer_step): one group of 8 rollouts x (512 + 512) per call,
-    recompute with activations kept, the frozen reference's log-probs, the
-    loss and the whole backward into f32 master gradients, then AdamW with the
-    global-norm clip. The rollouts come from the installed Q4 model."""
+    """The GRPO policy update at config[2] scale (``--config 4``: the MoE
+    config[4]) (sm_policy_prepare + sm_policy_optimizer_step): one group of 8
+    rollouts x (prompt + new tokens) per call, recompute with activations kept,
+    the frozen reference's log-probs, the loss and the whole backward into f32
+    master gradients, then AdamW with the global-norm clip. The rollouts come
+    from the installed Q4 model."""
     import torch
 
     from summa_amd import train
     from summa_amd.configs import RL_WORKLOADS
     from summa_amd.model import Model
-    wl = RL_WORKLOADS[2]
+    cfg_id = 4 if args.config == 4 else 2
+    wl = RL_WORKLOADS[cfg_id]
     mc = wl.model_config()
     dev = torch.device("cuda:0")
     d, F, V, Ly = mc.d_model, mc.ffn, mc.vocab, mc.layers
+    E, Fe = mc.experts, mc.expert_ffn
     qn = (mc.heads + 2 * mc.kv_heads) * mc.head_dim
     gen = torch.Generator(device=dev).manual_seed(0)
     nrm = lambda *sh: torch.randn(*sh, generator=gen, device=dev) * 0.02  # noqa: E731
     w = {"embed": nrm(V, d), "lm_head": nrm(V, d), "final_norm": torch.ones(d, device=dev),
          "attn_norm": torch.ones(Ly, d, device=dev), "ffn_norm": torch.ones(Ly, d, device=dev),
-         "qkv": nrm(Ly, qn, d), "o": nrm(Ly, d, mc.heads * mc.head_dim), "in": nrm(Ly, 2 * F, d),
-         "down": nrm(Ly, d, F)}
+         "qkv": nrm(Ly, qn, d), "o": nrm(Ly, d, mc.heads * mc.head_dim)}
+    if E:  # router logits ~ N(0, 1) (the configs' router init), stacked experts
+        w.update(router=torch.randn(Ly, E, d, generator=gen, device=dev) / d ** 0.5,
+                 exp_in=nrm(Ly, E, 2 * Fe, d), exp_down=nrm(Ly, E, d, Fe))
+        ffn_params = E * (3 * Fe * d + d)
+    else:
+        w.update({"in": nrm(Ly, 2 * F, d), "down": nrm(Ly, d, F)})
+        ffn_params = 3 * F * d
     pol = train.Policy(mc, w, dev)
     del w
     ref = Model(mc)
@@ -956,15 +965,15 @@ def bench_policy_update(args) -> dict:
                                   "optimizer_step_ms": round(sum(step) / len(step), 2)}
     p_ms, s_ms = by_planes["3"]["prepare_ms"], by_planes["3"]["optimizer_step_ms"]
     positions = G * (P + N - 1)
-    return {"metric": "GRPO policy update positions/s (config[2], one group per call)",
+    return {"metric": f"GRPO policy update positions/s (config[{cfg_id}], one group per call)",
             "value": positions / ((p_ms + s_ms) / 1e3), "unit": "positions/s",
             "ms_per_step": p_ms + s_ms,
             "dtype": "f32 masters, Q4G128 fake-quantized forward, three-plane bf16 GEMMs",
-            "config": {"workload": "policy_update config[2]", "rollouts": G, "prompt_len": P,
-                       "new_tokens": N},
+            "config": {"workload": f"policy_update config[{cfg_id}]", "rollouts": G,
+                       "prompt_len": P, "new_tokens": N},
             "prepare_ms": round(p_ms, 2), "optimizer_step_ms": round(s_ms, 2),
             "by_matmul_planes": by_planes,
-            "parameters": int(Ly * (qn * d + d * mc.heads * mc.head_dim + 3 * F * d + 2 * d)
+            "parameters": int(Ly * (qn * d + d * mc.heads * mc.head_dim + ffn_params + 2 * d)
                               + 2 * V * d + d),
             "first_prepare_lp_vs_rollout_max_abs": lp_gap}
 

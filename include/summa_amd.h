@@ -767,7 +767,10 @@ int sm_rl_prepare(sm_model* policy, sm_model* reference, const int32_t* prompts,
  * Trainable policy: the gradient and optimizer half of GrpoDeviceBatchRuntime
  * (posttrain.rs:1288-1305): prepare_device_batch stages gradients,
  * optimizer_step(learning_rate_scale) applies them. f32 master weights of a
- * dense decoder ([out, in] rows, tensor kinds SM_W_EMBED .. SM_W_LM_HEAD); a
+ * dense decoder ([out, in] rows, tensor kinds SM_W_EMBED .. SM_W_LM_HEAD) or
+ * of a top-2 MoE decoder (no SM_W_IN / SM_W_DOWN; SM_W_ROUTER, SM_W_EXPERT_IN,
+ * SM_W_EXPERT_DOWN per layer: SparseMoe, ffn.rs:478-711, trained through its
+ * combine, per-expert GEMM, gather and pair-softmax router gradients); a
  * quantized config runs its forward on fake-quantized weights (Q4G128
  * linears, bf16 embedding: what sm_policy_install puts into a quantized
  * model) with straight-through gradients (trainer.rs:312-318).

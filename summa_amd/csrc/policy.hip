@@ -7,18 +7,22 @@
 // summa-train/src/main.rs:667-694; Muon for the per-layer projections and
 // AdamW for the rest, trainer.rs:1124-1129, 1974-1975; muon.rs:196-285).
 //
-// Weights are f32 master copies of a dense decoder in the model's [out, in]
-// rows. For a quantized configuration the forward runs on fake-quantized
-// weights (Q4G128 linears, bf16 embedding: the values the inference model
-// holds after sm_policy_install) and the gradient passes straight through to
-// the masters (the fake-quantized parameter leaves of trainer.rs:312-318), so
-// the recomputed log-probs are those of the model that produced the rollouts.
+// Weights are f32 master copies of a dense or top-2 MoE decoder in the
+// model's [out, in] rows (an MoE layer: f32 router [E, d], experts stacked
+// [E * 2Fe, d] and [E * d, Fe]). For a quantized configuration the forward
+// runs on fake-quantized weights (Q4G128 linears and experts, bf16 embedding,
+// f32 router: the values the inference model holds after sm_policy_install)
+// and the gradient passes straight through to the masters (the fake-quantized
+// parameter leaves of trainer.rs:312-318), so the recomputed log-probs are
+// those of the model that produced the rollouts.
 //
 // Host composition over the library's kernels (the same steps as the Python
-// composition in summa_amd/train.py): embedding, RMSNorm, GEMMs, RoPE,
-// attention with its log-sum-exp, SwiGLU, fused CE; backward through the CE
-// gradient, GEMM data / weight gradients, RMSNorm, RoPE, attention, SwiGLU and
-// embedding backward kernels.
+// composition in summa_amd/train.py for dense layers): embedding, RMSNorm,
+// GEMMs, RoPE, attention with its log-sum-exp, SwiGLU (dense, or per expert
+// over the routes sorted by expert: router top-2, route plan, gather,
+// combine), fused CE; backward through the CE gradient, GEMM data / weight
+// gradients, RMSNorm, RoPE, attention, SwiGLU, the MoE combine / gather /
+// router gradients and embedding backward kernels.
 #include <cmath>
 #include <vector>
 
@@ -54,6 +58,18 @@ int sm_rl_logprobs(sm_model*, const int32_t*, const int32_t*, int64_t, int64_t, 
                    float*, void*);
 int sm_model_set_tensor(sm_model*, int, int, const float*, void*);
 int sm_q4_quantize(const void*, int, int64_t, uint8_t*, uint16_t*, int32_t*, void*);
+int64_t sm_moe_plan_words(int64_t, int64_t, int64_t);
+int sm_moe_router_top2(const void*, int, const float*, int64_t, int64_t, int64_t, float*, int32_t*,
+                       float*, void*);
+int sm_moe_route_plan(const int32_t*, int64_t, int64_t, int64_t, int32_t*, int32_t*, void*);
+int sm_moe_gather(const void*, int, const int32_t*, int64_t, int64_t, int64_t, int64_t, void*,
+                  void*);
+int sm_moe_gather_backward(const void*, int, const int32_t*, int64_t, int64_t, int64_t, int64_t,
+                           void*, void*);
+int sm_moe_combine(const float*, const float*, const int32_t*, int64_t, int64_t, int64_t, int64_t,
+                   float*, void*);
+int sm_moe_combine_backward(const void*, const void*, int, const float*, const int32_t*, int64_t,
+                            int64_t, int64_t, int64_t, void*, float*, void*);
 }
 
 namespace sm {
@@ -66,7 +82,8 @@ int rmsnorm_backward_parts(const float* x, const float* gamma, const float* dy, 
                            float* rinv_scratch, float* parts, hipStream_t st);
 namespace {
 
-constexpr int kKinds = 9;  // SM_W_EMBED .. SM_W_LM_HEAD
+constexpr int kKinds = 12;  // SM_W_EMBED .. SM_W_EXPERT_DOWN (a dense policy has no MoE kinds,
+                            // an MoE policy no dense FFN: those kinds have no elements)
 constexpr float kMuonMomentum = 0.95f;                          // muon.rs:10
 constexpr float kNsA = 3.4445f, kNsB = -4.775f, kNsC = 2.0315f;  // muon.rs:11
 constexpr int kNsSteps = 5;                                     // muon.rs:12
@@ -74,10 +91,13 @@ constexpr float kMuonEps = 1e-7f;                               // muon.rs:13
 
 bool is_layer_kind(int k) {
   return k == SM_W_ATTN_NORM || k == SM_W_QKV || k == SM_W_O || k == SM_W_FFN_NORM ||
-         k == SM_W_IN || k == SM_W_DOWN;
+         k == SM_W_IN || k == SM_W_DOWN || k == SM_W_ROUTER || k == SM_W_EXPERT_IN ||
+         k == SM_W_EXPERT_DOWN;
 }
+// the kinds a quantized model holds as Q4G128 (the router stays f32, ffn.rs:489)
 bool is_linear_kind(int k) {
-  return k == SM_W_QKV || k == SM_W_O || k == SM_W_IN || k == SM_W_DOWN || k == SM_W_LM_HEAD;
+  return k == SM_W_QKV || k == SM_W_O || k == SM_W_IN || k == SM_W_DOWN || k == SM_W_LM_HEAD ||
+         k == SM_W_EXPERT_IN || k == SM_W_EXPERT_DOWN;
 }
 bool is_muon_kind(int k) {  // the per-layer 2-D projections (trainer.rs:1974)
   return k == SM_W_QKV || k == SM_W_O || k == SM_W_IN || k == SM_W_DOWN;
@@ -163,6 +183,24 @@ __global__ void q4_decode_f32(const uint8_t* __restrict__ codes, const uint16_t*
 }
 // sum of squares (f64) of each 64 K-value chunk of `a` -> part[blockIdx.x]
 constexpr int64_t kSumChunk = 65536;
+// d logits of the top-2 router (weights = softmax over the two selected
+// logits, ffn.rs:494-507): dl[t, e] = p_j (g_j - sum_i p_i g_i) for the expert
+// e = idx[t, j] chosen in slot j, 0 for the unselected experts.
+__global__ void router_grad_kernel(const float* __restrict__ top_w, const float* __restrict__ gw,
+                                   const int32_t* __restrict__ idx, int64_t tokens, int E,
+                                   float* __restrict__ dl) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= tokens * E) return;
+  const int64_t t = i / E;
+  const int e = (int)(i % E);
+  const float p0 = top_w[2 * t], p1 = top_w[2 * t + 1];
+  const float g0 = gw[2 * t], g1 = gw[2 * t + 1];
+  const float mean = p0 * g0 + p1 * g1;
+  float v = 0.f;
+  if (idx[2 * t] == e) v = p0 * (g0 - mean);
+  else if (idx[2 * t + 1] == e) v = p1 * (g1 - mean);
+  dl[i] = v;
+}
 __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ a, int64_t n,
                                                     double* __restrict__ part) {
   __shared__ double wp[256 / kWave];
@@ -270,7 +308,7 @@ int fake_quantize(sm_policy* p, hipStream_t st) {
   uint8_t* codes = (uint8_t*)p->scratch.p;
   uint16_t* scales = (uint16_t*)(codes + groups * 64);
   for (int k = 0; k < kKinds; ++k) {
-    if (!is_linear_kind(k)) continue;
+    if (!is_linear_kind(k) || p->count[k] == 0) continue;
     const int64_t n = p->rows_per_layer[k] * p->cols[k];
     const int layers = (k == SM_W_LM_HEAD) ? 1 : c.layers;
     for (int l = 0; l < layers; ++l) {
@@ -326,10 +364,13 @@ extern "C" int sm_policy_create(const sm_model_config* cfg, const sm_optimizer_c
                  c.heads % c.kv_heads == 0 && c.ffn > 0 && c.vocab > 0 && c.max_seq > 0,
              "sm_policy_create: invalid model config");
   SM_REQUIRE(c.head_dim == 64 || c.head_dim == 128, "sm_policy_create: head_dim must be 64 or 128");
-  SM_REQUIRE(c.experts == 0, "sm_policy_create: the trainable policy is a dense decoder");
+  SM_REQUIRE(c.experts == 0 || (c.experts >= 2 && c.experts <= 64 && c.expert_ffn > 0),
+             "sm_policy_create: MoE configs need 2..=64 experts and expert_ffn > 0");
   if (c.quantized)
-    SM_REQUIRE(c.d_model % 128 == 0 && c.ffn % 128 == 0 && (c.heads * c.head_dim) % 128 == 0,
-               "sm_policy_create: quantized models need d_model, ffn and heads*head_dim % 128 == 0");
+    SM_REQUIRE(c.d_model % 128 == 0 && c.ffn % 128 == 0 && (c.heads * c.head_dim) % 128 == 0 &&
+                   (c.experts == 0 || c.expert_ffn % 128 == 0),
+               "sm_policy_create: quantized models need d_model, ffn, heads*head_dim (and "
+               "expert_ffn) %% 128 == 0");
   SM_REQUIRE(std::isfinite(opt->lr) && opt->lr >= 0.f && opt->beta1 >= 0.f && opt->beta1 < 1.f &&
                  opt->beta2 >= 0.f && opt->beta2 < 1.f && opt->eps > 0.f &&
                  opt->weight_decay >= 0.f && opt->muon_lr >= 0.f && std::isfinite(opt->grad_clip),
@@ -340,14 +381,19 @@ extern "C" int sm_policy_create(const sm_model_config* cfg, const sm_optimizer_c
   p->qdim = (int64_t)c.heads * c.head_dim;
   p->kvdim = (int64_t)c.kv_heads * c.head_dim;
   p->qn = p->qdim + 2 * p->kvdim;
-  const int64_t d = c.d_model, F = c.ffn;
+  const int64_t d = c.d_model, F = c.ffn, E = c.experts, Fe = c.expert_ffn;
+  const bool moe = E > 0;
+  // per-layer [rows, cols]: an MoE layer's experts stack along the rows
+  // ([E * 2Fe, d] and [E * d, Fe]) and replace the dense FFN
   const int64_t shape[kKinds][2] = {{c.vocab, d}, {1, d}, {p->qn, d}, {d, p->qdim}, {1, d},
-                                    {2 * F, d},  {d, F}, {1, d},     {c.vocab, d}};
+                                    {moe ? 0 : 2 * F, d}, {moe ? 0 : d, F}, {1, d},
+                                    {c.vocab, d}, {E, d}, {E * 2 * Fe, d}, {E * d, Fe}};
   auto fail = [&](int s) { sm_policy_destroy(p); return s; };
   for (int k = 0; k < kKinds; ++k) {
     p->rows_per_layer[k] = shape[k][0];
     p->cols[k] = shape[k][1];
     p->count[k] = shape[k][0] * shape[k][1] * (is_layer_kind(k) ? c.layers : 1);
+    if (p->count[k] == 0) continue;
     int s;
     if ((s = palloc(p, &p->w[k], p->count[k])) || (s = palloc(p, &p->g[k], p->count[k])) ||
         (s = palloc(p, &p->m1[k], p->count[k])) || (s = palloc(p, &p->m2[k], p->count[k])))
@@ -398,6 +444,7 @@ extern "C" int sm_policy_set_tensor(sm_policy* p, int kind, int layer, const flo
                                     void* stream) {
   SM_REQUIRE(p && src, "sm_policy_set_tensor: null argument");
   SM_REQUIRE(kind >= 0 && kind < kKinds, "sm_policy_set_tensor: tensor kind %d", kind);
+  SM_REQUIRE(p->count[kind] > 0, "sm_policy_set_tensor: tensor kind %d is not part of this policy", kind);
   const int64_t n = p->rows_per_layer[kind] * p->cols[kind];
   float* dst = p->w[kind];
   if (is_layer_kind(kind)) {
@@ -412,6 +459,7 @@ extern "C" int sm_policy_get_tensor(const sm_policy* p, int kind, int layer, flo
                                     int gradient, void* stream) {
   SM_REQUIRE(p && dst, "sm_policy_get_tensor: null argument");
   SM_REQUIRE(kind >= 0 && kind < kKinds, "sm_policy_get_tensor: tensor kind %d", kind);
+  SM_REQUIRE(p->count[kind] > 0, "sm_policy_get_tensor: tensor kind %d is not part of this policy", kind);
   const int64_t n = p->rows_per_layer[kind] * p->cols[kind];
   const float* src = gradient ? p->g[kind] : p->w[kind];
   if (is_layer_kind(kind)) {
@@ -425,6 +473,7 @@ extern "C" int sm_policy_get_tensor(const sm_policy* p, int kind, int layer, flo
 extern "C" int sm_policy_install(const sm_policy* p, sm_model* model, void* stream) {
   SM_REQUIRE(p && model, "sm_policy_install: null argument");
   for (int k = 0; k < kKinds; ++k) {
+    if (p->count[k] == 0) continue;
     const int64_t n = p->rows_per_layer[k] * p->cols[k];
     const int layers = is_layer_kind(k) ? p->cfg.layers : 1;
     for (int l = 0; l < layers; ++l)
@@ -460,16 +509,27 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   const int64_t d = c.d_model, H = c.heads, KVH = c.kv_heads, hd = c.head_dim, F = c.ffn;
   const int64_t V = c.vocab, qn = p->qn, qdim = p->qdim;
   if (c.quantized) SM_TRY(fake_quantize(p, st));
-  // ---- activation arena: per layer x0, h, qkv, q, k, v, o, lse, x1, h2, u, a
-  const int64_t per_layer = M * (d + d + qn + qdim + 2 * p->kvdim + qdim + H + d + d + 2 * F + F);
+  // ---- activation arena: per layer x0, h, qkv, q, k, v, o, lse, x1, h2 and the
+  // FFN's u, a (dense) or its routing and routed rows (MoE: top-2 indices and
+  // weights, route plan, gathered input, [gate | value], SwiGLU, expert output)
+  const int64_t E = c.experts, Fe = c.expert_ffn, RT = 2 * M;  // MoE routes (top-2)
+  const bool moe = E > 0;
+  const int64_t plan_words = moe ? sm_moe_plan_words(M, 2, E) : 0;
+  const int64_t ffn_layer = moe ? 2 * M + 2 * M + plan_words + RT * (d + 2 * Fe + Fe + d)
+                                : M * (2 * F + F);
+  const int64_t ffn_fixed = moe ? RT * d /*dyr*/ + 2 * M /*gw*/ + RT * Fe /*dar*/ +
+                                      RT * 2 * Fe /*dur*/ + RT * d /*drt*/ + M * E /*dlog*/ + 1
+                                : M * 2 * F /*du*/ + M * F /*da*/;
+  const int64_t per_layer =
+      M * (d + d + qn + qdim + 2 * p->kvdim + qdim + H + d + d) + ffn_layer;
   const int64_t fixed = M * d /*x*/ + M * d /*hf*/ + R * d /*hr*/ + R * V /*logits*/ +
-                        M * d /*dx*/ + M * d /*dhf*/ + R * d /*dhr*/ + M * 2 * F /*du*/ +
-                        M * F /*da*/ + M * d /*dh*/ + M * qdim /*do*/ + M * qdim /*dq*/ +
+                        M * d /*dx*/ + M * d /*dhf*/ + R * d /*dhr*/ + ffn_fixed +
+                        M * d /*dh*/ + M * qdim /*do*/ + M * qdim /*dq*/ +
                         2 * S * KVH * L * hd /*dk dv*/ + M * qn /*dqkv*/ + M /*rinv*/ +
                         S * H * L /*delta*/ + R /*row scale*/ + d /*dgamma final*/ + S /*pos0*/ +
                         rmsnorm_dgamma_chunks(M) * d /*dgamma parts*/;
   const size_t bytes = (size_t)(per_layer * c.layers + fixed) * 4 + (size_t)M * 4 /*ids*/ +
-                       (size_t)R * 8 /*rows*/ + (size_t)(12 * c.layers + 32) * 256;
+                       (size_t)R * 8 /*rows*/ + (size_t)(20 * c.layers + 48) * 256;
   SM_TRY(grow(p->act, bytes));
   char* cur = (char*)p->act.p;
   auto take = [&](int64_t n, size_t elem = 4) {
@@ -477,14 +537,26 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
     cur += ((size_t)n * elem + 255) / 256 * 256;
     return (void*)r;
   };
-  struct Saved { float *x0, *h, *qkv, *q, *k, *v, *o, *lse, *x1, *h2, *u, *a; };
+  struct Saved {
+    float *x0, *h, *qkv, *q, *k, *v, *o, *lse, *x1, *h2, *u, *a;
+    int32_t *tidx, *plan;
+    float *tw, *rt, *ur, *ar, *yr;
+    std::vector<int32_t> off;  // MoE: first sorted route of each expert (host)
+  };
   std::vector<Saved> sv(c.layers);
   for (auto& s : sv) {
     s.x0 = (float*)take(M * d); s.h = (float*)take(M * d); s.qkv = (float*)take(M * qn);
     s.q = (float*)take(M * qdim); s.k = (float*)take(S * KVH * L * hd);
     s.v = (float*)take(S * KVH * L * hd); s.o = (float*)take(M * qdim);
     s.lse = (float*)take(S * H * L); s.x1 = (float*)take(M * d); s.h2 = (float*)take(M * d);
-    s.u = (float*)take(M * 2 * F); s.a = (float*)take(M * F);
+    if (moe) {
+      s.tidx = (int32_t*)take(2 * M); s.tw = (float*)take(2 * M);
+      s.plan = (int32_t*)take(plan_words); s.rt = (float*)take(RT * d);
+      s.ur = (float*)take(RT * 2 * Fe); s.ar = (float*)take(RT * Fe); s.yr = (float*)take(RT * d);
+      s.off.assign(E + 1, 0);
+    } else {
+      s.u = (float*)take(M * 2 * F); s.a = (float*)take(M * F);
+    }
   }
   float* x = (float*)take(M * d);
   float* hf = (float*)take(M * d);
@@ -493,8 +565,16 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   float* dx = (float*)take(M * d);
   float* dhf = (float*)take(M * d);
   float* dhr = (float*)take(R * d);
-  float* du = (float*)take(M * 2 * F);
-  float* da = (float*)take(M * F);
+  float *du = nullptr, *da = nullptr, *dyr = nullptr, *gw = nullptr, *dar = nullptr;
+  float *dur = nullptr, *drt = nullptr, *dlog = nullptr;
+  int32_t* perr = nullptr;
+  if (moe) {
+    dyr = (float*)take(RT * d); gw = (float*)take(2 * M); dar = (float*)take(RT * Fe);
+    dur = (float*)take(RT * 2 * Fe); drt = (float*)take(RT * d); dlog = (float*)take(M * E);
+    perr = (int32_t*)take(1);
+  } else {
+    du = (float*)take(M * 2 * F); da = (float*)take(M * F);
+  }
   float* dh = (float*)take(M * d);
   float* dO = (float*)take(M * qdim);
   float* dq = (float*)take(M * qdim);
@@ -528,11 +608,43 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
     SM_TRY(pgemm(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
                       stream));
     SM_TRY(sm_rmsnorm(s.x1, fwl(p, SM_W_FFN_NORM, l), M, d, c.norm_eps, s.h2, SM_F32, stream));
-    SM_TRY(pgemm(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
-                      stream));
-    SM_TRY(sm_swiglu(s.u, SM_F32, M, F, s.a, stream));
     SM_HIP(hipMemcpyAsync(x, s.x1, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
-    SM_TRY(pgemm(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
+    if (moe) {
+      // SparseMoe::forward (ffn.rs:478-711): f32 router, top-2 with the weights
+      // a softmax over the pair, dropless expert SwiGLU FFNs over the routes
+      // sorted by expert, weighted combine into the residual
+      SM_TRY(sm_moe_router_top2(s.h2, SM_F32, fwl(p, SM_W_ROUTER, l), M, d, E, nullptr, s.tidx,
+                                s.tw, stream));
+      SM_HIP(hipMemsetAsync(perr, 0, 4, st));
+      SM_TRY(sm_moe_route_plan(s.tidx, M, 2, E, s.plan, perr, stream));
+      SM_TRY(sm_moe_gather(s.h2, SM_F32, s.plan, M, 2, E, d, s.rt, stream));
+      // the expert row ranges on the host, for one GEMM per expert (as the
+      // reference reads its counts, ffn.rs:586-598)
+      SM_HIP(hipMemcpyAsync(s.off.data(), s.plan + E, (size_t)(E + 1) * 4,
+                            hipMemcpyDeviceToHost, st));
+      SM_HIP(hipStreamSynchronize(st));
+      const float* win = fwl(p, SM_W_EXPERT_IN, l);
+      const float* wdn = fwl(p, SM_W_EXPERT_DOWN, l);
+      for (int64_t e = 0; e < E; ++e) {
+        const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
+        if (n <= 0) continue;
+        SM_TRY(pgemm(0, 1, n, 2 * Fe, d, 1.f, s.rt + o0 * d, d, win + e * 2 * Fe * d, d, 0.f,
+                     s.ur + o0 * 2 * Fe, 2 * Fe, stream));
+      }
+      SM_TRY(sm_swiglu(s.ur, SM_F32, RT, Fe, s.ar, stream));
+      for (int64_t e = 0; e < E; ++e) {
+        const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
+        if (n <= 0) continue;
+        SM_TRY(pgemm(0, 1, n, d, Fe, 1.f, s.ar + o0 * Fe, Fe, wdn + e * d * Fe, Fe, 0.f,
+                     s.yr + o0 * d, d, stream));
+      }
+      SM_TRY(sm_moe_combine(s.yr, s.tw, s.plan, M, 2, E, d, x, stream));
+    } else {
+      SM_TRY(pgemm(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
+                   stream));
+      SM_TRY(sm_swiglu(s.u, SM_F32, M, F, s.a, stream));
+      SM_TRY(pgemm(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
+    }
   }
   SM_TRY(sm_rmsnorm(x, fw(p, SM_W_FINAL_NORM), M, d, c.norm_eps, hf, SM_F32, stream));
   gather_rows_f32<<<blocks256(R * d), 256, 0, st>>>(hf, rows, R, (int)d, hr);
@@ -559,14 +671,51 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   SM_TRY(sm_axpby(dgf, p->g[SM_W_FINAL_NORM], d, 1.f, 1.f, stream));
   for (int l = c.layers - 1; l >= 0; --l) {
     Saved& s = sv[l];
-    // FFN: x = x1 + swiglu(h2 W_in^T) W_down^T
-    SM_TRY(pgemm(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
-    SM_TRY(pgemm(1, 0, d, F, M, 1.f, dx, d, s.a, F, 1.f, gl(p, SM_W_DOWN, l), F, stream));
-    SM_TRY(sm_swiglu_backward(s.u, da, SM_F32, M, F, du, stream));
-    SM_TRY(pgemm(1, 0, 2 * F, d, M, 1.f, du, 2 * F, s.h2, d, 1.f, gl(p, SM_W_IN, l), d,
-                      stream));
-    SM_TRY(pgemm(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
-                      stream));
+    if (moe) {
+      // x = x1 + sum_j w_j expert_{i_j}(h2): the combine's gradient to the
+      // routed outputs and to the weights, the experts' data and weight
+      // gradients per expert, the gather's sum back to the tokens, then the
+      // router (d logits of the pair through the pair softmax; f32-grade GEMMs
+      // as the reference keeps router math in f32)
+      SM_TRY(sm_moe_combine_backward(dx, s.yr, SM_F32, s.tw, s.plan, M, 2, E, d, dyr, gw,
+                                     stream));
+      const float* win = fwl(p, SM_W_EXPERT_IN, l);
+      const float* wdn = fwl(p, SM_W_EXPERT_DOWN, l);
+      float* gin = gl(p, SM_W_EXPERT_IN, l);
+      float* gdn = gl(p, SM_W_EXPERT_DOWN, l);
+      for (int64_t e = 0; e < E; ++e) {
+        const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
+        if (n <= 0) continue;
+        SM_TRY(pgemm(0, 0, n, Fe, d, 1.f, dyr + o0 * d, d, wdn + e * d * Fe, Fe, 0.f,
+                     dar + o0 * Fe, Fe, stream));
+        SM_TRY(pgemm(1, 0, d, Fe, n, 1.f, dyr + o0 * d, d, s.ar + o0 * Fe, Fe, 1.f,
+                     gdn + e * d * Fe, Fe, stream));
+      }
+      SM_TRY(sm_swiglu_backward(s.ur, dar, SM_F32, RT, Fe, dur, stream));
+      for (int64_t e = 0; e < E; ++e) {
+        const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
+        if (n <= 0) continue;
+        SM_TRY(pgemm(1, 0, 2 * Fe, d, n, 1.f, dur + o0 * 2 * Fe, 2 * Fe, s.rt + o0 * d, d, 1.f,
+                     gin + e * 2 * Fe * d, d, stream));
+        SM_TRY(pgemm(0, 0, n, d, 2 * Fe, 1.f, dur + o0 * 2 * Fe, 2 * Fe, win + e * 2 * Fe * d,
+                     d, 0.f, drt + o0 * d, d, stream));
+      }
+      SM_TRY(sm_moe_gather_backward(drt, SM_F32, s.plan, M, 2, E, d, dh, stream));
+      router_grad_kernel<<<blocks256(M * E), 256, 0, st>>>(s.tw, gw, s.tidx, M, (int)E, dlog);
+      SM_TRY(gemm_ex_planes(3, 0, 0, M, d, E, 1.f, dlog, E, fwl(p, SM_W_ROUTER, l), d, 1.f, dh,
+                            d, stream));
+      SM_TRY(gemm_ex_planes(3, 1, 0, E, d, M, 1.f, dlog, E, s.h2, d, 1.f,
+                            gl(p, SM_W_ROUTER, l), d, stream));
+    } else {
+      // FFN: x = x1 + swiglu(h2 W_in^T) W_down^T
+      SM_TRY(pgemm(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
+      SM_TRY(pgemm(1, 0, d, F, M, 1.f, dx, d, s.a, F, 1.f, gl(p, SM_W_DOWN, l), F, stream));
+      SM_TRY(sm_swiglu_backward(s.u, da, SM_F32, M, F, du, stream));
+      SM_TRY(pgemm(1, 0, 2 * F, d, M, 1.f, du, 2 * F, s.h2, d, 1.f, gl(p, SM_W_IN, l), d,
+                   stream));
+      SM_TRY(pgemm(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
+                   stream));
+    }
     SM_TRY(rmsnorm_backward_parts(s.x1, fwl(p, SM_W_FFN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
                                   gl(p, SM_W_FFN_NORM, l), rinv, dgparts, st));
     // attention: x1 = x0 + attn(rope(h W_qkv^T)) W_o^T
@@ -601,7 +750,7 @@ extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale
   for (int k = 0; k < kKinds; ++k) maxn = std::max(maxn, p->rows_per_layer[k] * p->cols[k]);
   int64_t ns_floats = 0;  // Newton-Schulz scratch: 2 N K + 2 min(N, K)^2 + 1 per projection
   for (int k = 0; k < kKinds; ++k)
-    if (is_muon_kind(k)) {
+    if (is_muon_kind(k) && p->count[k] > 0) {
       const int64_t n = p->rows_per_layer[k], kk = p->cols[k], r = std::min(n, kk);
       ns_floats = std::max(ns_floats, 2 * n * kk + 2 * r * r + 1);
     }
@@ -615,6 +764,7 @@ extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale
   float* ns_tmp = upd + maxn;
   for (int k = 0, off = 0; k < kKinds; ++k) {
     const int64_t nb = ceil_div(p->count[k], kSumChunk);
+    if (nb == 0) continue;
     sumsq_kernel<<<(unsigned)nb, 256, 0, st>>>(p->g[k], p->count[k], parts + off);
     off += (int)nb;
   }
@@ -628,8 +778,9 @@ extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale
   SM_REQUIRE(std::isfinite(norm), "non-finite gradient norm at optimizer step %lld: %g",
              (long long)(p->adam_step + 1), (double)norm);
   for (int k = 0; k < kKinds; ++k)
-    clip_scale_kernel<<<blocks256(p->count[k]), 256, 0, st>>>(p->g[k], p->count[k], acc,
-                                                              p->opt.grad_clip);
+    if (p->count[k] > 0)
+      clip_scale_kernel<<<blocks256(p->count[k]), 256, 0, st>>>(p->g[k], p->count[k], acc,
+                                                                p->opt.grad_clip);
   SM_LAUNCH_CHECK();
   const auto& o = p->opt;
   const float lr = (float)(o.lr * learning_rate_scale);
@@ -638,6 +789,7 @@ extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale
   ++p->adam_step;
   if (muon) ++p->muon_step;
   for (int k = 0; k < kKinds; ++k) {
+    if (p->count[k] == 0) continue;
     if (muon && is_muon_kind(k)) {
       // BatchedMuon::step (muon.rs:196-215): momentum, Newton-Schulz, and the
       // learning rate scaled by sqrt(max(1, d_in / d_out)) of Burn's [d_in, d_out]

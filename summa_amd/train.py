@@ -25,6 +25,8 @@ from ._lib import SM_F32, call
 from .model import Model, ModelConfig
 
 LAYER_KEYS = ("attn_norm", "qkv", "o", "ffn_norm", "in", "down")
+# per-layer tensors of an MoE policy (stacked experts, the f32 router)
+MOE_LAYER_KEYS = ("router", "exp_in", "exp_down")
 MUON_MOMENTUM = 0.95                       # muon.rs:10
 NS_COEFFICIENTS = (3.4445, -4.775, 2.0315)  # muon.rs:11
 NS_STEPS = 5                               # muon.rs:12
@@ -261,7 +263,8 @@ class OptimizerConfigC(C.Structure):
 
 
 _POLICY_KINDS = {"embed": 0, "attn_norm": 1, "qkv": 2, "o": 3, "ffn_norm": 4, "in": 5,
-                 "down": 6, "final_norm": 7, "lm_head": 8}
+                 "down": 6, "final_norm": 7, "lm_head": 8, "router": 9, "exp_in": 10,
+                 "exp_down": 11}
 
 
 class Policy:
@@ -290,7 +293,7 @@ class Policy:
                 t = arr.to(device=device, dtype=torch.float32).contiguous()
             else:
                 t = torch.as_tensor(np.ascontiguousarray(arr, dtype=np.float32)).to(device)
-            if name in LAYER_KEYS:
+            if name in LAYER_KEYS or name in MOE_LAYER_KEYS:
                 for i in range(cfg.layers):
                     call("sm_policy_set_tensor", self._h, _POLICY_KINDS[name], i,
                          t[i].contiguous().data_ptr(), _st())
@@ -319,9 +322,11 @@ class Policy:
         """A master weight (or its staged gradient), [out, in] rows."""
         c = self.cfg
         d, F, qn = c.d_model, c.ffn, (c.heads + 2 * c.kv_heads) * c.head_dim
+        E, Fe = c.experts, c.expert_ffn
         shape = {"embed": (c.vocab, d), "lm_head": (c.vocab, d), "attn_norm": (d,),
                  "ffn_norm": (d,), "final_norm": (d,), "qkv": (qn, d),
-                 "o": (d, c.heads * c.head_dim), "in": (2 * F, d), "down": (d, F)}[name]
+                 "o": (d, c.heads * c.head_dim), "in": (2 * F, d), "down": (d, F),
+                 "router": (E, d), "exp_in": (E, 2 * Fe, d), "exp_down": (E, d, Fe)}[name]
         out = torch.empty(shape, dtype=torch.float32, device=self.dev)
         call("sm_policy_get_tensor", self._h, _POLICY_KINDS[name], layer, out.data_ptr(),
              int(gradient), _st())

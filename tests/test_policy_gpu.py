@@ -15,7 +15,7 @@ from summa_amd.model import Model, ModelConfig, rl_prepare
 
 from _workloads import build_models
 from summa_amd.configs import RL_WORKLOADS
-from test_train_gpu import CFG, _torch_lp
+from test_train_gpu import CFG, _attn_t, _rope_t, _torch_lp
 
 pytestmark = pytest.mark.gpu
 
@@ -109,18 +109,21 @@ def test_native_policy_gradient_on_matrix_cores(dev, planes):
 
 
 @pytest.mark.timeout(600)
-def test_policy_at_config2_geometry_against_oracle(dev):
+@pytest.mark.parametrize("cfg_id", [2, 4])
+def test_policy_at_full_geometry_against_oracle(dev, cfg_id):
     """The trainable policy at config[2]'s full geometry (24 layers, d 2048,
     16 / 4 heads, F 5632, V 65536: 1.35 G f32 masters, fake-quantized Q4G128
-    forward) on a small batch rolled out by the installed Q4 model: its
+    forward) and at config[4]'s (16 MoE layers of 32 experts, top-2, f32
+    routers) on a small batch rolled out by the installed Q4 model: its
     recompute (f32 activations, matrix-core GEMMs at these shapes, tiled
     attention) against the CPU oracle's quantized model with q, k and v kept
     in f32 as the policy keeps them (an f32 computation: 5e-5 after 24
     layers; measured 1e-5), then one optimizer step (finite norm) after which the installed
     model's log-probs move."""
-    wl = RL_WORKLOADS[2]
+    wl = RL_WORKLOADS[cfg_id]
     mc, (model,), host_w = build_models(wl, dev, seed=3, count=1)
-    print(f"case policy at config[2] geometry: layers={mc.layers} d={mc.d_model}", flush=True)
+    print(f"case policy at config[{cfg_id}] geometry: layers={mc.layers} d={mc.d_model} "
+          f"experts={mc.experts}", flush=True)
     pol = train.Policy(mc, host_w, dev)
     G, P, N = 4, 24, 8
     gen = torch.Generator().manual_seed(11)
@@ -143,6 +146,103 @@ def test_policy_at_config2_geometry_against_oracle(dev):
     before = model.logprobs(prompts, tok)
     pol.install(model)
     assert float((model.logprobs(prompts, tok) - before).abs().max()) > 0
+
+
+MOE_CFG = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
+                      vocab=1000, max_seq=32, quantized=False, experts=4, expert_ffn=128)
+
+
+def _torch_lp_moe(w, cfg, prompts, tokens):
+    """Independent float64 restatement of an MoE decoder's recompute: f64
+    router, the top two experts by logit (the first index on equal logits),
+    weights softmax over the pair, SwiGLU experts, weighted sum
+    (SparseMoe::forward, ffn.rs:478-711). Also returns, per layer, the gap
+    between each token's second and third largest router logits."""
+    S, P = prompts.shape
+    N = tokens.shape[1]
+    L = P + N - 1
+    H, KVH, hd, eps = cfg.heads, cfg.kv_heads, cfg.head_dim, cfg.norm_eps
+    E, Fe = cfg.experts, cfg.expert_ffn
+    ids = torch.cat([prompts, tokens[:, :N - 1]], 1).long()
+    rms = lambda x, g: x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps) * g  # noqa: E731
+    half = hd // 2
+    freq = float(cfg.rope_theta) ** (-2.0 * torch.arange(half, dtype=torch.float64) / hd)
+    ang = torch.arange(L, dtype=torch.float64)[:, None] * freq[None, :]
+    tab = torch.stack([torch.cos(ang), torch.sin(ang)], -1).float().double()
+    pos = torch.arange(L)
+    x = w["embed"][ids]
+    gaps = []
+    for i in range(cfg.layers):
+        h = rms(x, w["attn_norm"][i])
+        qkv = h @ w["qkv"][i].T
+        q = _rope_t(qkv[..., :H * hd].reshape(S, L, H, hd), tab, pos)
+        k = _rope_t(qkv[..., H * hd:(H + KVH) * hd].reshape(S, L, KVH, hd), tab, pos)
+        v = qkv[..., (H + KVH) * hd:].reshape(S, L, KVH, hd)
+        o, _ = _attn_t(q, k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), H, KVH)
+        x = x + o.reshape(S, L, H * hd) @ w["o"][i].T
+        h2 = rms(x, w["ffn_norm"][i]).reshape(S * L, -1)
+        logits = h2 @ w["router"][i].T
+        srt = logits.detach().sort(-1, descending=True).values
+        gaps.append(float((srt[:, 1] - srt[:, 2]).min()))
+        i0 = logits.detach().argmax(-1)
+        masked = logits.detach().clone()
+        masked[torch.arange(S * L), i0] = -float("inf")
+        i1 = masked.argmax(-1)
+        pr = torch.softmax(torch.stack([logits.gather(1, i0[:, None])[:, 0],
+                                        logits.gather(1, i1[:, None])[:, 0]], 1), -1)
+        ys = []
+        for e in range(E):
+            u = h2 @ w["exp_in"][i][e].T
+            ys.append((torch.nn.functional.silu(u[:, :Fe]) * u[:, Fe:]) @ w["exp_down"][i][e].T)
+        ys = torch.stack(ys)  # [E, tokens, d]
+        t = torch.arange(S * L)
+        y = pr[:, :1] * ys[i0, t] + pr[:, 1:] * ys[i1, t]
+        x = x + y.reshape(S, L, -1)
+    hf = rms(x, w["final_norm"])[:, P - 1:P - 1 + N]
+    logits = hf @ w["lm_head"].T
+    return torch.log_softmax(logits, -1).gather(-1, tokens.long()[..., None])[..., 0], gaps
+
+
+@pytest.mark.parametrize("planes", [3])
+def test_moe_policy_gradient_matches_autograd(dev, planes):
+    """An MoE policy (4 experts, top-2): the recompute and the staged gradient
+    of every tensor (router and experts included) against float64 autograd of
+    the independent MoE restatement, where every token's routing is
+    unambiguous (second and third router logits apart by > 1e-4, checked), at
+    the plane counts' bounds (PLANE_BOUNDS); then an optimizer step."""
+    print(f"case moe policy planes={planes}", flush=True)
+    cfg = MOE_CFG
+    w = oracle.random_weights(cfg.oracle_cfg(), seed=31, std=0.05)
+    pol = train.Policy(cfg, w, dev, matmul_planes=planes)
+    prompts, tokens, rewards = _batch(cfg, 7, dev)
+    beh = torch.full(tokens.shape, -7.0, device=dev)
+    out = pol.prepare(None, prompts, tokens, beh, rewards, kl_coefficient=0.0)
+    assert int(out["flags"].abs().sum()) == 0
+    wt = {k: torch.from_numpy(np.asarray(v, dtype=np.float64)).requires_grad_(True)
+          for k, v in w.items()}
+    lp_t, gaps = _torch_lp_moe(wt, cfg, prompts.cpu(), tokens.cpu())
+    print(f"  routing gaps per layer {[f'{g:.2e}' for g in gaps]}", flush=True)
+    assert min(gaps) > 1e-4
+    lp_bound, grad_bound = PLANE_BOUNDS[planes]
+    lp_err = float((out["lp_cur"].cpu().double() - lp_t.detach()).abs().max())
+    print(f"  max |lp - f64| {lp_err:.2e}", flush=True)
+    assert lp_err < lp_bound
+    (out["dlp"].cpu().double() * lp_t).sum().backward()
+    for k, t in wt.items():
+        layers = range(cfg.layers) if k in train.LAYER_KEYS + train.MOE_LAYER_KEYS else [-1]
+        for layer in layers:
+            got = pol.tensor(k, layer, gradient=True).cpu().double()
+            want = t.grad[layer] if layer >= 0 else t.grad
+            err = (got - want).abs().max().item() / (want.abs().max().item() + 1e-12)
+            cos = float((got * want).sum() / (got.norm() * want.norm() + 1e-300))
+            print(f"  {k}[{layer}] relative gradient error {err:.2e}, cosine {cos:.6f}",
+                  flush=True)
+            assert err < grad_bound, (k, layer)
+            assert cos >= 0.9999, (k, layer)
+    before = pol.tensor("exp_in", 1).clone()
+    norm = pol.optimizer_step(1.0)
+    assert np.isfinite(norm) and norm > 0
+    assert float((pol.tensor("exp_in", 1) - before).abs().max()) > 0
 
 
 def test_native_optimizer_step_adamw_and_clip(dev):
@@ -246,8 +346,45 @@ def test_quantized_policy_recompute_equals_rollout_model(dev):
     assert float((model.logprobs(prompts, tok) - before).abs().max()) > 1e-4
 
 
+def test_quantized_moe_policy_recompute_equals_rollout_model(dev):
+    """The same for an MoE config (4 experts, top-2, Q4G128 experts, f32
+    router): the policy's recompute against the installed Q4 model's rollout
+    log-probs (the router decisions of the two agree except at near-ties of
+    the 16-bit-activation logits, so the bound is checked on 95 % of the
+    positions and every position stays within 0.5), and an update moves the
+    installed model."""
+    qc = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512,
+                     vocab=1024, max_seq=32, quantized=True, experts=4, expert_ffn=128)
+    w = oracle.random_weights(qc.oracle_cfg(), seed=17, std=0.05)
+    pol = train.Policy(qc, w, dev)
+    model = Model(qc)
+    pol.install(model)
+    prompts, _, rewards = _batch(qc, 8, dev)
+    tok, beh = model.generate(prompts, 6, temperature=1.0, seed=3)
+    out = pol.prepare(None, prompts, tok, beh, rewards, kl_coefficient=0.0)
+    diff = (out["lp_cur"] - beh).abs().flatten().cpu()
+    q95 = float(diff.quantile(0.95))
+    print(f"quantized MoE policy recompute vs Q4 rollout: max {float(diff.max()):.2e}, "
+          f"95th percentile {q95:.2e}", flush=True)
+    assert q95 <= 2e-3 and float(diff.max()) <= 0.5
+    before = model.logprobs(prompts, tok)
+    pol.optimizer_step(1.0)
+    pol.install(model)
+    assert float((model.logprobs(prompts, tok) - before).abs().max()) > 1e-4
+
+
 def test_policy_rejects_bad_config(dev):
     bad = ModelConfig(layers=1, d_model=256, heads=4, kv_heads=4, head_dim=64, ffn=512,
-                      vocab=100, max_seq=16, quantized=True, experts=4, expert_ffn=256)
-    with pytest.raises(_lib.SummaError, match="dense decoder"):
+                      vocab=100, max_seq=16, quantized=True, experts=1, expert_ffn=256)
+    with pytest.raises(_lib.SummaError, match="2..=64 experts"):
         train.Policy(bad, {}, dev)
+    bad.experts, bad.expert_ffn = 4, 200  # quantized experts need 128-wide groups
+    with pytest.raises(_lib.SummaError, match="% 128 == 0"):
+        train.Policy(bad, {}, dev)
+    dense = ModelConfig(layers=1, d_model=256, heads=4, kv_heads=4, head_dim=64, ffn=512,
+                        vocab=100, max_seq=16, quantized=False)
+    pol = train.Policy(dense, {}, dev)
+    buf = torch.empty(16, device=dev)
+    with pytest.raises(_lib.SummaError, match="not part of this policy"):
+        _lib.call("sm_policy_get_tensor", pol._h, 9, 0, buf.data_ptr(), 0,
+                  torch.cuda.current_stream().cuda_stream)
