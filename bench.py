@@ -978,9 +978,65 @@ def bench_policy_update(args) -> dict:
             "first_prepare_lp_vs_rollout_max_abs": lp_gap}
 
 
+def bench_decode_gemms(args) -> dict:
+    """config[2]'s decode projections at the decode shape (M 256 rollouts, f16-
+    pair activations, synthetic Q4G128 weights), each launched 10 times (the
+    launches the committed counter summaries of the decode GEMMs profile):
+    FFN-in (2 x 5632 columns, SwiGLU f16-pair epilogue), a 3072-column store of
+    the qkv shape, and o (2048 x 2048) and down (2048 x 5632) through the fused
+    residual + RMSNorm path (sm_q4_matmul_add_rmsnorm). Value: the FFN-in's
+    event-timed average per call."""
+    import ctypes
+
+    import torch
+
+    from summa_amd import _lib, ops
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    M = 256
+    L = _lib.lib()
+
+    def q4(n, k, seed):
+        w = torch.empty(n, k, device=dev)
+        ops.fill_normal(w, 0, 0.02, seed=seed)
+        return ops.Q4Weight.quantize(w)
+    ws = torch.zeros(64 << 20, dtype=torch.uint8, device=dev)
+    x = torch.empty(M, 2048, device=dev)
+    ops.fill_normal(x, 0, 1, seed=2)
+    xp = ops.f16_pair(x)
+    xf = torch.empty(M, 5632, device=dev)
+    ops.fill_normal(xf, 0, 1, seed=3)
+    xfp = ops.f16_pair(xf)
+    w_in, w_qkv = q4(11264, 2048, 1), q4(3072, 2048, 4)
+    w_o, w_dn = q4(2048, 2048, 5), q4(2048, 5632, 6)
+    resid = torch.zeros(M, 2048, device=dev)
+    gamma = torch.ones(2048, device=dev)
+    h = torch.empty(M, 4096, dtype=torch.float16, device=dev)
+
+    def addnorm(w, xx, K):
+        _lib.check(L.sm_q4_matmul_add_rmsnorm(
+            w.tcodes.data_ptr(), w.tscales.data_ptr(), 2048, K, xx.data_ptr(), _lib.SM_F16X2, M,
+            2 * K, resid.data_ptr(), gamma.data_ptr(), ctypes.c_float(1e-5), h.data_ptr(),
+            ws.data_ptr(), ws.numel(), ctypes.c_void_p(st.cuda_stream)))
+    calls = {
+        "ffn_in": lambda: ops.q4_matmul(w_in, xp, epilogue=_lib.SM_EPI_SWIGLU_F16X2, pair=True,
+                                        workspace=ws),
+        "qkv_shape": lambda: ops.q4_matmul(w_qkv, xp, pair=True, workspace=ws),
+        "o_add_rmsnorm": lambda: addnorm(w_o, xp, 2048),
+        "down_add_rmsnorm": lambda: addnorm(w_dn, xfp, 5632)}
+    res = {}
+    for name, fn in calls.items():
+        res[name] = round(_time_launches(fn, 10) * 1e3, 2)
+    return {"metric": "decode FFN-in us per call (config[2] decode shape, M 256)",
+            "value": res["ffn_in"], "unit": "us", "higher_is_better": False,
+            "ms_per_step": res["ffn_in"] / 1e3, "dtype": "q4g128 weights, f16-pair activations",
+            "config": {"workload": "decode_gemms config[2]", "M": M},
+            "us_per_call": res}
+
+
 WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress, "q4_gemv": bench_q4_gemv,
              "recompute_gemm": bench_recompute_gemm, "policy_update": bench_policy_update,
-             "decode_attention": bench_decode_attention}
+             "decode_attention": bench_decode_attention, "decode_gemms": bench_decode_gemms}
 
 
 def main() -> int:
