@@ -792,6 +792,7 @@ int launch_thick(const Q4Args& a, int epi, hipStream_t st, int ks) {
     SM_TK(EPI_SWIGLU_BF16)
     SM_TK(EPI_SWIGLU_F16)
     SM_TK(EPI_SWIGLU_F16X2)
+    SM_TK(EPI_ADD_F32)
 #undef SM_TK
     default: set_error("sm_q4_matmul: thick kernel for epilogue %d", epi); return SM_ERR_INVALID;
   }
@@ -803,9 +804,9 @@ int launch_thick(const Q4Args& a, int epi, hipStream_t st, int ks) {
 // (config[2]: M 256, 2 x 5632): 4 waves of 2 x 2 blocks (32 x 128 tiles).
 // Measured against the batch kernel (42.3 us) on that shape, 16-column wave
 // tiles: 33.7 us; 8 waves 34.5; 64-row tiles 40.3; 4 column blocks 38.5; the
-// 16-row form 38.8. Other decode projections measured no faster in this form
-// (qkv 15.6 -> 16-25 us, o 14.6 -> 11.7 us unsplit but the split fused-norm
-// path is faster, down 22.8 -> 30-68 us), so they keep their kernels.
+// 16-row form 38.8. The qkv projection measured no faster in this form
+// (15.6 -> 16-25 us); the residual projections take it in K splits
+// (thick_add_rmsnorm_splits).
 inline bool use_thick(int64_t M, int64_t logical_cols, int epi, int xt) {
   return is_swiglu(epi) && (xt == X_F16X2 || xt == X_F16) && M > 128 && M <= 256 &&
          logical_cols > 8192;
@@ -1273,6 +1274,26 @@ int add_rmsnorm_splits(int64_t M, int64_t N, int64_t K, int xt, int64_t ws_bytes
   return (int)ceil_div(ng, gper);  // every split non-empty
 }
 
+// The residual projections of the fused add + RMSNorm at 128 < M <= 256
+// (config[2], M 256, N 2048): the thick-wave kernel over K splits sized for
+// about 512 workgroups, 16-row wave tiles for K <= 2048 and 32-row ones past
+// it. Measured, GEMM + split reduction: o (K 2048) 13.3 + 4.5 us with the
+// grouped kernel in 4 splits -> 11.4 + 4.3 us in 2 (16-row tiles; 4 splits
+// 12.9, 32-row tiles 13.5); down (K 8192) 20.4 + 5.0 -> 19.9 + 4.6 us in 4
+// (32-row tiles; 16-row tiles 21.2, 2 and 8 splits 24.9 and 21.3). Returns
+// the split count (0: keep the grouped kernel) and the tile height in mt.
+int thick_add_rmsnorm_splits(int64_t M, int64_t N, int64_t K, int64_t ws_bytes, int& mt) {
+  if (M <= 128 || M > 256 || N < 2048) return 0;
+  mt = (K > 2048) ? 2 : 1;
+  const int ng = (int)(K / 128);
+  const int64_t base = ceil_div(N, 4 * 16 * 2) * ceil_div(M, 16 * mt);
+  int ks = (int)std::min<int64_t>(ng / 3, std::max<int64_t>(1, 512 / base));
+  while (ks > 1 && (int64_t)ks * M * N * 4 > ws_bytes) --ks;
+  if (ks < 2) return 0;
+  const int gper = (int)ceil_div(ng, ks);
+  return (int)ceil_div(ng, gper);
+}
+
 // ----------------------------------------------------------- quantizer ---
 // One wave per 128-element group; lane l owns elements 2l, 2l+1 (one byte).
 __device__ inline float round_half_away(float v) {
@@ -1440,7 +1461,7 @@ int matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N, 
                        int64_t workspace_bytes, const float* wr, int64_t E, float* logits,
                        int32_t* top_idx, float* top_w, void* stream) {
   const int xt = xmode_of(x_dtype);
-  const int ks = (xt >= 0 && workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
+  int ks = (xt >= 0 && workspace && reinterpret_cast<uintptr_t>(workspace) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(resid) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(gamma) % 16 == 0 &&
                   reinterpret_cast<uintptr_t>(h_out) % 8 == 0 &&
@@ -1461,11 +1482,23 @@ int matmul_add_rmsnorm(const uint8_t* codes, const uint16_t* scales, int64_t N, 
              "sm_q4_matmul_add_rmsnorm: bad matmul operands");
   Q4Args a{codes, scales, x, resid, (int)M, (int)N, (int)K, (int)ldx, (int)N, (int)N};
   const int ng = (int)(K / 128);
-  a.gper = (int)ceil_div(ng, ks);
   a.part = static_cast<float*>(workspace);
-  const int64_t rt = ceil_div(M, 16);
-  if (xt == X_F16X2) SM_TRY(launch_grouped_lds<X_F16X2>(a, EPI_ADD_F32, st, rt, ks, false));
-  else SM_TRY(launch_grouped_lds<X_F16>(a, EPI_ADD_F32, st, rt, ks, false));
+  int mt = 0;
+  if (const int tks = thick_add_rmsnorm_splits(M, N, K, workspace_bytes, mt)) {
+    ks = tks;
+    a.gper = (int)ceil_div(ng, ks);
+    if (xt == X_F16X2)
+      SM_TRY((mt == 1 ? launch_thick<4, 1, 2, X_F16X2>(a, EPI_ADD_F32, st, ks)
+                      : launch_thick<4, 2, 2, X_F16X2>(a, EPI_ADD_F32, st, ks)));
+    else
+      SM_TRY((mt == 1 ? launch_thick<4, 1, 2, X_F16>(a, EPI_ADD_F32, st, ks)
+                      : launch_thick<4, 2, 2, X_F16>(a, EPI_ADD_F32, st, ks)));
+  } else {
+    a.gper = (int)ceil_div(ng, ks);
+    const int64_t rt = ceil_div(M, 16);
+    if (xt == X_F16X2) SM_TRY(launch_grouped_lds<X_F16X2>(a, EPI_ADD_F32, st, rt, ks, false));
+    else SM_TRY(launch_grouped_lds<X_F16>(a, EPI_ADD_F32, st, rt, ks, false));
+  }
   const unsigned blocks = (unsigned)M;
   _Float16* h = static_cast<_Float16*>(h_out);
 #define SM_ARK(V, KS)                                                                       \
