@@ -75,7 +75,10 @@ int sm_moe_combine_backward(const void*, const void*, int, const float*, const i
 namespace sm {
 int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                    float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
-                   float beta, float* C, int64_t ldc, void* stream);  // train.hip
+                   float beta, float* C, int64_t ldc, void* stream, float* scratch = nullptr,
+                   int64_t scratch_floats = 0);  // train.hip
+int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N,
+                                   int64_t K);  // gemm_mfma.hip
 int64_t rmsnorm_dgamma_chunks(int64_t rows);                          // train.hip
 int rmsnorm_backward_parts(const float* x, const float* gamma, const float* dy, int64_t rows,
                            int64_t d, float eps, int accumulate, float* dx, float* dgamma,
@@ -500,14 +503,19 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   SM_REQUIRE(L <= c.max_seq, "sequence length %lld exceeds max_seq_len %d", (long long)L,
              c.max_seq);
   hipStream_t st = as_stream(stream);
-  // the prepare's GEMMs on the policy's plane count
+  const int64_t d = c.d_model, H = c.heads, KVH = c.kv_heads, hd = c.head_dim, F = c.ffn;
+  const int64_t V = c.vocab, qn = p->qn, qdim = p->qdim;
+  // the prepare's GEMMs on the policy's plane count, with room for their
+  // transposed operands (tps: the largest need of the backward's (1, 0) and
+  // (0, 0) products below)
+  float* tps = nullptr;
+  int64_t tps_floats = 0;
   auto pgemm = [&](int ta, int tb, int64_t m, int64_t n, int64_t k, float alpha, const float* A,
                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
                    void* sp) {
-    return gemm_ex_planes(p->planes, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, sp);
+    return gemm_ex_planes(p->planes, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, sp,
+                          tps, tps_floats);
   };
-  const int64_t d = c.d_model, H = c.heads, KVH = c.kv_heads, hd = c.head_dim, F = c.ffn;
-  const int64_t V = c.vocab, qn = p->qn, qdim = p->qdim;
   if (c.quantized) SM_TRY(fake_quantize(p, st));
   // ---- activation arena: per layer x0, h, qkv, q, k, v, o, lse, x1, h2 and the
   // FFN's u, a (dense) or its routing and routed rows (MoE: top-2 indices and
@@ -520,6 +528,18 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   const int64_t ffn_fixed = moe ? RT * d /*dyr*/ + 2 * M /*gw*/ + RT * Fe /*dar*/ +
                                       RT * 2 * Fe /*dur*/ + RT * d /*drt*/ + M * E /*dlog*/ + 1
                                 : M * 2 * F /*du*/ + M * F /*da*/;
+  // transposed operands of the backward's weight (1, 0) and data (0, 0) GEMMs
+  auto tneed = [](bool ta, bool tb, int64_t m, int64_t n, int64_t k) {
+    return gemm_planes_scratch_floats(ta, tb, m, n, k);
+  };
+  int64_t tp_need = std::max(tneed(true, false, V, d, R), tneed(false, false, R, d, V));
+  const int64_t lin[4][2] = {{qn, d}, {d, qdim}, {2 * F, d}, {d, F}};  // {out, in}
+  for (int i = 0; i < (moe ? 2 : 4); ++i)
+    tp_need = std::max({tp_need, tneed(true, false, lin[i][0], lin[i][1], M),
+                        tneed(false, false, M, lin[i][1], lin[i][0])});
+  if (moe)
+    tp_need = std::max({tp_need, tneed(true, false, d, Fe, RT), tneed(false, false, RT, Fe, d),
+                        tneed(true, false, 2 * Fe, d, RT), tneed(false, false, RT, d, 2 * Fe)});
   const int64_t per_layer =
       M * (d + d + qn + qdim + 2 * p->kvdim + qdim + H + d + d) + ffn_layer;
   const int64_t fixed = M * d /*x*/ + M * d /*hf*/ + R * d /*hr*/ + R * V /*logits*/ +
@@ -527,7 +547,7 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
                         M * d /*dh*/ + M * qdim /*do*/ + M * qdim /*dq*/ +
                         2 * S * KVH * L * hd /*dk dv*/ + M * qn /*dqkv*/ + M /*rinv*/ +
                         S * H * L /*delta*/ + R /*row scale*/ + d /*dgamma final*/ + S /*pos0*/ +
-                        rmsnorm_dgamma_chunks(M) * d /*dgamma parts*/;
+                        rmsnorm_dgamma_chunks(M) * d /*dgamma parts*/ + tp_need;
   const size_t bytes = (size_t)(per_layer * c.layers + fixed) * 4 + (size_t)M * 4 /*ids*/ +
                        (size_t)R * 8 /*rows*/ + (size_t)(20 * c.layers + 48) * 256;
   SM_TRY(grow(p->act, bytes));
@@ -586,6 +606,8 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   float* rscale = (float*)take(R);
   float* dgf = (float*)take(d);
   float* dgparts = (float*)take(rmsnorm_dgamma_chunks(M) * d);
+  tps = (float*)take(tp_need);
+  tps_floats = tp_need;
   int32_t* pos0 = (int32_t*)take(S);
   int32_t* ids = (int32_t*)take(M);
   int64_t* rows = (int64_t*)take(R, 8);

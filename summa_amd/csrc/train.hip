@@ -533,14 +533,18 @@ inline unsigned g256(int64_t n) { return (unsigned)ceil_div(n, 256); }
 
 int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
                 const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
-                int64_t ldc, hipStream_t st);  // gemm_mfma.hip
+                int64_t ldc, hipStream_t st, float* scratch = nullptr,
+                int64_t scratch_floats = 0);  // gemm_mfma.hip
+int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64_t K);
 
 // sm_gemm_ex with the matrix-core launches on `planes` bf16 planes per operand
 // (3: f32-grade; 2: 16-bit operands; 1: bf16 operands); the small problems
-// stay on the f32 FMA kernel.
+// stay on the f32 FMA kernel. scratch (optional, 16-byte aligned): room for
+// the matrix-core launch's transposed operands (gemm_planes_scratch_floats).
 int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                    float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
-                   float beta, float* C, int64_t ldc, void* stream) {
+                   float beta, float* C, int64_t ldc, void* stream, float* scratch,
+                   int64_t scratch_floats) {
   SM_REQUIRE(A && B && C, "sm_gemm_ex: null buffer");
   SM_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1 << 30) && N < (1 << 30) && K < (1 << 30),
              "sm_gemm_ex: bad shape");
@@ -553,7 +557,7 @@ int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, i
   // small ones, where a launch has few 128 x 128 tiles, here
   if (K >= 32 && M * N >= (int64_t)128 * 128 * 16 && M * N * K >= ((int64_t)1 << 27))
     return gemm_planes(planes, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta,
-                       C, ldc, st);
+                       C, ldc, st, scratch, scratch_floats);
   const dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
 #define SM_GX(TA, TB)                                                                        \
   gemm_ex_kernel<TA, TB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, \
@@ -573,7 +577,8 @@ using namespace sm;
 extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K, float alpha,
                           const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                           float* C, int64_t ldc, void* stream) {
-  return gemm_ex_planes(3, trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream);
+  return gemm_ex_planes(3, trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream,
+                        nullptr, 0);
 }
 
 extern "C" int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy,

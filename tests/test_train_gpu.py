@@ -121,6 +121,34 @@ def test_gemm_planes_reduced(dev, planes, ta, tb, M, N, K, pad):
     assert dist > 3 * err  # the kernel follows the plane model, not the exact product
 
 
+@pytest.mark.parametrize("planes", [1, 3])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", [(300, 260, 333), (513, 130, 1030)])
+def test_gemm_planes_scratch_is_bit_exact(dev, planes, ta, tb, M, N, K):
+    """sm_gemm_planes_ws (operands whose k is not contiguous transposed into
+    the scratch first, rows padded to 4 floats) equals sm_gemm_planes (the
+    kernel's own transposed loads) bit for bit, with alpha and beta; a
+    scratch one float short runs the plain path (still equal)."""
+    print(f"case gemm_planes_ws planes={planes} ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(M + N + K + 4 * ta + 2 * tb)
+    a = torch.randn((K, M) if ta else (M, K), generator=g, device=dev)
+    b = torch.randn((N, K) if tb else (K, N), generator=g, device=dev)
+    c0 = torch.randn(M, N, generator=g, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    need = int(_lib.lib().sm_gemm_planes_scratch_bytes(ta, tb, M, N, K))
+    kp = (K + 3) // 4 * 4
+    assert need == 4 * ((M * kp if ta else 0) + (0 if tb else N * kp))
+    ref = c0.clone()
+    call("sm_gemm_planes", planes, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0), b.data_ptr(),
+         b.stride(0), 0.5, ref.data_ptr(), N, st)
+    for nbytes in (need, max(need - 4, 0)):
+        scratch = torch.full((max(need, 16) // 4,), float("nan"), device=dev)
+        out = c0.clone()
+        call("sm_gemm_planes_ws", planes, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0),
+             b.data_ptr(), b.stride(0), 0.5, out.data_ptr(), N, scratch.data_ptr(), nbytes, st)
+        assert torch.equal(out, ref), (nbytes, float((out - ref).abs().max()))
+
+
 def test_gemm_planes_rejects_bad_count(dev):
     x = torch.zeros(4, 4, device=dev)
     for planes in (0, 4):
