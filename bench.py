@@ -1034,9 +1034,69 @@ def bench_decode_gemms(args) -> dict:
             "us_per_call": res}
 
 
+def bench_policy_gemms(args) -> dict:
+    """The policy update's largest GEMM shapes at config[2] (one GRPO group:
+    8 x 1023 positions, d 2048, F 5632, V 65536; the last group's 4096 scored
+    rows for the LM head) through sm_gemm_planes_ws as the prepare runs them
+    (operands whose k is not contiguous transposed into the scratch first,
+    transposes inside the timing), for 3, 2 and 1 bf16 planes. Per shape: the
+    event-timed average of 5 calls, algorithmic f32 TF/s (2 M N K) and the
+    fraction of the 2.5 PF/s bf16 MFMA peak in issued plane products (6, 3 or
+    1 per f32 product). Value: the smallest three-plane fraction among the
+    backward (weight and data gradient) shapes."""
+    import ctypes
+
+    import torch
+
+    from summa_amd import _lib
+    dev = torch.device("cuda:0")
+    st = torch.cuda.current_stream()
+    L = _lib.lib()
+    M, d, F, V, R = 8 * 1023, 2048, 5632, 65536, 4096
+    shapes = {  # name: (trans_a, trans_b, M, N, K)
+        "fwd_ffn_in": (0, 1, M, 2 * F, d), "dW_ffn_in": (1, 0, 2 * F, d, M),
+        "dX_ffn_in": (0, 0, M, d, 2 * F), "fwd_down": (0, 1, M, d, F),
+        "dW_down": (1, 0, d, F, M), "dX_down": (0, 0, M, F, d),
+        "dW_o": (1, 0, d, d, M), "dX_o": (0, 0, M, d, d),
+        "fwd_lm_head": (0, 1, R, V, d), "dW_lm_head": (1, 0, V, d, R),
+        "dX_lm_head": (0, 0, R, d, V)}
+    need = max(int(L.sm_gemm_planes_scratch_bytes(ta, tb, m, n, k))
+               for ta, tb, m, n, k in shapes.values())
+    scratch = torch.empty(max(need, 16) // 4, device=dev)
+    products = {3: 6, 2: 3, 1: 1}
+    res = {}
+    for planes in (3, 2, 1):
+        res[str(planes)] = {}
+        for name, (ta, tb, m, n, k) in shapes.items():
+            a = torch.randn((k, m) if ta else (m, k), device=dev)
+            b = torch.randn((n, k) if tb else (k, n), device=dev)
+            c = torch.empty(m, n, device=dev)
+
+            def call():
+                _lib.check(L.sm_gemm_planes_ws(
+                    planes, ta, tb, m, n, k, ctypes.c_float(1.0), a.data_ptr(), a.stride(0),
+                    b.data_ptr(), b.stride(0), ctypes.c_float(0.0), c.data_ptr(), n,
+                    scratch.data_ptr(), scratch.numel() * 4, ctypes.c_void_p(st.cuda_stream)))
+            sec = _time_launches(call, 5) / 1e3
+            tf = 2.0 * m * n * k / sec / 1e12
+            res[str(planes)][name] = {"us": round(sec * 1e6, 1), "f32_TFs": round(tf, 1),
+                                      "mfma_frac": round(tf * products[planes] / 2500.0, 3)}
+            log(f"bench: policy GEMM planes={planes} {name}: {sec * 1e6:.1f} us, "
+                f"{tf:.1f} TF/s, MFMA {tf * products[planes] / 2500.0:.3f}")
+            del a, b, c
+    worst = min(v["mfma_frac"] for k_, v in res["3"].items() if not k_.startswith("fwd"))
+    return {"metric": "policy-update backward GEMM MFMA fraction (config[2] shapes, 3 planes, min)",
+            "value": worst, "unit": "fraction of 2.5 PF/s", "higher_is_better": True,
+            "ms_per_step": sum(v["us"] for v in res["3"].values()) / 1e3,
+            "dtype": "f32 via bf16 planes",
+            "config": {"workload": "policy_gemms config[2]", "positions": M},
+            "by_planes": res}
+
+
 WORKLOADS = {"rl_step": bench_rl_step, "ce_stress": bench_ce_stress, "q4_gemv": bench_q4_gemv,
              "recompute_gemm": bench_recompute_gemm, "policy_update": bench_policy_update,
-             "decode_attention": bench_decode_attention, "decode_gemms": bench_decode_gemms}
+             "decode_attention": bench_decode_attention, "decode_gemms": bench_decode_gemms,
+             "policy_gemms": bench_policy_gemms}
 
 
 def main() -> int:
