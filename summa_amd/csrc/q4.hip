@@ -859,12 +859,15 @@ int launch_grouped_lds_nb(const Q4Args& a, int epi, hipStream_t st, int64_t row_
 // projection's 2048 columns enough workgroups). Dense non-SwiGLU launches of
 // at most 128 rows take 128 columns (one 16-column block per wave; the same
 // bits): config[1] rollout 213.4 -> 206.8 ms, config[4] 844 -> 837 ms, while
-// config[2]'s 256-row decode is 0.8 % slower that way and keeps 256.
+// config[2]'s 256-row decode is 0.8 % slower that way and keeps 256. The
+// qkv projection with its RoPE epilogue keeps 256 columns from K 2048 on
+// (config[4]: 17.3 -> 16.1 us per call; at config[1]'s K 768 the narrow
+// tile stays faster, 9.3 against 11.6 us).
 template <int XT>
 int launch_grouped_lds(const Q4Args& a, int epi, hipStream_t st, int64_t row_tiles, int ks = 1,
                        bool reduce = true) {
 
-  if (!a.tiles && !is_swiglu(epi) && a.M <= 128)
+  if (!a.tiles && !is_swiglu(epi) && a.M <= 128 && !(epi == 6 && a.K >= 2048))
     return launch_grouped_lds_nb<XT, 1>(a, epi, st, row_tiles, ks, reduce);
   return launch_grouped_lds_nb<XT, 2>(a, epi, st, row_tiles, ks, reduce);
 }
