@@ -75,14 +75,26 @@ __global__ __launch_bounds__(256, PRE ? 4 : 1) void attn_decode_kernel(
   __shared__ float pbuf[4][QM][TK];
   __shared__ float mrg_m[4][QM], mrg_l[4][QM];
   __shared__ float mrg_o[4][QM][HD];
-  // PRE: the prefix partials of this (sequence, KV head), staged at the start
-  // so their loads overlap the key loop: [head][split][HD] O, [head][split][2]
-  __shared__ float pre_os[PRE ? QM * kMaxPrefixSplits * HD : 1];
+  // PRE: the prefix partials of this (sequence, KV head), [head][split][HD] O
+  // and [head][split][2] (max, sum), staged in LDS for the final merge. Every
+  // load is issued up front (16 bytes per thread per 1024 floats of O) next
+  // to the query loads, and stored after them, so the start of the kernel
+  // waits for one memory round trip instead of one per staging pass.
+  __shared__ __attribute__((aligned(16))) float pre_os[PRE ? QM * kMaxPrefixSplits * HD : 1];
   __shared__ float pre_mls[PRE ? QM * kMaxPrefixSplits * 2 : 1];
+  constexpr int PV = PRE ? (QM * kMaxPrefixSplits * HD + 1023) / 1024 : 1;  // f4 per thread
+  f4 pv[PV];
+  float pml = 0.f;
+  const int n_o = qpk * nsplit * HD, n_ml = qpk * nsplit * 2;  // n_o % 4 == 0
   if constexpr (PRE) {
     const size_t first = ((size_t)s * H + kvh * qpk) * nsplit;  // this WG's first slot
-    for (int e = threadIdx.x; e < qpk * nsplit * HD; e += 256) pre_os[e] = pre_o[first * HD + e];
-    for (int e = threadIdx.x; e < qpk * nsplit * 2; e += 256) pre_mls[e] = pre_ml[first * 2 + e];
+    const f4* src = reinterpret_cast<const f4*>(pre_o + first * HD);
+#pragma unroll
+    for (int i = 0; i < PV; ++i) {
+      const int e4 = (int)threadIdx.x + i * 256;
+      if (4 * e4 < n_o) pv[i] = src[e4];
+    }
+    if ((int)threadIdx.x < n_ml) pml = pre_ml[first * 2 + threadIdx.x];
   }
 
   // A operand: query head (kvh*qpk + j) if j < qpk.
@@ -95,6 +107,14 @@ __global__ __launch_bounds__(256, PRE ? 4 : 1) void attn_decode_kernel(
     } else {
       qa[st] = op8{};
     }
+  }
+  if constexpr (PRE) {
+#pragma unroll
+    for (int i = 0; i < PV; ++i) {
+      const int e4 = (int)threadIdx.x + i * 256;
+      if (4 * e4 < n_o) reinterpret_cast<f4*>(pre_os)[e4] = pv[i];
+    }
+    if ((int)threadIdx.x < n_ml) pre_mls[threadIdx.x] = pml;
   }
 
   float m_i[QM], l_i[QM], o[QM][DPL];
