@@ -1039,10 +1039,13 @@ def bench_policy_gemms(args) -> dict:
     8 x 1023 positions, d 2048, F 5632, V 65536; the last group's 4096 scored
     rows for the LM head) through sm_gemm_planes_ws as the prepare runs them
     (operands whose k is not contiguous transposed into the scratch first,
-    transposes inside the timing), for 3, 2 and 1 bf16 planes. Per shape: the
+    transposes inside the timing; the forward and data-gradient shapes with a
+    fake-quantized B, exact in two bf16 planes, as in the quantized prepare),
+    for 3, 2 and 1 bf16 planes. Per shape: the
     event-timed average of 5 calls, algorithmic f32 TF/s (2 M N K) and the
     fraction of the 2.5 PF/s bf16 MFMA peak in issued plane products (6, 3 or
-    1 per f32 product). Value: the smallest three-plane fraction among the
+    1 per f32 product; 5 at three planes with a two-plane B). Value: the
+    smallest three-plane fraction among the
     backward (weight and data gradient) shapes."""
     import ctypes
 
@@ -1063,7 +1066,7 @@ def bench_policy_gemms(args) -> dict:
     need = max(int(L.sm_gemm_planes_scratch_bytes(ta, tb, m, n, k))
                for ta, tb, m, n, k in shapes.values())
     scratch = torch.empty(max(need, 16) // 4, device=dev)
-    products = {3: 6, 2: 3, 1: 1}
+    products = {3: 6, 2: 3, 1: 1}  # per f32 product (three planes with a two-plane B: 5)
     res = {}
     for planes in (3, 2, 1):
         res[str(planes)] = {}
@@ -1072,17 +1075,24 @@ def bench_policy_gemms(args) -> dict:
             b = torch.randn((n, k) if tb else (k, n), device=dev)
             c = torch.empty(m, n, device=dev)
 
+            # forward and data gradients multiply by the fake-quantized weight
+            # (B; exact in two bf16 planes), as the quantized policy's prepare does
+            bp = 0 if name.startswith("dW") else 2
+            if bp == 2:
+                b = (torch.randint(-7, 8, b.shape, device=dev).float() * (1.0 / 128)).contiguous()
+
             def call():
                 _lib.check(L.sm_gemm_planes_ws(
-                    planes, ta, tb, m, n, k, ctypes.c_float(1.0), a.data_ptr(), a.stride(0),
+                    planes, bp, ta, tb, m, n, k, ctypes.c_float(1.0), a.data_ptr(), a.stride(0),
                     b.data_ptr(), b.stride(0), ctypes.c_float(0.0), c.data_ptr(), n,
                     scratch.data_ptr(), scratch.numel() * 4, ctypes.c_void_p(st.cuda_stream)))
             sec = _time_launches(call, 5) / 1e3
             tf = 2.0 * m * n * k / sec / 1e12
+            npr = 5 if (planes == 3 and bp == 2) else products[planes]
             res[str(planes)][name] = {"us": round(sec * 1e6, 1), "f32_TFs": round(tf, 1),
-                                      "mfma_frac": round(tf * products[planes] / 2500.0, 3)}
+                                      "mfma_frac": round(tf * npr / 2500.0, 3)}
             log(f"bench: policy GEMM planes={planes} {name}: {sec * 1e6:.1f} us, "
-                f"{tf:.1f} TF/s, MFMA {tf * products[planes] / 2500.0:.3f}")
+                f"{tf:.1f} TF/s, MFMA {tf * npr / 2500.0:.3f}")
             del a, b, c
     worst = min(v["mfma_frac"] for k_, v in res["3"].items() if not k_.startswith("fwd"))
     return {"metric": "policy-update backward GEMM MFMA fraction (config[2] shapes, 3 planes, min)",

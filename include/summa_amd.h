@@ -565,12 +565,16 @@ int sm_gemm_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, i
  * whose k is not contiguous (op(A) of a transposed A, op(B) of an
  * untransposed B) is transposed into it first, so that both operands stream
  * along k; the result is sm_gemm_planes' bit for bit. A smaller scratch runs
- * sm_gemm_planes as is. (The policy update's backward GEMMs run this way.) */
+ * sm_gemm_planes as is. b_planes 2 (with planes 3) declares every B value
+ * exact in two bf16 planes (value - bf16(value) is itself a bf16, as for a
+ * bf16 scale times a 4-bit code): the zero third plane of B is then not
+ * multiplied (five plane products instead of six, the same bits); 0 or 3:
+ * no such claim. (The policy update's GEMMs run this way.) */
 int64_t sm_gemm_planes_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N, int64_t K);
-int sm_gemm_planes_ws(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
-                      float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
-                      float beta, float* C, int64_t ldc, void* scratch, int64_t scratch_bytes,
-                      void* stream);
+int sm_gemm_planes_ws(int planes, int b_planes, int trans_a, int trans_b, int64_t M, int64_t N,
+                      int64_t K, float alpha, const float* A, int64_t lda, const float* B,
+                      int64_t ldb, float beta, float* C, int64_t ldc, void* scratch,
+                      int64_t scratch_bytes, void* stream);
 int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy, int64_t rows,
                         int64_t d, float eps, int accumulate, float* dx, float* dgamma,
                         float* rinv_scratch, void* stream);

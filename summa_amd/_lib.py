@@ -94,8 +94,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_gemm_planes": (i32, [i32, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64,
                              vp]),
     "sm_gemm_planes_scratch_bytes": (i64, [i32, i32, i64, i64, i64]),
-    "sm_gemm_planes_ws": (i32, [i32, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp, i64,
-                                vp, i64, vp]),
+    "sm_gemm_planes_ws": (i32, [i32, i32, i32, i32, i64, i64, i64, f32, vp, i64, vp, i64, f32, vp,
+                                i64, vp, i64, vp]),
     "sm_rmsnorm_backward": (i32, [vp, vp, vp, i64, i64, f32, i32, vp, vp, vp, vp]),
     "sm_rope_qk": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp]),
     "sm_attn_backward_f32": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, vp,

@@ -121,28 +121,37 @@ struct TileLoader {
   }
 };
 
-// plane pairs (pa, pb) of each product, smallest weight first
-template <int P> struct Products;
-template <> struct Products<3> {
+// plane pairs (pa, pb) of each product, smallest weight first. PB = 2 with
+// P = 3: B's values are exact in two planes (b2 = 0; a fake-quantized weight,
+// a bf16 scale times a 4-bit code, has at most 11 significant bits, so its
+// residual after the first plane has at most 3 and fits the second), so the
+// a0 b2 product, exactly zero, is not formed; the other five keep their order
+// and the result its bits.
+template <int P, int PB = P> struct Products;
+template <> struct Products<3, 3> {
   static constexpr int n = 6;
   static constexpr int a[6] = {2, 1, 0, 1, 0, 0}, b[6] = {0, 1, 2, 0, 1, 0};
 };
-template <> struct Products<2> {
+template <> struct Products<3, 2> {
+  static constexpr int n = 5;
+  static constexpr int a[5] = {2, 1, 1, 0, 0}, b[5] = {0, 1, 0, 1, 0};
+};
+template <> struct Products<2, 2> {
   static constexpr int n = 3;
   static constexpr int a[3] = {1, 0, 0}, b[3] = {0, 1, 0};
 };
-template <> struct Products<1> {
+template <> struct Products<1, 1> {
   static constexpr int n = 1;
   static constexpr int a[1] = {0}, b[1] = {0};
 };
 
-template <bool TA, bool TB, int P>
+template <bool TA, bool TB, int P, int PB = P>
 __global__ __launch_bounds__(256, 2) void gemm_planes_kernel(
     const float* __restrict__ A, int64_t lda, const float* __restrict__ B, int64_t ldb,
     float* __restrict__ C, int64_t ldc, int M, int N, int K, float alpha, float beta, int vec_a,
     int vec_b) {
   __shared__ __attribute__((aligned(16))) __bf16 As[P * kPlane];
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[P * kPlane];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[PB * kPlane];
   const int t = threadIdx.x, wave = t / kWave, lane = t % kWave;
   const int wm = wave / 2, wn = wave % 2;
   const int m0 = (int)blockIdx.y * kBM, n0 = (int)blockIdx.x * kBM;
@@ -156,7 +165,7 @@ __global__ __launch_bounds__(256, 2) void gemm_planes_kernel(
   la.load(0, va);
   lb.load(0, vb);
   la.template store<P>(va, As);
-  lb.template store<P>(vb, Bs);
+  lb.template store<PB>(vb, Bs);
   __syncthreads();
 
   f32x16 acc[2][2];
@@ -176,29 +185,32 @@ __global__ __launch_bounds__(256, 2) void gemm_planes_kernel(
     }
 #pragma unroll
     for (int ks = 0; ks < kBK; ks += 16) {
-      bf16x8 a[P][2], b[P][2];
+      bf16x8 a[P][2], b[PB][2];
 #pragma unroll
       for (int p = 0; p < P; ++p)
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 2; ++i)
           a[p][i] = *reinterpret_cast<const bf16x8*>(As + p * kPlane + (wm * 64 + i * 32) * kRS +
                                                      fo + ks);
+#pragma unroll
+      for (int p = 0; p < PB; ++p)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
           b[p][i] = *reinterpret_cast<const bf16x8*>(Bs + p * kPlane + (wn * 64 + i * 32) * kRS +
                                                      fo + ks);
-        }
 #pragma unroll
-      for (int q = 0; q < Products<P>::n; ++q)
+      for (int q = 0; q < Products<P, PB>::n; ++q)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
 #pragma unroll
           for (int j = 0; j < 2; ++j)
             acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-                a[Products<P>::a[q]][i], b[Products<P>::b[q]][j], acc[i][j], 0, 0, 0);
+                a[Products<P, PB>::a[q]][i], b[Products<P, PB>::b[q]][j], acc[i][j], 0, 0, 0);
     }
     if (more) {
       __syncthreads();  // every wave is done with this step's tiles
       la.template store<P>(va, As);
-      lb.template store<P>(vb, Bs);
+      lb.template store<PB>(vb, Bs);
       __syncthreads();
     }
   }
@@ -248,12 +260,12 @@ void transpose_f32(const float* in, int64_t ld, int64_t R, int64_t C, float* out
   transpose_f32_kernel<<<grid, 256, 0, st>>>(in, ld, (int)R, (int)C, out, ldo);
 }
 
-template <int P>
+template <int P, int PB = P>
 void launch_planes(bool ta, bool tb, dim3 grid, hipStream_t st, const float* A, int64_t lda,
                    const float* B, int64_t ldb, float* C, int64_t ldc, int M, int N, int K,
                    float alpha, float beta, int vec_a, int vec_b) {
 #define SM_GB(TA, TB)                                                                      \
-  gemm_planes_kernel<TA, TB, P><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K,    \
+  gemm_planes_kernel<TA, TB, P, PB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, M, N, K,\
                                                        alpha, beta, vec_a, vec_b)
   if (ta && tb) SM_GB(true, true);
   else if (ta) SM_GB(true, false);
@@ -271,7 +283,8 @@ int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64
 
 int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
                 const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
-                int64_t ldc, hipStream_t st, float* scratch, int64_t scratch_floats) {
+                int64_t ldc, hipStream_t st, float* scratch, int64_t scratch_floats,
+                int b_planes) {
   // With a scratch, an operand whose k is not its contiguous dimension (op(A)
   // of a transposed A, op(B) of an untransposed B) is first transposed into
   // it, rows padded to a multiple of 4 floats, so that the GEMM runs with
@@ -314,6 +327,9 @@ int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, f
   else if (planes == 2)
     launch_planes<2>(ta, tb, grid, st, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, alpha,
                      beta, vec_a, vec_b);
+  else if (b_planes == 2)  // B exact in two planes: five products (Products<3, 2>)
+    launch_planes<3, 2>(ta, tb, grid, st, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, alpha,
+                        beta, vec_a, vec_b);
   else
     launch_planes<3>(ta, tb, grid, st, A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, alpha,
                      beta, vec_a, vec_b);
@@ -347,7 +363,7 @@ extern "C" int sm_gemm_mfma(int trans_a, int trans_b, int64_t M, int64_t N, int6
   SM_TRY(check_gemm("sm_gemm_mfma", M, N, K, A, lda, B, ldb, C, ldc, trans_a, trans_b));
   if (M == 0 || N == 0) return SM_OK;
   return gemm_planes(3, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc,
-                     as_stream(stream), nullptr, 0);
+                     as_stream(stream), nullptr, 0, 3);
 }
 
 extern "C" int sm_gemm_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N,
@@ -359,7 +375,7 @@ extern "C" int sm_gemm_planes(int planes, int trans_a, int trans_b, int64_t M, i
   SM_TRY(check_gemm("sm_gemm_planes", M, N, K, A, lda, B, ldb, C, ldc, trans_a, trans_b));
   if (M == 0 || N == 0) return SM_OK;
   return gemm_planes(planes, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C,
-                     ldc, as_stream(stream), nullptr, 0);
+                     ldc, as_stream(stream), nullptr, 0, 3);
 }
 
 extern "C" int64_t sm_gemm_planes_scratch_bytes(int trans_a, int trans_b, int64_t M, int64_t N,
@@ -368,18 +384,21 @@ extern "C" int64_t sm_gemm_planes_scratch_bytes(int trans_a, int trans_b, int64_
   return 4 * sm::gemm_planes_scratch_floats(trans_a != 0, trans_b != 0, M, N, K);
 }
 
-extern "C" int sm_gemm_planes_ws(int planes, int trans_a, int trans_b, int64_t M, int64_t N,
-                                 int64_t K, float alpha, const float* A, int64_t lda,
+extern "C" int sm_gemm_planes_ws(int planes, int b_planes, int trans_a, int trans_b, int64_t M,
+                                 int64_t N, int64_t K, float alpha, const float* A, int64_t lda,
                                  const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
                                  void* scratch, int64_t scratch_bytes, void* stream) {
   using namespace sm;
   SM_REQUIRE(planes >= 1 && planes <= 3, "sm_gemm_planes: planes must be 1, 2 or 3 (got %d)",
              planes);
+  SM_REQUIRE(b_planes == 0 || b_planes == 2 || b_planes == 3,
+             "sm_gemm_planes_ws: b_planes must be 0, 2 or 3 (got %d)", b_planes);
   SM_TRY(check_gemm("sm_gemm_planes", M, N, K, A, lda, B, ldb, C, ldc, trans_a, trans_b));
   SM_REQUIRE(scratch_bytes >= 0 && (scratch || scratch_bytes == 0) &&
                  reinterpret_cast<uintptr_t>(scratch) % 16 == 0,
              "sm_gemm_planes_ws: bad scratch");
   if (M == 0 || N == 0) return SM_OK;
   return gemm_planes(planes, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta, C,
-                     ldc, as_stream(stream), static_cast<float*>(scratch), scratch_bytes / 4);
+                     ldc, as_stream(stream), static_cast<float*>(scratch), scratch_bytes / 4,
+                     b_planes == 2 ? 2 : 3);
 }

@@ -76,7 +76,7 @@ namespace sm {
 int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                    float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
                    float beta, float* C, int64_t ldc, void* stream, float* scratch = nullptr,
-                   int64_t scratch_floats = 0);  // train.hip
+                   int64_t scratch_floats = 0, int b_planes = 3);  // train.hip
 int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N,
                                    int64_t K);  // gemm_mfma.hip
 int64_t rmsnorm_dgamma_chunks(int64_t rows);                          // train.hip
@@ -562,7 +562,17 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
                    int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
                    void* sp) {
     return gemm_ex_planes(p->planes, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, sp,
-                          tps, tps_floats);
+                          tps, tps_floats, 3);
+  };
+  // the same with B a weight the forward uses: a quantized policy's are its
+  // fake-quantized copies (a bf16 scale times a 4-bit code), exact in two bf16
+  // planes, so three-plane products skip B's zero third plane (same bits)
+  const int wb_planes = c.quantized ? 2 : 3;
+  auto wgemm = [&](int ta, int tb, int64_t m, int64_t n, int64_t k, float alpha, const float* A,
+                   int64_t lda, const float* B, int64_t ldb, float beta, float* C, int64_t ldc,
+                   void* sp) {
+    return gemm_ex_planes(p->planes, ta, tb, m, n, k, alpha, A, lda, B, ldb, beta, C, ldc, sp,
+                          tps, tps_floats, wb_planes);
   };
   if (c.quantized) SM_TRY(fake_quantize(p, st));
   // ---- activation arena: per layer x0, h, qkv, q, k, v, o, lse, x1, h2 and the
@@ -668,14 +678,14 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
     Saved& s = sv[l];
     SM_HIP(hipMemcpyAsync(s.x0, x, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
     SM_TRY(sm_rmsnorm(s.x0, fwl(p, SM_W_ATTN_NORM, l), M, d, c.norm_eps, s.h, SM_F32, stream));
-    SM_TRY(pgemm(0, 1, M, qn, d, 1.f, s.h, d, fwl(p, SM_W_QKV, l), d, 0.f, s.qkv, qn, stream));
+    SM_TRY(wgemm(0, 1, M, qn, d, 1.f, s.h, d, fwl(p, SM_W_QKV, l), d, 0.f, s.qkv, qn, stream));
     SM_TRY(sm_rope_qk(s.qkv, p->rope, pos0, S, L, H, KVH, hd, 0, stream));
     split_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(s.qkv, (int)S, (int)L, (int)H, (int)KVH,
                                                      (int)hd, s.q, s.k, s.v);
     SM_TRY(sm_attn_prefill_lse(s.q, s.k, s.v, pos0, s.o, s.lse, SM_F32, SM_F32, S, L, H, KVH, L,
                                hd, stream));
     SM_HIP(hipMemcpyAsync(s.x1, s.x0, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
-    SM_TRY(pgemm(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
+    SM_TRY(wgemm(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
                       stream));
     SM_TRY(sm_rmsnorm(s.x1, fwl(p, SM_W_FFN_NORM, l), M, d, c.norm_eps, s.h2, SM_F32, stream));
     SM_HIP(hipMemcpyAsync(x, s.x1, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
@@ -698,27 +708,27 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
       for (int64_t e = 0; e < E; ++e) {
         const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
         if (n <= 0) continue;
-        SM_TRY(pgemm(0, 1, n, 2 * Fe, d, 1.f, s.rt + o0 * d, d, win + e * 2 * Fe * d, d, 0.f,
+        SM_TRY(wgemm(0, 1, n, 2 * Fe, d, 1.f, s.rt + o0 * d, d, win + e * 2 * Fe * d, d, 0.f,
                      s.ur + o0 * 2 * Fe, 2 * Fe, stream));
       }
       SM_TRY(sm_swiglu(s.ur, SM_F32, RT, Fe, s.ar, stream));
       for (int64_t e = 0; e < E; ++e) {
         const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
         if (n <= 0) continue;
-        SM_TRY(pgemm(0, 1, n, d, Fe, 1.f, s.ar + o0 * Fe, Fe, wdn + e * d * Fe, Fe, 0.f,
+        SM_TRY(wgemm(0, 1, n, d, Fe, 1.f, s.ar + o0 * Fe, Fe, wdn + e * d * Fe, Fe, 0.f,
                      s.yr + o0 * d, d, stream));
       }
       SM_TRY(sm_moe_combine(s.yr, s.tw, s.plan, M, 2, E, d, x, stream));
     } else {
-      SM_TRY(pgemm(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
+      SM_TRY(wgemm(0, 1, M, 2 * F, d, 1.f, s.h2, d, fwl(p, SM_W_IN, l), d, 0.f, s.u, 2 * F,
                    stream));
       SM_TRY(sm_swiglu(s.u, SM_F32, M, F, s.a, stream));
-      SM_TRY(pgemm(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
+      SM_TRY(wgemm(0, 1, M, d, F, 1.f, s.a, F, fwl(p, SM_W_DOWN, l), F, 1.f, x, d, stream));
     }
   }
   SM_TRY(sm_rmsnorm(x, fw(p, SM_W_FINAL_NORM), M, d, c.norm_eps, hf, SM_F32, stream));
   gather_rows_f32<<<blocks256(R * d), 256, 0, st>>>(hf, rows, R, (int)d, hr);
-  SM_TRY(pgemm(0, 1, R, V, d, 1.f, hr, d, fw(p, SM_W_LM_HEAD), d, 0.f, logits, V, stream));
+  SM_TRY(wgemm(0, 1, R, V, d, 1.f, hr, d, fw(p, SM_W_LM_HEAD), d, 0.f, logits, V, stream));
   SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, lp_cur, nullptr, nullptr, 1.f, nullptr,
                     nullptr, stream));
   // ---- the frozen reference and the loss
@@ -733,7 +743,7 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, nullptr, nullptr, logits, 1.f, rscale,
                     nullptr, stream));
   SM_TRY(pgemm(1, 0, V, d, R, 1.f, logits, V, hr, d, 1.f, p->g[SM_W_LM_HEAD], d, stream));
-  SM_TRY(pgemm(0, 0, R, d, V, 1.f, logits, V, fw(p, SM_W_LM_HEAD), d, 0.f, dhr, d, stream));
+  SM_TRY(wgemm(0, 0, R, d, V, 1.f, logits, V, fw(p, SM_W_LM_HEAD), d, 0.f, dhr, d, stream));
   SM_HIP(hipMemsetAsync(dhf, 0, (size_t)M * d * 4, st));
   scatter_rows_f32<<<blocks256(R * d), 256, 0, st>>>(dhr, rows, R, (int)d, dhf);
   SM_TRY(rmsnorm_backward_parts(x, fw(p, SM_W_FINAL_NORM), dhf, M, d, c.norm_eps, 0, dx, dgf,
@@ -756,7 +766,7 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
       for (int64_t e = 0; e < E; ++e) {
         const int64_t o0 = s.off[e], n = s.off[e + 1] - o0;
         if (n <= 0) continue;
-        SM_TRY(pgemm(0, 0, n, Fe, d, 1.f, dyr + o0 * d, d, wdn + e * d * Fe, Fe, 0.f,
+        SM_TRY(wgemm(0, 0, n, Fe, d, 1.f, dyr + o0 * d, d, wdn + e * d * Fe, Fe, 0.f,
                      dar + o0 * Fe, Fe, stream));
         SM_TRY(pgemm(1, 0, d, Fe, n, 1.f, dyr + o0 * d, d, s.ar + o0 * Fe, Fe, 1.f,
                      gdn + e * d * Fe, Fe, stream));
@@ -767,7 +777,7 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
         if (n <= 0) continue;
         SM_TRY(pgemm(1, 0, 2 * Fe, d, n, 1.f, dur + o0 * 2 * Fe, 2 * Fe, s.rt + o0 * d, d, 1.f,
                      gin + e * 2 * Fe * d, d, stream));
-        SM_TRY(pgemm(0, 0, n, d, 2 * Fe, 1.f, dur + o0 * 2 * Fe, 2 * Fe, win + e * 2 * Fe * d,
+        SM_TRY(wgemm(0, 0, n, d, 2 * Fe, 1.f, dur + o0 * 2 * Fe, 2 * Fe, win + e * 2 * Fe * d,
                      d, 0.f, drt + o0 * d, d, stream));
       }
       SM_TRY(sm_moe_gather_backward(drt, SM_F32, s.plan, M, 2, E, d, dh, stream));
@@ -778,18 +788,18 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
                             gl(p, SM_W_ROUTER, l), d, stream));
     } else {
       // FFN: x = x1 + swiglu(h2 W_in^T) W_down^T
-      SM_TRY(pgemm(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
+      SM_TRY(wgemm(0, 0, M, F, d, 1.f, dx, d, fwl(p, SM_W_DOWN, l), F, 0.f, da, F, stream));
       SM_TRY(pgemm(1, 0, d, F, M, 1.f, dx, d, s.a, F, 1.f, gl(p, SM_W_DOWN, l), F, stream));
       SM_TRY(sm_swiglu_backward(s.u, da, SM_F32, M, F, du, stream));
       SM_TRY(pgemm(1, 0, 2 * F, d, M, 1.f, du, 2 * F, s.h2, d, 1.f, gl(p, SM_W_IN, l), d,
                    stream));
-      SM_TRY(pgemm(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
+      SM_TRY(wgemm(0, 0, M, d, 2 * F, 1.f, du, 2 * F, fwl(p, SM_W_IN, l), d, 0.f, dh, d,
                    stream));
     }
     SM_TRY(rmsnorm_backward_parts(s.x1, fwl(p, SM_W_FFN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
                                   gl(p, SM_W_FFN_NORM, l), rinv, dgparts, st));
     // attention: x1 = x0 + attn(rope(h W_qkv^T)) W_o^T
-    SM_TRY(pgemm(0, 0, M, qdim, d, 1.f, dx, d, fwl(p, SM_W_O, l), qdim, 0.f, dO, qdim,
+    SM_TRY(wgemm(0, 0, M, qdim, d, 1.f, dx, d, fwl(p, SM_W_O, l), qdim, 0.f, dO, qdim,
                       stream));
     SM_TRY(pgemm(1, 0, d, qdim, M, 1.f, dx, d, s.o, qdim, 1.f, gl(p, SM_W_O, l), qdim,
                       stream));
@@ -799,7 +809,7 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
                                                      (int)KVH, (int)hd, dqkv);
     SM_TRY(sm_rope_qk(dqkv, p->rope, pos0, S, L, H, KVH, hd, 1, stream));
     SM_TRY(pgemm(1, 0, qn, d, M, 1.f, dqkv, qn, s.h, d, 1.f, gl(p, SM_W_QKV, l), d, stream));
-    SM_TRY(pgemm(0, 0, M, d, qn, 1.f, dqkv, qn, fwl(p, SM_W_QKV, l), d, 0.f, dh, d, stream));
+    SM_TRY(wgemm(0, 0, M, d, qn, 1.f, dqkv, qn, fwl(p, SM_W_QKV, l), d, 0.f, dh, d, stream));
     SM_TRY(rmsnorm_backward_parts(s.x0, fwl(p, SM_W_ATTN_NORM, l), dh, M, d, c.norm_eps, 1, dx,
                                   gl(p, SM_W_ATTN_NORM, l), rinv, dgparts, st));
   }

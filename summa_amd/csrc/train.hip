@@ -538,17 +538,19 @@ inline unsigned g256(int64_t n) { return (unsigned)ceil_div(n, 256); }
 int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
                 const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
                 int64_t ldc, hipStream_t st, float* scratch = nullptr,
-                int64_t scratch_floats = 0);  // gemm_mfma.hip
+                int64_t scratch_floats = 0, int b_planes = 3);  // gemm_mfma.hip
 int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64_t K);
 
 // sm_gemm_ex with the matrix-core launches on `planes` bf16 planes per operand
 // (3: f32-grade; 2: 16-bit operands; 1: bf16 operands); the small problems
 // stay on the f32 FMA kernel. scratch (optional, 16-byte aligned): room for
 // the matrix-core launch's transposed operands (gemm_planes_scratch_floats).
+// b_planes 2: B's values are exact in two bf16 planes (fake-quantized
+// weights), so three-plane products skip the zero third plane of B.
 int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, int64_t K,
                    float alpha, const float* A, int64_t lda, const float* B, int64_t ldb,
                    float beta, float* C, int64_t ldc, void* stream, float* scratch,
-                   int64_t scratch_floats) {
+                   int64_t scratch_floats, int b_planes) {
   SM_REQUIRE(A && B && C, "sm_gemm_ex: null buffer");
   SM_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < (1 << 30) && N < (1 << 30) && K < (1 << 30),
              "sm_gemm_ex: bad shape");
@@ -561,7 +563,7 @@ int gemm_ex_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, i
   // small ones, where a launch has few 128 x 128 tiles, here
   if (K >= 32 && M * N >= (int64_t)128 * 128 * 16 && M * N * K >= ((int64_t)1 << 27))
     return gemm_planes(planes, trans_a != 0, trans_b != 0, M, N, K, alpha, A, lda, B, ldb, beta,
-                       C, ldc, st, scratch, scratch_floats);
+                       C, ldc, st, scratch, scratch_floats, b_planes);
   const dim3 grid((unsigned)ceil_div(N, 64), (unsigned)ceil_div(M, 64));
 #define SM_GX(TA, TB)                                                                        \
   gemm_ex_kernel<TA, TB><<<grid, 256, 0, st>>>(A, lda, B, ldb, C, ldc, (int)M, (int)N, (int)K, \
@@ -582,7 +584,7 @@ extern "C" int sm_gemm_ex(int trans_a, int trans_b, int64_t M, int64_t N, int64_
                           const float* A, int64_t lda, const float* B, int64_t ldb, float beta,
                           float* C, int64_t ldc, void* stream) {
   return gemm_ex_planes(3, trans_a, trans_b, M, N, K, alpha, A, lda, B, ldb, beta, C, ldc, stream,
-                        nullptr, 0);
+                        nullptr, 0, 3);
 }
 
 extern "C" int sm_rmsnorm_backward(const float* x, const float* gamma, const float* dy,

@@ -144,9 +144,40 @@ def test_gemm_planes_scratch_is_bit_exact(dev, planes, ta, tb, M, N, K):
     for nbytes in (need, max(need - 4, 0)):
         scratch = torch.full((max(need, 16) // 4,), float("nan"), device=dev)
         out = c0.clone()
-        call("sm_gemm_planes_ws", planes, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0),
+        call("sm_gemm_planes_ws", planes, 0, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0),
              b.data_ptr(), b.stride(0), 0.5, out.data_ptr(), N, scratch.data_ptr(), nbytes, st)
         assert torch.equal(out, ref), (nbytes, float((out - ref).abs().max()))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 1), (0, 0), (1, 1)])
+def test_gemm_planes_two_plane_b_is_bit_exact(dev, ta, tb):
+    """b_planes 2 (B exact in two bf16 planes, as the policy's fake-quantized
+    weights are: bf16 scales times 4-bit codes) gives three-plane GEMMs the
+    same bits with five plane products as with six; B values that are not
+    two-plane exact (a plain f32 B) do differ, so the flag does change the
+    arithmetic. Bad b_planes values are rejected."""
+    M, N, K = 300, 260, 1030
+    print(f"case gemm_planes two-plane B ta={ta} tb={tb}", flush=True)
+    g = torch.Generator(device=dev).manual_seed(5 + ta + 2 * tb)
+    a = torch.randn((K, M) if ta else (M, K), generator=g, device=dev)
+    bshape = (N, K) if tb else (K, N)
+    codes = torch.randint(-7, 8, bshape, generator=g, device=dev).float()
+    scale = (torch.rand(bshape, generator=g, device=dev) * 0.05 + 0.01).bfloat16().float()
+    bq = codes * scale  # a bf16 scale times a 4-bit code, exact in f32
+    bf = torch.randn(bshape, generator=g, device=dev)
+    st = torch.cuda.current_stream().cuda_stream
+    need = int(_lib.lib().sm_gemm_planes_scratch_bytes(ta, tb, M, N, K))
+    scratch = torch.empty(max(need, 16) // 4, device=dev)
+
+    def run(b, bp):
+        out = torch.zeros(M, N, device=dev)
+        call("sm_gemm_planes_ws", 3, bp, ta, tb, M, N, K, 1.0, a.data_ptr(), a.stride(0),
+             b.data_ptr(), b.stride(0), 0.0, out.data_ptr(), N, scratch.data_ptr(), need, st)
+        return out
+    assert torch.equal(run(bq, 2), run(bq, 3))
+    assert not torch.equal(run(bf, 2), run(bf, 3))
+    with pytest.raises(_lib.SummaError, match="b_planes must be"):
+        run(bq, 1)
 
 
 def test_gemm_planes_rejects_bad_count(dev):
