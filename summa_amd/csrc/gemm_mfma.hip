@@ -43,6 +43,7 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef f32x4 f4;
 
 constexpr int kBM = 128, kBK = 32, kRS = kBK + 8;  // tile rows, k per step, LDS row stride
 constexpr int kPlane = kBM * kRS;                   // bf16 per plane of one operand tile
@@ -254,10 +255,47 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
   }
 }
 
+// The same with 16-byte accesses (R, C, ld, ldo multiples of 4, 16-byte
+// aligned rows): thread (row group, f4 column) reads four consecutive floats
+// of an input row and, after the barrier, gathers four consecutive input rows
+// of one column from LDS into one 16-byte store of an output row.
+__global__ __launch_bounds__(256) void transpose_f32x4_kernel(const float* __restrict__ in,
+                                                              int64_t ld, int R, int C,
+                                                              float* __restrict__ out,
+                                                              int64_t ldo) {
+  __shared__ float t[64][65];
+  const int r0 = (int)blockIdx.y * 64, c0 = (int)blockIdx.x * 64;
+  const int q = threadIdx.x % 16, rg = threadIdx.x / 16;  // f4 column, row (group)
+  f4 v[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = r0 + rg + 16 * i, c = c0 + 4 * q;
+    v[i] = (r < R && c < C) ? *reinterpret_cast<const f4*>(in + (int64_t)r * ld + c)
+                            : f4{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) t[rg + 16 * i][4 * q + e] = v[i][e];
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int cl = rg + 16 * i, c = c0 + cl, r = r0 + 4 * q;  // output row c, columns r..r+3
+    if (c < C && r < R) {
+      const f4 w = f4{t[4 * q][cl], t[4 * q + 1][cl], t[4 * q + 2][cl], t[4 * q + 3][cl]};
+      *reinterpret_cast<f4*>(out + (int64_t)c * ldo + r) = w;
+    }
+  }
+}
+
 void transpose_f32(const float* in, int64_t ld, int64_t R, int64_t C, float* out, int64_t ldo,
                    hipStream_t st) {
   const dim3 grid((unsigned)ceil_div(C, 64), (unsigned)ceil_div(R, 64));
-  transpose_f32_kernel<<<grid, 256, 0, st>>>(in, ld, (int)R, (int)C, out, ldo);
+  const bool v4 = R % 4 == 0 && C % 4 == 0 && ld % 4 == 0 && ldo % 4 == 0 &&
+                  reinterpret_cast<uintptr_t>(in) % 16 == 0 &&
+                  reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  if (v4) transpose_f32x4_kernel<<<grid, 256, 0, st>>>(in, ld, (int)R, (int)C, out, ldo);
+  else transpose_f32_kernel<<<grid, 256, 0, st>>>(in, ld, (int)R, (int)C, out, ldo);
 }
 
 template <int P, int PB = P>
