@@ -564,8 +564,9 @@ int sm_gemm_planes(int planes, int trans_a, int trans_b, int64_t M, int64_t N, i
  * sm_gemm_planes_scratch_bytes(trans_a, trans_b, M, N, K) bytes: an operand
  * whose k is not contiguous (op(A) of a transposed A, op(B) of an
  * untransposed B) is transposed into it first, so that both operands stream
- * along k; the result is sm_gemm_planes' bit for bit. A smaller scratch runs
- * sm_gemm_planes as is. b_planes 2 (with planes 3) declares every B value
+ * along k (at one plane both operands are converted once into bf16 copies
+ * there instead); the result is sm_gemm_planes' bit for bit. A smaller
+ * scratch runs sm_gemm_planes as is. b_planes 2 (with planes 3) declares every B value
  * exact in two bf16 planes (value - bf16(value) is itself a bf16, as for a
  * bf16 scale times a 4-bit code): the zero third plane of B is then not
  * multiplied (five plane products instead of six, the same bits); 0 or 3:

@@ -35,6 +35,8 @@
 // wave reads its 2 + 2 fragments of each plane and issues the MFMAs product
 // by product across its four blocks, so four independent accumulations
 // separate two dependent ones.
+#include <algorithm>
+
 #include "common.hpp"
 
 namespace sm {
@@ -232,6 +234,201 @@ __global__ __launch_bounds__(256, 2) void gemm_planes_kernel(
     }
 }
 
+// ---- pre-split operands: each operand split once into its bf16 planes,
+// padded and zero-filled, [P][Rp][Kp] (Rp a multiple of 128 rows, Kp of 32
+// k), so that the GEMM's K loop only copies 16-byte chunks into LDS. The
+// planes are those the tile loader forms (split_pair on the same values, 0
+// past the matrix), in the same LDS layout, so the products and their order,
+// and the result, are the same bit for bit.
+
+// op(X) row r, k contiguous: element (r, k) at X[r * ld + k]. Thread: 8
+// consecutive k of one row (two 16-byte loads when aligned), one 16-byte
+// store per plane.
+template <int P>
+__global__ __launch_bounds__(256) void split_rows_kernel(const float* __restrict__ X, int64_t ld,
+                                                         int R, int K, __bf16* __restrict__ out,
+                                                         int Rp, int Kp, int vec) {
+  const int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int kc = Kp / 8;
+  if (c >= (int64_t)Rp * kc) return;
+  const int r = (int)(c / kc), k = (int)(c % kc) * 8;
+  float v[8];
+  if (vec && r < R && k + 8 <= K) {
+    const f4 a = *reinterpret_cast<const f4*>(X + (int64_t)r * ld + k);
+    const f4 b = *reinterpret_cast<const f4*>(X + (int64_t)r * ld + k + 4);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = a[e];
+      v[4 + e] = b[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = (r < R && k + e < K) ? X[(int64_t)r * ld + k + e] : 0.f;
+  }
+  u32x4 w[P];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t x[P];
+    split_pair<P>(v[2 * i], v[2 * i + 1], x);
+#pragma unroll
+    for (int p = 0; p < P; ++p) w[p][i] = x[p];
+  }
+#pragma unroll
+  for (int p = 0; p < P; ++p)
+    *reinterpret_cast<u32x4*>(out + (int64_t)p * Rp * Kp + (int64_t)r * Kp + k) = w[p];
+}
+
+// op(X) row r = column r of X: element (r, k) at X[k * ld + r]. 64 k x 64 r
+// tiles through LDS (reads 64 consecutive r per wave instruction), then
+// thread: 8 consecutive k of one r, one 16-byte store per plane.
+template <int P>
+__global__ __launch_bounds__(256) void split_cols_kernel(const float* __restrict__ X, int64_t ld,
+                                                         int R, int K, __bf16* __restrict__ out,
+                                                         int Rp, int Kp) {
+  __shared__ float t[64][65];  // [k][r]
+  const int k0 = (int)blockIdx.x * 64, r0 = (int)blockIdx.y * 64;
+  const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
+  for (int i = ty; i < 64; i += 4) {
+    const int k = k0 + i, r = r0 + tx;
+    t[i][tx] = (k < K && r < R) ? X[(int64_t)k * ld + r] : 0.f;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = (int)threadIdx.x + 256 * h, rl = c / 8, kl = (c % 8) * 8;
+    if (k0 + kl >= Kp) continue;
+    u32x4 w[P];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t x[P];
+      split_pair<P>(t[kl + 2 * i][rl], t[kl + 2 * i + 1][rl], x);
+#pragma unroll
+      for (int p = 0; p < P; ++p) w[p][i] = x[p];
+    }
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      *reinterpret_cast<u32x4*>(out + (int64_t)p * Rp * Kp + (int64_t)(r0 + rl) * Kp + k0 + kl) =
+          w[p];
+  }
+}
+
+// C = alpha op(A) op(B) + beta C from pre-split planes: A [P][Mp][Kp], B
+// [PB][Np][Kp] (B's rows are op(B)'s columns). gemm_planes_kernel's tiles,
+// waves, LDS layout and MFMA order; per 32-k step a thread copies two
+// 16-byte chunks (one row's 8 k) of each plane of each operand, requested one
+// step ahead.
+template <int P, int PB>
+__global__ __launch_bounds__(256, 2) void gemm_split_kernel(
+    const __bf16* __restrict__ A, const __bf16* __restrict__ B, int Kp, int64_t pa, int64_t pb,
+    float* __restrict__ C, int64_t ldc, int M, int N, float alpha, float beta) {
+  __shared__ __attribute__((aligned(16))) __bf16 As[P * kPlane];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[PB * kPlane];
+  const int t = threadIdx.x, wave = t / kWave, lane = t % kWave;
+  const int wm = wave / 2, wn = wave % 2;
+  const int m0 = (int)blockIdx.y * kBM, n0 = (int)blockIdx.x * kBM;
+  // chunk h of this thread: row (t + 256 h) / 4, k 8 ((t + 256 h) % 4)
+  int64_t ga[2], gb[2];
+  int lo[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int c = t + 256 * h, row = c / 4, k8 = (c % 4) * 8;
+    ga[h] = (int64_t)(m0 + row) * Kp + k8;
+    gb[h] = (int64_t)(n0 + row) * Kp + k8;
+    lo[h] = row * kRS + k8;
+  }
+  u32x4 ra[P][2], rb[PB][2];
+  auto gload = [&](int k0) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) ra[p][h] = *reinterpret_cast<const u32x4*>(A + p * pa + ga[h] + k0);
+#pragma unroll
+      for (int p = 0; p < PB; ++p) rb[p][h] = *reinterpret_cast<const u32x4*>(B + p * pb + gb[h] + k0);
+    }
+  };
+  auto lstore = [&]() {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int p = 0; p < P; ++p) *reinterpret_cast<u32x4*>(As + p * kPlane + lo[h]) = ra[p][h];
+#pragma unroll
+      for (int p = 0; p < PB; ++p) *reinterpret_cast<u32x4*>(Bs + p * kPlane + lo[h]) = rb[p][h];
+    }
+  };
+  gload(0);
+  lstore();
+  __syncthreads();
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+  const int fo = (lane % 32) * kRS + 8 * (lane / 32);
+  for (int k0 = 0; k0 < Kp; k0 += kBK) {
+    const bool more = k0 + kBK < Kp;  // uniform
+    if (more) gload(k0 + kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK; ks += 16) {
+      bf16x8 a[P][2], b[PB][2];
+#pragma unroll
+      for (int p = 0; p < P; ++p)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          a[p][i] = *reinterpret_cast<const bf16x8*>(As + p * kPlane + (wm * 64 + i * 32) * kRS +
+                                                     fo + ks);
+#pragma unroll
+      for (int p = 0; p < PB; ++p)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          b[p][i] = *reinterpret_cast<const bf16x8*>(Bs + p * kPlane + (wn * 64 + i * 32) * kRS +
+                                                     fo + ks);
+#pragma unroll
+      for (int q = 0; q < Products<P, PB>::n; ++q)
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                a[Products<P, PB>::a[q]][i], b[Products<P, PB>::b[q]][j], acc[i][j], 0, 0, 0);
+    }
+    if (more) {
+      __syncthreads();  // every wave is done with this step's tiles
+      lstore();
+      __syncthreads();
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + j * 32 + lane % 32;
+      if (col >= N) continue;
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * 64 + i * 32 + 8 * (e / 4) + 4 * (lane / 32) + e % 4;
+        if (row >= M) continue;
+        float* o = C + (int64_t)row * ldc + col;
+        *o = beta == 0.f ? alpha * acc[i][j][e] : fmaf(alpha, acc[i][j][e], beta * *o);
+      }
+    }
+}
+
+// op(X) (rows r, k along kc or across) -> planes [P][Rp][Kp] at out
+template <int P>
+void split_operand(const float* X, int64_t ld, bool kc, int64_t R, int64_t K, __bf16* out,
+                   int64_t Rp, int64_t Kp, hipStream_t st) {
+  if (kc) {
+    const int vec = (ld % 4 == 0 && reinterpret_cast<uintptr_t>(X) % 16 == 0) ? 1 : 0;
+    split_rows_kernel<P><<<(unsigned)ceil_div(Rp * (Kp / 8), 256), 256, 0, st>>>(
+        X, ld, (int)R, (int)K, out, (int)Rp, (int)Kp, vec);
+  } else {
+    const dim3 grid((unsigned)ceil_div(Kp, 64), (unsigned)(Rp / 64));
+    split_cols_kernel<P><<<grid, 256, 0, st>>>(X, ld, (int)R, (int)K, out, (int)Rp, (int)Kp);
+  }
+}
+
 // out[c * ldo + r] = in[r * ld + c] for an R x C f32 matrix: 64 x 64 tiles
 // through LDS (65-float rows, so the column reads of the write phase spread
 // over the banks); each wave instruction reads and writes 64 consecutive
@@ -242,13 +439,11 @@ __global__ __launch_bounds__(256) void transpose_f32_kernel(const float* __restr
   __shared__ float t[64][65];
   const int r0 = (int)blockIdx.y * 64, c0 = (int)blockIdx.x * 64;
   const int tx = threadIdx.x % 64, ty = threadIdx.x / 64;
-#pragma unroll
   for (int i = ty; i < 64; i += 4) {
     const int r = r0 + i, c = c0 + tx;
     if (r < R && c < C) t[i][tx] = in[(int64_t)r * ld + c];
   }
   __syncthreads();
-#pragma unroll
   for (int i = ty; i < 64; i += 4) {
     const int c = c0 + i, r = r0 + tx;
     if (c < C && r < R) out[(int64_t)c * ldo + r] = t[tx][i];
@@ -314,25 +509,71 @@ void launch_planes(bool ta, bool tb, dim3 grid, hipStream_t st, const float* A, 
 
 }  // namespace
 
-int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64_t K) {
+// scratch for the transposed-operand path (floats)
+int64_t transpose_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64_t K) {
   const int64_t kp = (K + 3) / 4 * 4;
   return (ta ? M * kp : 0) + (tb ? 0 : N * kp);
+}
+
+// scratch for the pre-split path with P planes of A and PB of B (floats)
+int64_t split_scratch_floats(int P, int PB, int64_t M, int64_t N, int64_t K) {
+  const int64_t Mp = ceil_div(M, kBM) * kBM, Np = ceil_div(N, kBM) * kBM, Kp = ceil_div(K, kBK) * kBK;
+  return (P * Mp * Kp + PB * Np * Kp + 1) / 2;
+}
+
+// the most any call needs (the pre-split path runs at one plane)
+int64_t gemm_planes_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64_t K) {
+  return std::max(split_scratch_floats(1, 1, M, N, K), transpose_scratch_floats(ta, tb, M, N, K));
 }
 
 int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, float alpha,
                 const float* A, int64_t lda, const float* B, int64_t ldb, float beta, float* C,
                 int64_t ldc, hipStream_t st, float* scratch, int64_t scratch_floats,
                 int b_planes) {
-  // With a scratch, an operand whose k is not its contiguous dimension (op(A)
-  // of a transposed A, op(B) of an untransposed B) is first transposed into
-  // it, rows padded to a multiple of 4 floats, so that the GEMM runs with
-  // 16-byte loads along k on both operands. The tiles reach LDS with the same
-  // values in the same k order, so the result is the same bit for bit.
-  // Measured on one GRPO group's shapes (config[2], three planes, event-timed,
-  // transposes included): FFN-in weight gradient 2.78 -> 2.30 ms, its data
-  // gradient 2.28 -> 1.99 ms; LM head 7.40 -> 6.21 and 6.45 -> 5.93 ms; the
-  // policy update's prepare 500 -> 475 ms per group.
-  const int64_t need = gemm_planes_scratch_floats(ta, tb, M, N, K);
+  const int P = planes, PB = (planes == 3 && b_planes == 2) ? 2 : planes;
+  const bool al16 = scratch && reinterpret_cast<uintptr_t>(scratch) % 16 == 0;
+  // One plane, with room for both operands' bf16 copies: each is converted
+  // once (transposed on the way where its k is not contiguous) and
+  // gemm_split_kernel only copies chunks into LDS in its K loop: the same
+  // values, LDS tiles and MFMA order, so the same bits. Measured on the policy
+  // update's config[2] shapes: 1.4-1.9x faster at one plane (FFN-in forward
+  // 780 -> 517 us, LM head forward 3.90 -> 2.04 ms); at two and three planes
+  // the same form was 0-35 % slower (its staged chunks of every plane leave
+  // two waves per SIMD where the in-loop split keeps three), so they keep the
+  // in-loop split.
+  if (P == 1 && al16 && split_scratch_floats(P, PB, M, N, K) <= scratch_floats) {
+    const int64_t Mp = ceil_div(M, kBM) * kBM, Np = ceil_div(N, kBM) * kBM;
+    const int64_t Kp = ceil_div(K, kBK) * kBK;
+    __bf16* sa = reinterpret_cast<__bf16*>(scratch);
+    __bf16* sb = sa + (int64_t)P * Mp * Kp;  // 16-byte aligned: Mp Kp is a multiple of 4096
+    if (P == 1) split_operand<1>(A, lda, !ta, M, K, sa, Mp, Kp, st);
+    else if (P == 2) split_operand<2>(A, lda, !ta, M, K, sa, Mp, Kp, st);
+    else split_operand<3>(A, lda, !ta, M, K, sa, Mp, Kp, st);
+    if (PB == 1) split_operand<1>(B, ldb, tb, N, K, sb, Np, Kp, st);
+    else if (PB == 2) split_operand<2>(B, ldb, tb, N, K, sb, Np, Kp, st);
+    else split_operand<3>(B, ldb, tb, N, K, sb, Np, Kp, st);
+    const dim3 g2((unsigned)(Np / kBM), (unsigned)(Mp / kBM));
+#define SM_GS(PA_, PB_)                                                                        \
+  gemm_split_kernel<PA_, PB_><<<g2, 256, 0, st>>>(sa, sb, (int)Kp, Mp * Kp, Np * Kp, C, ldc,   \
+                                                  (int)M, (int)N, alpha, beta)
+    if (P == 1) SM_GS(1, 1);
+    else if (P == 2) SM_GS(2, 2);
+    else if (PB == 2) SM_GS(3, 2);
+    else SM_GS(3, 3);
+#undef SM_GS
+    SM_LAUNCH_CHECK();
+    return SM_OK;
+  }
+  // Else, with a smaller scratch, an operand whose k is not its contiguous
+  // dimension (op(A) of a transposed A, op(B) of an untransposed B) is first
+  // transposed into it, rows padded to a multiple of 4 floats, so that the
+  // GEMM runs with 16-byte loads along k on both operands. The tiles reach
+  // LDS with the same values in the same k order, so the result is the same
+  // bit for bit. Measured on one GRPO group's shapes (config[2], three
+  // planes, event-timed, transposes included): FFN-in weight gradient 2.78 ->
+  // 2.30 ms, its data gradient 2.28 -> 1.99 ms; LM head 7.40 -> 6.21 and 6.45
+  // -> 5.93 ms.
+  const int64_t need = transpose_scratch_floats(ta, tb, M, N, K);
   if (scratch && need > 0 && need <= scratch_floats &&
       reinterpret_cast<uintptr_t>(scratch) % 16 == 0) {
     const int64_t kp = (K + 3) / 4 * 4;

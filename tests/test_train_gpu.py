@@ -121,14 +121,17 @@ def test_gemm_planes_reduced(dev, planes, ta, tb, M, N, K, pad):
     assert dist > 3 * err  # the kernel follows the plane model, not the exact product
 
 
-@pytest.mark.parametrize("planes", [1, 3])
+@pytest.mark.parametrize("planes", [1, 2, 3])
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
 @pytest.mark.parametrize("M,N,K", [(300, 260, 333), (513, 130, 1030)])
 def test_gemm_planes_scratch_is_bit_exact(dev, planes, ta, tb, M, N, K):
-    """sm_gemm_planes_ws (operands whose k is not contiguous transposed into
-    the scratch first, rows padded to 4 floats) equals sm_gemm_planes (the
-    kernel's own transposed loads) bit for bit, with alpha and beta; a
-    scratch one float short runs the plain path (still equal)."""
+    """sm_gemm_planes_ws equals sm_gemm_planes (the kernel's own plane split
+    and transposed loads) bit for bit, with alpha and beta, on each of its
+    paths: a scratch of sm_gemm_planes_scratch_bytes (one plane: both operands
+    converted once into zero-padded bf16 copies, transposed where k is not
+    contiguous; more planes: the transposes below); one only big enough for
+    the transposes of the operands whose k is not contiguous (rows padded to
+    4 floats); none."""
     print(f"case gemm_planes_ws planes={planes} ta={ta} tb={tb} M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device=dev).manual_seed(M + N + K + 4 * ta + 2 * tb)
     a = torch.randn((K, M) if ta else (M, K), generator=g, device=dev)
@@ -136,12 +139,14 @@ def test_gemm_planes_scratch_is_bit_exact(dev, planes, ta, tb, M, N, K):
     c0 = torch.randn(M, N, generator=g, device=dev)
     st = torch.cuda.current_stream().cuda_stream
     need = int(_lib.lib().sm_gemm_planes_scratch_bytes(ta, tb, M, N, K))
-    kp = (K + 3) // 4 * 4
-    assert need == 4 * ((M * kp if ta else 0) + (0 if tb else N * kp))
+    kp4 = (K + 3) // 4 * 4
+    trans = 4 * ((M * kp4 if ta else 0) + (0 if tb else N * kp4))
+    mp, np_, kp = -(-M // 128) * 128, -(-N // 128) * 128, -(-K // 32) * 32
+    assert need == max(4 * ((mp * kp + np_ * kp + 1) // 2), trans)
     ref = c0.clone()
     call("sm_gemm_planes", planes, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0), b.data_ptr(),
          b.stride(0), 0.5, ref.data_ptr(), N, st)
-    for nbytes in (need, max(need - 4, 0)):
+    for nbytes in (need, trans, 0):
         scratch = torch.full((max(need, 16) // 4,), float("nan"), device=dev)
         out = c0.clone()
         call("sm_gemm_planes_ws", planes, 0, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0),
@@ -169,12 +174,14 @@ def test_gemm_planes_two_plane_b_is_bit_exact(dev, ta, tb):
     need = int(_lib.lib().sm_gemm_planes_scratch_bytes(ta, tb, M, N, K))
     scratch = torch.empty(max(need, 16) // 4, device=dev)
 
-    def run(b, bp):
+    def run(b, bp, nbytes=need):
         out = torch.zeros(M, N, device=dev)
         call("sm_gemm_planes_ws", 3, bp, ta, tb, M, N, K, 1.0, a.data_ptr(), a.stride(0),
-             b.data_ptr(), b.stride(0), 0.0, out.data_ptr(), N, scratch.data_ptr(), need, st)
+             b.data_ptr(), b.stride(0), 0.0, out.data_ptr(), N, scratch.data_ptr(), nbytes, st)
         return out
-    assert torch.equal(run(bq, 2), run(bq, 3))
+    ref = run(bq, 3)
+    assert torch.equal(run(bq, 2), ref)  # pre-split planes
+    assert torch.equal(run(bq, 2, 0), ref)  # the kernel's own split
     assert not torch.equal(run(bf, 2), run(bf, 3))
     with pytest.raises(_lib.SummaError, match="b_planes must be"):
         run(bq, 1)
