@@ -313,33 +313,34 @@ __global__ __launch_bounds__(256) void split_cols_kernel(const float* __restrict
 }
 
 // C = alpha op(A) op(B) + beta C from pre-split planes: A [P][Mp][Kp], B
-// [PB][Np][Kp] (B's rows are op(B)'s columns). gemm_planes_kernel's tiles,
-// waves, LDS layout and MFMA order; per 32-k step a thread copies two
-// 16-byte chunks (one row's 8 k) of each plane of each operand, requested one
-// step ahead.
-template <int P, int PB>
+// [PB][Np][Kp] (B's rows are op(B)'s columns; Kp a multiple of BK).
+// gemm_planes_kernel's tiles, waves and MFMA order, with BK k per step (rows
+// of BK + 8 in LDS); per step a thread copies BK / 16 16-byte chunks (8 k of
+// one row) of each plane of each operand, requested one step ahead.
+template <int P, int PB, int BK = kBK>
 __global__ __launch_bounds__(256, 2) void gemm_split_kernel(
     const __bf16* __restrict__ A, const __bf16* __restrict__ B, int Kp, int64_t pa, int64_t pb,
     float* __restrict__ C, int64_t ldc, int M, int N, float alpha, float beta) {
-  __shared__ __attribute__((aligned(16))) __bf16 As[P * kPlane];
-  __shared__ __attribute__((aligned(16))) __bf16 Bs[PB * kPlane];
+  constexpr int RS = BK + 8, PL = kBM * RS, CH = BK / 16;  // LDS row, plane, chunks per thread
+  __shared__ __attribute__((aligned(16))) __bf16 As[P * PL];
+  __shared__ __attribute__((aligned(16))) __bf16 Bs[PB * PL];
   const int t = threadIdx.x, wave = t / kWave, lane = t % kWave;
   const int wm = wave / 2, wn = wave % 2;
   const int m0 = (int)blockIdx.y * kBM, n0 = (int)blockIdx.x * kBM;
-  // chunk h of this thread: row (t + 256 h) / 4, k 8 ((t + 256 h) % 4)
-  int64_t ga[2], gb[2];
-  int lo[2];
+  // chunk h of this thread: row (t + 256 h) / (BK / 8), k 8 ((t + 256 h) % (BK / 8))
+  int64_t ga[CH], gb[CH];
+  int lo[CH];
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    const int c = t + 256 * h, row = c / 4, k8 = (c % 4) * 8;
+  for (int h = 0; h < CH; ++h) {
+    const int c = t + 256 * h, row = c / (BK / 8), k8 = (c % (BK / 8)) * 8;
     ga[h] = (int64_t)(m0 + row) * Kp + k8;
     gb[h] = (int64_t)(n0 + row) * Kp + k8;
-    lo[h] = row * kRS + k8;
+    lo[h] = row * RS + k8;
   }
-  u32x4 ra[P][2], rb[PB][2];
+  u32x4 ra[P][CH], rb[PB][CH];
   auto gload = [&](int k0) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < CH; ++h) {
 #pragma unroll
       for (int p = 0; p < P; ++p) ra[p][h] = *reinterpret_cast<const u32x4*>(A + p * pa + ga[h] + k0);
 #pragma unroll
@@ -348,11 +349,11 @@ __global__ __launch_bounds__(256, 2) void gemm_split_kernel(
   };
   auto lstore = [&]() {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < CH; ++h) {
 #pragma unroll
-      for (int p = 0; p < P; ++p) *reinterpret_cast<u32x4*>(As + p * kPlane + lo[h]) = ra[p][h];
+      for (int p = 0; p < P; ++p) *reinterpret_cast<u32x4*>(As + p * PL + lo[h]) = ra[p][h];
 #pragma unroll
-      for (int p = 0; p < PB; ++p) *reinterpret_cast<u32x4*>(Bs + p * kPlane + lo[h]) = rb[p][h];
+      for (int p = 0; p < PB; ++p) *reinterpret_cast<u32x4*>(Bs + p * PL + lo[h]) = rb[p][h];
     }
   };
   gload(0);
@@ -365,24 +366,24 @@ __global__ __launch_bounds__(256, 2) void gemm_split_kernel(
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
-  const int fo = (lane % 32) * kRS + 8 * (lane / 32);
-  for (int k0 = 0; k0 < Kp; k0 += kBK) {
-    const bool more = k0 + kBK < Kp;  // uniform
-    if (more) gload(k0 + kBK);
+  const int fo = (lane % 32) * RS + 8 * (lane / 32);
+  for (int k0 = 0; k0 < Kp; k0 += BK) {
+    const bool more = k0 + BK < Kp;  // uniform
+    if (more) gload(k0 + BK);
 #pragma unroll
-    for (int ks = 0; ks < kBK; ks += 16) {
+    for (int ks = 0; ks < BK; ks += 16) {
       bf16x8 a[P][2], b[PB][2];
 #pragma unroll
       for (int p = 0; p < P; ++p)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          a[p][i] = *reinterpret_cast<const bf16x8*>(As + p * kPlane + (wm * 64 + i * 32) * kRS +
+          a[p][i] = *reinterpret_cast<const bf16x8*>(As + p * PL + (wm * 64 + i * 32) * RS +
                                                      fo + ks);
 #pragma unroll
       for (int p = 0; p < PB; ++p)
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-          b[p][i] = *reinterpret_cast<const bf16x8*>(Bs + p * kPlane + (wn * 64 + i * 32) * kRS +
+          b[p][i] = *reinterpret_cast<const bf16x8*>(Bs + p * PL + (wn * 64 + i * 32) * RS +
                                                      fo + ks);
 #pragma unroll
       for (int q = 0; q < Products<P, PB>::n; ++q)
@@ -515,9 +516,16 @@ int64_t transpose_scratch_floats(bool ta, bool tb, int64_t M, int64_t N, int64_t
   return (ta ? M * kp : 0) + (tb ? 0 : N * kp);
 }
 
+// k per step of the one-plane pre-split GEMM. Measured against 32 (two
+// barriers per 8 MFMAs a wave): 7-18 % faster on the policy update's shapes
+// (LM head forward 2.00 -> 1.67 ms); 128 (two waves per SIMD) mixed, the
+// FFN-in forward and LM head slower.
+constexpr int kSplitBK = 64;
+
 // scratch for the pre-split path with P planes of A and PB of B (floats)
 int64_t split_scratch_floats(int P, int PB, int64_t M, int64_t N, int64_t K) {
-  const int64_t Mp = ceil_div(M, kBM) * kBM, Np = ceil_div(N, kBM) * kBM, Kp = ceil_div(K, kBK) * kBK;
+  const int64_t Mp = ceil_div(M, kBM) * kBM, Np = ceil_div(N, kBM) * kBM;
+  const int64_t Kp = ceil_div(K, kSplitBK) * kSplitBK;
   return (P * Mp * Kp + PB * Np * Kp + 1) / 2;
 }
 
@@ -535,32 +543,23 @@ int gemm_planes(int planes, bool ta, bool tb, int64_t M, int64_t N, int64_t K, f
   // One plane, with room for both operands' bf16 copies: each is converted
   // once (transposed on the way where its k is not contiguous) and
   // gemm_split_kernel only copies chunks into LDS in its K loop: the same
-  // values, LDS tiles and MFMA order, so the same bits. Measured on the policy
-  // update's config[2] shapes: 1.4-1.9x faster at one plane (FFN-in forward
-  // 780 -> 517 us, LM head forward 3.90 -> 2.04 ms); at two and three planes
+  // values and MFMA order, so the same bits. Measured on the policy update's
+  // config[2] shapes: 1.4-1.9x faster at one plane with 32-k steps (FFN-in
+  // forward 780 -> 517 us, LM head forward 3.90 -> 2.04 ms; 430 us and 1.65 ms
+  // with 64-k steps); at two and three planes
   // the same form was 0-35 % slower (its staged chunks of every plane leave
   // two waves per SIMD where the in-loop split keeps three), so they keep the
   // in-loop split.
   if (P == 1 && al16 && split_scratch_floats(P, PB, M, N, K) <= scratch_floats) {
     const int64_t Mp = ceil_div(M, kBM) * kBM, Np = ceil_div(N, kBM) * kBM;
-    const int64_t Kp = ceil_div(K, kBK) * kBK;
+    const int64_t Kp = ceil_div(K, kSplitBK) * kSplitBK;
     __bf16* sa = reinterpret_cast<__bf16*>(scratch);
-    __bf16* sb = sa + (int64_t)P * Mp * Kp;  // 16-byte aligned: Mp Kp is a multiple of 4096
-    if (P == 1) split_operand<1>(A, lda, !ta, M, K, sa, Mp, Kp, st);
-    else if (P == 2) split_operand<2>(A, lda, !ta, M, K, sa, Mp, Kp, st);
-    else split_operand<3>(A, lda, !ta, M, K, sa, Mp, Kp, st);
-    if (PB == 1) split_operand<1>(B, ldb, tb, N, K, sb, Np, Kp, st);
-    else if (PB == 2) split_operand<2>(B, ldb, tb, N, K, sb, Np, Kp, st);
-    else split_operand<3>(B, ldb, tb, N, K, sb, Np, Kp, st);
+    __bf16* sb = sa + Mp * Kp;  // 16-byte aligned: Mp Kp is a multiple of 8192
+    split_operand<1>(A, lda, !ta, M, K, sa, Mp, Kp, st);
+    split_operand<1>(B, ldb, tb, N, K, sb, Np, Kp, st);
     const dim3 g2((unsigned)(Np / kBM), (unsigned)(Mp / kBM));
-#define SM_GS(PA_, PB_)                                                                        \
-  gemm_split_kernel<PA_, PB_><<<g2, 256, 0, st>>>(sa, sb, (int)Kp, Mp * Kp, Np * Kp, C, ldc,   \
-                                                  (int)M, (int)N, alpha, beta)
-    if (P == 1) SM_GS(1, 1);
-    else if (P == 2) SM_GS(2, 2);
-    else if (PB == 2) SM_GS(3, 2);
-    else SM_GS(3, 3);
-#undef SM_GS
+    gemm_split_kernel<1, 1, kSplitBK><<<g2, 256, 0, st>>>(sa, sb, (int)Kp, Mp * Kp, Np * Kp, C,
+                                                          ldc, (int)M, (int)N, alpha, beta);
     SM_LAUNCH_CHECK();
     return SM_OK;
   }

@@ -141,7 +141,7 @@ def test_gemm_planes_scratch_is_bit_exact(dev, planes, ta, tb, M, N, K):
     need = int(_lib.lib().sm_gemm_planes_scratch_bytes(ta, tb, M, N, K))
     kp4 = (K + 3) // 4 * 4
     trans = 4 * ((M * kp4 if ta else 0) + (0 if tb else N * kp4))
-    mp, np_, kp = -(-M // 128) * 128, -(-N // 128) * 128, -(-K // 32) * 32
+    mp, np_, kp = -(-M // 128) * 128, -(-N // 128) * 128, -(-K // 64) * 64
     assert need == max(4 * ((mp * kp + np_ * kp + 1) // 2), trans)
     ref = c0.clone()
     call("sm_gemm_planes", planes, ta, tb, M, N, K, 0.75, a.data_ptr(), a.stride(0), b.data_ptr(),
