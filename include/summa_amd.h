@@ -585,6 +585,23 @@ int sm_attn_backward_f32(const float* q, const float* k, const float* v, const f
                          const float* dout, const float* lse, int64_t S, int64_t L, int64_t H,
                          int64_t KVH, int64_t head_dim, float* dq, float* dk, float* dv,
                          float* delta_scratch, void* stream);
+/* The f32 attention forward (sm_attn_prefill_lse with dtype SM_F32: causal,
+ * positions pos0[s] + i, log-sum-exp out) and its backward
+ * (sm_attn_backward_f32) with bf16 matrix-core operands: every product takes
+ * its f32 operands rounded to bf16 (nearest even) and accumulates in f32. This
+ * is the 16-bit precision of the reference's CUDA-path flash attention (F16
+ * in, F32 accumulate, cube_attention.rs:127-220) and of its backward, which
+ * forms P and dS in bf16 (cube_attention.rs:53-95); the policy update runs it
+ * with one-plane (bf16) matmuls (sm_policy_set_matmul_planes 1). Rows shorter
+ * than 32 positions keep the f32 kernels. Same arguments as the f32 calls. */
+int sm_attn_prefill_lse_bf16ops(const float* q, const float* kcache, const float* vcache,
+                                const int32_t* pos0, float* out, float* lse, int64_t S,
+                                int64_t L, int64_t H, int64_t KVH, int64_t cap, int64_t head_dim,
+                                void* stream);
+int sm_attn_backward_bf16ops(const float* q, const float* k, const float* v, const float* o,
+                             const float* dout, const float* lse, int64_t S, int64_t L,
+                             int64_t H, int64_t KVH, int64_t head_dim, float* dq, float* dk,
+                             float* dv, float* delta_scratch, void* stream);
 int sm_embed_backward(const int32_t* ids, const float* dx, int64_t rows, int64_t d,
                       int64_t vocab, float* dtable, void* stream);
 int sm_adamw_step(float* param, const float* grad, float* m, float* v, int64_t n, float lr,

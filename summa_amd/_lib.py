@@ -100,6 +100,10 @@ SIGNATURES: dict[str, tuple] = {
     "sm_rope_qk": (i32, [vp, vp, vp, i64, i64, i64, i64, i64, i32, vp]),
     "sm_attn_backward_f32": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, vp,
                                    vp]),
+    "sm_attn_backward_bf16ops": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp,
+                                       vp, vp]),
+    "sm_attn_prefill_lse_bf16ops": (i32, [vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, i64, i64,
+                                          vp]),
     "sm_embed_backward": (i32, [vp, vp, i64, i64, i64, vp, vp]),
     "sm_adamw_step": (i32, [vp, vp, vp, vp, i64, f32, f32, f32, f32, f32, i64, vp]),
     "sm_muon_momentum": (i32, [vp, vp, vp, i64, f32, i32, vp]),

@@ -699,7 +699,12 @@ __global__ __launch_bounds__(256) void attn_valu_f32_kernel(
 // Measured at one GRPO group's shape (8 x 1023 positions, 16 / 4 heads, hd
 // 128): 0.87-0.93 ms per layer with f32 FMAs on 32 x 32 LDS tiles, 0.38-0.40
 // ms here.
-template <int HD>
+// LP: bf16 operands (v_mfma_f32_16x16x16bf16_1k, f32 accumulation), the
+// 16-bit precision of the reference's CUDA-path flash attention: each run of
+// four f32 steps e = 0..3 (lane group g: k = 4 g + e) is one bf16 MFMA whose
+// lane group g supplies k = 4 g .. 4 g + 3, the same operands rounded to
+// bf16 (round to nearest even) and the same output layout.
+template <int HD, bool LP>
 __global__ __launch_bounds__(256, 2) void attn_f32_mfma_kernel(
     const float* __restrict__ q, const float* __restrict__ kc, const float* __restrict__ vc,
     const int32_t* __restrict__ pos0, int pos_off, float* __restrict__ out,
@@ -725,6 +730,11 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma_kernel(
 #pragma unroll
     for (int c = 0; c < NC; ++c) qf[c] = *reinterpret_cast<const f4*>(qr + 16 * c);
   }
+  bf16x4_t qb[NC];  // LP: the query fragments as bf16, formed once
+  if constexpr (LP) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) qb[c] = to_bf16x4(qf[c]);
+  }
   float m = -INFINITY, l = 0.f;
   f4 o[DB];
 #pragma unroll
@@ -749,9 +759,13 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma_kernel(
 #pragma unroll
       for (int c = 0; c < NC; ++c) {
         const f4 kv = *reinterpret_cast<const f4*>(Ks + (b * 16 + j) * RS + 16 * c + 4 * g);
+        if constexpr (LP) {
+          st[b] = mfma_bf16_16x16x16(to_bf16x4(kv), qb[c], st[b]);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
-          st[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qf[c][e], st[b], 0, 0, 0);
+          for (int e = 0; e < 4; ++e)
+            st[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kv[e], qf[c][e], st[b], 0, 0, 0);
+        }
       }
     }
     float mx = -INFINITY;
@@ -781,15 +795,29 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma_kernel(
     sum += __shfl_xor(sum, 32, kWave);
     l = l * alpha + sum;
     m = mnew;
+    if constexpr (LP) {
+      const bf16x4_t pb[2] = {to_bf16x4(st[0]), to_bf16x4(st[1])};
 #pragma unroll
-    for (int d = 0; d < DB; ++d) {
-      o[d] *= alpha;
+      for (int d = 0; d < DB; ++d) {
+        o[d] *= alpha;
 #pragma unroll
-      for (int b = 0; b < 2; ++b)
+        for (int b = 0; b < 2; ++b) {
+          const float* vp = Vs + (b * 16 + 4 * g) * RS + d * 16 + j;
+          const f4 va = f4{vp[0], vp[RS], vp[2 * RS], vp[3 * RS]};
+          o[d] = mfma_bf16_16x16x16(to_bf16x4(va), pb[b], o[d]);
+        }
+      }
+    } else {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(Vs[(b * 16 + 4 * g + r) * RS + d * 16 + j],
-                                                      st[b][r], o[d], 0, 0, 0);
+      for (int d = 0; d < DB; ++d) {
+        o[d] *= alpha;
+#pragma unroll
+        for (int b = 0; b < 2; ++b)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                Vs[(b * 16 + 4 * g + r) * RS + d * 16 + j], st[b][r], o[d], 0, 0, 0);
+      }
     }
   }
   if (!rin) return;
@@ -805,10 +833,12 @@ __global__ __launch_bounds__(256, 2) void attn_f32_mfma_kernel(
   if (lse && g == 0) lse[((size_t)s * H + h) * L + row] = m + logf(l);
 }
 
+// bf16_ops: the matrix-core path (L >= 32, hd 64 or 128) with bf16 operands;
+// shorter rows keep the f32 VALU kernel.
 int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_t* pos0,
                   int pos_off, float* out, float* lse, int S, int L, int H, int KVH, int cap,
                   int hd, hipStream_t st, const AttnStrides* qs_in = nullptr,
-                  const AttnStrides* os_in = nullptr, bool causal = true) {
+                  const AttnStrides* os_in = nullptr, bool causal = true, bool bf16_ops = false) {
   const int64_t n = (int64_t)S * L * H;  // queries, one wave each
   if (n == 0) return SM_OK;
   if ((reinterpret_cast<uintptr_t>(q) | reinterpret_cast<uintptr_t>(kc) |
@@ -823,12 +853,17 @@ int attn_valu_f32(const float* q, const float* kc, const float* vc, const int32_
   const int cz = causal ? 1 : 0;
   if (L >= 32 && ceil_div(L, 64) <= 65535 && (hd == 64 || hd == 128)) {  // many queries
     const dim3 grid((unsigned)((int64_t)S * H), (unsigned)ceil_div(L, 64));
-    if (hd == 64)
-      attn_f32_mfma_kernel<64><<<grid, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L,
-                                                     H, KVH, cap, scale, qs, os, cz);
-    else
-      attn_f32_mfma_kernel<128><<<grid, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L,
-                                                      H, KVH, cap, scale, qs, os, cz);
+#define SM_AF(HD, LP)                                                                       \
+  attn_f32_mfma_kernel<HD, LP><<<grid, 256, 0, st>>>(q, kc, vc, pos0, pos_off, out, lse, S, L, \
+                                                     H, KVH, cap, scale, qs, os, cz)
+    if (hd == 64) {
+      if (bf16_ops) SM_AF(64, true);
+      else SM_AF(64, false);
+    } else {
+      if (bf16_ops) SM_AF(128, true);
+      else SM_AF(128, false);
+    }
+#undef SM_AF
     SM_LAUNCH_CHECK();
     return SM_OK;
   }
@@ -1070,6 +1105,23 @@ extern "C" int sm_attn_prefill_lse(const void* q, const void* kcache, const void
   return attn_prefill_16((const uint16_t*)q, (const uint16_t*)kcache, (const uint16_t*)vcache,
                          pos0, out, lse, dtype == SM_F16, om, (int)S, (int)L, (int)H, (int)KVH,
                          (int)cap, (int)head_dim, st);
+}
+
+extern "C" int sm_attn_prefill_lse_bf16ops(const float* q, const float* kcache,
+                                           const float* vcache, const int32_t* pos0, float* out,
+                                           float* lse, int64_t S, int64_t L, int64_t H,
+                                           int64_t KVH, int64_t cap, int64_t head_dim,
+                                           void* stream) {
+  using namespace sm;
+  SM_REQUIRE(q && kcache && vcache && pos0 && out, "sm_attn_prefill_lse_bf16ops: null buffer");
+  SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && H % KVH == 0,
+             "sm_attn_prefill_lse_bf16ops: bad shape");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128,
+             "sm_attn_prefill_lse_bf16ops: head_dim must be 64 or 128");
+  SM_REQUIRE(cap > 0 && cap <= (1 << 24), "sm_attn_prefill_lse_bf16ops: bad cache capacity");
+  if (S == 0 || L == 0) return SM_OK;
+  return attn_valu_f32(q, kcache, vcache, pos0, 0, out, lse, (int)S, (int)L, (int)H, (int)KVH,
+                       (int)cap, (int)head_dim, as_stream(stream), nullptr, nullptr, true, true);
 }
 
 extern "C" int sm_attention(const void* q, const void* k, const void* v, int dtype, int64_t B,

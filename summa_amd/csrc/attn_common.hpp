@@ -10,6 +10,17 @@ namespace sm {
 typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Four f32 values rounded to bf16 (nearest even), as the 16-bit lanes the
+// k = 16 bf16 MFMA takes (lane group g supplies k = 4 g .. 4 g + 3).
+typedef short bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16v4_t __attribute__((ext_vector_type(4)));
+__device__ inline bf16x4_t to_bf16x4(f4 v) {
+  return __builtin_bit_cast(bf16x4_t, __builtin_convertvector(v, bf16v4_t));
+}
+__device__ inline f4 mfma_bf16_16x16x16(bf16x4_t a, bf16x4_t b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
 // 8 x 16-bit operand for the score MFMA: raw bits of q / K, typed per cache dtype.
 template <bool KF16> struct Op8;
 template <> struct Op8<false> {

@@ -46,6 +46,12 @@ int sm_rmsnorm_backward(const float*, const float*, const float*, int64_t, int64
 int sm_attn_backward_f32(const float*, const float*, const float*, const float*, const float*,
                          const float*, int64_t, int64_t, int64_t, int64_t, int64_t, float*, float*,
                          float*, float*, void*);
+int sm_attn_prefill_lse_bf16ops(const float*, const float*, const float*, const int32_t*, float*,
+                                float*, int64_t, int64_t, int64_t, int64_t, int64_t, int64_t,
+                                void*);
+int sm_attn_backward_bf16ops(const float*, const float*, const float*, const float*, const float*,
+                             const float*, int64_t, int64_t, int64_t, int64_t, int64_t, float*,
+                             float*, float*, float*, void*);
 int sm_embed_backward(const int32_t*, const float*, int64_t, int64_t, int64_t, float*, void*);
 int sm_adamw_step(float*, const float*, float*, float*, int64_t, float, float, float, float, float,
                   int64_t, void*);
@@ -220,12 +226,22 @@ __global__ __launch_bounds__(256) void sumsq_kernel(const float* __restrict__ a,
     part[blockIdx.x] = t;
   }
 }
-// acc[0] = sum of part[0..n) in order (deterministic)
-__global__ void sum_parts_kernel(const double* __restrict__ part, int64_t n,
-                                 double* __restrict__ acc) {
+// acc[0] = sum of part[0..n): one workgroup, thread t adding parts t, t + 256,
+// ... in order, then the 256 sums in a fixed tree (deterministic). A single
+// thread adding the parts one after another took 1.4 ms at config[2]'s
+// 21k parts.
+__global__ __launch_bounds__(256) void sum_parts_kernel(const double* __restrict__ part,
+                                                        int64_t n, double* __restrict__ acc) {
+  __shared__ double sh[256];
   double t = 0.0;
-  for (int64_t i = 0; i < n; ++i) t += part[i];
-  acc[0] = t;
+  for (int64_t i = threadIdx.x; i < n; i += 256) t += part[i];
+  sh[threadIdx.x] = t;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if ((int)threadIdx.x < w) sh[threadIdx.x] += sh[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) acc[0] = sh[0];
 }
 // g *= max_norm / norm when the norm (sqrt(acc[0])) exceeds max_norm > 0
 __global__ void clip_scale_kernel(float* __restrict__ g, int64_t n, const double* __restrict__ acc,
@@ -682,8 +698,13 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
     SM_TRY(sm_rope_qk(s.qkv, p->rope, pos0, S, L, H, KVH, hd, 0, stream));
     split_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(s.qkv, (int)S, (int)L, (int)H, (int)KVH,
                                                      (int)hd, s.q, s.k, s.v);
-    SM_TRY(sm_attn_prefill_lse(s.q, s.k, s.v, pos0, s.o, s.lse, SM_F32, SM_F32, S, L, H, KVH, L,
-                               hd, stream));
+    // one plane (bf16 matmul operands): attention on bf16 operands as well
+    if (p->planes == 1)
+      SM_TRY(sm_attn_prefill_lse_bf16ops(s.q, s.k, s.v, pos0, s.o, s.lse, S, L, H, KVH, L, hd,
+                                         stream));
+    else
+      SM_TRY(sm_attn_prefill_lse(s.q, s.k, s.v, pos0, s.o, s.lse, SM_F32, SM_F32, S, L, H, KVH,
+                                 L, hd, stream));
     SM_HIP(hipMemcpyAsync(s.x1, s.x0, (size_t)M * d * 4, hipMemcpyDeviceToDevice, st));
     SM_TRY(wgemm(0, 1, M, d, qdim, 1.f, s.o, qdim, fwl(p, SM_W_O, l), qdim, 1.f, s.x1, d,
                       stream));
@@ -803,8 +824,8 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
                       stream));
     SM_TRY(pgemm(1, 0, d, qdim, M, 1.f, dx, d, s.o, qdim, 1.f, gl(p, SM_W_O, l), qdim,
                       stream));
-    SM_TRY(sm_attn_backward_f32(s.q, s.k, s.v, s.o, dO, s.lse, S, L, H, KVH, hd, dq, dk, dv,
-                                delta, stream));
+    SM_TRY((p->planes == 1 ? sm_attn_backward_bf16ops : sm_attn_backward_f32)(
+        s.q, s.k, s.v, s.o, dO, s.lse, S, L, H, KVH, hd, dq, dk, dv, delta, stream));
     merge_qkv_f32<<<blocks256(M * qn), 256, 0, st>>>(dq, dk, dv, (int)S, (int)L, (int)H,
                                                      (int)KVH, (int)hd, dqkv);
     SM_TRY(sm_rope_qk(dqkv, p->rope, pos0, S, L, H, KVH, hd, 1, stream));
@@ -848,7 +869,7 @@ extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale
     sumsq_kernel<<<(unsigned)nb, 256, 0, st>>>(p->g[k], p->count[k], parts + off);
     off += (int)nb;
   }
-  sum_parts_kernel<<<1, 1, 0, st>>>(parts, nparts, acc);
+  sum_parts_kernel<<<1, 256, 0, st>>>(parts, nparts, acc);
   SM_LAUNCH_CHECK();
   double sumsq = 0.0;
   SM_HIP(hipMemcpyAsync(&sumsq, acc, 8, hipMemcpyDeviceToHost, st));

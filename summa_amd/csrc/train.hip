@@ -285,7 +285,14 @@ __device__ inline void stage_rows(float* __restrict__ dst, int valid, Src src) {
 // dK += dS^T Q. dQ pass: Q and dO rows in registers; per key block S = Q K^T,
 // dP = dO V^T, dS to LDS, dQ += dS K. One owner per output and a fixed order
 // of additions (deterministic).
-template <int HD>
+// LP: bf16 operands on v_mfma_f32_16x16x16bf16_1k (f32 accumulation), the
+// 16-bit precision of the reference's CUDA-path attention backward
+// (cube_attention.rs:53-95 forms P and dS in bf16). The head-dim contractions
+// take each run of four f32 steps e = 0..3 as one MFMA (lane group g: k =
+// 4 g .. 4 g + 3, the same operands rounded to bf16); the row / key
+// contractions take rows (keys) 16 q + 4 g .. 16 q + 4 g + 3 from lane group g
+// in step q, so the P / dS operand is one 16-byte LDS read.
+template <int HD, bool LP>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_mfma_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -293,7 +300,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_mfma_kernel(
     AttnStrides qs, int causal) {
   constexpr int T = kAB, RS = HD + 4, PS = T + 4, NC = HD / 16, DBW = HD / 32;
   __shared__ __attribute__((aligned(16))) float Qs[T * RS], Gs[T * RS];
-  __shared__ float Ps[T * PS], Ds[T * PS];  // [key][row]
+  __shared__ __attribute__((aligned(16))) float Ps[T * PS], Ds[T * PS];  // [key][row]
   __shared__ float ls_s[T], dl_s[T];
   const int sk = (int)blockIdx.x, s = sk / KVH, kvh = sk % KVH;  // (sequence, KV head)
   const int k0 = (int)blockIdx.y * T;                            // heaviest (first) keys first
@@ -310,6 +317,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_mfma_kernel(
     for (int c = 0; c < NC; ++c) {
       kf[c] = *reinterpret_cast<const f4*>(kr + 16 * c);
       vf[c] = *reinterpret_cast<const f4*>(vr + 16 * c);
+    }
+  }
+  bf16x4_t kb16[LP ? NC : 1], vb16[LP ? NC : 1];  // LP: K and V fragments as bf16
+  if constexpr (LP) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      kb16[c] = to_bf16x4(kf[c]);
+      vb16[c] = to_bf16x4(vf[c]);
     }
   }
   f4 adk[DBW], adv[DBW];
@@ -335,10 +350,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_mfma_kernel(
       for (int c = 0; c < NC; ++c) {
         const f4 qv = *reinterpret_cast<const f4*>(Qs + (rb * 16 + j) * RS + 16 * c + 4 * g);
         const f4 gv = *reinterpret_cast<const f4*>(Gs + (rb * 16 + j) * RS + 16 * c + 4 * g);
+        if constexpr (LP) {
+          st = mfma_bf16_16x16x16(kb16[c], to_bf16x4(qv), st);
+          dpt = mfma_bf16_16x16x16(vb16[c], to_bf16x4(gv), dpt);
+        } else {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[c][e], qv[e], st, 0, 0, 0);
-          dpt = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[c][e], gv[e], dpt, 0, 0, 0);
+          for (int e = 0; e < 4; ++e) {
+            st = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[c][e], qv[e], st, 0, 0, 0);
+            dpt = __builtin_amdgcn_mfma_f32_16x16x4f32(vf[c][e], gv[e], dpt, 0, 0, 0);
+          }
         }
       }
 #pragma unroll
@@ -351,16 +371,35 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_mfma_kernel(
         Ds[kl * PS + rl] = p * (dpt[r] - dl_s[rl]) * scale;
       }
       __syncthreads();
+      if constexpr (LP) {
 #pragma unroll
-      for (int c = 0; c < T / 4; ++c) {  // rows 4c + g
-        const int row = 4 * c + g;
-        const float pa = Ps[(kb * 16 + j) * PS + row];
-        const float da = Ds[(kb * 16 + j) * PS + row];
+        for (int qq = 0; qq < T / 16; ++qq) {  // rows 16 qq + 4 g .. + 3
+          const int row = 16 * qq + 4 * g;
+          const bf16x4_t pa = to_bf16x4(*reinterpret_cast<const f4*>(Ps + (kb * 16 + j) * PS + row));
+          const bf16x4_t da = to_bf16x4(*reinterpret_cast<const f4*>(Ds + (kb * 16 + j) * PS + row));
 #pragma unroll
-        for (int b = 0; b < DBW; ++b) {
-          const int dim = (db0 + b) * 16 + j;
-          adv[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, Gs[row * RS + dim], adv[b], 0, 0, 0);
-          adk[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(da, Qs[row * RS + dim], adk[b], 0, 0, 0);
+          for (int b = 0; b < DBW; ++b) {
+            const int dim = (db0 + b) * 16 + j;
+            const float* gp = Gs + row * RS + dim;
+            const float* qp = Qs + row * RS + dim;
+            adv[b] = mfma_bf16_16x16x16(pa, to_bf16x4(f4{gp[0], gp[RS], gp[2 * RS], gp[3 * RS]}),
+                                        adv[b]);
+            adk[b] = mfma_bf16_16x16x16(da, to_bf16x4(f4{qp[0], qp[RS], qp[2 * RS], qp[3 * RS]}),
+                                        adk[b]);
+          }
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < T / 4; ++c) {  // rows 4c + g
+          const int row = 4 * c + g;
+          const float pa = Ps[(kb * 16 + j) * PS + row];
+          const float da = Ds[(kb * 16 + j) * PS + row];
+#pragma unroll
+          for (int b = 0; b < DBW; ++b) {
+            const int dim = (db0 + b) * 16 + j;
+            adv[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(pa, Gs[row * RS + dim], adv[b], 0, 0, 0);
+            adk[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(da, Qs[row * RS + dim], adk[b], 0, 0, 0);
+          }
         }
       }
     }
@@ -377,7 +416,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dkv_mfma_kernel(
     }
 }
 
-template <int HD>
+template <int HD, bool LP>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ dout, const float* __restrict__ lse, const float* __restrict__ delta,
@@ -385,7 +424,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma_kernel(
     int causal) {
   constexpr int T = kAB, RS = HD + 4, PS = T + 4, NC = HD / 16, DBW = HD / 32;
   __shared__ __attribute__((aligned(16))) float Ks[T * RS], Vs[T * RS];
-  __shared__ float Ds[T * PS];  // [row][key]
+  __shared__ __attribute__((aligned(16))) float Ds[T * PS];  // [row][key]
   const int sh = (int)blockIdx.x, s = sh / H, h = sh % H;
   const int sk = s * KVH + h / (H / KVH);
   const int nqb = (L + T - 1) / T;
@@ -403,6 +442,14 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma_kernel(
     for (int c = 0; c < NC; ++c) {
       qf[c] = *reinterpret_cast<const f4*>(qr + 16 * c);
       gf[c] = *reinterpret_cast<const f4*>(gr + 16 * c);
+    }
+  }
+  bf16x4_t qb16[LP ? NC : 1], gb16[LP ? NC : 1];  // LP: Q and dO fragments as bf16
+  if constexpr (LP) {
+#pragma unroll
+    for (int c = 0; c < NC; ++c) {
+      qb16[c] = to_bf16x4(qf[c]);
+      gb16[c] = to_bf16x4(gf[c]);
     }
   }
   float ls[4], dl[4];  // rows rb*16 + 4g + r of the score block
@@ -430,10 +477,15 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma_kernel(
     for (int c = 0; c < NC; ++c) {
       const f4 kv = *reinterpret_cast<const f4*>(Ks + (kb * 16 + j) * RS + 16 * c + 4 * g);
       const f4 vv = *reinterpret_cast<const f4*>(Vs + (kb * 16 + j) * RS + 16 * c + 4 * g);
+      if constexpr (LP) {
+        sc = mfma_bf16_16x16x16(qb16[c], to_bf16x4(kv), sc);
+        dp = mfma_bf16_16x16x16(gb16[c], to_bf16x4(vv), dp);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[c][e], kv[e], sc, 0, 0, 0);
-        dp = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[c][e], vv[e], dp, 0, 0, 0);
+        for (int e = 0; e < 4; ++e) {
+          sc = __builtin_amdgcn_mfma_f32_16x16x4f32(qf[c][e], kv[e], sc, 0, 0, 0);
+          dp = __builtin_amdgcn_mfma_f32_16x16x4f32(gf[c][e], vv[e], dp, 0, 0, 0);
+        }
       }
     }
 #pragma unroll
@@ -445,14 +497,28 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_mfma_kernel(
       Ds[rl * PS + kl] = p * (dp[r] - dl[r]) * scale;
     }
     __syncthreads();
+    if constexpr (LP) {
 #pragma unroll
-    for (int c = 0; c < T / 4; ++c) {  // keys 4c + g
-      const int key = 4 * c + g;
-      const float a = Ds[(rb * 16 + j) * PS + key];
+      for (int qq = 0; qq < T / 16; ++qq) {  // keys 16 qq + 4 g .. + 3
+        const int key = 16 * qq + 4 * g;
+        const bf16x4_t a = to_bf16x4(*reinterpret_cast<const f4*>(Ds + (rb * 16 + j) * PS + key));
 #pragma unroll
-      for (int b = 0; b < DBW; ++b)
-        adq[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Ks[key * RS + (db0 + b) * 16 + j],
-                                                      adq[b], 0, 0, 0);
+        for (int b = 0; b < DBW; ++b) {
+          const float* kp = Ks + key * RS + (db0 + b) * 16 + j;
+          adq[b] = mfma_bf16_16x16x16(a, to_bf16x4(f4{kp[0], kp[RS], kp[2 * RS], kp[3 * RS]}),
+                                      adq[b]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < T / 4; ++c) {  // keys 4c + g
+        const int key = 4 * c + g;
+        const float a = Ds[(rb * 16 + j) * PS + key];
+#pragma unroll
+        for (int b = 0; b < DBW; ++b)
+          adq[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(a, Ks[key * RS + (db0 + b) * 16 + j],
+                                                        adq[b], 0, 0, 0);
+      }
     }
   }
 #pragma unroll
@@ -656,7 +722,8 @@ namespace {
 int attn_backward_f32(const float* q, const float* k, const float* v, const float* o,
                       const float* dout, const float* lse, int64_t S, int64_t L, int64_t H,
                       int64_t KVH, int64_t head_dim, float* dq, float* dk, float* dv,
-                      float* delta_scratch, const AttnStrides& qs, bool causal, hipStream_t st) {
+                      float* delta_scratch, const AttnStrides& qs, bool causal, hipStream_t st,
+                      bool bf16_ops = false) {
   auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
   SM_REQUIRE(al16(q) && al16(k) && al16(v) && al16(dout) && qs.seq % 4 == 0 && qs.pos % 4 == 0 &&
                  qs.head % 4 == 0,
@@ -668,19 +735,24 @@ int attn_backward_f32(const float* q, const float* k, const float* v, const floa
   const unsigned rows_blocks = (unsigned)ceil_div(S * H * L, 4);
   const dim3 gkv((unsigned)(S * KVH), (unsigned)ceil_div(L, kAB));
   const dim3 gq((unsigned)(S * H), (unsigned)ceil_div(L, kAB));
-#define SM_AB(HD)                                                                              \
+#define SM_AB(HD, LP)                                                                          \
   do {                                                                                         \
     attn_bwd_delta_kernel<HD><<<rows_blocks, 256, 0, st>>>(o, dout, (int)S, (int)L, (int)H, qs, \
                                                            delta_scratch);                     \
-    attn_bwd_dkv_mfma_kernel<HD><<<gkv, 256, 0, st>>>(q, k, v, dout, lse, delta_scratch,      \
-                                                      (int)S, (int)L, (int)H, (int)KVH, scale, \
-                                                      dk, dv, qs, cz);                         \
-    attn_bwd_dq_mfma_kernel<HD><<<gq, 256, 0, st>>>(q, k, v, dout, lse, delta_scratch, (int)S, \
-                                                    (int)L, (int)H, (int)KVH, scale, dq, qs,   \
-                                                    cz);                                       \
+    attn_bwd_dkv_mfma_kernel<HD, LP><<<gkv, 256, 0, st>>>(q, k, v, dout, lse, delta_scratch,  \
+                                                          (int)S, (int)L, (int)H, (int)KVH,    \
+                                                          scale, dk, dv, qs, cz);              \
+    attn_bwd_dq_mfma_kernel<HD, LP><<<gq, 256, 0, st>>>(q, k, v, dout, lse, delta_scratch,    \
+                                                        (int)S, (int)L, (int)H, (int)KVH,      \
+                                                        scale, dq, qs, cz);                    \
   } while (0)
-  if (head_dim == 64) SM_AB(64);
-  else SM_AB(128);
+  if (head_dim == 64) {
+    if (bf16_ops) SM_AB(64, true);
+    else SM_AB(64, false);
+  } else {
+    if (bf16_ops) SM_AB(128, true);
+    else SM_AB(128, false);
+  }
 #undef SM_AB
   SM_LAUNCH_CHECK();
   return SM_OK;
@@ -700,6 +772,23 @@ extern "C" int sm_attn_backward_f32(const float* q, const float* k, const float*
   return attn_backward_f32(q, k, v, o, dout, lse, S, L, H, KVH, head_dim, dq, dk, dv,
                            delta_scratch, AttnStrides::rows(L, H, head_dim), true,
                            as_stream(stream));
+}
+
+extern "C" int sm_attn_backward_bf16ops(const float* q, const float* k, const float* v,
+                                        const float* o, const float* dout, const float* lse,
+                                        int64_t S, int64_t L, int64_t H, int64_t KVH,
+                                        int64_t head_dim, float* dq, float* dk, float* dv,
+                                        float* delta_scratch, void* stream) {
+  SM_REQUIRE(q && k && v && o && dout && lse && dq && dk && dv && delta_scratch,
+             "sm_attn_backward_bf16ops: null buffer");
+  SM_REQUIRE(S >= 0 && L >= 0 && H > 0 && KVH > 0 && H % KVH == 0,
+             "sm_attn_backward_bf16ops: bad shape");
+  SM_REQUIRE(head_dim == 64 || head_dim == 128,
+             "sm_attn_backward_bf16ops: head_dim must be 64 or 128");
+  if (S == 0 || L == 0) return SM_OK;
+  return attn_backward_f32(q, k, v, o, dout, lse, S, L, H, KVH, head_dim, dq, dk, dv,
+                           delta_scratch, AttnStrides::rows(L, H, head_dim), true,
+                           as_stream(stream), true);
 }
 
 extern "C" int sm_attention_backward(const float* q, const float* k, const float* v,

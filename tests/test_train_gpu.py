@@ -298,6 +298,70 @@ def test_attention_backward_matches_autograd(dev, hd, H, KVH, L):
         torch.testing.assert_close(got.cpu().double(), want, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("hd,H,KVH,L", [(64, 4, 2, 21), (128, 8, 2, 100), (64, 4, 1, 70),
+                                        (128, 2, 2, 64), (128, 16, 4, 160)])
+def test_attention_bf16ops_forward_and_backward(dev, hd, H, KVH, L):
+    """sm_attn_prefill_lse_bf16ops / sm_attn_backward_bf16ops (the one-plane
+    policy's attention: bf16 operands, f32 accumulation) against float64
+    autograd: every output within bf16-operand error (relative Frobenius error
+    <= 1e-2, worst element <= 5 % of the largest), and measurably different
+    from the f32 kernels on the same inputs, so the bf16 path is the one that
+    ran; the f32 kernels stay within 1e-5 there. Rows shorter than 32 keep the
+    f32 forward (L 21: bit-equal to sm_attn_prefill_lse)."""
+    print(f"case attention bf16ops hd={hd} H={H} KVH={KVH} L={L}", flush=True)
+    S = 2
+    q = torch.randn(S, L, H, hd, dtype=torch.float64, requires_grad=True)
+    k = torch.randn(S, KVH, L, hd, dtype=torch.float64, requires_grad=True)
+    v = torch.randn(S, KVH, L, hd, dtype=torch.float64, requires_grad=True)
+    o, lse = _attn_t(q, k, v, H, KVH)
+    do = torch.randn_like(o)
+    o.backward(do)
+    qd, kd, vd, dod = (t.detach().float().contiguous().to(dev) for t in (q, k, v, do))
+    pos0 = torch.zeros(S, dtype=torch.int32, device=dev)
+
+    def fwd(name, *dt):
+        out = torch.empty_like(qd)
+        ls = torch.empty(S * H, L, device=dev)
+        call(name, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), pos0.data_ptr(), out.data_ptr(),
+             ls.data_ptr(), *dt, S, L, H, KVH, L, hd, _st())
+        return out, ls
+
+    def bwd(name, od, lsed):
+        dq, dk, dv = torch.empty_like(qd), torch.empty_like(kd), torch.empty_like(vd)
+        delta = torch.empty(S * H * L, device=dev)
+        call(name, qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), od.data_ptr(), dod.data_ptr(),
+             lsed.data_ptr(), S, L, H, KVH, hd, dq.data_ptr(), dk.data_ptr(), dv.data_ptr(),
+             delta.data_ptr(), _st())
+        return dq, dk, dv
+
+    def rel(got, want):
+        got = got.cpu().double().reshape(want.shape)
+        return float((got - want).norm() / want.norm()), float(
+            (got - want).abs().max() / want.abs().max())
+
+    o16, l16 = fwd("sm_attn_prefill_lse_bf16ops")
+    o32, l32 = fwd("sm_attn_prefill_lse", _lib.SM_F32, _lib.SM_F32)
+    if L < 32:
+        assert torch.equal(o16, o32) and torch.equal(l16, l32)
+    else:
+        fr, mx = rel(o16, o.detach())
+        assert fr <= 1e-2 and mx <= 5e-2, (fr, mx)
+        assert rel(o32, o.detach())[0] <= 1e-5
+        assert rel(o16, o32.cpu().double())[0] > 1e-5  # the bf16 operands were used
+    lse_want = lse.detach().reshape(S * H, L)
+    assert float((l16.cpu().double() - lse_want).abs().max()) <= 5e-2
+    # both backwards from the exact forward, so only the backward's operands differ
+    od = o.detach().float().contiguous().to(dev)
+    lsed = lse.detach().float().contiguous().to(dev)
+    g16 = bwd("sm_attn_backward_bf16ops", od, lsed)
+    g32 = bwd("sm_attn_backward_f32", od, lsed)
+    for got, ref, want in zip(g16, g32, (q.grad, k.grad, v.grad)):
+        fr, mx = rel(got, want)
+        assert fr <= 1e-2 and mx <= 5e-2, (fr, mx)
+        assert rel(ref, want)[0] <= 1e-5
+        assert rel(got, ref.cpu().double())[0] > 1e-5
+
+
 CFG = ModelConfig(layers=2, d_model=256, heads=4, kv_heads=2, head_dim=64, ffn=512, vocab=1000,
                   max_seq=32, quantized=False)
 
