@@ -961,8 +961,22 @@ def bench_policy_update(args) -> dict:
                 step.append(e1.elapsed_time(e2))
             log(f"bench: policy update planes={planes} {i}: prepare {e0.elapsed_time(e1):.1f} ms, "
                 f"optimizer step {e1.elapsed_time(e2):.1f} ms")
+        # the same prepare with the frozen model's log-probs given (as the RL
+        # step's recompute returns them), so the update does not run it again
+        ref_lp = out["lp_ref"].clone()
+        prep_g = []
+        for i in range(args.warmup + args.steps):
+            e0.record(st)
+            pol.prepare(None, prompts, tok, beh, rewards, reference_lp=ref_lp)
+            e1.record(st)
+            pol.optimizer_step(1.0)
+            torch.cuda.synchronize()
+            if i >= args.warmup:
+                prep_g.append(e0.elapsed_time(e1))
         by_planes[str(planes)] = {"prepare_ms": round(sum(prep) / len(prep), 2),
-                                  "optimizer_step_ms": round(sum(step) / len(step), 2)}
+                                  "optimizer_step_ms": round(sum(step) / len(step), 2),
+                                  "prepare_given_reference_lp_ms":
+                                      round(sum(prep_g) / len(prep_g), 2)}
     p_ms, s_ms = by_planes["3"]["prepare_ms"], by_planes["3"]["optimizer_step_ms"]
     positions = G * (P + N - 1)
     return {"metric": f"GRPO policy update positions/s (config[{cfg_id}], one group per call)",

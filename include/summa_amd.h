@@ -816,6 +816,12 @@ int sm_rl_prepare(sm_model* policy, sm_model* reference, const int32_t* prompts,
  *   frozen reference's log-probs (sm_rl_logprobs on `reference`), the GRPO
  *   loss (as sm_grpo_loss) and the backward of sum(dlp * lp_cur), added to the
  *   staged gradients. Arguments as sm_rl_prepare.
+ * sm_policy_prepare_with_ref: the same with the frozen reference's log-probs
+ *   given, reference_lp [S, N] f32 over the same tokens (as sm_rl_prepare or
+ *   sm_rl_logprobs returned them for the step's recompute; nullable when
+ *   kl_coefficient is 0), so the update does not run the frozen model again:
+ *   grpo_loss_tensor's reference_token_log_probs input (posttrain.rs:874-1028).
+ *   With the same log-probs the results equal sm_policy_prepare's bit for bit.
  * sm_policy_optimizer_step: clip, optimizer update at lr * scale, staged
  *   gradients cleared; grad_norm (nullable, host) gets the pre-clip norm; a
  *   non-finite norm fails with the reference's message (trainer.rs:1959-1964).
@@ -848,6 +854,13 @@ int sm_policy_prepare(sm_policy* policy, sm_model* reference, const int32_t* pro
                       double clip_epsilon, double advantage_epsilon, double kl_coefficient,
                       float* lp_cur, float* lp_ref, float* group_stats, float* dlp,
                       int32_t* flags, void* stream);
+int sm_policy_prepare_with_ref(sm_policy* policy, const float* reference_lp,
+                               const int32_t* prompts, const int32_t* tokens,
+                               const float* behavior_lp, const float* rewards, const float* mask,
+                               int64_t groups, int64_t group_size, int64_t P, int64_t N,
+                               double clip_epsilon, double advantage_epsilon,
+                               double kl_coefficient, float* lp_cur, float* group_stats,
+                               float* dlp, int32_t* flags, void* stream);
 int sm_policy_optimizer_step(sm_policy* policy, double learning_rate_scale, float* grad_norm,
                              void* stream);
 

@@ -139,6 +139,8 @@ SIGNATURES: dict[str, tuple] = {
     "sm_policy_install": (i32, [vp, vp, vp]),
     "sm_policy_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64,
                                 vp, vp, vp, vp, vp, vp]),
+    "sm_policy_prepare_with_ref": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64,
+                                         f64, vp, vp, vp, vp, vp]),
     "sm_policy_optimizer_step": (i32, [vp, f64, vp, vp]),
     "sm_fill_normal": (i32, [vp, i32, i64, f32, f32, u64, vp]),
     "sm_fill_ce_stress": (i32, [vp, i32, vp, i64, i64, f32, f32, u64, vp]),

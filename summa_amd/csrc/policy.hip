@@ -550,16 +550,19 @@ extern "C" int sm_policy_install(const sm_policy* p, sm_model* model, void* stre
   return SM_OK;
 }
 
-extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_t* prompts,
-                                 const int32_t* tokens, const float* behavior_lp,
-                                 const float* rewards, const float* mask, int64_t groups,
-                                 int64_t group_size, int64_t P, int64_t N, double clip_epsilon,
-                                 double advantage_epsilon, double kl_coefficient, float* lp_cur,
-                                 float* lp_ref, float* group_stats, float* dlp, int32_t* flags,
-                                 void* stream) {
+namespace {
+// sm_policy_prepare's body. The frozen reference's log-probs come from
+// `reference` (computed here into lp_ref) or, with no reference model, from
+// ref_lp_in (computed by the caller over the same tokens).
+int policy_prepare(sm_policy* p, sm_model* reference, const float* ref_lp_in,
+                   const int32_t* prompts, const int32_t* tokens, const float* behavior_lp,
+                   const float* rewards, const float* mask, int64_t groups, int64_t group_size,
+                   int64_t P, int64_t N, double clip_epsilon, double advantage_epsilon,
+                   double kl_coefficient, float* lp_cur, float* lp_ref, float* group_stats,
+                   float* dlp, int32_t* flags, void* stream) {
   SM_REQUIRE(p && prompts && tokens && behavior_lp && rewards && lp_cur && dlp,
              "sm_policy_prepare: null argument");
-  SM_REQUIRE(kl_coefficient == 0.0 || (reference && lp_ref),
+  SM_REQUIRE(kl_coefficient == 0.0 || (reference && lp_ref) || ref_lp_in,
              "GRPO rollout needs reference log-probs for positive KL coefficient");
   SM_REQUIRE(groups > 0 && group_size > 0 && P > 0 && N > 0, "sm_policy_prepare: bad shape");
   const auto& c = p->cfg;
@@ -753,11 +756,14 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   SM_TRY(sm_ce_rows(logits, SM_F32, tokens, R, V, V, lp_cur, nullptr, nullptr, 1.f, nullptr,
                     nullptr, stream));
   // ---- the frozen reference and the loss
-  const bool use_ref = reference && lp_ref;
-  if (use_ref) SM_TRY(sm_rl_logprobs(reference, prompts, tokens, S, P, N, 0, lp_ref, stream));
-  SM_TRY(sm_grpo_loss(rewards, lp_cur, behavior_lp, use_ref ? lp_ref : nullptr, mask, groups,
-                      group_size, N, clip_epsilon, advantage_epsilon, kl_coefficient, group_stats,
-                      nullptr, dlp, flags, stream));
+  const float* ref_lp = ref_lp_in;
+  if (reference && lp_ref) {
+    SM_TRY(sm_rl_logprobs(reference, prompts, tokens, S, P, N, 0, lp_ref, stream));
+    ref_lp = lp_ref;
+  }
+  SM_TRY(sm_grpo_loss(rewards, lp_cur, behavior_lp, ref_lp, mask, groups, group_size, N,
+                      clip_epsilon, advantage_epsilon, kl_coefficient, group_stats, nullptr, dlp,
+                      flags, stream));
   // ---- backward of sum(dlp * lp), gradients added to the staged ones.
   // d lp / d logits = onehot - softmax: the CE gradient with scale -dlp per row
   neg_f32<<<blocks256(R), 256, 0, st>>>(dlp, R, rscale);
@@ -838,6 +844,32 @@ extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_
   SM_LAUNCH_CHECK();
   p->staged = true;
   return SM_OK;
+}
+}  // namespace
+
+extern "C" int sm_policy_prepare(sm_policy* p, sm_model* reference, const int32_t* prompts,
+                                 const int32_t* tokens, const float* behavior_lp,
+                                 const float* rewards, const float* mask, int64_t groups,
+                                 int64_t group_size, int64_t P, int64_t N, double clip_epsilon,
+                                 double advantage_epsilon, double kl_coefficient, float* lp_cur,
+                                 float* lp_ref, float* group_stats, float* dlp, int32_t* flags,
+                                 void* stream) {
+  return policy_prepare(p, reference, nullptr, prompts, tokens, behavior_lp, rewards, mask,
+                        groups, group_size, P, N, clip_epsilon, advantage_epsilon,
+                        kl_coefficient, lp_cur, lp_ref, group_stats, dlp, flags, stream);
+}
+
+extern "C" int sm_policy_prepare_with_ref(sm_policy* p, const float* reference_lp,
+                                          const int32_t* prompts, const int32_t* tokens,
+                                          const float* behavior_lp, const float* rewards,
+                                          const float* mask, int64_t groups, int64_t group_size,
+                                          int64_t P, int64_t N, double clip_epsilon,
+                                          double advantage_epsilon, double kl_coefficient,
+                                          float* lp_cur, float* group_stats, float* dlp,
+                                          int32_t* flags, void* stream) {
+  return policy_prepare(p, nullptr, reference_lp, prompts, tokens, behavior_lp, rewards, mask,
+                        groups, group_size, P, N, clip_epsilon, advantage_epsilon,
+                        kl_coefficient, lp_cur, nullptr, group_stats, dlp, flags, stream);
 }
 
 extern "C" int sm_policy_optimizer_step(sm_policy* p, double learning_rate_scale,

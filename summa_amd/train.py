@@ -333,22 +333,38 @@ class Policy:
         return out
 
     def prepare(self, reference, prompts, tokens, behavior_lp, rewards, mask=None,
-                clip_epsilon=0.2, advantage_epsilon=1e-6, kl_coefficient=0.04):
+                clip_epsilon=0.2, advantage_epsilon=1e-6, kl_coefficient=0.04,
+                reference_lp=None):
         """sm_policy_prepare: like ``model.rl_prepare`` for the trainable
-        policy; the gradient of the loss is added to the staged gradients."""
+        policy; the gradient of the loss is added to the staged gradients.
+        With ``reference`` None and ``reference_lp`` given ([S, N] f32, the
+        frozen model's log-probs over the same tokens, e.g. the step's
+        ``rl_prepare`` output) it runs sm_policy_prepare_with_ref, which does
+        not run the frozen model again."""
         groups, G = rewards.shape
         S, P = prompts.shape
         N = tokens.shape[1]
         dev = prompts.device
         lp_cur = torch.empty(S, N, dtype=torch.float32, device=dev)
-        lp_ref = (torch.empty(S, N, dtype=torch.float32, device=dev)
-                  if reference is not None else None)
         stats = torch.empty(groups, 5, dtype=torch.float32, device=dev)
         dlp = torch.empty(S, N, dtype=torch.float32, device=dev)
         flags = torch.empty(groups, dtype=torch.int32, device=dev)
+        msk = None if mask is None else mask.data_ptr()
+        if reference is None and reference_lp is not None:
+            if reference_lp.shape != (S, N) or reference_lp.dtype != torch.float32:
+                raise ValueError("reference_lp must be float32 [S, N]")
+            ref = reference_lp.contiguous()
+            call("sm_policy_prepare_with_ref", self._h, ref.data_ptr(), prompts.data_ptr(),
+                 tokens.data_ptr(), behavior_lp.data_ptr(), rewards.data_ptr(), msk, groups, G,
+                 P, N, float(clip_epsilon), float(advantage_epsilon), float(kl_coefficient),
+                 lp_cur.data_ptr(), stats.data_ptr(), dlp.data_ptr(), flags.data_ptr(), _st())
+            return {"lp_cur": lp_cur, "lp_ref": ref, "stats": stats, "dlp": dlp,
+                    "flags": flags}
+        lp_ref = (torch.empty(S, N, dtype=torch.float32, device=dev)
+                  if reference is not None else None)
         call("sm_policy_prepare", self._h, reference.handle if reference is not None else None,
              prompts.data_ptr(), tokens.data_ptr(), behavior_lp.data_ptr(), rewards.data_ptr(),
-             None if mask is None else mask.data_ptr(), groups, G, P, N, float(clip_epsilon),
+             msk, groups, G, P, N, float(clip_epsilon),
              float(advantage_epsilon), float(kl_coefficient), lp_cur.data_ptr(),
              None if lp_ref is None else lp_ref.data_ptr(), stats.data_ptr(), dlp.data_ptr(),
              flags.data_ptr(), _st())

@@ -325,6 +325,51 @@ def test_native_grpo_update_lowers_the_loss(dev):
                                atol=1e-5)
 
 
+@pytest.mark.parametrize("planes", [3, 1])
+def test_prepare_with_given_reference_lp_is_bit_exact(dev, planes):
+    """sm_policy_prepare_with_ref (the frozen model's log-probs passed in, as
+    grpo_loss_tensor takes reference_token_log_probs) against sm_policy_prepare
+    with the frozen model, on two policies with the same weights: lp_cur, the
+    group statistics, dlp, the flags and every staged gradient bit for bit,
+    with a positive KL coefficient (the embedding gradient up to the order of its
+    atomic adds); a positive KL coefficient without reference log-probs fails."""
+    print(f"case prepare with given reference lp planes={planes}", flush=True)
+    w = oracle.random_weights(CFG.oracle_cfg(), seed=31, std=0.05)
+    frozen = Model(CFG)
+    frozen.load_host_weights(oracle.random_weights(CFG.oracle_cfg(), seed=32, std=0.05), dev)
+    pa = train.Policy(CFG, w, dev, matmul_planes=planes)
+    pb = train.Policy(CFG, w, dev, matmul_planes=planes)
+    G, B = 8, 2
+    prompts = torch.from_numpy(np.random.default_rng(6).integers(0, CFG.vocab, (B * G, 8))
+                               .astype(np.int32)).to(dev)
+    tok = torch.from_numpy(np.random.default_rng(7).integers(0, CFG.vocab, (B * G, 6))
+                           .astype(np.int32)).to(dev)
+    beh = torch.full(tok.shape, -7.0, device=dev)
+    rewards = torch.from_numpy(np.random.default_rng(8).random((B, G)).astype(np.float32)).to(dev)
+    a = pa.prepare(frozen, prompts, tok, beh, rewards, kl_coefficient=0.04)
+    b = pb.prepare(None, prompts, tok, beh, rewards, kl_coefficient=0.04,
+                   reference_lp=a["lp_ref"].clone())
+    for k in ("lp_cur", "stats", "dlp", "flags"):
+        assert torch.equal(a[k], b[k]), k
+    assert float(a["stats"][:, 3].abs().sum()) > 0  # the KL term took part
+    for k in train.LAYER_KEYS:
+        for layer in range(CFG.layers):
+            assert torch.equal(pa.tensor(k, layer, gradient=True),
+                               pb.tensor(k, layer, gradient=True)), (k, layer)
+    for k in ("lm_head", "final_norm"):
+        assert torch.equal(pa.tensor(k, gradient=True), pb.tensor(k, gradient=True)), k
+    # the embedding gradient is a scatter of atomic f32 adds (sm_embed_backward):
+    # repeated ids add in run-dependent order, so it is equal up to f32 rounding
+    torch.testing.assert_close(pa.tensor("embed", gradient=True),
+                               pb.tensor("embed", gradient=True), rtol=1e-5, atol=1e-8)
+    with pytest.raises(_lib.SummaError, match="reference log-probs"):
+        _lib.call("sm_policy_prepare_with_ref", pb._h, None, prompts.data_ptr(),
+                  tok.data_ptr(), beh.data_ptr(), rewards.data_ptr(), None, B, G, 8, 6, 0.2,
+                  1e-6, 0.04, a["lp_cur"].data_ptr(), a["stats"].data_ptr(),
+                  a["dlp"].data_ptr(), a["flags"].data_ptr(),
+                  torch.cuda.current_stream().cuda_stream)
+
+
 def test_quantized_policy_recompute_equals_rollout_model(dev):
     """A quantized config trains f32 masters with fake-quantized forward
     weights: its recompute equals the installed Q4 model's log-probs (2e-3,
