@@ -738,6 +738,8 @@ def bench_rl_step(args) -> dict:
     for k in ("steps", "warmup", "rollout_tok_s"):
         leg.pop(k)
     line.update(leg)
+    if args.leg_only:  # the chosen config's RL step alone (per-config kernel profiles)
+        return line
     # the other quantized configs' RL steps (a few steps each: they run the
     # same kernels at other shapes)
     for idx in (1, 2, 4):
@@ -1133,6 +1135,9 @@ def main() -> int:
     p.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 4],
                    help="rl_step: BASELINE config index (2 = the headline line)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--leg-only", action="store_true",
+                   help="rl_step: only the --config leg (no other configs, dominant-kernel, "
+                        "GEMV, CE or CPU legs), for per-config kernel profiles")
     args = p.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the RL step is "
