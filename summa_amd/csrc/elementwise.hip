@@ -177,15 +177,46 @@ __global__ __launch_bounds__(kSampleThreads) void sample_kernel(const float* __r
   // rng_key(seed, r, c) = mix64(row_key ^ c * K2): the per-row half is hoisted.
   const uint64_t row_key = mix64(seed + 0x9e3779b97f4a7c15ull * ((uint64_t)r + 1));
   const uint64_t cbase = (uint64_t)step * (uint64_t)vocab;
-  for (int v = threadIdx.x; v < vocab; v += kSampleThreads) {
-    const float x = row[v];
+  constexpr uint64_t kK2 = 0xd1b54a32d192ed03ull;
+  // hc = (cbase + v) * K2 (mod 2^64), the counter half of rng_key
+  auto visit_h = [&](float x, int v, uint64_t hc) {
     if (x > m) { s = s * __expf(m - x) + 1.f; m = x; } else { s += __expf(x - m); }
     float key = x;
     if (inv_temp > 0.f) {
-      const float u = u01(mix64(row_key ^ ((cbase + (uint64_t)v) * 0xd1b54a32d192ed03ull)));
+      const float u = u01(mix64(row_key ^ hc));
       key = x * inv_temp - logf(-logf(u));
     }
     if (key > best) { best = key; bidx = v; }  // v increases per thread: first max kept
+  };
+  auto visit = [&](float x, int v) { visit_h(x, v, (cbase + (uint64_t)v) * kK2); };
+  // four consecutive elements: one 64-bit multiply for the first counter, the
+  // next three K2 apart (the same values mod 2^64; the hash is VALU-bound on
+  // its 64-bit multiplies)
+  auto visit4 = [&](const float4& a, int v) {
+    const uint64_t h0 = (cbase + (uint64_t)v) * kK2;
+    visit_h(a.x, v, h0);
+    visit_h(a.y, v + 1, h0 + kK2);
+    visit_h(a.z, v + 2, h0 + 2 * kK2);
+    visit_h(a.w, v + 3, h0 + 3 * kK2);
+  };
+  if (vocab % 4 == 0 && ld % 4 == 0 && reinterpret_cast<uintptr_t>(logits) % 16 == 0) {
+    // 16-byte loads, four of them in flight per thread: thread t takes float4s
+    // t, t + T, t + 2T, ... (T threads), so its elements still come in
+    // increasing order. One element per load left the row's 256 KB waiting on
+    // one load per thread at a time (40 us at config[2]'s 256 x 65536).
+    const float4* row4 = reinterpret_cast<const float4*>(row);
+    const int n4 = vocab / 4;
+    int i = threadIdx.x;
+    for (; i + 3 * kSampleThreads < n4; i += 4 * kSampleThreads) {
+      float4 a[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) a[u] = row4[i + u * kSampleThreads];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) visit4(a[u], 4 * (i + u * kSampleThreads));
+    }
+    for (; i < n4; i += kSampleThreads) visit4(row4[i], 4 * i);
+  } else {
+    for (int v = threadIdx.x; v < vocab; v += kSampleThreads) visit(row[v], v);
   }
   // wave reduce (max with lowest index on ties)
 #pragma unroll
