@@ -504,16 +504,16 @@ def cpu_recompute_leg(wl, host) -> dict:
             "rows_extrapolated": {"layer_rows": layer_rows, "head_rows": head_rows}}
 
 
-def cpu_baseline_rl(wl, host_weights, c0=None, ce=None) -> dict:
-    """The C oracle (the reference CPU path restated: fp32, batch 1 per
-    rollout, generate.rs:68-124) on the GPU box's host cores, on a bounded
-    sample of the workload: one rollout, a 64-token prompt prefilled untimed,
-    then cached decode steps (rollout tok/s = 1 / time per step, the rate of
-    the reference's per-rollout loop); warm-up, then the median of 5 reps, at
-    1 thread and at every core. Plus the log-prob recompute at the config's
-    real context (cpu_recompute_leg), the GRPO loss over the full [S, N]
-    arrays, config[3]'s CE on a row sample (cpu_ce_leg) and config[0]'s full
-    RL step with its oracle parity verdict."""
+def cpu_rl_leg(wl, host_weights) -> dict:
+    """One config's RL step on the C oracle (the reference CPU path restated:
+    fp32, batch 1 per rollout, generate.rs:68-124) on the GPU box's host
+    cores, on a bounded sample: one rollout, a 64-token prompt prefilled
+    untimed, then cached decode steps (rollout tok/s = 1 / time per step, the
+    rate of the reference's per-rollout loop); warm-up, then the median of 5
+    reps, at 1 thread and at every core. Plus the log-prob recompute at the
+    config's real context (cpu_recompute_leg), the GRPO loss over the full
+    [S, N] arrays, and the RL step extrapolated from those (S * N tokens at
+    the all-core rollout rate, the recompute, the loss)."""
     import numpy as np
 
     import oracle
@@ -537,7 +537,7 @@ def cpu_baseline_rl(wl, host_weights, c0=None, ce=None) -> dict:
         out[label] = {"threads": n, "s_per_token": round(med, 4),
                       "rollout_tok_s": round(1.0 / med, 4)}
     oracle.set_threads(0)
-    log("bench: cpu recompute sample")
+    log(f"bench: cpu recompute sample (config[{wl.index}])")
     out["recompute"] = cpu_recompute_leg(wl, host)
     del host
     # GRPO loss over the whole batch's [S, N] arrays (f64 oracle)
@@ -550,20 +550,41 @@ def cpu_baseline_rl(wl, host_weights, c0=None, ce=None) -> dict:
         oracle.grpo_loss(rng.random(sh[:2]), cur, beh, cur, None, CLIP_EPSILON,
                          ADVANTAGE_EPSILON, KL_COEFFICIENT)
     out["grpo_loss_ms"] = round((time.perf_counter() - t0) / 5 * 1e3, 3)
+    rollout_s = wl.rollouts * wl.new_tokens / out["all_threads"]["rollout_tok_s"]
+    out["rl_step_s_extrapolated"] = round(
+        rollout_s + out["recompute"]["rl_step_recompute_s_extrapolated"]
+        + out["grpo_loss_ms"] / 1e3, 1)
+    out["sample"] = (f"config[{wl.index}] model, 1 rollout: 64-token prompt prefilled untimed, "
+                     f"then median of 5 reps of cached decode steps (1 thread: 1 step per rep, "
+                     f"all threads: 2); recompute: {CPU_RECOMPUTE_ROWS} rows at the end of a "
+                     f"{wl.prompt_len + wl.new_tokens - 1}-position context; GRPO loss over the "
+                     f"full {list(sh)} arrays; RL step = {wl.rollouts} x {wl.new_tokens} tokens "
+                     f"at the all-core rate + recompute + loss")
+    return out
+
+
+def cpu_baseline_rl(wl, host_weights, c0=None, ce=None, others=None) -> dict:
+    """The C oracle on the host cores (cpu_rl_leg) for the line's config, then
+    config[3]'s CE on a row sample (cpu_ce_leg), config[0]'s full RL step with
+    its oracle parity verdict, and cpu_rl_leg for the other configs whose
+    weights the line kept (``others``: config index -> device weights)."""
+    out = cpu_rl_leg(wl, host_weights)
+    sample = out.pop("sample")
     res = {"value": out["all_threads"]["rollout_tok_s"], "unit": "rollout tok/s",
            "cores": out["all_threads"]["threads"], "kind": "port",
-           "sample": (f"config[{wl.index}] Q4 model, 1 rollout: 64-token prompt prefilled "
-                      f"untimed, then median of 5 reps of cached decode steps (1 thread: 1 "
-                      f"step per rep, all threads: 2); recompute: {CPU_RECOMPUTE_ROWS} rows at "
-                      f"the end of a {wl.prompt_len + wl.new_tokens - 1}-position context; "
-                      f"GRPO loss over the full {list(sh)} arrays; config[3] CE over "
-                      f"{CPU_CE_ROWS} of its rows"),
+           "sample": sample + f"; config[3] CE over {CPU_CE_ROWS} of its rows",
            "cpu_model": _cpu_model(), "nproc": os.cpu_count(), **out}
     if ce is not None:
         log("bench: cpu CE sample (config[3])")
         res["ce_config3"] = cpu_ce_leg(*ce)
     if c0 is not None:
         res["config0"] = c0
+    from summa_amd.configs import RL_WORKLOADS
+    for idx, dw in (others or {}).items():
+        log(f"bench: cpu baseline config[{idx}]")
+        host_w = _model_host_weights(dw)
+        res[f"config{idx}"] = cpu_rl_leg(RL_WORKLOADS[idx], host_w)
+        del host_w
     return res
 
 
@@ -742,12 +763,14 @@ def bench_rl_step(args) -> dict:
         return line
     # the other quantized configs' RL steps (a few steps each: they run the
     # same kernels at other shapes)
+    others = {}
     for idx in (1, 2, 4):
         if idx == args.config or args.config == 0:
             continue
         log(f"bench: config[{idx}]")
         sub = rl_step_leg(RL_WORKLOADS[idx], dev, steps=3, warmup=1, seed=idx)
-        for k in ("_value", "_f_ms", "_weights"):
+        others[idx] = sub.pop("_weights")  # for its CPU baseline leg
+        for k in ("_value", "_f_ms"):
             sub.pop(k)
         line[f"config{idx}"] = sub
     log("bench: dominant kernel (recompute FFN-in GEMM)")
@@ -769,7 +792,7 @@ def bench_rl_step(args) -> dict:
     log("bench: config[0]")
     c0 = config0_leg(dev)
     line["config0"] = {k: v for k, v in c0.items() if not k.startswith("_")}
-    line["_cpu"] = (dweights, c0, ce_sample, ce)
+    line["_cpu"] = (dweights, c0, ce_sample, ce, others)
     return line
 
 
@@ -1156,11 +1179,11 @@ def main() -> int:
     if not args.no_cpu_baseline and cpu is not None:
         log("bench: cpu baseline (oracle on the host cores)")
         from summa_amd.configs import RL_WORKLOADS
-        dweights, c0, ce_sample, ce = cpu
+        dweights, c0, ce_sample, ce, others = cpu
         host_w = _model_host_weights(dweights)
         del dweights
         out["cpu_baseline"] = cpu_baseline_rl(RL_WORKLOADS[args.config], host_w, cpu_config0(c0),
-                                              (ce_sample, ce))
+                                              (ce_sample, ce), others)
     print(json.dumps(out), flush=True)
     return 0
 
