@@ -969,7 +969,7 @@ def bench_policy_update(args) -> dict:
     by_planes, lp_gap = {}, None
     # the f32-grade three-plane GEMMs (the headline), then 16-bit and bf16
     # operands (the reference's CUDA-path matmul precision)
-    for planes in (3, 2, 1):
+    for planes in ((args.planes,) if args.planes else (3, 2, 1)):
         pol.set_matmul_planes(planes)
         prep, step = [], []
         for i in range(args.warmup + args.steps):
@@ -1002,12 +1002,13 @@ def bench_policy_update(args) -> dict:
                                   "optimizer_step_ms": round(sum(step) / len(step), 2),
                                   "prepare_given_reference_lp_ms":
                                       round(sum(prep_g) / len(prep_g), 2)}
-    p_ms, s_ms = by_planes["3"]["prepare_ms"], by_planes["3"]["optimizer_step_ms"]
+    head = str(args.planes or 3)
+    p_ms, s_ms = by_planes[head]["prepare_ms"], by_planes[head]["optimizer_step_ms"]
     positions = G * (P + N - 1)
     return {"metric": f"GRPO policy update positions/s (config[{cfg_id}], one group per call)",
             "value": positions / ((p_ms + s_ms) / 1e3), "unit": "positions/s",
             "ms_per_step": p_ms + s_ms,
-            "dtype": "f32 masters, Q4G128 fake-quantized forward, three-plane bf16 GEMMs",
+            "dtype": (f"f32 masters, Q4G128 fake-quantized forward, {head}-plane bf16 GEMMs"),
             "config": {"workload": f"policy_update config[{cfg_id}]", "rollouts": G,
                        "prompt_len": P, "new_tokens": N},
             "prepare_ms": round(p_ms, 2), "optimizer_step_ms": round(s_ms, 2),
@@ -1158,6 +1159,8 @@ def main() -> int:
     p.add_argument("--config", type=int, default=2, choices=[0, 1, 2, 4],
                    help="rl_step: BASELINE config index (2 = the headline line)")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--planes", type=int, default=0, choices=[0, 1, 2, 3],
+                   help="policy_update: only this matmul plane count (0: 3, 2 and 1)")
     p.add_argument("--leg-only", action="store_true",
                    help="rl_step: only the --config leg (no other configs, dominant-kernel, "
                         "GEMV, CE or CPU legs), for per-config kernel profiles")
