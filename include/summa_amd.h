@@ -516,6 +516,51 @@ int sm_swiglu_backward(const void* gate_value, const void* grad, int dtype, int6
                        int64_t F, void* grad_gate_value, void* stream);
 
 /* ------------------------------------------------------------------------
+ * Float-weight grouped expert projections and the route permutation at the
+ * reference's dispatch seam (GroupedLinearBackend, grouped_linear.rs:23-60;
+ * RowPermutationBackend, row_permute.rs:33-41). All f32, f32-grade products
+ * (sm_gemm_ex per expert with rows, in expert order; no allocation).
+ * counts: HOST array [experts] of the rows per expert, as
+ *   grouped_linear_inner takes them (Vec<usize>); they must sum to routes.
+ * sm_row_permute: out[i] = input[order[i]] over rows of `cols` elements
+ *   (row_permute_inner; its backward is the same call with the inverse
+ *   permutation); order entries outside [0, rows) give zero rows; out must
+ *   not alias input. dtype SM_F32, SM_BF16 or SM_F16 (bits copied).
+ * sm_grouped_linear: out [routes, d_out] = input [routes, d_in] rows of expert
+ *   e (counts[e] consecutive rows, experts in order) times weight[e]
+ *   ([E, d_in, d_out] row-major) (grouped_linear_inner).
+ * sm_grouped_linear_backward: grad_input = grad W_e^T and grad_weight[e] =
+ *   input_e^T grad_e, zero for an expert without rows; either output
+ *   nullable (grouped_linear_backward, grouped_linear.rs:30-37, 524-570).
+ * sm_grouped_swiglu_mlp: projected [routes, 2I] = grouped_linear(input,
+ *   in_weight [E, d, 2I]) as [gate | value], hidden [routes, I] =
+ *   silu(gate) * value, out [routes, d_out] = grouped_linear(hidden,
+ *   down_weight [E, I, d_out]) (grouped_swiglu_mlp_inner, :779-799).
+ * sm_grouped_swiglu_mlp_backward: grad_input, grad_in_weight,
+ *   grad_down_weight from the forward's projected and hidden
+ *   (grouped_swiglu_mlp_backward, :801-826); scratch: routes * 3 * I floats. */
+int sm_row_permute(const void* input, int dtype, int64_t rows, int64_t cols,
+                   const int32_t* order, void* out, void* stream);
+int sm_grouped_linear(const float* input, const float* weight, const int64_t* counts,
+                      int64_t experts, int64_t routes, int64_t d_in, int64_t d_out, float* out,
+                      void* stream);
+int sm_grouped_linear_backward(const float* input, const float* weight, const float* grad,
+                               const int64_t* counts, int64_t experts, int64_t routes,
+                               int64_t d_in, int64_t d_out, float* grad_input,
+                               float* grad_weight, void* stream);
+int sm_grouped_swiglu_mlp(const float* input, const float* in_weight, const float* down_weight,
+                          const int64_t* counts, int64_t experts, int64_t routes, int64_t d,
+                          int64_t intermediate, int64_t d_out, float* out, float* projected,
+                          float* hidden, void* stream);
+int sm_grouped_swiglu_mlp_backward(const float* input, const float* in_weight,
+                                   const float* down_weight, const int64_t* counts,
+                                   int64_t experts, int64_t routes, int64_t d,
+                                   int64_t intermediate, int64_t d_out, const float* projected,
+                                   const float* hidden, const float* grad, float* grad_input,
+                                   float* grad_in_weight, float* grad_down_weight,
+                                   float* scratch, void* stream);
+
+/* ------------------------------------------------------------------------
  * Policy-update kernels (backward of the recompute and the optimizer step:
  * prepare_device_batch autodiff + optimizer_step, posttrain.rs:1288-1305,
  * trainer.rs:1974-1975), f32 with f32 accumulation.

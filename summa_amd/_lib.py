@@ -131,6 +131,12 @@ SIGNATURES: dict[str, tuple] = {
     "sm_rl_logprobs": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
     "sm_rl_prepare": (i32, [vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, f64, f64, f64, i64,
                             vp, vp, vp, vp, vp, vp]),
+    "sm_row_permute": (i32, [vp, i32, i64, i64, vp, vp, vp]),
+    "sm_grouped_linear": (i32, [vp, vp, vp, i64, i64, i64, i64, vp, vp]),
+    "sm_grouped_linear_backward": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, vp, vp, vp]),
+    "sm_grouped_swiglu_mlp": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp, vp]),
+    "sm_grouped_swiglu_mlp_backward": (i32, [vp, vp, vp, vp, i64, i64, i64, i64, i64, vp, vp, vp,
+                                             vp, vp, vp, vp, vp]),
     "sm_policy_create": (i32, [vp, vp, vp]),
     "sm_policy_destroy": (i32, [vp]),
     "sm_policy_set_matmul_planes": (i32, [vp, i32]),
