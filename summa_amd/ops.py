@@ -583,6 +583,114 @@ def swiglu_backward(gate_value: torch.Tensor, grad: torch.Tensor) -> torch.Tenso
     return out
 
 
+# ------------------------------------- float-weight grouped experts, permute --
+
+def _host_counts(counts, experts: int, routes: int):
+    import numpy as np
+    c = np.ascontiguousarray([int(x) for x in counts], dtype=np.int64)
+    if c.shape != (experts,):
+        raise ValueError("one route count is required per expert")
+    if int(c.sum()) != routes:
+        raise ValueError("route counts must cover the input")
+    return c
+
+
+def _f32_dev(t: torch.Tensor, name: str) -> torch.Tensor:
+    _dev(t, name)
+    if t.dtype != torch.float32:
+        raise TypeError(f"{name} must be float32")
+    return t.contiguous()
+
+
+def grouped_linear(input: torch.Tensor, weight: torch.Tensor, counts) -> torch.Tensor:
+    """GroupedLinearBackend::grouped_linear_inner (grouped_linear.rs:23-28,
+    65-86): input [routes, d_in] with counts[e] consecutive rows per expert,
+    weight [E, d_in, d_out] -> [routes, d_out] (sm_grouped_linear)."""
+    x, w = _f32_dev(input, "input"), _f32_dev(weight, "weight")
+    R, din = x.shape
+    E, wdin, dout = w.shape
+    if wdin != din:
+        raise ValueError("grouped linear input width mismatch")
+    c = _host_counts(counts, E, R)
+    out = torch.empty(R, dout, dtype=torch.float32, device=x.device)
+    call("sm_grouped_linear", x.data_ptr(), w.data_ptr(), c.ctypes.data, E, R, din, dout,
+         out.data_ptr(), _stream())
+    return out
+
+
+def grouped_linear_backward(input: torch.Tensor, weight: torch.Tensor, grad: torch.Tensor,
+                            counts) -> tuple:
+    """grouped_linear_backward (grouped_linear.rs:30-37): (grad_input,
+    grad_weight), zero weight gradient for an expert without rows."""
+    x, w, g = _f32_dev(input, "input"), _f32_dev(weight, "weight"), _f32_dev(grad, "grad")
+    R, din = x.shape
+    E, _, dout = w.shape
+    c = _host_counts(counts, E, R)
+    gx, gw = torch.empty_like(x), torch.empty_like(w)
+    call("sm_grouped_linear_backward", x.data_ptr(), w.data_ptr(), g.data_ptr(), c.ctypes.data,
+         E, R, din, dout, gx.data_ptr(), gw.data_ptr(), _stream())
+    return gx, gw
+
+
+def grouped_swiglu_mlp(input: torch.Tensor, in_weight: torch.Tensor, down_weight: torch.Tensor,
+                       counts, intermediate: int) -> tuple:
+    """grouped_swiglu_mlp_inner (grouped_linear.rs:40-49, 779-799):
+    (output [routes, d_out], projected [routes, 2I] as [gate | value],
+    hidden [routes, I])."""
+    x = _f32_dev(input, "input")
+    wi, wd = _f32_dev(in_weight, "in_weight"), _f32_dev(down_weight, "down_weight")
+    R, d = x.shape
+    E, _, two_i = wi.shape
+    if two_i != 2 * intermediate or wd.shape[1] != intermediate or wd.shape[0] != E:
+        raise ValueError("grouped SwiGLU MLP weight shapes do not match the intermediate width")
+    dout = wd.shape[2]
+    c = _host_counts(counts, E, R)
+    out = torch.empty(R, dout, dtype=torch.float32, device=x.device)
+    proj = torch.empty(R, 2 * intermediate, dtype=torch.float32, device=x.device)
+    hid = torch.empty(R, intermediate, dtype=torch.float32, device=x.device)
+    call("sm_grouped_swiglu_mlp", x.data_ptr(), wi.data_ptr(), wd.data_ptr(), c.ctypes.data, E, R,
+         d, intermediate, dout, out.data_ptr(), proj.data_ptr(), hid.data_ptr(), _stream())
+    return out, proj, hid
+
+
+def grouped_swiglu_mlp_backward(input, in_weight, down_weight, counts, projected, hidden, grad,
+                                intermediate: int) -> tuple:
+    """grouped_swiglu_mlp_backward (grouped_linear.rs:50-60, 801-826):
+    (grad_input, grad_in_weight, grad_down_weight)."""
+    x = _f32_dev(input, "input")
+    wi, wd = _f32_dev(in_weight, "in_weight"), _f32_dev(down_weight, "down_weight")
+    p, h, g = _f32_dev(projected, "projected"), _f32_dev(hidden, "hidden"), _f32_dev(grad, "grad")
+    R, d = x.shape
+    E = wi.shape[0]
+    dout = wd.shape[2]
+    c = _host_counts(counts, E, R)
+    gx, gwi, gwd = torch.empty_like(x), torch.empty_like(wi), torch.empty_like(wd)
+    scratch = torch.empty(max(R, 1) * 3 * intermediate, dtype=torch.float32, device=x.device)
+    call("sm_grouped_swiglu_mlp_backward", x.data_ptr(), wi.data_ptr(), wd.data_ptr(),
+         c.ctypes.data, E, R, d, intermediate, dout, p.data_ptr(), h.data_ptr(), g.data_ptr(),
+         gx.data_ptr(), gwi.data_ptr(), gwd.data_ptr(), scratch.data_ptr(), _stream())
+    return gx, gwi, gwd
+
+
+def row_permute(input: torch.Tensor, order: torch.Tensor, inverse: torch.Tensor | None = None
+                ) -> torch.Tensor:
+    """RowPermutationBackend::row_permute_inner (row_permute.rs:33-41):
+    out[i] = input[order[i]] over the rows (bits copied); ``inverse`` is the
+    backward's order (accepted for the trait's signature, unused here)."""
+    _dev(input, "input")
+    _dev(order, "order")
+    dt = {torch.float32: SM_F32, torch.bfloat16: SM_BF16, torch.float16: SM_F16}.get(input.dtype)
+    if dt is None:
+        raise TypeError("input must be float32, bfloat16 or float16")
+    if input.dim() != 2 or order.dtype != torch.int32 or order.shape != (input.shape[0],):
+        raise ValueError("row_permute takes [rows, cols] input and int32 order [rows]")
+    x, o = input.contiguous(), order.contiguous()
+    out = torch.empty_like(x)
+    call("sm_row_permute", x.data_ptr(), dt, x.shape[0], x.shape[1], o.data_ptr(), out.data_ptr(),
+         _stream())
+    return out
+
+
 # ------------------------------------------------------------- attention ---
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,

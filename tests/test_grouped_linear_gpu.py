@@ -179,3 +179,40 @@ def test_grouped_linear_rejects_bad_counts(dev):
         with pytest.raises(_lib.SummaError, match=msg):
             call("sm_grouped_linear", x.data_ptr(), w.data_ptr(), c.ctypes.data, 2, 6, 4, 3,
                  y.data_ptr(), _st())
+
+
+def test_python_mirrors_equal_the_abi_calls(dev):
+    """summa_amd.ops' grouped_linear / _backward, grouped_swiglu_mlp / _backward
+    and row_permute (the reference's function names and argument order) give
+    the C-ABI calls' bits and reject counts that do not cover the input."""
+    from summa_amd import ops
+    counts = [3, 0, 6, 2]
+    E, R, d, I, dout = 4, 11, 32, 24, 16
+    g = torch.Generator(device=dev).manual_seed(5)
+    x = torch.randn(R, d, generator=g, device=dev)
+    w = torch.randn(E, d, dout, generator=g, device=dev) * 0.1
+    grad = torch.randn(R, dout, generator=g, device=dev)
+    c = _counts(counts)
+    y = torch.empty(R, dout, device=dev)
+    call("sm_grouped_linear", x.data_ptr(), w.data_ptr(), c.ctypes.data, E, R, d, dout,
+         y.data_ptr(), _st())
+    assert torch.equal(ops.grouped_linear(x, w, counts), y)
+    gx, gw = ops.grouped_linear_backward(x, w, grad, counts)
+    gx2, gw2 = torch.empty_like(x), torch.empty_like(w)
+    call("sm_grouped_linear_backward", x.data_ptr(), w.data_ptr(), grad.data_ptr(), c.ctypes.data,
+         E, R, d, dout, gx2.data_ptr(), gw2.data_ptr(), _st())
+    assert torch.equal(gx, gx2) and torch.equal(gw, gw2)
+    wi = torch.randn(E, d, 2 * I, generator=g, device=dev) * 0.1
+    wd = torch.randn(E, I, dout, generator=g, device=dev) * 0.1
+    out, proj, hid = ops.grouped_swiglu_mlp(x, wi, wd, counts, I)
+    assert torch.equal(proj, ops.grouped_linear(x, wi, counts))
+    assert torch.equal(hid, ops.swiglu(proj))
+    assert torch.equal(out, ops.grouped_linear(hid, wd, counts))
+    gxm, gwi, gwd = ops.grouped_swiglu_mlp_backward(x, wi, wd, counts, proj, hid, grad, I)
+    gh, gwd2 = ops.grouped_linear_backward(hid, wd, grad, counts)
+    gxm2, gwi2 = ops.grouped_linear_backward(x, wi, ops.swiglu_backward(proj, gh), counts)
+    assert torch.equal(gwd, gwd2) and torch.equal(gxm, gxm2) and torch.equal(gwi, gwi2)
+    order = torch.randperm(R, generator=g, device=dev).to(torch.int32)
+    assert torch.equal(ops.row_permute(x, order), x.index_select(0, order.long()))
+    with pytest.raises(ValueError, match="cover the input"):
+        ops.grouped_linear(x, w, [3, 0, 6, 1])
