@@ -86,14 +86,18 @@ def test_sample_ex_matches_oracle(dev, V, case):
 def test_sample_ex_with_options_off_equals_sample(dev, T):
     from summa_amd._lib import call
     rows, V = 16, 32768
-    logits = torch.randn(rows, V, device=dev) * 3
+    g = torch.Generator(device=dev).manual_seed(11)
+    logits = torch.randn(rows, V, device=dev, generator=g) * 3
     a = torch.empty(rows, dtype=torch.int32, device=dev)
     la = torch.empty(rows, device=dev)
     call("sm_sample", logits.data_ptr(), rows, V, V, T, 5, 9, a.data_ptr(), 1, la.data_ptr(), 1,
          None, torch.cuda.current_stream().cuda_stream)
     b, lb = sampling.sample(logits, SamplingConfig(temperature=T), seed=5, step=9)
     assert torch.equal(a, b)
-    torch.testing.assert_close(la, lb, rtol=0, atol=1e-6)
+    # The two kernels visit a row's elements in different per-thread orders
+    # (sm_sample reads 16-byte groups), so the log-sum-exp behind the log-prob
+    # is rounded differently: a few ulp of |lp| ~ 15 (ulp 9.5e-7).
+    torch.testing.assert_close(la, lb, rtol=0, atol=1e-5)
 
 
 def test_top_k_ties_keep_the_lowest_indices(dev):
