@@ -12,6 +12,17 @@ def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs an MI355X (runs through libsumma_amd.so)")
 
 
+@pytest.fixture(autouse=True)
+def _fixed_global_rng():
+    """Each test starts from the same torch and numpy global generator state, so
+    its unseeded random inputs do not depend on which tests ran before it."""
+    import numpy as np
+    import torch
+
+    torch.manual_seed(1234)
+    np.random.seed(1234)
+
+
 @pytest.fixture(scope="session")
 def dev():
     import torch
