@@ -3,6 +3,7 @@ import ctypes
 import re
 from pathlib import Path
 
+import numpy as np
 import pytest
 
 from summa_amd import _lib
@@ -131,3 +132,34 @@ def test_linear_cross_entropy_host_checks():
     assert st == -1 and L.sm_last_error().decode() == "logical vocabulary 20 must be in 1..=16"
     st = L.sm_linear_cross_entropy(16, 16, None, 16, 4, 8, 16, 16, 2, 0, 16, None, ws, 100, None)
     assert st == -1 and b"workspace holds 100 bytes" in L.sm_last_error()
+
+
+def test_grouped_linear_and_row_permute_host_checks():
+    """The grouped expert projections and the route permutation reject bad
+    arguments before any device work: counts that do not cover the routes or
+    hold a negative entry (grouped_linear_inner takes per-expert row counts,
+    summa-llm/src/model/grouped_linear.rs:23-60), a missing scratch, an
+    unsupported dtype and an output that aliases the input."""
+    import numpy as np
+
+    L = _lib.lib()
+    dummy = 1 << 20  # never dereferenced: each call fails its checks first
+    for counts, msg in (([2, 3], b"cover the input (5 != 6)"),
+                        ([7, -1], b"negative count for expert 1")):
+        c = np.asarray(counts, dtype=np.int64)
+        st = L.sm_grouped_linear(dummy, dummy, c.ctypes.data, 2, 6, 4, 3, dummy, None)
+        assert st == -1 and msg in L.sm_last_error()
+        st = L.sm_grouped_linear_backward(dummy, dummy, dummy, c.ctypes.data, 2, 6, 4, 3, dummy,
+                                          dummy, None)
+        assert st == -1 and msg in L.sm_last_error()
+    st = L.sm_grouped_linear(dummy, dummy, None, 2, 6, 4, 3, dummy, None)
+    assert st == -1 and b"null counts" in L.sm_last_error()
+    c = np.asarray([6, 0], dtype=np.int64)
+    st = L.sm_grouped_swiglu_mlp_backward(dummy, dummy, dummy, c.ctypes.data, 2, 6, 4, 5, 3,
+                                          dummy, dummy, dummy, dummy, dummy, dummy, None, None)
+    assert st == -1 and b"null buffer" in L.sm_last_error()
+    st = L.sm_row_permute(dummy, 7, 4, 8, dummy, dummy + 4096, None)
+    assert st == -1 and b"dtype must be" in L.sm_last_error()
+    st = L.sm_row_permute(dummy, 0, 4, 8, dummy + 64, dummy, None)
+    assert st == -1 and b"must not alias" in L.sm_last_error()
+    assert L.sm_row_permute(dummy, 0, 0, 8, dummy + 64, dummy + 4096, None) == 0
