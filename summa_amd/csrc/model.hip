@@ -575,16 +575,14 @@ int head(sm_model* m, const float* xrows, int64_t M, float* logits, hipStream_t 
   return linear_f32out(m, m->lm_head, m->h.p, M, logits, false, st);
 }
 
-// Prompt groups: S must be whole groups of G and every prompt row equal to
-// its group's first (checked on the device; one host synchronisation).
-// Whether the model's prompt state was computed for groups of G x P with the
-// current weights and buffers (its prompts still to be compared).
 // Whether the buffers holding the prompt state are those it was recorded in.
 bool pstate_bufs_same(const sm_model* m) {
   return m->pstate_gens[0] == m->pkc.gen && m->pstate_gens[1] == m->pvc.gen &&
          m->pstate_gens[2] == m->prow.gen && m->pstate_gens[3] == m->pids.gen;
 }
 
+// Whether the model's prompt state was computed for groups of G x P with the
+// current weights and buffers (its prompts still to be compared).
 bool pstate_matches(const sm_model* m, int64_t groups, int64_t P) {
   return m->pstate_valid && m->pstate_weights == m->weights_version && pstate_bufs_same(m) &&
          m->pstate_groups == groups && m->pstate_G == m->prompt_group && m->pstate_P == P;
